@@ -1,0 +1,210 @@
+"""Benchmark of the MoE block on one MI355X.
+
+Default workload: the full-size K2-class MoE layer (hidden 7168, 384 routed experts
+top-8, expert intermediate 2048 in MXFP4 = E2M1 codes + E8M0 per-32 scales, one bf16
+shared expert of intermediate 2048, sigmoid router with bias, routed scale 2.5) decoding
+batch-1 tokens.  A step is one layer invocation on one token; the tokens rotate over a
+pool of 64 distinct seeded bf16 N(0,1) activations resident in HBM, so successive steps
+touch different experts.  Weights are synthetic (seeded generator, random init).
+
+Prints ONE JSON line (rank 0):
+  value        microseconds per token for the whole layer (lower is better)
+  roofline     the dominant kernel's algorithmic HBM bytes per launch over its average
+               duration (HIP events on the launch stream), against 8 TB/s
+  cpu_baseline the reference's own C kernels composing the same layer on this host's
+               cores (oracle/_ref, "reference"), or the oracle port when that library is
+               absent ("port"), on a bounded sample of tokens
+"""
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "kimi-k3-for-me_amd")
+
+H, E, K, I, SI = 7168, 384, 8, 2048, 2048
+HBM_PEAK_GBS = 8000.0
+B_EXPERT = 3 * I * H // 2 + 3 * I * H // 32          # 23,396,352 bytes per routed expert
+B_SHARED = 3 * SI * H * 2                             # 88,080,384
+B_ROUTER = E * H * 4 + E * 4                          # 11,011,584
+
+
+def load_k3x():
+    spec = importlib.util.spec_from_file_location("k3x", os.path.join(PKG, "k3x.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def kernel_bytes(U, T):
+    """Algorithmic HBM bytes per launch of the three decode kernels (each weight byte
+    once, activations included)."""
+    k1 = B_ROUTER + 2 * SI * H * 2 + T * H * 2
+    k2 = U * 2 * (I * H // 2 + I * H // 32)
+    k3 = U * (H * I // 2 + H * I // 32) + H * SI * 2 + T * H * 4
+    return {"k1_router_shared": k1, "k2_gateup": k2, "k3_down": k3}
+
+
+def cpu_baseline(n_tokens=24, min_seconds=10.0):
+    """The layer on the host CPU over a bounded sample of tokens (same seeded layer)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import ctypes as C
+    import oracle_lib as ol
+    import synth
+
+    L = synth.full(seed=1)
+    x = L.x(n_tokens, bf16=True, stream_sub=7)
+    ref = ol.ref()
+    kind = "reference" if ref is not None else "port"
+    # route once to know which experts the sample needs, then generate only those
+    idx = np.empty((n_tokens, K), np.int32)
+    wt = np.empty((n_tokens, K), np.float32)
+    for t in range(n_tokens):
+        xt = np.ascontiguousarray(x[t])
+        ol.oracle().ko_router(ol.ptr(idx[t], ol.I32P), ol.ptr(wt[t], ol.F32P),
+                              ol.ptr(xt, ol.F32P), ol.ptr(L.gate, ol.F32P),
+                              ol.ptr(L.bias, ol.F32P), H, E, K, 1, 2.5)
+    need = sorted(set(idx.ravel().tolist()))
+    bank = (ol.KoExpert * E)()
+    keep = {}
+    for e in need:
+        d = {k: v.copy() for k, v in L.expert(e).items()}
+        keep[e] = d
+        for k in ("p1", "s1", "p3", "s3", "p2", "s2"):
+            setattr(bank[e], k, d[k].ctypes.data_as(ol.U8P))
+    out = np.empty((1, H), np.float32)
+    ii = np.empty((1, K), np.int32)
+    ww = np.empty((1, K), np.float32)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        for t in range(n_tokens):
+            xt = np.ascontiguousarray(x[t:t + 1])
+            t0 = time.perf_counter()
+            if ref is not None:
+                ref.refdrv_k2_tokens(ol.ptr(out, ol.F32P), ol.ptr(xt, ol.F32P), 1, H, E, K, I, SI,
+                                     2.5, 1, ol.ptr(L.gate, ol.F32P), ol.ptr(L.bias, ol.F32P),
+                                     bank, ol.ptr(L.sh1, ol.U16P), ol.ptr(L.sh3, ol.U16P),
+                                     ol.ptr(L.sh2, ol.U16P), ol.ptr(ii, ol.I32P),
+                                     ol.ptr(ww, ol.F32P))
+            else:
+                L.oracle_moe(xt)
+            times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start >= min_seconds:
+            break
+    us = float(np.median(times) * 1e6)
+    cores = int(ol.oracle().ko_threads())
+    return {"value": round(us, 1), "unit": "us/token", "cores": cores, "kind": kind,
+            "sample": f"{len(times)} layer calls over {n_tokens} distinct bf16 tokens of the "
+                      f"same seeded layer ({len(need)} experts generated), median per token, "
+                      f"OpenMP threads {cores}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(collectives and sharding are out of scope); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    assert torch.cuda.is_available(), "no GPU visible"
+    k3x = load_k3x()
+    dev = torch.device("cuda:0")
+    cfg = k3x.make_cfg(H, E, K, I, 1, 1, 2.5)
+    t_build = time.perf_counter()
+    layer = k3x.MoELayer.synthetic(cfg, seed=1, router_sigma=0.02, bias_sigma=0.1)
+    build_s = time.perf_counter() - t_build
+    n_pool = 64
+    xs = k3x.synth_normal_f32(n_pool * H, k3x.synth_key(1, 0, k3x.STREAM_X, 100))
+    xpool = torch.from_numpy(xs.reshape(n_pool, H)).to(dev).to(torch.bfloat16).contiguous()
+    out = torch.empty((1, H), dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    sh = stream.cuda_stream
+    row = xpool.stride(0) * 2
+
+    def step(i):
+        layer.forward(out.data_ptr(), xpool.data_ptr() + (i % n_pool) * row, 1, k3x.K3X_BF16,
+                      stream=sh)
+
+    with torch.cuda.stream(stream):
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        for i in range(args.steps):
+            step(args.warmup + i)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    wall_ms = (t1 - t0) * 1e3 / args.steps
+    gpu_ms = ev0.elapsed_time(ev1) / args.steps
+
+    # per-kernel durations: HIP events between the kernels, on the launch stream
+    layer.set_timing(True)
+    names = ["k1_router_shared", "k2_gateup", "k3_down"]
+    per = {n: [] for n in names}
+    with torch.cuda.stream(stream):
+        for i in range(args.steps):
+            step(i)
+            ms = layer.last_ms()
+            for n, v in zip(names, ms):
+                per[n].append(v)
+    layer.set_timing(False)
+    avg = {n: float(np.mean(v)) for n, v in per.items()}
+    kb = kernel_bytes(U=K, T=1)
+    dom = max(avg, key=lambda n: avg[n])
+    achieved = kb[dom] / (avg[dom] * 1e-3) / 1e9
+    layer_bytes = K * B_EXPERT + B_SHARED + B_ROUTER + H * 2 + H * 4
+    rec = {
+        "metric": "moe_layer_decode_b1_us_per_token",
+        "value": round(wall_ms * 1e3, 2),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4-e2m1xe8m0 weights, bf16 mfma (hi+lo activations), fp32 accumulate",
+        "data": "synthetic (seeded random weights and bf16 N(0,1) tokens)",
+        "config": {"workload": "K2-class MoE layer decode b=1: hidden 7168, 384 experts top-8, "
+                               "inter 2048 MXFP4, 1 bf16 shared expert",
+                   "tokens_per_step": 1, "token_pool": n_pool, "parallelism": "none (1 GPU)"},
+        "layer_hbm_gbs": round(layer_bytes / (wall_ms * 1e-3) / 1e9, 1),
+        "gpu_event_ms_per_step": round(gpu_ms, 5),
+        "kernel_avg_us": {n: round(v * 1e3, 2) for n, v in avg.items()},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": kb[dom]},
+        "layer_build_s": round(build_s, 2),
+    }
+    layer.close()
+    del xpool, out
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        rec["cpu_baseline"] = cpu_baseline(min_seconds=args.cpu_seconds)
+    else:
+        rec["cpu_baseline"] = None
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,192 @@
+/* k3x_moe.h - MI355X (gfx950) MoE block behind a C ABI.
+ *
+ * The reference engine's MoE block (router scoring and top-k, dispatch, grouped SwiGLU
+ * experts over packed MXFP4 weights with E8M0 per-32 scales, the shared expert and the
+ * weighted combine) runs on the CPU through
+ *
+ *     void k3_moe        (float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
+ *                         int T, int *idx, float *wt, float *scratch);   k3.h:629-630
+ *     void k3_moe_prefill(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
+ *                         int T, int *idx, float *wt, float *scratch);   k3.h:636-637
+ *
+ * This library computes the same block on one GPU with the layer's weights resident in
+ * HBM.  A layer is uploaded once (k3x_moe_layer_create, pulling every expert through the
+ * same get() supplier contract as K3ExpertSrc) and then run any number of times, either
+ * from host pointers with the k3_moe semantics (k3x_moe / k3x_moe_prefill) or on device
+ * pointers on a caller's HIP stream (k3x_moe_forward).
+ *
+ * Everything here is plain C: pointers, sizes and status codes; no HIP or torch types.
+ * Every call returns 0 or a negative K3X_E_* status (the reference aborts or counts a
+ * drop instead; see each call).  Thread model: one layer handle is used by one host
+ * thread at a time; kernels of one call run in order on the stream given.
+ *
+ * Variant covered: the K2-class layer (no latent projection, SwiGLU, one or more shared
+ * experts in bf16, sigmoid router with a selection bias).  In the reference's terms that
+ * is latent = hidden with identity down/up, latent_norm = 0 and situ_b1 = situ_b2 = 2^64.
+ */
+#ifndef K3X_MOE_H
+#define K3X_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ----------------------------------------------------------------- */
+#define K3X_OK          0
+#define K3X_E_ARG      -1   /* NULL pointer, T < 0, bad dtype                              */
+#define K3X_E_SHAPE    -2   /* hidden or moe_inter not a multiple of 128, group != 32,
+                               topk outside 1..64, T above the layer's limit             */
+#define K3X_E_HIP      -3   /* a HIP runtime call or kernel launch failed                */
+#define K3X_E_NOMEM    -4   /* device or host allocation failed                          */
+#define K3X_E_DROP     -5   /* an expert could not be fetched (k3x_expert_drops counts it) */
+#define K3X_E_NODEV    -6   /* no usable gfx950 device                                    */
+
+/* Human-readable text of a status code (static storage). */
+const char *k3x_strerror(int status);
+
+/* ---- configuration: the MoE fields of K3Cfg (k3.h:94-102) -------------------------- */
+typedef struct k3x_cfg {
+    int   hidden;         /* 7168 */
+    int   n_experts;      /* 384 */
+    int   topk;           /* 8 */
+    int   moe_inter;      /* 2048, routed and per shared expert */
+    int   n_shared;       /* 1: shared intermediate = n_shared * moe_inter */
+    int   moe_renorm;     /* 1: renormalise the top-k weights */
+    float routed_scale;   /* 2.5 */
+    int   group;          /* MXFP4 group size; only 32 is supported (K3_MXFP4_GROUP) */
+} k3x_cfg;
+
+/* ---- one routed expert, still MXFP4: K3ExpertQ (k3.h:507-516) ----------------------
+ * Row-major [out][in]: packed [rows][in/2] bytes (low nibble = even element),
+ * scales [rows][in/group] E8M0 bytes.  p1/s1 gate [I][H], p3/s3 up [I][H],
+ * p2/s2 down [H][I]. */
+typedef struct k3x_expert_q {
+    const unsigned char *p1, *s1;
+    const unsigned char *p3, *s3;
+    const unsigned char *p2, *s2;
+} k3x_expert_q;
+
+/* ---- expert supplier: the get() half of K3ExpertSrc (k3.h:521-544) -----------------
+ * get() returns 0 and fills *out, or non-zero when the expert cannot be fetched. The
+ * pointers need stay valid only until get() is called again. */
+typedef struct k3x_expert_src {
+    int  (*get)(struct k3x_expert_src *self, int layer, int expert, k3x_expert_q *out);
+    void *ctx;
+} k3x_expert_src;
+
+/* ---- a layer's weights: the K2 subset of K3MoeW (k3.h:546-569) ----------------------
+ * gate fp32 [n_experts][hidden], bias fp32 [n_experts] (may be NULL),
+ * sh1/sh3 bf16 [n_shared*moe_inter][hidden], sh2 bf16 [hidden][n_shared*moe_inter]
+ * (all three NULL when n_shared == 0).  Experts come from src, or from bank
+ * ([n_experts] entries) when src is NULL. */
+typedef struct k3x_moe_w {
+    const float        *gate, *bias;
+    const uint16_t     *sh1, *sh3, *sh2;
+    k3x_expert_src     *src;
+    const k3x_expert_q *bank;
+    int                 layer;
+} k3x_moe_w;
+
+typedef struct k3x_moe_layer k3x_moe_layer;
+
+/* Upload a layer to device `device` and keep it resident.  Every expert is fetched
+ * once through src->get (or read from bank) and re-laid out for the matrix cores.
+ * A failed fetch increments k3x_expert_drops and fails the call with K3X_E_DROP (the
+ * reference would skip the term per token and leave the caller to check the counter:
+ * k3_ops.c:1916-1926). Replaces the per-token expert fetches of k3_moe (k3_ops.c:1905-
+ * 1931) by one upload. */
+int  k3x_moe_layer_create(const k3x_cfg *c, const k3x_moe_w *w, int device,
+                          k3x_moe_layer **out);
+void k3x_moe_layer_destroy(k3x_moe_layer *L);
+
+/* Bytes of device memory the layer holds (weights plus its working buffers). */
+size_t k3x_moe_layer_bytes(const k3x_moe_layer *L);
+
+/* Read expert e back from the device in the reference's row-major layout (host
+ * buffers sized as in k3x_expert_q).  For checking and for handing experts back. */
+int  k3x_moe_layer_read_expert(const k3x_moe_layer *L, int e, unsigned char *p1,
+                               unsigned char *s1, unsigned char *p3, unsigned char *s3,
+                               unsigned char *p2, unsigned char *s2);
+
+/* ---- device-pointer forward --------------------------------------------------------
+ * out  fp32 [T][hidden] device, overwritten (or resid + MoE when resid != NULL;
+ *      resid may equal out).
+ * x    [T][hidden] device, K3X_F32 or K3X_BF16.
+ * idx/wt  optional device [T][topk]: every token's routing (expert indices in selection
+ *      order, combine weights after renorm and routed_scale), as k3_router writes them
+ *      (k3_ops.c:1700-1716).
+ * stream  a hipStream_t, or NULL for the null stream.  Asynchronous: returns after
+ *      enqueueing.  T <= 8 runs the decode path (fused dequant-GEMV on the matrix cores,
+ *      every unique expert read once per call); larger T runs the prefill pipeline
+ *      (device top-k, histogram, prefix sum, grouped GEMM, combine). */
+#define K3X_F32  0
+#define K3X_BF16 1
+int  k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
+                     const float *resid, int *idx, float *wt, void *stream);
+
+/* RMSNorm of T rows on the device: y = w * x * inv, inv = 1/sqrt(mean(x^2) + eps)
+ * (k3_rmsnorm, k3_ops.c:132-140).  x, y fp32 [T][n], w fp32 [n], device pointers. */
+int  k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
+                 void *stream);
+
+/* ---- host-pointer drop-ins with the reference's semantics ---------------------------
+ * k3x_moe mirrors k3_moe (k3.h:629-630): out [T][hidden] overwritten, x [T][hidden]
+ * fp32, idx/wt [topk] left holding the LAST token's routing.  k3x_moe_prefill mirrors
+ * k3_moe_prefill (k3.h:636-637); on this device both run the same pipeline, whose
+ * results do not depend on how tokens are grouped into calls.  Synchronous.  The
+ * reference's scratch argument has no counterpart: working memory lives in the layer. */
+int  k3x_moe(k3x_moe_layer *L, float *out, const float *x, int T, int *idx, float *wt);
+int  k3x_moe_prefill(k3x_moe_layer *L, float *out, const float *x, int T, int *idx,
+                     float *wt);
+
+/* k3_expert_drops (k3.h:576-580): experts that could not be fetched. */
+extern long k3x_expert_drops;
+
+/* ---- synthetic layers --------------------------------------------------------------
+ * A layer whose weights come from a counter-based generator (splitmix64 per element),
+ * so any element can be regenerated on its own on the CPU: the router fp32 N(0,
+ * router_sigma); the bias N(0, bias_sigma), or Zipf-skewed alpha*(pi(e)+1)^-zipf_s over
+ * a seeded permutation pi when zipf_alpha > 0; E2M1 codes uniform over 16; E8M0 scales
+ * uniform over [scale_lo, scale_hi]; shared weights bf16 N(0, shared_sigma).
+ * Expert bytes are generated directly in device memory. */
+typedef struct k3x_synth_spec {
+    uint64_t seed;
+    int      layer;
+    double   router_sigma;   /* 0.02 */
+    double   bias_sigma;     /* 0.1 */
+    double   zipf_alpha;     /* 0: normal bias */
+    double   zipf_s;         /* 1.1 */
+    int      scale_lo;       /* 121 */
+    int      scale_hi;       /* 125 */
+    double   shared_sigma;   /* 0.02 */
+} k3x_synth_spec;
+
+int  k3x_synth_layer_create(const k3x_cfg *c, const k3x_synth_spec *s, int device,
+                            k3x_moe_layer **out);
+
+/* Generator stream ids and the element rule, exposed so a checker can regenerate any
+ * tensor of a synthetic layer on the host. */
+enum {
+    K3X_STREAM_ROUTER = 0, K3X_STREAM_BIAS = 1, K3X_STREAM_X = 2, K3X_STREAM_SH1 = 3,
+    K3X_STREAM_SH3 = 4, K3X_STREAM_SH2 = 5, K3X_STREAM_NORM = 6,
+    K3X_STREAM_CODES = 10, K3X_STREAM_SCALES = 11
+};
+uint64_t k3x_synth_key(uint64_t seed, int layer, int stream, int sub);
+void     k3x_synth_normal_f32(float *dst, size_t n, uint64_t key, double mu, double sigma);
+void     k3x_synth_normal_bf16(uint16_t *dst, size_t n, uint64_t key, double mu,
+                               double sigma);
+
+/* ---- timing hooks ---------------------------------------------------------------
+ * The kernels the last k3x_moe_forward on L enqueued, bracketed by two HIP events on
+ * the stream it used (recorded when timing is on).  ms receives the elapsed time of
+ * the last timed call after a synchronize. */
+int  k3x_moe_layer_set_timing(k3x_moe_layer *L, int on);
+int  k3x_moe_layer_last_ms(k3x_moe_layer *L, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,141 @@
+/* k3x_internal.h - what the C host layer (k3x_moe.c) and the HIP kernels
+ * (k3x_kernels.hip) share: the device layer record, the HBM layouts and the launchers.
+ *
+ * HBM layout of a layer (one allocation per region, all 256-byte aligned):
+ *
+ *   router   fp32 [n_experts][hidden]            as given (k3_router's W)
+ *   bias     fp32 [n_experts]
+ *   experts  n_experts records of K3X tiled MXFP4, each: gate tiles, up tiles, down tiles
+ *   shared   bf16 tiled gate, up, down (n_shared*moe_inter intermediate)
+ *   work     the per-call buffers (routing, activations in B-fragment layout, partials)
+ *
+ * K3X TILED MXFP4 (a matrix of R rows by K columns, R % 16 == 0, K % 128 == 0).
+ *   The matrix is cut into R/16 row tiles, stored one after another.  A tile is K/128
+ *   "quads" of 128 columns, grouped four to a "super-quad".  A super-quad holds the
+ *   codes of its nq (<= 4) quads, 1024 bytes each, then 256 bytes of scales:
+ *     codes of quad q, lane l (m = l % 16, kq = l / 16): the 16 bytes of row 16*rt + m
+ *       that hold columns 128*q + 32*kq .. +31 (one 32-column scale group, low nibble =
+ *       even column, as in the reference's packed rows);
+ *     scales, lane l: 4 bytes, byte j = scale byte of row 16*rt + m, group 4*(4*S+j)+kq
+ *       (0 where quad 4*S+j does not exist).
+ *   So one 16-byte load per lane reads a whole scale group, and a wave's load covers
+ *   1024 contiguous bytes.  Lane (m, kq) is the matrix cores' A-operand lane for row m
+ *   and k-slots 8*kq..8*kq+7 of v_mfma_f32_16x16x32_bf16; dword t of its 16 bytes feeds
+ *   the t-th product of the quad, so product t of quad q pairs k-slot 8*kq + j with
+ *   column 128*q + 32*kq + 8*t + j.  The B operand (activations) uses the same map.
+ *
+ * K3X TILED BF16 (R % 16 == 0, K % 128 == 0): R/16 tiles of K/128 quads of 4 KB; in quad
+ *   q, product t, lane l holds row 16*rt + m, columns 128*q + 32*kq + 8*t .. +7.
+ *
+ * B FRAGMENTS (activations of up to 8 tokens): for a K-long vector set, [K/128][4][64]
+ *   entries of 8 bf16: quad q, product t, lane l = n + 16*kq holds column n's elements
+ *   128*q + 32*kq + 8*t .. +7.  Column 2*i is token i rounded to bf16 ("hi"), column
+ *   2*i+1 the bf16 of the remainder ("lo"); hi + lo carries 16 significant bits.
+ */
+#ifndef K3X_INTERNAL_H
+#define K3X_INTERNAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/k3x_moe.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define K3X_DECODE_MAX_T 8       /* tokens per call on the decode path (2 columns each) */
+#define K3X_MAX_TOPK     64      /* K3_MAX_TOPK, k3.h:857-864 */
+#define K3X_ROUTER_WAVES 8       /* experts per router workgroup (one wave each) */
+
+/* byte sizes of the tiled formats */
+static inline size_t k3x_fp4_tile_bytes(int K)
+{
+    const int nq = K / 128, ns = (nq + 3) / 4;
+    return (size_t)nq * 1024 + (size_t)ns * 256;
+}
+static inline size_t k3x_fp4_matrix_bytes(int R, int K) { return (size_t)(R / 16) * k3x_fp4_tile_bytes(K); }
+static inline size_t k3x_bf16_matrix_bytes(int R, int K) { return (size_t)R * K * 2; }
+
+/* routing summary written by the router, read by the expert kernels */
+typedef struct k3x_route {
+    int   nu;                                   /* unique experts in this call        */
+    int   pad[63];
+    int   uniq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];        /* first-seen order           */
+    float wtok[K3X_DECODE_MAX_T * K3X_MAX_TOPK][K3X_DECODE_MAX_T]; /* [u][token] weight, 0 = not routed */
+} k3x_route;
+
+/* prefill working buffers, grown on demand */
+typedef struct k3x_prefill_buf {
+    int     cap_T;          /* tokens the buffers hold */
+    void   *base;           /* one device allocation   */
+    size_t  bytes;
+    float  *score, *choice; /* [T][n_experts]          */
+    int    *idx;            /* [T][K]                  */
+    float  *wt;             /* [T][K]                  */
+    int    *counts;         /* [n_experts + 1]         */
+    int    *offsets;        /* [n_experts + 1]         */
+    int    *cursor;         /* [n_experts]             */
+    int    *perm_tok;       /* [T*K] token of each permuted row */
+    int    *pos;            /* [T][K] permuted row of each (token, slot) */
+    int    *tiles;          /* [T*K/16 + n_experts] work list of (expert, row0) */
+    int    *ntiles;         /* [1] */
+    uint16_t *xb;           /* [T][hidden] bf16 hi, then lo: [2][T][hidden] */
+    float  *act;            /* [T*K][moe_inter]        */
+    uint16_t *actb;         /* [2][T*K][moe_inter] bf16 hi/lo */
+    float  *y;              /* [T*K][hidden] expert outputs   */
+    float  *sact;           /* [T][SI] shared activation      */
+    uint16_t *sactb;        /* [2][T][SI]              */
+} k3x_prefill_buf;
+
+struct k3x_moe_layer {
+    k3x_cfg   cfg;
+    int       device;
+    int       SI;                 /* n_shared * moe_inter */
+    /* weights */
+    float    *router;             /* [E][H] */
+    float    *bias;               /* [E] (zeros when absent) */
+    uint8_t  *experts;            /* E * expert_bytes */
+    size_t    expert_bytes, gate_off, up_off, down_off;
+    uint16_t *sh_gate, *sh_up, *sh_down;   /* tiled bf16, NULL when SI == 0 */
+    /* decode working buffers */
+    float    *score, *choice;     /* [DECODE_MAX_T][E] */
+    int      *idx;                /* [DECODE_MAX_T][K] */
+    float    *wt;                 /* [DECODE_MAX_T][K] */
+    unsigned *counter;            /* last-workgroup ticket of the router */
+    k3x_route *route;
+    uint16_t *xB;                 /* B fragments of x: [H/128][4][64][8] */
+    uint16_t *actB;               /* [DECODE_MAX_T*K][I/128][4][64][8] */
+    uint16_t *shB;                /* [SI/128][4][64][8] */
+    float    *shpart;             /* [2 mats][2 halves][SI][16] */
+    k3x_prefill_buf pf;
+    size_t    bytes;
+    /* timing */
+    int       timing;
+    void     *ev[8];
+    int       n_ev_used;
+    /* host staging for the drop-in calls */
+    void     *h_dev_x, *h_dev_out;
+    size_t    h_cap;
+};
+
+/* ---- launchers (k3x_kernels.hip), all return 0 or K3X_E_HIP ---------------------- */
+int k3x_dev_check(int device);
+int k3x_dev_tile_fp4(uint8_t *dst, const uint8_t *packed, const uint8_t *scales, int R,
+                     int K, void *stream);
+int k3x_dev_tile_bf16(uint16_t *dst, const uint16_t *src, int R, int K, void *stream);
+int k3x_dev_untile_fp4(uint8_t *packed, uint8_t *scales, const uint8_t *src, int R, int K,
+                       void *stream);
+int k3x_dev_synth_fp4(uint8_t *dst, int R, int K, uint64_t code_key, uint64_t scale_key,
+                      int lo, int hi, void *stream);
+int k3x_dev_decode(struct k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
+                   const float *resid, int *idx, float *wt, void *stream);
+int k3x_dev_prefill(struct k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
+                    const float *resid, int *idx, float *wt, void *stream);
+int k3x_dev_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
+                    void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

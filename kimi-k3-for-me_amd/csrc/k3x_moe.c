@@ -1,0 +1,480 @@
+/* k3x_moe.c - the C host side of the MoE block: layer upload, call validation and the
+ * drop-in entry points.  Kernels live in k3x_kernels.hip behind the k3x_dev_* launchers.
+ *
+ * Follows the reference's MoE entry points (include/k3/k3.h:571-637, src/core/
+ * k3_ops.c:1862-2132) and its expert supplier contract (K3ExpertSrc, k3.h:518-544);
+ * the differences are listed in include/k3x_moe.h (weights resident in HBM, status codes
+ * instead of abort()).
+ */
+#include "k3x_internal.h"
+
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+long k3x_expert_drops = 0;
+
+const char *k3x_strerror(int s)
+{
+    switch (s) {
+    case K3X_OK:      return "ok";
+    case K3X_E_ARG:   return "invalid argument";
+    case K3X_E_SHAPE: return "unsupported shape";
+    case K3X_E_HIP:   return "HIP runtime error";
+    case K3X_E_NOMEM: return "out of memory";
+    case K3X_E_DROP:  return "expert could not be fetched";
+    case K3X_E_NODEV: return "no usable gfx950 device";
+    default:          return "unknown status";
+    }
+}
+
+#define HIPCHK(call)                                                                   \
+    do {                                                                               \
+        hipError_t e_ = (call);                                                        \
+        if (e_ != hipSuccess) {                                                        \
+            fprintf(stderr, "k3x: %s failed: %s\n", #call, hipGetErrorString(e_));     \
+            rc = (e_ == hipErrorOutOfMemory) ? K3X_E_NOMEM : K3X_E_HIP;                \
+            goto fail;                                                                 \
+        }                                                                              \
+    } while (0)
+
+#define RCCHK(call)                                                                    \
+    do {                                                                               \
+        rc = (call);                                                                   \
+        if (rc) goto fail;                                                             \
+    } while (0)
+
+static int cfg_ok(const k3x_cfg *c)
+{
+    if (!c) return K3X_E_ARG;
+    if (c->hidden <= 0 || c->n_experts <= 0 || c->topk <= 0 || c->moe_inter <= 0 ||
+        c->n_shared < 0)
+        return K3X_E_SHAPE;
+    if (c->hidden % 128 || c->moe_inter % 128) return K3X_E_SHAPE;
+    if (c->group != 32) return K3X_E_SHAPE;
+    if (c->topk > K3X_MAX_TOPK || c->topk > c->n_experts) return K3X_E_SHAPE;
+    if (c->n_experts > 1024) return K3X_E_SHAPE;
+    return 0;
+}
+
+static void layout(k3x_moe_layer *L)
+{
+    const int H = L->cfg.hidden, I = L->cfg.moe_inter;
+    const size_t gu = k3x_fp4_matrix_bytes(I, H), dn = k3x_fp4_matrix_bytes(H, I);
+    L->gate_off = 0;
+    L->up_off = gu;
+    L->down_off = 2 * gu;
+    L->expert_bytes = (2 * gu + dn + 255) & ~(size_t)255;
+}
+
+static int dmalloc(void **p, size_t n, size_t *total)
+{
+    n = (n + 255) & ~(size_t)255;
+    if (hipMalloc(p, n ? n : 256) != hipSuccess) { *p = NULL; return K3X_E_NOMEM; }
+    *total += n;
+    return 0;
+}
+
+/* Allocate every device region of a layer; weights are filled by the caller. */
+static int layer_alloc(k3x_moe_layer *L)
+{
+    const k3x_cfg *c = &L->cfg;
+    const int H = c->hidden, E = c->n_experts, I = c->moe_inter, K = c->topk;
+    int rc;
+    layout(L);
+    L->SI = c->moe_inter * c->n_shared;
+    size_t *b = &L->bytes;
+    RCCHK(dmalloc((void **)&L->router, (size_t)E * H * 4, b));
+    RCCHK(dmalloc((void **)&L->bias, (size_t)E * 4, b));
+    RCCHK(dmalloc((void **)&L->experts, (size_t)E * L->expert_bytes, b));
+    if (L->SI > 0) {
+        RCCHK(dmalloc((void **)&L->sh_gate, k3x_bf16_matrix_bytes(L->SI, H), b));
+        RCCHK(dmalloc((void **)&L->sh_up, k3x_bf16_matrix_bytes(L->SI, H), b));
+        RCCHK(dmalloc((void **)&L->sh_down, k3x_bf16_matrix_bytes(H, L->SI), b));
+        RCCHK(dmalloc((void **)&L->shB, (size_t)L->SI * 16 * 2, b));
+        RCCHK(dmalloc((void **)&L->shpart, (size_t)4 * L->SI * 16 * 4, b));
+    }
+    RCCHK(dmalloc((void **)&L->score, (size_t)K3X_DECODE_MAX_T * E * 4, b));
+    RCCHK(dmalloc((void **)&L->choice, (size_t)K3X_DECODE_MAX_T * E * 4, b));
+    RCCHK(dmalloc((void **)&L->idx, (size_t)K3X_DECODE_MAX_T * K * 4, b));
+    RCCHK(dmalloc((void **)&L->wt, (size_t)K3X_DECODE_MAX_T * K * 4, b));
+    RCCHK(dmalloc((void **)&L->counter, 256, b));
+    RCCHK(dmalloc((void **)&L->route, sizeof(k3x_route), b));
+    RCCHK(dmalloc((void **)&L->xB, (size_t)H * 16 * 2, b));
+    RCCHK(dmalloc((void **)&L->actB, (size_t)K3X_DECODE_MAX_T * K * I * 16 * 2, b));
+    if (hipMemset(L->counter, 0, 256) != hipSuccess) return K3X_E_HIP;
+    if (hipMemset(L->bias, 0, (size_t)E * 4) != hipSuccess) return K3X_E_HIP;
+    return 0;
+fail:
+    return rc;
+}
+
+static void layer_free(k3x_moe_layer *L)
+{
+    if (!L) return;
+    void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shB,
+                 L->shpart, L->score, L->choice, L->idx, L->wt, L->counter, L->route,
+                 L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out};
+    for (size_t i = 0; i < sizeof p / sizeof p[0]; i++)
+        if (p[i]) hipFree(p[i]);
+    for (int i = 0; i < 8; i++)
+        if (L->ev[i]) hipEventDestroy((hipEvent_t)L->ev[i]);
+    free(L);
+}
+
+void k3x_moe_layer_destroy(k3x_moe_layer *L)
+{
+    if (!L) return;
+    hipSetDevice(L->device);
+    hipDeviceSynchronize();
+    layer_free(L);
+}
+
+size_t k3x_moe_layer_bytes(const k3x_moe_layer *L) { return L ? L->bytes + L->pf.bytes : 0; }
+
+static int new_layer(const k3x_cfg *c, int device, k3x_moe_layer **out)
+{
+    int rc = cfg_ok(c);
+    if (rc) return rc;
+    if ((rc = k3x_dev_check(device))) return rc;
+    if (hipSetDevice(device) != hipSuccess) return K3X_E_NODEV;
+    k3x_moe_layer *L = (k3x_moe_layer *)calloc(1, sizeof *L);
+    if (!L) return K3X_E_NOMEM;
+    L->cfg = *c;
+    L->device = device;
+    if ((rc = layer_alloc(L))) { layer_free(L); return rc; }
+    *out = L;
+    return 0;
+}
+
+/* Shared expert upload: three bf16 matrices, re-laid out on the device. */
+static int upload_shared(k3x_moe_layer *L, const uint16_t *sh1, const uint16_t *sh3,
+                         const uint16_t *sh2)
+{
+    const int H = L->cfg.hidden, SI = L->SI;
+    int rc = 0;
+    void *stage = NULL;
+    if (SI <= 0) return 0;
+    if (!sh1 || !sh3 || !sh2) return K3X_E_ARG;
+    const size_t n = (size_t)SI * H * 2;
+    HIPCHK(hipMalloc(&stage, n));
+    HIPCHK(hipMemcpy(stage, sh1, n, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_bf16(L->sh_gate, (const uint16_t *)stage, SI, H, NULL));
+    HIPCHK(hipDeviceSynchronize());
+    HIPCHK(hipMemcpy(stage, sh3, n, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_bf16(L->sh_up, (const uint16_t *)stage, SI, H, NULL));
+    HIPCHK(hipDeviceSynchronize());
+    HIPCHK(hipMemcpy(stage, sh2, n, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_bf16(L->sh_down, (const uint16_t *)stage, H, SI, NULL));
+    HIPCHK(hipDeviceSynchronize());
+fail:
+    if (stage) hipFree(stage);
+    return rc;
+}
+
+/* One expert: its six arrays copied to a staging area, then tiled into the arena. */
+static int upload_expert(k3x_moe_layer *L, int e, const k3x_expert_q *q, uint8_t *stage)
+{
+    const int H = L->cfg.hidden, I = L->cfg.moe_inter;
+    const size_t pg = (size_t)I * H / 2, sg = (size_t)I * H / 32;
+    uint8_t *base = L->experts + (size_t)e * L->expert_bytes;
+    int rc = 0;
+    if (!q->p1 || !q->s1 || !q->p3 || !q->s3 || !q->p2 || !q->s2) return K3X_E_ARG;
+    /* staging: p1 s1 p3 s3 p2 s2, each at its own offset */
+    uint8_t *p1 = stage, *s1 = p1 + pg, *p3 = s1 + sg, *s3 = p3 + pg, *p2 = s3 + sg,
+            *s2 = p2 + pg;
+    HIPCHK(hipMemcpy(p1, q->p1, pg, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(s1, q->s1, sg, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(p3, q->p3, pg, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(s3, q->s3, sg, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(p2, q->p2, pg, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(s2, q->s2, sg, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_fp4(base + L->gate_off, p1, s1, I, H, NULL));
+    RCCHK(k3x_dev_tile_fp4(base + L->up_off, p3, s3, I, H, NULL));
+    RCCHK(k3x_dev_tile_fp4(base + L->down_off, p2, s2, H, I, NULL));
+    HIPCHK(hipDeviceSynchronize());
+fail:
+    return rc;
+}
+
+int k3x_moe_layer_create(const k3x_cfg *c, const k3x_moe_w *w, int device,
+                         k3x_moe_layer **out)
+{
+    if (!c || !w || !out || !w->gate || (!w->src && !w->bank)) return K3X_E_ARG;
+    if (w->src && !w->src->get) return K3X_E_ARG;
+    *out = NULL;
+    k3x_moe_layer *L = NULL;
+    int rc = new_layer(c, device, &L);
+    if (rc) return rc;
+    const int H = c->hidden, E = c->n_experts, I = c->moe_inter;
+    uint8_t *stage = NULL;
+    HIPCHK(hipMemcpy(L->router, w->gate, (size_t)E * H * 4, hipMemcpyHostToDevice));
+    if (w->bias) HIPCHK(hipMemcpy(L->bias, w->bias, (size_t)E * 4, hipMemcpyHostToDevice));
+    RCCHK(upload_shared(L, w->sh1, w->sh3, w->sh2));
+    HIPCHK(hipMalloc((void **)&stage, 3 * ((size_t)I * H / 2 + (size_t)I * H / 32)));
+    for (int e = 0; e < E; e++) {
+        k3x_expert_q q;
+        if (w->src) {
+            memset(&q, 0, sizeof q);
+            if (w->src->get(w->src, w->layer, e, &q) != 0) {
+                k3x_expert_drops++;
+                fprintf(stderr, "EXPERT DROP: layer %d expert %d failed to load\n", w->layer,
+                        e);
+                rc = K3X_E_DROP;
+                goto fail;
+            }
+        } else {
+            q = w->bank[e];
+        }
+        RCCHK(upload_expert(L, e, &q, stage));
+    }
+    hipFree(stage);
+    *out = L;
+    return 0;
+fail:
+    if (stage) hipFree(stage);
+    layer_free(L);
+    return rc;
+}
+
+int k3x_moe_layer_read_expert(const k3x_moe_layer *L, int e, unsigned char *p1,
+                              unsigned char *s1, unsigned char *p3, unsigned char *s3,
+                              unsigned char *p2, unsigned char *s2)
+{
+    if (!L || e < 0 || e >= L->cfg.n_experts) return K3X_E_ARG;
+    const int H = L->cfg.hidden, I = L->cfg.moe_inter;
+    const size_t pg = (size_t)I * H / 2, sg = (size_t)I * H / 32;
+    const uint8_t *base = L->experts + (size_t)e * L->expert_bytes;
+    uint8_t *st = NULL;
+    int rc = 0;
+    HIPCHK(hipSetDevice(L->device));
+    HIPCHK(hipMalloc((void **)&st, pg + sg));
+    const struct { const uint8_t *src; int R, K; unsigned char *p, *s; } m[3] = {
+        {base + L->gate_off, I, H, p1, s1},
+        {base + L->up_off, I, H, p3, s3},
+        {base + L->down_off, H, I, p2, s2}};
+    for (int i = 0; i < 3; i++) {
+        RCCHK(k3x_dev_untile_fp4(st, st + pg, m[i].src, m[i].R, m[i].K, NULL));
+        HIPCHK(hipDeviceSynchronize());
+        if (m[i].p) HIPCHK(hipMemcpy(m[i].p, st, pg, hipMemcpyDeviceToHost));
+        if (m[i].s) HIPCHK(hipMemcpy(m[i].s, st + pg, sg, hipMemcpyDeviceToHost));
+    }
+fail:
+    if (st) hipFree(st);
+    return rc;
+}
+
+/* ---------------------------------------------------------------- forward ---- */
+int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
+                    const float *resid, int *idx, float *wt, void *stream)
+{
+    if (!L || (T > 0 && (!out || !x))) return K3X_E_ARG;
+    if (T < 0 || (x_dtype != K3X_F32 && x_dtype != K3X_BF16)) return K3X_E_ARG;
+    if (((uintptr_t)x & 15) || ((uintptr_t)out & 15)) return K3X_E_ARG;
+    if ((idx == NULL) != (wt == NULL)) return K3X_E_ARG;
+    if (T == 0) return 0;
+    if (T <= K3X_DECODE_MAX_T)
+        return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, stream);
+    return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
+}
+
+int k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
+                void *stream)
+{
+    if (!y || !x || !w || n <= 0 || T < 0) return K3X_E_ARG;
+    return k3x_dev_rmsnorm(y, x, w, n, T, eps, stream);
+}
+
+/* Host-pointer drop-ins: stage x and out through device buffers held by the layer. */
+static int host_call(k3x_moe_layer *L, float *out, const float *x, int T, int *idx,
+                     float *wt)
+{
+    if (!L || (T > 0 && (!out || !x))) return K3X_E_ARG;
+    if (T <= 0) return T < 0 ? K3X_E_ARG : 0;
+    const k3x_cfg *c = &L->cfg;
+    const size_t n = (size_t)T * c->hidden * 4;
+    const size_t nr = (size_t)T * c->topk * 4;
+    int rc = 0;
+    HIPCHK(hipSetDevice(L->device));
+    if (L->h_cap < n + 2 * nr) {
+        if (L->h_dev_x) hipFree(L->h_dev_x);
+        if (L->h_dev_out) hipFree(L->h_dev_out);
+        L->h_dev_x = L->h_dev_out = NULL;
+        L->h_cap = 0;
+        HIPCHK(hipMalloc(&L->h_dev_x, n + 2 * nr + 512));
+        HIPCHK(hipMalloc(&L->h_dev_out, n));
+        L->h_cap = n + 2 * nr;
+    }
+    {
+        char *dx = (char *)L->h_dev_x;
+        int *didx = (int *)(dx + ((n + 255) & ~(size_t)255));
+        float *dwt = (float *)((char *)didx + ((nr + 255) & ~(size_t)255));
+        HIPCHK(hipMemcpy(dx, x, n, hipMemcpyHostToDevice));
+        RCCHK(k3x_moe_forward(L, (float *)L->h_dev_out, dx, K3X_F32, T, NULL, didx, dwt, NULL));
+        HIPCHK(hipDeviceSynchronize());
+        HIPCHK(hipMemcpy(out, L->h_dev_out, n, hipMemcpyDeviceToHost));
+        if (idx) {
+            const size_t last = (size_t)(T - 1) * c->topk;
+            HIPCHK(hipMemcpy(idx, didx + last, (size_t)c->topk * 4, hipMemcpyDeviceToHost));
+        }
+        if (wt) {
+            const size_t last = (size_t)(T - 1) * c->topk;
+            HIPCHK(hipMemcpy(wt, dwt + last, (size_t)c->topk * 4, hipMemcpyDeviceToHost));
+        }
+    }
+fail:
+    return rc;
+}
+
+int k3x_moe(k3x_moe_layer *L, float *out, const float *x, int T, int *idx, float *wt)
+{
+    return host_call(L, out, x, T, idx, wt);
+}
+
+int k3x_moe_prefill(k3x_moe_layer *L, float *out, const float *x, int T, int *idx,
+                    float *wt)
+{
+    return host_call(L, out, x, T, idx, wt);
+}
+
+/* ---------------------------------------------------------------- timing ---- */
+int k3x_moe_layer_set_timing(k3x_moe_layer *L, int on)
+{
+    if (!L) return K3X_E_ARG;
+    if (on) {
+        for (int i = 0; i < 8; i++)
+            if (!L->ev[i] && hipEventCreate((hipEvent_t *)&L->ev[i]) != hipSuccess)
+                return K3X_E_HIP;
+    }
+    L->timing = on ? 1 : 0;
+    L->n_ev_used = 0;
+    return 0;
+}
+
+int k3x_moe_layer_last_ms(k3x_moe_layer *L, float *ms)
+{
+    if (!L || !ms || !L->timing || L->n_ev_used < 2) return K3X_E_ARG;
+    for (int i = 0; i + 1 < L->n_ev_used; i++) {
+        if (hipEventSynchronize((hipEvent_t)L->ev[i + 1]) != hipSuccess) return K3X_E_HIP;
+        if (hipEventElapsedTime(&ms[i], (hipEvent_t)L->ev[i], (hipEvent_t)L->ev[i + 1]) !=
+            hipSuccess)
+            return K3X_E_HIP;
+    }
+    return L->n_ev_used - 1;
+}
+
+/* ---------------------------------------------------------------- synthetic ---- */
+static uint64_t mix64(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static uint64_t draw(uint64_t key, uint64_t i) { return mix64(key + (i + 1) * 0x9E3779B97F4A7C15ull); }
+
+uint64_t k3x_synth_key(uint64_t seed, int layer, int stream, int sub)
+{
+    uint64_t k = mix64(seed + 0x9E3779B97F4A7C15ull * (uint64_t)(layer + 1));
+    k = mix64(k ^ (0xD1B54A32D192ED03ull * (uint64_t)(stream + 1)));
+    return mix64(k + (uint64_t)(uint32_t)sub);
+}
+
+/* Box-Muller on the two 32-bit halves of one draw, in double, rounded to float once. */
+static double normal_of(uint64_t u)
+{
+    const double u1 = ((double)(u >> 32) + 0.5) * 0x1p-32;
+    const double u2 = ((double)(u & 0xFFFFFFFFull) + 0.5) * 0x1p-32;
+    return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+}
+
+void k3x_synth_normal_f32(float *dst, size_t n, uint64_t key, double mu, double sigma)
+{
+#pragma omp parallel for schedule(static) if (n > 65536)
+    for (size_t i = 0; i < n; i++) dst[i] = (float)(mu + sigma * normal_of(draw(key, i)));
+}
+
+static uint16_t to_bf16(float f)
+{
+    union { float f; uint32_t u; } v = {f};
+    if ((v.u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((v.u >> 16) | 0x40u);
+    return (uint16_t)((v.u + 0x7FFFu + ((v.u >> 16) & 1u)) >> 16);
+}
+
+void k3x_synth_normal_bf16(uint16_t *dst, size_t n, uint64_t key, double mu, double sigma)
+{
+#pragma omp parallel for schedule(static) if (n > 65536)
+    for (size_t i = 0; i < n; i++)
+        dst[i] = to_bf16((float)(mu + sigma * normal_of(draw(key, i))));
+}
+
+int k3x_synth_layer_create(const k3x_cfg *c, const k3x_synth_spec *s, int device,
+                           k3x_moe_layer **out)
+{
+    if (!c || !s || !out) return K3X_E_ARG;
+    if (s->scale_lo < 0 || s->scale_hi > 255 || s->scale_lo > s->scale_hi) return K3X_E_ARG;
+    *out = NULL;
+    k3x_moe_layer *L = NULL;
+    int rc = new_layer(c, device, &L);
+    if (rc) return rc;
+    const int H = c->hidden, E = c->n_experts, I = c->moe_inter, SI = L->SI;
+    float *hf = NULL;
+    uint16_t *hb = NULL;
+    hf = (float *)malloc((size_t)E * H * 4);
+    if (!hf) { rc = K3X_E_NOMEM; goto fail; }
+    k3x_synth_normal_f32(hf, (size_t)E * H, k3x_synth_key(s->seed, s->layer, K3X_STREAM_ROUTER, 0),
+                         0.0, s->router_sigma);
+    HIPCHK(hipMemcpy(L->router, hf, (size_t)E * H * 4, hipMemcpyHostToDevice));
+    if (s->zipf_alpha > 0.0) {
+        int *perm = (int *)malloc((size_t)E * sizeof(int));
+        if (!perm) { rc = K3X_E_NOMEM; goto fail; }
+        const uint64_t key = k3x_synth_key(s->seed, s->layer, K3X_STREAM_BIAS, 0);
+        for (int e = 0; e < E; e++) perm[e] = e;
+        for (int e = E - 1; e > 0; e--) {
+            const int j = (int)(draw(key, (uint64_t)e) % (uint64_t)(e + 1));
+            const int t = perm[e]; perm[e] = perm[j]; perm[j] = t;
+        }
+        for (int e = 0; e < E; e++) hf[e] = (float)(s->zipf_alpha * pow((double)(perm[e] + 1), -s->zipf_s));
+        free(perm);
+    } else {
+        k3x_synth_normal_f32(hf, (size_t)E, k3x_synth_key(s->seed, s->layer, K3X_STREAM_BIAS, 0),
+                             0.0, s->bias_sigma);
+    }
+    HIPCHK(hipMemcpy(L->bias, hf, (size_t)E * 4, hipMemcpyHostToDevice));
+    free(hf);
+    hf = NULL;
+    if (SI > 0) {
+        hb = (uint16_t *)malloc((size_t)SI * H * 2 * 3);
+        if (!hb) { rc = K3X_E_NOMEM; goto fail; }
+        const size_t n = (size_t)SI * H;
+        k3x_synth_normal_bf16(hb, n, k3x_synth_key(s->seed, s->layer, K3X_STREAM_SH1, 0), 0.0,
+                              s->shared_sigma);
+        k3x_synth_normal_bf16(hb + n, n, k3x_synth_key(s->seed, s->layer, K3X_STREAM_SH3, 0),
+                              0.0, s->shared_sigma);
+        k3x_synth_normal_bf16(hb + 2 * n, n, k3x_synth_key(s->seed, s->layer, K3X_STREAM_SH2, 0),
+                              0.0, s->shared_sigma);
+        RCCHK(upload_shared(L, hb, hb + n, hb + 2 * n));
+        free(hb);
+        hb = NULL;
+    }
+    for (int e = 0; e < E; e++) {
+        uint8_t *base = L->experts + (size_t)e * L->expert_bytes;
+        const struct { size_t off; int R, K, m; } mm[3] = {
+            {L->gate_off, I, H, 0}, {L->up_off, I, H, 1}, {L->down_off, H, I, 2}};
+        for (int i = 0; i < 3; i++)
+            RCCHK(k3x_dev_synth_fp4(base + mm[i].off, mm[i].R, mm[i].K,
+                                    k3x_synth_key(s->seed, s->layer, K3X_STREAM_CODES, 3 * e + mm[i].m),
+                                    k3x_synth_key(s->seed, s->layer, K3X_STREAM_SCALES, 3 * e + mm[i].m),
+                                    s->scale_lo, s->scale_hi, NULL));
+    }
+    HIPCHK(hipDeviceSynchronize());
+    *out = L;
+    return 0;
+fail:
+    free(hf);
+    free(hb);
+    layer_free(L);
+    return rc;
+}

@@ -1,0 +1,105 @@
+/* k3x_ref_adapter.c - the binding a maintainer of the reference engine adds to route its
+ * MoE block to libk3x.  Compiled inside the reference's build (it includes the
+ * reference's k3.h); it is not part of libk3x.so.
+ *
+ * k3_moe_gpu / k3_moe_prefill_gpu have the signatures of k3_moe / k3_moe_prefill
+ * (include/k3/k3.h:629-637).  On first use of a layer they upload it through the
+ * layer's own K3ExpertSrc (k3.h:521-544) and keep the handle; afterwards every call runs
+ * on the GPU.  Only the K2-class form is accepted: latent == hidden with identity
+ * down/up, latent_norm == 0, SiTU betas >= 2^64 (SwiGLU), bf16 shared weights; anything
+ * else returns -1 so the caller keeps the CPU path (k3_ops.c:1862, :2008).
+ */
+#include "k3.h"
+#include "k3x_moe.h"
+
+#include <stdio.h>
+#include <string.h>
+
+#define K3X_ADAPTER_MAX_LAYERS 128
+
+static k3x_moe_layer *g_layers[K3X_ADAPTER_MAX_LAYERS];
+static const K3MoeW *g_owner[K3X_ADAPTER_MAX_LAYERS];
+
+typedef struct {
+    k3x_expert_src  base;   /* first member: the callback casts back */
+    K3ExpertSrc    *src;
+} adapter_src;
+
+static int adapter_get(k3x_expert_src *self, int layer, int expert, k3x_expert_q *out)
+{
+    adapter_src *a = (adapter_src *)self;
+    K3ExpertQ q;
+    if (a->src->get(a->src, layer, expert, &q) != 0) return -1;
+    out->p1 = q.p1; out->s1 = q.s1;
+    out->p3 = q.p3; out->s3 = q.s3;
+    out->p2 = q.p2; out->s2 = q.s2;
+    return 0;
+}
+
+static int k2_form(const K3MoeW *w, const K3Cfg *c)
+{
+    return w->src && w->src->get && c->latent == c->hidden && !c->latent_norm &&
+           c->situ_b1 >= 0x1p64f && c->situ_b2 >= 0x1p64f && w->wdt == K3_WBF16 &&
+           !w->cache_only && w->layer >= 0 && w->layer < K3X_ADAPTER_MAX_LAYERS;
+}
+
+static k3x_moe_layer *layer_for(const K3MoeW *w, const K3Cfg *c)
+{
+    if (g_layers[w->layer] && g_owner[w->layer] == w) return g_layers[w->layer];
+    k3x_cfg kc;
+    memset(&kc, 0, sizeof kc);
+    kc.hidden = c->hidden;
+    kc.n_experts = c->n_experts;
+    kc.topk = c->topk;
+    kc.moe_inter = c->moe_inter;
+    kc.n_shared = c->n_shared;
+    kc.moe_renorm = c->moe_renorm;
+    kc.routed_scale = c->routed_scale;
+    kc.group = K3_MXFP4_GROUP;
+    adapter_src as;
+    memset(&as, 0, sizeof as);
+    as.base.get = adapter_get;
+    as.src = w->src;
+    k3x_moe_w kw;
+    memset(&kw, 0, sizeof kw);
+    kw.gate = w->gate;
+    kw.bias = w->bias;
+    kw.sh1 = (const uint16_t *)w->sh1;
+    kw.sh3 = (const uint16_t *)w->sh3;
+    kw.sh2 = (const uint16_t *)w->sh2;
+    kw.src = &as.base;
+    kw.layer = w->layer;
+    k3x_moe_layer *L = NULL;
+    const int rc = k3x_moe_layer_create(&kc, &kw, 0, &L);
+    if (rc) {
+        /* a failed fetch was counted in k3x_expert_drops; mirror it for the CLI check
+         * (k3_run.c:1027-1031) */
+        if (rc == K3X_E_DROP) k3_expert_drops++;
+        fprintf(stderr, "k3x: layer %d upload failed: %s\n", w->layer, k3x_strerror(rc));
+        return NULL;
+    }
+    if (g_layers[w->layer]) k3x_moe_layer_destroy(g_layers[w->layer]);
+    g_layers[w->layer] = L;
+    g_owner[w->layer] = w;
+    return L;
+}
+
+int k3_moe_gpu(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T, int *idx,
+               float *wt, float *scratch)
+{
+    (void)scratch;
+    if (!k2_form(w, c)) return -1;
+    k3x_moe_layer *L = layer_for(w, c);
+    if (!L) return -1;
+    return k3x_moe(L, out, x, T, idx, wt) == K3X_OK ? 0 : -1;
+}
+
+int k3_moe_prefill_gpu(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T,
+                       int *idx, float *wt, float *scratch)
+{
+    (void)scratch;
+    if (!k2_form(w, c)) return -1;
+    k3x_moe_layer *L = layer_for(w, c);
+    if (!L) return -1;
+    return k3x_moe_prefill(L, out, x, T, idx, wt) == K3X_OK ? 0 : -1;
+}

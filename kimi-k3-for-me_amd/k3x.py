@@ -1,0 +1,267 @@
+"""Python view of libk3x (the MoE block for MI355X), through its C ABI.
+
+Mirrors the reference's MoE interface (k3_moe / k3_moe_prefill, include/k3/k3.h:
+629-637; K3Cfg MoE fields k3.h:94-102; K3ExpertQ k3.h:507-516) with a device-resident
+layer handle.  Every call goes through lib/libk3x.so; there is no Python or CPU
+fallback: when the library is missing or no gfx950 device is visible, calls raise.
+
+Device pointers are plain integers (e.g. torch.Tensor.data_ptr()); streams are
+integers too (torch.cuda.Stream.cuda_stream) or 0 for the null stream.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libk3x.so")
+
+K3X_F32 = 0
+K3X_BF16 = 1
+DECODE_MAX_T = 8
+
+STREAM_ROUTER, STREAM_BIAS, STREAM_X, STREAM_SH1, STREAM_SH3, STREAM_SH2, STREAM_NORM = range(7)
+STREAM_CODES, STREAM_SCALES = 10, 11
+
+# the C-ABI surface declared in include/k3x_moe.h
+EXPORTS = [
+    "k3x_strerror", "k3x_moe_layer_create", "k3x_moe_layer_destroy", "k3x_moe_layer_bytes",
+    "k3x_moe_layer_read_expert", "k3x_moe_forward", "k3x_rmsnorm", "k3x_moe",
+    "k3x_moe_prefill", "k3x_expert_drops", "k3x_synth_layer_create", "k3x_synth_key",
+    "k3x_synth_normal_f32", "k3x_synth_normal_bf16", "k3x_moe_layer_set_timing",
+    "k3x_moe_layer_last_ms",
+]
+
+
+class K3XError(RuntimeError):
+    def __init__(self, status, what):
+        super().__init__(f"{what}: {strerror(status)} ({status})")
+        self.status = status
+
+
+class Cfg(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("n_experts", C.c_int), ("topk", C.c_int),
+                ("moe_inter", C.c_int), ("n_shared", C.c_int), ("moe_renorm", C.c_int),
+                ("routed_scale", C.c_float), ("group", C.c_int)]
+
+
+class ExpertQ(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("p1", "s1", "p3", "s3", "p2", "s2")]
+
+
+class ExpertSrc(C.Structure):
+    pass
+
+
+GET_FN = C.CFUNCTYPE(C.c_int, C.POINTER(ExpertSrc), C.c_int, C.c_int, C.POINTER(ExpertQ))
+ExpertSrc._fields_ = [("get", GET_FN), ("ctx", C.c_void_p)]
+
+
+class MoeW(C.Structure):
+    _fields_ = [("gate", C.c_void_p), ("bias", C.c_void_p), ("sh1", C.c_void_p),
+                ("sh3", C.c_void_p), ("sh2", C.c_void_p), ("src", C.POINTER(ExpertSrc)),
+                ("bank", C.POINTER(ExpertQ)), ("layer", C.c_int)]
+
+
+class SynthSpec(C.Structure):
+    _fields_ = [("seed", C.c_uint64), ("layer", C.c_int), ("router_sigma", C.c_double),
+                ("bias_sigma", C.c_double), ("zipf_alpha", C.c_double),
+                ("zipf_s", C.c_double), ("scale_lo", C.c_int), ("scale_hi", C.c_int),
+                ("shared_sigma", C.c_double)]
+
+
+_lib = None
+
+
+def lib():
+    """Load libk3x.so (raises when it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libk3x not built ({LIB_PATH}); run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        vp, i, f = C.c_void_p, C.c_int, C.c_float
+        L.k3x_strerror.restype = C.c_char_p
+        L.k3x_strerror.argtypes = [i]
+        L.k3x_moe_layer_create.argtypes = [C.POINTER(Cfg), C.POINTER(MoeW), i, C.POINTER(vp)]
+        L.k3x_moe_layer_destroy.argtypes = [vp]
+        L.k3x_moe_layer_destroy.restype = None
+        L.k3x_moe_layer_bytes.argtypes = [vp]
+        L.k3x_moe_layer_bytes.restype = C.c_size_t
+        L.k3x_moe_layer_read_expert.argtypes = [vp, i] + [vp] * 6
+        L.k3x_moe_forward.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
+        L.k3x_rmsnorm.argtypes = [vp, vp, vp, i, i, f, vp]
+        L.k3x_moe.argtypes = [vp, vp, vp, i, vp, vp]
+        L.k3x_moe_prefill.argtypes = [vp, vp, vp, i, vp, vp]
+        L.k3x_synth_layer_create.argtypes = [C.POINTER(Cfg), C.POINTER(SynthSpec), i,
+                                             C.POINTER(vp)]
+        L.k3x_synth_key.argtypes = [C.c_uint64, i, i, i]
+        L.k3x_synth_key.restype = C.c_uint64
+        L.k3x_synth_normal_f32.argtypes = [vp, C.c_size_t, C.c_uint64, C.c_double, C.c_double]
+        L.k3x_synth_normal_f32.restype = None
+        L.k3x_synth_normal_bf16.argtypes = [vp, C.c_size_t, C.c_uint64, C.c_double, C.c_double]
+        L.k3x_synth_normal_bf16.restype = None
+        L.k3x_moe_layer_set_timing.argtypes = [vp, i]
+        L.k3x_moe_layer_last_ms.argtypes = [vp, C.POINTER(C.c_float)]
+        _lib = L
+    return _lib
+
+
+def strerror(status):
+    try:
+        return lib().k3x_strerror(status).decode()
+    except RuntimeError:
+        return "libk3x not loaded"
+
+
+def _check(rc, what):
+    if rc < 0:
+        raise K3XError(rc, what)
+    return rc
+
+
+def expert_drops():
+    return C.c_long.in_dll(lib(), "k3x_expert_drops").value
+
+
+def make_cfg(hidden, n_experts, topk, moe_inter, n_shared=1, moe_renorm=1, routed_scale=2.5,
+             group=32):
+    return Cfg(hidden, n_experts, topk, moe_inter, n_shared, moe_renorm, routed_scale, group)
+
+
+def _vp(a):
+    return None if a is None else a.ctypes.data
+
+
+class MoELayer:
+    """A device-resident MoE layer (k3x_moe_layer)."""
+
+    def __init__(self, handle, cfg):
+        self.h = C.c_void_p(handle)
+        self.cfg = cfg
+
+    # -- construction -------------------------------------------------------------
+    @classmethod
+    def from_bank(cls, cfg, gate, bias, experts, sh1=None, sh3=None, sh2=None, device=0):
+        """experts: list of dicts with numpy uint8 arrays p1,s1,p3,s3,p2,s2."""
+        keep = [gate, bias, sh1, sh3, sh2]
+        bank = (ExpertQ * cfg.n_experts)()
+        for e, ex in enumerate(experts):
+            for k in ("p1", "s1", "p3", "s3", "p2", "s2"):
+                arr = np.ascontiguousarray(ex[k], dtype=np.uint8)
+                keep.append(arr)
+                setattr(bank[e], k, arr.ctypes.data)
+        w = MoeW(_vp(gate), _vp(bias), _vp(sh1), _vp(sh3), _vp(sh2), None,
+                 C.cast(bank, C.POINTER(ExpertQ)), 0)
+        h = C.c_void_p()
+        _check(lib().k3x_moe_layer_create(C.byref(cfg), C.byref(w), device, C.byref(h)),
+               "k3x_moe_layer_create")
+        return cls(h.value, cfg)
+
+    @classmethod
+    def from_source(cls, cfg, gate, bias, get, sh1=None, sh3=None, sh2=None, layer=0,
+                    device=0):
+        """get(layer, expert) -> dict of numpy arrays, or None for a failed fetch."""
+        hold = {}
+
+        def _get(src, lay, e, out):
+            ex = get(lay, e)
+            if ex is None:
+                return -1
+            arrs = {k: np.ascontiguousarray(ex[k], dtype=np.uint8)
+                    for k in ("p1", "s1", "p3", "s3", "p2", "s2")}
+            hold["cur"] = arrs
+            for k, a in arrs.items():
+                setattr(out.contents, k, a.ctypes.data)
+            return 0
+
+        cb = GET_FN(_get)
+        src = ExpertSrc(cb, None)
+        w = MoeW(_vp(gate), _vp(bias), _vp(sh1), _vp(sh3), _vp(sh2), C.pointer(src), None,
+                 layer)
+        h = C.c_void_p()
+        _check(lib().k3x_moe_layer_create(C.byref(cfg), C.byref(w), device, C.byref(h)),
+               "k3x_moe_layer_create")
+        return cls(h.value, cfg)
+
+    @classmethod
+    def synthetic(cls, cfg, seed=0, layer=0, router_sigma=0.02, bias_sigma=0.1, zipf_alpha=0.0,
+                  zipf_s=1.1, scale_lo=121, scale_hi=125, shared_sigma=0.02, device=0):
+        spec = SynthSpec(seed, layer, router_sigma, bias_sigma, zipf_alpha, zipf_s, scale_lo,
+                         scale_hi, shared_sigma)
+        h = C.c_void_p()
+        _check(lib().k3x_synth_layer_create(C.byref(cfg), C.byref(spec), device, C.byref(h)),
+               "k3x_synth_layer_create")
+        return cls(h.value, cfg)
+
+    def close(self):
+        if self.h:
+            lib().k3x_moe_layer_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- calls --------------------------------------------------------------------
+    def nbytes(self):
+        return lib().k3x_moe_layer_bytes(self.h)
+
+    def forward(self, out_ptr, x_ptr, T, x_dtype=K3X_F32, resid_ptr=0, idx_ptr=0, wt_ptr=0,
+                stream=0):
+        """Device pointers (ints); asynchronous on `stream`."""
+        _check(lib().k3x_moe_forward(self.h, out_ptr, x_ptr, x_dtype, T, resid_ptr or None,
+                                     idx_ptr or None, wt_ptr or None, stream or None),
+               "k3x_moe_forward")
+
+    def moe(self, x, prefill=False):
+        """Host call with k3_moe semantics: returns (out, idx_last, wt_last)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T = x.shape[0]
+        out = np.empty_like(x)
+        idx = np.zeros(self.cfg.topk, np.int32)
+        wt = np.zeros(self.cfg.topk, np.float32)
+        fn = lib().k3x_moe_prefill if prefill else lib().k3x_moe
+        _check(fn(self.h, out.ctypes.data, x.ctypes.data, T, idx.ctypes.data, wt.ctypes.data),
+               "k3x_moe")
+        return out, idx, wt
+
+    def read_expert(self, e):
+        H, I = self.cfg.hidden, self.cfg.moe_inter
+        d = {"p1": np.empty((I, H // 2), np.uint8), "s1": np.empty((I, H // 32), np.uint8),
+             "p3": np.empty((I, H // 2), np.uint8), "s3": np.empty((I, H // 32), np.uint8),
+             "p2": np.empty((H, I // 2), np.uint8), "s2": np.empty((H, I // 32), np.uint8)}
+        _check(lib().k3x_moe_layer_read_expert(self.h, e, *[d[k].ctypes.data for k in
+                                                          ("p1", "s1", "p3", "s3", "p2", "s2")]),
+               "k3x_moe_layer_read_expert")
+        return d
+
+    def set_timing(self, on):
+        _check(lib().k3x_moe_layer_set_timing(self.h, 1 if on else 0), "set_timing")
+
+    def last_ms(self):
+        ms = (C.c_float * 8)()
+        n = _check(lib().k3x_moe_layer_last_ms(self.h, ms), "last_ms")
+        return [ms[i] for i in range(n)]
+
+
+def rmsnorm(y_ptr, x_ptr, w_ptr, n, T, eps, stream=0):
+    _check(lib().k3x_rmsnorm(y_ptr, x_ptr, w_ptr, n, T, eps, stream or None), "k3x_rmsnorm")
+
+
+def synth_key(seed, layer, stream, sub=0):
+    return lib().k3x_synth_key(seed, layer, stream, sub)
+
+
+def synth_normal_f32(n, key, mu=0.0, sigma=1.0):
+    a = np.empty(n, np.float32)
+    lib().k3x_synth_normal_f32(a.ctypes.data, n, key, mu, sigma)
+    return a
+
+
+def synth_normal_bf16(n, key, mu=0.0, sigma=1.0):
+    a = np.empty(n, np.uint16)
+    lib().k3x_synth_normal_bf16(a.ctypes.data, n, key, mu, sigma)
+    return a

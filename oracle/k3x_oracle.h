@@ -1,0 +1,108 @@
+/* k3x_oracle.h - CPU restatement of the reference MoE arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the product library links, loads or calls this
+ * code; only tests/, the smoke check and the CPU-baseline leg of bench.py do, and only
+ * as the checker (or, for the baseline, as the CPU path being timed beside the GPU).
+ *
+ * Every function restates one routine of the reference engine's numeric core
+ * (src/core/k3_ops.c) with the same floating-point contract: the same accumulator
+ * partition, the same reduction tree, the same float/double conversions, compiled with
+ * -ffp-contract=off and without -ffast-math.  The file:line each one follows is in its
+ * comment.  The K2-class layer (no latent, SwiGLU, one shared expert) is expressed the
+ * way the reference's own k3_moe computes it with latent = hidden, identity down/up
+ * projections and SiTU betas of 2^64; ko_moe and ko_moe_prefill are that computation
+ * with the identity products written out (they are exact, see k3x_oracle.c).
+ *
+ * Parity status of each function (how it is pinned) is stated in its comment.
+ */
+#ifndef K3X_ORACLE_H
+#define K3X_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- primitive kernels --------------------------------------------------------- */
+float ko_e2m1(int code);                  /* k3_ops.c:2624-2627 */
+float ko_e8m0(int byte);                  /* k3_ops.c:3125-3132 (255 -> 0) */
+float ko_sigmoidf(float x);               /* k3_ops.c:143 */
+
+void ko_rmsnorm(float *y, const float *x, const float *w, int n, float eps);
+void ko_situ_glu(float *y, const float *x, int n, float b1, float b2);
+void ko_router(int *idx, float *w, const float *x, const float *W, const float *bias,
+               int hidden, int n_experts, int topk, int renorm, float routed_scale);
+/* returns 0, or -1 when in is odd or group is not a multiple of 16 (the x86 flat
+ * contract this oracle restates covers group % 16 == 0 only) */
+int  ko_matmul_mxfp4(float *y, const float *x, const uint8_t *packed,
+                     const uint8_t *scales, int in, int rows, int group);
+void ko_mxfp4_dequant(float *y, const uint8_t *packed, const uint8_t *scales, int rows,
+                      int pcols, int group);
+void ko_matmul_bf16(float *y, const float *x, const uint16_t *W, int in, int out);
+void ko_matmul_f32(float *y, const float *x, const float *W, int in, int out);
+
+/* ---- the K2-class MoE layer ---------------------------------------------------- */
+typedef struct {
+    int   hidden, n_experts, topk, moe_inter, n_shared;
+    int   renorm;
+    float routed_scale;
+    float situ_b1, situ_b2;        /* 2^64 for SwiGLU */
+    int   group;                   /* MXFP4 group, 32 */
+} ko_cfg;
+
+typedef struct {
+    const uint8_t *p1, *s1;        /* gate [I][H/2], [I][H/group] */
+    const uint8_t *p3, *s3;        /* up   [I][H/2], [I][H/group] */
+    const uint8_t *p2, *s2;        /* down [H][I/2], [H][I/group] */
+} ko_expert;
+
+/* Expert supplier, the K3ExpertSrc.get contract (k3.h:518-523): 0 on success. */
+typedef int (*ko_get_fn)(void *ctx, int expert, ko_expert *q);
+
+typedef struct {
+    const float    *gate, *bias;   /* [n_experts][hidden] fp32, [n_experts] fp32 */
+    ko_get_fn       get;
+    void           *ctx;
+    const uint16_t *sh1, *sh3;     /* bf16 [n_shared*I][hidden] */
+    const uint16_t *sh2;           /* bf16 [hidden][n_shared*I] */
+} ko_weights;
+
+/* Per token: route, run the top-k experts, combine in top-k order, add the shared
+ * expert. idx/wt receive [T][topk] routing (the reference leaves only the last token's;
+ * this keeps every token's for the tests). Returns the number of dropped experts. */
+long ko_moe(float *out, const float *x, int T, const ko_cfg *c, const ko_weights *w,
+            int *idx, float *wt);
+/* The batched-prefill form (unique experts in first-seen order per 64-token sub-chunk,
+ * contributions summed in top-k order). Bit-identical to ko_moe; get() is called once
+ * per unique expert per sub-chunk, and *n_get receives the number of get() calls. */
+long ko_moe_prefill(float *out, const float *x, int T, const ko_cfg *c,
+                    const ko_weights *w, int *idx, float *wt, long *n_get);
+
+/* Eight-layer stack step (BASELINE config 4 shape): h += MoE_l(RMSNorm_l(h)), layer by
+ * layer, following the decoder layer's MoE half (k3_ops.c:2559-2589). */
+long ko_stack_step(float *h, int T, int n_layers, const ko_cfg *c,
+                   const ko_weights *const *w, const float *const *norm_w, float eps);
+
+/* ---- synthetic inputs ---------------------------------------------------------- */
+/* The counter-based generator shared by the tests and the product's synthetic-layer
+ * builder: value i of a stream depends only on (seed, layer, stream, sub, i). */
+uint64_t ko_mix64(uint64_t z);
+uint64_t ko_key(uint64_t seed, int layer, int stream, int sub);
+uint64_t ko_draw(uint64_t key, uint64_t i);
+void ko_fill_normal_f32(float *dst, size_t n, uint64_t key, double mu, double sigma);
+void ko_fill_normal_bf16(uint16_t *dst, size_t n, uint64_t key, double mu, double sigma);
+void ko_fill_codes(uint8_t *dst, size_t n, uint64_t key);
+void ko_fill_scales(uint8_t *dst, size_t n, uint64_t key, int lo, int hi);
+void ko_zipf_bias(float *bias, int n_experts, uint64_t key, double alpha, double s);
+uint16_t ko_f32_to_bf16(float f);
+
+/* ---- bench helper -------------------------------------------------------------- */
+double ko_now(void);
+int    ko_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

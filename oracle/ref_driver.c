@@ -1,0 +1,153 @@
+/* ref_driver.c - a thin harness around the COMPILED REFERENCE (test infrastructure).
+ *
+ * Built only by oracle/Makefile's `ref` target, together with the reference's own
+ * src/core/k3_ops.c compiled where it lies, into oracle/_ref/libk3ref.so.  It exists so
+ * the tests can run the reference's k3_moe / k3_moe_prefill on a K2-class layer and
+ * compare the oracle's restatement against it bit for bit.
+ *
+ * The K2 layer is expressed with the reference's own types (k3.h:94-102, 507-569):
+ * latent = hidden with bf16 identity down/up projections, latent_norm off, SiTU betas
+ * 2^64 (SwiGLU), one shared expert, experts served through a K3ExpertSrc whose get()
+ * points into caller-owned packed MXFP4 arrays.
+ */
+#include "k3.h"
+
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef struct {
+    const unsigned char *p1, *s1, *p3, *s3, *p2, *s2;
+} drv_expert;
+
+typedef struct {
+    K3ExpertSrc       src;     /* first member: get() casts self back */
+    const drv_expert *bank;
+    int               n;
+    const int        *fail;    /* optional [n]: 1 makes get() fail (a forced drop) */
+    long              gets;
+} drv_src;
+
+static int drv_get(K3ExpertSrc *self, int layer, int e, K3ExpertQ *out)
+{
+    drv_src *s = (drv_src *)self;
+    (void)layer;
+    s->gets++;
+    if (e < 0 || e >= s->n) return -1;
+    if (s->fail && s->fail[e]) return -1;
+    out->p1 = s->bank[e].p1; out->s1 = s->bank[e].s1;
+    out->p3 = s->bank[e].p3; out->s3 = s->bank[e].s3;
+    out->p2 = s->bank[e].p2; out->s2 = s->bank[e].s2;
+    return 0;
+}
+
+static uint16_t *identity_bf16(int n)
+{
+    uint16_t *m = (uint16_t *)calloc((size_t)n * n, sizeof(uint16_t));
+    if (!m) return NULL;
+    for (int i = 0; i < n; i++) m[(size_t)i * n + i] = 0x3F80; /* 1.0 */
+    return m;
+}
+
+/* Runs k3_moe (prefill == 0) or k3_moe_prefill (prefill == 1) over T tokens.
+ * idx/wt receive the LAST token's routing (what the reference leaves there).
+ * Returns the change in k3_expert_drops; *gets receives the number of get() calls. */
+long refdrv_moe(float *out, const float *x, int T, int hidden, int n_experts, int topk,
+                int inter, int n_shared, float routed_scale, int renorm,
+                const float *gate, const float *bias, const drv_expert *bank,
+                const int *fail, const uint16_t *sh1, const uint16_t *sh3,
+                const uint16_t *sh2, int prefill, int *idx, float *wt, long *gets)
+{
+    K3Cfg c;
+    memset(&c, 0, sizeof c);
+    c.hidden = hidden;
+    c.n_experts = n_experts;
+    c.topk = topk;
+    c.n_shared = n_shared;
+    c.latent = hidden;
+    c.moe_inter = inter;
+    c.routed_scale = routed_scale;
+    c.moe_renorm = renorm;
+    c.latent_norm = 0;
+    c.situ_b1 = 0x1p64f;
+    c.situ_b2 = 0x1p64f;
+    c.rms_eps = 1e-5f;
+
+    uint16_t *eye = identity_bf16(hidden);
+    if (!eye) return -1000000;
+    drv_src s;
+    memset(&s, 0, sizeof s);
+    s.src.get = drv_get;
+    s.bank = bank;
+    s.n = n_experts;
+    s.fail = fail;
+
+    K3MoeW w;
+    memset(&w, 0, sizeof w);
+    w.gate = gate;
+    w.bias = bias;
+    w.down = eye;
+    w.up = eye;
+    w.sh1 = sh1;
+    w.sh3 = sh3;
+    w.sh2 = sh2;
+    w.wdt = K3_WBF16;
+    w.src = &s.src;
+    w.layer = 0;
+
+    float *scratch = (float *)malloc(k3_moe_scratch(&c, T) * sizeof(float));
+    if (!scratch) { free(eye); return -1000000; }
+    const long d0 = k3_expert_drops;
+    if (prefill) k3_moe_prefill(out, x, &w, &c, T, idx, wt, scratch);
+    else         k3_moe(out, x, &w, &c, T, idx, wt, scratch);
+    const long dd = k3_expert_drops - d0;
+    if (gets) *gets = s.gets;
+    free(scratch);
+    free(eye);
+    return dd;
+}
+
+/* One K2-class layer over T tokens with the reference's own kernels and nothing else:
+ * k3_router, then per selected expert 3 x k3_matmul_mxfp4 + k3_situ_glu and the float
+ * combine in top-k order (k3_ops.c:1879-1942), then the shared expert with
+ * k3_matmul_bf16 + k3_situ_glu (moe_shared, :1848-1860).  Without the identity latent
+ * projections of refdrv_moe this is the reference's work for the layer, which is what
+ * the CPU baseline times.  Bit-identical to refdrv_moe's output. idx/wt: [T][K]. */
+long refdrv_k2_tokens(float *out, const float *x, int T, int H, int E, int K, int I,
+                      int SI, float routed_scale, int renorm, const float *gate,
+                      const float *bias, const drv_expert *bank, const uint16_t *sh1,
+                      const uint16_t *sh3, const uint16_t *sh2, int *idx, float *wt)
+{
+    float *gu = (float *)malloc((size_t)2 * I * sizeof(float));
+    float *act = (float *)malloc((size_t)I * sizeof(float));
+    float *edn = (float *)malloc((size_t)H * sizeof(float));
+    float *sgu = (float *)malloc((size_t)2 * (SI > 0 ? SI : 1) * sizeof(float));
+    float *sdn = (float *)malloc((size_t)H * sizeof(float));
+    if (!gu || !act || !edn || !sgu || !sdn) return -1;
+    const float b = 0x1p64f;
+    for (int t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * H;
+        float *acc = out + (size_t)t * H;
+        int *it = idx + (size_t)t * K;
+        float *wtt = wt + (size_t)t * K;
+        k3_router(it, wtt, xt, gate, bias, H, E, K, renorm, routed_scale);
+        for (int i = 0; i < H; i++) acc[i] = 0.0f;
+        for (int j = 0; j < K; j++) {
+            const drv_expert *q = &bank[it[j]];
+            k3_matmul_mxfp4(gu, xt, q->p1, q->s1, H, I, K3_MXFP4_GROUP);
+            k3_matmul_mxfp4(gu + I, xt, q->p3, q->s3, H, I, K3_MXFP4_GROUP);
+            k3_situ_glu(act, gu, I, b, b);
+            k3_matmul_mxfp4(edn, act, q->p2, q->s2, I, H, K3_MXFP4_GROUP);
+            for (int i = 0; i < H; i++) acc[i] += wtt[j] * edn[i];
+        }
+        if (SI > 0) {
+            k3_matmul_bf16(sgu, xt, sh1, H, SI);
+            k3_matmul_bf16(sgu + SI, xt, sh3, H, SI);
+            k3_situ_glu(sgu, sgu, SI, b, b);
+            k3_matmul_bf16(sdn, sgu, sh2, SI, H);
+            for (int i = 0; i < H; i++) acc[i] += sdn[i];
+        }
+    }
+    free(gu); free(act); free(edn); free(sgu); free(sdn);
+    return 0;
+}

@@ -1,0 +1,182 @@
+"""Seeded K2-class layers on the host, from the oracle's counter-based generator.
+
+Test infrastructure.  The product library has its own implementation of the same rule
+(k3x_synth_*); tests/test_abi.py checks the two agree bit for bit, so a layer built here
+and one built by k3x_synth_layer_create hold the same weights.
+
+Streams follow include/k3x_moe.h: router 0, bias 1, x 2, sh1 3, sh3 4, sh2 5, norm 6,
+expert codes 10 and scales 11 with sub = 3*expert + {0 gate, 1 up, 2 down}.
+"""
+import ctypes as C
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from oracle_lib import (F32P, GET_FN, I32P, KoCfg, KoExpert, KoWeights, U8P, U16P, oracle,
+                        ptr)
+
+S_ROUTER, S_BIAS, S_X, S_SH1, S_SH3, S_SH2, S_NORM = range(7)
+S_CODES, S_SCALES = 10, 11
+
+
+def key(seed, layer, stream, sub=0):
+    return oracle().ko_key(seed, layer, stream, sub)
+
+
+def normal_f32(n, k, mu=0.0, sigma=1.0):
+    a = np.empty(n, np.float32)
+    oracle().ko_fill_normal_f32(ptr(a, F32P), n, k, mu, sigma)
+    return a
+
+
+def normal_bf16(n, k, mu=0.0, sigma=1.0):
+    a = np.empty(n, np.uint16)
+    oracle().ko_fill_normal_bf16(ptr(a, U16P), n, k, mu, sigma)
+    return a
+
+
+def codes(n, k):
+    a = np.empty(n, np.uint8)
+    oracle().ko_fill_codes(ptr(a, U8P), n, k)
+    return a
+
+
+def scales(n, k, lo, hi):
+    a = np.empty(n, np.uint8)
+    oracle().ko_fill_scales(ptr(a, U8P), n, k, lo, hi)
+    return a
+
+
+def bf16_to_f32(h):
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(f):
+    u = np.ascontiguousarray(f, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+@dataclass
+class Layer:
+    H: int
+    E: int
+    K: int
+    I: int
+    n_shared: int = 1
+    seed: int = 0
+    layer: int = 0
+    router_sigma: float = 0.02
+    bias_sigma: float = 0.1
+    zipf_alpha: float = 0.0
+    zipf_s: float = 1.1
+    scale_lo: int = 121
+    scale_hi: int = 125
+    shared_sigma: float = 0.02
+    routed_scale: float = 2.5
+    renorm: int = 1
+    gate: np.ndarray = None
+    bias: np.ndarray = None
+    sh1: np.ndarray = None
+    sh3: np.ndarray = None
+    sh2: np.ndarray = None
+    _cache: dict = field(default_factory=dict)
+
+    def __post_init__(self):
+        H, E, I, SI = self.H, self.E, self.I, self.I * self.n_shared
+        s, l = self.seed, self.layer
+        self.gate = normal_f32(E * H, key(s, l, S_ROUTER), 0.0, self.router_sigma).reshape(E, H)
+        if self.zipf_alpha > 0:
+            self.bias = np.empty(E, np.float32)
+            oracle().ko_zipf_bias(ptr(self.bias, F32P), E, key(s, l, S_BIAS), self.zipf_alpha,
+                                  self.zipf_s)
+        else:
+            self.bias = normal_f32(E, key(s, l, S_BIAS), 0.0, self.bias_sigma)
+        if SI > 0:
+            self.sh1 = normal_bf16(SI * H, key(s, l, S_SH1), 0.0, self.shared_sigma).reshape(SI, H)
+            self.sh3 = normal_bf16(SI * H, key(s, l, S_SH3), 0.0, self.shared_sigma).reshape(SI, H)
+            self.sh2 = normal_bf16(H * SI, key(s, l, S_SH2), 0.0, self.shared_sigma).reshape(H, SI)
+
+    def expert(self, e):
+        """Expert e's six arrays in the reference's row-major layout (cached)."""
+        if e in self._cache:
+            return self._cache[e]
+        H, I, s, l = self.H, self.I, self.seed, self.layer
+        d = {}
+        for m, (pk, sk, R, Kc) in enumerate((("p1", "s1", I, H), ("p3", "s3", I, H),
+                                             ("p2", "s2", H, I))):
+            d[pk] = codes(R * Kc // 2, key(s, l, S_CODES, 3 * e + m)).reshape(R, Kc // 2)
+            d[sk] = scales(R * Kc // 32, key(s, l, S_SCALES, 3 * e + m), self.scale_lo,
+                           self.scale_hi).reshape(R, Kc // 32)
+        if len(self._cache) > 64:
+            self._cache.clear()
+        self._cache[e] = d
+        return d
+
+    def x(self, T, bf16=True, stream_sub=0):
+        """T tokens N(0,1); rounded to bf16 values (returned as fp32) when bf16."""
+        v = normal_f32(T * self.H, key(self.seed, self.layer, S_X, stream_sub)).reshape(T, self.H)
+        if bf16:
+            v = bf16_to_f32(f32_to_bf16(v)).reshape(T, self.H)
+        return v
+
+    # ---- the oracle on this layer ------------------------------------------------
+    def ko_cfg(self):
+        return KoCfg(self.H, self.E, self.K, self.I, self.n_shared, self.renorm,
+                     self.routed_scale, 2.0 ** 64, 2.0 ** 64, 32)
+
+    def _weights(self, fail=None):
+        keep = []
+
+        def get(ctx, e, q):
+            if fail is not None and e in fail:
+                return -1
+            d = self.expert(e)
+            keep.append(d)
+            for k in ("p1", "s1", "p3", "s3", "p2", "s2"):
+                setattr(q.contents, k, d[k].ctypes.data_as(U8P))
+            return 0
+
+        cb = GET_FN(get)
+        w = KoWeights(ptr(self.gate, F32P), ptr(self.bias, F32P), cb, None,
+                      ptr(self.sh1, U16P), ptr(self.sh3, U16P), ptr(self.sh2, U16P))
+        return w, cb, keep
+
+    def oracle_moe(self, x, prefill=False, fail=None):
+        x = np.ascontiguousarray(x, np.float32)
+        T = x.shape[0]
+        out = np.empty_like(x)
+        idx = np.empty((T, self.K), np.int32)
+        wt = np.empty((T, self.K), np.float32)
+        cfg = self.ko_cfg()
+        w, cb, keep = self._weights(fail)
+        if prefill:
+            ng = C.c_long(0)
+            drops = oracle().ko_moe_prefill(ptr(out, F32P), ptr(x, F32P), T, C.byref(cfg),
+                                            C.byref(w), ptr(idx, I32P), ptr(wt, F32P),
+                                            C.byref(ng))
+            return out, idx, wt, drops, ng.value
+        drops = oracle().ko_moe(ptr(out, F32P), ptr(x, F32P), T, C.byref(cfg), C.byref(w),
+                                ptr(idx, I32P), ptr(wt, F32P))
+        return out, idx, wt, drops
+
+    def all_experts(self):
+        return [self.expert(e) for e in range(self.E)]
+
+
+def tiny(seed=0, **kw):
+    """The reference-CPU-path configuration: H 256, 16 experts top-4, I 128, 1 shared."""
+    return Layer(H=256, E=16, K=4, I=128, seed=seed, **kw)
+
+
+def full(seed=0, **kw):
+    """The K2-class shape: H 7168, 384 experts top-8, I 2048, 1 bf16 shared expert."""
+    return Layer(H=7168, E=384, K=8, I=2048, seed=seed, **kw)
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))

@@ -41,13 +41,17 @@ def load_k3x():
     return mod
 
 
+KERNELS = ["k1_router_shared", "k1b_select_shdown", "k2_gateup", "k3_down"]
+
+
 def kernel_bytes(U, T):
-    """Algorithmic HBM bytes per launch of the three decode kernels (each weight byte
-    once, activations included)."""
+    """Algorithmic HBM bytes per launch of the four decode kernels (each weight byte
+    once; activations included)."""
     k1 = B_ROUTER + 2 * SI * H * 2 + T * H * 2
+    k1b = H * SI * 2 + T * H * 4
     k2 = U * 2 * (I * H // 2 + I * H // 32)
-    k3 = U * (H * I // 2 + H * I // 32) + H * SI * 2 + T * H * 4
-    return {"k1_router_shared": k1, "k2_gateup": k2, "k3_down": k3}
+    k3 = U * (H * I // 2 + H * I // 32) + 2 * T * H * 4
+    return dict(zip(KERNELS, (k1, k1b, k2, k3)))
 
 
 def cpu_baseline(n_tokens=24, min_seconds=10.0):
@@ -157,7 +161,7 @@ def main():
 
     # per-kernel durations: HIP events between the kernels, on the launch stream
     layer.set_timing(True)
-    names = ["k1_router_shared", "k2_gateup", "k3_down"]
+    names = KERNELS
     per = {n: [] for n in names}
     with torch.cuda.stream(stream):
         for i in range(args.steps):

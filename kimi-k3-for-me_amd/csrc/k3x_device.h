@@ -1,0 +1,285 @@
+// k3x_device.h - device helpers shared by the gfx950 kernels: bf16 rounding, the
+// reference's sigmoid and SwiGLU, MXFP4 dequantisation into matrix-core operands, the
+// bf16 MFMA, range-checked buffer loads and the tiled-layout offsets (k3x_internal.h
+// describes the layouts).
+#ifndef K3X_DEVICE_H
+#define K3X_DEVICE_H
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "k3x_internal.h"
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+#define WAVE 64
+
+// ------------------------------------------------------------------ rounding
+__device__ __forceinline__ uint32_t f2bf(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+
+// v = hi + lo with hi, lo bf16: hi = rne(v), lo = rne(v - hi) (v - hi is exact).
+__device__ __forceinline__ void split_bf16(float v, uint32_t &hi, uint32_t &lo)
+{
+    hi = f2bf(v);
+    lo = f2bf(v - bf2f(hi));
+}
+
+// ------------------------------------------------------------------ reference math
+// The reference's sigmoid, 1/(1+expf(-x)) in float (k3_ops.c:143).  exp is evaluated in
+// double and rounded once: the correctly rounded expf(-x) except within ~2^-29
+// relative of a float rounding midpoint.
+__device__ __forceinline__ float sigmoid_ref(float x)
+{
+    const float e = (float)exp(-(double)x);
+    return 1.0f / (1.0f + e);
+}
+
+// SwiGLU as k3_situ_glu computes it at 2^64 betas: a = g*sigmoid(g), y = a*u, in float.
+__device__ __forceinline__ float swiglu(float g, float u)
+{
+    const float a = g * sigmoid_ref(g);
+    return a * u;
+}
+
+// ------------------------------------------------------------------ MXFP4 -> bf16
+// 8 E2M1 codes (one dword, low nibble = lower column) times 2^(s-127) -> 8 bf16, exact
+// for scale bytes 1..252 (v_cvt_scalef32_pk_bf16_fp4 takes the scale as an fp32 power
+// of two; from byte 253 on, 6 x 2^(s-127) overflows bf16).  Other bytes take dq8_exact.
+__device__ __forceinline__ bf16x8 dq8(uint32_t codes, float scale)
+{
+    const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, scale, 0);
+    const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, scale, 1);
+    const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, scale, 2);
+    const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(codes, scale, 3);
+    bf16x8 r = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+    return r;
+}
+
+__device__ __forceinline__ float e8m0_scale(uint32_t b) { return __uint_as_float(b << 23); }
+
+// Any E8M0 byte, the reference's way (k3_ops.c:3125-3132, :3427-3433): the weight is the
+// float product E2M1[c] * 2^(b-127) (2^-127 subnormal for byte 0, zero for 255, inf on
+// overflow), rounded to bf16 (exact except where that float is below bf16's range).
+__device__ __attribute__((noinline)) bf16x8 dq8_exact(uint32_t codes, uint32_t b)
+{
+    const float sc = (b == 255u) ? 0.0f : (b == 0u ? __uint_as_float(0x00400000u)
+                                                   : __uint_as_float(b << 23));
+    uint32_t h[8];
+    for (int j = 0; j < 8; j++) {
+        const uint32_t c = (codes >> (4 * j)) & 15u;
+        const uint32_t m = c & 7u;
+        const float mag = m == 0 ? 0.0f : (m == 1 ? 0.5f : (float)(2 + (m & 1)) * (float)(1u << ((m >> 1) - 1)) * 0.5f);
+        const float v = (c & 8u) ? -mag : mag;
+        h[j] = f2bf(v * sc);
+    }
+    u32x4 r = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
+
+// Weights are streamed once per call: non-temporal loads keep them from displacing
+// reused data (activations, B fragments) in the caches.
+__device__ __forceinline__ u32x4 ldw16(const void *p)
+{
+    return __builtin_nontemporal_load((const u32x4 *)p);
+}
+__device__ __forceinline__ uint32_t ldw4(const void *p)
+{
+    return __builtin_nontemporal_load((const uint32_t *)p);
+}
+
+// ------------------------------------------------------------------ buffer loads
+// Range-checked loads: an offset at or beyond the buffer's size returns zeros without a
+// memory access (used for B-fragment lanes whose column holds no token).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+#define K3X_OOB 0xFFFFFFF0u
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// ------------------------------------------------------------------ layout offsets
+__device__ __forceinline__ size_t fp4_tile_bytes(int K)
+{
+    const int nq = K >> 7, ns = (nq + 3) >> 2;
+    return (size_t)nq * 1024 + (size_t)ns * 256;
+}
+
+// COMPACT B FRAGMENTS of NC = 2T live columns: entry (q, t, kq, n) holds the 8 bf16 of
+// column n at K-indices 128q + 32kq + 8t .. +7, stored at entry index
+// ((q*4 + t)*4 + kq)*NC + n, 16 bytes each; K*NC*2 bytes for a K-long set.
+// Element offset (bf16 units) of K-index r, column n:
+__device__ __forceinline__ size_t bfrag_off(int r, int n, int NC)
+{
+    const int q = r >> 7, kq = (r & 127) >> 5, t = (r & 31) >> 3, j = r & 7;
+    return ((((size_t)q * 4 + t) * 4 + kq) * NC + n) * 8 + j;
+}
+
+// ------------------------------------------------------------------ activations
+// 4 / 8 consecutive activations (base a multiple of 4 / 8), widened to float.
+__device__ __forceinline__ void load_x4(const void *x, int bf, size_t base, float (&v)[4])
+{
+    if (bf) {
+        const u32x2 r = *(const u32x2 *)((const uint16_t *)x + base);
+        v[0] = bf2f(r[0] & 0xFFFFu); v[1] = bf2f(r[0] >> 16);
+        v[2] = bf2f(r[1] & 0xFFFFu); v[3] = bf2f(r[1] >> 16);
+    } else {
+        const f32x4 r = *(const f32x4 *)((const float *)x + base);
+        v[0] = r[0]; v[1] = r[1]; v[2] = r[2]; v[3] = r[3];
+    }
+}
+
+__device__ __forceinline__ void load_x8(const void *x, int bf, size_t base, float (&v)[8])
+{
+    if (bf) {
+        const u32x4 r = ld16((const uint16_t *)x + base);
+        for (int j = 0; j < 4; j++) { v[2 * j] = bf2f(r[j] & 0xFFFFu); v[2 * j + 1] = bf2f(r[j] >> 16); }
+    } else {
+        const f32x4 r0 = *(const f32x4 *)((const float *)x + base);
+        const f32x4 r1 = *(const f32x4 *)((const float *)x + base + 4);
+        for (int j = 0; j < 4; j++) { v[j] = r0[j]; v[4 + j] = r1[j]; }
+    }
+}
+
+// One B fragment (8 bf16 of the hi or the lo column) from 8 activations.
+__device__ __forceinline__ u32x4 bfrag_of(const float (&v)[8], int hl)
+{
+    uint32_t h[8];
+    for (int j = 0; j < 8; j++) {
+        uint32_t hi, lo;
+        split_bf16(v[j], hi, lo);
+        h[j] = hl ? lo : hi;
+    }
+    u32x4 r = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    return r;
+}
+
+// ------------------------------------------------------------------ quad streaming
+// One quad of a tiled fp4 matrix for this lane: 16 code bytes (4 products x 8 codes) and
+// the super-quad's scale dword (the quad's byte is picked when it is used, so a prefetch
+// never waits for its own data).
+struct Q4 {
+    u32x4    c;
+    uint32_t s;
+};
+
+__device__ __forceinline__ size_t fp4_quad_off(int q)
+{
+    return (size_t)(q >> 2) * 4352 + (size_t)(q & 3) * 1024;
+}
+__device__ __forceinline__ size_t fp4_scale_off(int q, int nQ)
+{
+    const int S = q >> 2, nq = min(4, nQ - 4 * S);
+    return (size_t)S * 4352 + (size_t)nq * 1024;
+}
+
+__device__ __forceinline__ void q4_load(Q4 &a, const uint8_t *tile, int q, int nQ, int lane)
+{
+    a.c = ldw16(tile + fp4_quad_off(q) + lane * 16);
+    a.s = ldw4(tile + fp4_scale_off(q, nQ) + lane * 4);
+}
+
+// Four B fragments of quad q (products t = 0..3) through a range-checked buffer.
+struct B4 {
+    u32x4 b[4];
+};
+
+// Where a lane's B fragments come from: a compact B-fragment set of NC columns at byte
+// offset `boff`, either in global memory through a range-checked buffer (lanes whose
+// column is not live read zeros without an access) or staged in LDS (those lanes read a
+// zero entry placed after the set).
+struct BSrc {
+    rsrc_t         r;
+    const uint8_t *lds;      // staged copy, or nullptr
+    uint32_t       zero;     // byte offset of the zero entry in the staged copy
+    int            NC;
+};
+
+__device__ __forceinline__ void b4_load(B4 &b, const BSrc &s, uint32_t boff, int q, int lane,
+                                        bool live)
+{
+    const int n = lane & 15, kq = lane >> 4;
+    const uint32_t e0 = boff + (uint32_t)(((q * 4) * 4 + kq) * s.NC + n) * 16u;
+    const uint32_t ts = (uint32_t)(4 * s.NC * 16);
+    const bool on = live && n < s.NC;
+    if (s.lds) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            b.b[t] = *(const u32x4 *)(s.lds + (on ? e0 + ts * t : s.zero));
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; t++) b.b[t] = bload16(s.r, on ? e0 + ts * t : K3X_OOB);
+    }
+}
+
+// Stage `bytes` (a multiple of 16) of a compact B set into LDS and append a zero entry;
+// all threads of the workgroup take part; returns the zero entry's offset.
+__device__ __forceinline__ uint32_t stage_b(uint8_t *lds, const void *src, uint32_t bytes,
+                                            int tid, int nthreads)
+{
+    for (uint32_t o = (uint32_t)tid * 16u; o < bytes; o += (uint32_t)nthreads * 16u)
+        *(u32x4 *)(lds + o) = ld16((const uint8_t *)src + o);
+    if (tid == 0) *(u32x4 *)(lds + bytes) = (u32x4){0u, 0u, 0u, 0u};
+    return bytes;
+}
+
+// d += dequant(a) x b for one quad (its scale byte is byte `sel` of a.s).  EXACT takes
+// the reference's float product for any scale byte; the fast path needs bytes 1..252
+// (every weight finite; the layer records per expert which path its bytes need).
+// `valid` false marks a padding quad (zero B fragments): the exact path then zeroes the
+// codes too, so an infinite weight cannot turn the zero product into NaN.
+template <bool EXACT>
+__device__ __forceinline__ void q4_mfma(f32x4 &d, const Q4 &a, int sel, const B4 &b,
+                                        bool valid = true)
+{
+    const uint32_t sb = (a.s >> (8 * sel)) & 255u;
+    if (!EXACT) {
+        const float sc = e8m0_scale(sb);
+#pragma unroll
+        for (int t = 0; t < 4; t++) d = mfma(dq8(a.c[t], sc), as_bf16x8(b.b[t]), d);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            d = mfma(dq8_exact(valid ? a.c[t] : 0u, sb), as_bf16x8(b.b[t]), d);
+    }
+}
+
+// Cross-wave sum of per-lane accumulators through LDS; wave 0 ends with the total.
+template <int NV, int NW>
+__device__ __forceinline__ void wave_sum_lds(float (&acc)[NV], float *lds, int wave, int lane)
+{
+    if (wave != 0)
+        for (int v = 0; v < NV; v++) lds[((wave - 1) * NV + v) * WAVE + lane] = acc[v];
+    __syncthreads();
+    if (wave == 0)
+        for (int w = 1; w < NW; w++)
+            for (int v = 0; v < NV; v++) acc[v] += lds[((w - 1) * NV + v) * WAVE + lane];
+}
+
+#endif

@@ -62,7 +62,7 @@ typedef struct k3x_route {
     int   nu;                                   /* unique experts in this call        */
     int   pad[63];
     int   uniq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];        /* first-seen order           */
-    float wtok[K3X_DECODE_MAX_T * K3X_MAX_TOPK][K3X_DECODE_MAX_T]; /* [u][token] weight, 0 = not routed */
+    float wtok[K3X_DECODE_MAX_T * K3X_MAX_TOPK][K3X_DECODE_MAX_T]; /* [u][token], 0 = not chosen */
 } k3x_route;
 
 /* prefill working buffers, grown on demand */
@@ -97,17 +97,18 @@ struct k3x_moe_layer {
     float    *bias;               /* [E] (zeros when absent) */
     uint8_t  *experts;            /* E * expert_bytes */
     size_t    expert_bytes, gate_off, up_off, down_off;
+    int      *xflags;             /* [E] bit 0 gate, 1 up, 2 down: a scale byte outside
+                                     1..252 (the exact dequantisation path is needed) */
     uint16_t *sh_gate, *sh_up, *sh_down;   /* tiled bf16, NULL when SI == 0 */
     /* decode working buffers */
     float    *score, *choice;     /* [DECODE_MAX_T][E] */
     int      *idx;                /* [DECODE_MAX_T][K] */
     float    *wt;                 /* [DECODE_MAX_T][K] */
-    unsigned *counter;            /* last-workgroup ticket of the router */
     k3x_route *route;
     uint16_t *xB;                 /* B fragments of x: [H/128][4][64][8] */
     uint16_t *actB;               /* [DECODE_MAX_T*K][I/128][4][64][8] */
     uint16_t *shB;                /* [SI/128][4][64][8] */
-    float    *shpart;             /* [2 mats][2 halves][SI][16] */
+    float    *ysh;                /* [DECODE_MAX_T][H] shared expert output */
     k3x_prefill_buf pf;
     size_t    bytes;
     /* timing */

@@ -1,0 +1,209 @@
+// k3x_layout.hip - moving weights into the layer's HBM layouts (k3x_internal.h): the
+// tiled MXFP4 and bf16 formats, their inverse, the synthetic-layer generator (writing
+// tiled bytes directly), and the device RMSNorm (k3_rmsnorm, k3_ops.c:132-140).
+#include <string.h>
+
+#include "k3x_device.h"
+
+#define NT 256
+
+// ------------------------------------------------------------------ layout kernels
+__global__ void tile_fp4_kernel(uint8_t *dst, const uint8_t *packed, const uint8_t *scales,
+                                int R, int K)
+{
+    const int nQ = K >> 7, nS = (nQ + 3) >> 2, tiles = R >> 4;
+    const size_t tb = fp4_tile_bytes(K);
+    const long total = (long)tiles * nS * 64;
+    for (long f = blockIdx.x * (long)blockDim.x + threadIdx.x; f < total;
+         f += (long)gridDim.x * blockDim.x) {
+        const int l = f & 63;
+        const int S = (f >> 6) % nS;
+        const int rt = (int)((f >> 6) / nS);
+        const int m = l & 15, kq = l >> 4;
+        const int row = rt * 16 + m;
+        const int nq = min(4, nQ - 4 * S);
+        uint8_t *so = dst + (size_t)rt * tb + (size_t)S * 4352;
+        uint32_t sw = 0;
+        for (int j = 0; j < nq; j++) {
+            const int q = 4 * S + j;
+            const uint8_t *src = packed + (size_t)row * (K / 2) + (size_t)(128 * q + 32 * kq) / 2;
+            for (int b = 0; b < 16; b++) so[j * 1024 + l * 16 + b] = src[b];
+            sw |= (uint32_t)scales[(size_t)row * (K / 32) + 4 * q + kq] << (8 * j);
+        }
+        *(uint32_t *)(so + nq * 1024 + l * 4) = sw;
+    }
+}
+
+__global__ void untile_fp4_kernel(uint8_t *packed, uint8_t *scales, const uint8_t *src,
+                                  int R, int K)
+{
+    const int nQ = K >> 7, nS = (nQ + 3) >> 2, tiles = R >> 4;
+    const size_t tb = fp4_tile_bytes(K);
+    const long total = (long)tiles * nS * 64;
+    for (long f = blockIdx.x * (long)blockDim.x + threadIdx.x; f < total;
+         f += (long)gridDim.x * blockDim.x) {
+        const int l = f & 63;
+        const int S = (f >> 6) % nS;
+        const int rt = (int)((f >> 6) / nS);
+        const int m = l & 15, kq = l >> 4;
+        const int row = rt * 16 + m;
+        const int nq = min(4, nQ - 4 * S);
+        const uint8_t *so = src + (size_t)rt * tb + (size_t)S * 4352;
+        const uint32_t sw = *(const uint32_t *)(so + nq * 1024 + l * 4);
+        for (int j = 0; j < nq; j++) {
+            const int q = 4 * S + j;
+            uint8_t *d = packed + (size_t)row * (K / 2) + (size_t)(128 * q + 32 * kq) / 2;
+            for (int b = 0; b < 16; b++) d[b] = so[j * 1024 + l * 16 + b];
+            scales[(size_t)row * (K / 32) + 4 * q + kq] = (uint8_t)(sw >> (8 * j));
+        }
+    }
+}
+
+__global__ void tile_bf16_kernel(uint16_t *dst, const uint16_t *src, int R, int K)
+{
+    const int nQ = K >> 7;
+    const long total = (long)(R >> 4) * nQ * 4 * 64;      // one 8-element run each
+    for (long f = blockIdx.x * (long)blockDim.x + threadIdx.x; f < total;
+         f += (long)gridDim.x * blockDim.x) {
+        const int l = f & 63, t = (f >> 6) & 3;
+        const long qt = f >> 8;
+        const int q = qt % nQ, rt = (int)(qt / nQ);
+        const int m = l & 15, kq = l >> 4;
+        const uint16_t *s = src + (size_t)(rt * 16 + m) * K + 128 * q + 32 * kq + 8 * t;
+        uint16_t *d = dst + (size_t)f * 8;
+        for (int j = 0; j < 8; j++) d[j] = s[j];
+    }
+}
+
+// splitmix64 finaliser and counter draw (the synthetic-layer rule, k3x_moe.h)
+__device__ __forceinline__ uint64_t mix64(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint64_t draw(uint64_t key, uint64_t i)
+{
+    return mix64(key + (i + 1) * 0x9E3779B97F4A7C15ull);
+}
+
+// Synthetic expert matrix written straight into the tiled layout: code byte i of the
+// row-major packed array is byte (i % 8) of draw(code_key, i / 8); scale byte i is
+// lo + (draw(scale_key, i) >> 32) % (hi - lo + 1).
+__global__ void synth_fp4_kernel(uint8_t *dst, int R, int K, uint64_t ck, uint64_t sk,
+                                 int lo, int hi)
+{
+    const int nQ = K >> 7, nS = (nQ + 3) >> 2, tiles = R >> 4;
+    const size_t tb = fp4_tile_bytes(K);
+    const uint64_t span = (uint64_t)(hi - lo + 1);
+    const long total = (long)tiles * nS * 64;
+    for (long f = blockIdx.x * (long)blockDim.x + threadIdx.x; f < total;
+         f += (long)gridDim.x * blockDim.x) {
+        const int l = f & 63;
+        const int S = (f >> 6) % nS;
+        const int rt = (int)((f >> 6) / nS);
+        const int m = l & 15, kq = l >> 4;
+        const int row = rt * 16 + m;
+        const int nq = min(4, nQ - 4 * S);
+        uint8_t *so = dst + (size_t)rt * tb + (size_t)S * 4352;
+        uint32_t sw = 0;
+        for (int j = 0; j < nq; j++) {
+            const int q = 4 * S + j;
+            const uint64_t i0 = (uint64_t)row * (K / 2) + (uint64_t)(128 * q + 32 * kq) / 2;
+            // i0 is a multiple of 16, so the 16 bytes are two whole draws
+            const uint64_t d0 = draw(ck, i0 >> 3), d1 = draw(ck, (i0 >> 3) + 1);
+            u32x4 v = {(uint32_t)d0, (uint32_t)(d0 >> 32), (uint32_t)d1, (uint32_t)(d1 >> 32)};
+            *(u32x4 *)(so + j * 1024 + l * 16) = v;
+            const uint64_t si = (uint64_t)row * (K / 32) + 4 * q + kq;
+            sw |= (uint32_t)(lo + (int)((draw(sk, si) >> 32) % span)) << (8 * j);
+        }
+        *(uint32_t *)(so + nq * 1024 + l * 4) = sw;
+    }
+}
+
+// ------------------------------------------------------------------ RMSNorm
+__global__ void __launch_bounds__(NT) rmsnorm_kernel(float *y, const float *x, const float *w,
+                                                      int n, float eps)
+{
+    __shared__ double red[NT / WAVE];
+    const float *xr = x + (size_t)blockIdx.x * n;
+    float *yr = y + (size_t)blockIdx.x * n;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n; i += NT) ss += (double)xr[i] * (double)xr[i];
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x / WAVE] = ss;
+    __syncthreads();
+    double tot = 0.0;
+    for (int i = 0; i < NT / WAVE; i++) tot += red[i];
+    const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
+    for (int i = threadIdx.x; i < n; i += NT) yr[i] = w[i] * xr[i] * inv;
+}
+
+// ------------------------------------------------------------------ launchers
+
+static inline int hip_ok(hipError_t e) { return e == hipSuccess ? 0 : K3X_E_HIP; }
+static inline int launch_ok(void) { return hip_ok(hipGetLastError()); }
+
+static int grid_for(long total, int block)
+{
+    long g = (total + block - 1) / block;
+    if (g < 1) g = 1;
+    if (g > 65535L * 16) g = 65535L * 16;
+    return (int)g;
+}
+
+extern "C" int k3x_dev_check(int device)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) return K3X_E_NODEV;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device) != hipSuccess) return K3X_E_NODEV;
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) return K3X_E_NODEV;   // gfx950 only
+    return 0;
+}
+
+extern "C" int k3x_dev_tile_fp4(uint8_t *dst, const uint8_t *packed, const uint8_t *scales,
+                                int R, int K, void *stream)
+{
+    const long total = (long)(R >> 4) * (((K >> 7) + 3) >> 2) * 64;
+    hipLaunchKernelGGL(tile_fp4_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+                       (hipStream_t)stream, dst, packed, scales, R, K);
+    return launch_ok();
+}
+
+extern "C" int k3x_dev_untile_fp4(uint8_t *packed, uint8_t *scales, const uint8_t *src,
+                                  int R, int K, void *stream)
+{
+    const long total = (long)(R >> 4) * (((K >> 7) + 3) >> 2) * 64;
+    hipLaunchKernelGGL(untile_fp4_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+                       (hipStream_t)stream, packed, scales, src, R, K);
+    return launch_ok();
+}
+
+extern "C" int k3x_dev_tile_bf16(uint16_t *dst, const uint16_t *src, int R, int K,
+                                 void *stream)
+{
+    const long total = (long)(R >> 4) * (K >> 7) * 4 * 64;
+    hipLaunchKernelGGL(tile_bf16_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+                       (hipStream_t)stream, dst, src, R, K);
+    return launch_ok();
+}
+
+extern "C" int k3x_dev_synth_fp4(uint8_t *dst, int R, int K, uint64_t code_key,
+                                 uint64_t scale_key, int lo, int hi, void *stream)
+{
+    const long total = (long)(R >> 4) * (((K >> 7) + 3) >> 2) * 64;
+    hipLaunchKernelGGL(synth_fp4_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+                       (hipStream_t)stream, dst, R, K, code_key, scale_key, lo, hi);
+    return launch_ok();
+}
+
+extern "C" int k3x_dev_rmsnorm(float *y, const float *x, const float *w, int n, int T,
+                               float eps, void *stream)
+{
+    if (T <= 0) return 0;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(NT), 0, (hipStream_t)stream, y, x, w,
+                       n, eps);
+    return launch_ok();
+}
+

@@ -89,22 +89,21 @@ static int layer_alloc(k3x_moe_layer *L)
     RCCHK(dmalloc((void **)&L->router, (size_t)E * H * 4, b));
     RCCHK(dmalloc((void **)&L->bias, (size_t)E * 4, b));
     RCCHK(dmalloc((void **)&L->experts, (size_t)E * L->expert_bytes, b));
+    RCCHK(dmalloc((void **)&L->xflags, (size_t)E * sizeof(int), b));
     if (L->SI > 0) {
         RCCHK(dmalloc((void **)&L->sh_gate, k3x_bf16_matrix_bytes(L->SI, H), b));
         RCCHK(dmalloc((void **)&L->sh_up, k3x_bf16_matrix_bytes(L->SI, H), b));
         RCCHK(dmalloc((void **)&L->sh_down, k3x_bf16_matrix_bytes(H, L->SI), b));
         RCCHK(dmalloc((void **)&L->shB, (size_t)L->SI * 16 * 2, b));
-        RCCHK(dmalloc((void **)&L->shpart, (size_t)4 * L->SI * 16 * 4, b));
+        RCCHK(dmalloc((void **)&L->ysh, (size_t)K3X_DECODE_MAX_T * H * 4, b));
     }
     RCCHK(dmalloc((void **)&L->score, (size_t)K3X_DECODE_MAX_T * E * 4, b));
     RCCHK(dmalloc((void **)&L->choice, (size_t)K3X_DECODE_MAX_T * E * 4, b));
     RCCHK(dmalloc((void **)&L->idx, (size_t)K3X_DECODE_MAX_T * K * 4, b));
     RCCHK(dmalloc((void **)&L->wt, (size_t)K3X_DECODE_MAX_T * K * 4, b));
-    RCCHK(dmalloc((void **)&L->counter, 256, b));
     RCCHK(dmalloc((void **)&L->route, sizeof(k3x_route), b));
     RCCHK(dmalloc((void **)&L->xB, (size_t)H * 16 * 2, b));
     RCCHK(dmalloc((void **)&L->actB, (size_t)K3X_DECODE_MAX_T * K * I * 16 * 2, b));
-    if (hipMemset(L->counter, 0, 256) != hipSuccess) return K3X_E_HIP;
     if (hipMemset(L->bias, 0, (size_t)E * 4) != hipSuccess) return K3X_E_HIP;
     return 0;
 fail:
@@ -114,8 +113,8 @@ fail:
 static void layer_free(k3x_moe_layer *L)
 {
     if (!L) return;
-    void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shB,
-                 L->shpart, L->score, L->choice, L->idx, L->wt, L->counter, L->route,
+    void *p[] = {L->router, L->bias, L->experts, L->xflags, L->sh_gate, L->sh_up, L->sh_down, L->shB,
+                 L->ysh, L->score, L->choice, L->idx, L->wt, L->route,
                  L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out};
     for (size_t i = 0; i < sizeof p / sizeof p[0]; i++)
         if (p[i]) hipFree(p[i]);
@@ -174,6 +173,19 @@ fail:
     return rc;
 }
 
+/* Bit m of the result: matrix m (0 gate, 1 up, 2 down) has a scale byte outside 1..252,
+ * where a weight can be zero-scaled, subnormal-scaled or infinite and the kernels take
+ * the exact dequantisation path. */
+static int scale_flags(const k3x_expert_q *q, size_t sg)
+{
+    const unsigned char *s[3] = {q->s1, q->s3, q->s2};
+    int f = 0;
+    for (int m = 0; m < 3; m++)
+        for (size_t i = 0; i < sg; i++)
+            if (s[m][i] == 0 || s[m][i] >= 253) { f |= 1 << m; break; }
+    return f;
+}
+
 /* One expert: its six arrays copied to a staging area, then tiled into the arena. */
 static int upload_expert(k3x_moe_layer *L, int e, const k3x_expert_q *q, uint8_t *stage)
 {
@@ -210,10 +222,13 @@ int k3x_moe_layer_create(const k3x_cfg *c, const k3x_moe_w *w, int device,
     if (rc) return rc;
     const int H = c->hidden, E = c->n_experts, I = c->moe_inter;
     uint8_t *stage = NULL;
+    int *flags = NULL;
     HIPCHK(hipMemcpy(L->router, w->gate, (size_t)E * H * 4, hipMemcpyHostToDevice));
     if (w->bias) HIPCHK(hipMemcpy(L->bias, w->bias, (size_t)E * 4, hipMemcpyHostToDevice));
     RCCHK(upload_shared(L, w->sh1, w->sh3, w->sh2));
     HIPCHK(hipMalloc((void **)&stage, 3 * ((size_t)I * H / 2 + (size_t)I * H / 32)));
+    flags = (int *)calloc((size_t)E, sizeof(int));
+    if (!flags) { rc = K3X_E_NOMEM; goto fail; }
     for (int e = 0; e < E; e++) {
         k3x_expert_q q;
         if (w->src) {
@@ -229,12 +244,16 @@ int k3x_moe_layer_create(const k3x_cfg *c, const k3x_moe_w *w, int device,
             q = w->bank[e];
         }
         RCCHK(upload_expert(L, e, &q, stage));
+        flags[e] = scale_flags(&q, (size_t)I * H / 32);
     }
+    HIPCHK(hipMemcpy(L->xflags, flags, (size_t)E * sizeof(int), hipMemcpyHostToDevice));
     hipFree(stage);
+    free(flags);
     *out = L;
     return 0;
 fail:
     if (stage) hipFree(stage);
+    free(flags);
     layer_free(L);
     return rc;
 }
@@ -345,7 +364,9 @@ int k3x_moe_layer_set_timing(k3x_moe_layer *L, int on)
     if (!L) return K3X_E_ARG;
     if (on) {
         for (int i = 0; i < 8; i++)
-            if (!L->ev[i] && hipEventCreate((hipEvent_t *)&L->ev[i]) != hipSuccess)
+            if (!L->ev[i] &&
+                hipEventCreateWithFlags((hipEvent_t *)&L->ev[i], hipEventDisableSystemFence) !=
+                    hipSuccess)
                 return K3X_E_HIP;
     }
     L->timing = on ? 1 : 0;
@@ -458,6 +479,15 @@ int k3x_synth_layer_create(const k3x_cfg *c, const k3x_synth_spec *s, int device
         RCCHK(upload_shared(L, hb, hb + n, hb + 2 * n));
         free(hb);
         hb = NULL;
+    }
+    {
+        const int f = (s->scale_lo < 1 || s->scale_hi > 252) ? 7 : 0;
+        hf = (float *)malloc((size_t)E * sizeof(int));
+        if (!hf) { rc = K3X_E_NOMEM; goto fail; }
+        for (int e = 0; e < E; e++) ((int *)hf)[e] = f;
+        HIPCHK(hipMemcpy(L->xflags, hf, (size_t)E * sizeof(int), hipMemcpyHostToDevice));
+        free(hf);
+        hf = NULL;
     }
     for (int e = 0; e < E; e++) {
         uint8_t *base = L->experts + (size_t)e * L->expert_bytes;

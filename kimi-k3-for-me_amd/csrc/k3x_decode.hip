@@ -13,249 +13,268 @@
 //                     output rows (the weighted combine, :1941-1942), plus the shared
 //                     result (:1859) and an optional residual.
 //
-// Each weight byte is read once per call, with non-temporal loads.  Weights are
-// dequantised in registers (E2M1 x 2^(s-127) is exact in bf16) and multiplied on
-// v_mfma_f32_16x16x32_bf16 against activations split into bf16 hi + lo columns: every
-// product is exact and only the fp32 accumulation rounds.  The activations (B
-// fragments, compact layout: k3x_device.h) are staged in LDS when they fit, so a
-// workgroup's loop waits on nothing but its own weight stream.
+// Each weight byte is read once per call.  Weights are dequantised in registers
+// (E2M1 x 2^(s-127) is exact in bf16) and multiplied on v_mfma_f32_16x16x32_bf16 against
+// activations split into bf16 hi + lo columns: every product is exact and only the fp32
+// accumulation rounds.
+//
+// Streaming.  A workgroup's weights are cut into wave-uniform items (an fp4 super-quad,
+// 4352 bytes per 16 rows, or a bf16 quad, 4096 bytes) that its waves take interleaved,
+// so the workgroup reads one contiguous window at a time.  Each wave keeps its next two
+// items in flight through range-checked, non-temporal buffer loads; loads past a wave's
+// last item carry an out-of-range offset, which returns zeros without touching memory,
+// so every loop iteration issues the same loads and the compiler's wait counts stay
+// exact.  The activations (B fragments, compact layout: k3x_device.h) are staged in LDS
+// when they fit: their loads are issued before the first weights, so the loop waits on
+// nothing but its own weight stream.
 #include "k3x_device.h"
 
-#define NT1 1024    // k1 workgroup: 16 waves
+#define NT1 512     // k1 workgroup: 8 waves
 #define NT  256     // k1b / k2 workgroup: 4 waves
 #define NT3 512     // k3 workgroup: 8 waves
 #define STAGE_MAX 65536u   // largest B set staged in LDS (bytes)
+#define SQ_BYTES 4352u     // an fp4 super-quad of a 16-row tile
 
 extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
 
-// B source over a compact set of `bytes` at `src` (NC columns): staged into dynamic LDS
-// when `stage`, else read through a range-checked buffer.  Every thread must call it.
-__device__ __forceinline__ BSrc make_bsrc(const void *src, uint32_t bytes, int NC, bool stage,
-                                          int nthreads)
+#define AI __attribute__((always_inline))
+
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE); }
+
+// Number of items w, w + st, ... below n.
+__device__ __forceinline__ int strided_count(int w, int st, int n) { return w < n ? (n - 1 - w) / st + 1 : 0; }
+
+// ------------------------------------------------------------------ loads
+// Weights: range-checked buffer loads with the non-temporal cache policy (they are read
+// once per call and should not displace the activations).
+#define CPOL_NT 2
+__device__ __forceinline__ u32x4 wld16(rsrc_t r, uint32_t off)
 {
-    BSrc b;
-    b.NC = NC;
-    b.r = make_rsrc(src, bytes);
-    b.lds = nullptr;
-    b.zero = 0;
-    if (stage) {
-        b.zero = stage_b(dyn_lds, src, bytes, threadIdx.x, nthreads);
-        b.lds = dyn_lds;
-        __syncthreads();
-    }
-    return b;
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_NT);
+}
+__device__ __forceinline__ uint32_t wld4(rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_NT);
 }
 
-// ------------------------------------------------------------------ streaming loops
-// The loops below are branch-free in steady state: a wave's range is walked in steps of
-// four (two) quads; a quad past the range multiplies weights of the range's last quad (a
-// valid address) by zero B fragments, so every load is issued unconditionally and the
-// compiler keeps the prefetches in flight.
-
-// Quads q0, q0 + st, ... (cnt of them) of a gate/up pair of fp4 tiles.  The waves of a
-// workgroup take interleaved quads (q0 = wave, st = waves), so at any moment the
-// workgroup reads one contiguous window of each matrix.  Weights are loaded four quads
-// ahead into a ring (slot k % 4, refilled right after the quad is multiplied), B
-// fragments one quad ahead.  pair_prime issues the first four quads' loads (as early as
-// the addresses are known); pair_run consumes them.
-struct PairRing {
-    Q4 g[4], u[4];
-};
-
-__device__ __forceinline__ void pair_prime(PairRing &ring, const uint8_t *tg, const uint8_t *tu,
-                                           int nQ, int q0, int st, int cnt, int lane)
+// Items 0 .. cnt-1 through a ring of R slots: ld(slot, k) issues item k's loads (any k;
+// k >= cnt must load nothing), use(slot, k) consumes item k.  ring_prime issues the
+// first R items; ring_loop runs the rest, refilling a slot right after it is used.
+// Scheduling barriers keep each slot's loads together and in slot order, in the prime
+// as in the loop: the wait counts of the loop body are derived from both orders.
+#define SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+template <int R, class LD>
+__device__ __forceinline__ void ring_prime(LD ld)
 {
-    if (cnt <= 0) return;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int q = q0 + st * min(i, cnt - 1);
-        q4_load(ring.g[i], tg, q, nQ, lane);
-        q4_load(ring.u[i], tu, q, nQ, lane);
+    for (int i = 0; i < R; i++) {
+        SCHED_FENCE();
+        ld(i, i);
     }
+    SCHED_FENCE();
 }
 
-template <bool EXACT>
-__device__ __forceinline__ void pair_run(f32x4 &dg, f32x4 &du, PairRing &ring,
-                                         const uint8_t *tg, const uint8_t *tu, int nQ,
-                                         const BSrc &bs, int q0, int st, int cnt, int lane,
-                                         bool live)
+template <int R, class LD, class USE>
+__device__ __forceinline__ void ring_loop(int cnt, LD ld, USE use)
 {
-    if (cnt <= 0) return;
-    B4 bc;
-    b4_load(bc, bs, 0u, q0, lane, live);
-    for (int k0 = 0; k0 < cnt; k0 += 4) {
+    int k = 0;
+    for (; k + R <= cnt; k += R) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int k = k0 + i;
-            const int q = q0 + st * min(k, cnt - 1);
-            B4 bn;
-            b4_load(bn, bs, 0u, q0 + st * min(k + 1, cnt - 1), lane, live && k + 1 < cnt);
-            q4_mfma<EXACT>(dg, ring.g[i], q & 3, bc, k < cnt);
-            q4_mfma<EXACT>(du, ring.u[i], q & 3, bc, k < cnt);
-            const int qn = q0 + st * min(k + 4, cnt - 1);
-            q4_load(ring.g[i], tg, qn, nQ, lane);
-            q4_load(ring.u[i], tu, qn, nQ, lane);
-            bc = bn;
+        for (int i = 0; i < R; i++) {
+            use(i, k + i);
+            SCHED_FENCE();
+            ld(i, k + i + R);
+            SCHED_FENCE();
         }
     }
-}
-
-// Quads [fa, fb) of the flattened (unique expert u, quad q) stream of the down
-// products of one output row tile; expert u's B fragments start at u * slot_bytes.
-struct DownSrc {
-    const uint8_t *experts;
-    size_t         expert_bytes, down_off, tb;
-    const int     *uniq;
-    int            nQ, rt;
-    uint32_t       slot_bytes;
-};
-
-__device__ __forceinline__ void down_load(Q4 &a, const DownSrc &s, int f, int lane)
-{
-    const int u = f / s.nQ, q = f % s.nQ;
-    const uint8_t *tile = s.experts + (size_t)s.uniq[u] * s.expert_bytes + s.down_off +
-                          (size_t)s.rt * s.tb;
-    q4_load(a, tile, q, s.nQ, lane);
-}
-
-struct DownRing {
-    Q4 a[4];
-};
-
-// Flattened indices f0, f0 + st, ... (cnt of them).
-__device__ __forceinline__ void down_prime(DownRing &ring, const DownSrc &s, int f0, int st,
-                                           int cnt, int lane)
-{
-    if (cnt <= 0) return;
 #pragma unroll
-    for (int i = 0; i < 4; i++) down_load(ring.a[i], s, f0 + st * min(i, cnt - 1), lane);
+    for (int i = 0; i < R - 1; i++)
+        if (k + i < cnt) use(i, k + i);
 }
 
-template <bool EXACT>
-__device__ __forceinline__ void down_run(f32x4 &d, DownRing &ring, const DownSrc &s,
-                                         const BSrc &bs, int f0, int st, int cnt, int lane,
-                                         bool live)
-{
-    if (cnt <= 0) return;
-    B4 bc;
-    b4_load(bc, bs, (uint32_t)(f0 / s.nQ) * s.slot_bytes, f0 % s.nQ, lane, live);
-    for (int k0 = 0; k0 < cnt; k0 += 4) {
+// ------------------------------------------------------------------ LDS staging
+// Copy `bytes` (a multiple of 16) of global memory to the start of dynamic LDS.  issue()
+// loads up to MAXR 16-byte pieces per thread into registers; commit() stores them and
+// copies what is left.  Issued before the weight loads, the staging loads come back
+// first, so commit's wait leaves the weights in flight.
+template <int MAXR>
+struct Stage {
+    u32x4    v[MAXR];
+    rsrc_t   r;
+    uint32_t bytes;
+
+    __device__ __forceinline__ void issue(const void *src, uint32_t nbytes, int nthreads)
+    {
+        bytes = nbytes;
+        r = make_rsrc(src, nbytes);
+        const uint32_t step = (uint32_t)nthreads * 16u;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int k = k0 + i;
-            const int f = f0 + st * min(k, cnt - 1);
-            const int fn = f0 + st * min(k + 1, cnt - 1);
-            B4 bn;
-            b4_load(bn, bs, (uint32_t)(fn / s.nQ) * s.slot_bytes, fn % s.nQ, lane,
-                    live && k + 1 < cnt);
-            q4_mfma<EXACT>(d, ring.a[i], (f % s.nQ) & 3, bc, k < cnt);
-            down_load(ring.a[i], s, f0 + st * min(k + 4, cnt - 1), lane);
-            bc = bn;
-        }
+        for (int i = 0; i < MAXR; i++) v[i] = bload16(r, threadIdx.x * 16u + i * step);
     }
+    __device__ __forceinline__ void commit(int nthreads)
+    {
+        const uint32_t step = (uint32_t)nthreads * 16u;
+#pragma unroll
+        for (int i = 0; i < MAXR; i++) {
+            const uint32_t o = threadIdx.x * 16u + i * step;
+            if (o < bytes) *(u32x4 *)(dyn_lds + o) = v[i];
+        }
+        for (uint32_t o = threadIdx.x * 16u + MAXR * step; o < bytes; o += step)
+            *(u32x4 *)(dyn_lds + o) = bload16(r, o);
+    }
+};
+
+// ------------------------------------------------------------------ B fragments
+// A lane's view of a compact B set of NC columns, in LDS (staged at offset 0) or in
+// global memory.  Lane (n, kq) reads entry ((q*4 + t)*4 + kq)*NC + n of quad q.  A lane
+// whose column holds no token (n >= NC) reads column 0's entry instead: a B column only
+// reaches the same column of the product, which is discarded.
+template <bool LDSB>
+struct BFrag {
+    rsrc_t   r;
+    uint32_t off;
+    int      NC;
+
+    __device__ __forceinline__ void init(const void *gsrc, uint32_t bytes, int NC_, int lane)
+    {
+        NC = NC_;
+        const int n = lane & 15, kq = lane >> 4;
+        off = (uint32_t)((kq * NC + (n < NC ? n : 0)) * 16);
+        if (!LDSB) r = make_rsrc(gsrc, bytes);
+    }
+    // product t of quad q of the set `sbase` bytes in (wave-uniform)
+    __device__ __forceinline__ u32x4 get(uint32_t sbase, int q, int t) const
+    {
+        const uint32_t o = off + (uint32_t)(q * 256 * NC + t * 64 * NC);
+        if (LDSB) return *(const u32x4 *)(dyn_lds + sbase + o);
+        return __builtin_amdgcn_raw_buffer_load_b128(r, o, sbase, 0);
+    }
+};
+
+// ------------------------------------------------------------------ fp4 super-quads
+// A super-quad of a tiled fp4 matrix for this lane: four 16-byte code groups (one scale
+// group each) and the scale dword (byte j for quad j).
+struct SQ {
+    u32x4    c[4];
+    uint32_t s;
+};
+
+// base: the super-quad's byte offset in the tile, or K3X_OOB (loads nothing)
+__device__ __forceinline__ void sq_load(SQ &a, rsrc_t r, uint32_t base, int lane)
+{
+    const uint32_t o = base + (uint32_t)lane * 16u;
+    a.c[0] = wld16(r, o);
+    a.c[1] = wld16(r, o + 1024u);
+    a.c[2] = wld16(r, o + 2048u);
+    a.c[3] = wld16(r, o + 3072u);
+    a.s = wld4(r, base + 4096u + (uint32_t)lane * 4u);
 }
 
-// One bf16 quad of a tiled matrix: four 16-byte A fragments per lane.
+// A operand of product t of quad j.  EXACT takes the reference's float product for any
+// scale byte; the fast path needs bytes 1..252.
+template <bool EXACT>
+__device__ __forceinline__ bf16x8 sq_a(const SQ &a, int j, int t)
+{
+    const uint32_t sb = (a.s >> (8 * j)) & 255u;
+    if (EXACT) return dq8_exact(a.c[j][t], sb);
+    return dq8(a.c[j][t], e8m0_scale(sb));
+}
+
+// d += dequant(a) x B over super-quad S (quads 4S .. 4S+3)
+template <bool EXACT, bool LDSB>
+__device__ __forceinline__ void sq_mfma(f32x4 &d, const SQ &a, const BFrag<LDSB> &b,
+                                        uint32_t sbase, int S)
+{
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            d = mfma(sq_a<EXACT>(a, j, t), as_bf16x8(b.get(sbase, 4 * S + j, t)), d);
+}
+
+// gate and up over the same B
+template <bool EXACT, bool LDSB>
+__device__ __forceinline__ void sq_mfma2(f32x4 &dg, f32x4 &du, const SQ &g, const SQ &u,
+                                         const BFrag<LDSB> &b, int S)
+{
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const bf16x8 bv = as_bf16x8(b.get(0u, 4 * S + j, t));
+            dg = mfma(sq_a<EXACT>(g, j, t), bv, dg);
+            du = mfma(sq_a<EXACT>(u, j, t), bv, du);
+        }
+}
+
+// ------------------------------------------------------------------ bf16 quads
+// One quad of a tiled bf16 matrix for this lane: four 16-byte A fragments.
 struct QB {
     u32x4 a[4];
 };
 
-__device__ __forceinline__ void qb_load(QB &a, const uint8_t *tile, int q, int lane)
+__device__ __forceinline__ void qb_load(QB &a, rsrc_t r, uint32_t base, int lane)
 {
-    const uint8_t *p = tile + (size_t)q * 4096 + lane * 16;
+    const uint32_t o = base + (uint32_t)lane * 16u;
 #pragma unroll
-    for (int t = 0; t < 4; t++) a.a[t] = ldw16(p + t * 1024);
+    for (int t = 0; t < 4; t++) a.a[t] = wld16(r, o + 1024u * t);
 }
 
-__device__ __forceinline__ void qb_mfma(f32x4 &d, const QB &a, const B4 &b)
+__device__ __forceinline__ void qb_mfma(f32x4 &d, const QB &a, const u32x4 (&b)[4])
 {
 #pragma unroll
-    for (int t = 0; t < 4; t++) d = mfma(as_bf16x8(a.a[t]), as_bf16x8(b.b[t]), d);
+    for (int t = 0; t < 4; t++) d = mfma(as_bf16x8(a.a[t]), as_bf16x8(b[t]), d);
 }
-
-// Quads q0, q0 + st, ... (cnt of them) of one tiled bf16 matrix (two with PAIR,
-// sharing the B fragments): weights two quads ahead, B one quad ahead; lb(b, q, on)
-// loads quad q's fragments (zeros when !on).  bf16_prime issues the first two quads'
-// loads.
-struct BfRing {
-    QB g[2], u[2];
-};
-
-template <bool PAIR>
-__device__ __forceinline__ void bf16_prime(BfRing &ring, const uint8_t *tg, const uint8_t *tu,
-                                           int q0, int st, int cnt, int lane)
-{
-    if (cnt <= 0) return;
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int q = q0 + st * min(i, cnt - 1);
-        qb_load(ring.g[i], tg, q, lane);
-        if (PAIR) qb_load(ring.u[i], tu, q, lane);
-    }
-}
-
-template <bool PAIR, class LB>
-__device__ __forceinline__ void bf16_run(f32x4 &dg, f32x4 &du, BfRing &ring, const uint8_t *tg,
-                                         const uint8_t *tu, LB lb, int q0, int st, int cnt,
-                                         int lane)
-{
-    if (cnt <= 0) return;
-    B4 bc;
-    lb(bc, q0, true);
-    for (int k0 = 0; k0 < cnt; k0 += 2) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int k = k0 + i;
-            B4 bn;
-            lb(bn, q0 + st * min(k + 1, cnt - 1), k + 1 < cnt);
-            qb_mfma(dg, ring.g[i], bc);
-            if (PAIR) qb_mfma(du, ring.u[i], bc);
-            const int qn = q0 + st * min(k + 2, cnt - 1);
-            qb_load(ring.g[i], tg, qn, lane);
-            if (PAIR) qb_load(ring.u[i], tu, qn, lane);
-            bc = bn;
-        }
-    }
-}
-
-// Number of indices w, w + st, ... below n.
-__device__ __forceinline__ int strided_count(int w, int st, int n) { return w < n ? (n - 1 - w) / st + 1 : 0; }
 
 // B fragments of quad q straight from activations x [T][H] (no staging): bf16 x is its
-// own hi column (lo = 0) and is read through a range-checked buffer; fp32 x is split
-// here.
-__device__ __forceinline__ void bx_load(B4 &b, const void *x, int x_bf16, rsrc_t xr, int H,
-                                        int q, int lane, bool live)
+// own hi column (lo = 0); fp32 x is split here.
+__device__ __forceinline__ void bx_load(u32x4 (&b)[4], const void *x, int x_bf16, rsrc_t xr,
+                                        int H, int NC, int q, int lane)
 {
-    const int n = lane & 15, kq = lane >> 4, tok = n >> 1, hl = n & 1;
+    const int n0 = lane & 15, kq = lane >> 4;
+    const int n = n0 < NC ? n0 : 0, tok = n >> 1, hl = n & 1;
     if (x_bf16) {
         const uint32_t off = (uint32_t)(((size_t)tok * H + (size_t)q * 128 + kq * 32) * 2);
 #pragma unroll
-        for (int t = 0; t < 4; t++) b.b[t] = bload16(xr, (live && !hl) ? off + 16u * t : K3X_OOB);
+        for (int t = 0; t < 4; t++) b[t] = bload16(xr, hl ? K3X_OOB : off + 16u * t);
     } else {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            b.b[t] = (u32x4){0u, 0u, 0u, 0u};
-            if (live) {
-                float xv[8];
-                load_x8(x, 0, (size_t)tok * H + (size_t)q * 128 + kq * 32 + t * 8, xv);
-                b.b[t] = bfrag_of(xv, hl);
-            }
+            float xv[8];
+            load_x8(x, 0, (size_t)tok * H + (size_t)q * 128 + kq * 32 + t * 8, xv);
+            b[t] = bfrag_of(xv, hl);
         }
     }
 }
 
-// Compact B fragments of x [T][H] (NC = 2T columns: hi, lo per token), entries
-// [e0, e1) of the set, written by `nthreads` threads from `tid`.
-__device__ __forceinline__ void x_to_bfrags(uint8_t *dst, const void *x, int x_bf16, int H,
-                                            int NC, int e0, int e1, int tid, int nthreads)
+// Compact B fragments of x [T][H] (NC = 2T columns) over nq quads (quads from H/128 on
+// are zeros), written by `nthreads` threads.
+__device__ __forceinline__ void x_to_bset(uint8_t *dst, const void *x, int x_bf16, int H, int NC,
+                                          int nq, int tid, int nthreads)
 {
-    for (int f = e0 + tid; f < e1; f += nthreads) {
+    const int nQ = H >> 7, ne = nq * 16 * NC;
+    for (int f = tid; f < ne; f += nthreads) {
         const int n = f % NC, kq = (f / NC) & 3, t = (f / (NC * 4)) & 3, q = f / (NC * 16);
-        float xv[8];
-        load_x8(x, x_bf16, (size_t)(n >> 1) * H + (size_t)q * 128 + kq * 32 + t * 8, xv);
-        *(u32x4 *)(dst + (size_t)f * 16) = bfrag_of(xv, n & 1);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (q < nQ) {
+            float xv[8];
+            load_x8(x, x_bf16, (size_t)(n >> 1) * H + (size_t)q * 128 + kq * 32 + t * 8, xv);
+            v = bfrag_of(xv, n & 1);
+        }
+        *(u32x4 *)(dst + (size_t)f * 16) = v;
     }
+}
+
+// hi + lo columns of a product summed per token (lanes n, n^1), then
+// f(row0, token, values) on the even lanes of live columns: wave 0's rows row0 + i.
+template <int NV, class F>
+__device__ __forceinline__ void per_token(const float (&acc)[NV], int NC, int lane, F f)
+{
+    const int n = lane & 15, kq = lane >> 4;
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] = acc[i] + __shfl_xor(acc[i], 1);
+    if ((n & 1) == 0 && n < NC) f(4 * kq, n >> 1, v);
 }
 
 // ------------------------------------------------------------------ K1
@@ -266,12 +285,11 @@ struct K1Args {
     int          x_bf16;
     int          T, H, E;
     float       *score, *choice;   // [T][E]
-    uint16_t    *xB;               // compact B fragments of x, for k2
+    uint16_t    *xB;               // compact B set of x over whole super-quads, for k2
     int          n_rwg;            // router workgroups
     const uint16_t *sh_gate, *sh_up;
     int          SI;
-    uint16_t    *shB;              // compact B fragments of the shared activation
-    int          stage;            // shared workgroups build x's fragments in LDS
+    uint16_t    *shB;              // compact B set of the shared activation, for k1b
 };
 
 #define RWAVES 4                     // waves per expert row in the router
@@ -339,70 +357,144 @@ __device__ void k1_router(const K1Args &a, float *lds)
     }
 }
 
-// Shared expert gate and up for 16 rows over the full K, sixteen waves splitting the
-// quads, then SwiGLU (hi + lo columns summed first) into the shared activation's
-// compact B fragments.
+// x's B set for one workgroup, in LDS: pair p covers the hi and lo entries of one token
+// at (q, t, kq); up to K1_MAXP pairs per thread are loaded before the weights.
+#define K1_MAXP 2
+struct XPairs {
+    u32x4 a[K1_MAXP], b[K1_MAXP];
+};
+
+__device__ __forceinline__ void xp_pos(int p, int T, int H, int &tok, int &q, int &t, int &kq,
+                                       size_t &elem)
+{
+    tok = p % T;
+    const int r = p / T;
+    kq = r & 3; t = (r >> 2) & 3; q = r >> 4;
+    elem = (size_t)tok * H + (size_t)q * 128 + kq * 32 + t * 8;
+}
+
+__device__ __forceinline__ void xp_load(u32x4 &a, u32x4 &b, rsrc_t xr, int x_bf16, size_t elem,
+                                        bool on)
+{
+    if (x_bf16) {
+        a = bload16(xr, on ? (uint32_t)(elem * 2) : K3X_OOB);
+        b = (u32x4){0u, 0u, 0u, 0u};
+    } else {
+        a = bload16(xr, on ? (uint32_t)(elem * 4) : K3X_OOB);
+        b = bload16(xr, on ? (uint32_t)(elem * 4 + 16) : K3X_OOB);
+    }
+}
+
+__device__ __forceinline__ void xp_store(const u32x4 &a, const u32x4 &b, int x_bf16, int tok,
+                                         int q, int t, int kq, int NC)
+{
+    float xv[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        xv[2 * j] = x_bf16 ? bf2f(a[j] & 0xFFFFu) : __uint_as_float(j < 2 ? a[2 * j] : b[2 * j - 4]);
+        xv[2 * j + 1] = x_bf16 ? bf2f(a[j] >> 16) : __uint_as_float(j < 2 ? a[2 * j + 1] : b[2 * j - 3]);
+    }
+    const uint32_t e0 = (uint32_t)(((q * 4 + t) * 4 + kq) * NC + 2 * tok) * 16u;
+    *(u32x4 *)(dyn_lds + e0) = bfrag_of(xv, 0);
+    *(u32x4 *)(dyn_lds + e0 + 16u) = bfrag_of(xv, 1);
+}
+
+// Shared expert gate and up products for 16 rows over the full K, sixteen waves taking
+// interleaved quads (each wave both matrices of a quad, over one B read); then SwiGLU
+// per token and the activation's hi/lo B fragments into shB.
+template <bool LDSX>
 __device__ void k1_shared(const K1Args &a, float *lds, int rt)
 {
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int NW = NT1 / WAVE;
     const int nQ = a.H >> 7, NC = 2 * a.T;
-    const int n = lane & 15, kq = lane >> 4;
-    const bool live = n < NC;
     const int cnt = strided_count(wave, NW, nQ);
-    const uint8_t *tg = (const uint8_t *)(a.sh_gate + (size_t)rt * nQ * 2048);
-    const uint8_t *tu = (const uint8_t *)(a.sh_up + (size_t)rt * nQ * 2048);
+    const uint32_t tbytes = (uint32_t)nQ * 4096u;
+    const rsrc_t rg = make_rsrc(a.sh_gate + (size_t)rt * 16 * a.H, tbytes);
+    const rsrc_t ru = make_rsrc(a.sh_up + (size_t)rt * 16 * a.H, tbytes);
+    const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.T * a.H * (a.x_bf16 ? 2 : 4)));
+    const int npairs = nQ * 16 * a.T;
+    XPairs xp;
+    if (LDSX) {
+#pragma unroll
+        for (int i = 0; i < K1_MAXP; i++) {
+            const int p = threadIdx.x + i * NT1;
+            int tok, q, t, kq;
+            size_t elem;
+            xp_pos(p, a.T, a.H, tok, q, t, kq, elem);
+            xp_load(xp.a[i], xp.b[i], xr, a.x_bf16, elem, p < npairs);
+        }
+    }
+    QB g[2], u[2];
+    auto ld = [&](int i, int k) AI {
+        const uint32_t o = k < cnt ? (uint32_t)(wave + NW * k) * 4096u : K3X_OOB;
+        qb_load(g[i], rg, o, lane);
+        qb_load(u[i], ru, o, lane);
+    };
+    ring_prime<2>(ld);
     f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
-    BfRing ring;
-    if (a.stage) {
-        // x's fragments built once per workgroup in LDS
-        const uint32_t bytes = (uint32_t)(a.H * NC * 2);
-        x_to_bfrags(dyn_lds, a.x, a.x_bf16, a.H, NC, 0, nQ * 16 * NC, threadIdx.x, NT1);
-        if (threadIdx.x == 0) *(u32x4 *)(dyn_lds + bytes) = (u32x4){0u, 0u, 0u, 0u};
-        bf16_prime<true>(ring, tg, tu, wave, NW, cnt, lane);
+    if (LDSX) {
+#pragma unroll
+        for (int i = 0; i < K1_MAXP; i++) {
+            const int p = threadIdx.x + i * NT1;
+            int tok, q, t, kq;
+            size_t elem;
+            xp_pos(p, a.T, a.H, tok, q, t, kq, elem);
+            if (p < npairs) xp_store(xp.a[i], xp.b[i], a.x_bf16, tok, q, t, kq, NC);
+        }
+        for (int p = threadIdx.x + K1_MAXP * NT1; p < npairs; p += NT1) {
+            int tok, q, t, kq;
+            size_t elem;
+            xp_pos(p, a.T, a.H, tok, q, t, kq, elem);
+            u32x4 va, vb;
+            xp_load(va, vb, xr, a.x_bf16, elem, true);
+            xp_store(va, vb, a.x_bf16, tok, q, t, kq, NC);
+        }
         __syncthreads();
-        BSrc bs;
-        bs.NC = NC;
-        bs.lds = dyn_lds;
-        bs.zero = bytes;
-        bf16_run<true>(dg, du, ring, tg, tu,
-                       [&](B4 &b, int q, bool on) { b4_load(b, bs, 0u, q, lane, live && on); },
-                       wave, NW, cnt, lane);
+        BFrag<true> bf;
+        bf.init(nullptr, 0u, NC, lane);
+        ring_loop<2>(cnt, ld, [&](int i, int k) AI {
+            const int q = wave + NW * k;
+            u32x4 b[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) b[t] = bf.get(0u, q, t);
+            qb_mfma(dg, g[i], b);
+            qb_mfma(du, u[i], b);
+        });
     } else {
-        bf16_prime<true>(ring, tg, tu, wave, NW, cnt, lane);
-        const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.T * a.H * 2));
-        bf16_run<true>(dg, du, ring, tg, tu,
-                       [&](B4 &b, int q, bool on) { bx_load(b, a.x, a.x_bf16, xr, a.H, q, lane, live && on); },
-                       wave, NW, cnt, lane);
+        ring_loop<2>(cnt, ld, [&](int i, int k) AI {
+            u32x4 b[4];
+            bx_load(b, a.x, a.x_bf16, xr, a.H, NC, wave + NW * k, lane);
+            qb_mfma(dg, g[i], b);
+            qb_mfma(du, u[i], b);
+        });
     }
     float acc[8] = {dg[0], dg[1], dg[2], dg[3], du[0], du[1], du[2], du[3]};
     wave_sum_lds<8, NT1 / WAVE>(acc, lds, wave, lane);
     if (wave != 0) return;
-    const int tok = n >> 1;
-    for (int i = 0; i < 4; i++) {
-        const float g = acc[i] + __shfl_xor(acc[i], 1);
-        const float v = acc[4 + i] + __shfl_xor(acc[4 + i], 1);
-        if ((n & 1) == 0 && live) {
+    per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&v)[8]) AI {
+        for (int i = 0; i < 4; i++) {
             uint32_t hi, lo;
-            split_bf16(swiglu(g, v), hi, lo);
-            const int r = rt * 16 + 4 * kq + i;
+            split_bf16(swiglu(v[i], v[4 + i]), hi, lo);
+            const int r = rt * 16 + r0 + i;
             a.shB[bfrag_off(r, 2 * tok, NC)] = (uint16_t)hi;
             a.shB[bfrag_off(r, 2 * tok + 1, NC)] = (uint16_t)lo;
         }
-    }
+    });
 }
 
+template <bool LDSX>
 __global__ void __launch_bounds__(NT1) k1_router_shared(K1Args a)
 {
     __shared__ float lds[(NT1 / WAVE - 1) * 8 * WAVE];
     if ((int)blockIdx.x < a.n_rwg) {
         k1_router(a, lds);
-        const int NC = 2 * a.T, ne = (a.H >> 7) * 16 * NC;
-        x_to_bfrags((uint8_t *)a.xB, a.x, a.x_bf16, a.H, NC, 0, ne,
-                    blockIdx.x * NT1 + threadIdx.x, a.n_rwg * NT1);
+        const int nS = ((a.H >> 7) + 3) >> 2;
+        x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS,
+                  blockIdx.x * NT1 + threadIdx.x, a.n_rwg * NT1);
         return;
     }
-    k1_shared(a, lds, blockIdx.x - a.n_rwg);
+    k1_shared<LDSX>(a, lds, blockIdx.x - a.n_rwg);
 }
 
 // ------------------------------------------------------------------ top-k
@@ -434,15 +526,16 @@ __device__ __forceinline__ float bload_f32(rsrc_t r, uint32_t off)
 // weight 0).  A 32-step bitwise search with ballot counts finds the k-th largest key;
 // the k selected are then ranked.  Weights are the unbiased scores, renormalised through
 // a double sum and a float reciprocal, then scaled (:1710-1716).  Results in s_idx/s_w.
-template <int NC>
+// NE: 64-expert chunks held per lane.
+template <int NE>
 __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, int renorm,
                           float routed_scale, int *s_idx, float *s_w, uint64_t *s_key,
                           int *s_e, float *s_sc, int lane)
 {
-    uint32_t key[NC];
-    float sco[NC];
+    uint32_t key[NE];
+    float sco[NE];
 #pragma unroll
-    for (int c = 0; c < NC; c++) {
+    for (int c = 0; c < NE; c++) {
         const int e = lane + WAVE * c;
         const uint32_t off = row_off + 4u * (uint32_t)e;
         const float v = bload_f32(cr, e < E ? off : K3X_OOB);
@@ -451,7 +544,7 @@ __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, 
     }
     int nvalid = 0;
 #pragma unroll
-    for (int c = 0; c < NC; c++) nvalid += __popcll(__ballot(key[c] > K_NEG_INF));
+    for (int c = 0; c < NE; c++) nvalid += __popcll(__ballot(key[c] > K_NEG_INF));
     const int ke = min(K, nvalid);
     uint32_t tau = 0xFFFFFFFFu;
     if (ke > 0) {
@@ -460,17 +553,17 @@ __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, 
             const uint32_t cand = tau | (1u << b);
             int cnt = 0;
 #pragma unroll
-            for (int c = 0; c < NC; c++) cnt += __popcll(__ballot(key[c] >= cand));
+            for (int c = 0; c < NE; c++) cnt += __popcll(__ballot(key[c] >= cand));
             if (cnt >= ke) tau = cand;
         }
     }
     int ngt = 0;
 #pragma unroll
-    for (int c = 0; c < NC; c++) ngt += __popcll(__ballot(key[c] > tau));
+    for (int c = 0; c < NE; c++) ngt += __popcll(__ballot(key[c] > tau));
     int need = ke - ngt;                    // ties at tau, taken in ascending index
     int base = 0;
 #pragma unroll
-    for (int c = 0; c < NC; c++) {
+    for (int c = 0; c < NE; c++) {
         const uint64_t eq = __ballot(ke > 0 && key[c] == tau);
         const int take = min(need, (int)__popcll(eq));
         need -= take;
@@ -521,41 +614,55 @@ struct KSArgs {
     int           *idx;  float *wt;        // internal [T][K]
     int           *uidx; float *uwt;       // optional caller copies
     int            T, H;
-    const uint16_t *sh_down, *shB;
+    const uint16_t *sh_down;
+    const uint16_t *shB;           // compact B set of the shared activation
     float         *ysh;            // [T][H] shared expert output
     int            SI;
-    int            stage;          // shB staged in LDS
 };
 
-// Shared expert down product for 16 output rows: four waves splitting the quads.
+// Shared expert down product for 16 output rows: four waves on interleaved quads, the
+// shared activation's B set staged in LDS when it fits.
+template <bool LDSB>
 __device__ void ks_shared_down(const KSArgs &a, float *lds, int rt)
 {
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    const int NW = NT / WAVE;
     const int nQS = a.SI >> 7, NC = 2 * a.T;
-    const int n = lane & 15;
-    const bool live = n < NC;
-    const uint8_t *tile = (const uint8_t *)(a.sh_down + (size_t)rt * nQS * 2048);
-    const int cnt = strided_count(wave, NT / WAVE, nQS);
-    BfRing ring;
-    bf16_prime<false>(ring, tile, tile, wave, NT / WAVE, cnt, lane);
-    const BSrc bs = make_bsrc(a.shB, (uint32_t)(a.SI * NC * 2), NC, a.stage != 0, NT);
-    f32x4 d = {0.f, 0.f, 0.f, 0.f}, unused = {0.f, 0.f, 0.f, 0.f};
-    bf16_run<false>(d, unused, ring, tile, tile,
-                    [&](B4 &b, int q, bool on) { b4_load(b, bs, 0u, q, lane, live && on); },
-                    wave, NT / WAVE, cnt, lane);
+    const int cnt = strided_count(wave, NW, nQS);
+    const uint32_t bbytes = (uint32_t)nQS * 256u * NC;
+    const rsrc_t rw = make_rsrc(a.sh_down + (size_t)rt * 16 * a.SI, (uint32_t)nQS * 4096u);
+    Stage<8> st;
+    if (LDSB) st.issue(a.shB, bbytes, NT);
+    QB ring[2];
+    auto ld = [&](int i, int k) AI {
+        qb_load(ring[i], rw, k < cnt ? (uint32_t)(wave + NW * k) * 4096u : K3X_OOB, lane);
+    };
+    ring_prime<2>(ld);
+    if (LDSB) {
+        st.commit(NT);
+        __syncthreads();
+    }
+    BFrag<LDSB> bf;
+    bf.init(a.shB, bbytes, NC, lane);
+    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+    ring_loop<2>(cnt, ld, [&](int i, int k) AI {
+        const int q = wave + NW * k;
+        u32x4 b[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) b[t] = bf.get(0u, q, t);
+        qb_mfma(d, ring[i], b);
+    });
     float acc[4] = {d[0], d[1], d[2], d[3]};
     wave_sum_lds<4, NT / WAVE>(acc, lds, wave, lane);
     if (wave != 0) return;
-    const int kq = lane >> 4, tok = n >> 1;
-    for (int i = 0; i < 4; i++) {
-        const float y = acc[i] + __shfl_xor(acc[i], 1);
-        if ((n & 1) == 0 && live) a.ysh[(size_t)tok * a.H + rt * 16 + 4 * kq + i] = y;
-    }
+    per_token<4>(acc, NC, lane, [&](int r0, int tok, const float (&v)[4]) AI {
+        for (int i = 0; i < 4; i++) a.ysh[(size_t)tok * a.H + rt * 16 + r0 + i] = v[i];
+    });
 }
 
 // Routing of every token (one wave per token), then the unique experts in first-seen
 // order over (token, slot) and each one's weight per token (0 where not chosen).
-template <int NC>
+template <int NE>
 __device__ void ks_select(const KSArgs &a)
 {
     __shared__ int      s_idx[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
@@ -568,7 +675,7 @@ __device__ void ks_select(const KSArgs &a)
     const rsrc_t cr = make_rsrc(a.choice, (uint32_t)(a.T * a.E * 4));
     const rsrc_t sr = make_rsrc(a.score, (uint32_t)(a.T * a.E * 4));
     for (int t = wave; t < a.T; t += NT / WAVE)
-        wave_topk<NC>(cr, sr, (uint32_t)(t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
+        wave_topk<NE>(cr, sr, (uint32_t)(t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
                       s_idx[t], s_w[t], s_key[wave], s_e[wave], s_sc[wave], lane);
     for (int e = threadIdx.x; e < a.E; e += NT) s_slot[e] = -1;
     __syncthreads();
@@ -595,12 +702,12 @@ __device__ void ks_select(const KSArgs &a)
     }
 }
 
-template <int NC>
+template <int NE, bool LDSB>
 __global__ void __launch_bounds__(NT) k1b_select_shdown(KSArgs a)
 {
     __shared__ float lds[(NT / WAVE - 1) * 4 * WAVE];
-    if (blockIdx.x == 0) { ks_select<NC>(a); return; }
-    ks_shared_down(a, lds, blockIdx.x - 1);
+    if (blockIdx.x == 0) { ks_select<NE>(a); return; }
+    ks_shared_down<LDSB>(a, lds, blockIdx.x - 1);
 }
 
 // ------------------------------------------------------------------ K2
@@ -608,57 +715,74 @@ struct K2Args {
     const uint8_t *experts;
     size_t         expert_bytes, gate_off, up_off;
     const k3x_route *route;
-    const int     *xflags;         // [E] bit 0 gate, 1 up, 2 down: scale bytes need EXACT
-    const uint16_t *xB;            // compact B fragments of x
-    uint16_t      *actB;           // compact B fragments of each unique expert's activation
+    const uint16_t *xB;            // compact B set of x over whole super-quads
+    uint16_t      *actB;           // one compact B set per unique expert (slot)
     int            T, H, I;
-    int            stage;
 };
 
+// Gate and up products of 16 rows of one unique expert: four waves on interleaved
+// super-quads; SwiGLU, the token's routing weight for this expert (0 where the token did
+// not choose it) and the bf16 hi/lo split into the expert's activation slot.
+template <bool EXACT, bool LDSB>
 __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
 {
     __shared__ float lds[(NT / WAVE - 1) * 8 * WAVE];
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    const int NW = NT / WAVE;
+    const int NC = 2 * a.T;
     const int nTiles = a.I >> 4;
     const int u = blockIdx.x / nTiles, rt = blockIdx.x % nTiles;
     if (u >= a.route->nu) return;
+    const int nS = ((a.H >> 7) + 3) >> 2;
+    const uint32_t bbytes = (uint32_t)nS * 1024u * NC;
+    Stage<8> st;
+    if (LDSB) st.issue(a.xB, bbytes, NT);
     const int e = a.route->uniq[u];
-    const int NC = 2 * a.T;
-    const size_t tb = fp4_tile_bytes(a.H);
-    const uint8_t *ex = a.experts + (size_t)e * a.expert_bytes;
-    const uint8_t *tg = ex + a.gate_off + (size_t)rt * tb;
-    const uint8_t *tu = ex + a.up_off + (size_t)rt * tb;
-    const int nQ = a.H >> 7;
-    const int cnt = strided_count(wave, NT / WAVE, nQ);
-    const int n = lane & 15;
-    const bool live = n < NC;
-    PairRing ring;
-    pair_prime(ring, tg, tu, nQ, wave, NT / WAVE, cnt, lane);
-    const int flags = a.xflags[e];
-    const BSrc bs = make_bsrc(a.xB, (uint32_t)(a.H * NC * 2), NC, a.stage != 0, NT);
+    const uint32_t tb = (uint32_t)fp4_tile_bytes(a.H);
+    const uint8_t *ex = a.experts + (size_t)e * a.expert_bytes + (size_t)rt * tb;
+    const rsrc_t rg = make_rsrc(ex + a.gate_off, tb);
+    const rsrc_t ru = make_rsrc(ex + a.up_off, tb);
+    const int cnt = strided_count(wave, NW, nS);
+    SQ g[2], v[2];
+    auto ld = [&](int i, int k) AI {
+        const uint32_t o = k < cnt ? (uint32_t)(wave + NW * k) * SQ_BYTES : K3X_OOB;
+        sq_load(g[i], rg, o, lane);
+        sq_load(v[i], ru, o, lane);
+    };
+    ring_prime<2>(ld);
+    if (LDSB) {
+        st.commit(NT);
+        __syncthreads();
+    }
+    BFrag<LDSB> bf;
+    bf.init(a.xB, bbytes, NC, lane);
     f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
-    if (flags & 3) pair_run<true>(dg, du, ring, tg, tu, nQ, bs, wave, NT / WAVE, cnt, lane, live);
-    else           pair_run<false>(dg, du, ring, tg, tu, nQ, bs, wave, NT / WAVE, cnt, lane, live);
+    ring_loop<2>(cnt, ld, [&](int i, int k) AI {
+        sq_mfma2<EXACT, LDSB>(dg, du, g[i], v[i], bf, wave + NW * k);
+    });
     float acc[8] = {dg[0], dg[1], dg[2], dg[3], du[0], du[1], du[2], du[3]};
     wave_sum_lds<8, NT / WAVE>(acc, lds, wave, lane);
+    // the slot holds whole super-quads; its quads past I/128 stay zero
+    const int nSI = ((a.I >> 7) + 3) >> 2;
+    const uint32_t slot = (uint32_t)nSI * 1024u * NC;
+    uint8_t *dst = (uint8_t *)a.actB + (size_t)u * slot;
+    if (rt == 0)
+        for (uint32_t o = (uint32_t)(a.I >> 7) * 256u * NC + threadIdx.x * 16u; o < slot; o += NT * 16u)
+            *(u32x4 *)(dst + o) = (u32x4){0u, 0u, 0u, 0u};
     if (wave != 0) return;
-    // hi + lo columns, SwiGLU, the token's routing weight for this expert (0 if the token
-    // did not choose it), then the bf16 split for the down products
-    const int kq = lane >> 4, tok = n >> 1;
-    const float w = live ? a.route->wtok[u][tok] : 0.0f;
-    uint16_t *dst = a.actB + (size_t)u * ((size_t)a.I * NC);
-    for (int i = 0; i < 4; i++) {
-        const float g = acc[i] + __shfl_xor(acc[i], 1);
-        const float v = acc[4 + i] + __shfl_xor(acc[4 + i], 1);
-        if ((n & 1) == 0 && live) {
-            const float y = (w == 0.0f) ? 0.0f : w * swiglu(g, v);
+    const float *wtok = a.route->wtok[u];
+    uint16_t *d16 = (uint16_t *)dst;
+    per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&s)[8]) AI {
+        const float w = wtok[tok];
+        for (int i = 0; i < 4; i++) {
+            const float y = (w == 0.0f) ? 0.0f : w * swiglu(s[i], s[4 + i]);
             uint32_t hi, lo;
             split_bf16(y, hi, lo);
-            const int r = rt * 16 + 4 * kq + i;
-            dst[bfrag_off(r, 2 * tok, NC)] = (uint16_t)hi;
-            dst[bfrag_off(r, 2 * tok + 1, NC)] = (uint16_t)lo;
+            const int r = rt * 16 + r0 + i;
+            d16[bfrag_off(r, 2 * tok, NC)] = (uint16_t)hi;
+            d16[bfrag_off(r, 2 * tok + 1, NC)] = (uint16_t)lo;
         }
-    }
+    });
 }
 
 // ------------------------------------------------------------------ K3
@@ -666,62 +790,73 @@ struct K3Args {
     const uint8_t *experts;
     size_t         expert_bytes, down_off;
     const k3x_route *route;
-    const int     *xflags;
     const uint16_t *actB;
     const float   *ysh;            // shared output, or NULL
     float         *out;
     const float   *resid;
     int            T, H, I, K;
-    int            stage;          // stage the routed activations when nu*I*NC*2 <= STAGE_MAX
+    uint32_t       lds_bytes;      // dynamic LDS of the launch
 };
 
+// Down products of 16 output rows over every (unique expert, super-quad) item, eight
+// waves interleaved, into one accumulator set.
+template <bool EXACT, bool LDSB>
+__device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int lane, int nu)
+{
+    const int NW = NT3 / WAVE;
+    const int NC = 2 * a.T;
+    const int rt = blockIdx.x;
+    const int nSI = ((a.I >> 7) + 3) >> 2;
+    const uint32_t slot = (uint32_t)nSI * 1024u * NC;
+    const uint32_t tb = (uint32_t)fp4_tile_bytes(a.I);
+    const int cnt = strided_count(wave, NW, nu * nSI);
+    Stage<8> st;
+    if (LDSB) st.issue(a.actB, (uint32_t)nu * slot, NT3);
+    SQ ring[2];
+    auto ld = [&](int i, int k) AI {
+        const int it = wave + NW * k;
+        const bool on = k < cnt;
+        const int u = on ? it / nSI : 0, S = on ? it % nSI : 0;
+        const int e = on ? a.route->uniq[u] : 0;
+        const rsrc_t r = make_rsrc(a.experts + (size_t)e * a.expert_bytes + a.down_off +
+                                       (size_t)rt * tb, on ? tb : 0u);
+        sq_load(ring[i], r, (uint32_t)S * SQ_BYTES, lane);
+    };
+    ring_prime<2>(ld);
+    if (LDSB) {
+        st.commit(NT3);
+        __syncthreads();
+    }
+    BFrag<LDSB> bf;
+    bf.init(a.actB, (uint32_t)(a.T * a.K) * slot, NC, lane);
+    ring_loop<2>(cnt, ld, [&](int i, int k) AI {
+        const int it = wave + NW * k;
+        sq_mfma<EXACT, LDSB>(d, ring[i], bf, (uint32_t)(it / nSI) * slot, it % nSI);
+    });
+}
+
+template <bool EXACT>
 __global__ void __launch_bounds__(NT3) k3_down(K3Args a)
 {
     __shared__ float lds[(NT3 / WAVE - 1) * 4 * WAVE];
-    __shared__ int   s_uniq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];
-    __shared__ int   s_exact;
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int NW = NT3 / WAVE;
-    const int rt = blockIdx.x;
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int nu = a.route->nu;
-    const int NC = 2 * a.T;
-    if (threadIdx.x == 0) s_exact = 0;
-    for (int u = threadIdx.x; u < nu; u += NT3) s_uniq[u] = a.route->uniq[u];
-    __syncthreads();
-    const uint32_t slot = (uint32_t)(a.I * NC * 2);
-    const int nQI = a.I >> 7;
-    const int n = lane & 15;
-    const bool live = n < NC;
-    DownSrc ds;
-    ds.experts = a.experts; ds.expert_bytes = a.expert_bytes; ds.down_off = a.down_off;
-    ds.tb = fp4_tile_bytes(a.I); ds.uniq = s_uniq; ds.nQ = nQI; ds.rt = rt;
-    ds.slot_bytes = slot;
-    const int nf = nu * nQI;
-    const int cnt = strided_count(wave, NW, nf);
-    DownRing ring;
-    down_prime(ring, ds, wave, NW, cnt, lane);
-    for (int u = threadIdx.x; u < nu; u += NT3)
-        if (a.xflags[s_uniq[u]] & 4) s_exact = 1;
-    const bool stage = a.stage && (uint32_t)nu * slot <= STAGE_MAX;
-    const BSrc bs = make_bsrc(a.actB, stage ? (uint32_t)nu * slot : (uint32_t)(a.T * a.K) * slot,
-                              NC, stage, NT3);
-    __syncthreads();
+    const int nSI = ((a.I >> 7) + 3) >> 2;
+    const uint32_t slot = (uint32_t)nSI * 1024u * 2 * a.T;
     f32x4 d = {0.f, 0.f, 0.f, 0.f};
-    if (s_exact) down_run<true>(d, ring, ds, bs, wave, NW, cnt, lane, live);
-    else         down_run<false>(d, ring, ds, bs, wave, NW, cnt, lane, live);
+    if ((uint32_t)nu * slot <= a.lds_bytes) k3_body<EXACT, true>(a, d, wave, lane, nu);
+    else                                    k3_body<EXACT, false>(a, d, wave, lane, nu);
     float acc[4] = {d[0], d[1], d[2], d[3]};
     wave_sum_lds<4, NT3 / WAVE>(acc, lds, wave, lane);
     if (wave != 0) return;
-    const int kq = lane >> 4, tok = n >> 1;
-    for (int i = 0; i < 4; i++) {
-        const float y = acc[i] + __shfl_xor(acc[i], 1);
-        if ((n & 1) == 0 && live) {
-            const int r = rt * 16 + 4 * kq + i;
-            const size_t o = (size_t)tok * a.H + r;
-            const float ys = a.ysh ? y + a.ysh[o] : y;
+    const int rt = blockIdx.x;
+    per_token<4>(acc, 2 * a.T, lane, [&](int r0, int tok, const float (&v)[4]) AI {
+        for (int i = 0; i < 4; i++) {
+            const size_t o = (size_t)tok * a.H + rt * 16 + r0 + i;
+            const float ys = a.ysh ? v[i] + a.ysh[o] : v[i];
             a.out[o] = a.resid ? a.resid[o] + ys : ys;
         }
-    }
+    });
 }
 
 // ------------------------------------------------------------------ launcher
@@ -734,64 +869,79 @@ static int record(k3x_moe_layer *L, int i, hipStream_t s)
     return hipEventRecord((hipEvent_t)L->ev[i], s) == hipSuccess ? 0 : K3X_E_HIP;
 }
 
+template <int NE>
+static void launch_k1b(const KSArgs &as, bool ldsb, dim3 grid, size_t lds, hipStream_t s)
+{
+    if (ldsb) hipLaunchKernelGGL((k1b_select_shdown<NE, true>), grid, dim3(NT), lds, s, as);
+    else      hipLaunchKernelGGL((k1b_select_shdown<NE, false>), grid, dim3(NT), 0, s, as);
+}
+
 extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x_dtype,
                               int T, const float *resid, int *idx, float *wt, void *stream)
 {
     const k3x_cfg *c = &L->cfg;
     hipStream_t s = (hipStream_t)stream;
-    const int NC = 2 * T;
+    const int H = c->hidden, I = c->moe_inter, NC = 2 * T;
+    const int nQ = H / 128, nS = (nQ + 3) / 4, nSI = (I / 128 + 3) / 4;
     int rc;
+
     K1Args a1;
     a1.router = L->router; a1.bias = L->bias; a1.x = x; a1.x_bf16 = (x_dtype == K3X_BF16);
-    a1.T = T; a1.H = c->hidden; a1.E = c->n_experts;
+    a1.T = T; a1.H = H; a1.E = c->n_experts;
     a1.score = L->score; a1.choice = L->choice; a1.xB = L->xB;
     a1.n_rwg = (c->n_experts + NT1 / WAVE / RWAVES - 1) / (NT1 / WAVE / RWAVES);
     a1.sh_gate = L->sh_gate; a1.sh_up = L->sh_up; a1.SI = L->SI; a1.shB = L->shB;
-    const uint32_t xbytes = (uint32_t)(c->hidden * NC * 2);
-    a1.stage = xbytes <= STAGE_MAX;
+    const uint32_t xset = (uint32_t)nQ * 256u * NC;
     const int n_sh = L->SI > 0 ? L->SI / 16 : 0;
     if ((rc = record(L, 0, s))) return rc;
-    hipLaunchKernelGGL(k1_router_shared, dim3(a1.n_rwg + n_sh), dim3(NT1),
-                       a1.stage ? xbytes + 16 : 0, s, a1);
+    if (xset <= STAGE_MAX)
+        hipLaunchKernelGGL(k1_router_shared<true>, dim3(a1.n_rwg + n_sh), dim3(NT1), xset, s, a1);
+    else
+        hipLaunchKernelGGL(k1_router_shared<false>, dim3(a1.n_rwg + n_sh), dim3(NT1), 0, s, a1);
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 1, s))) return rc;
 
     KSArgs as;
     as.score = L->score; as.choice = L->choice; as.E = c->n_experts; as.K = c->topk;
     as.renorm = c->moe_renorm; as.routed_scale = c->routed_scale; as.route = L->route;
-    as.idx = L->idx; as.wt = L->wt; as.uidx = idx; as.uwt = wt; as.T = T; as.H = c->hidden;
+    as.idx = L->idx; as.wt = L->wt; as.uidx = idx; as.uwt = wt; as.T = T; as.H = H;
     as.sh_down = L->sh_down; as.shB = L->shB; as.ysh = L->ysh; as.SI = L->SI;
-    const uint32_t sbytes = (uint32_t)(L->SI * NC * 2);
-    as.stage = L->SI > 0 && sbytes <= STAGE_MAX;
-    const dim3 gs(1 + (L->SI > 0 ? c->hidden / 16 : 0));
-    const size_t ls = as.stage ? sbytes + 16 : 0;
-    if (c->n_experts <= 128)      hipLaunchKernelGGL(k1b_select_shdown<2>, gs, dim3(NT), ls, s, as);
-    else if (c->n_experts <= 256) hipLaunchKernelGGL(k1b_select_shdown<4>, gs, dim3(NT), ls, s, as);
-    else if (c->n_experts <= 384) hipLaunchKernelGGL(k1b_select_shdown<6>, gs, dim3(NT), ls, s, as);
-    else if (c->n_experts <= 512) hipLaunchKernelGGL(k1b_select_shdown<8>, gs, dim3(NT), ls, s, as);
-    else                          hipLaunchKernelGGL(k1b_select_shdown<16>, gs, dim3(NT), ls, s, as);
+    const dim3 gs(1 + (L->SI > 0 ? H / 16 : 0));
+    const uint32_t shset = (uint32_t)(L->SI / 128) * 256u * NC;
+    const bool ldsb = shset <= STAGE_MAX;
+    const size_t ls = ldsb ? shset : 0;
+    if (c->n_experts <= 128)      launch_k1b<2>(as, ldsb, gs, ls, s);
+    else if (c->n_experts <= 256) launch_k1b<4>(as, ldsb, gs, ls, s);
+    else if (c->n_experts <= 384) launch_k1b<6>(as, ldsb, gs, ls, s);
+    else if (c->n_experts <= 512) launch_k1b<8>(as, ldsb, gs, ls, s);
+    else                          launch_k1b<16>(as, ldsb, gs, ls, s);
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 2, s))) return rc;
 
     K2Args a2;
     a2.experts = L->experts; a2.expert_bytes = L->expert_bytes;
     a2.gate_off = L->gate_off; a2.up_off = L->up_off; a2.route = L->route;
-    a2.xflags = L->xflags;
-    a2.xB = L->xB; a2.actB = L->actB; a2.T = T; a2.H = c->hidden; a2.I = c->moe_inter;
-    a2.stage = xbytes <= STAGE_MAX;
-    hipLaunchKernelGGL(k2_gateup, dim3(T * c->topk * (c->moe_inter / 16)), dim3(NT),
-                       a2.stage ? xbytes + 16 : 0, s, a2);
+    a2.xB = L->xB; a2.actB = L->actB; a2.T = T; a2.H = H; a2.I = I;
+    const uint32_t xfp4 = (uint32_t)nS * 1024u * NC;
+    const bool ex2 = (L->special & 3) != 0, st2 = xfp4 <= STAGE_MAX;
+    const dim3 g2(T * c->topk * (I / 16));
+    if (ex2 && st2)  hipLaunchKernelGGL((k2_gateup<true, true>), g2, dim3(NT), xfp4, s, a2);
+    else if (ex2)    hipLaunchKernelGGL((k2_gateup<true, false>), g2, dim3(NT), 0, s, a2);
+    else if (st2)    hipLaunchKernelGGL((k2_gateup<false, true>), g2, dim3(NT), xfp4, s, a2);
+    else             hipLaunchKernelGGL((k2_gateup<false, false>), g2, dim3(NT), 0, s, a2);
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 3, s))) return rc;
 
     K3Args a3;
     a3.experts = L->experts; a3.expert_bytes = L->expert_bytes; a3.down_off = L->down_off;
-    a3.route = L->route; a3.xflags = L->xflags; a3.actB = L->actB;
+    a3.route = L->route; a3.actB = L->actB;
     a3.ysh = L->SI > 0 ? L->ysh : NULL;
-    a3.out = out; a3.resid = resid; a3.T = T; a3.H = c->hidden; a3.I = c->moe_inter;
-    a3.K = c->topk;
-    a3.stage = 1;
-    hipLaunchKernelGGL(k3_down, dim3(c->hidden / 16), dim3(NT3), STAGE_MAX + 16, s, a3);
+    a3.out = out; a3.resid = resid; a3.T = T; a3.H = H; a3.I = I; a3.K = c->topk;
+    const uint32_t slot = (uint32_t)nSI * 1024u * NC;
+    const size_t all = (size_t)T * c->topk * slot;
+    a3.lds_bytes = slot <= STAGE_MAX ? (uint32_t)(all < STAGE_MAX ? all : (STAGE_MAX / slot) * slot) : 0u;
+    if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(H / 16), dim3(NT3), a3.lds_bytes, s, a3);
+    else                hipLaunchKernelGGL(k3_down<false>, dim3(H / 16), dim3(NT3), a3.lds_bytes, s, a3);
     if ((rc = launch_ok())) return rc;
     return record(L, 4, s);
 }
@@ -804,8 +954,8 @@ extern "C" int k3x_dev_prefill(k3x_moe_layer *L, float *out, const void *x, int 
 {
     const int H = L->cfg.hidden, K = L->cfg.topk;
     const size_t es = (x_dtype == K3X_BF16) ? 2 : 4;
-    for (int t0 = 0; t0 < T; t0 += K3X_DECODE_MAX_T) {
-        const int n = min(K3X_DECODE_MAX_T, T - t0);
+    for (int t0 = 0; t0 < T; t0 += L->tdec) {
+        const int n = min(L->tdec, T - t0);
         const int rc = k3x_dev_decode(L, out + (size_t)t0 * H,
                                       (const char *)x + (size_t)t0 * H * es, x_dtype, n,
                                       resid ? resid + (size_t)t0 * H : NULL,

@@ -112,7 +112,7 @@ __device__ __forceinline__ uint32_t ldw4(const void *p)
 // Range-checked loads: an offset at or beyond the buffer's size returns zeros without a
 // memory access (used for B-fragment lanes whose column holds no token).
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
-#define K3X_OOB 0xFFFFFFF0u
+#define K3X_OOB 0x80000000u   /* beyond any buffer here, with room for offsets */
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes)
 {
@@ -127,8 +127,7 @@ __device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off)
 // ------------------------------------------------------------------ layout offsets
 __device__ __forceinline__ size_t fp4_tile_bytes(int K)
 {
-    const int nq = K >> 7, ns = (nq + 3) >> 2;
-    return (size_t)nq * 1024 + (size_t)ns * 256;
+    return (size_t)(((K >> 7) + 3) >> 2) * 4352;
 }
 
 // COMPACT B FRAGMENTS of NC = 2T live columns: entry (q, t, kq, n) holds the 8 bf16 of
@@ -178,96 +177,6 @@ __device__ __forceinline__ u32x4 bfrag_of(const float (&v)[8], int hl)
     }
     u32x4 r = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
     return r;
-}
-
-// ------------------------------------------------------------------ quad streaming
-// One quad of a tiled fp4 matrix for this lane: 16 code bytes (4 products x 8 codes) and
-// the super-quad's scale dword (the quad's byte is picked when it is used, so a prefetch
-// never waits for its own data).
-struct Q4 {
-    u32x4    c;
-    uint32_t s;
-};
-
-__device__ __forceinline__ size_t fp4_quad_off(int q)
-{
-    return (size_t)(q >> 2) * 4352 + (size_t)(q & 3) * 1024;
-}
-__device__ __forceinline__ size_t fp4_scale_off(int q, int nQ)
-{
-    const int S = q >> 2, nq = min(4, nQ - 4 * S);
-    return (size_t)S * 4352 + (size_t)nq * 1024;
-}
-
-__device__ __forceinline__ void q4_load(Q4 &a, const uint8_t *tile, int q, int nQ, int lane)
-{
-    a.c = ldw16(tile + fp4_quad_off(q) + lane * 16);
-    a.s = ldw4(tile + fp4_scale_off(q, nQ) + lane * 4);
-}
-
-// Four B fragments of quad q (products t = 0..3) through a range-checked buffer.
-struct B4 {
-    u32x4 b[4];
-};
-
-// Where a lane's B fragments come from: a compact B-fragment set of NC columns at byte
-// offset `boff`, either in global memory through a range-checked buffer (lanes whose
-// column is not live read zeros without an access) or staged in LDS (those lanes read a
-// zero entry placed after the set).
-struct BSrc {
-    rsrc_t         r;
-    const uint8_t *lds;      // staged copy, or nullptr
-    uint32_t       zero;     // byte offset of the zero entry in the staged copy
-    int            NC;
-};
-
-__device__ __forceinline__ void b4_load(B4 &b, const BSrc &s, uint32_t boff, int q, int lane,
-                                        bool live)
-{
-    const int n = lane & 15, kq = lane >> 4;
-    const uint32_t e0 = boff + (uint32_t)(((q * 4) * 4 + kq) * s.NC + n) * 16u;
-    const uint32_t ts = (uint32_t)(4 * s.NC * 16);
-    const bool on = live && n < s.NC;
-    if (s.lds) {
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-            b.b[t] = *(const u32x4 *)(s.lds + (on ? e0 + ts * t : s.zero));
-    } else {
-#pragma unroll
-        for (int t = 0; t < 4; t++) b.b[t] = bload16(s.r, on ? e0 + ts * t : K3X_OOB);
-    }
-}
-
-// Stage `bytes` (a multiple of 16) of a compact B set into LDS and append a zero entry;
-// all threads of the workgroup take part; returns the zero entry's offset.
-__device__ __forceinline__ uint32_t stage_b(uint8_t *lds, const void *src, uint32_t bytes,
-                                            int tid, int nthreads)
-{
-    for (uint32_t o = (uint32_t)tid * 16u; o < bytes; o += (uint32_t)nthreads * 16u)
-        *(u32x4 *)(lds + o) = ld16((const uint8_t *)src + o);
-    if (tid == 0) *(u32x4 *)(lds + bytes) = (u32x4){0u, 0u, 0u, 0u};
-    return bytes;
-}
-
-// d += dequant(a) x b for one quad (its scale byte is byte `sel` of a.s).  EXACT takes
-// the reference's float product for any scale byte; the fast path needs bytes 1..252
-// (every weight finite; the layer records per expert which path its bytes need).
-// `valid` false marks a padding quad (zero B fragments): the exact path then zeroes the
-// codes too, so an infinite weight cannot turn the zero product into NaN.
-template <bool EXACT>
-__device__ __forceinline__ void q4_mfma(f32x4 &d, const Q4 &a, int sel, const B4 &b,
-                                        bool valid = true)
-{
-    const uint32_t sb = (a.s >> (8 * sel)) & 255u;
-    if (!EXACT) {
-        const float sc = e8m0_scale(sb);
-#pragma unroll
-        for (int t = 0; t < 4; t++) d = mfma(dq8(a.c[t], sc), as_bf16x8(b.b[t]), d);
-    } else {
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-            d = mfma(dq8_exact(valid ? a.c[t] : 0u, sb), as_bf16x8(b.b[t]), d);
-    }
 }
 
 // Cross-wave sum of per-lane accumulators through LDS; wave 0 ends with the total.

@@ -11,8 +11,9 @@
  *
  * K3X TILED MXFP4 (a matrix of R rows by K columns, R % 16 == 0, K % 128 == 0).
  *   The matrix is cut into R/16 row tiles, stored one after another.  A tile is K/128
- *   "quads" of 128 columns, grouped four to a "super-quad".  A super-quad holds the
- *   codes of its nq (<= 4) quads, 1024 bytes each, then 256 bytes of scales:
+ *   "quads" of 128 columns, grouped four to a "super-quad" of 4352 bytes (the last one
+ *   padded with zero quads when K/128 is not a multiple of 4).  A super-quad holds the
+ *   codes of its 4 quads, 1024 bytes each, then 256 bytes of scales:
  *     codes of quad q, lane l (m = l % 16, kq = l / 16): the 16 bytes of row 16*rt + m
  *       that hold columns 128*q + 32*kq .. +31 (one 32-column scale group, low nibble =
  *       even column, as in the reference's packed rows);
@@ -45,14 +46,15 @@ extern "C" {
 #endif
 
 #define K3X_DECODE_MAX_T 8       /* tokens per call on the decode path (2 columns each) */
+#define K3X_STAGE_MAX    65536   /* bytes of activation fragments a workgroup stages in LDS */
 #define K3X_MAX_TOPK     64      /* K3_MAX_TOPK, k3.h:857-864 */
 #define K3X_ROUTER_WAVES 8       /* experts per router workgroup (one wave each) */
 
 /* byte sizes of the tiled formats */
 static inline size_t k3x_fp4_tile_bytes(int K)
 {
-    const int nq = K / 128, ns = (nq + 3) / 4;
-    return (size_t)nq * 1024 + (size_t)ns * 256;
+    const int ns = (K / 128 + 3) / 4;
+    return (size_t)ns * 4352;
 }
 static inline size_t k3x_fp4_matrix_bytes(int R, int K) { return (size_t)(R / 16) * k3x_fp4_tile_bytes(K); }
 static inline size_t k3x_bf16_matrix_bytes(int R, int K) { return (size_t)R * K * 2; }
@@ -92,22 +94,25 @@ struct k3x_moe_layer {
     k3x_cfg   cfg;
     int       device;
     int       SI;                 /* n_shared * moe_inter */
+    int       tdec;               /* tokens per decode-path call (<= K3X_DECODE_MAX_T) */
     /* weights */
     float    *router;             /* [E][H] */
     float    *bias;               /* [E] (zeros when absent) */
     uint8_t  *experts;            /* E * expert_bytes */
     size_t    expert_bytes, gate_off, up_off, down_off;
-    int      *xflags;             /* [E] bit 0 gate, 1 up, 2 down: a scale byte outside
-                                     1..252 (the exact dequantisation path is needed) */
+    int       special;            /* bit 0 gate, 1 up, 2 down: some expert's matrix has a
+                                     scale byte outside 1..252 (the exact dequantisation
+                                     kernels are launched) */
     uint16_t *sh_gate, *sh_up, *sh_down;   /* tiled bf16, NULL when SI == 0 */
     /* decode working buffers */
     float    *score, *choice;     /* [DECODE_MAX_T][E] */
     int      *idx;                /* [DECODE_MAX_T][K] */
     float    *wt;                 /* [DECODE_MAX_T][K] */
     k3x_route *route;
-    uint16_t *xB;                 /* B fragments of x: [H/128][4][64][8] */
-    uint16_t *actB;               /* [DECODE_MAX_T*K][I/128][4][64][8] */
-    uint16_t *shB;                /* [SI/128][4][64][8] */
+    uint16_t *xB;                 /* compact B set of x over whole super-quads of H */
+    uint16_t *actB;               /* DECODE_MAX_T*K slots: B set of each unique expert's
+                                     activation over whole super-quads of I */
+    uint16_t *shB;                /* B set of the shared activation (SI/128 quads) */
     float    *ysh;                /* [DECODE_MAX_T][H] shared expert output */
     k3x_prefill_buf pf;
     size_t    bytes;

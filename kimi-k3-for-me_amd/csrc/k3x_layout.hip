@@ -24,13 +24,13 @@ __global__ void tile_fp4_kernel(uint8_t *dst, const uint8_t *packed, const uint8
         const int nq = min(4, nQ - 4 * S);
         uint8_t *so = dst + (size_t)rt * tb + (size_t)S * 4352;
         uint32_t sw = 0;
-        for (int j = 0; j < nq; j++) {
+        for (int j = 0; j < 4; j++) {
             const int q = 4 * S + j;
             const uint8_t *src = packed + (size_t)row * (K / 2) + (size_t)(128 * q + 32 * kq) / 2;
-            for (int b = 0; b < 16; b++) so[j * 1024 + l * 16 + b] = src[b];
-            sw |= (uint32_t)scales[(size_t)row * (K / 32) + 4 * q + kq] << (8 * j);
+            for (int b = 0; b < 16; b++) so[j * 1024 + l * 16 + b] = j < nq ? src[b] : 0;
+            if (j < nq) sw |= (uint32_t)scales[(size_t)row * (K / 32) + 4 * q + kq] << (8 * j);
         }
-        *(uint32_t *)(so + nq * 1024 + l * 4) = sw;
+        *(uint32_t *)(so + 4096 + l * 4) = sw;
     }
 }
 
@@ -49,7 +49,7 @@ __global__ void untile_fp4_kernel(uint8_t *packed, uint8_t *scales, const uint8_
         const int row = rt * 16 + m;
         const int nq = min(4, nQ - 4 * S);
         const uint8_t *so = src + (size_t)rt * tb + (size_t)S * 4352;
-        const uint32_t sw = *(const uint32_t *)(so + nq * 1024 + l * 4);
+        const uint32_t sw = *(const uint32_t *)(so + 4096 + l * 4);
         for (int j = 0; j < nq; j++) {
             const int q = 4 * S + j;
             uint8_t *d = packed + (size_t)row * (K / 2) + (size_t)(128 * q + 32 * kq) / 2;
@@ -107,17 +107,20 @@ __global__ void synth_fp4_kernel(uint8_t *dst, int R, int K, uint64_t ck, uint64
         const int nq = min(4, nQ - 4 * S);
         uint8_t *so = dst + (size_t)rt * tb + (size_t)S * 4352;
         uint32_t sw = 0;
-        for (int j = 0; j < nq; j++) {
+        for (int j = 0; j < 4; j++) {
             const int q = 4 * S + j;
-            const uint64_t i0 = (uint64_t)row * (K / 2) + (uint64_t)(128 * q + 32 * kq) / 2;
-            // i0 is a multiple of 16, so the 16 bytes are two whole draws
-            const uint64_t d0 = draw(ck, i0 >> 3), d1 = draw(ck, (i0 >> 3) + 1);
-            u32x4 v = {(uint32_t)d0, (uint32_t)(d0 >> 32), (uint32_t)d1, (uint32_t)(d1 >> 32)};
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (j < nq) {
+                const uint64_t i0 = (uint64_t)row * (K / 2) + (uint64_t)(128 * q + 32 * kq) / 2;
+                // i0 is a multiple of 16, so the 16 bytes are two whole draws
+                const uint64_t d0 = draw(ck, i0 >> 3), d1 = draw(ck, (i0 >> 3) + 1);
+                v = (u32x4){(uint32_t)d0, (uint32_t)(d0 >> 32), (uint32_t)d1, (uint32_t)(d1 >> 32)};
+                const uint64_t si = (uint64_t)row * (K / 32) + 4 * q + kq;
+                sw |= (uint32_t)(lo + (int)((draw(sk, si) >> 32) % span)) << (8 * j);
+            }
             *(u32x4 *)(so + j * 1024 + l * 16) = v;
-            const uint64_t si = (uint64_t)row * (K / 32) + 4 * q + kq;
-            sw |= (uint32_t)(lo + (int)((draw(sk, si) >> 32) % span)) << (8 * j);
         }
-        *(uint32_t *)(so + nq * 1024 + l * 4) = sw;
+        *(uint32_t *)(so + 4096 + l * 4) = sw;
     }
 }
 

@@ -85,16 +85,16 @@ static int layer_alloc(k3x_moe_layer *L)
     int rc;
     layout(L);
     L->SI = c->moe_inter * c->n_shared;
+    L->tdec = K3X_DECODE_MAX_T;
     size_t *b = &L->bytes;
     RCCHK(dmalloc((void **)&L->router, (size_t)E * H * 4, b));
     RCCHK(dmalloc((void **)&L->bias, (size_t)E * 4, b));
     RCCHK(dmalloc((void **)&L->experts, (size_t)E * L->expert_bytes, b));
-    RCCHK(dmalloc((void **)&L->xflags, (size_t)E * sizeof(int), b));
     if (L->SI > 0) {
         RCCHK(dmalloc((void **)&L->sh_gate, k3x_bf16_matrix_bytes(L->SI, H), b));
         RCCHK(dmalloc((void **)&L->sh_up, k3x_bf16_matrix_bytes(L->SI, H), b));
         RCCHK(dmalloc((void **)&L->sh_down, k3x_bf16_matrix_bytes(H, L->SI), b));
-        RCCHK(dmalloc((void **)&L->shB, (size_t)L->SI * 16 * 2, b));
+        RCCHK(dmalloc((void **)&L->shB, (size_t)L->SI * 2 * K3X_DECODE_MAX_T * 2, b));
         RCCHK(dmalloc((void **)&L->ysh, (size_t)K3X_DECODE_MAX_T * H * 4, b));
     }
     RCCHK(dmalloc((void **)&L->score, (size_t)K3X_DECODE_MAX_T * E * 4, b));
@@ -102,8 +102,10 @@ static int layer_alloc(k3x_moe_layer *L)
     RCCHK(dmalloc((void **)&L->idx, (size_t)K3X_DECODE_MAX_T * K * 4, b));
     RCCHK(dmalloc((void **)&L->wt, (size_t)K3X_DECODE_MAX_T * K * 4, b));
     RCCHK(dmalloc((void **)&L->route, sizeof(k3x_route), b));
-    RCCHK(dmalloc((void **)&L->xB, (size_t)H * 16 * 2, b));
-    RCCHK(dmalloc((void **)&L->actB, (size_t)K3X_DECODE_MAX_T * K * I * 16 * 2, b));
+    /* B sets of 2*DECODE_MAX_T columns over whole super-quads (512 elements) */
+    const size_t hs = (size_t)(H + 511) / 512 * 512, is = (size_t)(I + 511) / 512 * 512;
+    RCCHK(dmalloc((void **)&L->xB, hs * 2 * K3X_DECODE_MAX_T * 2, b));
+    RCCHK(dmalloc((void **)&L->actB, (size_t)K3X_DECODE_MAX_T * K * is * 2 * K3X_DECODE_MAX_T * 2, b));
     if (hipMemset(L->bias, 0, (size_t)E * 4) != hipSuccess) return K3X_E_HIP;
     return 0;
 fail:
@@ -113,7 +115,7 @@ fail:
 static void layer_free(k3x_moe_layer *L)
 {
     if (!L) return;
-    void *p[] = {L->router, L->bias, L->experts, L->xflags, L->sh_gate, L->sh_up, L->sh_down, L->shB,
+    void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shB,
                  L->ysh, L->score, L->choice, L->idx, L->wt, L->route,
                  L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out};
     for (size_t i = 0; i < sizeof p / sizeof p[0]; i++)
@@ -222,13 +224,10 @@ int k3x_moe_layer_create(const k3x_cfg *c, const k3x_moe_w *w, int device,
     if (rc) return rc;
     const int H = c->hidden, E = c->n_experts, I = c->moe_inter;
     uint8_t *stage = NULL;
-    int *flags = NULL;
     HIPCHK(hipMemcpy(L->router, w->gate, (size_t)E * H * 4, hipMemcpyHostToDevice));
     if (w->bias) HIPCHK(hipMemcpy(L->bias, w->bias, (size_t)E * 4, hipMemcpyHostToDevice));
     RCCHK(upload_shared(L, w->sh1, w->sh3, w->sh2));
     HIPCHK(hipMalloc((void **)&stage, 3 * ((size_t)I * H / 2 + (size_t)I * H / 32)));
-    flags = (int *)calloc((size_t)E, sizeof(int));
-    if (!flags) { rc = K3X_E_NOMEM; goto fail; }
     for (int e = 0; e < E; e++) {
         k3x_expert_q q;
         if (w->src) {
@@ -244,16 +243,13 @@ int k3x_moe_layer_create(const k3x_cfg *c, const k3x_moe_w *w, int device,
             q = w->bank[e];
         }
         RCCHK(upload_expert(L, e, &q, stage));
-        flags[e] = scale_flags(&q, (size_t)I * H / 32);
+        L->special |= scale_flags(&q, (size_t)I * H / 32);
     }
-    HIPCHK(hipMemcpy(L->xflags, flags, (size_t)E * sizeof(int), hipMemcpyHostToDevice));
     hipFree(stage);
-    free(flags);
     *out = L;
     return 0;
 fail:
     if (stage) hipFree(stage);
-    free(flags);
     layer_free(L);
     return rc;
 }
@@ -294,7 +290,7 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     if (((uintptr_t)x & 15) || ((uintptr_t)out & 15)) return K3X_E_ARG;
     if ((idx == NULL) != (wt == NULL)) return K3X_E_ARG;
     if (T == 0) return 0;
-    if (T <= K3X_DECODE_MAX_T)
+    if (T <= L->tdec)
         return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, stream);
     return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
 }
@@ -480,15 +476,7 @@ int k3x_synth_layer_create(const k3x_cfg *c, const k3x_synth_spec *s, int device
         free(hb);
         hb = NULL;
     }
-    {
-        const int f = (s->scale_lo < 1 || s->scale_hi > 252) ? 7 : 0;
-        hf = (float *)malloc((size_t)E * sizeof(int));
-        if (!hf) { rc = K3X_E_NOMEM; goto fail; }
-        for (int e = 0; e < E; e++) ((int *)hf)[e] = f;
-        HIPCHK(hipMemcpy(L->xflags, hf, (size_t)E * sizeof(int), hipMemcpyHostToDevice));
-        free(hf);
-        hf = NULL;
-    }
+    L->special = (s->scale_lo < 1 || s->scale_hi > 252) ? 7 : 0;
     for (int e = 0; e < E; e++) {
         uint8_t *base = L->experts + (size_t)e * L->expert_bytes;
         const struct { size_t off; int R, K, m; } mm[3] = {

@@ -54,6 +54,20 @@ def kernel_bytes(U, T):
     return dict(zip(KERNELS, (k1, k1b, k2, k3)))
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary (FETCH_SIZE and
+    WRITE_SIZE runs scaled by a plain copy's readings), or None."""
+    path = os.path.join(ROOT, "profiles", "decode_b1_hbm_traffic.md")
+    try:
+        for line in open(path):
+            f = line.split()
+            if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == kernel:
+                return int(f[2])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(n_tokens=24, min_seconds=10.0):
     """The layer on the host CPU over a bounded sample of tokens (same seeded layer)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -109,6 +123,24 @@ def cpu_baseline(n_tokens=24, min_seconds=10.0):
                       f"OpenMP threads {cores}"}
 
 
+def copy_calibration(torch, mib, reps):
+    """A plain device-to-device copy of a known size: FETCH_SIZE and WRITE_SIZE read
+    for it give the factor between those counters and bytes moved."""
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / reps
+    print(json.dumps({"copy_bytes": n, "reps": reps, "ms_per_copy": round(ms, 4),
+                      "copy_gbs": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -116,6 +148,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only time a plain device copy of MIB MiB (the reference kernel for "
+                         "the HBM byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -125,6 +160,9 @@ def main():
 
     import torch
     assert torch.cuda.is_available(), "no GPU visible"
+    if args.calibrate_copy:
+        copy_calibration(torch, args.calibrate_copy, max(args.steps, 1))
+        return
     k3x = load_k3x()
     dev = torch.device("cuda:0")
     cfg = k3x.make_cfg(H, E, K, I, 1, 1, 2.5)
@@ -196,7 +234,7 @@ def main():
         "kernel_avg_us": {n: round(v * 1e3, 2) for n, v in avg.items()},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
                      "algorithmic_bytes_per_launch": kb[dom]},
         "layer_build_s": round(build_s, 2),
     }

@@ -113,7 +113,7 @@ int  k3x_moe_layer_read_expert(const k3x_moe_layer *L, int e, unsigned char *p1,
 
 /* ---- device-pointer forward --------------------------------------------------------
  * out  fp32 [T][hidden] device, overwritten (or resid + MoE when resid != NULL;
- *      resid may equal out).
+ *      resid may equal out).  x, out and resid are 16-byte aligned (else K3X_E_ARG).
  * x    [T][hidden] device, K3X_F32 or K3X_BF16.
  * idx/wt  optional device [T][topk]: every token's routing (expert indices in selection
  *      order, combine weights after renorm and routed_scale), as k3_router writes them

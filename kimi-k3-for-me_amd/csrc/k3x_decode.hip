@@ -28,6 +28,7 @@
 // when they fit: their loads are issued before the first weights, so the loop waits on
 // nothing but its own weight stream.
 #include "k3x_device.h"
+#include "k3x_topk.h"
 
 #define NT1 512     // k1 workgroup: 8 waves
 #define NT  256     // k1b / k2 workgroup: 4 waves
@@ -37,32 +38,11 @@
 
 extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
 
-#define AI __attribute__((always_inline))
-
-__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE); }
-
-// Number of items w, w + st, ... below n.
-__device__ __forceinline__ int strided_count(int w, int st, int n) { return w < n ? (n - 1 - w) / st + 1 : 0; }
-
-// ------------------------------------------------------------------ loads
-// Weights: range-checked buffer loads with the non-temporal cache policy (they are read
-// once per call and should not displace the activations).
-#define CPOL_NT 2
-__device__ __forceinline__ u32x4 wld16(rsrc_t r, uint32_t off)
-{
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_NT);
-}
-__device__ __forceinline__ uint32_t wld4(rsrc_t r, uint32_t off)
-{
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_NT);
-}
-
 // Items 0 .. cnt-1 through a ring of R slots: ld(slot, k) issues item k's loads (any k;
 // k >= cnt must load nothing), use(slot, k) consumes item k.  ring_prime issues the
 // first R items; ring_loop runs the rest, refilling a slot right after it is used.
 // Scheduling barriers keep each slot's loads together and in slot order, in the prime
 // as in the loop: the wait counts of the loop body are derived from both orders.
-#define SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 template <int R, class LD>
 __device__ __forceinline__ void ring_prime(LD ld)
 {
@@ -497,114 +477,6 @@ __global__ void __launch_bounds__(NT1) k1_router_shared(K1Args a)
     k1_shared<LDSX>(a, lds, blockIdx.x - a.n_rwg);
 }
 
-// ------------------------------------------------------------------ top-k
-// Order-preserving key of a choice value: larger float -> larger key; -0 is +0 (they
-// compare equal in the reference); NaN -> 0 (never selected); -inf -> K_NEG_INF (never
-// selected either: the reference's strict '>' against -inf fails).
-#define K_NEG_INF 0x007FFFFFu
-__device__ __forceinline__ uint32_t choice_key(float f)
-{
-    uint32_t u = __float_as_uint(f);
-    if (f != f) return 0u;
-    if (u == 0x80000000u) u = 0u;
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ int lanes_below(uint64_t m)
-{
-    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-}
-
-__device__ __forceinline__ float bload_f32(rsrc_t r, uint32_t off)
-{
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-}
-
-// One token's top-k by one wave, equal to the reference's repeated maximum
-// (k3_ops.c:1700-1708): the K largest choices in descending order, the lower index first
-// among equal values, NaN and -inf never taken (a pick with nothing left gives index 0,
-// weight 0).  A 32-step bitwise search with ballot counts finds the k-th largest key;
-// the k selected are then ranked.  Weights are the unbiased scores, renormalised through
-// a double sum and a float reciprocal, then scaled (:1710-1716).  Results in s_idx/s_w.
-// NE: 64-expert chunks held per lane.
-template <int NE>
-__device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, int renorm,
-                          float routed_scale, int *s_idx, float *s_w, uint64_t *s_key,
-                          int *s_e, float *s_sc, int lane)
-{
-    uint32_t key[NE];
-    float sco[NE];
-#pragma unroll
-    for (int c = 0; c < NE; c++) {
-        const int e = lane + WAVE * c;
-        const uint32_t off = row_off + 4u * (uint32_t)e;
-        const float v = bload_f32(cr, e < E ? off : K3X_OOB);
-        sco[c] = bload_f32(sr, e < E ? off : K3X_OOB);
-        key[c] = e < E ? choice_key(v) : 0u;
-    }
-    int nvalid = 0;
-#pragma unroll
-    for (int c = 0; c < NE; c++) nvalid += __popcll(__ballot(key[c] > K_NEG_INF));
-    const int ke = min(K, nvalid);
-    uint32_t tau = 0xFFFFFFFFu;
-    if (ke > 0) {
-        tau = 0u;
-        for (int b = 31; b >= 0; b--) {
-            const uint32_t cand = tau | (1u << b);
-            int cnt = 0;
-#pragma unroll
-            for (int c = 0; c < NE; c++) cnt += __popcll(__ballot(key[c] >= cand));
-            if (cnt >= ke) tau = cand;
-        }
-    }
-    int ngt = 0;
-#pragma unroll
-    for (int c = 0; c < NE; c++) ngt += __popcll(__ballot(key[c] > tau));
-    int need = ke - ngt;                    // ties at tau, taken in ascending index
-    int base = 0;
-#pragma unroll
-    for (int c = 0; c < NE; c++) {
-        const uint64_t eq = __ballot(ke > 0 && key[c] == tau);
-        const int take = min(need, (int)__popcll(eq));
-        need -= take;
-        const bool sel = (ke > 0) && (key[c] > tau || (key[c] == tau && lanes_below(eq) < take));
-        const uint64_t sm = __ballot(sel);
-        if (sel) {
-            const int pos = base + lanes_below(sm);
-            const int e = lane + WAVE * c;
-            s_key[pos] = ((uint64_t)key[c] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
-            s_e[pos] = e;
-            s_sc[pos] = sco[c];
-        }
-        base += (int)__popcll(sm);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    if (lane < ke) {
-        const uint64_t my = s_key[lane];
-        int rank = 0;
-        for (int i = 0; i < ke; i++) rank += s_key[i] > my;
-        s_idx[rank] = s_e[lane];
-        s_w[rank] = s_sc[lane];
-    } else if (lane < K) {
-        s_idx[lane] = 0;
-        s_w[lane] = 0.0f;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    if (lane == 0) {
-        if (renorm && K > 1) {
-            double sum = 0.0;
-            for (int j = 0; j < K; j++) sum += (double)s_w[j];
-            const float inv = (float)(1.0 / (sum + 1e-20));
-            for (int j = 0; j < K; j++) s_w[j] *= inv;
-        }
-        for (int j = 0; j < K; j++) s_w[j] *= routed_scale;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-}
-
 // ------------------------------------------------------------------ K1b
 struct KSArgs {
     const float   *score, *choice;
@@ -944,24 +816,4 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     else                hipLaunchKernelGGL(k3_down<false>, dim3(H / 16), dim3(NT3), a3.lds_bytes, s, a3);
     if ((rc = launch_ok())) return rc;
     return record(L, 4, s);
-}
-
-// Prefill, first form: the decode pipeline over consecutive groups of up to
-// K3X_DECODE_MAX_T tokens.  Each token's result depends only on its own routing, so the
-// grouping changes no result.
-extern "C" int k3x_dev_prefill(k3x_moe_layer *L, float *out, const void *x, int x_dtype,
-                               int T, const float *resid, int *idx, float *wt, void *stream)
-{
-    const int H = L->cfg.hidden, K = L->cfg.topk;
-    const size_t es = (x_dtype == K3X_BF16) ? 2 : 4;
-    for (int t0 = 0; t0 < T; t0 += L->tdec) {
-        const int n = min(L->tdec, T - t0);
-        const int rc = k3x_dev_decode(L, out + (size_t)t0 * H,
-                                      (const char *)x + (size_t)t0 * H * es, x_dtype, n,
-                                      resid ? resid + (size_t)t0 * H : NULL,
-                                      idx ? idx + (size_t)t0 * K : NULL,
-                                      wt ? wt + (size_t)t0 * K : NULL, stream);
-        if (rc) return rc;
-    }
-    return 0;
 }

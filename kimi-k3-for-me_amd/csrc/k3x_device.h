@@ -124,6 +124,29 @@ __device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off)
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
 
+// ------------------------------------------------------------------ waves
+#define AI __attribute__((always_inline))
+
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE); }
+
+// Number of items w, w + st, ... below n.
+__device__ __forceinline__ int strided_count(int w, int st, int n) { return w < n ? (n - 1 - w) / st + 1 : 0; }
+
+// ------------------------------------------------------------------ weight loads
+// Weights: range-checked buffer loads with the non-temporal cache policy (they are read
+// once per call and should not displace the activations).
+#define CPOL_NT 2
+__device__ __forceinline__ u32x4 wld16(rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_NT);
+}
+__device__ __forceinline__ uint32_t wld4(rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_NT);
+}
+
+#define SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+
 // ------------------------------------------------------------------ layout offsets
 __device__ __forceinline__ size_t fp4_tile_bytes(int K)
 {

@@ -67,27 +67,25 @@ typedef struct k3x_route {
     float wtok[K3X_DECODE_MAX_T * K3X_MAX_TOPK][K3X_DECODE_MAX_T]; /* [u][token], 0 = not chosen */
 } k3x_route;
 
-/* prefill working buffers, grown on demand */
+/* prefill working buffers (one allocation), sized for cap_T tokens per pipeline run */
 typedef struct k3x_prefill_buf {
-    int     cap_T;          /* tokens the buffers hold */
-    void   *base;           /* one device allocation   */
-    size_t  bytes;
-    float  *score, *choice; /* [T][n_experts]          */
-    int    *idx;            /* [T][K]                  */
-    float  *wt;             /* [T][K]                  */
-    int    *counts;         /* [n_experts + 1]         */
-    int    *offsets;        /* [n_experts + 1]         */
-    int    *cursor;         /* [n_experts]             */
-    int    *perm_tok;       /* [T*K] token of each permuted row */
-    int    *pos;            /* [T][K] permuted row of each (token, slot) */
-    int    *tiles;          /* [T*K/16 + n_experts] work list of (expert, row0) */
-    int    *ntiles;         /* [1] */
-    uint16_t *xb;           /* [T][hidden] bf16 hi, then lo: [2][T][hidden] */
-    float  *act;            /* [T*K][moe_inter]        */
-    uint16_t *actb;         /* [2][T*K][moe_inter] bf16 hi/lo */
-    float  *y;              /* [T*K][hidden] expert outputs   */
-    float  *sact;           /* [T][SI] shared activation      */
-    uint16_t *sactb;        /* [2][T][SI]              */
+    int       cap_T;
+    void     *base;
+    size_t    bytes;
+    uint16_t *xhl;          /* [T][H/8][2][8] bf16 hi/lo activation rows            */
+    float    *score, *choice; /* [T][E]                                             */
+    int      *idx;          /* [T][K]                                                */
+    float    *wt;           /* [T][K]                                                */
+    int      *counts;       /* [E] tokens per expert                                 */
+    int      *offsets;      /* [E+1] first permuted row of each expert               */
+    int      *cursor;       /* [E]                                                   */
+    int      *tb_gu, *tb_dn;  /* [E+1] first GEMM tile of each expert               */
+    int      *perm_tok;     /* [T*K] token of each permuted row                      */
+    float    *perm_w;       /* [T*K] routing weight of each permuted row             */
+    int      *pos_of;       /* [T*K] permuted row of each (token, slot)              */
+    uint16_t *act;          /* [T*K][I/8][2][8] routed activations, hi/lo            */
+    uint16_t *act_sh;       /* [T][SI/8][2][8] shared activations                    */
+    float    *y;            /* [T*K + T][H] expert and shared output rows            */
 } k3x_prefill_buf;
 
 struct k3x_moe_layer {
@@ -138,6 +136,7 @@ int k3x_dev_decode(struct k3x_moe_layer *L, float *out, const void *x, int x_dty
                    const float *resid, int *idx, float *wt, void *stream);
 int k3x_dev_prefill(struct k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                     const float *resid, int *idx, float *wt, void *stream);
+int k3x_pf_reserve(struct k3x_moe_layer *L, int T);   /* k3x_moe.c */
 int k3x_dev_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
                     void *stream);
 

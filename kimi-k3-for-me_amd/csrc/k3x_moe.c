@@ -281,13 +281,61 @@ fail:
     return rc;
 }
 
+/* Prefill working buffers for T tokens per pipeline run: one allocation, carved into
+ * 256-byte-aligned regions; grown (never shrunk) when a larger T arrives. */
+int k3x_pf_reserve(k3x_moe_layer *L, int T)
+{
+    k3x_prefill_buf *B = &L->pf;
+    if (T <= B->cap_T) return 0;
+    const k3x_cfg *c = &L->cfg;
+    const size_t H = (size_t)c->hidden, E = (size_t)c->n_experts, K = (size_t)c->topk,
+                 I = (size_t)c->moe_inter, SI = (size_t)L->SI, t = (size_t)T;
+    const size_t sz[] = {
+        t * H * 4,                 /* xhl     */
+        t * E * 4, t * E * 4,      /* score, choice */
+        t * K * 4, t * K * 4,      /* idx, wt */
+        E * 4, (E + 1) * 4, E * 4, /* counts, offsets, cursor */
+        (E + 1) * 4, (E + 1) * 4,  /* tb_gu, tb_dn */
+        t * K * 4, t * K * 4, t * K * 4,   /* perm_tok, perm_w, pos_of */
+        t * K * I * 4,             /* act     */
+        (SI ? t * SI * 4 : 256),   /* act_sh  */
+        (t * K + t) * H * 4,       /* y       */
+    };
+    enum { N = sizeof sz / sizeof sz[0] };
+    size_t off[N], total = 0;
+    for (int i = 0; i < N; i++) {
+        off[i] = total;
+        total += (sz[i] + 255) & ~(size_t)255;
+    }
+    void *base = NULL;
+    if (hipSetDevice(L->device) != hipSuccess) return K3X_E_HIP;
+    if (hipMalloc(&base, total) != hipSuccess) return K3X_E_NOMEM;
+    if (B->base) {
+        if (hipDeviceSynchronize() != hipSuccess) { hipFree(base); return K3X_E_HIP; }
+        hipFree(B->base);
+    }
+    char *p = (char *)base;
+    B->base = base; B->bytes = total; B->cap_T = T;
+    B->xhl = (uint16_t *)(p + off[0]);
+    B->score = (float *)(p + off[1]);   B->choice = (float *)(p + off[2]);
+    B->idx = (int *)(p + off[3]);       B->wt = (float *)(p + off[4]);
+    B->counts = (int *)(p + off[5]);    B->offsets = (int *)(p + off[6]);
+    B->cursor = (int *)(p + off[7]);
+    B->tb_gu = (int *)(p + off[8]);     B->tb_dn = (int *)(p + off[9]);
+    B->perm_tok = (int *)(p + off[10]); B->perm_w = (float *)(p + off[11]);
+    B->pos_of = (int *)(p + off[12]);
+    B->act = (uint16_t *)(p + off[13]); B->act_sh = (uint16_t *)(p + off[14]);
+    B->y = (float *)(p + off[15]);
+    return 0;
+}
+
 /* ---------------------------------------------------------------- forward ---- */
 int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                     const float *resid, int *idx, float *wt, void *stream)
 {
     if (!L || (T > 0 && (!out || !x))) return K3X_E_ARG;
     if (T < 0 || (x_dtype != K3X_F32 && x_dtype != K3X_BF16)) return K3X_E_ARG;
-    if (((uintptr_t)x & 15) || ((uintptr_t)out & 15)) return K3X_E_ARG;
+    if (((uintptr_t)x & 15) || ((uintptr_t)out & 15) || ((uintptr_t)resid & 15)) return K3X_E_ARG;
     if ((idx == NULL) != (wt == NULL)) return K3X_E_ARG;
     if (T == 0) return 0;
     if (T <= L->tdec)

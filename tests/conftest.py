@@ -42,3 +42,10 @@ def ref_lib():
     if r is None:
         pytest.skip("compiled reference (oracle/_ref) not built: reference tree absent")
     return r
+
+
+@pytest.fixture(scope="session")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "no GPU visible"
+    return t

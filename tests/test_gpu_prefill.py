@@ -1,0 +1,120 @@
+"""GPU parity of the prefill pipeline (more than 8 tokens per call), through the C ABI.
+
+Same bar as the decode path: selected expert indices bit-exact (ties to the lower index),
+routing weights to float rounding, outputs within TOL relative L2 of the oracle, which is
+bitwise the reference's k3_moe / k3_moe_prefill.  At the full size (2048 tokens, Zipf-
+skewed routing) the oracle's router runs for every token and its whole layer for a
+sample of tokens; every token is also checked against the decode path, whose grouping of
+tokens must not change any result.
+"""
+import numpy as np
+import pytest
+
+import synth
+from gpu_util import bank_layer, dev_forward, say, synth_layer
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3          # relative L2, from the north star
+
+
+def decode_forward(torch, k3x, layer, x, bf16):
+    """The same tokens through the decode path, 8 at a time."""
+    outs, idxs, wts = [], [], []
+    for t0 in range(0, x.shape[0], 8):
+        o, i, w = dev_forward(torch, k3x, layer, x[t0:t0 + 8], bf16=bf16)
+        outs.append(o); idxs.append(i); wts.append(w)
+    return np.concatenate(outs), np.concatenate(idxs), np.concatenate(wts)
+
+
+@pytest.mark.parametrize("T,bf16", [(9, False), (37, False), (37, True), (130, True)])
+def test_tiny_prefill_vs_oracle(torch, k3x, T, bf16):
+    say(f"case: tiny layer prefill T={T} bf16={bf16} vs oracle")
+    L = synth.tiny(seed=11)
+    layer = bank_layer(k3x, L)
+    x = L.x(T, bf16=bf16, stream_sub=T)
+    o, idx, wt, _ = L.oracle_moe(x)
+    out, i2, w2 = dev_forward(torch, k3x, layer, x, bf16=bf16)
+    assert np.array_equal(i2, idx)
+    np.testing.assert_allclose(w2, wt, rtol=1e-6)
+    err = synth.rel_l2(out, o)
+    say(f"  rel_l2={err:.3e}")
+    assert err < TOL
+    layer.close()
+
+
+def test_tiny_prefill_special_scales_and_resid(torch, k3x):
+    """Scale bytes 255 (group zeroed) and a wide exponent range take the exact
+    dequantisation kernels; resid + MoE."""
+    say("case: tiny layer prefill, scale bytes 255 and 100..140, with residual")
+    L = synth.tiny(seed=12, scale_lo=100, scale_hi=140)
+    for e in range(L.E):
+        d = L.expert(e)
+        d["s1"][0, 1] = 255
+        d["s3"][5, 0] = 255
+        d["s2"][7, 2] = 255
+    layer = bank_layer(k3x, L)
+    x = L.x(40, bf16=False)
+    r = L.x(40, bf16=False, stream_sub=77)
+    o, idx, _, _ = L.oracle_moe(x)
+    out, i2, _ = dev_forward(torch, k3x, layer, x, resid=r)
+    assert np.array_equal(i2, idx)
+    err = synth.rel_l2(out, o + r)
+    say(f"  rel_l2={err:.3e}")
+    assert err < TOL
+    layer.close()
+
+
+def test_tiny_prefill_grouping_invariant(torch, k3x):
+    """Prefill of 64 tokens equals the decode path over the same tokens 8 at a time."""
+    say("case: tiny layer, prefill T=64 vs decode in groups of 8")
+    L = synth.tiny(seed=13)
+    layer = bank_layer(k3x, L)
+    x = L.x(64, bf16=False, stream_sub=3)
+    out, idx, wt = dev_forward(torch, k3x, layer, x)
+    o2, i2, w2 = decode_forward(torch, k3x, layer, x, False)
+    assert np.array_equal(idx, i2)
+    np.testing.assert_allclose(wt, w2, rtol=1e-6)
+    err = synth.rel_l2(out, o2)
+    say(f"  rel_l2(prefill, decode)={err:.3e}")
+    assert err < 1e-5
+    layer.close()
+
+
+def test_full_prefill_2048_zipf(torch, k3x):
+    """The full-size layer, one 2048-token chunk of bf16 activations, Zipf-skewed bias."""
+    import oracle_lib as ol
+    say("case: full-size prefill, 2048 bf16 tokens, Zipf bias (alpha 1.0, s 1.1)")
+    L = synth.full(seed=3, zipf_alpha=1.0)
+    layer = synth_layer(k3x, L)
+    T = 2048
+    x = L.x(T, bf16=True, stream_sub=5)
+    out, idx, wt = dev_forward(torch, k3x, layer, x, bf16=True)
+    counts = np.bincount(idx.ravel(), minlength=L.E)
+    say(f"  experts used {int((counts > 0).sum())}, tokens per expert max {counts.max()} "
+        f"median {int(np.median(counts))}")
+    # routing of every token against the oracle's router (the reference's arithmetic)
+    ri = np.empty((T, L.K), np.int32)
+    rw = np.empty((T, L.K), np.float32)
+    for t in range(T):
+        xt = np.ascontiguousarray(x[t])
+        ol.oracle().ko_router(ol.ptr(ri[t], ol.I32P), ol.ptr(rw[t], ol.F32P),
+                              ol.ptr(xt, ol.F32P), ol.ptr(L.gate, ol.F32P),
+                              ol.ptr(L.bias, ol.F32P), L.H, L.E, L.K, 1, 2.5)
+    assert np.array_equal(idx, ri)
+    np.testing.assert_allclose(wt, rw, rtol=1e-6)
+    say("  routing of all 2048 tokens equals the oracle's")
+    # every token against the decode path
+    o2, i2, _ = decode_forward(torch, k3x, layer, x, True)
+    assert np.array_equal(idx, i2)
+    err = synth.rel_l2(out, o2)
+    say(f"  rel_l2(prefill, decode) over 2048 tokens = {err:.3e}")
+    assert err < 1e-5
+    # a sample of tokens against the whole oracle layer
+    sample = [0, 1, 777, 2047]
+    o, oi, _, _ = L.oracle_moe(x[sample])
+    assert np.array_equal(idx[sample], oi)
+    err = synth.rel_l2(out[sample], o)
+    say(f"  rel_l2(prefill, oracle) on tokens {sample} = {err:.3e}")
+    assert err < TOL
+    layer.close()

@@ -80,6 +80,9 @@ typedef struct k3x_prefill_buf {
     int      *offsets;      /* [E+1] first permuted row of each expert               */
     int      *cursor;       /* [E]                                                   */
     int      *tb_gu, *tb_dn;  /* [E+1] first GEMM tile of each expert               */
+    void     *desc_gu, *desc_dn;   /* per GEMM tile {expert, row block, row, rows}      */
+    int       ndesc_gu, ndesc_dn;  /* entries of each table                            */
+    uint16_t *xp;           /* [2][H/8][T*K][8] gate/up activations, permuted rows    */
     int      *perm_tok;     /* [T*K] token of each permuted row                      */
     float    *perm_w;       /* [T*K] routing weight of each permuted row             */
     int      *pos_of;       /* [T*K] permuted row of each (token, slot)              */

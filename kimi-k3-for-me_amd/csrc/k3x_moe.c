@@ -300,12 +300,21 @@ int k3x_pf_reserve(k3x_moe_layer *L, int T)
         t * K * I * 4,             /* act     */
         (SI ? t * SI * 4 : 256),   /* act_sh  */
         (t * K + t) * H * 4,       /* y       */
+        t * K * H * 4,             /* xp      */
+        0, 0,                      /* desc_gu, desc_dn (set below) */
     };
     enum { N = sizeof sz / sizeof sz[0] };
+    /* GEMM tiles: at most ceil(rows/64) row blocks by (T*K/16 + E + 1) column blocks */
+    const int ndg = (int)(((I + 63) / 64) * (t * K / 16 + E + 1));
+    const int ndd = (int)(((H + 63) / 64) * (t * K / 16 + E + 1));
+    size_t szs[N];
+    for (int i = 0; i < N; i++) szs[i] = sz[i];
+    szs[N - 2] = (size_t)ndg * 16;
+    szs[N - 1] = (size_t)ndd * 16;
     size_t off[N], total = 0;
     for (int i = 0; i < N; i++) {
         off[i] = total;
-        total += (sz[i] + 255) & ~(size_t)255;
+        total += (szs[i] + 255) & ~(size_t)255;
     }
     void *base = NULL;
     if (hipSetDevice(L->device) != hipSuccess) return K3X_E_HIP;
@@ -326,6 +335,9 @@ int k3x_pf_reserve(k3x_moe_layer *L, int T)
     B->pos_of = (int *)(p + off[12]);
     B->act = (uint16_t *)(p + off[13]); B->act_sh = (uint16_t *)(p + off[14]);
     B->y = (float *)(p + off[15]);
+    B->xp = (uint16_t *)(p + off[16]);
+    B->desc_gu = p + off[17]; B->ndesc_gu = ndg;
+    B->desc_dn = p + off[18]; B->ndesc_dn = ndd;
     return 0;
 }
 

@@ -25,17 +25,21 @@
 #define PF_CHUNK 4096          // tokens per pipeline run
 
 // ------------------------------------------------------------------ split
-// x [T][H] (bf16 or fp32) -> xhl [T][H/8][2][8] bf16: per 8 elements the hi halves, then
-// the lo halves.  Block 0 also clears the expert histogram.
+// Activation planes, the GEMMs' B source: x [T][H] (bf16 or fp32) -> xg [2][H/8][T][8]
+// bf16, plane 0 the hi parts, plane 1 the lo parts, each k-group of 8 elements
+// token-major, so that one k-group of consecutive rows is contiguous.  Block 0 also
+// clears the expert histogram.
 __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int T, int H,
-                                                  uint16_t *xhl, int *counts, int E)
+                                                  uint16_t *xg, int *counts, int E)
 {
     if (blockIdx.x == 0)
         for (int e = threadIdx.x; e < E; e += PF_NT) counts[e] = 0;
-    const size_t g = (size_t)blockIdx.x * PF_NT + threadIdx.x;
-    if (g >= (size_t)T * (H >> 3)) return;
+    const size_t i = (size_t)blockIdx.x * PF_NT + threadIdx.x;     // (t, group) pairs
+    const int G8 = H >> 3;
+    if (i >= (size_t)T * G8) return;
+    const int t = (int)(i / G8), gi = (int)(i % G8);
     float v[8];
-    load_x8(x, x_bf16, g * 8, v);
+    load_x8(x, x_bf16, i * 8, v);
     uint32_t hi[8], lo[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) split_bf16(v[j], hi[j], lo[j]);
@@ -45,18 +49,19 @@ __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int
         h[j] = hi[2 * j] | (hi[2 * j + 1] << 16);
         l[j] = lo[2 * j] | (lo[2 * j + 1] << 16);
     }
-    *(u32x4 *)(xhl + g * 16) = h;
-    *(u32x4 *)(xhl + g * 16 + 8) = l;
+    *(u32x4 *)(xg + ((size_t)gi * T + t) * 8) = h;
+    *(u32x4 *)(xg + ((size_t)(G8 + gi) * T + t) * 8) = l;
 }
 
 // ------------------------------------------------------------------ router
-// Logits of a 64-token x 32-expert tile; each thread owns 4 tokens x 2 experts and runs
-// their chains in double over i = 0 .. H-1 in order (a product of two floats is exact in
-// double, so the chain equals the reference's fma-free loop).  K is staged 32 at a time
-// in LDS as double.
-#define RT_TOK 64
-#define RT_EXP 32
-#define RT_KC  32
+// Logits of a 32-token x 64-expert tile; thread (ty, tx) owns tokens 2ty, 2ty+1 and
+// experts 4tx .. 4tx+3 and runs their eight chains in double over i = 0 .. H-1 in order
+// (a product of two floats is exact in double, so each chain equals the reference's
+// fma-free loop).  K is staged 64 at a time: activations as double, weights as float
+// (widened at use); the next chunk is fetched into registers during the current one.
+#define RT_TOK 32
+#define RT_EXP 64
+#define RT_KC  64
 
 struct PfRouterArgs {
     const void  *x;
@@ -66,51 +71,63 @@ struct PfRouterArgs {
     float       *score, *choice;
 };
 
+typedef __attribute__((__vector_size__(2 * sizeof(double)))) double f64x2;
+
 __global__ void __launch_bounds__(PF_NT) pf_router(PfRouterArgs a)
 {
-    __shared__ double xs[RT_KC][RT_TOK];
-    __shared__ double ws[RT_KC][RT_EXP];
+    __shared__ __attribute__((aligned(16))) double xs[RT_KC][RT_TOK];
+    __shared__ __attribute__((aligned(16))) float ws[RT_KC][RT_EXP];
     const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
     const int tok0 = blockIdx.x * RT_TOK, e0 = blockIdx.y * RT_EXP;
-    double acc[4][2];
+    double acc[2][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i][0] = acc[i][1] = 0.0;
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = 0.0;
+    // staging roles, so that a wave's LDS stores are contiguous: x: token tid%32, k from
+    // (tid/32)*8; W: expert tid%64, k from (tid/64)*16
+    const int xt = threadIdx.x % RT_TOK, xk = (threadIdx.x / RT_TOK) * 8;
+    const int we = threadIdx.x % RT_EXP, wk = (threadIdx.x / RT_EXP) * 16;
+    const bool xon = tok0 + xt < a.T, won = e0 + we < a.E;
+    const float *wrow = a.W + (size_t)(won ? e0 + we : 0) * a.H + wk;
+    const size_t xrow = (size_t)(xon ? tok0 + xt : 0) * a.H + xk;
+    float xv[8];
+    f32x4 wv[4];
+    auto fetch = [&](int k0) AI {
+        if (xon) load_x8(a.x, a.x_bf16, xrow + k0, xv);
+        else for (int j = 0; j < 8; j++) xv[j] = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            wv[c] = won ? *(const f32x4 *)(wrow + k0 + 4 * c) : (f32x4){0.f, 0.f, 0.f, 0.f};
+    };
+    fetch(0);
     for (int k0 = 0; k0 < a.H; k0 += RT_KC) {
-        // x tile: 64 tokens x 32 k, 8 per thread; W tile: 32 experts x 32 k, 4 per thread
-        for (int f = threadIdx.x; f < RT_TOK * RT_KC / 4; f += PF_NT) {
-            const int t = f / (RT_KC / 4), kk = (f % (RT_KC / 4)) * 4;
-            float v[4] = {0.f, 0.f, 0.f, 0.f};
-            if (tok0 + t < a.T) load_x4(a.x, a.x_bf16, (size_t)(tok0 + t) * a.H + k0 + kk, v);
-#pragma unroll
-            for (int j = 0; j < 4; j++) xs[kk + j][t] = (double)v[j];
-        }
-        for (int f = threadIdx.x; f < RT_EXP * RT_KC / 4; f += PF_NT) {
-            const int e = f / (RT_KC / 4), kk = (f % (RT_KC / 4)) * 4;
-            f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (e0 + e < a.E) v = *(const f32x4 *)(a.W + (size_t)(e0 + e) * a.H + k0 + kk);
-#pragma unroll
-            for (int j = 0; j < 4; j++) ws[kk + j][e] = (double)v[j];
-        }
         __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 8; j++) xs[xk + j][xt] = (double)xv[j];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) ws[wk + 4 * c + j][we] = wv[c][j];
+        __syncthreads();
+        if (k0 + RT_KC < a.H) fetch(k0 + RT_KC);
 #pragma unroll 8
         for (int k = 0; k < RT_KC; k++) {
-            double xv[4], wv[2];
+            const f64x2 x2 = *(const f64x2 *)&xs[k][2 * ty];
+            const f32x4 w4 = *(const f32x4 *)&ws[k][4 * tx];
 #pragma unroll
-            for (int i = 0; i < 4; i++) xv[i] = xs[k][ty + 16 * i];
-#pragma unroll
-            for (int j = 0; j < 2; j++) wv[j] = ws[k][tx + 16 * j];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++) acc[i][j] = __fma_rn(xv[i], wv[j], acc[i][j]);
+            for (int j = 0; j < 4; j++) {
+                const double wd = (double)w4[j];
+                acc[0][j] = __fma_rn(x2[0], wd, acc[0][j]);
+                acc[1][j] = __fma_rn(x2[1], wd, acc[1][j]);
+            }
         }
-        __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int t = tok0 + ty + 16 * i, e = e0 + tx + 16 * j;
+        for (int j = 0; j < 4; j++) {
+            const int t = tok0 + 2 * ty + i, e = e0 + 4 * tx + j;
             if (t < a.T && e < a.E) {
                 const float sc = sigmoid_ref((float)acc[i][j]);
                 a.score[(size_t)t * a.E + e] = sc;
@@ -155,28 +172,38 @@ __global__ void __launch_bounds__(PF_NT) pf_topk(PfTopkArgs a)
 }
 
 // ------------------------------------------------------------------ scan
-// One workgroup: offsets[e] = sum of counts below e; tile bases of the two routed GEMMs
-// (expert e gets nrb x ceil(count/tpb) tiles); cursors cleared.
+// One workgroup of 1024 threads (E <= 1024): offsets[e] = sum of counts below e; tile
+// bases of the two routed GEMMs (expert e gets nrb x ceil(count/tpb) tiles); cursors
+// cleared.  Three inclusive scans in LDS, one element per thread.
 __global__ void __launch_bounds__(1024) pf_scan(const int *counts, int E, int *offsets,
                                                 int *cursor, int *tb_gu, int tpb_gu, int nrb_gu,
                                                 int *tb_dn, int tpb_dn, int nrb_dn)
 {
-    __shared__ int s_c[1024];
-    for (int e = threadIdx.x; e < E; e += 1024) {
-        s_c[e] = counts[e];
-        cursor[e] = 0;
+    __shared__ int s[3][1024];
+    const int e = threadIdx.x;
+    const int c = e < E ? counts[e] : 0;
+    int v[3] = {c, nrb_gu * ((c + tpb_gu - 1) / tpb_gu), nrb_dn * ((c + tpb_dn - 1) / tpb_dn)};
+    if (e < E) cursor[e] = 0;
+    for (int d = 1; d < 1024; d <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 3; i++) s[i][e] = v[i];
+        __syncthreads();
+        if (e >= d)
+#pragma unroll
+            for (int i = 0; i < 3; i++) v[i] += s[i][e - d];
+        __syncthreads();
     }
+    // v = inclusive sums; the exclusive value of e is the inclusive value of e - 1
+#pragma unroll
+    for (int i = 0; i < 3; i++) s[i][e] = v[i];
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int o = 0, g = 0, d = 0;
-        for (int e = 0; e < E; e++) {
-            const int c = s_c[e];
-            offsets[e] = o; tb_gu[e] = g; tb_dn[e] = d;
-            o += c;
-            g += nrb_gu * ((c + tpb_gu - 1) / tpb_gu);
-            d += nrb_dn * ((c + tpb_dn - 1) / tpb_dn);
-        }
-        offsets[E] = o; tb_gu[E] = g; tb_dn[E] = d;
+    if (e < E) {
+        offsets[e] = e == 0 ? 0 : s[0][e - 1];
+        tb_gu[e] = e == 0 ? 0 : s[1][e - 1];
+        tb_dn[e] = e == 0 ? 0 : s[2][e - 1];
+    }
+    if (e == E - 1) {
+        offsets[E] = v[0]; tb_gu[E] = v[1]; tb_dn[E] = v[2];
     }
 }
 
@@ -194,31 +221,75 @@ __global__ void __launch_bounds__(PF_NT) pf_scatter(const int *idx, const float 
     pos_of[i] = p;
 }
 
+// ------------------------------------------------------------------ permute
+// The gate/up B source in permuted order: xp [HL][H/8][T*K][8] = xg rows perm_tok[p], so
+// that one k-group of an expert's segment is contiguous.
+__global__ void __launch_bounds__(PF_NT) pf_permute(const uint16_t *xg, int T, int G8, int HL,
+                                                    const int *perm_tok, int TK, uint16_t *xp)
+{
+    const size_t i = (size_t)blockIdx.x * PF_NT + threadIdx.x;    // ((hl*G8 + g)*TK + p)
+    if (i >= (size_t)HL * G8 * TK) return;
+    const int p = (int)(i % TK);
+    const size_t hg = i / TK;
+    *(u32x4 *)(xp + i * 8) = *(const u32x4 *)(xg + (hg * T + perm_tok[p]) * 8);
+}
+
+// ------------------------------------------------------------------ tile tables
+// One descriptor per GEMM tile: {group, row block, first permuted row, tokens}; expert e
+// owns tiles tb[e] .. tb[e+1)-1, row blocks outer, column blocks inner.
+__global__ void __launch_bounds__(PF_NT) pf_tiles(const int *counts, const int *offsets,
+                                                  const int *tb_gu, int tpb_gu, int nrb_gu,
+                                                  int4 *desc_gu, const int *tb_dn, int tpb_dn,
+                                                  int nrb_dn, int4 *desc_dn)
+{
+    const int e = blockIdx.x, c = counts[e], off = offsets[e];
+    for (int pass = 0; pass < 2; pass++) {
+        const int tpb = pass ? tpb_dn : tpb_gu, nrb = pass ? nrb_dn : nrb_gu;
+        int4 *desc = (pass ? desc_dn : desc_gu) + (pass ? tb_dn[e] : tb_gu[e]);
+        const int nc = (c + tpb - 1) / tpb;
+        for (int rel = threadIdx.x; rel < nrb * nc; rel += PF_NT) {
+            const int rb = rel / nc, cb = rel % nc;
+            desc[rel] = make_int4(e, rb, off + cb * tpb, min(tpb, c - cb * tpb));
+        }
+    }
+}
+
 // ------------------------------------------------------------------ grouped GEMM
 // Y[p][r] = sum_k W_g[r][k] B[p][k] over the permuted rows p of group g (an expert's
 // segment, or all tokens for the shared expert).  A workgroup computes a tile of
 // NW*RT*16 weight rows (NMAT matrices: gate and up together) by one column block of
 // CT*16 B columns (TPB tokens; HL columns per token: hi, or hi and lo); its four waves
-// own RT row tiles each and share the column block, staged in LDS one 128-wide quad at
-// a time (double buffered).  Each thread keeps three quads of loads in flight (weights
-// for its row tiles, its share of the next B quads), issued in quad order so that one
-// wait per quad, before the LDS store of the next B quad, releases exactly one quad.
+// own RT row tiles each and share the column block.
+//
+// K advances one 128-wide quad per step through a ring of RING slots: a slot holds the
+// quad's weights for this wave's tiles (registers, range-checked buffer loads) and the
+// quad's B block (LDS, filled by buffer loads straight to LDS: lane i of a load writes
+// 16 bytes at the load's LDS base + 16 i; rows past the block's tokens read out of range
+// and land as zeros).  Each step waits for its own slot's loads, meets the other waves
+// at one barrier (after which every wave's share of the B block is in LDS and the slot
+// used by the previous step is free), refills that slot RING-1 quads ahead and runs the
+// quad's MFMAs.
+//
+// B sources are activation planes [2][K/8][rows][8] bf16 (hi, lo; each k-group
+// row-major over rows), so the 16-byte pieces of one k-group over consecutive rows are
+// contiguous.
 struct PfGemmArgs {
     const uint8_t  *wm[2];      // group 0's matrices (gate, up) or (down), tiled
     size_t          gstride;    // bytes between groups' records
     int             R, K;       // rows and inner dimension of each matrix
     int             G;          // groups
-    const int      *gcount;     // [G] rows per group, or NULL: n0 rows in group 0
-    const int      *goff;       // [G] first permuted row of each group
-    const int      *tbase;      // [G+1] first tile of each group
+    const int4     *desc;       // per tile {group, row block, first row, rows}, or NULL:
+                                // one group of n0 rows
+    const int      *tbase;      // [G+1] first tile of each group (tbase[G] = tiles)
     int             n0;
-    const uint16_t *bsrc;       // B source rows [*][K/8][2][8] bf16
-    uint32_t        bsrc_bytes;
-    const int      *perm;       // B source row of permuted row p, or NULL: row_base + p
+    const uint16_t *bsrc;       // B planes [2][K/8][brows][8] bf16
+    int             brows;      // rows of each B plane
+    const int      *perm;       // B row of permuted row p, or NULL: row_base + p
     int             row_base;
     const float    *pw;         // weight of permuted row p (gate/up epilogue), or NULL: 1
-    uint16_t       *act;        // gate/up: output rows [*][R/8][2][8] bf16 hi/lo
-    float          *y;          // down: output rows [*][R] fp32
+    uint16_t       *act;        // gate/up output planes [2][R/8][arows][8] bf16
+    int             arows;
+    float          *y;          // down output rows [*][R] fp32
     int             out_base;   // output row = out_base + p
 };
 
@@ -236,6 +307,25 @@ struct AQuad<false, NMAT, RT> {             // bf16: 4 x 16 bytes per tile
     u32x4 c[NMAT][RT][4];
 };
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (expcnt left at its maximum), gfx9 encoding
+#define WAIT_VMCNT_LGKM0(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4))
+
+// Meet the other waves once this wave's loads of a quad are in (N = vector loads issued
+// after the quad's; exact, since the wait is what makes LDS data written by loads safe to
+// read) and its LDS reads of the previous quad are done.  A bare s_barrier:
+// __syncthreads' release fence would wait for every load in flight; the empty asm keeps
+// the compiler from moving LDS accesses across it.
+template <int N>
+__device__ __forceinline__ void meet()
+{
+    WAIT_VMCNT_LGKM0(N);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <bool FP4, bool EXACT, int NMAT, int RT, int CT, int HL, bool GU>
 __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
 {
@@ -244,31 +334,31 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
     constexpr int TPB = NCOL / HL;
     constexpr int RPB = NW * RT * 16;
     constexpr int QB = NCOL * 128 * 2;             // B bytes per quad
-    constexpr int NST = QB / (PF_NT * 16);         // B pieces per thread per quad
-    constexpr int RING = 3;
-    static_assert(NST * PF_NT * 16 == QB, "B quad must split evenly");
-    __shared__ __attribute__((aligned(16))) uint8_t sB[2 * QB];
+    constexpr int NJ = QB / (PF_NT * 16);          // LDS loads per wave per quad
+    constexpr int RING = 4;
+    constexpr int LPI = NMAT * RT * (FP4 ? 2 : 4) + NJ;   // vector loads per slot per wave
+    static_assert(NJ * PF_NT * 16 == QB, "B quad must split evenly");
+    static_assert((RING - 2) * LPI < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) uint8_t sB[RING * QB];
 
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int nrb = (a.R + RPB - 1) / RPB;
     // ---- which tile
-    int g = 0, cnt = a.n0, off = 0, t0 = 0;
+    int g = 0, rb, ntok, p0;
     const int tile = blockIdx.x;
-    if (a.gcount) {
-        if (tile >= a.tbase[a.G]) return;
-        int lo = 0, hi = a.G - 1;                  // the last group whose first tile <= tile
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (a.tbase[mid] <= tile) lo = mid; else hi = mid - 1;
-        }
-        g = lo; cnt = a.gcount[g]; off = a.goff[g]; t0 = a.tbase[g];
-    } else if (tile >= nrb * ((cnt + TPB - 1) / TPB)) {
-        return;
+    if (a.desc) {
+        const int ntiles = a.tbase[a.G];
+        const int4 d = a.desc[tile];
+        if (tile >= ntiles) return;
+        g = d.x; rb = d.y; p0 = d.z; ntok = d.w;
+    } else {
+        const int nc = (a.n0 + TPB - 1) / TPB;
+        if (tile >= nrb * nc) return;
+        rb = tile / nc;
+        const int cb = tile % nc;
+        p0 = cb * TPB;
+        ntok = min(TPB, a.n0 - p0);
     }
-    const int nc = (cnt + TPB - 1) / TPB;
-    const int rel = tile - t0, rb = rel / nc, cb = rel % nc;
-    const int ntok = min(TPB, cnt - cb * TPB);
-    const int p0 = off + cb * TPB;
     const int nQ = a.K >> 7;
 
     // ---- this wave's weight tiles
@@ -284,25 +374,26 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
             ra[m][i] = make_rsrc(a.wm[m] + (size_t)g * a.gstride + (size_t)rt * tbytes,
                                  rvalid[i] ? tbytes : 0u);
     }
-    // ---- this thread's B pieces: piece f = (n*16 + g8)*HL + hl of each quad
-    const rsrc_t rb_src = make_rsrc(a.bsrc, a.bsrc_bytes);
-    uint32_t soff[NST], doff[NST];
+    // ---- this lane's B pieces: entry e = (wave*NJ + j)*64 + lane of each quad's block,
+    // e = (t*4 + kq)*NCOL + col, col = tok*HL + hl; k-group g8 = kq*4 + t of the quad
+    const int G8 = a.K >> 3;
+    const rsrc_t rbs = make_rsrc(a.bsrc, (uint32_t)((size_t)2 * G8 * a.brows * 16));
+    const uint32_t qstep = (uint32_t)a.brows * 256u;               // 16 k-groups
+    uint32_t boff[NJ];
 #pragma unroll
-    for (int s = 0; s < NST; s++) {
-        const int f = threadIdx.x + PF_NT * s;
-        const int n = f / (16 * HL), r2 = f % (16 * HL), g8 = r2 / HL, hl = r2 % HL;
-        const int kq = g8 >> 2, t = g8 & 3;
-        doff[s] = (uint32_t)(((t * 4 + kq) * NCOL + n * HL + hl) * 16);
-        if (n < ntok) {
-            const int row = a.perm ? a.perm[p0 + n] : a.row_base + p0 + n;
-            soff[s] = (uint32_t)row * (uint32_t)(a.K * 4) + (uint32_t)(g8 * 32 + hl * 16);
+    for (int j = 0; j < NJ; j++) {
+        const int e = (wave * NJ + j) * WAVE + lane;
+        const int tk = e / NCOL, col = e % NCOL;
+        const int t = tk >> 2, kq = tk & 3, tok = col / HL, hl = col % HL;
+        if (tok < ntok) {
+            const int row = a.perm ? a.perm[p0 + tok] : a.row_base + p0 + tok;
+            boff[j] = ((uint32_t)(hl * G8 + kq * 4 + t) * (uint32_t)a.brows + (uint32_t)row) * 16u;
         } else {
-            soff[s] = K3X_OOB;
+            boff[j] = K3X_OOB;
         }
     }
 
     AQuad<FP4, NMAT, RT> A[RING];
-    u32x4 Bq[RING][NST];
     auto ld = [&](int slot, int q) AI {
         const bool on = q < nQ;
 #pragma unroll
@@ -321,13 +412,14 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
                     for (int t = 0; t < 4; t++) A[slot].c[m][i][t] = wld16(ra[m][i], o + 1024u * t);
                 }
             }
+        // no select here: an out-of-range base stays out of range (bases < 2^30, steps
+        // < 2^30), and a quad past the end loads bytes that are never used
 #pragma unroll
-        for (int s = 0; s < NST; s++)
-            Bq[slot][s] = bload16(rb_src, on && soff[s] != K3X_OOB ? soff[s] + (uint32_t)q * 512u : K3X_OOB);
-    };
-    auto stage = [&](int slot, int buf) AI {
-#pragma unroll
-        for (int s = 0; s < NST; s++) *(u32x4 *)(sB + buf * QB + doff[s]) = Bq[slot][s];
+        for (int j = 0; j < NJ; j++) {
+            const uint32_t o = boff[j] + (uint32_t)q * qstep;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rbs, (lds_void *)(sB + slot * QB + (wave * NJ + j) * 1024), 16, o, 0, 0, 0);
+        }
     };
 
     f32x4 acc[NMAT][RT][CT];
@@ -339,8 +431,8 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
             for (int c = 0; c < CT; c++) acc[m][i][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     const int n16 = lane & 15, kq = lane >> 4;
-    auto compute = [&](int slot, int q, int buf) AI {
-        const uint8_t *bb = sB + buf * QB;
+    auto compute = [&](int slot, int q) AI {
+        const uint8_t *bb = sB + slot * QB;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             bf16x8 bf[CT];
@@ -366,35 +458,34 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
     };
 
 #pragma unroll
-    for (int s = 0; s < RING; s++) {
+    for (int s = 0; s < RING - 1; s++) {
         SCHED_FENCE();
         ld(s, s);
     }
     SCHED_FENCE();
-    stage(0, 0);
-    __syncthreads();
     int q = 0;
     for (; q + RING <= nQ; q += RING) {
 #pragma unroll
         for (int s = 0; s < RING; s++) {
-            compute(s, q + s, (q + s) & 1);
+            meet<(RING - 2) * LPI>();
             SCHED_FENCE();
-            ld(s, q + s + RING);
+            ld((s + RING - 1) % RING, q + s + RING - 1);
             SCHED_FENCE();
-            stage((s + 1) % RING, (q + s + 1) & 1);
-            __syncthreads();
+            compute(s, q + s);
         }
     }
-#pragma unroll
-    for (int s = 0; s < RING - 1; s++) {
-        if (q + s < nQ) {
-            compute(s, q + s, (q + s) & 1);
-            stage((s + 1) % RING, (q + s + 1) & 1);
-            __syncthreads();
-        }
-    }
+    // the last quads: their loads are all in flight already and nothing more is issued
+    // (a refill here would be dead, and the compiler drops the dead register loads, so
+    // the wait counts below count only what the loop and the prime issued)
+    static_assert(RING == 4, "tail written for a ring of 4");
+    if (q < nQ)     { meet<2 * LPI>(); compute(0, q); }
+    if (q + 1 < nQ) { meet<LPI>();     compute(1, q + 1); }
+    if (q + 2 < nQ) { meet<0>();       compute(2, q + 2); }
+    // no load to LDS may still be landing when the workgroup ends
+    WAIT_VMCNT_LGKM0(0);
 
     // ---- epilogue: lane (n16, kq) holds rows 4*kq .. 4*kq+3 of each row tile, column n16
+    const int G8o = a.R >> 3;
 #pragma unroll
     for (int c = 0; c < CT; c++) {
         const int col = c * 16 + n16;
@@ -423,10 +514,10 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
                     const float yv = (w == 0.0f) ? 0.0f : w * swiglu(v0[j], v1[j]);
                     split_bf16(yv, hi[j], lo[j]);
                 }
-                uint16_t *dst = a.act + (size_t)(a.out_base + p) * (size_t)(a.R * 2) +
-                                (size_t)(r0 >> 3) * 16 + (r0 & 7);
-                *(u32x2 *)dst = (u32x2){hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
-                *(u32x2 *)(dst + 8) = (u32x2){lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+                const size_t o = ((size_t)(r0 >> 3) * a.arows + (size_t)(a.out_base + p)) * 8 + (r0 & 7);
+                const size_t plane = (size_t)G8o * a.arows * 8;
+                *(u32x2 *)(a.act + o) = (u32x2){hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+                *(u32x2 *)(a.act + plane + o) = (u32x2){lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
             } else {
                 float *dst = a.y + (size_t)(a.out_base + p) * a.R + r0;
                 *(f32x4 *)dst = (f32x4){v0[0], v0[1], v0[2], v0[3]};
@@ -466,7 +557,7 @@ static void launch_topk(const PfTopkArgs &a, hipStream_t s)
 
 // gate/up and down launch shapes of the routed GEMMs
 #define GU_RT 2
-#define GU_CT 4
+#define GU_CT 2
 #define DN_RT 4
 #define DN_CT 4
 
@@ -516,17 +607,25 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     hipLaunchKernelGGL(pf_scatter, dim3(cdiv(TK, PF_NT)), dim3(PF_NT), 0, s, B->idx, B->wt, TK, K,
                        B->offsets, B->cursor, B->perm_tok, B->perm_w, B->pos_of);
     if ((rc = launch_ok())) return rc;
+    hipLaunchKernelGGL(pf_tiles, dim3(E), dim3(PF_NT), 0, s, B->counts, B->offsets, B->tb_gu,
+                       tpb_gu, nrb_gu, (int4 *)B->desc_gu, B->tb_dn, tpb_dn, nrb_dn,
+                       (int4 *)B->desc_dn);
+    if ((rc = launch_ok())) return rc;
+    hipLaunchKernelGGL(pf_permute, dim3(cdiv((size_t)HLg * (H / 8) * TK, PF_NT)), dim3(PF_NT), 0, s,
+                       B->xhl, T, H / 8, HLg, B->perm_tok, TK, B->xp);
+    if ((rc = launch_ok())) return rc;
 
-    const size_t act_row = (size_t)I * 4, ash_row = (size_t)SI * 4;   // bytes per hi/lo row
     // routed gate/up: B rows are tokens of xhl through perm_tok
     PfGemmArgs g;
     memset(&g, 0, sizeof g);
     g.wm[0] = L->experts + L->gate_off; g.wm[1] = L->experts + L->up_off;
     g.gstride = L->expert_bytes;
-    g.R = I; g.K = H; g.G = E; g.gcount = B->counts; g.goff = B->offsets; g.tbase = B->tb_gu;
-    g.bsrc = B->xhl; g.bsrc_bytes = (uint32_t)((size_t)T * H * 4); g.perm = B->perm_tok;
-    g.pw = B->perm_w; g.act = B->act; g.out_base = 0;
+    g.R = I; g.K = H; g.G = E; g.desc = (const int4 *)B->desc_gu; g.tbase = B->tb_gu;
+    g.bsrc = B->xp; g.brows = TK; g.perm = NULL; g.row_base = 0;
+    g.pw = B->perm_w; g.act = B->act; g.arows = TK; g.out_base = 0;
     const unsigned grid_gu = nrb_gu * (cdiv(TK, tpb_gu) + (unsigned)(E < TK ? E : TK));
+    const unsigned grid_dn = nrb_dn * (cdiv(TK, tpb_dn) + (unsigned)(E < TK ? E : TK));
+    if (grid_gu > (unsigned)B->ndesc_gu || grid_dn > (unsigned)B->ndesc_dn) return K3X_E_SHAPE;
     const bool ex_gu = (L->special & 3) != 0;
     if (ex_gu) { if (HLg == 1) launch_gu_fp4<true, 1>(g, grid_gu, s); else launch_gu_fp4<true, 2>(g, grid_gu, s); }
     else       { if (HLg == 1) launch_gu_fp4<false, 1>(g, grid_gu, s); else launch_gu_fp4<false, 2>(g, grid_gu, s); }
@@ -536,10 +635,9 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     PfGemmArgs d;
     memset(&d, 0, sizeof d);
     d.wm[0] = L->experts + L->down_off; d.gstride = L->expert_bytes;
-    d.R = H; d.K = I; d.G = E; d.gcount = B->counts; d.goff = B->offsets; d.tbase = B->tb_dn;
-    d.bsrc = B->act; d.bsrc_bytes = (uint32_t)(TK * act_row); d.perm = NULL; d.row_base = 0;
+    d.R = H; d.K = I; d.G = E; d.desc = (const int4 *)B->desc_dn; d.tbase = B->tb_dn;
+    d.bsrc = B->act; d.brows = TK; d.perm = NULL; d.row_base = 0;
     d.y = B->y; d.out_base = 0;
-    const unsigned grid_dn = nrb_dn * (cdiv(TK, tpb_dn) + (unsigned)(E < TK ? E : TK));
     if (L->special & 4)
         hipLaunchKernelGGL((pf_gemm<true, true, 1, DN_RT, DN_CT, 2, false>), dim3(grid_dn), dim3(PF_NT), 0, s, d);
     else
@@ -554,8 +652,8 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
         memset(&sg, 0, sizeof sg);
         sg.wm[0] = (const uint8_t *)L->sh_gate; sg.wm[1] = (const uint8_t *)L->sh_up;
         sg.R = SI; sg.K = H; sg.G = 1; sg.n0 = T;
-        sg.bsrc = B->xhl; sg.bsrc_bytes = (uint32_t)((size_t)T * H * 4); sg.row_base = 0;
-        sg.act = B->act_sh; sg.out_base = 0;
+        sg.bsrc = B->xhl; sg.brows = T; sg.row_base = 0;
+        sg.act = B->act_sh; sg.arows = T; sg.out_base = 0;
         const int tpb_sg = 4 * 16 / HLg, nrb_sg = cdiv(SI, (PF_NT / WAVE) * 1 * 16);
         const unsigned grid_sg = nrb_sg * cdiv(T, tpb_sg);
         if (HLg == 1)
@@ -566,7 +664,7 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
         PfGemmArgs sd;
         memset(&sd, 0, sizeof sd);
         sd.wm[0] = (const uint8_t *)L->sh_down; sd.R = H; sd.K = SI; sd.G = 1; sd.n0 = T;
-        sd.bsrc = B->act_sh; sd.bsrc_bytes = (uint32_t)(T * ash_row); sd.row_base = 0;
+        sd.bsrc = B->act_sh; sd.brows = T; sd.row_base = 0;
         sd.y = B->y; sd.out_base = TK;
         const int nrb_sd = cdiv(H, (PF_NT / WAVE) * 2 * 16);
         const unsigned grid_sd = nrb_sd * cdiv(T, 32);
@@ -587,10 +685,14 @@ extern "C" int k3x_dev_prefill(k3x_moe_layer *L, float *out, const void *x, int 
 {
     const int H = L->cfg.hidden, K = L->cfg.topk;
     const size_t es = (x_dtype == K3X_BF16) ? 2 : 4;
-    int rc = k3x_pf_reserve(L, T < PF_CHUNK ? T : PF_CHUNK);
+    // activation planes of one chunk stay under 1 GiB, so 32-bit buffer offsets hold
+    const size_t wide = (size_t)(H > L->cfg.moe_inter ? H : L->cfg.moe_inter);
+    int chunk = (int)(((size_t)1 << 30) / ((size_t)K * wide * 4));
+    chunk = chunk < 1 ? 1 : (chunk > PF_CHUNK ? PF_CHUNK : chunk);
+    int rc = k3x_pf_reserve(L, T < chunk ? T : chunk);
     if (rc) return rc;
-    for (int t0 = 0; t0 < T; t0 += PF_CHUNK) {
-        const int n = T - t0 < PF_CHUNK ? T - t0 : PF_CHUNK;
+    for (int t0 = 0; t0 < T; t0 += chunk) {
+        const int n = T - t0 < chunk ? T - t0 : chunk;
         rc = pf_chunk(L, out + (size_t)t0 * H, (const char *)x + (size_t)t0 * H * es, x_dtype, n,
                       resid ? resid + (size_t)t0 * H : NULL, idx ? idx + (size_t)t0 * K : NULL,
                       wt ? wt + (size_t)t0 * K : NULL, (hipStream_t)stream);

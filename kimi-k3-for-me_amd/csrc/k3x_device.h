@@ -95,6 +95,16 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c)
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+
+// 32x32x16: A lane l = row l%32, k-slots 8*(l/32) .. +7; B lane l = column l%32, same
+// k-slots; D lane l holds column l%32, rows 8a + 4*(l/32) + b in element 4a + b.  Twice
+// the 16x16x32 form's throughput on gfx950 for the same operand registers.
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
 
 // Weights are streamed once per call: non-temporal loads keep them from displacing

@@ -526,6 +526,225 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
     }
 }
 
+// ------------------------------------------------------------------ grouped GEMM, 32x32
+// The routed GEMMs (MXFP4 weights) on v_mfma_f32_32x32x16_bf16.  Same tiling, ring and
+// barrier protocol as pf_gemm; a wave owns RT32 row tiles of 32 rows (two 16-row tiles of
+// the fp4 layout) and the workgroup CT32 column tiles of 32 B columns.
+//
+// K order.  Within a quad, lane L (row R = L%32, h = L/32) loads two 16-byte scale
+// groups of row R: group kq = h (load 0) and kq = 2 + h (load 1).  Dword d of load g
+// feeds the MFMA of step (g, d) with k = 64g + 32h + 8d .. +7, so one 32x32x16 step
+// multiplies k-slots {64g + 8d .. +7} (lanes 0-31) and {64g + 32 + 8d .. +7} (lanes
+// 32-63).  The B block in LDS is laid out to match: entry ((g*4 + d)*2 + h)*NCOL + col
+// holds those 8 k of column col.  Every product of the quad is formed exactly once;
+// only the order of the fp32 additions differs from the 16x16 form.
+template <bool EXACT, int NMAT, int RT32, int CT32, int HL, bool GU>
+__global__ void __launch_bounds__(PF_NT, 2) pf_gemm32(PfGemmArgs a)
+{
+    constexpr int NW = PF_NT / WAVE;
+    constexpr int NCOL = CT32 * 32;
+    constexpr int TPB = NCOL / HL;
+    constexpr int RPB = NW * RT32 * 32;
+    constexpr int QB = NCOL * 128 * 2;
+    constexpr int NJ = QB / (PF_NT * 16);
+    constexpr int RING = 4;
+    constexpr int LPI = NMAT * RT32 * 4 + NJ;       // 2 code + 2 scale loads per 32 rows
+    static_assert(NJ * PF_NT * 16 == QB, "B quad must split evenly");
+    static_assert((RING - 2) * LPI < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) uint8_t sB[RING * QB];
+
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    const int nrb = (a.R + RPB - 1) / RPB;
+    int g = 0, rb, ntok, p0;
+    {
+        // Workgroups are dealt to the 8 XCDs round-robin; tiles are dealt to them in
+        // contiguous runs instead (XCD x takes tiles x*per .. x*per + per-1 in order), so
+        // the column blocks of one weight row block run back to back on one XCD and
+        // re-read the weights from its L2.  The grid is a multiple of 8.
+        const int ntiles = a.desc ? a.tbase[a.G] : nrb * ((a.n0 + TPB - 1) / TPB);
+        const int per = (ntiles + 7) >> 3;
+        const int k = blockIdx.x >> 3, tile = (blockIdx.x & 7) * per + k;
+        if (k >= per || tile >= ntiles) return;
+        if (a.desc) {
+            const int4 d = a.desc[tile];
+            g = d.x; rb = d.y; p0 = d.z; ntok = d.w;
+        } else {
+            const int nc = (a.n0 + TPB - 1) / TPB;
+            rb = tile / nc;
+            const int cb = tile % nc;
+            p0 = cb * TPB;
+            ntok = min(TPB, a.n0 - p0);
+        }
+    }
+    const int nQ = a.K >> 7;
+
+    // ---- weights: row tile pair i = 16-row tiles 2*tp, 2*tp+1 of this wave
+    const uint32_t tbytes = (uint32_t)fp4_tile_bytes(a.K);
+    const int R16 = a.R >> 4;
+    const int Rl = lane & 31, h = lane >> 5;
+    rsrc_t ra[NMAT][RT32];
+    int tp16[RT32];
+#pragma unroll
+    for (int i = 0; i < RT32; i++) {
+        const int t16 = ((rb * NW + wave) * RT32 + i) * 2;
+        tp16[i] = t16;
+        const int ntl = R16 - t16 < 0 ? 0 : (R16 - t16 > 2 ? 2 : R16 - t16);
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+            ra[m][i] = make_rsrc(a.wm[m] + (size_t)g * a.gstride + (size_t)t16 * tbytes,
+                                 (uint32_t)ntl * tbytes);
+    }
+    // this lane's offsets inside a pair: its 16-row tile, row, and group h (load 0)
+    const uint32_t lc = (uint32_t)(Rl >> 4) * tbytes + (uint32_t)((Rl & 15) + 16 * h) * 16u;
+    const uint32_t ls = (uint32_t)(Rl >> 4) * tbytes + 4096u + (uint32_t)((Rl & 15) + 16 * h) * 4u;
+
+    // ---- B pieces: entry e = (wave*NJ + j)*64 + lane; e = gdh*NCOL + col,
+    // gdh = (g*4 + d)*2 + h -> k-group 8g + 4h + d of the quad
+    const int G8 = a.K >> 3;
+    const rsrc_t rbs = make_rsrc(a.bsrc, (uint32_t)((size_t)2 * G8 * a.brows * 16));
+    const uint32_t qstep = (uint32_t)a.brows * 256u;
+    uint32_t boff[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int e = (wave * NJ + j) * WAVE + lane;
+        const int gdh = e / NCOL, col = e % NCOL;
+        const int gg = gdh >> 3, dd = (gdh >> 1) & 3, hh = gdh & 1;
+        const int tok = col / HL, hl = col % HL;
+        if (tok < ntok) {
+            const int row = a.perm ? a.perm[p0 + tok] : a.row_base + p0 + tok;
+            boff[j] = ((uint32_t)(hl * G8 + 8 * gg + 4 * hh + dd) * (uint32_t)a.brows + (uint32_t)row) * 16u;
+        } else {
+            boff[j] = K3X_OOB;
+        }
+    }
+
+    struct AQ {
+        u32x4    c[NMAT][RT32][2];
+        uint32_t s[NMAT][RT32][2];
+    };
+    AQ A[RING];
+    auto ld = [&](int slot, int q) AI {
+        const bool on = q < nQ;
+        const uint32_t qc = (uint32_t)(q >> 2) * 4352u + (uint32_t)(q & 3) * 1024u;
+        const uint32_t qs = (uint32_t)(q >> 2) * 4352u;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int i = 0; i < RT32; i++)
+#pragma unroll
+                for (int gl = 0; gl < 2; gl++) {
+                    A[slot].c[m][i][gl] = wld16(ra[m][i], on ? lc + qc + 512u * gl : K3X_OOB);
+                    A[slot].s[m][i][gl] = wld4(ra[m][i], on ? ls + qs + 128u * gl : K3X_OOB);
+                }
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const uint32_t o = boff[j] + (uint32_t)q * qstep;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rbs, (lds_void *)(sB + slot * QB + (wave * NJ + j) * 1024), 16, o, 0, 0, 0);
+        }
+    };
+
+    f32x16 acc[NMAT][RT32][CT32];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int i = 0; i < RT32; i++)
+#pragma unroll
+            for (int c = 0; c < CT32; c++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[m][i][c][v] = 0.f;
+
+    auto compute = [&](int slot, int q) AI {
+        const uint8_t *bb = sB + slot * QB;
+        const int sh = 8 * (q & 3);
+#pragma unroll
+        for (int gl = 0; gl < 2; gl++)
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                bf16x8 bf[CT32];
+#pragma unroll
+                for (int c = 0; c < CT32; c++)
+                    bf[c] = as_bf16x8(*(const u32x4 *)(bb + (((gl * 4 + d) * 2 + h) * NCOL + c * 32 + Rl) * 16));
+#pragma unroll
+                for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                    for (int i = 0; i < RT32; i++) {
+                        const uint32_t sb = (A[slot].s[m][i][gl] >> sh) & 255u;
+                        const bf16x8 av = EXACT ? dq8_exact(A[slot].c[m][i][gl][d], sb)
+                                                : dq8(A[slot].c[m][i][gl][d], e8m0_scale(sb));
+#pragma unroll
+                        for (int c = 0; c < CT32; c++) acc[m][i][c] = mfma32(av, bf[c], acc[m][i][c]);
+                    }
+            }
+    };
+
+#pragma unroll
+    for (int s = 0; s < RING - 1; s++) {
+        SCHED_FENCE();
+        ld(s, s);
+    }
+    SCHED_FENCE();
+    int q = 0;
+    for (; q + RING <= nQ; q += RING) {
+#pragma unroll
+        for (int s = 0; s < RING; s++) {
+            meet<(RING - 2) * LPI>();
+            SCHED_FENCE();
+            ld((s + RING - 1) % RING, q + s + RING - 1);
+            SCHED_FENCE();
+            compute(s, q + s);
+        }
+    }
+    static_assert(RING == 4, "tail written for a ring of 4");
+    if (q < nQ)     { meet<2 * LPI>(); compute(0, q); }
+    if (q + 1 < nQ) { meet<LPI>();     compute(1, q + 1); }
+    if (q + 2 < nQ) { meet<0>();       compute(2, q + 2); }
+    WAIT_VMCNT_LGKM0(0);
+
+    // ---- epilogue: lane holds column Rl of each column tile, rows 8a + 4h + b
+    const int G8o = a.R >> 3;
+#pragma unroll
+    for (int c = 0; c < CT32; c++) {
+        const int col = c * 32 + Rl;
+        const int tl = col / HL;
+        const bool writer = (HL == 1 || (col & 1) == 0) && tl < ntok;
+        const int p = p0 + tl;
+#pragma unroll
+        for (int i = 0; i < RT32; i++)
+#pragma unroll
+            for (int aa = 0; aa < 4; aa++) {
+                const int r0 = tp16[i] * 16 + 8 * aa + 4 * h;
+                float v0[4], v1[4];
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    v0[b] = acc[0][i][c][4 * aa + b];
+                    if (HL == 2) v0[b] += __shfl_xor(v0[b], 1);
+                    if (NMAT == 2) {
+                        v1[b] = acc[NMAT - 1][i][c][4 * aa + b];
+                        if (HL == 2) v1[b] += __shfl_xor(v1[b], 1);
+                    }
+                }
+                if (!writer || r0 >= a.R) continue;
+                if (GU) {
+                    const float w = a.pw ? a.pw[p] : 1.0f;
+                    uint32_t hi[4], lo[4];
+#pragma unroll
+                    for (int b = 0; b < 4; b++) {
+                        const float yv = (w == 0.0f) ? 0.0f : w * swiglu(v0[b], v1[b]);
+                        split_bf16(yv, hi[b], lo[b]);
+                    }
+                    const size_t o = ((size_t)(r0 >> 3) * a.arows + (size_t)(a.out_base + p)) * 8 + (r0 & 7);
+                    const size_t plane = (size_t)G8o * a.arows * 8;
+                    *(u32x2 *)(a.act + o) = (u32x2){hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+                    *(u32x2 *)(a.act + plane + o) = (u32x2){lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+                } else {
+                    float *dst = a.y + (size_t)(a.out_base + p) * a.R + r0;
+                    *(f32x4 *)dst = (f32x4){v0[0], v0[1], v0[2], v0[3]};
+                }
+            }
+    }
+}
+
 // ------------------------------------------------------------------ combine
 // out[t] = ((y[pos(t,0)] + y[pos(t,1)]) + ... ) + y_shared[t], then + resid.
 __global__ void __launch_bounds__(PF_NT) pf_combine(const float *y, const int *pos_of, int T, int K,
@@ -555,16 +774,17 @@ static void launch_topk(const PfTopkArgs &a, hipStream_t s)
     hipLaunchKernelGGL(pf_topk<NE>, dim3(cdiv(a.T, PF_NT / WAVE)), dim3(PF_NT), 0, s, a);
 }
 
-// gate/up and down launch shapes of the routed GEMMs
-#define GU_RT 2
-#define GU_CT 2
-#define DN_RT 4
-#define DN_CT 4
+// gate/up and down launch shapes of the routed GEMMs (pf_gemm32): 32-row tiles per
+// wave, 32-column tiles per workgroup
+#define GU_RT32 1
+#define GU_CT32 1
+#define DN_RT32 2
+#define DN_CT32 2
 
 template <bool EXACT, int HL>
-static void launch_gu_fp4(const PfGemmArgs &a, unsigned grid, hipStream_t s)
+static void launch_gu(const PfGemmArgs &a, unsigned grid, hipStream_t s)
 {
-    hipLaunchKernelGGL((pf_gemm<true, EXACT, 2, GU_RT, GU_CT, HL, true>), dim3(grid), dim3(PF_NT), 0, s, a);
+    hipLaunchKernelGGL((pf_gemm32<EXACT, 2, GU_RT32, GU_CT32, HL, true>), dim3(grid), dim3(PF_NT), 0, s, a);
 }
 
 static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
@@ -599,8 +819,8 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     else               launch_topk<16>(at, s);
     if ((rc = launch_ok())) return rc;
 
-    const int tpb_gu = GU_CT * 16 / HLg, nrb_gu = cdiv(I, (PF_NT / WAVE) * GU_RT * 16);
-    const int tpb_dn = DN_CT * 16 / 2, nrb_dn = cdiv(H, (PF_NT / WAVE) * DN_RT * 16);
+    const int tpb_gu = GU_CT32 * 32 / HLg, nrb_gu = cdiv(I, (PF_NT / WAVE) * GU_RT32 * 32);
+    const int tpb_dn = DN_CT32 * 32 / 2, nrb_dn = cdiv(H, (PF_NT / WAVE) * DN_RT32 * 32);
     hipLaunchKernelGGL(pf_scan, dim3(1), dim3(1024), 0, s, B->counts, E, B->offsets, B->cursor,
                        B->tb_gu, tpb_gu, nrb_gu, B->tb_dn, tpb_dn, nrb_dn);
     if ((rc = launch_ok())) return rc;
@@ -623,12 +843,12 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     g.R = I; g.K = H; g.G = E; g.desc = (const int4 *)B->desc_gu; g.tbase = B->tb_gu;
     g.bsrc = B->xp; g.brows = TK; g.perm = NULL; g.row_base = 0;
     g.pw = B->perm_w; g.act = B->act; g.arows = TK; g.out_base = 0;
-    const unsigned grid_gu = nrb_gu * (cdiv(TK, tpb_gu) + (unsigned)(E < TK ? E : TK));
-    const unsigned grid_dn = nrb_dn * (cdiv(TK, tpb_dn) + (unsigned)(E < TK ? E : TK));
+    const unsigned grid_gu = (nrb_gu * (cdiv(TK, tpb_gu) + (unsigned)(E < TK ? E : TK)) + 7) & ~7u;
+    const unsigned grid_dn = (nrb_dn * (cdiv(TK, tpb_dn) + (unsigned)(E < TK ? E : TK)) + 7) & ~7u;
     if (grid_gu > (unsigned)B->ndesc_gu || grid_dn > (unsigned)B->ndesc_dn) return K3X_E_SHAPE;
     const bool ex_gu = (L->special & 3) != 0;
-    if (ex_gu) { if (HLg == 1) launch_gu_fp4<true, 1>(g, grid_gu, s); else launch_gu_fp4<true, 2>(g, grid_gu, s); }
-    else       { if (HLg == 1) launch_gu_fp4<false, 1>(g, grid_gu, s); else launch_gu_fp4<false, 2>(g, grid_gu, s); }
+    if (ex_gu) { if (HLg == 1) launch_gu<true, 1>(g, grid_gu, s); else launch_gu<true, 2>(g, grid_gu, s); }
+    else       { if (HLg == 1) launch_gu<false, 1>(g, grid_gu, s); else launch_gu<false, 2>(g, grid_gu, s); }
     if ((rc = launch_ok())) return rc;
 
     // routed down: B rows are the activation rows, in permuted order
@@ -639,9 +859,9 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     d.bsrc = B->act; d.brows = TK; d.perm = NULL; d.row_base = 0;
     d.y = B->y; d.out_base = 0;
     if (L->special & 4)
-        hipLaunchKernelGGL((pf_gemm<true, true, 1, DN_RT, DN_CT, 2, false>), dim3(grid_dn), dim3(PF_NT), 0, s, d);
+        hipLaunchKernelGGL((pf_gemm32<true, 1, DN_RT32, DN_CT32, 2, false>), dim3(grid_dn), dim3(PF_NT), 0, s, d);
     else
-        hipLaunchKernelGGL((pf_gemm<true, false, 1, DN_RT, DN_CT, 2, false>), dim3(grid_dn), dim3(PF_NT), 0, s, d);
+        hipLaunchKernelGGL((pf_gemm32<false, 1, DN_RT32, DN_CT32, 2, false>), dim3(grid_dn), dim3(PF_NT), 0, s, d);
     if ((rc = launch_ok())) return rc;
 
     int sh_row0 = -1;

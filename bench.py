@@ -54,6 +54,58 @@ def kernel_bytes(U, T):
     return dict(zip(KERNELS, (k1, k1b, k2, k3)))
 
 
+PREFILL_T = 2048
+
+
+def prefill_leg(torch, k3x, reps=5):
+    """Prefill of one 2048-token chunk of bf16 N(0,1) activations through the full-size
+    layer with Zipf-skewed routing (bias alpha*(pi(e)+1)^-1.1, alpha 1.0, seeded
+    permutation pi).  Algorithmic bytes: every weight byte of the experts the chunk uses,
+    the shared expert and the router, once, plus the activations in and out.  FLOPs: 2 per
+    multiply-add of the routed experts (T*K*3*I*H), the shared expert and the router."""
+    T = PREFILL_T
+    cfg = k3x.make_cfg(H, E, K, I, 1, 1, 2.5)
+    layer = k3x.MoELayer.synthetic(cfg, seed=3, zipf_alpha=1.0)
+    xs = k3x.synth_normal_f32(T * H, k3x.synth_key(3, 0, k3x.STREAM_X, 5))
+    x = torch.from_numpy(xs.reshape(T, H)).cuda().to(torch.bfloat16).contiguous()
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wt = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.Stream()
+    sh = stream.cuda_stream
+
+    def run():
+        layer.forward(out.data_ptr(), x.data_ptr(), T, k3x.K3X_BF16, 0, idx.data_ptr(),
+                      wt.data_ptr(), stream=sh)
+
+    with torch.cuda.stream(stream):
+        run()
+        run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    used = int(torch.unique(idx).numel())
+    layer_bytes = used * B_EXPERT + B_SHARED + B_ROUTER + T * H * 2 + T * H * 4
+    flops = 2.0 * T * (K * 3 * I * H + 3 * I * H + E * H)
+    layer.close()
+    del x, out, idx, wt
+    torch.cuda.empty_cache()
+    return {"workload": f"prefill {T} bf16 tokens, Zipf-skewed routing (alpha 1.0, s 1.1)",
+            "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_chunk": round(ms, 3),
+            "experts_used": used,
+            "hbm_gbs": round(layer_bytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "mfma_frac_mxfp4_peak": round(flops / (ms * 1e-3) / 1e12 / 10100.0, 4),
+            "mfma_frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / 2500.0, 4),
+            "reps": reps}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed counter summary (FETCH_SIZE and
     WRITE_SIZE runs scaled by a plain copy's readings), or None."""
@@ -147,6 +199,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 2048-token prefill leg")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only run the prefill leg and print its record")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only time a plain device copy of MIB MiB (the reference kernel for "
@@ -162,6 +217,9 @@ def main():
     assert torch.cuda.is_available(), "no GPU visible"
     if args.calibrate_copy:
         copy_calibration(torch, args.calibrate_copy, max(args.steps, 1))
+        return
+    if args.prefill_only:
+        print(json.dumps(prefill_leg(torch, load_k3x())), flush=True)
         return
     k3x = load_k3x()
     dev = torch.device("cuda:0")
@@ -241,6 +299,8 @@ def main():
     layer.close()
     del xpool, out
     torch.cuda.empty_cache()
+    if not args.no_prefill:
+        rec["prefill"] = prefill_leg(torch, k3x)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(min_seconds=args.cpu_seconds)
     else:

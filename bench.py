@@ -106,6 +106,60 @@ def prefill_leg(torch, k3x, reps=5):
             "reps": reps}
 
 
+STACK_LAYERS, STACK_TOKENS = 8, 256
+
+
+def stack_leg(torch, k3x):
+    """Eight stacked full-size layers (seed 10+l each, about 73 GB resident), each step
+    h = h + MoE_l(RMSNorm_l(h)) with norm weights 1 + N(0, 0.1), replayed from one HIP
+    graph per token; 256 consecutive batch-1 tokens from a seeded N(0,1) stream.  The
+    token copies in and out stay on the stream between replays."""
+    cfg = k3x.make_cfg(H, E, K, I, 1, 1, 2.5)
+    layers, norms = [], []
+    for l in range(STACK_LAYERS):
+        layers.append(k3x.MoELayer.synthetic(cfg, seed=10 + l, layer=l))
+        w = k3x.synth_normal_f32(H, k3x.synth_key(10 + l, l, k3x.STREAM_NORM, 0), 1.0, 0.1)
+        norms.append(torch.from_numpy(w).cuda())
+    xs = k3x.synth_normal_f32(STACK_TOKENS * H, k3x.synth_key(10, 0, k3x.STREAM_X, 7))
+    x = torch.from_numpy(xs.reshape(STACK_TOKENS, H)).cuda()
+    out = torch.empty_like(x)
+    h = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    S = k3x.Stack(layers, [w.data_ptr() for w in norms], eps=1e-5, max_T=1)
+    stream = torch.cuda.Stream()
+    sh = stream.cuda_stream
+
+    def step(t):
+        h.copy_(x[t:t + 1])
+        S.forward(h.data_ptr(), 1, sh)
+        out[t:t + 1].copy_(h)
+
+    with torch.cuda.stream(stream):
+        for t in range(8):
+            step(t)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for t in range(STACK_TOKENS):
+            step(t)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    us_tok = ms * 1e3 / STACK_TOKENS
+    per_layer_bytes = K * B_EXPERT + B_SHARED + B_ROUTER + H * 4 * 4
+    gbs = STACK_LAYERS * per_layer_bytes / (us_tok * 1e-6) / 1e9
+    finite = bool(torch.isfinite(out).all().item())
+    S.close()
+    for l in layers:
+        l.close()
+    del x, out, h, norms
+    torch.cuda.empty_cache()
+    return {"workload": f"{STACK_LAYERS} stacked layers, RMSNorm + MoE + residual each, "
+                        f"{STACK_TOKENS} batch-1 tokens, one HIP graph replay per token",
+            "us_per_token": round(us_tok, 2), "us_per_layer": round(us_tok / STACK_LAYERS, 2),
+            "sustained_hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "outputs_finite": finite}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed counter summary (FETCH_SIZE and
     WRITE_SIZE runs scaled by a plain copy's readings), or None."""
@@ -200,6 +254,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 2048-token prefill leg")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 8-layer stack leg")
+    ap.add_argument("--stack-only", action="store_true",
+                    help="only run the 8-layer stack leg and print its record")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the prefill leg and print its record")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -220,6 +277,9 @@ def main():
         return
     if args.prefill_only:
         print(json.dumps(prefill_leg(torch, load_k3x())), flush=True)
+        return
+    if args.stack_only:
+        print(json.dumps(stack_leg(torch, load_k3x())), flush=True)
         return
     k3x = load_k3x()
     dev = torch.device("cuda:0")
@@ -301,6 +361,8 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_prefill:
         rec["prefill"] = prefill_leg(torch, k3x)
+    if not args.no_stack:
+        rec["stack"] = stack_leg(torch, k3x)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(min_seconds=args.cpu_seconds)
     else:

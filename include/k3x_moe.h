@@ -179,6 +179,24 @@ void     k3x_synth_normal_f32(float *dst, size_t n, uint64_t key, double mu, dou
 void     k3x_synth_normal_bf16(uint16_t *dst, size_t n, uint64_t key, double mu,
                                double sigma);
 
+/* ---- stacked layers ------------------------------------------------------------------
+ * The MoE half of consecutive decoder layers (k3_decoder_layer_core, k3_ops.c:2547-2589,
+ * without attention): for each layer l, h = h + MoE_l(RMSNorm(h; norm_w[l], eps)), the
+ * norm as k3_rmsnorm (k3_ops.c:132-140) and the residual add as :2589.
+ * k3x_stack_create takes n_layers device-resident layers of one hidden size on one
+ * device (borrowed: they must outlive the stack; their timing hooks must be off) and
+ * their RMSNorm weights (device fp32 [hidden] each, borrowed), and reserves working
+ * memory for up to max_T tokens per call.
+ * k3x_stack_forward runs the sequence on h (device fp32 [T][hidden], updated in place)
+ * on `stream`.  The first call for a given (h, T) records the whole sequence into a HIP
+ * graph; later calls with the same (h, T) replay it (a new (h, T) records a new graph).
+ * Two calls on one stack must be ordered on one stream. */
+typedef struct k3x_stack k3x_stack;
+int  k3x_stack_create(k3x_moe_layer *const *layers, const float *const *norm_w, int n_layers,
+                      float eps, int max_T, k3x_stack **out);
+int  k3x_stack_forward(k3x_stack *S, float *h, int T, void *stream);
+void k3x_stack_destroy(k3x_stack *S);
+
 /* ---- timing hooks ---------------------------------------------------------------
  * The kernels the last k3x_moe_forward on L enqueued, bracketed by two HIP events on
  * the stream it used (recorded when timing is on).  ms receives the elapsed time of

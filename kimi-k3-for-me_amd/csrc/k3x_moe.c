@@ -556,3 +556,91 @@ fail:
     layer_free(L);
     return rc;
 }
+
+/* ---------------------------------------------------------------- stacks ---- */
+#define K3X_STACK_MAX 256
+struct k3x_stack {
+    int             n, max_T, device, H;
+    float           eps;
+    k3x_moe_layer  *layers[K3X_STACK_MAX];
+    const float    *norm_w[K3X_STACK_MAX];
+    float          *y;              /* [max_T][H] normalised activations */
+    hipStream_t     cap;            /* private stream the sequence is recorded on */
+    hipGraph_t      graph;
+    hipGraphExec_t  exec;
+    float          *g_h;            /* (h, T) the recorded graph is bound to */
+    int             g_T;
+};
+
+int k3x_stack_create(k3x_moe_layer *const *layers, const float *const *norm_w, int n_layers,
+                     float eps, int max_T, k3x_stack **out)
+{
+    if (!layers || !norm_w || !out || n_layers <= 0 || n_layers > K3X_STACK_MAX || max_T <= 0)
+        return K3X_E_ARG;
+    *out = NULL;
+    const int H = layers[0] ? layers[0]->cfg.hidden : 0, dev = layers[0] ? layers[0]->device : 0;
+    for (int l = 0; l < n_layers; l++) {
+        if (!layers[l] || !norm_w[l]) return K3X_E_ARG;
+        if (layers[l]->cfg.hidden != H || layers[l]->device != dev) return K3X_E_SHAPE;
+        if (layers[l]->timing) return K3X_E_ARG;
+    }
+    k3x_stack *S = (k3x_stack *)calloc(1, sizeof *S);
+    if (!S) return K3X_E_NOMEM;
+    int rc = 0;
+    S->n = n_layers; S->max_T = max_T; S->device = dev; S->H = H; S->eps = eps;
+    for (int l = 0; l < n_layers; l++) { S->layers[l] = layers[l]; S->norm_w[l] = norm_w[l]; }
+    HIPCHK(hipSetDevice(dev));
+    if (hipMalloc((void **)&S->y, (size_t)max_T * H * 4) != hipSuccess) { rc = K3X_E_NOMEM; goto fail; }
+    HIPCHK(hipStreamCreateWithFlags(&S->cap, hipStreamNonBlocking));
+    /* every allocation a call can make happens here, never while recording */
+    if (max_T > K3X_DECODE_MAX_T)
+        for (int l = 0; l < n_layers; l++) RCCHK(k3x_pf_reserve(layers[l], max_T));
+    *out = S;
+    return 0;
+fail:
+    k3x_stack_destroy(S);
+    return rc;
+}
+
+static int stack_record(k3x_stack *S, float *h, int T)
+{
+    int rc = 0;
+    if (S->exec) { hipGraphExecDestroy(S->exec); S->exec = NULL; }
+    if (S->graph) { hipGraphDestroy(S->graph); S->graph = NULL; }
+    HIPCHK(hipStreamBeginCapture(S->cap, hipStreamCaptureModeThreadLocal));
+    for (int l = 0; l < S->n && !rc; l++) {
+        rc = k3x_rmsnorm(S->y, h, S->norm_w[l], S->H, T, S->eps, S->cap);
+        if (!rc) rc = k3x_moe_forward(S->layers[l], h, S->y, K3X_F32, T, h, NULL, NULL, S->cap);
+    }
+    hipGraph_t g = NULL;
+    const hipError_t ec = hipStreamEndCapture(S->cap, &g);
+    if (rc) { if (g) hipGraphDestroy(g); return rc; }
+    if (ec != hipSuccess || !g) return K3X_E_HIP;
+    S->graph = g;
+    HIPCHK(hipGraphInstantiate(&S->exec, S->graph, NULL, NULL, 0));
+    S->g_h = h; S->g_T = T;
+fail:
+    return rc;
+}
+
+int k3x_stack_forward(k3x_stack *S, float *h, int T, void *stream)
+{
+    if (!S || !h || T <= 0 || ((uintptr_t)h & 15)) return K3X_E_ARG;
+    if (T > S->max_T) return K3X_E_SHAPE;
+    int rc = 0;
+    HIPCHK(hipSetDevice(S->device));
+    if (!S->exec || S->g_h != h || S->g_T != T) RCCHK(stack_record(S, h, T));
+    HIPCHK(hipGraphLaunch(S->exec, (hipStream_t)stream));
+fail:
+    return rc;
+}
+
+void k3x_stack_destroy(k3x_stack *S)
+{
+    if (!S) return;
+    if (S->exec) hipGraphExecDestroy(S->exec);
+    if (S->graph) hipGraphDestroy(S->graph);
+    if (S->cap) hipStreamDestroy(S->cap);
+    if (S->y) hipFree(S->y);
+    free(S);
+}

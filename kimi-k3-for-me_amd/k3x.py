@@ -29,7 +29,7 @@ EXPORTS = [
     "k3x_moe_layer_read_expert", "k3x_moe_forward", "k3x_rmsnorm", "k3x_moe",
     "k3x_moe_prefill", "k3x_expert_drops", "k3x_synth_layer_create", "k3x_synth_key",
     "k3x_synth_normal_f32", "k3x_synth_normal_bf16", "k3x_moe_layer_set_timing",
-    "k3x_moe_layer_last_ms",
+    "k3x_moe_layer_last_ms", "k3x_stack_create", "k3x_stack_forward", "k3x_stack_destroy",
 ]
 
 
@@ -103,6 +103,10 @@ def lib():
         L.k3x_synth_normal_bf16.restype = None
         L.k3x_moe_layer_set_timing.argtypes = [vp, i]
         L.k3x_moe_layer_last_ms.argtypes = [vp, C.POINTER(C.c_float)]
+        L.k3x_stack_create.argtypes = [C.POINTER(vp), C.POINTER(vp), i, f, i, C.POINTER(vp)]
+        L.k3x_stack_forward.argtypes = [vp, vp, i, vp]
+        L.k3x_stack_destroy.argtypes = [vp]
+        L.k3x_stack_destroy.restype = None
         _lib = L
     return _lib
 
@@ -265,3 +269,32 @@ def synth_normal_bf16(n, key, mu=0.0, sigma=1.0):
     a = np.empty(n, np.uint16)
     lib().k3x_synth_normal_bf16(a.ctypes.data, n, key, mu, sigma)
     return a
+
+
+class Stack:
+    """Consecutive layers' MoE halves, h = h + MoE_l(RMSNorm_l(h)), replayed from a HIP
+    graph (k3x_stack).  Layers and norm weights are borrowed: keep them alive."""
+
+    def __init__(self, layers, norm_ptrs, eps=1e-5, max_T=1):
+        n = len(layers)
+        la = (C.c_void_p * n)(*[l.h.value for l in layers])
+        na = (C.c_void_p * n)(*norm_ptrs)
+        h = C.c_void_p()
+        _check(lib().k3x_stack_create(la, na, n, eps, max_T, C.byref(h)), "k3x_stack_create")
+        self.h = h
+        self.layers = list(layers)
+
+    def forward(self, h_ptr, T, stream=0):
+        """h (device fp32 [T][hidden]) updated in place, asynchronously on `stream`."""
+        _check(lib().k3x_stack_forward(self.h, h_ptr, T, stream or None), "k3x_stack_forward")
+
+    def close(self):
+        if self.h:
+            lib().k3x_stack_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -4,8 +4,12 @@ Default workload: the full-size K2-class MoE layer (hidden 7168, 384 routed expe
 top-8, expert intermediate 2048 in MXFP4 = E2M1 codes + E8M0 per-32 scales, one bf16
 shared expert of intermediate 2048, sigmoid router with bias, routed scale 2.5) decoding
 batch-1 tokens.  A step is one layer invocation on one token; the tokens rotate over a
-pool of 64 distinct seeded bf16 N(0,1) activations resident in HBM, so successive steps
-touch different experts.  Weights are synthetic (seeded generator, random init).
+pool of 64 distinct seeded bf16 N(0,1) activations resident in HBM, and the steps rotate
+over 4 layers of that shape, so every step reads its weights from HBM (a single layer
+called back to back finds its router and shared expert, 99 MB, still in the 256 MB
+last-level cache; that figure is reported as warm_one_layer_us_per_token).  Weights are
+synthetic (seeded generator, random init).  The record also carries the 2048-token
+prefill leg and the 8-layer stack leg.
 
 Prints ONE JSON line (rank 0):
   value        microseconds per token for the whole layer (lower is better)
@@ -32,6 +36,7 @@ HBM_PEAK_GBS = 8000.0
 B_EXPERT = 3 * I * H // 2 + 3 * I * H // 32          # 23,396,352 bytes per routed expert
 B_SHARED = 3 * SI * H * 2                             # 88,080,384
 B_ROUTER = E * H * 4 + E * 4                          # 11,011,584
+NROT = 4                                              # layers the decode steps rotate over
 
 
 def load_k3x():
@@ -41,16 +46,18 @@ def load_k3x():
     return mod
 
 
-KERNELS = ["k1_router_shared", "k1b_select_shdown", "k2_gateup", "k3_down"]
+KERNELS = ["k1_router_bset", "k1b_select_shared", "k2_gateup", "k3_down"]
 
 
 def kernel_bytes(U, T):
     """Algorithmic HBM bytes per launch of the four decode kernels (each weight byte
-    once; activations included)."""
-    k1 = B_ROUTER + 2 * SI * H * 2 + T * H * 2
-    k1b = H * SI * 2 + T * H * 4
+    once; activations included): k1 the router weights, k1b the shared expert's gate/up
+    weights, k2 the unique experts' gate/up weights, k3 the unique experts' and the
+    shared expert's down weights and the output."""
+    k1 = B_ROUTER + T * H * 2
+    k1b = 2 * SI * H * 2
     k2 = U * 2 * (I * H // 2 + I * H // 32)
-    k3 = U * (H * I // 2 + H * I // 32) + 2 * T * H * 4
+    k3 = U * (H * I // 2 + H * I // 32) + H * SI * 2 + T * H * 4
     return dict(zip(KERNELS, (k1, k1b, k2, k3)))
 
 
@@ -285,8 +292,12 @@ def main():
     dev = torch.device("cuda:0")
     cfg = k3x.make_cfg(H, E, K, I, 1, 1, 2.5)
     t_build = time.perf_counter()
-    layer = k3x.MoELayer.synthetic(cfg, seed=1, router_sigma=0.02, bias_sigma=0.1)
-    build_s = time.perf_counter() - t_build
+    # NROT layers of the same shape, used in turn: between two calls of one layer the
+    # other layers stream about 860 MB, so no weight of the call is still in the 256 MB
+    # last-level cache -- as in a model with many layers.
+    layers = [k3x.MoELayer.synthetic(cfg, seed=1 + j, router_sigma=0.02, bias_sigma=0.1)
+              for j in range(NROT)]
+    build_s = (time.perf_counter() - t_build) / NROT
     n_pool = 64
     xs = k3x.synth_normal_f32(n_pool * H, k3x.synth_key(1, 0, k3x.STREAM_X, 100))
     xpool = torch.from_numpy(xs.reshape(n_pool, H)).to(dev).to(torch.bfloat16).contiguous()
@@ -295,37 +306,42 @@ def main():
     sh = stream.cuda_stream
     row = xpool.stride(0) * 2
 
-    def step(i):
-        layer.forward(out.data_ptr(), xpool.data_ptr() + (i % n_pool) * row, 1, k3x.K3X_BF16,
-                      stream=sh)
+    def step(i, rot=NROT):
+        layers[i % rot].forward(out.data_ptr(), xpool.data_ptr() + (i % n_pool) * row, 1,
+                                k3x.K3X_BF16, stream=sh)
 
-    with torch.cuda.stream(stream):
-        for i in range(args.warmup):
-            step(i)
-        torch.cuda.synchronize()
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        ev0.record(stream)
-        for i in range(args.steps):
-            step(args.warmup + i)
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-    wall_ms = (t1 - t0) * 1e3 / args.steps
-    gpu_ms = ev0.elapsed_time(ev1) / args.steps
+    def timed(rot):
+        with torch.cuda.stream(stream):
+            for i in range(args.warmup):
+                step(i, rot)
+            torch.cuda.synchronize()
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            ev0.record(stream)
+            for i in range(args.steps):
+                step(args.warmup + i, rot)
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+        return (t1 - t0) * 1e3 / args.steps, ev0.elapsed_time(ev1) / args.steps
+
+    wall_ms, gpu_ms = timed(NROT)
+    warm_ms, _ = timed(1)
 
     # per-kernel durations: HIP events between the kernels, on the launch stream
-    layer.set_timing(True)
+    for l in layers:
+        l.set_timing(True)
     names = KERNELS
     per = {n: [] for n in names}
     with torch.cuda.stream(stream):
         for i in range(args.steps):
             step(i)
-            ms = layer.last_ms()
+            ms = layers[i % NROT].last_ms()
             for n, v in zip(names, ms):
                 per[n].append(v)
-    layer.set_timing(False)
+    for l in layers:
+        l.set_timing(False)
     avg = {n: float(np.mean(v)) for n, v in per.items()}
     kb = kernel_bytes(U=K, T=1)
     dom = max(avg, key=lambda n: avg[n])
@@ -346,7 +362,8 @@ def main():
         "data": "synthetic (seeded random weights and bf16 N(0,1) tokens)",
         "config": {"workload": "K2-class MoE layer decode b=1: hidden 7168, 384 experts top-8, "
                                "inter 2048 MXFP4, 1 bf16 shared expert",
-                   "tokens_per_step": 1, "token_pool": n_pool, "parallelism": "none (1 GPU)"},
+                   "tokens_per_step": 1, "token_pool": n_pool, "layers_rotated": NROT,
+                   "parallelism": "none (1 GPU)"},
         "layer_hbm_gbs": round(layer_bytes / (wall_ms * 1e-3) / 1e9, 1),
         "gpu_event_ms_per_step": round(gpu_ms, 5),
         "kernel_avg_us": {n: round(v * 1e3, 2) for n, v in avg.items()},
@@ -355,8 +372,10 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
                      "algorithmic_bytes_per_launch": kb[dom]},
         "layer_build_s": round(build_s, 2),
+        "warm_one_layer_us_per_token": round(warm_ms * 1e3, 2),
     }
-    layer.close()
+    for l in layers:
+        l.close()
     del xpool, out
     torch.cuda.empty_cache()
     if not args.no_prefill:

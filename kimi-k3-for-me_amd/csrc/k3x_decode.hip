@@ -1,17 +1,21 @@
 // k3x_decode.hip - the decode path of the MoE block (T <= 8 tokens), four launches:
 //
-//   k1_router_shared  router logits in double, sigmoid, +bias (k3_router, k3_ops.c:1624-
-//                     1694) for every expert, and the shared expert's gate/up products
-//                     with SwiGLU (moe_shared, :1848-1857) in the same launch.
-//   k1b_select_shdown one workgroup selects each token's top-k (:1700-1716) and lists the
+//   k1_router_bset    router logits in double, sigmoid, +bias (k3_router, k3_ops.c:1624-
+//                     1694) for every expert, and x's B fragments for the products.
+//   k1b_select_shared workgroup 0 selects each token's top-k (:1700-1716) and lists the
 //                     unique experts (the dedup of moe_prefill_routed, :2067-2081) while
-//                     the others stream the shared expert's down product (:1858).
-//   k2_gateup         each unique expert's gate/up products (k3_matmul_mxfp4,
-//                     :3323-3776) with SwiGLU (k3_situ_glu at 2^64 betas, :148-161) and the
+//                     the others stream the shared expert's gate/up weights (moe_shared,
+//                     :1848-1857) in parts of K.
+//   k2_gateup         the shared activation: the parts added, SwiGLU (k3_situ_glu at 2^64
+//                     betas, :148-161), in the first workgroups; then each unique expert's
+//                     gate/up products (k3_matmul_mxfp4, :3323-3776) with SwiGLU and the
 //                     routing weight folded in.
-//   k3_down           each unique expert's down product into one accumulator set per 16
-//                     output rows (the weighted combine, :1941-1942), plus the shared
-//                     result (:1859) and an optional residual.
+//   k3_down           each unique expert's down product and the shared expert's (:1858)
+//                     into one accumulator set per 16 output rows (the weighted combine,
+//                     :1941-1942, plus the shared result, :1859), and an optional residual.
+//
+// The router runs alone so that its 11 MB arrive first; the selection then overlaps the
+// shared expert's stream.
 //
 // Each weight byte is read once per call.  Weights are dequantised in registers
 // (E2M1 x 2^(s-127) is exact in bf16) and multiplied on v_mfma_f32_16x16x32_bf16 against
@@ -30,8 +34,8 @@
 #include "k3x_device.h"
 #include "k3x_topk.h"
 
-#define NT1 512     // k1 workgroup: 8 waves
-#define NT  256     // k1b / k2 workgroup: 4 waves
+#define NT1 256     // k1 / k1b workgroup: 4 waves
+#define NT  256     // k2 workgroup: 4 waves
 #define NT3 512     // k3 workgroup: 8 waves
 #define STAGE_MAX 65536u   // largest B set staged in LDS (bytes)
 #define SQ_BYTES 4352u     // an fp4 super-quad of a 16-row tile
@@ -257,6 +261,85 @@ __device__ __forceinline__ void per_token(const float (&acc)[NV], int NC, int la
     if ((n & 1) == 0 && n < NC) f(4 * kq, n >> 1, v);
 }
 
+// ------------------------------------------------------------------ selection
+struct KSArgs {
+    const float   *score, *choice;
+    int            E, K, renorm;
+    float          routed_scale;
+    k3x_route     *route;          // unique experts and per-(expert, token) weights, for k2/k3
+    int           *idx;  float *wt;        // internal [T][K]
+    int           *uidx; float *uwt;       // optional caller copies
+    int            T;
+};
+
+// Routing of every token (one wave per token), then the unique experts in first-seen
+// order over (token, slot) and each one's weight per token: the sum of its slots' weights
+// (0 where not chosen; a slot repeated by a round that found nothing adds 0).  The list
+// is built in parallel: each expert's first item by an LDS minimum, the first items'
+// slots by ballots, then one weight per (slot, token).
+template <int NE>
+__device__ void ks_select(const KSArgs &a)
+{
+    static_assert(NT1 == NT, "the selection runs in a k1b workgroup");
+    constexpr int NW = NT / WAVE;
+    __shared__ int      s_idx[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
+    __shared__ float    s_w[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
+    __shared__ int      s_first[1024];
+    __shared__ int      s_uq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];
+    __shared__ int      s_wc[NW];
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const rsrc_t cr = make_rsrc(a.choice, (uint32_t)(a.T * a.E * 4));
+    const rsrc_t sr = make_rsrc(a.score, (uint32_t)(a.T * a.E * 4));
+    for (int t = wave; t < a.T; t += NW)
+        wave_topk<NE>(cr, sr, (uint32_t)(t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
+                      s_idx[t], s_w[t], lane);
+    for (int e = threadIdx.x; e < a.E; e += NT) s_first[e] = 0x7FFFFFFF;
+    __syncthreads();
+    const int TK = a.T * a.K;
+    for (int i = threadIdx.x; i < TK; i += NT) {
+        const int t = i / a.K, j = i % a.K;
+        const int ex = s_idx[t][j];
+        a.idx[i] = ex;
+        a.wt[i] = s_w[t][j];
+        if (a.uidx) { a.uidx[i] = ex; a.uwt[i] = s_w[t][j]; }
+        atomicMin(&s_first[ex], i);
+    }
+    __syncthreads();
+    int base = 0;
+    for (int c0 = 0; c0 < TK; c0 += NT) {          // uniform trip count
+        const int i = c0 + threadIdx.x;
+        const int ex = i < TK ? s_idx[i / a.K][i % a.K] : 0;
+        const bool first = i < TK && s_first[ex] == i;
+        const uint64_t m = __ballot(first);
+        if (lane == 0) s_wc[wave] = __popcll(m);
+        __syncthreads();
+        int off = base, tot = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            off += w < wave ? s_wc[w] : 0;
+            tot += s_wc[w];
+        }
+        if (first) {
+            const int slot = off + lanes_below(m);
+            s_uq[slot] = ex;
+            a.route->uniq[slot] = ex;
+        }
+        base += tot;
+        __syncthreads();
+    }
+    const int nu = base;
+    for (int f = threadIdx.x; f < nu * K3X_DECODE_MAX_T; f += NT) {
+        const int slot = f / K3X_DECODE_MAX_T, t = f % K3X_DECODE_MAX_T;
+        const int ex = s_uq[slot];
+        float w = 0.0f;
+        if (t < a.T)
+            for (int j = 0; j < a.K; j++)
+                if (s_idx[t][j] == ex) w += s_w[t][j];
+        a.route->wtok[slot][t] = w;
+    }
+    if (threadIdx.x == 0) a.route->nu = nu;
+}
+
 // ------------------------------------------------------------------ K1
 struct K1Args {
     const float *router;     // [E][H]
@@ -265,15 +348,12 @@ struct K1Args {
     int          x_bf16;
     int          T, H, E;
     float       *score, *choice;   // [T][E]
-    uint16_t    *xB;               // compact B set of x over whole super-quads, for k2
-    int          n_rwg;            // router workgroups
-    const uint16_t *sh_gate, *sh_up;
-    int          SI;
-    uint16_t    *shB;              // compact B set of the shared activation, for k1b
+    uint16_t    *xB;               // compact B set of x over whole super-quads
+    int          n_rwg;            // workgroups
 };
 
 #define RWAVES 4                     // waves per expert row in the router
-#define RCH    4                     // float4 chunks per lane held at once
+#define RCH    8                     // float4 chunks per lane held at once
 
 // Router logits: four waves per expert, sum_i W[e][i] x[i] in double (a product of two
 // floats is exact in double; only the order of the additions differs from the
@@ -337,249 +417,84 @@ __device__ void k1_router(const K1Args &a, float *lds)
     }
 }
 
-// x's B set for one workgroup, in LDS: pair p covers the hi and lo entries of one token
-// at (q, t, kq); up to K1_MAXP pairs per thread are loaded before the weights.
-#define K1_MAXP 2
-struct XPairs {
-    u32x4 a[K1_MAXP], b[K1_MAXP];
+// Router logits of NT1 / WAVE / RWAVES experts, and a share of x's B set for k1b/k2.
+__global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
+{
+    __shared__ float lds[(NT1 / WAVE - 1) * 8 * WAVE];
+    k1_router(a, lds);
+    const int nS = ((a.H >> 7) + 3) >> 2;
+    x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS,
+              blockIdx.x * NT1 + threadIdx.x, a.n_rwg * NT1);
+}
+
+// ------------------------------------------------------------------ K1b
+struct K1bArgs {
+    KSArgs         ks;             // the selection, in workgroup 0
+    const uint16_t *xB;
+    int            T, H;
+    const uint16_t *sh_gate, *sh_up;
+    int            SI;
+    int            nparts;         // parts of K the shared gate/up products are split into
+    float         *shp;            // [nparts][2][T][SI] partial gate and up sums, for k2
 };
 
-__device__ __forceinline__ void xp_pos(int p, int T, int H, int &tok, int &q, int &t, int &kq,
-                                       size_t &elem)
-{
-    tok = p % T;
-    const int r = p / T;
-    kq = r & 3; t = (r >> 2) & 3; q = r >> 4;
-    elem = (size_t)tok * H + (size_t)q * 128 + kq * 32 + t * 8;
-}
-
-__device__ __forceinline__ void xp_load(u32x4 &a, u32x4 &b, rsrc_t xr, int x_bf16, size_t elem,
-                                        bool on)
-{
-    if (x_bf16) {
-        a = bload16(xr, on ? (uint32_t)(elem * 2) : K3X_OOB);
-        b = (u32x4){0u, 0u, 0u, 0u};
-    } else {
-        a = bload16(xr, on ? (uint32_t)(elem * 4) : K3X_OOB);
-        b = bload16(xr, on ? (uint32_t)(elem * 4 + 16) : K3X_OOB);
-    }
-}
-
-__device__ __forceinline__ void xp_store(const u32x4 &a, const u32x4 &b, int x_bf16, int tok,
-                                         int q, int t, int kq, int NC)
-{
-    float xv[8];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        xv[2 * j] = x_bf16 ? bf2f(a[j] & 0xFFFFu) : __uint_as_float(j < 2 ? a[2 * j] : b[2 * j - 4]);
-        xv[2 * j + 1] = x_bf16 ? bf2f(a[j] >> 16) : __uint_as_float(j < 2 ? a[2 * j + 1] : b[2 * j - 3]);
-    }
-    const uint32_t e0 = (uint32_t)(((q * 4 + t) * 4 + kq) * NC + 2 * tok) * 16u;
-    *(u32x4 *)(dyn_lds + e0) = bfrag_of(xv, 0);
-    *(u32x4 *)(dyn_lds + e0 + 16u) = bfrag_of(xv, 1);
-}
-
-// Shared expert gate and up products for 16 rows over the full K, sixteen waves taking
-// interleaved quads (each wave both matrices of a quad, over one B read); then SwiGLU
-// per token and the activation's hi/lo B fragments into shB.
-template <bool LDSX>
-__device__ void k1_shared(const K1Args &a, float *lds, int rt)
+// Shared expert gate and up partial products: workgroup sb takes rows 16*rt .. +15 over
+// quads [q0, q0+nq) of part `part` of K, that slice of x's B set staged in LDS; its four
+// waves take those quads interleaved (each wave both matrices of a quad, over one B
+// read).  The hi + lo columns are summed per token and the partial gate and up values
+// written to shp.
+__device__ void k1b_shared(const K1bArgs &a, float *lds, int sb)
 {
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int NW = NT1 / WAVE;
+    const int P = a.nparts, rt = sb / P, part = sb % P;
     const int nQ = a.H >> 7, NC = 2 * a.T;
-    const int cnt = strided_count(wave, NW, nQ);
+    const int q0 = part * nQ / P, nq = (part + 1) * nQ / P - q0;
+    const int cnt = strided_count(wave, NW, nq);
     const uint32_t tbytes = (uint32_t)nQ * 4096u;
     const rsrc_t rg = make_rsrc(a.sh_gate + (size_t)rt * 16 * a.H, tbytes);
     const rsrc_t ru = make_rsrc(a.sh_up + (size_t)rt * 16 * a.H, tbytes);
-    const rsrc_t xr = make_rsrc(a.x, (uint32_t)((size_t)a.T * a.H * (a.x_bf16 ? 2 : 4)));
-    const int npairs = nQ * 16 * a.T;
-    XPairs xp;
-    if (LDSX) {
-#pragma unroll
-        for (int i = 0; i < K1_MAXP; i++) {
-            const int p = threadIdx.x + i * NT1;
-            int tok, q, t, kq;
-            size_t elem;
-            xp_pos(p, a.T, a.H, tok, q, t, kq, elem);
-            xp_load(xp.a[i], xp.b[i], xr, a.x_bf16, elem, p < npairs);
-        }
-    }
+    Stage<8> st;
+    st.issue(a.xB + (size_t)q0 * 128 * NC, (uint32_t)nq * 256u * NC, NT1);
     QB g[2], u[2];
     auto ld = [&](int i, int k) AI {
-        const uint32_t o = k < cnt ? (uint32_t)(wave + NW * k) * 4096u : K3X_OOB;
+        const uint32_t o = k < cnt ? (uint32_t)(q0 + wave + NW * k) * 4096u : K3X_OOB;
         qb_load(g[i], rg, o, lane);
         qb_load(u[i], ru, o, lane);
     };
     ring_prime<2>(ld);
+    st.commit(NT1);
+    __syncthreads();
+    BFrag<true> bf;
+    bf.init(nullptr, 0u, NC, lane);
     f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
-    if (LDSX) {
-#pragma unroll
-        for (int i = 0; i < K1_MAXP; i++) {
-            const int p = threadIdx.x + i * NT1;
-            int tok, q, t, kq;
-            size_t elem;
-            xp_pos(p, a.T, a.H, tok, q, t, kq, elem);
-            if (p < npairs) xp_store(xp.a[i], xp.b[i], a.x_bf16, tok, q, t, kq, NC);
-        }
-        for (int p = threadIdx.x + K1_MAXP * NT1; p < npairs; p += NT1) {
-            int tok, q, t, kq;
-            size_t elem;
-            xp_pos(p, a.T, a.H, tok, q, t, kq, elem);
-            u32x4 va, vb;
-            xp_load(va, vb, xr, a.x_bf16, elem, true);
-            xp_store(va, vb, a.x_bf16, tok, q, t, kq, NC);
-        }
-        __syncthreads();
-        BFrag<true> bf;
-        bf.init(nullptr, 0u, NC, lane);
-        ring_loop<2>(cnt, ld, [&](int i, int k) AI {
-            const int q = wave + NW * k;
-            u32x4 b[4];
-#pragma unroll
-            for (int t = 0; t < 4; t++) b[t] = bf.get(0u, q, t);
-            qb_mfma(dg, g[i], b);
-            qb_mfma(du, u[i], b);
-        });
-    } else {
-        ring_loop<2>(cnt, ld, [&](int i, int k) AI {
-            u32x4 b[4];
-            bx_load(b, a.x, a.x_bf16, xr, a.H, NC, wave + NW * k, lane);
-            qb_mfma(dg, g[i], b);
-            qb_mfma(du, u[i], b);
-        });
-    }
-    float acc[8] = {dg[0], dg[1], dg[2], dg[3], du[0], du[1], du[2], du[3]};
-    wave_sum_lds<8, NT1 / WAVE>(acc, lds, wave, lane);
-    if (wave != 0) return;
-    per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&v)[8]) AI {
-        for (int i = 0; i < 4; i++) {
-            uint32_t hi, lo;
-            split_bf16(swiglu(v[i], v[4 + i]), hi, lo);
-            const int r = rt * 16 + r0 + i;
-            a.shB[bfrag_off(r, 2 * tok, NC)] = (uint16_t)hi;
-            a.shB[bfrag_off(r, 2 * tok + 1, NC)] = (uint16_t)lo;
-        }
-    });
-}
-
-template <bool LDSX>
-__global__ void __launch_bounds__(NT1) k1_router_shared(K1Args a)
-{
-    __shared__ float lds[(NT1 / WAVE - 1) * 8 * WAVE];
-    if ((int)blockIdx.x < a.n_rwg) {
-        k1_router(a, lds);
-        const int nS = ((a.H >> 7) + 3) >> 2;
-        x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS,
-                  blockIdx.x * NT1 + threadIdx.x, a.n_rwg * NT1);
-        return;
-    }
-    k1_shared<LDSX>(a, lds, blockIdx.x - a.n_rwg);
-}
-
-// ------------------------------------------------------------------ K1b
-struct KSArgs {
-    const float   *score, *choice;
-    int            E, K, renorm;
-    float          routed_scale;
-    k3x_route     *route;          // unique experts and per-(expert, token) weights, for k2/k3
-    int           *idx;  float *wt;        // internal [T][K]
-    int           *uidx; float *uwt;       // optional caller copies
-    int            T, H;
-    const uint16_t *sh_down;
-    const uint16_t *shB;           // compact B set of the shared activation
-    float         *ysh;            // [T][H] shared expert output
-    int            SI;
-};
-
-// Shared expert down product for 16 output rows: four waves on interleaved quads, the
-// shared activation's B set staged in LDS when it fits.
-template <bool LDSB>
-__device__ void ks_shared_down(const KSArgs &a, float *lds, int rt)
-{
-    const int wave = wave_id(), lane = threadIdx.x % WAVE;
-    const int NW = NT / WAVE;
-    const int nQS = a.SI >> 7, NC = 2 * a.T;
-    const int cnt = strided_count(wave, NW, nQS);
-    const uint32_t bbytes = (uint32_t)nQS * 256u * NC;
-    const rsrc_t rw = make_rsrc(a.sh_down + (size_t)rt * 16 * a.SI, (uint32_t)nQS * 4096u);
-    Stage<8> st;
-    if (LDSB) st.issue(a.shB, bbytes, NT);
-    QB ring[2];
-    auto ld = [&](int i, int k) AI {
-        qb_load(ring[i], rw, k < cnt ? (uint32_t)(wave + NW * k) * 4096u : K3X_OOB, lane);
-    };
-    ring_prime<2>(ld);
-    if (LDSB) {
-        st.commit(NT);
-        __syncthreads();
-    }
-    BFrag<LDSB> bf;
-    bf.init(a.shB, bbytes, NC, lane);
-    f32x4 d = {0.f, 0.f, 0.f, 0.f};
     ring_loop<2>(cnt, ld, [&](int i, int k) AI {
         const int q = wave + NW * k;
         u32x4 b[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) b[t] = bf.get(0u, q, t);
-        qb_mfma(d, ring[i], b);
+        qb_mfma(dg, g[i], b);
+        qb_mfma(du, u[i], b);
     });
-    float acc[4] = {d[0], d[1], d[2], d[3]};
-    wave_sum_lds<4, NT / WAVE>(acc, lds, wave, lane);
+    float acc[8] = {dg[0], dg[1], dg[2], dg[3], du[0], du[1], du[2], du[3]};
+    wave_sum_lds<8, NT1 / WAVE>(acc, lds, wave, lane);
     if (wave != 0) return;
-    per_token<4>(acc, NC, lane, [&](int r0, int tok, const float (&v)[4]) AI {
-        for (int i = 0; i < 4; i++) a.ysh[(size_t)tok * a.H + rt * 16 + r0 + i] = v[i];
+    per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&v)[8]) AI {
+        float *pg = a.shp + (((size_t)part * 2 + 0) * a.T + tok) * a.SI + rt * 16 + r0;
+        float *pu = a.shp + (((size_t)part * 2 + 1) * a.T + tok) * a.SI + rt * 16 + r0;
+        *(f32x4 *)pg = (f32x4){v[0], v[1], v[2], v[3]};
+        *(f32x4 *)pu = (f32x4){v[4], v[5], v[6], v[7]};
     });
 }
 
-// Routing of every token (one wave per token), then the unique experts in first-seen
-// order over (token, slot) and each one's weight per token (0 where not chosen).
+// Workgroup 0 selects every token's experts while the others stream the shared expert's
+// gate/up weights.
 template <int NE>
-__device__ void ks_select(const KSArgs &a)
+__global__ void __launch_bounds__(NT1) k1b_select_shared(K1bArgs a)
 {
-    __shared__ int      s_idx[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
-    __shared__ float    s_w[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
-    __shared__ uint64_t s_key[NT / WAVE][K3X_MAX_TOPK];
-    __shared__ int      s_e[NT / WAVE][K3X_MAX_TOPK];
-    __shared__ float    s_sc[NT / WAVE][K3X_MAX_TOPK];
-    __shared__ int      s_slot[1024];
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const rsrc_t cr = make_rsrc(a.choice, (uint32_t)(a.T * a.E * 4));
-    const rsrc_t sr = make_rsrc(a.score, (uint32_t)(a.T * a.E * 4));
-    for (int t = wave; t < a.T; t += NT / WAVE)
-        wave_topk<NE>(cr, sr, (uint32_t)(t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
-                      s_idx[t], s_w[t], s_key[wave], s_e[wave], s_sc[wave], lane);
-    for (int e = threadIdx.x; e < a.E; e += NT) s_slot[e] = -1;
-    __syncthreads();
-    for (int i = threadIdx.x; i < a.T * a.K; i += NT) {
-        const int t = i / a.K, j = i % a.K;
-        a.idx[i] = s_idx[t][j];
-        a.wt[i] = s_w[t][j];
-        if (a.uidx) { a.uidx[i] = s_idx[t][j]; a.uwt[i] = s_w[t][j]; }
-    }
-    if (threadIdx.x == 0) {
-        int nu = 0;
-        for (int t = 0; t < a.T; t++)
-            for (int j = 0; j < a.K; j++) {
-                const int ex = s_idx[t][j];
-                if (s_slot[ex] < 0) {
-                    s_slot[ex] = nu;
-                    a.route->uniq[nu] = ex;
-                    for (int tt = 0; tt < K3X_DECODE_MAX_T; tt++) a.route->wtok[nu][tt] = 0.0f;
-                    nu++;
-                }
-                a.route->wtok[s_slot[ex]][t] = s_w[t][j];
-            }
-        a.route->nu = nu;
-    }
-}
-
-template <int NE, bool LDSB>
-__global__ void __launch_bounds__(NT) k1b_select_shdown(KSArgs a)
-{
-    __shared__ float lds[(NT / WAVE - 1) * 4 * WAVE];
-    if (blockIdx.x == 0) { ks_select<NE>(a); return; }
-    ks_shared_down<LDSB>(a, lds, blockIdx.x - 1);
+    __shared__ float lds[(NT1 / WAVE - 1) * 8 * WAVE];
+    if (blockIdx.x == 0) ks_select<NE>(a.ks);
+    else                 k1b_shared(a, lds, blockIdx.x - 1);
 }
 
 // ------------------------------------------------------------------ K2
@@ -590,7 +505,60 @@ struct K2Args {
     const uint16_t *xB;            // compact B set of x over whole super-quads
     uint16_t      *actB;           // one compact B set per unique expert (slot)
     int            T, H, I;
+    int            n_fin;          // workgroups of the shared activation (the first ones)
+    int            SI, nparts;
+    const float   *shp;            // [nparts][2][T][SI] partial gate and up sums (k1)
+    uint16_t      *shB;            // compact B set of the shared activation, for k3
 };
+
+// The shared activation for rows 128*w .. 128*w+127: the parts of k1's gate and up sums
+// added in part order (all parts' loads issued at once; parts past nparts read as 0),
+// SwiGLU, and the hi/lo B fragments into shB (2 entries of 8 rows per token).  Item f:
+// matrix m, token, 8-row group r8; its sums meet the other matrix's in LDS.
+#define FIN_ROWS 128
+__device__ void k2_shared_act(const K2Args &a, int w)
+{
+    const int T = a.T, P = a.nparts, NG = FIN_ROWS / 8;
+    const int nitem = 2 * T * NG;                      // <= NT (T <= 8)
+    float *fl = (float *)dyn_lds;
+    const int f = threadIdx.x;
+    if (f < nitem) {
+        const int m = f / (T * NG), rest = f % (T * NG), tok = rest % T;
+        const int r8 = w * NG + rest / T;
+        const rsrc_t pr = make_rsrc(a.shp, (uint32_t)P * 2u * T * a.SI * 4u);
+        u32x4 v[K3X_SHARED_PARTS][2];
+#pragma unroll
+        for (int p = 0; p < K3X_SHARED_PARTS; p++) {
+            const uint32_t o = p < P
+                ? (uint32_t)((((size_t)(p * 2 + m) * T + tok) * a.SI + r8 * 8) * 4) : K3X_OOB;
+            v[p][0] = bload16(pr, o);
+            v[p][1] = bload16(pr, o + 16u);
+        }
+        float sum[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) sum[k] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < K3X_SHARED_PARTS; p++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                sum[k] += __uint_as_float(v[p][0][k]);
+                sum[4 + k] += __uint_as_float(v[p][1][k]);
+            }
+#pragma unroll
+        for (int k = 0; k < 8; k++) fl[f * 8 + k] = sum[k];
+    }
+    __syncthreads();
+    if (f < nitem / 2) {
+        const int tok = f % T, r8 = w * NG + f / T;           // rows 8*r8 .. 8*r8+7
+        const int q = r8 >> 4, kq = (r8 >> 2) & 3, t = r8 & 3;
+        float y[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) y[k] = swiglu(fl[f * 8 + k], fl[(nitem / 2 + f) * 8 + k]);
+        const size_t e = (((size_t)q * 4 + t) * 4 + kq) * (2 * T) + 2 * tok;
+        *(u32x4 *)(a.shB + e * 8) = bfrag_of(y, 0);
+        *(u32x4 *)(a.shB + (e + 1) * 8) = bfrag_of(y, 1);
+    }
+}
 
 // Gate and up products of 16 rows of one unique expert: four waves on interleaved
 // super-quads; SwiGLU, the token's routing weight for this expert (0 where the token did
@@ -599,11 +567,16 @@ template <bool EXACT, bool LDSB>
 __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
 {
     __shared__ float lds[(NT / WAVE - 1) * 8 * WAVE];
+    if ((int)blockIdx.x < a.n_fin) {
+        k2_shared_act(a, blockIdx.x);
+        return;
+    }
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int NW = NT / WAVE;
     const int NC = 2 * a.T;
     const int nTiles = a.I >> 4;
-    const int u = blockIdx.x / nTiles, rt = blockIdx.x % nTiles;
+    const int blk = blockIdx.x - a.n_fin;
+    const int u = blk / nTiles, rt = blk % nTiles;
     if (u >= a.route->nu) return;
     const int nS = ((a.H >> 7) + 3) >> 2;
     const uint32_t bbytes = (uint32_t)nS * 1024u * NC;
@@ -663,15 +636,26 @@ struct K3Args {
     size_t         expert_bytes, down_off;
     const k3x_route *route;
     const uint16_t *actB;
-    const float   *ysh;            // shared output, or NULL
+    const uint16_t *sh_down;       // shared expert down matrix (tiled bf16), or NULL
+    const uint16_t *shB;           // compact B set of the shared activation
+    int            SI;
     float         *out;
     const float   *resid;
     int            T, H, I, K;
     uint32_t       lds_bytes;      // dynamic LDS of the launch
 };
 
-// Down products of 16 output rows over every (unique expert, super-quad) item, eight
-// waves interleaved, into one accumulator set.
+// A bf16 quad of the shared down matrix with its B fragments (read from the shared
+// activation's B set in global memory, which every workgroup reads: an L2 hit).
+struct QBB {
+    QB    a;
+    u32x4 b[4];
+};
+
+// Down products of 16 output rows over every (unique expert, super-quad) item, then the
+// shared expert's down product over its bf16 quads, eight waves interleaved, into one
+// accumulator set.  Both rings are primed first, so the shared quads' loads are in
+// flight while the routed items stream.
 template <bool EXACT, bool LDSB>
 __device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int lane, int nu)
 {
@@ -699,12 +683,29 @@ __device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int
         st.commit(NT3);
         __syncthreads();
     }
+    const int nQS = a.sh_down ? a.SI >> 7 : 0;
+    const int cs = strided_count(wave, NW, nQS);
+    const rsrc_t rw = make_rsrc(a.sh_down + (size_t)rt * 16 * a.SI, (uint32_t)nQS * 4096u);
+    const rsrc_t rb = make_rsrc(a.shB, (uint32_t)nQS * 256u * NC);
+    const int n = lane & 15, kq = lane >> 4;
+    const uint32_t boff = (uint32_t)((kq * NC + (n < NC ? n : 0)) * 16);
+    QBB ring2[2];
+    auto ld2 = [&](int i, int k) AI {
+        const bool on = k < cs;
+        const int q = wave + NW * k;
+        qb_load(ring2[i].a, rw, on ? (uint32_t)q * 4096u : K3X_OOB, lane);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            ring2[i].b[t] = bload16(rb, on ? boff + (uint32_t)(q * 256 * NC + t * 64 * NC) : K3X_OOB);
+    };
+    ring_prime<2>(ld2);
     BFrag<LDSB> bf;
     bf.init(a.actB, (uint32_t)(a.T * a.K) * slot, NC, lane);
     ring_loop<2>(cnt, ld, [&](int i, int k) AI {
         const int it = wave + NW * k;
         sq_mfma<EXACT, LDSB>(d, ring[i], bf, (uint32_t)(it / nSI) * slot, it % nSI);
     });
+    ring_loop<2>(cs, ld2, [&](int i, int k) AI { qb_mfma(d, ring2[i].a, ring2[i].b); });
 }
 
 template <bool EXACT>
@@ -725,8 +726,7 @@ __global__ void __launch_bounds__(NT3) k3_down(K3Args a)
     per_token<4>(acc, 2 * a.T, lane, [&](int r0, int tok, const float (&v)[4]) AI {
         for (int i = 0; i < 4; i++) {
             const size_t o = (size_t)tok * a.H + rt * 16 + r0 + i;
-            const float ys = a.ysh ? v[i] + a.ysh[o] : v[i];
-            a.out[o] = a.resid ? a.resid[o] + ys : ys;
+            a.out[o] = a.resid ? a.resid[o] + v[i] : v[i];
         }
     });
 }
@@ -742,10 +742,9 @@ static int record(k3x_moe_layer *L, int i, hipStream_t s)
 }
 
 template <int NE>
-static void launch_k1b(const KSArgs &as, bool ldsb, dim3 grid, size_t lds, hipStream_t s)
+static void launch_k1b(const K1bArgs &a, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (ldsb) hipLaunchKernelGGL((k1b_select_shdown<NE, true>), grid, dim3(NT), lds, s, as);
-    else      hipLaunchKernelGGL((k1b_select_shdown<NE, false>), grid, dim3(NT), 0, s, as);
+    hipLaunchKernelGGL((k1b_select_shared<NE>), grid, dim3(NT1), lds, s, a);
 }
 
 extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x_dtype,
@@ -755,6 +754,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     hipStream_t s = (hipStream_t)stream;
     const int H = c->hidden, I = c->moe_inter, NC = 2 * T;
     const int nQ = H / 128, nS = (nQ + 3) / 4, nSI = (I / 128 + 3) / 4;
+    const int P = k3x_shared_parts(nQ);
     int rc;
 
     K1Args a1;
@@ -762,31 +762,27 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a1.T = T; a1.H = H; a1.E = c->n_experts;
     a1.score = L->score; a1.choice = L->choice; a1.xB = L->xB;
     a1.n_rwg = (c->n_experts + NT1 / WAVE / RWAVES - 1) / (NT1 / WAVE / RWAVES);
-    a1.sh_gate = L->sh_gate; a1.sh_up = L->sh_up; a1.SI = L->SI; a1.shB = L->shB;
-    const uint32_t xset = (uint32_t)nQ * 256u * NC;
-    const int n_sh = L->SI > 0 ? L->SI / 16 : 0;
     if ((rc = record(L, 0, s))) return rc;
-    if (xset <= STAGE_MAX)
-        hipLaunchKernelGGL(k1_router_shared<true>, dim3(a1.n_rwg + n_sh), dim3(NT1), xset, s, a1);
-    else
-        hipLaunchKernelGGL(k1_router_shared<false>, dim3(a1.n_rwg + n_sh), dim3(NT1), 0, s, a1);
+    hipLaunchKernelGGL(k1_router_bset, dim3(a1.n_rwg), dim3(NT1), 0, s, a1);
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 1, s))) return rc;
 
-    KSArgs as;
+    K1bArgs ab;
+    KSArgs &as = ab.ks;
     as.score = L->score; as.choice = L->choice; as.E = c->n_experts; as.K = c->topk;
     as.renorm = c->moe_renorm; as.routed_scale = c->routed_scale; as.route = L->route;
-    as.idx = L->idx; as.wt = L->wt; as.uidx = idx; as.uwt = wt; as.T = T; as.H = H;
-    as.sh_down = L->sh_down; as.shB = L->shB; as.ysh = L->ysh; as.SI = L->SI;
-    const dim3 gs(1 + (L->SI > 0 ? H / 16 : 0));
-    const uint32_t shset = (uint32_t)(L->SI / 128) * 256u * NC;
-    const bool ldsb = shset <= STAGE_MAX;
-    const size_t ls = ldsb ? shset : 0;
-    if (c->n_experts <= 128)      launch_k1b<2>(as, ldsb, gs, ls, s);
-    else if (c->n_experts <= 256) launch_k1b<4>(as, ldsb, gs, ls, s);
-    else if (c->n_experts <= 384) launch_k1b<6>(as, ldsb, gs, ls, s);
-    else if (c->n_experts <= 512) launch_k1b<8>(as, ldsb, gs, ls, s);
-    else                          launch_k1b<16>(as, ldsb, gs, ls, s);
+    as.idx = L->idx; as.wt = L->wt; as.uidx = idx; as.uwt = wt; as.T = T;
+    ab.xB = L->xB; ab.T = T; ab.H = H;
+    ab.sh_gate = L->sh_gate; ab.sh_up = L->sh_up; ab.SI = L->SI;
+    ab.nparts = P; ab.shp = L->shp;
+    const uint32_t slice = (uint32_t)((nQ + P - 1) / P) * 256u * NC;   /* <= STAGE_MAX */
+    const int n_sh = L->SI > 0 ? (L->SI / 16) * P : 0;
+    const dim3 gb(1 + n_sh);
+    if (c->n_experts <= 128)      launch_k1b<2>(ab, gb, slice, s);
+    else if (c->n_experts <= 256) launch_k1b<4>(ab, gb, slice, s);
+    else if (c->n_experts <= 384) launch_k1b<6>(ab, gb, slice, s);
+    else if (c->n_experts <= 512) launch_k1b<8>(ab, gb, slice, s);
+    else                          launch_k1b<16>(ab, gb, slice, s);
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 2, s))) return rc;
 
@@ -794,20 +790,25 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a2.experts = L->experts; a2.expert_bytes = L->expert_bytes;
     a2.gate_off = L->gate_off; a2.up_off = L->up_off; a2.route = L->route;
     a2.xB = L->xB; a2.actB = L->actB; a2.T = T; a2.H = H; a2.I = I;
+    a2.n_fin = L->SI > 0 ? L->SI / FIN_ROWS : 0;
+    a2.SI = L->SI; a2.nparts = P; a2.shp = L->shp; a2.shB = L->shB;
+    const int n_routed = T * c->topk * (I / 16);
     const uint32_t xfp4 = (uint32_t)nS * 1024u * NC;
+    const uint32_t fin = 2u * NC * (FIN_ROWS / 8) * 8u * 4u;
     const bool ex2 = (L->special & 3) != 0, st2 = xfp4 <= STAGE_MAX;
-    const dim3 g2(T * c->topk * (I / 16));
-    if (ex2 && st2)  hipLaunchKernelGGL((k2_gateup<true, true>), g2, dim3(NT), xfp4, s, a2);
-    else if (ex2)    hipLaunchKernelGGL((k2_gateup<true, false>), g2, dim3(NT), 0, s, a2);
-    else if (st2)    hipLaunchKernelGGL((k2_gateup<false, true>), g2, dim3(NT), xfp4, s, a2);
-    else             hipLaunchKernelGGL((k2_gateup<false, false>), g2, dim3(NT), 0, s, a2);
+    const size_t l2 = (st2 && xfp4 > fin) ? xfp4 : fin;
+    const dim3 g2(a2.n_fin + n_routed);
+    if (ex2 && st2)  hipLaunchKernelGGL((k2_gateup<true, true>), g2, dim3(NT), l2, s, a2);
+    else if (ex2)    hipLaunchKernelGGL((k2_gateup<true, false>), g2, dim3(NT), l2, s, a2);
+    else if (st2)    hipLaunchKernelGGL((k2_gateup<false, true>), g2, dim3(NT), l2, s, a2);
+    else             hipLaunchKernelGGL((k2_gateup<false, false>), g2, dim3(NT), l2, s, a2);
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 3, s))) return rc;
 
     K3Args a3;
     a3.experts = L->experts; a3.expert_bytes = L->expert_bytes; a3.down_off = L->down_off;
     a3.route = L->route; a3.actB = L->actB;
-    a3.ysh = L->SI > 0 ? L->ysh : NULL;
+    a3.sh_down = L->SI > 0 ? L->sh_down : NULL; a3.shB = L->shB; a3.SI = L->SI;
     a3.out = out; a3.resid = resid; a3.T = T; a3.H = H; a3.I = I; a3.K = c->topk;
     const uint32_t slot = (uint32_t)nSI * 1024u * NC;
     const size_t all = (size_t)T * c->topk * slot;

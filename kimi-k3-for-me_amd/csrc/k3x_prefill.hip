@@ -151,16 +151,14 @@ __global__ void __launch_bounds__(PF_NT) pf_topk(PfTopkArgs a)
 {
     __shared__ int      s_idx[PF_NT / WAVE][K3X_MAX_TOPK];
     __shared__ float    s_w[PF_NT / WAVE][K3X_MAX_TOPK];
-    __shared__ uint64_t s_key[PF_NT / WAVE][K3X_MAX_TOPK];
-    __shared__ int      s_e[PF_NT / WAVE][K3X_MAX_TOPK];
-    __shared__ float    s_sc[PF_NT / WAVE][K3X_MAX_TOPK];
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int t = blockIdx.x * (PF_NT / WAVE) + wave;
     if (t >= a.T) return;
     const rsrc_t cr = make_rsrc(a.choice, (uint32_t)((size_t)a.T * a.E * 4));
     const rsrc_t sr = make_rsrc(a.score, (uint32_t)((size_t)a.T * a.E * 4));
     wave_topk<NE>(cr, sr, (uint32_t)((size_t)t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
-                  s_idx[wave], s_w[wave], s_key[wave], s_e[wave], s_sc[wave], lane);
+                  s_idx[wave], s_w[wave], lane);
+    __builtin_amdgcn_wave_barrier();
     if (lane < a.K) {
         const size_t o = (size_t)t * a.K + lane;
         const int e = s_idx[wave][lane];

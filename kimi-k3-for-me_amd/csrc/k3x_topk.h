@@ -27,89 +27,92 @@ __device__ __forceinline__ float bload_f32(rsrc_t r, uint32_t off)
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
-// One token's top-k by one wave, equal to the reference's repeated maximum
-// (k3_ops.c:1700-1708): the K largest choices in descending order, the lower index first
-// among equal values, NaN and -inf never taken (a pick with nothing left gives index 0,
-// weight 0).  A 32-step bitwise search with ballot counts finds the k-th largest key;
-// the k selected are then ranked.  Weights are the unbiased scores, renormalised through
-// a double sum and a float reciprocal, then scaled (:1710-1716).  Results in s_idx/s_w.
-// NE: 64-expert chunks held per lane.
+// Maximum of an unsigned value over the wave: DPP steps within quads and rows, then row
+// broadcasts across rows (lane 63 ends with the total), then a read of lane 63.  Lanes
+// that a step does not write take 0, the identity.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_max(uint32_t v)
+{
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, false);
+    return o > v ? o : v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+    v = dpp_max<0xB1, 0xF>(v);      // quad_perm [1,0,3,2]
+    v = dpp_max<0x4E, 0xF>(v);      // quad_perm [2,3,0,1]
+    v = dpp_max<0x124, 0xF>(v);     // row_ror:4
+    v = dpp_max<0x128, 0xF>(v);     // row_ror:8: every lane holds its row's maximum
+    v = dpp_max<0x142, 0xA>(v);     // row_bcast:15 into rows 1 and 3
+    v = dpp_max<0x143, 0xC>(v);     // row_bcast:31 into rows 2 and 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// One token's top-k by one wave, the reference's repeated maximum (k3_ops.c:1700-1708):
+// K rounds, each taking the largest remaining choice with the lower index first among
+// equal values.  Lane l holds experts l*NE .. l*NE+NE-1 (so a lower lane holds lower
+// indices) with their choice keys and scores, loaded once.  A round: each lane's best key
+// (the lowest of its indices among equals), the wave maximum, and the lowest lane holding
+// it by a ballot; that lane's expert and score are read as wave-uniform values and its key
+// cleared.  NaN and -inf are never taken; a round with nothing left gives index 0, weight
+// 0.  Weights are the unbiased scores, renormalised through a double sum in slot order and
+// a float reciprocal, then scaled (:1710-1716).  Results in s_idx/s_w (K entries).
 template <int NE>
 __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, int renorm,
-                          float routed_scale, int *s_idx, float *s_w, uint64_t *s_key,
-                          int *s_e, float *s_sc, int lane)
+                          float routed_scale, int *s_idx, float *s_w, int lane)
 {
     uint32_t key[NE];
-    float sco[NE];
+    float sc[NE];
 #pragma unroll
     for (int c = 0; c < NE; c++) {
-        const int e = lane + WAVE * c;
-        const uint32_t off = row_off + 4u * (uint32_t)e;
-        const float v = bload_f32(cr, e < E ? off : K3X_OOB);
-        sco[c] = bload_f32(sr, e < E ? off : K3X_OOB);
-        key[c] = e < E ? choice_key(v) : 0u;
+        const int e = lane * NE + c;
+        const uint32_t o = e < E ? row_off + 4u * (uint32_t)e : K3X_OOB;
+        const float v = bload_f32(cr, o);
+        sc[c] = bload_f32(sr, o);
+        const uint32_t k = choice_key(v);
+        key[c] = (e < E && k > K_NEG_INF) ? k : 0u;
     }
-    int nvalid = 0;
+    int mine_e = 0;               // lane j keeps round j's expert and score
+    float mine_s = 0.0f;
+    for (int j = 0; j < K; j++) {
+        uint32_t bk = key[0];
+        int bc = 0;
 #pragma unroll
-    for (int c = 0; c < NE; c++) nvalid += __popcll(__ballot(key[c] > K_NEG_INF));
-    const int ke = min(K, nvalid);
-    uint32_t tau = 0xFFFFFFFFu;
-    if (ke > 0) {
-        tau = 0u;
-        for (int b = 31; b >= 0; b--) {
-            const uint32_t cand = tau | (1u << b);
-            int cnt = 0;
-#pragma unroll
-            for (int c = 0; c < NE; c++) cnt += __popcll(__ballot(key[c] >= cand));
-            if (cnt >= ke) tau = cand;
+        for (int c = 1; c < NE; c++)
+            if (key[c] > bk) { bk = key[c]; bc = c; }
+        const uint32_t m = wave_max_u32(bk);
+        const uint64_t holders = __ballot(m != 0u && bk == m);
+        if (holders == 0ull) {                  // nothing left (uniform)
+            if (lane == j) { mine_e = 0; mine_s = 0.0f; }
+            continue;
         }
-    }
-    int ngt = 0;
+        const int w = (int)__builtin_ctzll(holders);
+        float bs = sc[0];
 #pragma unroll
-    for (int c = 0; c < NE; c++) ngt += __popcll(__ballot(key[c] > tau));
-    int need = ke - ngt;                    // ties at tau, taken in ascending index
-    int base = 0;
+        for (int c = 1; c < NE; c++)
+            if (c == bc) bs = sc[c];
+        const int wc = __builtin_amdgcn_readlane(bc, w);
+        const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs), w));
+        if (lane == w) {
 #pragma unroll
-    for (int c = 0; c < NE; c++) {
-        const uint64_t eq = __ballot(ke > 0 && key[c] == tau);
-        const int take = min(need, (int)__popcll(eq));
-        need -= take;
-        const bool sel = (ke > 0) && (key[c] > tau || (key[c] == tau && lanes_below(eq) < take));
-        const uint64_t sm = __ballot(sel);
-        if (sel) {
-            const int pos = base + lanes_below(sm);
-            const int e = lane + WAVE * c;
-            s_key[pos] = ((uint64_t)key[c] << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
-            s_e[pos] = e;
-            s_sc[pos] = sco[c];
+            for (int c = 0; c < NE; c++)
+                if (c == bc) key[c] = 0u;
         }
-        base += (int)__popcll(sm);
+        if (lane == j) { mine_e = w * NE + wc; mine_s = ws; }
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    if (lane < ke) {
-        const uint64_t my = s_key[lane];
-        int rank = 0;
-        for (int i = 0; i < ke; i++) rank += s_key[i] > my;
-        s_idx[rank] = s_e[lane];
-        s_w[rank] = s_sc[lane];
-    } else if (lane < K) {
-        s_idx[lane] = 0;
-        s_w[lane] = 0.0f;
+    float wgt = mine_s;
+    if (renorm && K > 1) {
+        double sum = 0.0;
+        for (int j = 0; j < K; j++)
+            sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine_s), j));
+        const float inv = (float)(1.0 / (sum + 1e-20));
+        wgt *= inv;
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    if (lane == 0) {
-        if (renorm && K > 1) {
-            double sum = 0.0;
-            for (int j = 0; j < K; j++) sum += (double)s_w[j];
-            const float inv = (float)(1.0 / (sum + 1e-20));
-            for (int j = 0; j < K; j++) s_w[j] *= inv;
-        }
-        for (int j = 0; j < K; j++) s_w[j] *= routed_scale;
+    wgt *= routed_scale;
+    if (lane < K) {
+        s_idx[lane] = mine_e;
+        s_w[lane] = wgt;
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
 }
 
 #endif

@@ -46,19 +46,19 @@ def load_k3x():
     return mod
 
 
-KERNELS = ["k1_router_bset", "k1b_select_shared", "k2_gateup", "k3_down"]
+KERNELS = ["k1_router_bset", "k1s_select", "k2_gateup", "k3_down"]
 
 
 def kernel_bytes(U, T):
     """Algorithmic HBM bytes per launch of the four decode kernels (each weight byte
-    once; activations included): k1 the router weights, k1b the shared expert's gate/up
-    weights, k2 the unique experts' gate/up weights, k3 the unique experts' and the
-    shared expert's down weights and the output."""
+    once; activations included): k1 the router weights, k1s the scores, k2 the shared expert's and the
+    unique experts' gate/up weights, k3 the unique experts' and the shared expert's down
+    weights and the output."""
     k1 = B_ROUTER + T * H * 2
-    k1b = 2 * SI * H * 2
-    k2 = U * 2 * (I * H // 2 + I * H // 32)
+    k1s = 2 * T * E * 4
+    k2 = 2 * SI * H * 2 + U * 2 * (I * H // 2 + I * H // 32)
     k3 = U * (H * I // 2 + H * I // 32) + H * SI * 2 + T * H * 4
-    return dict(zip(KERNELS, (k1, k1b, k2, k3)))
+    return dict(zip(KERNELS, (k1, k1s, k2, k3)))
 
 
 PREFILL_T = 2048

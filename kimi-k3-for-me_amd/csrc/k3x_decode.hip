@@ -1,21 +1,17 @@
 // k3x_decode.hip - the decode path of the MoE block (T <= 8 tokens), four launches:
 //
 //   k1_router_bset    router logits in double, sigmoid, +bias (k3_router, k3_ops.c:1624-
-//                     1694) for every expert, and x's B fragments for the products.
-//   k1b_select_shared workgroup 0 selects each token's top-k (:1700-1716) and lists the
-//                     unique experts (the dedup of moe_prefill_routed, :2067-2081) while
-//                     the others stream the shared expert's gate/up weights (moe_shared,
-//                     :1848-1857) in parts of K.
-//   k2_gateup         the shared activation: the parts added, SwiGLU (k3_situ_glu at 2^64
-//                     betas, :148-161), in the first workgroups; then each unique expert's
-//                     gate/up products (k3_matmul_mxfp4, :3323-3776) with SwiGLU and the
-//                     routing weight folded in.
+//                     1694) for every expert, and x's B fragments for the products.  The
+//                     router runs alone, so its 11 MB arrive first.
+//   k1s_select        one workgroup selects each token's top-k (:1700-1716) and lists the
+//                     unique experts (the dedup of moe_prefill_routed, :2067-2081).
+//   k2_gateup         first the shared expert's gate/up products over the full K with
+//                     SwiGLU (moe_shared, :1848-1857; k3_situ_glu at 2^64 betas, :148-161);
+//                     then each unique expert's gate/up products (k3_matmul_mxfp4,
+//                     :3323-3776) with SwiGLU and the routing weight folded in.
 //   k3_down           each unique expert's down product and the shared expert's (:1858)
 //                     into one accumulator set per 16 output rows (the weighted combine,
 //                     :1941-1942, plus the shared result, :1859), and an optional residual.
-//
-// The router runs alone so that its 11 MB arrive first; the selection then overlaps the
-// shared expert's stream.
 //
 // Each weight byte is read once per call.  Weights are dequantised in registers
 // (E2M1 x 2^(s-127) is exact in bf16) and multiplied on v_mfma_f32_16x16x32_bf16 against
@@ -34,7 +30,7 @@
 #include "k3x_device.h"
 #include "k3x_topk.h"
 
-#define NT1 256     // k1 / k1b workgroup: 4 waves
+#define NT1 256     // k1 workgroup: 4 waves
 #define NT  256     // k2 workgroup: 4 waves
 #define NT3 512     // k3 workgroup: 8 waves
 #define STAGE_MAX 65536u   // largest B set staged in LDS (bytes)
@@ -272,72 +268,121 @@ struct KSArgs {
     int            T;
 };
 
-// Routing of every token (one wave per token), then the unique experts in first-seen
-// order over (token, slot) and each one's weight per token: the sum of its slots' weights
-// (0 where not chosen; a slot repeated by a round that found nothing adds 0).  The list
-// is built in parallel: each expert's first item by an LDS minimum, the first items'
-// slots by ballots, then one weight per (slot, token).
-template <int NE>
-__device__ void ks_select(const KSArgs &a)
+// A workgroup's view of the routing, in LDS.
+struct KSLds {
+    int   idx[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
+    float w[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
+    int   first[1024];                          // per expert: its first (token, slot) item
+    int   uq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];  // unique experts, first-seen order
+    int   wc[NT / WAVE];
+};
+
+// Token t's weight for expert e: the sum of its slots' weights for e (0 where not
+// chosen; a slot repeated by a round that found nothing adds 0).
+__device__ __forceinline__ float ks_weight(const KSLds &l, int K, int t, int e)
 {
-    static_assert(NT1 == NT, "the selection runs in a k1b workgroup");
+    float w = 0.0f;
+    for (int j = 0; j < K; j++)
+        if (l.idx[t][j] == e) w += l.w[t][j];
+    return w;
+}
+
+// Routing of every token (one wave per token), then the unique experts in first-seen
+// order over (token, slot), built in parallel: each expert's first item by an LDS
+// minimum, the first items' slots by ballots.  Returns the number of unique experts.
+// With `publish`, also writes the indices and weights, the unique list and each unique
+// expert's weight per token for k2/k3.
+template <int NE>
+__device__ int ks_route(const KSArgs &a, KSLds &l, bool publish)
+{
     constexpr int NW = NT / WAVE;
-    __shared__ int      s_idx[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
-    __shared__ float    s_w[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
-    __shared__ int      s_first[1024];
-    __shared__ int      s_uq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];
-    __shared__ int      s_wc[NW];
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const rsrc_t cr = make_rsrc(a.choice, (uint32_t)(a.T * a.E * 4));
     const rsrc_t sr = make_rsrc(a.score, (uint32_t)(a.T * a.E * 4));
+    if (a.T == 1) {
+        // one token, all in wave 0 and its registers: lane j holds slot j; the unique
+        // experts are the slots whose expert no lower slot holds, each with the sum of
+        // its slots' weights in slot order
+        if (wave != 0) return 0;
+        int ex;
+        float w;
+        wave_topk<NE, 0>(cr, sr, 0u, a.E, a.K, a.renorm, a.routed_scale, l.idx[0], l.w[0],
+                         lane, &ex, &w);
+        const bool on = lane < a.K;
+        bool first = on;
+        float wsum = 0.0f;
+        for (int i = 0; i < a.K; i++) {
+            const int ei = __builtin_amdgcn_readlane(ex, i);
+            const float wi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), i));
+            first = first && !(i < lane && ei == ex);
+            wsum += ei == ex ? wi : 0.0f;
+        }
+        const uint64_t fm = __ballot(first);
+        const int nu = __popcll(fm);
+        if (first) l.uq[lanes_below(fm)] = ex;
+        if (publish) {
+            if (on) {
+                a.idx[lane] = ex;
+                a.wt[lane] = w;
+                if (a.uidx) { a.uidx[lane] = ex; a.uwt[lane] = w; }
+            }
+            if (first) {
+                const int slot = lanes_below(fm);
+                a.route->uniq[slot] = ex;
+                a.route->wtok[slot][0] = wsum;
+                for (int t = 1; t < K3X_DECODE_MAX_T; t++) a.route->wtok[slot][t] = 0.0f;
+            }
+            if (lane == 0) a.route->nu = nu;
+        }
+        return nu;
+    }
     for (int t = wave; t < a.T; t += NW)
-        wave_topk<NE>(cr, sr, (uint32_t)(t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
-                      s_idx[t], s_w[t], lane);
-    for (int e = threadIdx.x; e < a.E; e += NT) s_first[e] = 0x7FFFFFFF;
+        wave_topk<NE, 0>(cr, sr, (uint32_t)(t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
+                      l.idx[t], l.w[t], lane);
+    for (int e = threadIdx.x; e < a.E; e += NT) l.first[e] = 0x7FFFFFFF;
     __syncthreads();
     const int TK = a.T * a.K;
     for (int i = threadIdx.x; i < TK; i += NT) {
         const int t = i / a.K, j = i % a.K;
-        const int ex = s_idx[t][j];
-        a.idx[i] = ex;
-        a.wt[i] = s_w[t][j];
-        if (a.uidx) { a.uidx[i] = ex; a.uwt[i] = s_w[t][j]; }
-        atomicMin(&s_first[ex], i);
+        const int ex = l.idx[t][j];
+        if (publish) {
+            a.idx[i] = ex;
+            a.wt[i] = l.w[t][j];
+            if (a.uidx) { a.uidx[i] = ex; a.uwt[i] = l.w[t][j]; }
+        }
+        atomicMin(&l.first[ex], i);
     }
     __syncthreads();
     int base = 0;
     for (int c0 = 0; c0 < TK; c0 += NT) {          // uniform trip count
         const int i = c0 + threadIdx.x;
-        const int ex = i < TK ? s_idx[i / a.K][i % a.K] : 0;
-        const bool first = i < TK && s_first[ex] == i;
+        const int ex = i < TK ? l.idx[i / a.K][i % a.K] : 0;
+        const bool first = i < TK && l.first[ex] == i;
         const uint64_t m = __ballot(first);
-        if (lane == 0) s_wc[wave] = __popcll(m);
+        if (lane == 0) l.wc[wave] = __popcll(m);
         __syncthreads();
         int off = base, tot = 0;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            off += w < wave ? s_wc[w] : 0;
-            tot += s_wc[w];
+            off += w < wave ? l.wc[w] : 0;
+            tot += l.wc[w];
         }
         if (first) {
             const int slot = off + lanes_below(m);
-            s_uq[slot] = ex;
-            a.route->uniq[slot] = ex;
+            l.uq[slot] = ex;
+            if (publish) a.route->uniq[slot] = ex;
         }
         base += tot;
         __syncthreads();
     }
-    const int nu = base;
-    for (int f = threadIdx.x; f < nu * K3X_DECODE_MAX_T; f += NT) {
-        const int slot = f / K3X_DECODE_MAX_T, t = f % K3X_DECODE_MAX_T;
-        const int ex = s_uq[slot];
-        float w = 0.0f;
-        if (t < a.T)
-            for (int j = 0; j < a.K; j++)
-                if (s_idx[t][j] == ex) w += s_w[t][j];
-        a.route->wtok[slot][t] = w;
+    if (publish) {
+        for (int f = threadIdx.x; f < base * K3X_DECODE_MAX_T; f += NT) {
+            const int slot = f / K3X_DECODE_MAX_T, t = f % K3X_DECODE_MAX_T;
+            a.route->wtok[slot][t] = t < a.T ? ks_weight(l, a.K, t, l.uq[slot]) : 0.0f;
+        }
+        if (threadIdx.x == 0) a.route->nu = base;
     }
-    if (threadIdx.x == 0) a.route->nu = nu;
+    return base;
 }
 
 // ------------------------------------------------------------------ K1
@@ -417,7 +462,7 @@ __device__ void k1_router(const K1Args &a, float *lds)
     }
 }
 
-// Router logits of NT1 / WAVE / RWAVES experts, and a share of x's B set for k1b/k2.
+// Router logits of NT1 / WAVE / RWAVES experts, and a share of x's B set for k2.
 __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
 {
     __shared__ float lds[(NT1 / WAVE - 1) * 8 * WAVE];
@@ -427,46 +472,59 @@ __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
               blockIdx.x * NT1 + threadIdx.x, a.n_rwg * NT1);
 }
 
-// ------------------------------------------------------------------ K1b
-struct K1bArgs {
-    KSArgs         ks;             // the selection, in workgroup 0
-    const uint16_t *xB;
-    int            T, H;
+// One workgroup: the routing of every token and the unique experts, for k2 and k3.
+template <int NE>
+__global__ void __launch_bounds__(NT) k1s_select(KSArgs a)
+{
+    __shared__ KSLds ksl;
+    ks_route<NE>(a, ksl, true);
+}
+
+// ------------------------------------------------------------------ K2
+struct K2Args {
+    const k3x_route *route;        // from k1
+    const uint8_t *experts;
+    size_t         expert_bytes, gate_off, up_off;
+    const uint16_t *xB;            // compact B set of x over whole super-quads
+    uint16_t      *actB;           // one compact B set per unique expert (slot)
+    int            T, H, I;
+    int            n_sh;           // workgroups of the shared expert (the first ones)
     const uint16_t *sh_gate, *sh_up;
     int            SI;
-    int            nparts;         // parts of K the shared gate/up products are split into
-    float         *shp;            // [nparts][2][T][SI] partial gate and up sums, for k2
+    uint16_t      *shB;            // compact B set of the shared activation, for k3
 };
 
-// Shared expert gate and up partial products: workgroup sb takes rows 16*rt .. +15 over
-// quads [q0, q0+nq) of part `part` of K, that slice of x's B set staged in LDS; its four
-// waves take those quads interleaved (each wave both matrices of a quad, over one B
-// read).  The hi + lo columns are summed per token and the partial gate and up values
-// written to shp.
-__device__ void k1b_shared(const K1bArgs &a, float *lds, int sb)
+// Shared expert gate and up products for rows 16*rt .. +15 over the full K: four waves on
+// interleaved quads (each wave both matrices of a quad, over one B read); SwiGLU
+// (k3_situ_glu at 2^64 betas, k3_ops.c:148-161) per token and the activation's hi/lo B
+// fragments into shB.  These workgroups come first: they stream while the routed ones
+// work out the routing.
+template <bool LDSB>
+__device__ void k2_shared(const K2Args &a, float *lds, int rt)
 {
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
-    const int NW = NT1 / WAVE;
-    const int P = a.nparts, rt = sb / P, part = sb % P;
-    const int nQ = a.H >> 7, NC = 2 * a.T;
-    const int q0 = part * nQ / P, nq = (part + 1) * nQ / P - q0;
-    const int cnt = strided_count(wave, NW, nq);
+    const int NW = NT / WAVE;
+    const int nQ = a.H >> 7, nS = (nQ + 3) >> 2, NC = 2 * a.T;
+    const int cnt = strided_count(wave, NW, nQ);
     const uint32_t tbytes = (uint32_t)nQ * 4096u;
     const rsrc_t rg = make_rsrc(a.sh_gate + (size_t)rt * 16 * a.H, tbytes);
     const rsrc_t ru = make_rsrc(a.sh_up + (size_t)rt * 16 * a.H, tbytes);
+    const uint32_t bbytes = (uint32_t)nS * 1024u * NC;
     Stage<8> st;
-    st.issue(a.xB + (size_t)q0 * 128 * NC, (uint32_t)nq * 256u * NC, NT1);
+    if (LDSB) st.issue(a.xB, bbytes, NT);
     QB g[2], u[2];
     auto ld = [&](int i, int k) AI {
-        const uint32_t o = k < cnt ? (uint32_t)(q0 + wave + NW * k) * 4096u : K3X_OOB;
+        const uint32_t o = k < cnt ? (uint32_t)(wave + NW * k) * 4096u : K3X_OOB;
         qb_load(g[i], rg, o, lane);
         qb_load(u[i], ru, o, lane);
     };
     ring_prime<2>(ld);
-    st.commit(NT1);
-    __syncthreads();
-    BFrag<true> bf;
-    bf.init(nullptr, 0u, NC, lane);
+    if (LDSB) {
+        st.commit(NT);
+        __syncthreads();
+    }
+    BFrag<LDSB> bf;
+    bf.init(a.xB, bbytes, NC, lane);
     f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
     ring_loop<2>(cnt, ld, [&](int i, int k) AI {
         const int q = wave + NW * k;
@@ -477,87 +535,17 @@ __device__ void k1b_shared(const K1bArgs &a, float *lds, int sb)
         qb_mfma(du, u[i], b);
     });
     float acc[8] = {dg[0], dg[1], dg[2], dg[3], du[0], du[1], du[2], du[3]};
-    wave_sum_lds<8, NT1 / WAVE>(acc, lds, wave, lane);
+    wave_sum_lds<8, NT / WAVE>(acc, lds, wave, lane);
     if (wave != 0) return;
     per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&v)[8]) AI {
-        float *pg = a.shp + (((size_t)part * 2 + 0) * a.T + tok) * a.SI + rt * 16 + r0;
-        float *pu = a.shp + (((size_t)part * 2 + 1) * a.T + tok) * a.SI + rt * 16 + r0;
-        *(f32x4 *)pg = (f32x4){v[0], v[1], v[2], v[3]};
-        *(f32x4 *)pu = (f32x4){v[4], v[5], v[6], v[7]};
-    });
-}
-
-// Workgroup 0 selects every token's experts while the others stream the shared expert's
-// gate/up weights.
-template <int NE>
-__global__ void __launch_bounds__(NT1) k1b_select_shared(K1bArgs a)
-{
-    __shared__ float lds[(NT1 / WAVE - 1) * 8 * WAVE];
-    if (blockIdx.x == 0) ks_select<NE>(a.ks);
-    else                 k1b_shared(a, lds, blockIdx.x - 1);
-}
-
-// ------------------------------------------------------------------ K2
-struct K2Args {
-    const uint8_t *experts;
-    size_t         expert_bytes, gate_off, up_off;
-    const k3x_route *route;
-    const uint16_t *xB;            // compact B set of x over whole super-quads
-    uint16_t      *actB;           // one compact B set per unique expert (slot)
-    int            T, H, I;
-    int            n_fin;          // workgroups of the shared activation (the first ones)
-    int            SI, nparts;
-    const float   *shp;            // [nparts][2][T][SI] partial gate and up sums (k1)
-    uint16_t      *shB;            // compact B set of the shared activation, for k3
-};
-
-// The shared activation for rows 128*w .. 128*w+127: the parts of k1's gate and up sums
-// added in part order (all parts' loads issued at once; parts past nparts read as 0),
-// SwiGLU, and the hi/lo B fragments into shB (2 entries of 8 rows per token).  Item f:
-// matrix m, token, 8-row group r8; its sums meet the other matrix's in LDS.
-#define FIN_ROWS 128
-__device__ void k2_shared_act(const K2Args &a, int w)
-{
-    const int T = a.T, P = a.nparts, NG = FIN_ROWS / 8;
-    const int nitem = 2 * T * NG;                      // <= NT (T <= 8)
-    float *fl = (float *)dyn_lds;
-    const int f = threadIdx.x;
-    if (f < nitem) {
-        const int m = f / (T * NG), rest = f % (T * NG), tok = rest % T;
-        const int r8 = w * NG + rest / T;
-        const rsrc_t pr = make_rsrc(a.shp, (uint32_t)P * 2u * T * a.SI * 4u);
-        u32x4 v[K3X_SHARED_PARTS][2];
-#pragma unroll
-        for (int p = 0; p < K3X_SHARED_PARTS; p++) {
-            const uint32_t o = p < P
-                ? (uint32_t)((((size_t)(p * 2 + m) * T + tok) * a.SI + r8 * 8) * 4) : K3X_OOB;
-            v[p][0] = bload16(pr, o);
-            v[p][1] = bload16(pr, o + 16u);
+        for (int i = 0; i < 4; i++) {
+            uint32_t hi, lo;
+            split_bf16(swiglu(v[i], v[4 + i]), hi, lo);
+            const int r = rt * 16 + r0 + i;
+            a.shB[bfrag_off(r, 2 * tok, NC)] = (uint16_t)hi;
+            a.shB[bfrag_off(r, 2 * tok + 1, NC)] = (uint16_t)lo;
         }
-        float sum[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) sum[k] = 0.0f;
-#pragma unroll
-        for (int p = 0; p < K3X_SHARED_PARTS; p++)
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                sum[k] += __uint_as_float(v[p][0][k]);
-                sum[4 + k] += __uint_as_float(v[p][1][k]);
-            }
-#pragma unroll
-        for (int k = 0; k < 8; k++) fl[f * 8 + k] = sum[k];
-    }
-    __syncthreads();
-    if (f < nitem / 2) {
-        const int tok = f % T, r8 = w * NG + f / T;           // rows 8*r8 .. 8*r8+7
-        const int q = r8 >> 4, kq = (r8 >> 2) & 3, t = r8 & 3;
-        float y[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) y[k] = swiglu(fl[f * 8 + k], fl[(nitem / 2 + f) * 8 + k]);
-        const size_t e = (((size_t)q * 4 + t) * 4 + kq) * (2 * T) + 2 * tok;
-        *(u32x4 *)(a.shB + e * 8) = bfrag_of(y, 0);
-        *(u32x4 *)(a.shB + (e + 1) * 8) = bfrag_of(y, 1);
-    }
+    });
 }
 
 // Gate and up products of 16 rows of one unique expert: four waves on interleaved
@@ -567,22 +555,22 @@ template <bool EXACT, bool LDSB>
 __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
 {
     __shared__ float lds[(NT / WAVE - 1) * 8 * WAVE];
-    if ((int)blockIdx.x < a.n_fin) {
-        k2_shared_act(a, blockIdx.x);
+    if ((int)blockIdx.x < a.n_sh) {
+        k2_shared<LDSB>(a, lds, blockIdx.x);
         return;
     }
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int NW = NT / WAVE;
     const int NC = 2 * a.T;
     const int nTiles = a.I >> 4;
-    const int blk = blockIdx.x - a.n_fin;
+    const int blk = blockIdx.x - a.n_sh;
     const int u = blk / nTiles, rt = blk % nTiles;
     if (u >= a.route->nu) return;
+    const int e = a.route->uniq[u];
     const int nS = ((a.H >> 7) + 3) >> 2;
     const uint32_t bbytes = (uint32_t)nS * 1024u * NC;
     Stage<8> st;
     if (LDSB) st.issue(a.xB, bbytes, NT);
-    const int e = a.route->uniq[u];
     const uint32_t tb = (uint32_t)fp4_tile_bytes(a.H);
     const uint8_t *ex = a.experts + (size_t)e * a.expert_bytes + (size_t)rt * tb;
     const rsrc_t rg = make_rsrc(ex + a.gate_off, tb);
@@ -615,10 +603,9 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
         for (uint32_t o = (uint32_t)(a.I >> 7) * 256u * NC + threadIdx.x * 16u; o < slot; o += NT * 16u)
             *(u32x4 *)(dst + o) = (u32x4){0u, 0u, 0u, 0u};
     if (wave != 0) return;
-    const float *wtok = a.route->wtok[u];
     uint16_t *d16 = (uint16_t *)dst;
     per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&s)[8]) AI {
-        const float w = wtok[tok];
+        const float w = a.route->wtok[u][tok];
         for (int i = 0; i < 4; i++) {
             const float y = (w == 0.0f) ? 0.0f : w * swiglu(s[i], s[4 + i]);
             uint32_t hi, lo;
@@ -742,9 +729,9 @@ static int record(k3x_moe_layer *L, int i, hipStream_t s)
 }
 
 template <int NE>
-static void launch_k1b(const K1bArgs &a, dim3 grid, size_t lds, hipStream_t s)
+static void launch_sel(const KSArgs &a, hipStream_t s)
 {
-    hipLaunchKernelGGL((k1b_select_shared<NE>), grid, dim3(NT1), lds, s, a);
+    hipLaunchKernelGGL((k1s_select<NE>), dim3(1), dim3(NT), 0, s, a);
 }
 
 extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x_dtype,
@@ -754,7 +741,6 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     hipStream_t s = (hipStream_t)stream;
     const int H = c->hidden, I = c->moe_inter, NC = 2 * T;
     const int nQ = H / 128, nS = (nQ + 3) / 4, nSI = (I / 128 + 3) / 4;
-    const int P = k3x_shared_parts(nQ);
     int rc;
 
     K1Args a1;
@@ -767,37 +753,30 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 1, s))) return rc;
 
-    K1bArgs ab;
-    KSArgs &as = ab.ks;
+    KSArgs as;
     as.score = L->score; as.choice = L->choice; as.E = c->n_experts; as.K = c->topk;
     as.renorm = c->moe_renorm; as.routed_scale = c->routed_scale; as.route = L->route;
     as.idx = L->idx; as.wt = L->wt; as.uidx = idx; as.uwt = wt; as.T = T;
-    ab.xB = L->xB; ab.T = T; ab.H = H;
-    ab.sh_gate = L->sh_gate; ab.sh_up = L->sh_up; ab.SI = L->SI;
-    ab.nparts = P; ab.shp = L->shp;
-    const uint32_t slice = (uint32_t)((nQ + P - 1) / P) * 256u * NC;   /* <= STAGE_MAX */
-    const int n_sh = L->SI > 0 ? (L->SI / 16) * P : 0;
-    const dim3 gb(1 + n_sh);
-    if (c->n_experts <= 128)      launch_k1b<2>(ab, gb, slice, s);
-    else if (c->n_experts <= 256) launch_k1b<4>(ab, gb, slice, s);
-    else if (c->n_experts <= 384) launch_k1b<6>(ab, gb, slice, s);
-    else if (c->n_experts <= 512) launch_k1b<8>(ab, gb, slice, s);
-    else                          launch_k1b<16>(ab, gb, slice, s);
+    if (c->n_experts <= 128)      launch_sel<2>(as, s);
+    else if (c->n_experts <= 256) launch_sel<4>(as, s);
+    else if (c->n_experts <= 384) launch_sel<6>(as, s);
+    else if (c->n_experts <= 512) launch_sel<8>(as, s);
+    else                          launch_sel<16>(as, s);
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 2, s))) return rc;
 
     K2Args a2;
+    a2.route = L->route;
     a2.experts = L->experts; a2.expert_bytes = L->expert_bytes;
-    a2.gate_off = L->gate_off; a2.up_off = L->up_off; a2.route = L->route;
+    a2.gate_off = L->gate_off; a2.up_off = L->up_off;
     a2.xB = L->xB; a2.actB = L->actB; a2.T = T; a2.H = H; a2.I = I;
-    a2.n_fin = L->SI > 0 ? L->SI / FIN_ROWS : 0;
-    a2.SI = L->SI; a2.nparts = P; a2.shp = L->shp; a2.shB = L->shB;
+    a2.n_sh = L->SI > 0 ? L->SI / 16 : 0;
+    a2.sh_gate = L->sh_gate; a2.sh_up = L->sh_up; a2.SI = L->SI; a2.shB = L->shB;
     const int n_routed = T * c->topk * (I / 16);
     const uint32_t xfp4 = (uint32_t)nS * 1024u * NC;
-    const uint32_t fin = 2u * NC * (FIN_ROWS / 8) * 8u * 4u;
     const bool ex2 = (L->special & 3) != 0, st2 = xfp4 <= STAGE_MAX;
-    const size_t l2 = (st2 && xfp4 > fin) ? xfp4 : fin;
-    const dim3 g2(a2.n_fin + n_routed);
+    const size_t l2 = st2 ? xfp4 : 0;
+    const dim3 g2(a2.n_sh + n_routed);
     if (ex2 && st2)  hipLaunchKernelGGL((k2_gateup<true, true>), g2, dim3(NT), l2, s, a2);
     else if (ex2)    hipLaunchKernelGGL((k2_gateup<true, false>), g2, dim3(NT), l2, s, a2);
     else if (st2)    hipLaunchKernelGGL((k2_gateup<false, true>), g2, dim3(NT), l2, s, a2);

@@ -146,6 +146,9 @@ __device__ __forceinline__ int strided_count(int w, int st, int n) { return w < 
 // Weights: range-checked buffer loads with the non-temporal cache policy (they are read
 // once per call and should not displace the activations).
 #define CPOL_NT 2
+// device-coherent read (sc1): served from the level every XCD writes through to, never
+// from a line another XCD's L2 may hold stale
+#define CPOL_SC1 16
 __device__ __forceinline__ u32x4 wld16(rsrc_t r, uint32_t off)
 {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_NT);

@@ -48,17 +48,6 @@ extern "C" {
 #define K3X_DECODE_MAX_T 8       /* tokens per call on the decode path (2 columns each) */
 #define K3X_STAGE_MAX    65536   /* bytes of activation fragments a workgroup stages in LDS */
 #define K3X_MAX_TOPK     64      /* K3_MAX_TOPK, k3.h:857-864 */
-#define K3X_SHARED_PARTS 8       /* most parts of K the decode path splits the shared
-                                    expert's gate/up products into */
-
-/* Parts of K the decode path splits the shared gate/up products into: enough workgroups
- * to spread the shared weights over the chip, at least 8 quads of 128 per part. */
-static inline int k3x_shared_parts(int nQ)
-{
-    int p = nQ / 8;
-    return p < 1 ? 1 : (p > K3X_SHARED_PARTS ? K3X_SHARED_PARTS : p);
-}
-
 /* byte sizes of the tiled formats */
 static inline size_t k3x_fp4_tile_bytes(int K)
 {
@@ -122,7 +111,6 @@ struct k3x_moe_layer {
     uint16_t *xB;                 /* compact B set of x over whole super-quads of H */
     uint16_t *actB;               /* DECODE_MAX_T*K slots: B set of each unique expert's
                                      activation over whole super-quads of I */
-    float    *shp;                /* [SHARED_PARTS][2][DECODE_MAX_T][SI] partial sums */
     uint16_t *shB;                /* B set of the shared activation (SI/128 quads) */
     k3x_prefill_buf pf;
     size_t    bytes;

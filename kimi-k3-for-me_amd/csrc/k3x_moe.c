@@ -58,12 +58,6 @@ static int cfg_ok(const k3x_cfg *c)
     if (c->n_experts > 1024) return K3X_E_SHAPE;
     /* at least one token's shared activation fits the decode path's LDS set */
     if ((size_t)c->moe_inter * c->n_shared * 4 > K3X_STAGE_MAX) return K3X_E_SHAPE;
-    /* one part of K of the shared gate/up products: x's B set for 8 tokens fits LDS */
-    if (c->n_shared > 0) {
-        const int nQ = c->hidden / 128, P = k3x_shared_parts(nQ);
-        if ((size_t)((nQ + P - 1) / P) * 256 * 2 * K3X_DECODE_MAX_T > K3X_STAGE_MAX)
-            return K3X_E_SHAPE;
-    }
     return 0;
 }
 
@@ -107,8 +101,6 @@ static int layer_alloc(k3x_moe_layer *L)
         RCCHK(dmalloc((void **)&L->sh_up, k3x_bf16_matrix_bytes(L->SI, H), b));
         RCCHK(dmalloc((void **)&L->sh_down, k3x_bf16_matrix_bytes(H, L->SI), b));
         RCCHK(dmalloc((void **)&L->shB, (size_t)L->SI * 2 * K3X_DECODE_MAX_T * 2, b));
-        RCCHK(dmalloc((void **)&L->shp,
-                      (size_t)K3X_SHARED_PARTS * 2 * K3X_DECODE_MAX_T * L->SI * 4, b));
     }
     RCCHK(dmalloc((void **)&L->score, (size_t)K3X_DECODE_MAX_T * E * 4, b));
     RCCHK(dmalloc((void **)&L->choice, (size_t)K3X_DECODE_MAX_T * E * 4, b));
@@ -129,7 +121,7 @@ fail:
 static void layer_free(k3x_moe_layer *L)
 {
     if (!L) return;
-    void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shp, L->shB,
+    void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shB,
                  L->score, L->choice, L->idx, L->wt, L->route,
                  L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out};
     for (size_t i = 0; i < sizeof p / sizeof p[0]; i++)

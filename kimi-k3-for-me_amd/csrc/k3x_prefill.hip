@@ -156,7 +156,7 @@ __global__ void __launch_bounds__(PF_NT) pf_topk(PfTopkArgs a)
     if (t >= a.T) return;
     const rsrc_t cr = make_rsrc(a.choice, (uint32_t)((size_t)a.T * a.E * 4));
     const rsrc_t sr = make_rsrc(a.score, (uint32_t)((size_t)a.T * a.E * 4));
-    wave_topk<NE>(cr, sr, (uint32_t)((size_t)t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
+    wave_topk<NE, 0>(cr, sr, (uint32_t)((size_t)t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
                   s_idx[wave], s_w[wave], lane);
     __builtin_amdgcn_wave_barrier();
     if (lane < a.K) {

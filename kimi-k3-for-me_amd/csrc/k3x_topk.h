@@ -22,9 +22,10 @@ __device__ __forceinline__ int lanes_below(uint64_t m)
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+template <int CP>
 __device__ __forceinline__ float bload_f32(rsrc_t r, uint32_t off)
 {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CP));
 }
 
 // Maximum of an unsigned value over the wave: DPP steps within quads and rows, then row
@@ -51,35 +52,45 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 // One token's top-k by one wave, the reference's repeated maximum (k3_ops.c:1700-1708):
 // K rounds, each taking the largest remaining choice with the lower index first among
 // equal values.  Lane l holds experts l*NE .. l*NE+NE-1 (so a lower lane holds lower
-// indices) with their choice keys and scores, loaded once.  A round: each lane's best key
-// (the lowest of its indices among equals), the wave maximum, and the lowest lane holding
-// it by a ballot; that lane's expert and score are read as wave-uniform values and its key
-// cleared.  NaN and -inf are never taken; a round with nothing left gives index 0, weight
-// 0.  Weights are the unbiased scores, renormalised through a double sum in slot order and
-// a float reciprocal, then scaled (:1710-1716).  Results in s_idx/s_w (K entries).
-template <int NE>
+// indices) as 64-bit words key << 32 | ~index, loaded once (CP: the loads' cache
+// policy); in that order the entries still remaining after a round's winner W are exactly
+// those below W.  A round: each lane's largest word below the previous winner, the wave
+// maximum of their keys, the lowest lane holding it (a ballot: its word has the lowest
+// index among equal keys), and that lane's index and score read as wave-uniform values.
+// Branch-free.  NaN and -inf are never taken; a round with nothing left gives index 0,
+// weight 0.  Weights are the unbiased scores, renormalised through a double sum in slot
+// order and a float reciprocal, then scaled (:1710-1716).  Results in s_idx/s_w, and
+// lane j's (slot j's) in out_e/out_w when given.
+template <int NE, int CP>
 __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, int renorm,
-                          float routed_scale, int *s_idx, float *s_w, int lane)
+                          float routed_scale, int *s_idx, float *s_w, int lane,
+                          int *out_e = nullptr, float *out_w = nullptr)
 {
-    uint32_t key[NE];
+    uint64_t pk[NE];
     float sc[NE];
 #pragma unroll
     for (int c = 0; c < NE; c++) {
         const int e = lane * NE + c;
         const uint32_t o = e < E ? row_off + 4u * (uint32_t)e : K3X_OOB;
-        const float v = bload_f32(cr, o);
-        sc[c] = bload_f32(sr, o);
+        const float v = bload_f32<CP>(cr, o);
+        sc[c] = bload_f32<CP>(sr, o);
         const uint32_t k = choice_key(v);
-        key[c] = (e < E && k > K_NEG_INF) ? k : 0u;
+        pk[c] = (e < E && k > K_NEG_INF) ? ((uint64_t)k << 32) | (uint64_t)(~(uint32_t)e) : 0ull;
     }
+    uint64_t prev = ~0ull;        // the previous round's winner (none yet: above all)
     int mine_e = 0;               // lane j keeps round j's expert and score
     float mine_s = 0.0f;
     for (int j = 0; j < K; j++) {
-        uint32_t bk = key[0];
-        int bc = 0;
+        uint64_t best = 0ull;
+        float bs = 0.0f;
 #pragma unroll
-        for (int c = 1; c < NE; c++)
-            if (key[c] > bk) { bk = key[c]; bc = c; }
+        for (int c = 0; c < NE; c++) {
+            const uint64_t v = pk[c] < prev ? pk[c] : 0ull;
+            const bool gt = v > best;
+            best = gt ? v : best;
+            bs = gt ? sc[c] : bs;
+        }
+        const uint32_t bk = (uint32_t)(best >> 32);
         const uint32_t m = wave_max_u32(bk);
         const uint64_t holders = __ballot(m != 0u && bk == m);
         if (holders == 0ull) {                  // nothing left (uniform)
@@ -87,18 +98,10 @@ __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, 
             continue;
         }
         const int w = (int)__builtin_ctzll(holders);
-        float bs = sc[0];
-#pragma unroll
-        for (int c = 1; c < NE; c++)
-            if (c == bc) bs = sc[c];
-        const int wc = __builtin_amdgcn_readlane(bc, w);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)best, w);
         const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs), w));
-        if (lane == w) {
-#pragma unroll
-            for (int c = 0; c < NE; c++)
-                if (c == bc) key[c] = 0u;
-        }
-        if (lane == j) { mine_e = w * NE + wc; mine_s = ws; }
+        prev = ((uint64_t)m << 32) | lo;
+        if (lane == j) { mine_e = (int)~lo; mine_s = ws; }
     }
     float wgt = mine_s;
     if (renorm && K > 1) {
@@ -113,6 +116,7 @@ __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, 
         s_idx[lane] = mine_e;
         s_w[lane] = wgt;
     }
+    if (out_e) { *out_e = mine_e; *out_w = wgt; }
 }
 
 #endif

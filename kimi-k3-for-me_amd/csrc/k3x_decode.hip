@@ -228,9 +228,11 @@ __device__ __forceinline__ void bx_load(u32x4 (&b)[4], const void *x, int x_bf16
 }
 
 // Compact B fragments of x [T][H] (NC = 2T columns) over nq quads (quads from H/128 on
-// are zeros), written by `nthreads` threads.
+// are zeros), written by `nthreads` threads.  With nw, of the normalised rows
+// nw[i] * x[i] * inv[token] instead (fp32 x).
 __device__ __forceinline__ void x_to_bset(uint8_t *dst, const void *x, int x_bf16, int H, int NC,
-                                          int nq, int tid, int nthreads)
+                                          int nq, int tid, int nthreads,
+                                          const float *nw = nullptr, const float *inv = nullptr)
 {
     const int nQ = H >> 7, ne = nq * 16 * NC;
     for (int f = tid; f < ne; f += nthreads) {
@@ -239,6 +241,12 @@ __device__ __forceinline__ void x_to_bset(uint8_t *dst, const void *x, int x_bf1
         if (q < nQ) {
             float xv[8];
             load_x8(x, x_bf16, (size_t)(n >> 1) * H + (size_t)q * 128 + kq * 32 + t * 8, xv);
+            if (nw) {
+                float wv[8];
+                load_x8(nw, 0, (size_t)q * 128 + kq * 32 + t * 8, wv);
+#pragma unroll
+                for (int j = 0; j < 8; j++) xv[j] = wv[j] * xv[j] * inv[n >> 1];
+            }
             v = bfrag_of(xv, n & 1);
         }
         *(u32x4 *)(dst + (size_t)f * 16) = v;
@@ -395,15 +403,55 @@ struct K1Args {
     float       *score, *choice;   // [T][E]
     uint16_t    *xB;               // compact B set of x over whole super-quads
     int          n_rwg;            // workgroups
+    const float *norm_w;           // RMSNorm weights [H] (fp32 x), or NULL
+    float        eps;
 };
 
 #define RWAVES 4                     // waves per expert row in the router
 #define RCH    8                     // float4 chunks per lane held at once
 
+// RMSNorm's 1/rms of every token (k3_rmsnorm, k3_ops.c:132-140) in the order of
+// rmsnorm_kernel (k3x_layout.hip), so the normalised rows are bitwise that kernel's:
+// thread i sums the squares of its float4 chunks i, i + 256, ... in double, a shuffle tree
+// per wave, the four waves added in order.  Needs 256 threads and H <= 8192.
+__device__ void k1_norm_inv(const K1Args &a, float *lds, float *s_inv)
+{
+    static_assert(NT1 == 256 && RWAVES * WAVE == NT1, "one 256-thread workgroup per row");
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int nf4 = a.H >> 2;
+    const float *x = (const float *)a.x;
+    double *dl = (double *)lds;                                 // [4 waves][8]
+    for (int t = 0; t < a.T; t++) {
+        f32x4 xv[RCH];
+#pragma unroll
+        for (int c = 0; c < RCH; c++) {
+            const int f = threadIdx.x + NT1 * c;
+            xv[c] = f < nf4 ? *(const f32x4 *)(x + (size_t)t * a.H + 4 * f)
+                            : (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int c = 0; c < RCH; c++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) ss += (double)xv[c][k] * (double)xv[c][k];
+        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        if (lane == 0) dl[wave * K3X_DECODE_MAX_T + t] = ss;
+    }
+    __syncthreads();
+    if (threadIdx.x < a.T) {
+        double tot = 0.0;
+        for (int w = 0; w < NT1 / WAVE; w++) tot += dl[w * K3X_DECODE_MAX_T + threadIdx.x];
+        s_inv[threadIdx.x] = (float)(1.0 / sqrt(tot / (double)a.H + (double)a.eps));
+    }
+    __syncthreads();
+}
+
 // Router logits: four waves per expert, sum_i W[e][i] x[i] in double (a product of two
 // floats is exact in double; only the order of the additions differs from the
 // reference's single chain), then score = sigmoid((float)logit), choice = score + bias.
-__device__ void k1_router(const K1Args &a, float *lds)
+// With a.norm_w, x[i] is the normalised nw[i] * x[i] * inv (float, the reference's order);
+// the expert's weights are in flight while the norm is worked out.
+__device__ void k1_router(const K1Args &a, float *lds, float *s_inv)
 {
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int grp = wave / RWAVES, wq = wave % RWAVES;          // expert slot, quarter
@@ -412,32 +460,46 @@ __device__ void k1_router(const K1Args &a, float *lds)
     double acc[K3X_DECODE_MAX_T];
 #pragma unroll
     for (int t = 0; t < K3X_DECODE_MAX_T; t++) acc[t] = 0.0;
-    if (e < a.E) {
-        const float *row = a.router + (size_t)e * a.H;
-        const int tl = wq * WAVE + lane;                        // 0..255 within the expert
-        for (int f0 = 0; f0 < nf4; f0 += RWAVES * WAVE * RCH) {
-            f32x4 w[RCH];
+    const float *row = a.router + (size_t)(e < a.E ? e : 0) * a.H;
+    const int tl = wq * WAVE + lane;                            // 0..255 within the expert
+    for (int f0 = 0; f0 < nf4; f0 += RWAVES * WAVE * RCH) {
+        f32x4 w[RCH];
+#pragma unroll
+        for (int c = 0; c < RCH; c++) {
+            const int f = f0 + tl + RWAVES * WAVE * c;
+            w[c] = (f < nf4 && e < a.E) ? __builtin_nontemporal_load((const f32x4 *)(row + 4 * f))
+                                        : (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+        f32x4 nw[RCH];
+        if (a.norm_w) {                         // uniform; then f0 == 0 (H <= 8192)
+            k1_norm_inv(a, lds, s_inv);
 #pragma unroll
             for (int c = 0; c < RCH; c++) {
-                const int f = f0 + tl + RWAVES * WAVE * c;
-                w[c] = f < nf4 ? __builtin_nontemporal_load((const f32x4 *)(row + 4 * f))
-                               : (f32x4){0.f, 0.f, 0.f, 0.f};
+                const int f = tl + RWAVES * WAVE * c;
+                nw[c] = f < nf4 ? *(const f32x4 *)(a.norm_w + 4 * f) : (f32x4){0.f, 0.f, 0.f, 0.f};
             }
+        }
 #pragma unroll
-            for (int t = 0; t < K3X_DECODE_MAX_T; t++) {
-                if (t < a.T) {
-                    float xv[RCH][4];
+        for (int t = 0; t < K3X_DECODE_MAX_T; t++) {
+            if (t < a.T) {
+                float xv[RCH][4];
 #pragma unroll
-                    for (int c = 0; c < RCH; c++) {
-                        const int f = f0 + tl + RWAVES * WAVE * c;
-                        if (f < nf4) load_x4(a.x, a.x_bf16, (size_t)t * a.H + 4 * f, xv[c]);
-                        else xv[c][0] = xv[c][1] = xv[c][2] = xv[c][3] = 0.f;
-                    }
+                for (int c = 0; c < RCH; c++) {
+                    const int f = f0 + tl + RWAVES * WAVE * c;
+                    if (f < nf4) load_x4(a.x, a.x_bf16, (size_t)t * a.H + 4 * f, xv[c]);
+                    else xv[c][0] = xv[c][1] = xv[c][2] = xv[c][3] = 0.f;
+                }
+                if (a.norm_w) {
+                    const float inv = s_inv[t];
 #pragma unroll
                     for (int c = 0; c < RCH; c++)
 #pragma unroll
-                        for (int k = 0; k < 4; k++) acc[t] += (double)w[c][k] * (double)xv[c][k];
+                        for (int k = 0; k < 4; k++) xv[c][k] = nw[c][k] * xv[c][k] * inv;
                 }
+#pragma unroll
+                for (int c = 0; c < RCH; c++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) acc[t] += (double)w[c][k] * (double)xv[c][k];
             }
         }
     }
@@ -462,14 +524,16 @@ __device__ void k1_router(const K1Args &a, float *lds)
     }
 }
 
-// Router logits of NT1 / WAVE / RWAVES experts, and a share of x's B set for k2.
+// Router logits of NT1 / WAVE / RWAVES experts (of the RMSNorm of x when norm_w is given),
+// and a share of x's B set for k2.
 __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
 {
     __shared__ float lds[(NT1 / WAVE - 1) * 8 * WAVE];
-    k1_router(a, lds);
+    __shared__ float s_inv[K3X_DECODE_MAX_T];
+    k1_router(a, lds, s_inv);
     const int nS = ((a.H >> 7) + 3) >> 2;
     x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS,
-              blockIdx.x * NT1 + threadIdx.x, a.n_rwg * NT1);
+              blockIdx.x * NT1 + threadIdx.x, a.n_rwg * NT1, a.norm_w, s_inv);
 }
 
 // One workgroup: the routing of every token and the unique experts, for k2 and k3.
@@ -735,7 +799,8 @@ static void launch_sel(const KSArgs &a, hipStream_t s)
 }
 
 extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x_dtype,
-                              int T, const float *resid, int *idx, float *wt, void *stream)
+                              int T, const float *resid, int *idx, float *wt,
+                              const float *norm_w, float eps, void *stream)
 {
     const k3x_cfg *c = &L->cfg;
     hipStream_t s = (hipStream_t)stream;
@@ -748,6 +813,10 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a1.T = T; a1.H = H; a1.E = c->n_experts;
     a1.score = L->score; a1.choice = L->choice; a1.xB = L->xB;
     a1.n_rwg = (c->n_experts + NT1 / WAVE / RWAVES - 1) / (NT1 / WAVE / RWAVES);
+    a1.norm_w = norm_w; a1.eps = eps;
+    if (norm_w && (x_dtype == K3X_BF16 || H > RCH * NT1 * 4 || ((uintptr_t)x & 15) ||
+                   ((uintptr_t)norm_w & 15)))
+        return K3X_E_ARG;
     if ((rc = record(L, 0, s))) return rc;
     hipLaunchKernelGGL(k1_router_bset, dim3(a1.n_rwg), dim3(NT1), 0, s, a1);
     if ((rc = launch_ok())) return rc;

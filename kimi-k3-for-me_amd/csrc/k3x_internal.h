@@ -132,8 +132,11 @@ int k3x_dev_untile_fp4(uint8_t *packed, uint8_t *scales, const uint8_t *src, int
                        void *stream);
 int k3x_dev_synth_fp4(uint8_t *dst, int R, int K, uint64_t code_key, uint64_t scale_key,
                       int lo, int hi, void *stream);
+/* norm_w != NULL: the MoE input is the RMSNorm of x (fp32, 16-byte aligned, hidden <=
+ * 8192) with those weights and eps, worked out inside the router launch */
 int k3x_dev_decode(struct k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
-                   const float *resid, int *idx, float *wt, void *stream);
+                   const float *resid, int *idx, float *wt, const float *norm_w, float eps,
+                   void *stream);
 int k3x_dev_prefill(struct k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                     const float *resid, int *idx, float *wt, void *stream);
 int k3x_pf_reserve(struct k3x_moe_layer *L, int T);   /* k3x_moe.c */

@@ -125,21 +125,58 @@ __global__ void synth_fp4_kernel(uint8_t *dst, int R, int K, uint64_t ck, uint64
 }
 
 // ------------------------------------------------------------------ RMSNorm
+// RMSNorm of one row per workgroup (k3_rmsnorm, k3_ops.c:132-140): the sum of squares in
+// double (each product exact; the additions in a tree rather than the reference's
+// chain), inv rounded to float, then y = w * x * inv in float in the reference's order.
+// Rows of up to RN_MAX * NT * 4 floats (16-byte aligned) are loaded once, x and w
+// together with every load issued before the first use, and kept in registers between
+// the two passes; other rows take the plain loop.
+#define RN_MAX 8
 __global__ void __launch_bounds__(NT) rmsnorm_kernel(float *y, const float *x, const float *w,
                                                       int n, float eps)
 {
     __shared__ double red[NT / WAVE];
     const float *xr = x + (size_t)blockIdx.x * n;
     float *yr = y + (size_t)blockIdx.x * n;
+    const bool vec = (n & 3) == 0 && n <= RN_MAX * NT * 4 &&
+                     (((uintptr_t)xr | (uintptr_t)yr | (uintptr_t)w) & 15) == 0;
+    const int n4 = n >> 2;
+    f32x4 xv[RN_MAX], wv[RN_MAX];
     double ss = 0.0;
-    for (int i = threadIdx.x; i < n; i += NT) ss += (double)xr[i] * (double)xr[i];
+    if (vec) {
+#pragma unroll
+        for (int r = 0; r < RN_MAX; r++) {
+            const int i = threadIdx.x + r * NT;
+            xv[r] = i < n4 ? ((const f32x4 *)xr)[i] : (f32x4){0.f, 0.f, 0.f, 0.f};
+            wv[r] = i < n4 ? ((const f32x4 *)w)[i] : (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int r = 0; r < RN_MAX; r++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) ss += (double)xv[r][k] * (double)xv[r][k];
+    } else {
+        for (int i = threadIdx.x; i < n; i += NT) ss += (double)xr[i] * (double)xr[i];
+    }
     for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x / WAVE] = ss;
     __syncthreads();
     double tot = 0.0;
     for (int i = 0; i < NT / WAVE; i++) tot += red[i];
     const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
-    for (int i = threadIdx.x; i < n; i += NT) yr[i] = w[i] * xr[i] * inv;
+    if (vec) {
+#pragma unroll
+        for (int r = 0; r < RN_MAX; r++) {
+            const int i = threadIdx.x + r * NT;
+            if (i < n4) {
+                f32x4 o;
+#pragma unroll
+                for (int k = 0; k < 4; k++) o[k] = wv[r][k] * xv[r][k] * inv;
+                ((f32x4 *)yr)[i] = o;
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += NT) yr[i] = w[i] * xr[i] * inv;
+    }
 }
 
 // ------------------------------------------------------------------ launchers

@@ -357,7 +357,7 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     if ((idx == NULL) != (wt == NULL)) return K3X_E_ARG;
     if (T == 0) return 0;
     if (T <= L->tdec)
-        return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, stream);
+        return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, NULL, 0.0f, stream);
     return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
 }
 
@@ -615,8 +615,15 @@ static int stack_record(k3x_stack *S, float *h, int T)
     if (S->graph) { hipGraphDestroy(S->graph); S->graph = NULL; }
     HIPCHK(hipStreamBeginCapture(S->cap, hipStreamCaptureModeThreadLocal));
     for (int l = 0; l < S->n && !rc; l++) {
-        rc = k3x_rmsnorm(S->y, h, S->norm_w[l], S->H, T, S->eps, S->cap);
-        if (!rc) rc = k3x_moe_forward(S->layers[l], h, S->y, K3X_F32, T, h, NULL, NULL, S->cap);
+        k3x_moe_layer *L = S->layers[l];
+        const float *nw = S->norm_w[l];
+        if (T <= L->tdec && S->H <= 8192 && !((uintptr_t)nw & 15)) {
+            /* decode: the norm is worked out inside the router launch */
+            rc = k3x_dev_decode(L, h, h, K3X_F32, T, h, NULL, NULL, nw, S->eps, S->cap);
+        } else {
+            rc = k3x_rmsnorm(S->y, h, nw, S->H, T, S->eps, S->cap);
+            if (!rc) rc = k3x_moe_forward(L, h, S->y, K3X_F32, T, h, NULL, NULL, S->cap);
+        }
     }
     hipGraph_t g = NULL;
     const hipError_t ec = hipStreamEndCapture(S->cap, &g);

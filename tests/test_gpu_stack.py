@@ -74,6 +74,27 @@ def test_stack_graph_replays(torch, k3x, tiny_stack):
     S.close()
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_stack_fused_norm_equals_separate_norm(torch, k3x, tiny_stack, T):
+    """Decode-sized calls work the RMSNorm out inside the router launch; the result must be
+    bitwise what a separate k3x_rmsnorm followed by the MoE call gives."""
+    say(f"case: 3 tiny layers, T={T}, fused norm vs k3x_rmsnorm + forward, bitwise")
+    Ls, norms, layers, nd = tiny_stack
+    S = k3x.Stack(layers, [w.data_ptr() for w in nd], eps=EPS, max_T=8)
+    h0 = Ls[0].x(T, bf16=False, stream_sub=90 + T) * 3.0
+    h = torch.from_numpy(h0).cuda()
+    s = torch.cuda.current_stream().cuda_stream
+    S.forward(h.data_ptr(), T, s)
+    ref = torch.from_numpy(h0).cuda()
+    y = torch.empty_like(ref)
+    for L, w in zip(layers, nd):
+        k3x.rmsnorm(y.data_ptr(), ref.data_ptr(), w.data_ptr(), Ls[0].H, T, EPS, s)
+        L.forward(ref.data_ptr(), y.data_ptr(), T, k3x.K3X_F32, ref.data_ptr(), 0, 0, s)
+    torch.cuda.synchronize()
+    assert torch.equal(h, ref)
+    S.close()
+
+
 def test_stack_rejects_too_many_tokens(torch, k3x, tiny_stack):
     Ls, norms, layers, nd = tiny_stack
     S = k3x.Stack(layers, [w.data_ptr() for w in nd], eps=EPS, max_T=2)

@@ -77,7 +77,7 @@ typedef struct k3x_prefill_buf {
     int      *counts;       /* [E] tokens per expert                                 */
     int      *offsets;      /* [E+1] first permuted row of each expert               */
     int      *cursor;       /* [E]                                                   */
-    int      *tb_gu, *tb_dn;  /* [E+1] first GEMM tile of each expert               */
+    int      *tb_gu, *tb_dn;  /* [2][E+1] first GEMM tile of each expert in its class */
     void     *desc_gu, *desc_dn;   /* per GEMM tile {expert, row block, row, rows}      */
     int       ndesc_gu, ndesc_dn;  /* entries of each table                            */
     uint16_t *xp;           /* [2][H/8][T*K][8] gate/up activations, permuted rows    */

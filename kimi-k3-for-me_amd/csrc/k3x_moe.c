@@ -301,7 +301,7 @@ int k3x_pf_reserve(k3x_moe_layer *L, int T)
         t * E * 4, t * E * 4,      /* score, choice */
         t * K * 4, t * K * 4,      /* idx, wt */
         E * 4, (E + 1) * 4, E * 4, /* counts, offsets, cursor */
-        (E + 1) * 4, (E + 1) * 4,  /* tb_gu, tb_dn */
+        2 * (E + 1) * 4, 2 * (E + 1) * 4,  /* tb_gu, tb_dn: small and large tile classes */
         t * K * 4, t * K * 4, t * K * 4,   /* perm_tok, perm_w, pos_of */
         t * K * I * 4,             /* act     */
         (SI ? t * SI * 4 : 256),   /* act_sh  */

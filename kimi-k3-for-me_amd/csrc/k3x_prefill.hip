@@ -170,38 +170,63 @@ __global__ void __launch_bounds__(PF_NT) pf_topk(PfTopkArgs a)
 }
 
 // ------------------------------------------------------------------ scan
-// One workgroup of 1024 threads (E <= 1024): offsets[e] = sum of counts below e; tile
-// bases of the two routed GEMMs (expert e gets nrb x ceil(count/tpb) tiles); cursors
-// cleared.  Three inclusive scans in LDS, one element per thread.
-__global__ void __launch_bounds__(1024) pf_scan(const int *counts, int E, int *offsets,
-                                                int *cursor, int *tb_gu, int tpb_gu, int nrb_gu,
-                                                int *tb_dn, int tpb_dn, int nrb_dn)
+// One workgroup of 1024 threads (E <= 1024): offsets[e] = sum of counts below e, and the
+// tile bases of the two routed GEMMs.  Each GEMM has two tile classes: an expert with at
+// most tpb_s tokens takes nrb_s tiles of tpb_s columns (one column block), a larger one
+// nrb_b x ceil(count/tpb_b) tiles of tpb_b columns.  tb[0..E] are the small class's bases
+// (tb[E] = its tile count), tb[E+1 .. 2E+1] the large class's.  Cursors cleared.  Five
+// inclusive scans in LDS, one element per thread.
+struct PfScanArgs {
+    const int *counts;
+    int        E;
+    int       *offsets, *cursor;
+    int       *tb[2];                   // gate/up, down
+    int        tpb_s[2], tpb_b[2];      // columns of a tile, small and large class
+    int        nrb_s[2], nrb_b[2];      // row blocks, small and large class
+};
+
+__global__ void __launch_bounds__(1024) pf_scan(PfScanArgs a)
 {
-    __shared__ int s[3][1024];
-    const int e = threadIdx.x;
-    const int c = e < E ? counts[e] : 0;
-    int v[3] = {c, nrb_gu * ((c + tpb_gu - 1) / tpb_gu), nrb_dn * ((c + tpb_dn - 1) / tpb_dn)};
-    if (e < E) cursor[e] = 0;
+    __shared__ int s[5][1024];
+    const int e = threadIdx.x, E = a.E;
+    const int c = e < E ? a.counts[e] : 0;
+    int v[5];
+    v[0] = c;
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        const bool big = c > a.tpb_s[m];
+        v[1 + 2 * m] = big ? 0 : a.nrb_s[m] * ((c + a.tpb_s[m] - 1) / a.tpb_s[m]);
+        v[2 + 2 * m] = big ? a.nrb_b[m] * ((c + a.tpb_b[m] - 1) / a.tpb_b[m]) : 0;
+    }
+    if (e < E) a.cursor[e] = 0;
     for (int d = 1; d < 1024; d <<= 1) {
 #pragma unroll
-        for (int i = 0; i < 3; i++) s[i][e] = v[i];
+        for (int i = 0; i < 5; i++) s[i][e] = v[i];
         __syncthreads();
         if (e >= d)
 #pragma unroll
-            for (int i = 0; i < 3; i++) v[i] += s[i][e - d];
+            for (int i = 0; i < 5; i++) v[i] += s[i][e - d];
         __syncthreads();
     }
     // v = inclusive sums; the exclusive value of e is the inclusive value of e - 1
 #pragma unroll
-    for (int i = 0; i < 3; i++) s[i][e] = v[i];
+    for (int i = 0; i < 5; i++) s[i][e] = v[i];
     __syncthreads();
     if (e < E) {
-        offsets[e] = e == 0 ? 0 : s[0][e - 1];
-        tb_gu[e] = e == 0 ? 0 : s[1][e - 1];
-        tb_dn[e] = e == 0 ? 0 : s[2][e - 1];
+        a.offsets[e] = e == 0 ? 0 : s[0][e - 1];
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            a.tb[m][e] = e == 0 ? 0 : s[1 + 2 * m][e - 1];
+            a.tb[m][E + 1 + e] = e == 0 ? 0 : s[2 + 2 * m][e - 1];
+        }
     }
     if (e == E - 1) {
-        offsets[E] = v[0]; tb_gu[E] = v[1]; tb_dn[E] = v[2];
+        a.offsets[E] = v[0];
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            a.tb[m][E] = v[1 + 2 * m];
+            a.tb[m][2 * E + 1] = v[2 + 2 * m];
+        }
     }
 }
 
@@ -234,16 +259,17 @@ __global__ void __launch_bounds__(PF_NT) pf_permute(const uint16_t *xg, int T, i
 
 // ------------------------------------------------------------------ tile tables
 // One descriptor per GEMM tile: {group, row block, first permuted row, tokens}; expert e
-// owns tiles tb[e] .. tb[e+1)-1, row blocks outer, column blocks inner.
+// owns tiles tb[e] .. of its class's list (the small class's list first, then the large
+// class's from desc + tb[E]), row blocks outer, column blocks inner.
 __global__ void __launch_bounds__(PF_NT) pf_tiles(const int *counts, const int *offsets,
-                                                  const int *tb_gu, int tpb_gu, int nrb_gu,
-                                                  int4 *desc_gu, const int *tb_dn, int tpb_dn,
-                                                  int nrb_dn, int4 *desc_dn)
+                                                  PfScanArgs a, int4 *desc_gu, int4 *desc_dn)
 {
-    const int e = blockIdx.x, c = counts[e], off = offsets[e];
-    for (int pass = 0; pass < 2; pass++) {
-        const int tpb = pass ? tpb_dn : tpb_gu, nrb = pass ? nrb_dn : nrb_gu;
-        int4 *desc = (pass ? desc_dn : desc_gu) + (pass ? tb_dn[e] : tb_gu[e]);
+    const int e = blockIdx.x, c = counts[e], off = offsets[e], E = a.E;
+    for (int m = 0; m < 2; m++) {
+        const bool big = c > a.tpb_s[m];
+        const int tpb = big ? a.tpb_b[m] : a.tpb_s[m], nrb = big ? a.nrb_b[m] : a.nrb_s[m];
+        const int *tb = a.tb[m];
+        int4 *desc = (m ? desc_dn : desc_gu) + (big ? tb[E] + tb[E + 1 + e] : tb[e]);
         const int nc = (c + tpb - 1) / tpb;
         for (int rel = threadIdx.x; rel < nrb * nc; rel += PF_NT) {
             const int rb = rel / nc, cb = rel % nc;
@@ -275,10 +301,10 @@ struct PfGemmArgs {
     const uint8_t  *wm[2];      // group 0's matrices (gate, up) or (down), tiled
     size_t          gstride;    // bytes between groups' records
     int             R, K;       // rows and inner dimension of each matrix
-    int             G;          // groups
     const int4     *desc;       // per tile {group, row block, first row, rows}, or NULL:
                                 // one group of n0 rows
-    const int      *tbase;      // [G+1] first tile of each group (tbase[G] = tiles)
+    const int      *ntile;      // tiles in this launch's list
+    const int      *dbase;      // the list starts at desc + *dbase, or NULL: at desc
     int             n0;
     const uint16_t *bsrc;       // B planes [2][K/8][brows][8] bf16
     int             brows;      // rows of each B plane
@@ -345,9 +371,9 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
     int g = 0, rb, ntok, p0;
     const int tile = blockIdx.x;
     if (a.desc) {
-        const int ntiles = a.tbase[a.G];
-        const int4 d = a.desc[tile];
+        const int ntiles = *a.ntile;
         if (tile >= ntiles) return;
+        const int4 d = a.desc[tile];
         g = d.x; rb = d.y; p0 = d.z; ntok = d.w;
     } else {
         const int nc = (a.n0 + TPB - 1) / TPB;
@@ -536,18 +562,18 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
 // 32-63).  The B block in LDS is laid out to match: entry ((g*4 + d)*2 + h)*NCOL + col
 // holds those 8 k of column col.  Every product of the quad is formed exactly once;
 // only the order of the fp32 additions differs from the 16x16 form.
-template <bool EXACT, int NMAT, int RT32, int CT32, int HL, bool GU>
-__global__ void __launch_bounds__(PF_NT, 2) pf_gemm32(PfGemmArgs a)
+template <bool EXACT, int NMAT, int RT32, int CT32, int HL, bool GU, int NW>
+__global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
 {
-    constexpr int NW = PF_NT / WAVE;
+    constexpr int NTH = NW * WAVE;
     constexpr int NCOL = CT32 * 32;
     constexpr int TPB = NCOL / HL;
     constexpr int RPB = NW * RT32 * 32;
     constexpr int QB = NCOL * 128 * 2;
-    constexpr int NJ = QB / (PF_NT * 16);
+    constexpr int NJ = QB / (NTH * 16);
     constexpr int RING = 4;
     constexpr int LPI = NMAT * RT32 * 4 + NJ;       // 2 code + 2 scale loads per 32 rows
-    static_assert(NJ * PF_NT * 16 == QB, "B quad must split evenly");
+    static_assert(NJ * NTH * 16 == QB, "B quad must split evenly");
     static_assert((RING - 2) * LPI < 64, "vmcnt range");
     __shared__ __attribute__((aligned(16))) uint8_t sB[RING * QB];
 
@@ -559,12 +585,12 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm32(PfGemmArgs a)
         // contiguous runs instead (XCD x takes tiles x*per .. x*per + per-1 in order), so
         // the column blocks of one weight row block run back to back on one XCD and
         // re-read the weights from its L2.  The grid is a multiple of 8.
-        const int ntiles = a.desc ? a.tbase[a.G] : nrb * ((a.n0 + TPB - 1) / TPB);
+        const int ntiles = a.desc ? *a.ntile : nrb * ((a.n0 + TPB - 1) / TPB);
         const int per = (ntiles + 7) >> 3;
         const int k = blockIdx.x >> 3, tile = (blockIdx.x & 7) * per + k;
         if (k >= per || tile >= ntiles) return;
         if (a.desc) {
-            const int4 d = a.desc[tile];
+            const int4 d = a.desc[(a.dbase ? *a.dbase : 0) + tile];
             g = d.x; rb = d.y; p0 = d.z; ntok = d.w;
         } else {
             const int nc = (a.n0 + TPB - 1) / TPB;
@@ -772,18 +798,34 @@ static void launch_topk(const PfTopkArgs &a, hipStream_t s)
     hipLaunchKernelGGL(pf_topk<NE>, dim3(cdiv(a.T, PF_NT / WAVE)), dim3(PF_NT), 0, s, a);
 }
 
-// gate/up and down launch shapes of the routed GEMMs (pf_gemm32): 32-row tiles per
-// wave, 32-column tiles per workgroup
-#define GU_RT32 1
-#define GU_CT32 1
-#define DN_RT32 2
-#define DN_CT32 2
+// Launch shapes of the routed GEMMs (pf_gemm32): NW waves of RT32 32-row tiles per
+// workgroup and CT32 32-column tiles; a small shape for experts of at most one small
+// column block of tokens (little padding, more workgroups per CU) and a large one for the
+// others (fewer re-reads of their weights and activations).
+#define NW_S      4
+#define NW_B      8
+#define GU_RT32   1
+#define GU_CT32_S 1
+#define GU_CT32_B 3
+#define DN_RT32   2
+#define DN_CT32_S 2
+#define DN_CT32_B 3
 
-template <bool EXACT, int HL>
+template <bool EXACT, int HL, int CT32, int NW>
 static void launch_gu(const PfGemmArgs &a, unsigned grid, hipStream_t s)
 {
-    hipLaunchKernelGGL((pf_gemm32<EXACT, 2, GU_RT32, GU_CT32, HL, true>), dim3(grid), dim3(PF_NT), 0, s, a);
+    hipLaunchKernelGGL((pf_gemm32<EXACT, 2, GU_RT32, CT32, HL, true, NW>), dim3(grid),
+                       dim3(NW * WAVE), 0, s, a);
 }
+
+template <bool EXACT, int CT32, int NW>
+static void launch_dn(const PfGemmArgs &a, unsigned grid, hipStream_t s)
+{
+    hipLaunchKernelGGL((pf_gemm32<EXACT, 1, DN_RT32, CT32, 2, false, NW>), dim3(grid),
+                       dim3(NW * WAVE), 0, s, a);
+}
+
+static inline unsigned round8(size_t n) { return (unsigned)((n + 7) & ~(size_t)7); }
 
 static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                     const float *resid, int *uidx, float *uwt, hipStream_t s)
@@ -817,49 +859,69 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     else               launch_topk<16>(at, s);
     if ((rc = launch_ok())) return rc;
 
-    const int tpb_gu = GU_CT32 * 32 / HLg, nrb_gu = cdiv(I, (PF_NT / WAVE) * GU_RT32 * 32);
-    const int tpb_dn = DN_CT32 * 32 / 2, nrb_dn = cdiv(H, (PF_NT / WAVE) * DN_RT32 * 32);
-    hipLaunchKernelGGL(pf_scan, dim3(1), dim3(1024), 0, s, B->counts, E, B->offsets, B->cursor,
-                       B->tb_gu, tpb_gu, nrb_gu, B->tb_dn, tpb_dn, nrb_dn);
+    PfScanArgs sa;
+    sa.counts = B->counts; sa.E = E; sa.offsets = B->offsets; sa.cursor = B->cursor;
+    sa.tb[0] = B->tb_gu; sa.tb[1] = B->tb_dn;
+    sa.tpb_s[0] = GU_CT32_S * 32 / HLg; sa.tpb_b[0] = GU_CT32_B * 32 / HLg;
+    sa.nrb_s[0] = cdiv(I, NW_S * GU_RT32 * 32); sa.nrb_b[0] = cdiv(I, NW_B * GU_RT32 * 32);
+    sa.tpb_s[1] = DN_CT32_S * 32 / 2; sa.tpb_b[1] = DN_CT32_B * 32 / 2;
+    sa.nrb_s[1] = cdiv(H, NW_S * DN_RT32 * 32); sa.nrb_b[1] = cdiv(H, NW_B * DN_RT32 * 32);
+    hipLaunchKernelGGL(pf_scan, dim3(1), dim3(1024), 0, s, sa);
     if ((rc = launch_ok())) return rc;
     hipLaunchKernelGGL(pf_scatter, dim3(cdiv(TK, PF_NT)), dim3(PF_NT), 0, s, B->idx, B->wt, TK, K,
                        B->offsets, B->cursor, B->perm_tok, B->perm_w, B->pos_of);
     if ((rc = launch_ok())) return rc;
-    hipLaunchKernelGGL(pf_tiles, dim3(E), dim3(PF_NT), 0, s, B->counts, B->offsets, B->tb_gu,
-                       tpb_gu, nrb_gu, (int4 *)B->desc_gu, B->tb_dn, tpb_dn, nrb_dn,
-                       (int4 *)B->desc_dn);
+    hipLaunchKernelGGL(pf_tiles, dim3(E), dim3(PF_NT), 0, s, B->counts, B->offsets, sa,
+                       (int4 *)B->desc_gu, (int4 *)B->desc_dn);
     if ((rc = launch_ok())) return rc;
     hipLaunchKernelGGL(pf_permute, dim3(cdiv((size_t)HLg * (H / 8) * TK, PF_NT)), dim3(PF_NT), 0, s,
                        B->xhl, T, H / 8, HLg, B->perm_tok, TK, B->xp);
     if ((rc = launch_ok())) return rc;
 
-    // routed gate/up: B rows are tokens of xhl through perm_tok
+    // grids: upper bounds of each list (a small expert has one column block; large ones
+    // number at most TK / (tpb_s + 1)); surplus workgroups leave at once
+    unsigned grid_s[2], grid_b[2];
+    for (int m = 0; m < 2; m++) {
+        const size_t nbig = (size_t)TK / (sa.tpb_s[m] + 1);
+        grid_s[m] = round8((size_t)sa.nrb_s[m] * E);
+        grid_b[m] = round8((size_t)sa.nrb_b[m] * (cdiv(TK, sa.tpb_b[m]) + (nbig < (size_t)E ? nbig : (size_t)E)));
+    }
+    if (grid_s[0] + grid_b[0] > (unsigned)B->ndesc_gu || grid_s[1] + grid_b[1] > (unsigned)B->ndesc_dn)
+        return K3X_E_SHAPE;
+
+    // routed gate/up: B rows are the permuted activation rows
     PfGemmArgs g;
     memset(&g, 0, sizeof g);
     g.wm[0] = L->experts + L->gate_off; g.wm[1] = L->experts + L->up_off;
     g.gstride = L->expert_bytes;
-    g.R = I; g.K = H; g.G = E; g.desc = (const int4 *)B->desc_gu; g.tbase = B->tb_gu;
+    g.R = I; g.K = H; g.desc = (const int4 *)B->desc_gu;
     g.bsrc = B->xp; g.brows = TK; g.perm = NULL; g.row_base = 0;
     g.pw = B->perm_w; g.act = B->act; g.arows = TK; g.out_base = 0;
-    const unsigned grid_gu = (nrb_gu * (cdiv(TK, tpb_gu) + (unsigned)(E < TK ? E : TK)) + 7) & ~7u;
-    const unsigned grid_dn = (nrb_dn * (cdiv(TK, tpb_dn) + (unsigned)(E < TK ? E : TK)) + 7) & ~7u;
-    if (grid_gu > (unsigned)B->ndesc_gu || grid_dn > (unsigned)B->ndesc_dn) return K3X_E_SHAPE;
     const bool ex_gu = (L->special & 3) != 0;
-    if (ex_gu) { if (HLg == 1) launch_gu<true, 1>(g, grid_gu, s); else launch_gu<true, 2>(g, grid_gu, s); }
-    else       { if (HLg == 1) launch_gu<false, 1>(g, grid_gu, s); else launch_gu<false, 2>(g, grid_gu, s); }
+    PfGemmArgs gb = g;
+    g.ntile = B->tb_gu + E;
+    gb.ntile = B->tb_gu + 2 * E + 1; gb.dbase = B->tb_gu + E;
+    if (ex_gu) {
+        if (HLg == 1) { launch_gu<true, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<true, 1, GU_CT32_S, NW_S>(g, grid_s[0], s); }
+        else          { launch_gu<true, 2, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<true, 2, GU_CT32_S, NW_S>(g, grid_s[0], s); }
+    } else {
+        if (HLg == 1) { launch_gu<false, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<false, 1, GU_CT32_S, NW_S>(g, grid_s[0], s); }
+        else          { launch_gu<false, 2, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<false, 2, GU_CT32_S, NW_S>(g, grid_s[0], s); }
+    }
     if ((rc = launch_ok())) return rc;
 
     // routed down: B rows are the activation rows, in permuted order
     PfGemmArgs d;
     memset(&d, 0, sizeof d);
     d.wm[0] = L->experts + L->down_off; d.gstride = L->expert_bytes;
-    d.R = H; d.K = I; d.G = E; d.desc = (const int4 *)B->desc_dn; d.tbase = B->tb_dn;
+    d.R = H; d.K = I; d.desc = (const int4 *)B->desc_dn;
     d.bsrc = B->act; d.brows = TK; d.perm = NULL; d.row_base = 0;
     d.y = B->y; d.out_base = 0;
-    if (L->special & 4)
-        hipLaunchKernelGGL((pf_gemm32<true, 1, DN_RT32, DN_CT32, 2, false>), dim3(grid_dn), dim3(PF_NT), 0, s, d);
-    else
-        hipLaunchKernelGGL((pf_gemm32<false, 1, DN_RT32, DN_CT32, 2, false>), dim3(grid_dn), dim3(PF_NT), 0, s, d);
+    PfGemmArgs db = d;
+    d.ntile = B->tb_dn + E;
+    db.ntile = B->tb_dn + 2 * E + 1; db.dbase = B->tb_dn + E;
+    if (L->special & 4) { launch_dn<true, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<true, DN_CT32_S, NW_S>(d, grid_s[1], s); }
+    else                { launch_dn<false, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<false, DN_CT32_S, NW_S>(d, grid_s[1], s); }
     if ((rc = launch_ok())) return rc;
 
     int sh_row0 = -1;
@@ -869,7 +931,7 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
         PfGemmArgs sg;
         memset(&sg, 0, sizeof sg);
         sg.wm[0] = (const uint8_t *)L->sh_gate; sg.wm[1] = (const uint8_t *)L->sh_up;
-        sg.R = SI; sg.K = H; sg.G = 1; sg.n0 = T;
+        sg.R = SI; sg.K = H; sg.n0 = T;
         sg.bsrc = B->xhl; sg.brows = T; sg.row_base = 0;
         sg.act = B->act_sh; sg.arows = T; sg.out_base = 0;
         const int tpb_sg = 4 * 16 / HLg, nrb_sg = cdiv(SI, (PF_NT / WAVE) * 1 * 16);
@@ -881,7 +943,7 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
         if ((rc = launch_ok())) return rc;
         PfGemmArgs sd;
         memset(&sd, 0, sizeof sd);
-        sd.wm[0] = (const uint8_t *)L->sh_down; sd.R = H; sd.K = SI; sd.G = 1; sd.n0 = T;
+        sd.wm[0] = (const uint8_t *)L->sh_down; sd.R = H; sd.K = SI; sd.n0 = T;
         sd.bsrc = B->act_sh; sd.brows = T; sd.row_base = 0;
         sd.y = B->y; sd.out_base = TK;
         const int nrb_sd = cdiv(H, (PF_NT / WAVE) * 2 * 16);

@@ -46,19 +46,18 @@ def load_k3x():
     return mod
 
 
-KERNELS = ["k1_router_bset", "k1s_select", "k2_gateup", "k3_down"]
+KERNELS = ["k1_router_bset", "k2_gateup", "k3_down"]
 
 
 def kernel_bytes(U, T):
-    """Algorithmic HBM bytes per launch of the four decode kernels (each weight byte
-    once; activations included): k1 the router weights, k1s the scores, k2 the shared expert's and the
+    """Algorithmic HBM bytes per launch of the three decode kernels (each weight byte
+    once; activations included): k1 the router weights, k2 the scores, the shared expert's and the
     unique experts' gate/up weights, k3 the unique experts' and the shared expert's down
     weights and the output."""
     k1 = B_ROUTER + T * H * 2
-    k1s = 2 * T * E * 4
-    k2 = 2 * SI * H * 2 + U * 2 * (I * H // 2 + I * H // 32)
+    k2 = 2 * SI * H * 2 + U * 2 * (I * H // 2 + I * H // 32) + 2 * T * E * 4
     k3 = U * (H * I // 2 + H * I // 32) + H * SI * 2 + T * H * 4
-    return dict(zip(KERNELS, (k1, k1s, k2, k3)))
+    return dict(zip(KERNELS, (k1, k2, k3)))
 
 
 PREFILL_T = 2048
@@ -342,6 +341,7 @@ def main():
                 per[n].append(v)
     for l in layers:
         l.set_timing(False)
+        l.check()               # no decode workgroup gave up waiting for the selection
     avg = {n: float(np.mean(v)) for n, v in per.items()}
     kb = kernel_bytes(U=K, T=1)
     dom = max(avg, key=lambda n: avg[n])

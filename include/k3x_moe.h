@@ -43,6 +43,8 @@ extern "C" {
 #define K3X_E_NOMEM    -4   /* device or host allocation failed                          */
 #define K3X_E_DROP     -5   /* an expert could not be fetched (k3x_expert_drops counts it) */
 #define K3X_E_NODEV    -6   /* no usable gfx950 device                                    */
+#define K3X_E_WAIT     -7   /* a decode workgroup gave up waiting for the selection (never
+                               expected: k3x_moe_layer_check reports it)                   */
 
 /* Human-readable text of a status code (static storage). */
 const char *k3x_strerror(int status);
@@ -201,6 +203,10 @@ void k3x_stack_destroy(k3x_stack *S);
  * The kernels the last k3x_moe_forward on L enqueued, bracketed by two HIP events on
  * the stream it used (recorded when timing is on).  ms receives the elapsed time of
  * the last timed call after a synchronize. */
+/* Waits for the layer's work and reports (then clears) K3X_E_WAIT if any decode call since
+ * the last check had a workgroup give up waiting for the published selection; 0 otherwise.
+ * No counterpart in the reference (its CPU path has no cross-workgroup wait). */
+int  k3x_moe_layer_check(k3x_moe_layer *L);
 int  k3x_moe_layer_set_timing(k3x_moe_layer *L, int on);
 int  k3x_moe_layer_last_ms(k3x_moe_layer *L, float *ms);
 

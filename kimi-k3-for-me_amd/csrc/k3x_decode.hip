@@ -1,14 +1,15 @@
-// k3x_decode.hip - the decode path of the MoE block (T <= 8 tokens), four launches:
+// k3x_decode.hip - the decode path of the MoE block (T <= 8 tokens), three launches:
 //
 //   k1_router_bset    router logits in double, sigmoid, +bias (k3_router, k3_ops.c:1624-
 //                     1694) for every expert, and x's B fragments for the products.  The
 //                     router runs alone, so its 11 MB arrive first.
-//   k1s_select        one workgroup selects each token's top-k (:1700-1716) and lists the
-//                     unique experts (the dedup of moe_prefill_routed, :2067-2081).
-//   k2_gateup         first the shared expert's gate/up products over the full K with
-//                     SwiGLU (moe_shared, :1848-1857; k3_situ_glu at 2^64 betas, :148-161);
-//                     then each unique expert's gate/up products (k3_matmul_mxfp4,
-//                     :3323-3776) with SwiGLU and the routing weight folded in.
+//   k2_gateup         workgroup 0 selects each token's top-k (:1700-1716) and lists the
+//                     unique experts (the dedup of moe_prefill_routed, :2067-2081); the
+//                     shared expert's gate/up products over the full K with SwiGLU
+//                     (moe_shared, :1848-1857; k3_situ_glu at 2^64 betas, :148-161) stream
+//                     meanwhile; then each unique expert's gate/up products
+//                     (k3_matmul_mxfp4, :3323-3776) with SwiGLU and the routing weight
+//                     folded in, once the selection is published.
 //   k3_down           each unique expert's down product and the shared expert's (:1858)
 //                     into one accumulator set per 16 output rows (the weighted combine,
 //                     :1941-1942, plus the shared result, :1859), and an optional residual.
@@ -276,6 +277,17 @@ struct KSArgs {
     int            T;
 };
 
+// Stores of the published routing: written through to the device-coherent level, since
+// the routed workgroups of the same launch read them, possibly on another XCD.
+__device__ __forceinline__ void pub_i(int *p, int v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pub_f(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // A workgroup's view of the routing, in LDS.
 struct KSLds {
     int   idx[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
@@ -298,8 +310,8 @@ __device__ __forceinline__ float ks_weight(const KSLds &l, int K, int t, int e)
 // Routing of every token (one wave per token), then the unique experts in first-seen
 // order over (token, slot), built in parallel: each expert's first item by an LDS
 // minimum, the first items' slots by ballots.  Returns the number of unique experts.
-// With `publish`, also writes the indices and weights, the unique list and each unique
-// expert's weight per token for k2/k3.
+// With `publish`, also writes the indices and weights, and the unique list and each
+// unique expert's weight per token (written through) for the routed workgroups and k3.
 template <int NE>
 __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish)
 {
@@ -336,11 +348,11 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish)
             }
             if (first) {
                 const int slot = lanes_below(fm);
-                a.route->uniq[slot] = ex;
-                a.route->wtok[slot][0] = wsum;
-                for (int t = 1; t < K3X_DECODE_MAX_T; t++) a.route->wtok[slot][t] = 0.0f;
+                pub_i(&a.route->uniq[slot], ex);
+                pub_f(&a.route->wtok[slot][0], wsum);
+                for (int t = 1; t < K3X_DECODE_MAX_T; t++) pub_f(&a.route->wtok[slot][t], 0.0f);
             }
-            if (lane == 0) a.route->nu = nu;
+            if (lane == 0) pub_i(&a.route->nu, nu);
         }
         return nu;
     }
@@ -378,7 +390,7 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish)
         if (first) {
             const int slot = off + lanes_below(m);
             l.uq[slot] = ex;
-            if (publish) a.route->uniq[slot] = ex;
+            if (publish) pub_i(&a.route->uniq[slot], ex);
         }
         base += tot;
         __syncthreads();
@@ -386,9 +398,9 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish)
     if (publish) {
         for (int f = threadIdx.x; f < base * K3X_DECODE_MAX_T; f += NT) {
             const int slot = f / K3X_DECODE_MAX_T, t = f % K3X_DECODE_MAX_T;
-            a.route->wtok[slot][t] = t < a.T ? ks_weight(l, a.K, t, l.uq[slot]) : 0.0f;
+            pub_f(&a.route->wtok[slot][t], t < a.T ? ks_weight(l, a.K, t, l.uq[slot]) : 0.0f);
         }
-        if (threadIdx.x == 0) a.route->nu = base;
+        if (threadIdx.x == 0) pub_i(&a.route->nu, base);
     }
     return base;
 }
@@ -403,6 +415,7 @@ struct K1Args {
     float       *score, *choice;   // [T][E]
     uint16_t    *xB;               // compact B set of x over whole super-quads
     int          n_rwg;            // workgroups
+    int         *ready;            // k2's routing flag, cleared here
     const float *norm_w;           // RMSNorm weights [H] (fp32 x), or NULL
     float        eps;
 };
@@ -530,23 +543,24 @@ __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
 {
     __shared__ float lds[(NT1 / WAVE - 1) * 8 * WAVE];
     __shared__ float s_inv[K3X_DECODE_MAX_T];
-    k1_router(a, lds, s_inv);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *a.ready = 0;
+    // the B set's entries dealt across the workgroups (a few per workgroup), converted
+    // before the router's weights are requested when no norm is needed
     const int nS = ((a.H >> 7) + 3) >> 2;
-    x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS,
-              blockIdx.x * NT1 + threadIdx.x, a.n_rwg * NT1, a.norm_w, s_inv);
-}
-
-// One workgroup: the routing of every token and the unique experts, for k2 and k3.
-template <int NE>
-__global__ void __launch_bounds__(NT) k1s_select(KSArgs a)
-{
-    __shared__ KSLds ksl;
-    ks_route<NE>(a, ksl, true);
+    const int tid = threadIdx.x * a.n_rwg + blockIdx.x, nth = a.n_rwg * NT1;
+    if (!a.norm_w)
+        x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS, tid, nth);
+    k1_router(a, lds, s_inv);
+    if (a.norm_w)
+        x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS, tid, nth, a.norm_w, s_inv);
 }
 
 // ------------------------------------------------------------------ K2
 struct K2Args {
-    const k3x_route *route;        // from k1
+    KSArgs         ks;             // the routing, worked out by workgroup 0
+    const k3x_route *route;
+    int           *ready;          // set by workgroup 0 once the routing is out
+    int           *err;            // set by a routed workgroup that gave up waiting
     const uint8_t *experts;
     size_t         expert_bytes, gate_off, up_off;
     const uint16_t *xB;            // compact B set of x over whole super-quads
@@ -612,25 +626,60 @@ __device__ void k2_shared(const K2Args &a, float *lds, int rt)
     });
 }
 
+// Workgroup 0 works out the routing (ks_route) and publishes it: the unique list and
+// weights written through, waited for, then the ready flag (cleared by k1 of the same
+// call).  Next come the shared expert's workgroups, which need no routing and stream
+// meanwhile; then the routed ones, which wait for the flag.  Workgroups are dispatched
+// in order, so workgroup 0 is resident before any routed one waits, and it waits on
+// nothing.  The wait is still bounded (ROUTE_WAIT ticks of the 100 MHz clock, far above
+// the selection's few microseconds): a workgroup that gives up sets the error word
+// (k3x_moe_layer_check reports it) and leaves without touching the expert weights.
+#define ROUTE_WAIT 5000000ull      // 50 ms
+
 // Gate and up products of 16 rows of one unique expert: four waves on interleaved
 // super-quads; SwiGLU, the token's routing weight for this expert (0 where the token did
 // not choose it) and the bf16 hi/lo split into the expert's activation slot.
-template <bool EXACT, bool LDSB>
+template <bool EXACT, bool LDSB, int NE>
 __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
 {
     __shared__ float lds[(NT / WAVE - 1) * 8 * WAVE];
-    if ((int)blockIdx.x < a.n_sh) {
-        k2_shared<LDSB>(a, lds, blockIdx.x);
+    __shared__ int s_go;
+    if (blockIdx.x == 0) {
+        ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_store(a.ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if ((int)blockIdx.x <= a.n_sh) {
+        k2_shared<LDSB>(a, lds, blockIdx.x - 1);
         return;
     }
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int NW = NT / WAVE;
     const int NC = 2 * a.T;
     const int nTiles = a.I >> 4;
-    const int blk = blockIdx.x - a.n_sh;
+    const int blk = blockIdx.x - 1 - a.n_sh;
     const int u = blk / nTiles, rt = blk % nTiles;
-    if (u >= a.route->nu) return;
-    const int e = a.route->uniq[u];
+    if (threadIdx.x == 0) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        int go = 1;
+        while (__hip_atomic_load(a.ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > ROUTE_WAIT) {
+                __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                go = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        s_go = go;
+    }
+    __syncthreads();
+    if (!s_go) return;
+    const k3x_route *rte = a.route;
+    if (u >= __hip_atomic_load(&rte->nu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
+    const int e = __hip_atomic_load(&rte->uniq[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int nS = ((a.H >> 7) + 3) >> 2;
     const uint32_t bbytes = (uint32_t)nS * 1024u * NC;
     Stage<8> st;
@@ -669,7 +718,8 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     if (wave != 0) return;
     uint16_t *d16 = (uint16_t *)dst;
     per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&s)[8]) AI {
-        const float w = a.route->wtok[u][tok];
+        const float w = __hip_atomic_load(&rte->wtok[u][tok], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
         for (int i = 0; i < 4; i++) {
             const float y = (w == 0.0f) ? 0.0f : w * swiglu(s[i], s[4 + i]);
             uint32_t hi, lo;
@@ -793,9 +843,12 @@ static int record(k3x_moe_layer *L, int i, hipStream_t s)
 }
 
 template <int NE>
-static void launch_sel(const KSArgs &a, hipStream_t s)
+static void launch_k2(const K2Args &a, bool ex, bool st, dim3 grid, size_t lds, hipStream_t s)
 {
-    hipLaunchKernelGGL((k1s_select<NE>), dim3(1), dim3(NT), 0, s, a);
+    if (ex && st)  hipLaunchKernelGGL((k2_gateup<true, true, NE>), grid, dim3(NT), lds, s, a);
+    else if (ex)   hipLaunchKernelGGL((k2_gateup<true, false, NE>), grid, dim3(NT), lds, s, a);
+    else if (st)   hipLaunchKernelGGL((k2_gateup<false, true, NE>), grid, dim3(NT), lds, s, a);
+    else           hipLaunchKernelGGL((k2_gateup<false, false, NE>), grid, dim3(NT), lds, s, a);
 }
 
 extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x_dtype,
@@ -813,6 +866,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a1.T = T; a1.H = H; a1.E = c->n_experts;
     a1.score = L->score; a1.choice = L->choice; a1.xB = L->xB;
     a1.n_rwg = (c->n_experts + NT1 / WAVE / RWAVES - 1) / (NT1 / WAVE / RWAVES);
+    a1.ready = &L->route->ready;
     a1.norm_w = norm_w; a1.eps = eps;
     if (norm_w && (x_dtype == K3X_BF16 || H > RCH * NT1 * 4 || ((uintptr_t)x & 15) ||
                    ((uintptr_t)norm_w & 15)))
@@ -822,20 +876,12 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 1, s))) return rc;
 
-    KSArgs as;
+    K2Args a2;
+    KSArgs &as = a2.ks;
     as.score = L->score; as.choice = L->choice; as.E = c->n_experts; as.K = c->topk;
     as.renorm = c->moe_renorm; as.routed_scale = c->routed_scale; as.route = L->route;
     as.idx = L->idx; as.wt = L->wt; as.uidx = idx; as.uwt = wt; as.T = T;
-    if (c->n_experts <= 128)      launch_sel<2>(as, s);
-    else if (c->n_experts <= 256) launch_sel<4>(as, s);
-    else if (c->n_experts <= 384) launch_sel<6>(as, s);
-    else if (c->n_experts <= 512) launch_sel<8>(as, s);
-    else                          launch_sel<16>(as, s);
-    if ((rc = launch_ok())) return rc;
-    if ((rc = record(L, 2, s))) return rc;
-
-    K2Args a2;
-    a2.route = L->route;
+    a2.route = L->route; a2.ready = &L->route->ready; a2.err = &L->route->err;
     a2.experts = L->experts; a2.expert_bytes = L->expert_bytes;
     a2.gate_off = L->gate_off; a2.up_off = L->up_off;
     a2.xB = L->xB; a2.actB = L->actB; a2.T = T; a2.H = H; a2.I = I;
@@ -844,14 +890,16 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     const int n_routed = T * c->topk * (I / 16);
     const uint32_t xfp4 = (uint32_t)nS * 1024u * NC;
     const bool ex2 = (L->special & 3) != 0, st2 = xfp4 <= STAGE_MAX;
-    const size_t l2 = st2 ? xfp4 : 0;
-    const dim3 g2(a2.n_sh + n_routed);
-    if (ex2 && st2)  hipLaunchKernelGGL((k2_gateup<true, true>), g2, dim3(NT), l2, s, a2);
-    else if (ex2)    hipLaunchKernelGGL((k2_gateup<true, false>), g2, dim3(NT), l2, s, a2);
-    else if (st2)    hipLaunchKernelGGL((k2_gateup<false, true>), g2, dim3(NT), l2, s, a2);
-    else             hipLaunchKernelGGL((k2_gateup<false, false>), g2, dim3(NT), l2, s, a2);
+    size_t l2 = st2 ? xfp4 : 0;
+    if (l2 < sizeof(KSLds)) l2 = sizeof(KSLds);
+    const dim3 g2(1 + a2.n_sh + n_routed);
+    if (c->n_experts <= 128)      launch_k2<2>(a2, ex2, st2, g2, l2, s);
+    else if (c->n_experts <= 256) launch_k2<4>(a2, ex2, st2, g2, l2, s);
+    else if (c->n_experts <= 384) launch_k2<6>(a2, ex2, st2, g2, l2, s);
+    else if (c->n_experts <= 512) launch_k2<8>(a2, ex2, st2, g2, l2, s);
+    else                          launch_k2<16>(a2, ex2, st2, g2, l2, s);
     if ((rc = launch_ok())) return rc;
-    if ((rc = record(L, 3, s))) return rc;
+    if ((rc = record(L, 2, s))) return rc;
 
     K3Args a3;
     a3.experts = L->experts; a3.expert_bytes = L->expert_bytes; a3.down_off = L->down_off;
@@ -864,5 +912,5 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(H / 16), dim3(NT3), a3.lds_bytes, s, a3);
     else                hipLaunchKernelGGL(k3_down<false>, dim3(H / 16), dim3(NT3), a3.lds_bytes, s, a3);
     if ((rc = launch_ok())) return rc;
-    return record(L, 4, s);
+    return record(L, 3, s);
 }

@@ -60,7 +60,10 @@ static inline size_t k3x_bf16_matrix_bytes(int R, int K) { return (size_t)R * K 
 /* routing summary written by the router, read by the expert kernels */
 typedef struct k3x_route {
     int   nu;                                   /* unique experts in this call        */
-    int   pad[63];
+    int   ready;                                /* selection published (k2); cleared
+                                                   by k1 of the same call              */
+    int   err;                                  /* a routed workgroup gave up waiting */
+    int   pad[61];
     int   uniq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];        /* first-seen order           */
     float wtok[K3X_DECODE_MAX_T * K3X_MAX_TOPK][K3X_DECODE_MAX_T]; /* [u][token], 0 = not chosen */
 } k3x_route;

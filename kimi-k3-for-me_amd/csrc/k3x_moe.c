@@ -26,6 +26,7 @@ const char *k3x_strerror(int s)
     case K3X_E_NOMEM: return "out of memory";
     case K3X_E_DROP:  return "expert could not be fetched";
     case K3X_E_NODEV: return "no usable gfx950 device";
+    case K3X_E_WAIT:  return "decode workgroup gave up waiting for the selection";
     default:          return "unknown status";
     }
 }
@@ -359,6 +360,21 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     if (T <= L->tdec)
         return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, NULL, 0.0f, stream);
     return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
+}
+
+int k3x_moe_layer_check(k3x_moe_layer *L)
+{
+    if (!L) return K3X_E_ARG;
+    if (hipSetDevice(L->device) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+        return K3X_E_HIP;
+    int err = 0;
+    if (hipMemcpy(&err, &L->route->err, sizeof err, hipMemcpyDeviceToHost) != hipSuccess)
+        return K3X_E_HIP;
+    if (!err) return 0;
+    const int zero = 0;
+    if (hipMemcpy(&L->route->err, &zero, sizeof zero, hipMemcpyHostToDevice) != hipSuccess)
+        return K3X_E_HIP;
+    return K3X_E_WAIT;
 }
 
 int k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,

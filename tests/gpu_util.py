@@ -27,6 +27,7 @@ def dev_forward(torch, k3x, layer, x, bf16=False, resid=None):
     layer.forward(out.data_ptr(), xt.data_ptr(), T, k3x.K3X_BF16 if bf16 else k3x.K3X_F32,
                   rp, idx.data_ptr(), wt.data_ptr(), s.cuda_stream)
     torch.cuda.synchronize()
+    layer.check()
     return out.cpu().numpy(), idx.cpu().numpy(), wt.cpu().numpy()
 
 

@@ -35,6 +35,7 @@
 #define NT  256     // k2 workgroup: 4 waves
 #define NT3 512     // k3 workgroup: 8 waves
 #define STAGE_MAX 65536u   // largest B set staged in LDS (bytes)
+#define K3_LDS_MAX 73728u  // k3's dynamic LDS with the shared set: two workgroups per CU
 #define SQ_BYTES 4352u     // an fp4 super-quad of a 16-row tile
 
 extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
@@ -74,7 +75,7 @@ __device__ __forceinline__ void ring_loop(int cnt, LD ld, USE use)
 }
 
 // ------------------------------------------------------------------ LDS staging
-// Copy `bytes` (a multiple of 16) of global memory to the start of dynamic LDS.  issue()
+// Copy `bytes` (a multiple of 16) of global memory to dynamic LDS (at lds_off).  issue()
 // loads up to MAXR 16-byte pieces per thread into registers; commit() stores them and
 // copies what is left.  Issued before the weight loads, the staging loads come back
 // first, so commit's wait leaves the weights in flight.
@@ -92,16 +93,16 @@ struct Stage {
 #pragma unroll
         for (int i = 0; i < MAXR; i++) v[i] = bload16(r, threadIdx.x * 16u + i * step);
     }
-    __device__ __forceinline__ void commit(int nthreads)
+    __device__ __forceinline__ void commit(int nthreads, uint32_t lds_off = 0u)
     {
         const uint32_t step = (uint32_t)nthreads * 16u;
 #pragma unroll
         for (int i = 0; i < MAXR; i++) {
             const uint32_t o = threadIdx.x * 16u + i * step;
-            if (o < bytes) *(u32x4 *)(dyn_lds + o) = v[i];
+            if (o < bytes) *(u32x4 *)(dyn_lds + lds_off + o) = v[i];
         }
         for (uint32_t o = threadIdx.x * 16u + MAXR * step; o < bytes; o += step)
-            *(u32x4 *)(dyn_lds + o) = bload16(r, o);
+            *(u32x4 *)(dyn_lds + lds_off + o) = bload16(r, o);
     }
 };
 
@@ -743,7 +744,8 @@ struct K3Args {
     float         *out;
     const float   *resid;
     int            T, H, I, K;
-    uint32_t       lds_bytes;      // dynamic LDS of the launch
+    uint32_t       lds_bytes;      // LDS for the routed activation sets
+    uint32_t       sh_lds;         // LDS for the shared activation set (after them), or 0
 };
 
 // A bf16 quad of the shared down matrix with its B fragments (read from the shared
@@ -757,7 +759,7 @@ struct QBB {
 // shared expert's down product over its bf16 quads, eight waves interleaved, into one
 // accumulator set.  Both rings are primed first, so the shared quads' loads are in
 // flight while the routed items stream.
-template <bool EXACT, bool LDSB>
+template <bool EXACT, bool LDSB, bool SHL>
 __device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int lane, int nu)
 {
     const int NW = NT3 / WAVE;
@@ -767,8 +769,11 @@ __device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int
     const uint32_t slot = (uint32_t)nSI * 1024u * NC;
     const uint32_t tb = (uint32_t)fp4_tile_bytes(a.I);
     const int cnt = strided_count(wave, NW, nu * nSI);
+    const int nQS = a.sh_down ? a.SI >> 7 : 0;
     Stage<8> st;
     if (LDSB) st.issue(a.actB, (uint32_t)nu * slot, NT3);
+    Stage<1> st2;
+    if (SHL) st2.issue(a.shB, (uint32_t)nQS * 256u * NC, NT3);
     SQ ring[2];
     auto ld = [&](int i, int k) AI {
         const int it = wave + NW * k;
@@ -780,11 +785,6 @@ __device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int
         sq_load(ring[i], r, (uint32_t)S * SQ_BYTES, lane);
     };
     ring_prime<2>(ld);
-    if (LDSB) {
-        st.commit(NT3);
-        __syncthreads();
-    }
-    const int nQS = a.sh_down ? a.SI >> 7 : 0;
     const int cs = strided_count(wave, NW, nQS);
     const rsrc_t rw = make_rsrc(a.sh_down + (size_t)rt * 16 * a.SI, (uint32_t)nQS * 4096u);
     const rsrc_t rb = make_rsrc(a.shB, (uint32_t)nQS * 256u * NC);
@@ -795,18 +795,34 @@ __device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int
         const bool on = k < cs;
         const int q = wave + NW * k;
         qb_load(ring2[i].a, rw, on ? (uint32_t)q * 4096u : K3X_OOB, lane);
+        if (!SHL) {
 #pragma unroll
-        for (int t = 0; t < 4; t++)
-            ring2[i].b[t] = bload16(rb, on ? boff + (uint32_t)(q * 256 * NC + t * 64 * NC) : K3X_OOB);
+            for (int t = 0; t < 4; t++)
+                ring2[i].b[t] = bload16(rb, on ? boff + (uint32_t)(q * 256 * NC + t * 64 * NC) : K3X_OOB);
+        }
     };
     ring_prime<2>(ld2);
+    if (LDSB) st.commit(NT3);
+    if (SHL) st2.commit(NT3, a.lds_bytes);
+    if (LDSB || SHL) __syncthreads();
     BFrag<LDSB> bf;
     bf.init(a.actB, (uint32_t)(a.T * a.K) * slot, NC, lane);
     ring_loop<2>(cnt, ld, [&](int i, int k) AI {
         const int it = wave + NW * k;
         sq_mfma<EXACT, LDSB>(d, ring[i], bf, (uint32_t)(it / nSI) * slot, it % nSI);
     });
-    ring_loop<2>(cs, ld2, [&](int i, int k) AI { qb_mfma(d, ring2[i].a, ring2[i].b); });
+    BFrag<true> sbf;
+    sbf.init(nullptr, 0u, NC, lane);
+    ring_loop<2>(cs, ld2, [&](int i, int k) AI {
+        if (SHL) {
+            u32x4 b[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) b[t] = sbf.get(a.lds_bytes, wave + NW * k, t);
+            qb_mfma(d, ring2[i].a, b);
+        } else {
+            qb_mfma(d, ring2[i].a, ring2[i].b);
+        }
+    });
 }
 
 template <bool EXACT>
@@ -818,8 +834,11 @@ __global__ void __launch_bounds__(NT3) k3_down(K3Args a)
     const int nSI = ((a.I >> 7) + 3) >> 2;
     const uint32_t slot = (uint32_t)nSI * 1024u * 2 * a.T;
     f32x4 d = {0.f, 0.f, 0.f, 0.f};
-    if ((uint32_t)nu * slot <= a.lds_bytes) k3_body<EXACT, true>(a, d, wave, lane, nu);
-    else                                    k3_body<EXACT, false>(a, d, wave, lane, nu);
+    // both activation sets in LDS when they fit, else both read through L2
+    if ((uint32_t)nu * slot <= a.lds_bytes && a.sh_lds)
+        k3_body<EXACT, true, true>(a, d, wave, lane, nu);
+    else
+        k3_body<EXACT, false, false>(a, d, wave, lane, nu);
     float acc[4] = {d[0], d[1], d[2], d[3]};
     wave_sum_lds<4, NT3 / WAVE>(acc, lds, wave, lane);
     if (wave != 0) return;
@@ -909,8 +928,13 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     const uint32_t slot = (uint32_t)nSI * 1024u * NC;
     const size_t all = (size_t)T * c->topk * slot;
     a3.lds_bytes = slot <= STAGE_MAX ? (uint32_t)(all < STAGE_MAX ? all : (STAGE_MAX / slot) * slot) : 0u;
-    if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(H / 16), dim3(NT3), a3.lds_bytes, s, a3);
-    else                hipLaunchKernelGGL(k3_down<false>, dim3(H / 16), dim3(NT3), a3.lds_bytes, s, a3);
+    // the shared activation set beside them when two workgroups still fit a CU (without
+    // a shared expert, an empty set)
+    const uint32_t shb = (uint32_t)(L->SI / 128) * 256u * NC;
+    a3.sh_lds = (a3.lds_bytes && a3.lds_bytes + shb <= K3_LDS_MAX) ? (shb ? shb : 16u) : 0u;
+    const size_t l3 = (size_t)a3.lds_bytes + a3.sh_lds;
+    if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(H / 16), dim3(NT3), l3, s, a3);
+    else                hipLaunchKernelGGL(k3_down<false>, dim3(H / 16), dim3(NT3), l3, s, a3);
     if ((rc = launch_ok())) return rc;
     return record(L, 3, s);
 }

@@ -1,0 +1,63 @@
+"""GPU routing edge cases through the C ABI, decode and prefill, against the oracle (which
+is bitwise the reference's k3_router, k3_ops.c:1624-1719): exact ties between experts
+(the lower index first), NaN and -inf choices (never taken), +inf choices (taken first),
+fewer selectable experts than slots (the rounds that find nothing give index 0 and
+weight 0), and an expert count that is not a multiple of the wave width."""
+import numpy as np
+import pytest
+
+import synth
+from gpu_util import bank_layer, dev_forward, say
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def check(torch, k3x, L, label):
+    layer = bank_layer(k3x, L)
+    x = L.x(20, bf16=False, stream_sub=11)
+    o, idx, wt, _ = L.oracle_moe(x)
+    for T in (1, 3, 20):           # decode, decode, prefill
+        out, i2, w2 = dev_forward(torch, k3x, layer, x[:T])
+        assert np.array_equal(i2, idx[:T]), (label, T, i2, idx[:T])
+        np.testing.assert_allclose(w2, wt[:T], rtol=1e-6)
+        err = synth.rel_l2(out, o[:T])
+        say(f"  {label} T={T} rel_l2={err:.3e}")
+        assert err < TOL
+    layer.close()
+    return idx
+
+
+def test_exact_ties_lower_index_first(torch, k3x):
+    say("case: E=200 K=8, experts 3, 10, 150 with identical router rows and bias (ties)")
+    L = synth.Layer(H=256, E=200, K=8, I=128, seed=31)
+    for e in (10, 150):
+        L.gate[e] = L.gate[3]
+    L.bias[[3, 10, 150]] = 5.0             # certainly among the top-k
+    L.gate[77] = L.gate[160]
+    L.bias[77] = L.bias[160]                # a tie anywhere in the ranking
+    idx = check(torch, k3x, L, "ties")
+    for t in range(idx.shape[0]):
+        assert list(idx[t][:3]) == [3, 10, 150]
+
+
+def test_nan_and_infinite_choices(torch, k3x):
+    say("case: tiny layer, bias NaN / -inf on some experts, +inf on one")
+    L = synth.tiny(seed=32)
+    L.bias[[1, 4]] = np.nan
+    L.bias[[2, 9]] = -np.inf
+    L.bias[12] = np.inf
+    idx = check(torch, k3x, L, "nan/inf")
+    assert not np.isin(idx, [1, 2, 4, 9]).any()
+    assert (idx[:, 0] == 12).all()
+
+
+def test_fewer_selectable_than_slots(torch, k3x):
+    say("case: tiny layer, only three selectable experts for four slots")
+    L = synth.tiny(seed=33)
+    L.bias[:] = np.nan
+    L.bias[[5, 9, 14]] = 0.0
+    idx = check(torch, k3x, L, "few")
+    for t in range(idx.shape[0]):
+        assert sorted(idx[t][:3]) == [5, 9, 14] and idx[t][3] == 0

@@ -663,6 +663,13 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     const int nTiles = a.I >> 4;
     const int blk = blockIdx.x - 1 - a.n_sh;
     const int u = blk / nTiles, rt = blk % nTiles;
+    const int nS = ((a.H >> 7) + 3) >> 2;
+    const uint32_t bbytes = (uint32_t)nS * 1024u * NC;
+    if (LDSB) {                        // x's B set into LDS while the routing is worked out
+        Stage<8> st;
+        st.issue(a.xB, bbytes, NT);
+        st.commit(NT);
+    }
     if (threadIdx.x == 0) {
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         int go = 1;
@@ -681,10 +688,6 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     const k3x_route *rte = a.route;
     if (u >= __hip_atomic_load(&rte->nu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
     const int e = __hip_atomic_load(&rte->uniq[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int nS = ((a.H >> 7) + 3) >> 2;
-    const uint32_t bbytes = (uint32_t)nS * 1024u * NC;
-    Stage<8> st;
-    if (LDSB) st.issue(a.xB, bbytes, NT);
     const uint32_t tb = (uint32_t)fp4_tile_bytes(a.H);
     const uint8_t *ex = a.experts + (size_t)e * a.expert_bytes + (size_t)rt * tb;
     const rsrc_t rg = make_rsrc(ex + a.gate_off, tb);
@@ -697,10 +700,6 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
         sq_load(v[i], ru, o, lane);
     };
     ring_prime<2>(ld);
-    if (LDSB) {
-        st.commit(NT);
-        __syncthreads();
-    }
     BFrag<LDSB> bf;
     bf.init(a.xB, bbytes, NC, lane);
     f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};

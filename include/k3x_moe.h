@@ -207,6 +207,11 @@ void k3x_stack_destroy(k3x_stack *S);
  * the last check had a workgroup give up waiting for the published selection; 0 otherwise.
  * No counterpart in the reference (its CPU path has no cross-workgroup wait). */
 int  k3x_moe_layer_check(k3x_moe_layer *L);
+/* Failure injection for tests of the check above: sets the decode wait's bound (ticks of
+ * the 100 MHz clock; the default is 5,000,000 = 50 ms) and, with publish = 0, withholds
+ * the flag, so that every routed workgroup gives up after `ticks` and leaves.  Calls made
+ * so are not valid; restore with (5000000, 1).  No counterpart in the reference. */
+int  k3x_moe_layer_set_route_wait(k3x_moe_layer *L, unsigned long long ticks, int publish);
 int  k3x_moe_layer_set_timing(k3x_moe_layer *L, int on);
 int  k3x_moe_layer_last_ms(k3x_moe_layer *L, float *ms);
 

@@ -562,6 +562,8 @@ struct K2Args {
     const k3x_route *route;
     int           *ready;          // set by workgroup 0 once the routing is out
     int           *err;            // set by a routed workgroup that gave up waiting
+    uint64_t       wait_ticks;     // the routed workgroups' bound on the wait
+    int            publish;        // 0 only to exercise the bound (failure-handling test)
     const uint8_t *experts;
     size_t         expert_bytes, gate_off, up_off;
     const uint16_t *xB;            // compact B set of x over whole super-quads
@@ -632,10 +634,9 @@ __device__ void k2_shared(const K2Args &a, float *lds, int rt)
 // call).  Next come the shared expert's workgroups, which need no routing and stream
 // meanwhile; then the routed ones, which wait for the flag.  Workgroups are dispatched
 // in order, so workgroup 0 is resident before any routed one waits, and it waits on
-// nothing.  The wait is still bounded (ROUTE_WAIT ticks of the 100 MHz clock, far above
-// the selection's few microseconds): a workgroup that gives up sets the error word
-// (k3x_moe_layer_check reports it) and leaves without touching the expert weights.
-#define ROUTE_WAIT 5000000ull      // 50 ms
+// nothing.  The wait is still bounded (wait_ticks of the 100 MHz clock, by default 50 ms,
+// far above the selection's few microseconds): a workgroup that gives up sets the error
+// word (k3x_moe_layer_check reports it) and leaves without touching the expert weights.
 
 // Gate and up products of 16 rows of one unique expert: four waves on interleaved
 // super-quads; SwiGLU, the token's routing weight for this expert (0 where the token did
@@ -649,7 +650,7 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
         ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (threadIdx.x == 0)
+        if (threadIdx.x == 0 && a.publish)
             __hip_atomic_store(a.ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
@@ -674,7 +675,7 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         int go = 1;
         while (__hip_atomic_load(a.ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-            if (__builtin_amdgcn_s_memrealtime() - t0 > ROUTE_WAIT) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) {
                 __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 go = 0;
                 break;
@@ -900,6 +901,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     as.renorm = c->moe_renorm; as.routed_scale = c->routed_scale; as.route = L->route;
     as.idx = L->idx; as.wt = L->wt; as.uidx = idx; as.uwt = wt; as.T = T;
     a2.route = L->route; a2.ready = &L->route->ready; a2.err = &L->route->err;
+    a2.wait_ticks = L->wait_ticks; a2.publish = !L->no_publish;
     a2.experts = L->experts; a2.expert_bytes = L->expert_bytes;
     a2.gate_off = L->gate_off; a2.up_off = L->up_off;
     a2.xB = L->xB; a2.actB = L->actB; a2.T = T; a2.H = H; a2.I = I;

@@ -48,6 +48,7 @@ extern "C" {
 #define K3X_DECODE_MAX_T 8       /* tokens per call on the decode path (2 columns each) */
 #define K3X_STAGE_MAX    65536   /* bytes of activation fragments a workgroup stages in LDS */
 #define K3X_MAX_TOPK     64      /* K3_MAX_TOPK, k3.h:857-864 */
+#define K3X_ROUTE_WAIT_DEFAULT 5000000ull  /* 50 ms at 100 MHz: decode's bound on the wait */
 /* byte sizes of the tiled formats */
 static inline size_t k3x_fp4_tile_bytes(int K)
 {
@@ -117,6 +118,10 @@ struct k3x_moe_layer {
     uint16_t *shB;                /* B set of the shared activation (SI/128 quads) */
     k3x_prefill_buf pf;
     size_t    bytes;
+    /* decode: bound on the routed workgroups' wait for the published selection (ticks of
+     * the 100 MHz clock), and a failure-injection switch that withholds the flag */
+    uint64_t  wait_ticks;
+    int       no_publish;
     /* timing */
     int       timing;
     void     *ev[8];

@@ -152,6 +152,7 @@ static int new_layer(const k3x_cfg *c, int device, k3x_moe_layer **out)
     if (!L) return K3X_E_NOMEM;
     L->cfg = *c;
     L->device = device;
+    L->wait_ticks = K3X_ROUTE_WAIT_DEFAULT;
     if ((rc = layer_alloc(L))) { layer_free(L); return rc; }
     *out = L;
     return 0;
@@ -360,6 +361,14 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     if (T <= L->tdec)
         return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, NULL, 0.0f, stream);
     return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
+}
+
+int k3x_moe_layer_set_route_wait(k3x_moe_layer *L, unsigned long long ticks, int publish)
+{
+    if (!L) return K3X_E_ARG;
+    L->wait_ticks = ticks;
+    L->no_publish = !publish;
+    return 0;
 }
 
 int k3x_moe_layer_check(k3x_moe_layer *L)

@@ -30,7 +30,7 @@ EXPORTS = [
     "k3x_moe_prefill", "k3x_expert_drops", "k3x_synth_layer_create", "k3x_synth_key",
     "k3x_synth_normal_f32", "k3x_synth_normal_bf16", "k3x_moe_layer_set_timing",
     "k3x_moe_layer_last_ms", "k3x_stack_create", "k3x_stack_forward", "k3x_stack_destroy",
-    "k3x_moe_layer_check",
+    "k3x_moe_layer_check", "k3x_moe_layer_set_route_wait",
 ]
 
 
@@ -104,6 +104,7 @@ def lib():
         L.k3x_synth_normal_bf16.restype = None
         L.k3x_moe_layer_set_timing.argtypes = [vp, i]
         L.k3x_moe_layer_check.argtypes = [vp]
+        L.k3x_moe_layer_set_route_wait.argtypes = [vp, C.c_ulonglong, i]
         L.k3x_moe_layer_last_ms.argtypes = [vp, C.POINTER(C.c_float)]
         L.k3x_stack_create.argtypes = [C.POINTER(vp), C.POINTER(vp), i, f, i, C.POINTER(vp)]
         L.k3x_stack_forward.argtypes = [vp, vp, i, vp]
@@ -248,6 +249,12 @@ class MoELayer:
         """Raise if a decode call since the last check had a workgroup give up waiting for
         the published selection (K3X_E_WAIT)."""
         _check(lib().k3x_moe_layer_check(self.h), "k3x_moe_layer_check")
+
+    def set_route_wait(self, ticks, publish=True):
+        """Failure injection: bound of the decode wait in 100 MHz ticks; publish=False
+        withholds the selection's flag (calls made so are not valid)."""
+        _check(lib().k3x_moe_layer_set_route_wait(self.h, ticks, 1 if publish else 0),
+               "k3x_moe_layer_set_route_wait")
 
     def set_timing(self, on):
         _check(lib().k3x_moe_layer_set_timing(self.h, 1 if on else 0), "set_timing")

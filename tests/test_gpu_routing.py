@@ -61,3 +61,28 @@ def test_fewer_selectable_than_slots(torch, k3x):
     idx = check(torch, k3x, L, "few")
     for t in range(idx.shape[0]):
         assert sorted(idx[t][:3]) == [5, 9, 14] and idx[t][3] == 0
+
+
+def test_wait_bound_reports_and_recovers(torch, k3x):
+    """Failure handling of the decode wait, forced from the host: the selection's flag is
+    withheld and the bound set to 2 us, so every routed workgroup gives up (and exits);
+    the check reports K3X_E_WAIT once, and the next call with the defaults is valid."""
+    say("case: decode wait bound forced (flag withheld, 2 us), then restored")
+    L = synth.tiny(seed=34)
+    layer = bank_layer(k3x, L)
+    x = L.x(2, bf16=False, stream_sub=12)
+    o, idx, _, _ = L.oracle_moe(x)
+    layer.set_route_wait(200, publish=False)
+    xt = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    out = torch.empty_like(xt)
+    layer.forward(out.data_ptr(), xt.data_ptr(), 2, k3x.K3X_F32)
+    torch.cuda.synchronize()
+    with pytest.raises(k3x.K3XError) as ei:
+        layer.check()
+    assert "gave up waiting" in str(ei.value)
+    layer.check()                           # reported once
+    layer.set_route_wait(5000000, publish=True)
+    out2, i2, _ = dev_forward(torch, k3x, layer, x)
+    assert np.array_equal(i2, idx)
+    assert synth.rel_l2(out2, o) < TOL
+    layer.close()

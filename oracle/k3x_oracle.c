@@ -250,42 +250,81 @@ void ko_matmul_f32(float *y, const float *x, const float *W, int in, int out)
 }
 
 /* --------------------------------------------------------------- MoE layer ---- */
-/* The identity latent projections of the K2 emulation are exact: row o of an identity
- * matrix has one non-zero product (1 * v, exact) and fifteen accumulators of signed zeros,
- * so k3_tree16 returns v and (float) gives v back; the batched tiles are bit-identical
- * to the single-position GEMV (k3.h:437-444).  So z = x and out = accL before the shared
- * expert is added, for every finite aggregate. */
+/* k3_moe / k3_moe_prefill (k3_ops.c:1862-1952, 2008-2132).  The LatentMoE order
+ * (k3_ops.c:1793-1811): route on the full-width x; z = down . x; the selected experts at
+ * the latent width, their outputs summed in float in top-k order; RMSNorm of that
+ * aggregate when latent_norm; out = up . aggregate; then the shared expert on the
+ * ORIGINAL x, added unweighted.  Every trunk product (down, up, sh1, sh3, sh2) is the
+ * reference's k3_mmw_batch, which is bit-identical per position to the single-position
+ * GEMV (k3.h:437-444), so the oracle applies ko_matmul_bf16 / ko_matmul_f32 per token.
+ *
+ * With cfg.latent == 0 there is no projection: the reference's K2 emulation uses identity
+ * down/up, and those products are exact (row o of an identity matrix has one non-zero
+ * product, 1 * v, and fifteen accumulators of signed zeros, so k3_tree16 returns v and
+ * (float) gives v back), so z = x and out = aggregate before the shared expert. */
 
 typedef struct {
-    float *gu, *act, *edn, *sgu, *sdn;
+    float *gu, *act, *edn, *sgu, *sdn, *z, *acc;
 } moe_tmp;
+
+static int latent_of(const ko_cfg *c) { return c->latent > 0 ? c->latent : c->hidden; }
 
 static int moe_tmp_alloc(moe_tmp *m, const ko_cfg *c)
 {
     const size_t I = (size_t)c->moe_inter, H = (size_t)c->hidden;
+    const size_t L = (size_t)latent_of(c);
     const size_t SI = I * (size_t)c->n_shared;
     m->gu  = (float *)malloc(2 * I * sizeof(float));
     m->act = (float *)malloc(I * sizeof(float));
-    m->edn = (float *)malloc(H * sizeof(float));
-    m->sgu = (float *)malloc(2 * SI * sizeof(float));
+    m->edn = (float *)malloc(L * sizeof(float));
+    m->sgu = (float *)malloc((2 * SI + 1) * sizeof(float));
     m->sdn = (float *)malloc(H * sizeof(float));
-    return (m->gu && m->act && m->edn && m->sgu && m->sdn) ? 0 : -1;
+    m->z   = (float *)malloc(L * sizeof(float));
+    m->acc = (float *)malloc(L * sizeof(float));
+    return (m->gu && m->act && m->edn && m->sgu && m->sdn && m->z && m->acc) ? 0 : -1;
 }
 
 static void moe_tmp_free(moe_tmp *m)
 {
-    free(m->gu); free(m->act); free(m->edn); free(m->sgu); free(m->sdn);
+    free(m->gu); free(m->act); free(m->edn); free(m->sgu); free(m->sdn); free(m->z);
+    free(m->acc);
 }
 
-/* One expert applied to one token: k3_ops.c:1928-1931 (gate, up, SiTU, down). */
-static void expert_apply(float *edn, const float *xt, const ko_expert *q, const ko_cfg *c,
-                         const moe_tmp *m)
+/* A trunk product (k3_mmw_batch per position): bf16 or fp32 weights. */
+static void trunk_mm(float *y, const float *x, const void *W, int f32, int in, int out)
 {
-    const int H = c->hidden, I = c->moe_inter;
-    ko_matmul_mxfp4(m->gu,     xt, q->p1, q->s1, H, I, c->group);
-    ko_matmul_mxfp4(m->gu + I, xt, q->p3, q->s3, H, I, c->group);
+    if (f32) ko_matmul_f32(y, x, (const float *)W, in, out);
+    else     ko_matmul_bf16(y, x, (const uint16_t *)W, in, out);
+}
+
+/* Expert e fetched for use: 0, or non-zero for a drop (the get() contract).  The
+ * resident fp32 bank needs no fetch (k3_ops.c:1932-1938). */
+static int expert_get(const ko_weights *w, int e, ko_expert *q)
+{
+    if (!w->get) { memset(q, 0, sizeof *q); return 0; }
+    return w->get(w->ctx, e, q);
+}
+
+/* One expert applied to one latent row z: k3_ops.c:1928-1931 (MXFP4 gate, up, SiTU,
+ * down) or :1932-1938 (the resident fp32 bank through k3_matmul). */
+static void expert_apply(float *edn, const float *z, int e, const ko_expert *q,
+                         const ko_cfg *c, const ko_weights *w, const moe_tmp *m)
+{
+    const int L = latent_of(c), I = c->moe_inter;
+    if (!w->get) {
+        const float *e1 = w->w1 + (size_t)e * I * L;
+        const float *e3 = w->w3 + (size_t)e * I * L;
+        const float *e2 = w->w2 + (size_t)e * L * I;
+        ko_matmul_f32(m->gu,     z, e1, L, I);
+        ko_matmul_f32(m->gu + I, z, e3, L, I);
+        ko_situ_glu(m->act, m->gu, I, c->situ_b1, c->situ_b2);
+        ko_matmul_f32(edn, m->act, e2, I, L);
+        return;
+    }
+    ko_matmul_mxfp4(m->gu,     z, q->p1, q->s1, L, I, c->group);
+    ko_matmul_mxfp4(m->gu + I, z, q->p3, q->s3, L, I, c->group);
     ko_situ_glu(m->act, m->gu, I, c->situ_b1, c->situ_b2);
-    ko_matmul_mxfp4(edn, m->act, q->p2, q->s2, I, H, c->group);
+    ko_matmul_mxfp4(edn, m->act, q->p2, q->s2, I, L, c->group);
 }
 
 /* moe_shared, k3_ops.c:1848-1860: [sh1.x | sh3.x], SiTU over the gate half, sh2, then
@@ -295,37 +334,57 @@ static void shared_add(float *out, const float *xt, const ko_cfg *c, const ko_we
 {
     const int H = c->hidden, SI = c->moe_inter * c->n_shared;
     if (!w->sh1 || c->n_shared <= 0) return;
-    ko_matmul_bf16(m->sgu,      xt, w->sh1, H, SI);
-    ko_matmul_bf16(m->sgu + SI, xt, w->sh3, H, SI);
+    trunk_mm(m->sgu,      xt, w->sh1, w->trunk_f32, H, SI);
+    trunk_mm(m->sgu + SI, xt, w->sh3, w->trunk_f32, H, SI);
     ko_situ_glu(m->sgu, m->sgu, SI, c->situ_b1, c->situ_b2);
-    ko_matmul_bf16(m->sdn, m->sgu, w->sh2, SI, H);
+    trunk_mm(m->sdn, m->sgu, w->sh2, w->trunk_f32, SI, H);
     for (int i = 0; i < H; i++) out[i] += m->sdn[i];
 }
 
-/* k3_moe, k3_ops.c:1862-1952, with latent = hidden and identity down/up. */
+/* The latent input of token xt: down . x, or x itself without a projection. */
+static const float *latent_in(const float *xt, const ko_cfg *c, const ko_weights *w,
+                              float *z)
+{
+    if (c->latent <= 0) return xt;
+    trunk_mm(z, xt, w->down, w->trunk_f32, c->hidden, c->latent);
+    return z;
+}
+
+/* After the routed aggregate acc of one token: the latent RMSNorm (k3_ops.c:1946), then
+ * out = up . acc (:1950); without a projection acc already is out. */
+static void latent_out(float *out, float *acc, const ko_cfg *c, const ko_weights *w)
+{
+    const int L = latent_of(c);
+    if (c->latent_norm) ko_rmsnorm(acc, acc, w->latent_norm, L, c->rms_eps);
+    if (c->latent > 0) trunk_mm(out, acc, w->up, w->trunk_f32, L, c->hidden);
+}
+
 long ko_moe(float *out, const float *x, int T, const ko_cfg *c, const ko_weights *w,
             int *idx, float *wt)
 {
-    const int H = c->hidden, K = c->topk;
+    const int H = c->hidden, K = c->topk, L = latent_of(c);
     long drops = 0;
     moe_tmp m;
     if (moe_tmp_alloc(&m, c)) abort();
     for (int t = 0; t < T; t++) {
         const float *xt = x + (size_t)t * H;
-        float *acc = out + (size_t)t * H;
+        float *ot = out + (size_t)t * H;
+        float *acc = c->latent > 0 ? m.acc : ot;
         int *it = idx + (size_t)t * K;
         float *wtt = wt + (size_t)t * K;
+        const float *z = latent_in(xt, c, w, m.z);
         ko_router(it, wtt, xt, w->gate, w->bias, H, c->n_experts, K, c->renorm,
                   c->routed_scale);
-        for (int i = 0; i < H; i++) acc[i] = 0.0f;
+        for (int i = 0; i < L; i++) acc[i] = 0.0f;
         for (int j = 0; j < K; j++) {
             ko_expert q;
-            if (w->get(w->ctx, it[j], &q) != 0) { drops++; continue; }
-            expert_apply(m.edn, xt, &q, c, &m);
+            if (expert_get(w, it[j], &q) != 0) { drops++; continue; }
+            expert_apply(m.edn, z, it[j], &q, c, w, &m);
             const float wj = wtt[j];
-            for (int i = 0; i < H; i++) acc[i] += wj * m.edn[i];
+            for (int i = 0; i < L; i++) acc[i] += wj * m.edn[i];
         }
-        shared_add(acc, xt, c, w, &m);
+        latent_out(ot, acc, c, w);
+        shared_add(ot, xt, c, w, &m);
     }
     moe_tmp_free(&m);
     return drops;
@@ -345,23 +404,27 @@ long ko_moe_prefill(float *out, const float *x, int T, const ko_cfg *c,
         if (n_get) *n_get = (long)T * c->topk;
         return d;
     }
-    const int H = c->hidden, K = c->topk;
+    const int H = c->hidden, K = c->topk, L = latent_of(c);
     const int nmax = T < KO_DEDUP_CHUNK ? T : KO_DEDUP_CHUNK;
-    float *contrib = (float *)malloc((size_t)nmax * K * H * sizeof(float));
+    float *contrib = (float *)malloc((size_t)nmax * K * L * sizeof(float));
+    float *zc = (float *)malloc((size_t)nmax * L * sizeof(float));
     int *uniq = (int *)malloc((size_t)nmax * K * sizeof(int));
     char *seen = (char *)malloc((size_t)c->n_experts);
     int *ridx = (int *)malloc((size_t)nmax * K * sizeof(int));
     moe_tmp m;
-    if (!contrib || !uniq || !seen || !ridx || moe_tmp_alloc(&m, c)) abort();
+    if (!contrib || !zc || !uniq || !seen || !ridx || moe_tmp_alloc(&m, c)) abort();
     long drops = 0;
     for (int t0 = 0; t0 < T; t0 += KO_DEDUP_CHUNK) {
         const int n = (T - t0) < KO_DEDUP_CHUNK ? (T - t0) : KO_DEDUP_CHUNK;
         memset(seen, 0, (size_t)c->n_experts);
         int nu = 0;
+        const float *zt[KO_DEDUP_CHUNK];
         for (int t = 0; t < n; t++) {
+            const float *xt = x + (size_t)(t0 + t) * H;
+            zt[t] = latent_in(xt, c, w, zc + (size_t)t * L);
             int *it = idx + (size_t)(t0 + t) * K;
-            ko_router(it, wt + (size_t)(t0 + t) * K, x + (size_t)(t0 + t) * H, w->gate,
-                      w->bias, H, c->n_experts, K, c->renorm, c->routed_scale);
+            ko_router(it, wt + (size_t)(t0 + t) * K, xt, w->gate, w->bias, H, c->n_experts,
+                      K, c->renorm, c->routed_scale);
             for (int j = 0; j < K; j++) {
                 ridx[t * K + j] = it[j];
                 const int e = it[j];
@@ -372,7 +435,7 @@ long ko_moe_prefill(float *out, const float *x, int T, const ko_cfg *c,
             const int e = uniq[u];
             ko_expert q;
             gets++;
-            if (w->get(w->ctx, e, &q) != 0) {
+            if (expert_get(w, e, &q) != 0) {
                 drops++;
                 for (int i = 0; i < n * K; i++) if (ridx[i] == e) ridx[i] = -1;
                 continue;
@@ -380,26 +443,27 @@ long ko_moe_prefill(float *out, const float *x, int T, const ko_cfg *c,
             for (int t = 0; t < n; t++)
                 for (int j = 0; j < K; j++) {
                     if (ridx[t * K + j] != e) continue;
-                    expert_apply(contrib + ((size_t)t * K + j) * H,
-                                 x + (size_t)(t0 + t) * H, &q, c, &m);
+                    expert_apply(contrib + ((size_t)t * K + j) * L, zt[t], e, &q, c, w, &m);
                 }
         }
         for (int t = 0; t < n; t++) {
-            float *acc = out + (size_t)(t0 + t) * H;
+            float *ot = out + (size_t)(t0 + t) * H;
+            float *acc = c->latent > 0 ? m.acc : ot;
             const float *wtt = wt + (size_t)(t0 + t) * K;
-            for (int i = 0; i < H; i++) acc[i] = 0.0f;
+            for (int i = 0; i < L; i++) acc[i] = 0.0f;
             for (int j = 0; j < K; j++) {
                 if (ridx[t * K + j] < 0) continue;
                 const float wj = wtt[j];
-                const float *cb = contrib + ((size_t)t * K + j) * H;
-                for (int i = 0; i < H; i++) acc[i] += wj * cb[i];
+                const float *cb = contrib + ((size_t)t * K + j) * L;
+                for (int i = 0; i < L; i++) acc[i] += wj * cb[i];
             }
+            latent_out(ot, acc, c, w);
         }
     }
     for (int t = 0; t < T; t++)
         shared_add(out + (size_t)t * H, x + (size_t)t * H, c, w, &m);
     moe_tmp_free(&m);
-    free(contrib); free(uniq); free(seen); free(ridx);
+    free(contrib); free(zc); free(uniq); free(seen); free(ridx);
     if (n_get) *n_get = gets;
     return drops;
 }

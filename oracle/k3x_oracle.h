@@ -8,10 +8,12 @@
  * (src/core/k3_ops.c) with the same floating-point contract: the same accumulator
  * partition, the same reduction tree, the same float/double conversions, compiled with
  * -ffp-contract=off and without -ffast-math.  The file:line each one follows is in its
- * comment.  The K2-class layer (no latent, SwiGLU, one shared expert) is expressed the
- * way the reference's own k3_moe computes it with latent = hidden, identity down/up
- * projections and SiTU betas of 2^64; ko_moe and ko_moe_prefill are that computation
- * with the identity products written out (they are exact, see k3x_oracle.c).
+ * comment.  ko_moe / ko_moe_prefill follow k3_moe / k3_moe_prefill for both forms of the
+ * layer: the K3 LatentMoE (cfg.latent > 0: down projection, experts at the latent width,
+ * aggregate RMSNorm, up projection, SiTU betas) and the K2-class layer (cfg.latent == 0:
+ * no latent, SwiGLU, one shared expert), which the reference computes with latent =
+ * hidden, identity down/up and SiTU betas of 2^64; the oracle writes the identity
+ * products out (they are exact, see k3x_oracle.c).
  *
  * Parity status of each function (how it is pinned) is stated in its comment.
  */
@@ -50,6 +52,10 @@ typedef struct {
     float routed_scale;
     float situ_b1, situ_b2;        /* 2^64 for SwiGLU */
     int   group;                   /* MXFP4 group, 32 */
+    /* the LatentMoE fields (K3Cfg, k3.h:94-102); all zero for the K2 form */
+    int   latent;                  /* routed-expert width; 0: no projection (z = x) */
+    int   latent_norm;             /* 1: RMSNorm of the routed aggregate (k3_ops.c:1946) */
+    float rms_eps;
 } ko_cfg;
 
 typedef struct {
@@ -65,8 +71,15 @@ typedef struct {
     const float    *gate, *bias;   /* [n_experts][hidden] fp32, [n_experts] fp32 */
     ko_get_fn       get;
     void           *ctx;
-    const uint16_t *sh1, *sh3;     /* bf16 [n_shared*I][hidden] */
-    const uint16_t *sh2;           /* bf16 [hidden][n_shared*I] */
+    const void     *sh1, *sh3;     /* [n_shared*I][hidden] */
+    const void     *sh2;           /* [hidden][n_shared*I] */
+    /* LatentMoE (K3MoeW, k3.h:546-569): used when cfg.latent > 0 */
+    const void     *down, *up;     /* [latent][hidden], [hidden][latent] */
+    const float    *latent_norm;   /* [latent] fp32 */
+    int             trunk_f32;     /* 0: down/up/sh* are bf16 (K3_WBF16); 1: fp32 */
+    /* resident fp32 expert bank (the reference's w1/w3/w2, fixtures only), used when
+     * get is NULL: w1/w3 [n_experts][I][latent], w2 [n_experts][latent][I] */
+    const float    *w1, *w3, *w2;
 } ko_weights;
 
 /* Per token: route, run the top-k experts, combine in top-k order, add the shared

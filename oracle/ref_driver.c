@@ -2,8 +2,8 @@
  *
  * Built only by oracle/Makefile's `ref` target, together with the reference's own
  * src/core/k3_ops.c compiled where it lies, into oracle/_ref/libk3ref.so.  It exists so
- * the tests can run the reference's k3_moe / k3_moe_prefill on a K2-class layer and
- * compare the oracle's restatement against it bit for bit.
+ * the tests can run the reference's k3_moe / k3_moe_prefill on a K2-class layer or a K3
+ * LatentMoE layer and compare the oracle's restatement against it bit for bit.
  *
  * The K2 layer is expressed with the reference's own types (k3.h:94-102, 507-569):
  * latent = hidden with bf16 identity down/up projections, latent_norm off, SiTU betas
@@ -104,6 +104,68 @@ long refdrv_moe(float *out, const float *x, int T, int hidden, int n_experts, in
     if (gets) *gets = s.gets;
     free(scratch);
     free(eye);
+    return dd;
+}
+
+/* The layer in general form (the K3 LatentMoE, or anything K3Cfg expresses): k3_moe
+ * (prefill == 0) or k3_moe_prefill (prefill == 1) with the trunk matrices down/up/sh*
+ * as given (bf16 when trunk_f32 == 0, else fp32) and experts from the same get() source
+ * as refdrv_moe.  Same return and outputs as refdrv_moe. */
+typedef struct {
+    int   hidden, latent, n_experts, topk, inter, n_shared, renorm, latent_norm;
+    float routed_scale, rms_eps, situ_b1, situ_b2;
+} drv_cfg;
+
+long refdrv_moe_cfg(float *out, const float *x, int T, const drv_cfg *dc, const float *gate,
+                    const float *bias, const drv_expert *bank, const int *fail,
+                    const void *down, const void *up, const float *lnorm, const void *sh1,
+                    const void *sh3, const void *sh2, int trunk_f32, int prefill, int *idx,
+                    float *wt, long *gets)
+{
+    K3Cfg c;
+    memset(&c, 0, sizeof c);
+    c.hidden = dc->hidden;
+    c.latent = dc->latent;
+    c.n_experts = dc->n_experts;
+    c.topk = dc->topk;
+    c.moe_inter = dc->inter;
+    c.n_shared = dc->n_shared;
+    c.routed_scale = dc->routed_scale;
+    c.moe_renorm = dc->renorm;
+    c.latent_norm = dc->latent_norm;
+    c.situ_b1 = dc->situ_b1;
+    c.situ_b2 = dc->situ_b2;
+    c.rms_eps = dc->rms_eps;
+
+    drv_src s;
+    memset(&s, 0, sizeof s);
+    s.src.get = drv_get;
+    s.bank = bank;
+    s.n = dc->n_experts;
+    s.fail = fail;
+
+    K3MoeW w;
+    memset(&w, 0, sizeof w);
+    w.gate = gate;
+    w.bias = bias;
+    w.down = down;
+    w.up = up;
+    w.latent_norm = lnorm;
+    w.sh1 = sh1;
+    w.sh3 = sh3;
+    w.sh2 = sh2;
+    w.wdt = trunk_f32 ? K3_WF32 : K3_WBF16;
+    w.src = &s.src;
+    w.layer = 0;
+
+    float *scratch = (float *)malloc(k3_moe_scratch(&c, T) * sizeof(float));
+    if (!scratch) return -1000000;
+    const long d0 = k3_expert_drops;
+    if (prefill) k3_moe_prefill(out, x, &w, &c, T, idx, wt, scratch);
+    else         k3_moe(out, x, &w, &c, T, idx, wt, scratch);
+    const long dd = k3_expert_drops - d0;
+    if (gets) *gets = s.gets;
+    free(scratch);
     return dd;
 }
 

@@ -4,6 +4,8 @@ the reference tree; the GPU side only reads the .npz files).
 1. The reference's own op fixtures for this path, converted from JSON to compact .npz
    (data only): tests/fixtures/ops/{router,situ_glu,rmsnorm}.json and
    tests/fixtures/mxfp4.json (real checkpoint MXFP4 bytes with their exact dequant).
+   tests/fixtures/ops/moe.json (the whole LatentMoE block, fp32 experts and trunk) goes
+   to ref_moe_latent.npz.
 2. Whole-layer golden vectors of the K2-class layer computed by the COMPILED REFERENCE
    (oracle/_ref/libk3ref.so: the reference's k3_ops.c, k3_moe/k3_moe_prefill with
    identity latent projections and 2^64 SiTU betas) on seeded synthetic layers:
@@ -12,6 +14,9 @@ the reference tree; the GPU side only reads the .npz files).
      k2_full.npz  hidden 7168, 384 experts top-8, I 2048, 1 shared; 2 bf16 tokens
                   (normal bias) and 2 with Zipf bias; indices, weights, every 16th output
                   row element and an FNV-1a hash of the full output bits.
+   and of the K3 LatentMoE layer, the reference's k3_moe with real down/up projections:
+     k3_tiny.npz  hidden 256, latent 128, 16 experts top-4, I 128, 2 shared, SiTU 4/25,
+                  latent RMSNorm; 6 fp32 tokens; every output, index and weight.
 
 Usage: make -C oracle && make -C oracle ref && python tests/golden/make_golden.py
 """
@@ -64,6 +69,16 @@ def convert_ops():
                         swapped_first64=np.asarray(q["expected_swapped_nibbles"]["first64"], np.float32),
                         lut=np.asarray(q["e2m1_lut"], np.float32), group=q["group_size"],
                         tol_abs=man["tolerance"]["fp32_abs"], tol_rel=man["tolerance"]["fp32_rel"])
+    mo = json.load(open(os.path.join(FIX, "ops", "moe.json")))
+    rec = {k: mo[k] for k in ("hidden", "latent", "moe_inter", "n_experts", "top_k", "n_shared",
+                              "routed_scale", "renorm", "latent_norm", "rms_eps", "situ_b1",
+                              "situ_b2")}
+    for k, v in mo.items():
+        if isinstance(v, dict) and "data" in v:
+            rec[k] = arr(v).astype(np.float32).reshape(v["shape"])
+    rec["tol_abs"] = man["tolerance"]["fp32_abs"]
+    rec["tol_rel"] = man["tolerance"]["fp32_rel"]
+    np.savez_compressed(os.path.join(HERE, "ref_moe_latent.npz"), **rec)
 
 
 def ref_moe(L, x, prefill=False):
@@ -87,6 +102,33 @@ def ref_moe(L, x, prefill=False):
                            ol.ptr(idx, ol.I32P), ol.ptr(wt, ol.F32P), C.byref(gets))
     assert drops == 0
     return out, idx, wt
+
+
+def ref_moe_cfg(L, x, prefill=False):
+    """k3_moe / k3_moe_prefill of the compiled reference on a layer in general form."""
+    ref = ol.ref()
+    T = x.shape[0]
+    bank = (ol.KoExpert * L.E)()
+    keep = []
+    for e in range(L.E):
+        d = L.expert(e)
+        keep.append(d)
+        for k in ("p1", "s1", "p3", "s3", "p2", "s2"):
+            setattr(bank[e], k, d[k].ctypes.data_as(ol.U8P))
+    dc = ol.DrvCfg(L.H, L.latent, L.E, L.K, L.I, L.n_shared, L.renorm, L.latent_norm,
+                   L.routed_scale, L.rms_eps, L.situ_b1, L.situ_b2)
+    out = np.empty_like(x)
+    idx = np.empty(L.K, np.int32)
+    wt = np.empty(L.K, np.float32)
+    gets = C.c_long(0)
+    drops = ref.refdrv_moe_cfg(ol.ptr(out, ol.F32P), ol.ptr(x, ol.F32P), T, C.byref(dc),
+                               ol.ptr(L.gate, ol.F32P), ol.ptr(L.bias, ol.F32P), bank, None,
+                               ol.vptr(L.down), ol.vptr(L.up), ol.ptr(L.lnorm, ol.F32P),
+                               ol.vptr(L.sh1), ol.vptr(L.sh3), ol.vptr(L.sh2), 0,
+                               1 if prefill else 0, ol.ptr(idx, ol.I32P), ol.ptr(wt, ol.F32P),
+                               C.byref(gets))
+    assert drops == 0
+    return out, idx, wt, gets.value
 
 
 def fnv1a(a):
@@ -119,6 +161,17 @@ def k2_tiny():
                         T=8)
 
 
+def k3_tiny():
+    """The small LatentMoE layer (synth.tiny_latent, seed 0): 6 fp32 tokens through the
+    reference's k3_moe in one call; every output, index and weight."""
+    L = synth.tiny_latent(seed=0)
+    x = L.x(6, bf16=False)
+    out = ref_moe_cfg(L, x)[0]
+    idx, wt = route_ref(L, x)
+    np.savez_compressed(os.path.join(HERE, "k3_tiny.npz"), out=out, idx=idx, wt=wt, seed=0,
+                        T=6)
+
+
 def k2_full():
     rec = {}
     for name, kw, sub in (("normal", {}, 0), ("zipf", {"zipf_alpha": 1.0}, 1)):
@@ -143,6 +196,7 @@ if __name__ == "__main__":
     assert ol.ref() is not None, "build oracle/_ref first (make -C oracle ref)"
     convert_ops()
     k2_tiny()
+    k3_tiny()
     if "--no-full" not in sys.argv:
         k2_full()
     print("golden fixtures written to", HERE)

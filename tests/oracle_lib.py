@@ -27,7 +27,8 @@ class KoCfg(C.Structure):
     _fields_ = [("hidden", C.c_int), ("n_experts", C.c_int), ("topk", C.c_int),
                 ("moe_inter", C.c_int), ("n_shared", C.c_int), ("renorm", C.c_int),
                 ("routed_scale", C.c_float), ("situ_b1", C.c_float),
-                ("situ_b2", C.c_float), ("group", C.c_int)]
+                ("situ_b2", C.c_float), ("group", C.c_int), ("latent", C.c_int),
+                ("latent_norm", C.c_int), ("rms_eps", C.c_float)]
 
 
 class KoExpert(C.Structure):
@@ -40,7 +41,22 @@ GET_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.POINTER(KoExpert))
 
 class KoWeights(C.Structure):
     _fields_ = [("gate", F32P), ("bias", F32P), ("get", GET_FN), ("ctx", C.c_void_p),
-                ("sh1", U16P), ("sh3", U16P), ("sh2", U16P)]
+                ("sh1", C.c_void_p), ("sh3", C.c_void_p), ("sh2", C.c_void_p),
+                ("down", C.c_void_p), ("up", C.c_void_p), ("latent_norm", F32P),
+                ("trunk_f32", C.c_int), ("w1", F32P), ("w3", F32P), ("w2", F32P)]
+
+
+class DrvCfg(C.Structure):
+    """drv_cfg of oracle/ref_driver.c: the K3Cfg fields of the MoE block."""
+    _fields_ = [("hidden", C.c_int), ("latent", C.c_int), ("n_experts", C.c_int),
+                ("topk", C.c_int), ("inter", C.c_int), ("n_shared", C.c_int),
+                ("renorm", C.c_int), ("latent_norm", C.c_int), ("routed_scale", C.c_float),
+                ("rms_eps", C.c_float), ("situ_b1", C.c_float), ("situ_b2", C.c_float)]
+
+
+def vptr(a):
+    """Address of an array as a void pointer (None for None)."""
+    return a.ctypes.data if a is not None else None
 
 
 def _load(path):
@@ -124,6 +140,11 @@ def ref():
                                    C.c_int, C.c_float, C.c_int, F32P, F32P,
                                    C.POINTER(KoExpert), I32P, U16P, U16P, U16P, C.c_int,
                                    I32P, F32P, C.POINTER(C.c_long)]
+        lib.refdrv_moe_cfg.restype = C.c_long
+        lib.refdrv_moe_cfg.argtypes = [F32P, F32P, C.c_int, C.POINTER(DrvCfg), F32P, F32P,
+                                       C.POINTER(KoExpert), I32P, C.c_void_p, C.c_void_p,
+                                       F32P, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                       C.c_int, I32P, F32P, C.POINTER(C.c_long)]
         lib.refdrv_k2_tokens.restype = C.c_long
         lib.refdrv_k2_tokens.argtypes = [F32P, F32P, C.c_int, C.c_int, C.c_int, C.c_int,
                                          C.c_int, C.c_int, C.c_float, C.c_int, F32P, F32P,

@@ -1,11 +1,16 @@
-"""Seeded K2-class layers on the host, from the oracle's counter-based generator.
+"""Seeded MoE layers on the host, from the oracle's counter-based generator.
 
 Test infrastructure.  The product library has its own implementation of the same rule
 (k3x_synth_*); tests/test_abi.py checks the two agree bit for bit, so a layer built here
 and one built by k3x_synth_layer_create hold the same weights.
 
 Streams follow include/k3x_moe.h: router 0, bias 1, x 2, sh1 3, sh3 4, sh2 5, norm 6,
-expert codes 10 and scales 11 with sub = 3*expert + {0 gate, 1 up, 2 down}.
+latent down 7, latent up 8, latent norm 9, expert codes 10 and scales 11 with
+sub = 3*expert + {0 gate, 1 up, 2 down}.
+
+A layer with latent > 0 is the K3 LatentMoE form: experts at the latent width, bf16
+down [latent][H] and up [H][latent], the latent RMSNorm weights when latent_norm, and
+SiTU betas; latent == 0 is the K2-class form.
 """
 import ctypes as C
 from dataclasses import dataclass, field
@@ -13,9 +18,9 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from oracle_lib import (F32P, GET_FN, I32P, KoCfg, KoExpert, KoWeights, U8P, U16P, oracle,
-                        ptr)
+                        ptr, vptr)
 
-S_ROUTER, S_BIAS, S_X, S_SH1, S_SH3, S_SH2, S_NORM = range(7)
+S_ROUTER, S_BIAS, S_X, S_SH1, S_SH3, S_SH2, S_NORM, S_DOWN, S_UP, S_LNORM = range(10)
 S_CODES, S_SCALES = 10, 11
 
 
@@ -77,12 +82,26 @@ class Layer:
     shared_sigma: float = 0.02
     routed_scale: float = 2.5
     renorm: int = 1
+    latent: int = 0
+    latent_norm: int = 0
+    situ_b1: float = 2.0 ** 64
+    situ_b2: float = 2.0 ** 64
+    rms_eps: float = 1e-5
+    trunk_sigma: float = 0.02
     gate: np.ndarray = None
     bias: np.ndarray = None
     sh1: np.ndarray = None
     sh3: np.ndarray = None
     sh2: np.ndarray = None
+    down: np.ndarray = None
+    up: np.ndarray = None
+    lnorm: np.ndarray = None
     _cache: dict = field(default_factory=dict)
+
+    @property
+    def XL(self):
+        """The routed experts' width: the latent width, or H without a projection."""
+        return self.latent if self.latent > 0 else self.H
 
     def __post_init__(self):
         H, E, I, SI = self.H, self.E, self.I, self.I * self.n_shared
@@ -98,12 +117,18 @@ class Layer:
             self.sh1 = normal_bf16(SI * H, key(s, l, S_SH1), 0.0, self.shared_sigma).reshape(SI, H)
             self.sh3 = normal_bf16(SI * H, key(s, l, S_SH3), 0.0, self.shared_sigma).reshape(SI, H)
             self.sh2 = normal_bf16(H * SI, key(s, l, S_SH2), 0.0, self.shared_sigma).reshape(H, SI)
+        if self.latent > 0:
+            LT = self.latent
+            self.down = normal_bf16(LT * H, key(s, l, S_DOWN), 0.0, self.trunk_sigma).reshape(LT, H)
+            self.up = normal_bf16(H * LT, key(s, l, S_UP), 0.0, self.trunk_sigma).reshape(H, LT)
+        if self.latent_norm:
+            self.lnorm = normal_f32(self.XL, key(s, l, S_LNORM), 1.0, 0.1)
 
     def expert(self, e):
         """Expert e's six arrays in the reference's row-major layout (cached)."""
         if e in self._cache:
             return self._cache[e]
-        H, I, s, l = self.H, self.I, self.seed, self.layer
+        H, I, s, l = self.XL, self.I, self.seed, self.layer
         d = {}
         for m, (pk, sk, R, Kc) in enumerate((("p1", "s1", I, H), ("p3", "s3", I, H),
                                              ("p2", "s2", H, I))):
@@ -125,7 +150,8 @@ class Layer:
     # ---- the oracle on this layer ------------------------------------------------
     def ko_cfg(self):
         return KoCfg(self.H, self.E, self.K, self.I, self.n_shared, self.renorm,
-                     self.routed_scale, 2.0 ** 64, 2.0 ** 64, 32)
+                     self.routed_scale, self.situ_b1, self.situ_b2, 32, self.latent,
+                     self.latent_norm, self.rms_eps)
 
     def _weights(self, fail=None):
         keep = []
@@ -141,7 +167,8 @@ class Layer:
 
         cb = GET_FN(get)
         w = KoWeights(ptr(self.gate, F32P), ptr(self.bias, F32P), cb, None,
-                      ptr(self.sh1, U16P), ptr(self.sh3, U16P), ptr(self.sh2, U16P))
+                      vptr(self.sh1), vptr(self.sh3), vptr(self.sh2), vptr(self.down),
+                      vptr(self.up), ptr(self.lnorm, F32P), 0)
         return w, cb, keep
 
     def oracle_moe(self, x, prefill=False, fail=None):
@@ -169,6 +196,22 @@ class Layer:
 def tiny(seed=0, **kw):
     """The reference-CPU-path configuration: H 256, 16 experts top-4, I 128, 1 shared."""
     return Layer(H=256, E=16, K=4, I=128, seed=seed, **kw)
+
+
+def tiny_latent(seed=0, **kw):
+    """A small LatentMoE layer: H 256, latent 128, 16 experts top-4, I 128, 2 shared,
+    SiTU betas 4 and 25, the latent RMSNorm."""
+    kw = {"routed_scale": 1.0, "n_shared": 2, "latent": 128, "latent_norm": 1,
+          "situ_b1": 4.0, "situ_b2": 25.0, **kw}
+    return Layer(H=256, E=16, K=4, I=128, seed=seed, **kw)
+
+
+def k3(seed=0, **kw):
+    """The K3 LatentMoE shape: H 7168, latent 3584, 896 experts top-16, I 3072, 2 shared
+    bf16 experts, SiTU betas 4 and 25, the latent RMSNorm, routed_scale 1."""
+    kw = {"routed_scale": 1.0, "n_shared": 2, "latent": 3584, "latent_norm": 1,
+          "situ_b1": 4.0, "situ_b2": 25.0, **kw}
+    return Layer(H=7168, E=896, K=16, I=3072, seed=seed, **kw)
 
 
 def full(seed=0, **kw):

@@ -20,9 +20,14 @@
  * drop instead; see each call).  Thread model: one layer handle is used by one host
  * thread at a time; kernels of one call run in order on the stream given.
  *
- * Variant covered: the K2-class layer (no latent projection, SwiGLU, one or more shared
- * experts in bf16, sigmoid router with a selection bias).  In the reference's terms that
- * is latent = hidden with identity down/up, latent_norm = 0 and situ_b1 = situ_b2 = 2^64.
+ * Variants covered (both with a sigmoid router and a selection bias, MXFP4 routed experts
+ * and bf16 shared experts):
+ *   - the K3 LatentMoE (k3_ops.c:1793-1811): route on the full width, down-project to the
+ *     latent width, routed experts there with SiTU-GLU, the weighted sum RMSNormed, up-
+ *     projected, plus the shared experts on the original input (cfg.latent > 0);
+ *   - the K2-class layer: no latent projection, SwiGLU (cfg.latent == 0, betas 0).  In
+ *     the reference's terms that is latent = hidden with identity down/up, latent_norm =
+ *     0 and situ_b1 = situ_b2 = 2^64.
  */
 #ifndef K3X_MOE_H
 #define K3X_MOE_H
@@ -59,12 +64,20 @@ typedef struct k3x_cfg {
     int   moe_renorm;     /* 1: renormalise the top-k weights */
     float routed_scale;   /* 2.5 */
     int   group;          /* MXFP4 group size; only 32 is supported (K3_MXFP4_GROUP) */
+    /* The LatentMoE fields.  All zero gives the K2-class layer. */
+    int   latent;         /* 3584: the routed experts' width (a multiple of 128);
+                             0: no projection, experts at hidden */
+    int   latent_norm;    /* 1: RMSNorm of the routed aggregate (k3_ops.c:1946) */
+    float rms_eps;        /* that norm's epsilon, 1e-5 */
+    float situ_b1;        /* SiTU-GLU betas (k3_situ_glu, k3_ops.c:148-161): gate cap 4 */
+    float situ_b2;        /*   and up cap 25; 0 (or >= 2^64) leaves that half uncapped,
+                               so 0 and 0 is SwiGLU */
 } k3x_cfg;
 
 /* ---- one routed expert, still MXFP4: K3ExpertQ (k3.h:507-516) ----------------------
  * Row-major [out][in]: packed [rows][in/2] bytes (low nibble = even element),
- * scales [rows][in/group] E8M0 bytes.  p1/s1 gate [I][H], p3/s3 up [I][H],
- * p2/s2 down [H][I]. */
+ * scales [rows][in/group] E8M0 bytes.  With X the experts' width (latent, or hidden
+ * when latent == 0): p1/s1 gate [I][X], p3/s3 up [I][X], p2/s2 down [X][I]. */
 typedef struct k3x_expert_q {
     const unsigned char *p1, *s1;
     const unsigned char *p3, *s3;
@@ -79,17 +92,21 @@ typedef struct k3x_expert_src {
     void *ctx;
 } k3x_expert_src;
 
-/* ---- a layer's weights: the K2 subset of K3MoeW (k3.h:546-569) ----------------------
+/* ---- a layer's weights: K3MoeW (k3.h:546-569) with bf16 trunk matrices --------------
  * gate fp32 [n_experts][hidden], bias fp32 [n_experts] (may be NULL),
  * sh1/sh3 bf16 [n_shared*moe_inter][hidden], sh2 bf16 [hidden][n_shared*moe_inter]
  * (all three NULL when n_shared == 0).  Experts come from src, or from bank
- * ([n_experts] entries) when src is NULL. */
+ * ([n_experts] entries) when src is NULL.  With cfg.latent > 0: down bf16
+ * [latent][hidden], up bf16 [hidden][latent], and latent_norm fp32 [latent] when
+ * cfg.latent_norm (all ignored otherwise). */
 typedef struct k3x_moe_w {
     const float        *gate, *bias;
     const uint16_t     *sh1, *sh3, *sh2;
     k3x_expert_src     *src;
     const k3x_expert_q *bank;
     int                 layer;
+    const uint16_t     *down, *up;
+    const float        *latent_norm;
 } k3x_moe_w;
 
 typedef struct k3x_moe_layer k3x_moe_layer;
@@ -152,7 +169,8 @@ extern long k3x_expert_drops;
  * so any element can be regenerated on its own on the CPU: the router fp32 N(0,
  * router_sigma); the bias N(0, bias_sigma), or Zipf-skewed alpha*(pi(e)+1)^-zipf_s over
  * a seeded permutation pi when zipf_alpha > 0; E2M1 codes uniform over 16; E8M0 scales
- * uniform over [scale_lo, scale_hi]; shared weights bf16 N(0, shared_sigma).
+ * uniform over [scale_lo, scale_hi]; shared weights bf16 N(0, shared_sigma); for a
+ * latent layer, down and up bf16 N(0, trunk_sigma) and latent-norm weights fp32 N(1, 0.1).
  * Expert bytes are generated directly in device memory. */
 typedef struct k3x_synth_spec {
     uint64_t seed;
@@ -164,6 +182,7 @@ typedef struct k3x_synth_spec {
     int      scale_lo;       /* 121 */
     int      scale_hi;       /* 125 */
     double   shared_sigma;   /* 0.02 */
+    double   trunk_sigma;    /* 0.02 */
 } k3x_synth_spec;
 
 int  k3x_synth_layer_create(const k3x_cfg *c, const k3x_synth_spec *s, int device,
@@ -173,8 +192,8 @@ int  k3x_synth_layer_create(const k3x_cfg *c, const k3x_synth_spec *s, int devic
  * tensor of a synthetic layer on the host. */
 enum {
     K3X_STREAM_ROUTER = 0, K3X_STREAM_BIAS = 1, K3X_STREAM_X = 2, K3X_STREAM_SH1 = 3,
-    K3X_STREAM_SH3 = 4, K3X_STREAM_SH2 = 5, K3X_STREAM_NORM = 6,
-    K3X_STREAM_CODES = 10, K3X_STREAM_SCALES = 11
+    K3X_STREAM_SH3 = 4, K3X_STREAM_SH2 = 5, K3X_STREAM_NORM = 6, K3X_STREAM_DOWN = 7,
+    K3X_STREAM_UP = 8, K3X_STREAM_LNORM = 9, K3X_STREAM_CODES = 10, K3X_STREAM_SCALES = 11
 };
 uint64_t k3x_synth_key(uint64_t seed, int layer, int stream, int sub);
 void     k3x_synth_normal_f32(float *dst, size_t n, uint64_t key, double mu, double sigma);

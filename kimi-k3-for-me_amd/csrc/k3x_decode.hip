@@ -419,6 +419,10 @@ struct K1Args {
     int         *ready;            // k2's routing flag, cleared here
     const float *norm_w;           // RMSNorm weights [H] (fp32 x), or NULL
     float        eps;
+    // latent form: z = down . x for the routed experts (k1_zdown)
+    const uint16_t *ldown;         // tiled bf16 [XL][H], or NULL
+    int          XL;
+    uint16_t    *zB;               // compact B set of z over whole super-quads of XL
 };
 
 #define RWAVES 4                     // waves per expert row in the router
@@ -538,6 +542,94 @@ __device__ void k1_router(const K1Args &a, float *lds, float *s_inv)
     }
 }
 
+// One quad of x's B fragments, raw: lane (n, kq) holds token n/2's elements 128q + 32kq +
+// 8t .. +7 for each product t (fp32: two float4; bf16: one 16-byte load, lo lanes zero).
+// Split into bf16 hi/lo only when used, so the loads stay in flight in a ring.
+struct XQ {
+    f32x4 v[4][2];
+};
+
+__device__ __forceinline__ void xq_load(XQ &b, rsrc_t xr, int x_bf16, int H, int NC, int q,
+                                        bool on, int lane)
+{
+    const int n0 = lane & 15, kq = lane >> 4;
+    const int n = n0 < NC ? n0 : 0, tok = n >> 1, hl = n & 1;
+    const uint32_t e0 = (uint32_t)(tok * H + q * 128 + kq * 32);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        if (x_bf16) {
+            const u32x4 r = bload16(xr, on && !hl ? (e0 + 8u * t) * 2u : K3X_OOB);
+            b.v[t][0] = __builtin_bit_cast(f32x4, r);
+        } else {
+            b.v[t][0] = __builtin_bit_cast(f32x4, bload16(xr, on ? (e0 + 8u * t) * 4u : K3X_OOB));
+            b.v[t][1] = __builtin_bit_cast(f32x4, bload16(xr, on ? (e0 + 8u * t) * 4u + 16u : K3X_OOB));
+        }
+    }
+}
+
+__device__ __forceinline__ u32x4 xq_get(const XQ &b, int x_bf16, int t, int lane)
+{
+    if (x_bf16) return __builtin_bit_cast(u32x4, b.v[t][0]);
+    const float v[8] = {b.v[t][0][0], b.v[t][0][1], b.v[t][0][2], b.v[t][0][3],
+                        b.v[t][1][0], b.v[t][1][1], b.v[t][1][2], b.v[t][1][3]};
+    return bfrag_of(v, lane & 1);
+}
+
+// The latent down projection z = down . x (k3_mmw_batch, k3_ops.c:1871) for rows
+// 16*rt .. +15: four waves on interleaved bf16 quads, x's B fragments read from x with
+// each quad's weights; z's hi/lo B fragments into zB for k2's routed products.
+__device__ void k1_down(const K1Args &a, float *lds, int rt)
+{
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    constexpr int NW = NT1 / WAVE;
+    const int nQ = a.H >> 7, NC = 2 * a.T;
+    const int cnt = strided_count(wave, NW, nQ);
+    const rsrc_t rw = make_rsrc(a.ldown + (size_t)rt * 16 * a.H, (uint32_t)nQ * 4096u);
+    const rsrc_t xr = make_rsrc(a.x, (uint32_t)(a.T * a.H * (a.x_bf16 ? 2 : 4)));
+    QB w[2];
+    XQ b[2];
+    auto ld = [&](int i, int k) AI {
+        const bool on = k < cnt;
+        const int q = wave + NW * k;
+        qb_load(w[i], rw, on ? (uint32_t)q * 4096u : K3X_OOB, lane);
+        xq_load(b[i], xr, a.x_bf16, a.H, NC, q, on, lane);
+    };
+    ring_prime<2>(ld);
+    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+    ring_loop<2>(cnt, ld, [&](int i, int k) AI {
+        u32x4 bb[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) bb[t] = xq_get(b[i], a.x_bf16, t, lane);
+        qb_mfma(d, w[i], bb);
+    });
+    float acc[4] = {d[0], d[1], d[2], d[3]};
+    wave_sum_lds<4, NW>(acc, lds, wave, lane);
+    // z's set holds whole super-quads; its quads past XL/128 stay zero
+    const int nSX = ((a.XL >> 7) + 3) >> 2;
+    if (rt == 0)
+        for (uint32_t o = (uint32_t)(a.XL >> 7) * 256u * NC + threadIdx.x * 16u;
+             o < (uint32_t)nSX * 1024u * NC; o += NT1 * 16u)
+            *(u32x4 *)((uint8_t *)a.zB + o) = (u32x4){0u, 0u, 0u, 0u};
+    if (wave != 0) return;
+    per_token<4>(acc, NC, lane, [&](int r0, int tok, const float (&v)[4]) AI {
+        for (int i = 0; i < 4; i++) {
+            uint32_t hi, lo;
+            split_bf16(v[i], hi, lo);
+            const int r = rt * 16 + r0 + i;
+            a.zB[bfrag_off(r, 2 * tok, NC)] = (uint16_t)hi;
+            a.zB[bfrag_off(r, 2 * tok + 1, NC)] = (uint16_t)lo;
+        }
+    });
+}
+
+// The latent form's z = down . x, 16 rows per workgroup.  A launch of its own: folded
+// into k1_router_bset's grid, the two paths' register allocation merges badly (spills).
+__global__ void __launch_bounds__(NT1) k1_zdown(K1Args a)
+{
+    __shared__ float lds[(NT1 / WAVE - 1) * 4 * WAVE];
+    k1_down(a, lds, blockIdx.x);
+}
+
 // Router logits of NT1 / WAVE / RWAVES experts (of the RMSNorm of x when norm_w is given),
 // and a share of x's B set for k2.
 __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
@@ -573,12 +665,15 @@ struct K2Args {
     const uint16_t *sh_gate, *sh_up;
     int            SI;
     uint16_t      *shB;            // compact B set of the shared activation, for k3
+    const uint16_t *rB;            // the routed experts' input set: xB, or z's in the latent form
+    int            XL;             // its width (H, or the latent width)
+    float          b1, b2;         // SiTU betas (0: that half uncapped)
 };
 
 // Shared expert gate and up products for rows 16*rt .. +15 over the full K: four waves on
-// interleaved quads (each wave both matrices of a quad, over one B read); SwiGLU
-// (k3_situ_glu at 2^64 betas, k3_ops.c:148-161) per token and the activation's hi/lo B
-// fragments into shB.  These workgroups come first: they stream while the routed ones
+// interleaved quads (each wave both matrices of a quad, over one B read); SiTU-GLU
+// (k3_situ_glu, k3_ops.c:148-161) per token and the activation's hi/lo B fragments into
+// shB.  These workgroups come first: they stream while the routed ones
 // work out the routing.
 template <bool LDSB>
 __device__ void k2_shared(const K2Args &a, float *lds, int rt)
@@ -621,7 +716,7 @@ __device__ void k2_shared(const K2Args &a, float *lds, int rt)
     per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&v)[8]) AI {
         for (int i = 0; i < 4; i++) {
             uint32_t hi, lo;
-            split_bf16(swiglu(v[i], v[4 + i]), hi, lo);
+            split_bf16(situ(v[i], v[4 + i], a.b1, a.b2), hi, lo);
             const int r = rt * 16 + r0 + i;
             a.shB[bfrag_off(r, 2 * tok, NC)] = (uint16_t)hi;
             a.shB[bfrag_off(r, 2 * tok + 1, NC)] = (uint16_t)lo;
@@ -639,7 +734,7 @@ __device__ void k2_shared(const K2Args &a, float *lds, int rt)
 // word (k3x_moe_layer_check reports it) and leaves without touching the expert weights.
 
 // Gate and up products of 16 rows of one unique expert: four waves on interleaved
-// super-quads; SwiGLU, the token's routing weight for this expert (0 where the token did
+// super-quads; SiTU-GLU, the token's routing weight for this expert (0 where the token did
 // not choose it) and the bf16 hi/lo split into the expert's activation slot.
 template <bool EXACT, bool LDSB, int NE>
 __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
@@ -664,11 +759,11 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     const int nTiles = a.I >> 4;
     const int blk = blockIdx.x - 1 - a.n_sh;
     const int u = blk / nTiles, rt = blk % nTiles;
-    const int nS = ((a.H >> 7) + 3) >> 2;
+    const int nS = ((a.XL >> 7) + 3) >> 2;
     const uint32_t bbytes = (uint32_t)nS * 1024u * NC;
-    if (LDSB) {                        // x's B set into LDS while the routing is worked out
+    if (LDSB) {                        // the input's B set into LDS while the routing is worked out
         Stage<8> st;
-        st.issue(a.xB, bbytes, NT);
+        st.issue(a.rB, bbytes, NT);
         st.commit(NT);
     }
     if (threadIdx.x == 0) {
@@ -689,7 +784,7 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     const k3x_route *rte = a.route;
     if (u >= __hip_atomic_load(&rte->nu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
     const int e = __hip_atomic_load(&rte->uniq[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t tb = (uint32_t)fp4_tile_bytes(a.H);
+    const uint32_t tb = (uint32_t)fp4_tile_bytes(a.XL);
     const uint8_t *ex = a.experts + (size_t)e * a.expert_bytes + (size_t)rt * tb;
     const rsrc_t rg = make_rsrc(ex + a.gate_off, tb);
     const rsrc_t ru = make_rsrc(ex + a.up_off, tb);
@@ -702,7 +797,7 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     };
     ring_prime<2>(ld);
     BFrag<LDSB> bf;
-    bf.init(a.xB, bbytes, NC, lane);
+    bf.init(a.rB, bbytes, NC, lane);
     f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
     ring_loop<2>(cnt, ld, [&](int i, int k) AI {
         sq_mfma2<EXACT, LDSB>(dg, du, g[i], v[i], bf, wave + NW * k);
@@ -722,7 +817,7 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
         const float w = __hip_atomic_load(&rte->wtok[u][tok], __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
         for (int i = 0; i < 4; i++) {
-            const float y = (w == 0.0f) ? 0.0f : w * swiglu(s[i], s[4 + i]);
+            const float y = (w == 0.0f) ? 0.0f : w * situ(s[i], s[4 + i], a.b1, a.b2);
             uint32_t hi, lo;
             split_bf16(y, hi, lo);
             const int r = rt * 16 + r0 + i;
@@ -741,9 +836,9 @@ struct K3Args {
     const uint16_t *sh_down;       // shared expert down matrix (tiled bf16), or NULL
     const uint16_t *shB;           // compact B set of the shared activation
     int            SI;
-    float         *out;
+    float         *out;            // [T][H] (or the latent aggregates [T][XL])
     const float   *resid;
-    int            T, H, I, K;
+    int            T, H, I, K;     // H: the output rows (the latent width in that form)
     uint32_t       lds_bytes;      // LDS for the routed activation sets
     uint32_t       sh_lds;         // LDS for the shared activation set (after them), or 0
 };
@@ -851,6 +946,135 @@ __global__ void __launch_bounds__(NT3) k3_down(K3Args a)
     });
 }
 
+// ------------------------------------------------------------------ K4 (latent form)
+// The routed aggregates' RMSNorm (k3_rmsnorm on the aggregate, k3_ops.c:1946) and their
+// B set for the up projection.  Every workgroup works out 1/rms of every token (a double
+// sum of squares, as the reference), then writes its share of the set.
+struct KNArgs {
+    const float *acc;              // [T][XL]
+    const float *nw;               // [XL], or NULL: no norm
+    float        eps;
+    int          T, XL;
+    uint16_t    *latB;
+};
+
+#define NT4 256
+
+__global__ void __launch_bounds__(NT4) k4_latent_norm(KNArgs a)
+{
+    __shared__ double dl[NT4 / WAVE][K3X_DECODE_MAX_T];
+    __shared__ float s_inv[K3X_DECODE_MAX_T];
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    if (a.nw) {
+        for (int t = 0; t < a.T; t++) {
+            double ss = 0.0;
+            for (int i = threadIdx.x; i < a.XL; i += NT4) {
+                const double v = (double)a.acc[(size_t)t * a.XL + i];
+                ss += v * v;
+            }
+            for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+            if (lane == 0) dl[wave][t] = ss;
+        }
+        __syncthreads();
+        if (threadIdx.x < a.T) {
+            double tot = 0.0;
+            for (int w = 0; w < NT4 / WAVE; w++) tot += dl[w][threadIdx.x];
+            s_inv[threadIdx.x] = (float)(1.0 / sqrt(tot / (double)a.XL + (double)a.eps));
+        }
+        __syncthreads();
+    }
+    const int nS = ((a.XL >> 7) + 3) >> 2;
+    x_to_bset((uint8_t *)a.latB, a.acc, 0, a.XL, 2 * a.T, 4 * nS,
+              blockIdx.x * NT4 + threadIdx.x, gridDim.x * NT4, a.nw, a.nw ? s_inv : nullptr);
+}
+
+// The up projection (k3_ops.c:1950) of the normalised aggregates and the shared expert's
+// down product (moe_shared, :1858) for 16 output rows: eight waves on interleaved bf16
+// quads of `up` and then of the shared down matrix, into two accumulator sets; out =
+// up + shared (:1859), plus the residual.  BL: both B sets staged in LDS (the aggregates'
+// at 0, the shared activation's after it), else each quad's B fragments are read from
+// global memory with its weights.
+struct K4Args {
+    const uint16_t *up;            // tiled bf16 [H][XL]
+    const uint16_t *latB;          // B set of the normalised aggregates
+    const uint16_t *sh_down;       // tiled bf16 [H][SI], or NULL
+    const uint16_t *shB;           // B set of the shared activation
+    float          *out;
+    const float    *resid;
+    int             T, H, XL, SI;
+    uint32_t        lat_lds;       // bytes of the aggregates' set in LDS (BL)
+};
+
+#define K4_LDS_MAX 65536u          // both sets in LDS (with the static reduction area, two workgroups per CU)
+
+template <bool BL>
+__global__ void __launch_bounds__(NT3) k4_up(K4Args a)
+{
+    __shared__ float lds[(NT3 / WAVE - 1) * 8 * WAVE];
+    constexpr int NW = NT3 / WAVE;
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    const int NC = 2 * a.T, rt = blockIdx.x;
+    const int nQL = a.XL >> 7, nQS = a.sh_down ? a.SI >> 7 : 0;
+    const uint32_t lbytes = (uint32_t)nQL * 256u * NC, sbytes = (uint32_t)nQS * 256u * NC;
+    Stage<4> st1, st2;
+    if (BL) {
+        st1.issue(a.latB, lbytes, NT3);
+        st2.issue(a.shB, sbytes, NT3);
+    }
+    const int c1 = strided_count(wave, NW, nQL), c2 = strided_count(wave, NW, nQS);
+    const rsrc_t rw1 = make_rsrc(a.up + (size_t)rt * 16 * a.XL, (uint32_t)nQL * 4096u);
+    const rsrc_t rw2 = make_rsrc(nQS ? a.sh_down + (size_t)rt * 16 * a.SI : a.up,
+                                 (uint32_t)nQS * 4096u);
+    const rsrc_t rb1 = make_rsrc(a.latB, lbytes), rb2 = make_rsrc(a.shB, sbytes);
+    const int n = lane & 15, kq = lane >> 4;
+    const uint32_t boff = (uint32_t)((kq * NC + (n < NC ? n : 0)) * 16);
+    QBB r1[2], r2[2];
+    auto ldq = [&](QBB &it, rsrc_t rw, rsrc_t rb, int k, int cnt) AI {
+        const bool on = k < cnt;
+        const int q = wave + NW * k;
+        qb_load(it.a, rw, on ? (uint32_t)q * 4096u : K3X_OOB, lane);
+        if (!BL) {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                it.b[t] = bload16(rb, on ? boff + (uint32_t)(q * 256 * NC + t * 64 * NC) : K3X_OOB);
+        }
+    };
+    auto ld1 = [&](int i, int k) AI { ldq(r1[i], rw1, rb1, k, c1); };
+    auto ld2 = [&](int i, int k) AI { ldq(r2[i], rw2, rb2, k, c2); };
+    ring_prime<2>(ld1);
+    ring_prime<2>(ld2);
+    if (BL) {
+        st1.commit(NT3);
+        st2.commit(NT3, a.lat_lds);
+        __syncthreads();
+    }
+    BFrag<true> bf;
+    bf.init(nullptr, 0u, NC, lane);
+    f32x4 d1 = {0.f, 0.f, 0.f, 0.f}, d2 = {0.f, 0.f, 0.f, 0.f};
+    auto use = [&](f32x4 &d, const QBB &it, uint32_t sbase, int q) AI {
+        if (BL) {
+            u32x4 b[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) b[t] = bf.get(sbase, q, t);
+            qb_mfma(d, it.a, b);
+        } else {
+            qb_mfma(d, it.a, it.b);
+        }
+    };
+    ring_loop<2>(c1, ld1, [&](int i, int k) AI { use(d1, r1[i], 0u, wave + NW * k); });
+    ring_loop<2>(c2, ld2, [&](int i, int k) AI { use(d2, r2[i], a.lat_lds, wave + NW * k); });
+    float acc[8] = {d1[0], d1[1], d1[2], d1[3], d2[0], d2[1], d2[2], d2[3]};
+    wave_sum_lds<8, NW>(acc, lds, wave, lane);
+    if (wave != 0) return;
+    per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&v)[8]) AI {
+        for (int i = 0; i < 4; i++) {
+            const size_t o = (size_t)tok * a.H + rt * 16 + r0 + i;
+            const float y = v[i] + v[4 + i];
+            a.out[o] = a.resid ? a.resid[o] + y : y;
+        }
+    });
+}
+
 // ------------------------------------------------------------------ launcher
 static inline int launch_ok(void) { return hipGetLastError() == hipSuccess ? 0 : K3X_E_HIP; }
 
@@ -876,8 +1100,8 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
 {
     const k3x_cfg *c = &L->cfg;
     hipStream_t s = (hipStream_t)stream;
-    const int H = c->hidden, I = c->moe_inter, NC = 2 * T;
-    const int nQ = H / 128, nS = (nQ + 3) / 4, nSI = (I / 128 + 3) / 4;
+    const int H = c->hidden, I = c->moe_inter, NC = 2 * T, X = L->XL;
+    const int nQ = H / 128, nS = (nQ + 3) / 4, nSI = (I / 128 + 3) / 4, nSX = (X / 128 + 3) / 4;
     int rc;
 
     K1Args a1;
@@ -887,13 +1111,20 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a1.n_rwg = (c->n_experts + NT1 / WAVE / RWAVES - 1) / (NT1 / WAVE / RWAVES);
     a1.ready = &L->route->ready;
     a1.norm_w = norm_w; a1.eps = eps;
-    if (norm_w && (x_dtype == K3X_BF16 || H > RCH * NT1 * 4 || ((uintptr_t)x & 15) ||
+    a1.ldown = L->lat ? L->ldown : NULL; a1.XL = X; a1.zB = L->zB;
+    if (norm_w && (L->lat || x_dtype == K3X_BF16 || H > RCH * NT1 * 4 || ((uintptr_t)x & 15) ||
                    ((uintptr_t)norm_w & 15)))
         return K3X_E_ARG;
     if ((rc = record(L, 0, s))) return rc;
     hipLaunchKernelGGL(k1_router_bset, dim3(a1.n_rwg), dim3(NT1), 0, s, a1);
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 1, s))) return rc;
+    int ev = 2;                        // the next timing event
+    if (L->lat) {
+        hipLaunchKernelGGL(k1_zdown, dim3(X / 16), dim3(NT1), 0, s, a1);
+        if ((rc = launch_ok())) return rc;
+        if ((rc = record(L, ev++, s))) return rc;
+    }
 
     K2Args a2;
     KSArgs &as = a2.ks;
@@ -907,10 +1138,13 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a2.xB = L->xB; a2.actB = L->actB; a2.T = T; a2.H = H; a2.I = I;
     a2.n_sh = L->SI > 0 ? L->SI / 16 : 0;
     a2.sh_gate = L->sh_gate; a2.sh_up = L->sh_up; a2.SI = L->SI; a2.shB = L->shB;
+    a2.rB = L->lat ? L->zB : L->xB; a2.XL = X; a2.b1 = L->b1; a2.b2 = L->b2;
     const int n_routed = T * c->topk * (I / 16);
-    const uint32_t xfp4 = (uint32_t)nS * 1024u * NC;
-    const bool ex2 = (L->special & 3) != 0, st2 = xfp4 <= STAGE_MAX;
-    size_t l2 = st2 ? xfp4 : 0;
+    // the routed input's set and x's (the shared experts'): staged when both fit
+    const uint32_t xset = (uint32_t)nS * 1024u * NC, rset = (uint32_t)nSX * 1024u * NC;
+    const uint32_t bset = xset > rset ? xset : rset;
+    const bool ex2 = (L->special & 3) != 0, st2 = bset <= STAGE_MAX;
+    size_t l2 = st2 ? bset : 0;
     if (l2 < sizeof(KSLds)) l2 = sizeof(KSLds);
     const dim3 g2(1 + a2.n_sh + n_routed);
     if (c->n_experts <= 128)      launch_k2<2>(a2, ex2, st2, g2, l2, s);
@@ -919,23 +1153,49 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     else if (c->n_experts <= 512) launch_k2<8>(a2, ex2, st2, g2, l2, s);
     else                          launch_k2<16>(a2, ex2, st2, g2, l2, s);
     if ((rc = launch_ok())) return rc;
-    if ((rc = record(L, 2, s))) return rc;
+    if ((rc = record(L, ev++, s))) return rc;
 
+    // k3: the routed down products, plus the shared expert's into the same rows (K2 form),
+    // or into the latent aggregates alone (latent form; the shared expert goes to k4)
     K3Args a3;
     a3.experts = L->experts; a3.expert_bytes = L->expert_bytes; a3.down_off = L->down_off;
     a3.route = L->route; a3.actB = L->actB;
-    a3.sh_down = L->SI > 0 ? L->sh_down : NULL; a3.shB = L->shB; a3.SI = L->SI;
-    a3.out = out; a3.resid = resid; a3.T = T; a3.H = H; a3.I = I; a3.K = c->topk;
+    a3.sh_down = (L->SI > 0 && !L->lat) ? L->sh_down : NULL; a3.shB = L->shB; a3.SI = L->SI;
+    a3.out = L->lat ? L->accL : out; a3.resid = L->lat ? NULL : resid;
+    a3.T = T; a3.H = X; a3.I = I; a3.K = c->topk;
     const uint32_t slot = (uint32_t)nSI * 1024u * NC;
     const size_t all = (size_t)T * c->topk * slot;
     a3.lds_bytes = slot <= STAGE_MAX ? (uint32_t)(all < STAGE_MAX ? all : (STAGE_MAX / slot) * slot) : 0u;
     // the shared activation set beside them when two workgroups still fit a CU (without
-    // a shared expert, an empty set)
-    const uint32_t shb = (uint32_t)(L->SI / 128) * 256u * NC;
+    // a shared expert here, an empty set)
+    const uint32_t shb = a3.sh_down ? (uint32_t)(L->SI / 128) * 256u * NC : 0u;
     a3.sh_lds = (a3.lds_bytes && a3.lds_bytes + shb <= K3_LDS_MAX) ? (shb ? shb : 16u) : 0u;
     const size_t l3 = (size_t)a3.lds_bytes + a3.sh_lds;
-    if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(H / 16), dim3(NT3), l3, s, a3);
-    else                hipLaunchKernelGGL(k3_down<false>, dim3(H / 16), dim3(NT3), l3, s, a3);
+    if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(X / 16), dim3(NT3), l3, s, a3);
+    else                hipLaunchKernelGGL(k3_down<false>, dim3(X / 16), dim3(NT3), l3, s, a3);
     if ((rc = launch_ok())) return rc;
-    return record(L, 3, s);
+    if ((rc = record(L, ev++, s))) return rc;
+    if (!L->lat) return 0;
+
+    KNArgs an;
+    an.acc = L->accL; an.nw = c->latent_norm ? L->lnw : NULL; an.eps = c->rms_eps;
+    an.T = T; an.XL = X; an.latB = L->latB;
+    const int nent = 4 * nSX * 16 * NC;
+    hipLaunchKernelGGL(k4_latent_norm, dim3((nent + 4 * NT4 - 1) / (4 * NT4)), dim3(NT4), 0, s, an);
+    if ((rc = launch_ok())) return rc;
+    if ((rc = record(L, ev++, s))) return rc;
+
+    K4Args a4;
+    a4.up = L->lup; a4.latB = L->latB;
+    a4.sh_down = L->SI > 0 ? L->sh_down : NULL; a4.shB = L->shB;
+    a4.out = out; a4.resid = resid; a4.T = T; a4.H = H; a4.XL = X; a4.SI = L->SI;
+    const uint32_t lb = (uint32_t)(X / 128) * 256u * NC;
+    const uint32_t sb = a4.sh_down ? (uint32_t)(L->SI / 128) * 256u * NC : 0u;
+    a4.lat_lds = lb;
+    if (lb + sb <= K4_LDS_MAX)
+        hipLaunchKernelGGL(k4_up<true>, dim3(H / 16), dim3(NT3), (size_t)lb + sb, s, a4);
+    else
+        hipLaunchKernelGGL(k4_up<false>, dim3(H / 16), dim3(NT3), 0, s, a4);
+    if ((rc = launch_ok())) return rc;
+    return record(L, ev, s);
 }

@@ -53,6 +53,18 @@ __device__ __forceinline__ float swiglu(float g, float u)
     return a * u;
 }
 
+// SiTU-GLU as k3_situ_glu computes it (k3_ops.c:148-161): a = b1*tanh(g/b1) * sigmoid(g)
+// (the sigmoid takes the UNCAPPED gate), u' = b2*tanh(u/b2), y = a*u', in float.  tanh
+// is evaluated in double and rounded once.  A beta of 0 leaves its half uncapped, as a
+// beta of 2^64 does in the reference, so betas 0 and 0 give swiglu() exactly.
+__device__ __forceinline__ float situ(float g, float u, float b1, float b2)
+{
+    const float gc = b1 != 0.0f ? b1 * (float)tanh((double)(g / b1)) : g;
+    const float uc = b2 != 0.0f ? b2 * (float)tanh((double)(u / b2)) : u;
+    const float a = gc * sigmoid_ref(g);
+    return a * uc;
+}
+
 // ------------------------------------------------------------------ MXFP4 -> bf16
 // 8 E2M1 codes (one dword, low nibble = lower column) times 2^(s-127) -> 8 bf16, exact
 // for scale bytes 1..252 (v_cvt_scalef32_pk_bf16_fp4 takes the scale as an fp32 power

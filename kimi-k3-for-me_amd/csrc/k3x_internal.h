@@ -6,7 +6,9 @@
  *   router   fp32 [n_experts][hidden]            as given (k3_router's W)
  *   bias     fp32 [n_experts]
  *   experts  n_experts records of K3X tiled MXFP4, each: gate tiles, up tiles, down tiles
+ *            (gate/up [I][X], down [X][I], X = latent or hidden)
  *   shared   bf16 tiled gate, up, down (n_shared*moe_inter intermediate)
+ *   latent   bf16 tiled down [latent][hidden] and up [hidden][latent], fp32 norm weights
  *   work     the per-call buffers (routing, activations in B-fragment layout, partials)
  *
  * K3X TILED MXFP4 (a matrix of R rows by K columns, R % 16 == 0, K % 128 == 0).
@@ -97,6 +99,9 @@ struct k3x_moe_layer {
     k3x_cfg   cfg;
     int       device;
     int       SI;                 /* n_shared * moe_inter */
+    int       XL;                 /* the routed experts' width: cfg.latent, or hidden */
+    int       lat;                /* 1: latent projections (cfg.latent > 0) */
+    float     b1, b2;             /* SiTU betas; 0 where that half is uncapped */
     int       tdec;               /* tokens per decode-path call (<= K3X_DECODE_MAX_T) */
     /* weights */
     float    *router;             /* [E][H] */
@@ -107,6 +112,8 @@ struct k3x_moe_layer {
                                      scale byte outside 1..252 (the exact dequantisation
                                      kernels are launched) */
     uint16_t *sh_gate, *sh_up, *sh_down;   /* tiled bf16, NULL when SI == 0 */
+    uint16_t *ldown, *lup;        /* latent projections, tiled bf16 [XL][H] and [H][XL] */
+    float    *lnw;                /* [XL] latent RMSNorm weights, or NULL */
     /* decode working buffers */
     float    *score, *choice;     /* [DECODE_MAX_T][E] */
     int      *idx;                /* [DECODE_MAX_T][K] */
@@ -116,6 +123,9 @@ struct k3x_moe_layer {
     uint16_t *actB;               /* DECODE_MAX_T*K slots: B set of each unique expert's
                                      activation over whole super-quads of I */
     uint16_t *shB;                /* B set of the shared activation (SI/128 quads) */
+    uint16_t *zB;                 /* latent: B set of z = down . x over whole super-quads */
+    float    *accL;               /* latent: [DECODE_MAX_T][XL] routed aggregates */
+    uint16_t *latB;               /* latent: B set of the (normalised) aggregates */
     k3x_prefill_buf pf;
     size_t    bytes;
     /* decode: bound on the routed workgroups' wait for the published selection (ticks of

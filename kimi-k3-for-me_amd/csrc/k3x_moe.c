@@ -57,15 +57,14 @@ static int cfg_ok(const k3x_cfg *c)
     if (c->group != 32) return K3X_E_SHAPE;
     if (c->topk > K3X_MAX_TOPK || c->topk > c->n_experts) return K3X_E_SHAPE;
     if (c->n_experts > 1024) return K3X_E_SHAPE;
-    /* at least one token's shared activation fits the decode path's LDS set */
-    if ((size_t)c->moe_inter * c->n_shared * 4 > K3X_STAGE_MAX) return K3X_E_SHAPE;
+    if (c->latent < 0 || c->latent % 128) return K3X_E_SHAPE;
     return 0;
 }
 
 static void layout(k3x_moe_layer *L)
 {
-    const int H = L->cfg.hidden, I = L->cfg.moe_inter;
-    const size_t gu = k3x_fp4_matrix_bytes(I, H), dn = k3x_fp4_matrix_bytes(H, I);
+    const int X = L->XL, I = L->cfg.moe_inter;
+    const size_t gu = k3x_fp4_matrix_bytes(I, X), dn = k3x_fp4_matrix_bytes(X, I);
     L->gate_off = 0;
     L->up_off = gu;
     L->down_off = 2 * gu;
@@ -86,13 +85,14 @@ static int layer_alloc(k3x_moe_layer *L)
     const k3x_cfg *c = &L->cfg;
     const int H = c->hidden, E = c->n_experts, I = c->moe_inter, K = c->topk;
     int rc;
+    L->lat = c->latent > 0;
+    L->XL = L->lat ? c->latent : H;
+    /* a beta of 2^64 or more caps nothing any layer produces (b * tanhf(v / b) == v) */
+    L->b1 = (c->situ_b1 >= 0x1p64f || c->situ_b1 <= -0x1p64f) ? 0.0f : c->situ_b1;
+    L->b2 = (c->situ_b2 >= 0x1p64f || c->situ_b2 <= -0x1p64f) ? 0.0f : c->situ_b2;
     layout(L);
     L->SI = c->moe_inter * c->n_shared;
-    /* the decode path builds the shared activation of a call in LDS (4 bytes per token
-     * and intermediate row) */
     L->tdec = K3X_DECODE_MAX_T;
-    if (L->SI > 0 && (size_t)L->SI * 4 * L->tdec > K3X_STAGE_MAX)
-        L->tdec = (int)(K3X_STAGE_MAX / ((size_t)L->SI * 4));
     size_t *b = &L->bytes;
     RCCHK(dmalloc((void **)&L->router, (size_t)E * H * 4, b));
     RCCHK(dmalloc((void **)&L->bias, (size_t)E * 4, b));
@@ -108,6 +108,16 @@ static int layer_alloc(k3x_moe_layer *L)
     RCCHK(dmalloc((void **)&L->idx, (size_t)K3X_DECODE_MAX_T * K * 4, b));
     RCCHK(dmalloc((void **)&L->wt, (size_t)K3X_DECODE_MAX_T * K * 4, b));
     RCCHK(dmalloc((void **)&L->route, sizeof(k3x_route), b));
+    if (L->lat) {
+        const int X = L->XL;
+        const size_t xs = (size_t)(X + 511) / 512 * 512;
+        RCCHK(dmalloc((void **)&L->ldown, k3x_bf16_matrix_bytes(X, H), b));
+        RCCHK(dmalloc((void **)&L->lup, k3x_bf16_matrix_bytes(H, X), b));
+        RCCHK(dmalloc((void **)&L->zB, xs * 2 * K3X_DECODE_MAX_T * 2, b));
+        RCCHK(dmalloc((void **)&L->accL, (size_t)K3X_DECODE_MAX_T * X * 4, b));
+        RCCHK(dmalloc((void **)&L->latB, xs * 2 * K3X_DECODE_MAX_T * 2, b));
+    }
+    if (c->latent_norm) RCCHK(dmalloc((void **)&L->lnw, (size_t)L->XL * 4, b));
     if (hipMemset(L->route, 0, sizeof(k3x_route)) != hipSuccess) return K3X_E_HIP;
     /* B sets of 2*DECODE_MAX_T columns over whole super-quads (512 elements) */
     const size_t hs = (size_t)(H + 511) / 512 * 512, is = (size_t)(I + 511) / 512 * 512;
@@ -124,7 +134,8 @@ static void layer_free(k3x_moe_layer *L)
     if (!L) return;
     void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shB,
                  L->score, L->choice, L->idx, L->wt, L->route,
-                 L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out};
+                 L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out,
+                 L->ldown, L->lup, L->lnw, L->zB, L->accL, L->latB};
     for (size_t i = 0; i < sizeof p / sizeof p[0]; i++)
         if (p[i]) hipFree(p[i]);
     for (int i = 0; i < 8; i++)
@@ -183,6 +194,34 @@ fail:
     return rc;
 }
 
+/* Latent projections: bf16 down [XL][H] and up [H][XL] re-laid out on the device, and the
+ * latent RMSNorm weights.  Nothing without a latent projection (the norm weights are
+ * still taken when latent_norm is set). */
+static int upload_latent(k3x_moe_layer *L, const uint16_t *down, const uint16_t *up,
+                         const float *nw)
+{
+    const int H = L->cfg.hidden, X = L->XL;
+    int rc = 0;
+    void *stage = NULL;
+    if (L->cfg.latent_norm) {
+        if (!nw) return K3X_E_ARG;
+        HIPCHK(hipMemcpy(L->lnw, nw, (size_t)X * 4, hipMemcpyHostToDevice));
+    }
+    if (!L->lat) return 0;
+    if (!down || !up) return K3X_E_ARG;
+    const size_t n = (size_t)X * H * 2;
+    HIPCHK(hipMalloc(&stage, n));
+    HIPCHK(hipMemcpy(stage, down, n, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_bf16(L->ldown, (const uint16_t *)stage, X, H, NULL));
+    HIPCHK(hipDeviceSynchronize());
+    HIPCHK(hipMemcpy(stage, up, n, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_bf16(L->lup, (const uint16_t *)stage, H, X, NULL));
+    HIPCHK(hipDeviceSynchronize());
+fail:
+    if (stage) hipFree(stage);
+    return rc;
+}
+
 /* Bit m of the result: matrix m (0 gate, 1 up, 2 down) has a scale byte outside 1..252,
  * where a weight can be zero-scaled, subnormal-scaled or infinite and the kernels take
  * the exact dequantisation path. */
@@ -199,7 +238,7 @@ static int scale_flags(const k3x_expert_q *q, size_t sg)
 /* One expert: its six arrays copied to a staging area, then tiled into the arena. */
 static int upload_expert(k3x_moe_layer *L, int e, const k3x_expert_q *q, uint8_t *stage)
 {
-    const int H = L->cfg.hidden, I = L->cfg.moe_inter;
+    const int H = L->XL, I = L->cfg.moe_inter;
     const size_t pg = (size_t)I * H / 2, sg = (size_t)I * H / 32;
     uint8_t *base = L->experts + (size_t)e * L->expert_bytes;
     int rc = 0;
@@ -230,12 +269,13 @@ int k3x_moe_layer_create(const k3x_cfg *c, const k3x_moe_w *w, int device,
     k3x_moe_layer *L = NULL;
     int rc = new_layer(c, device, &L);
     if (rc) return rc;
-    const int H = c->hidden, E = c->n_experts, I = c->moe_inter;
+    const int H = c->hidden, E = c->n_experts, I = c->moe_inter, X = L->XL;
     uint8_t *stage = NULL;
     HIPCHK(hipMemcpy(L->router, w->gate, (size_t)E * H * 4, hipMemcpyHostToDevice));
     if (w->bias) HIPCHK(hipMemcpy(L->bias, w->bias, (size_t)E * 4, hipMemcpyHostToDevice));
     RCCHK(upload_shared(L, w->sh1, w->sh3, w->sh2));
-    HIPCHK(hipMalloc((void **)&stage, 3 * ((size_t)I * H / 2 + (size_t)I * H / 32)));
+    RCCHK(upload_latent(L, w->down, w->up, w->latent_norm));
+    HIPCHK(hipMalloc((void **)&stage, 3 * ((size_t)I * X / 2 + (size_t)I * X / 32)));
     for (int e = 0; e < E; e++) {
         k3x_expert_q q;
         if (w->src) {
@@ -251,7 +291,7 @@ int k3x_moe_layer_create(const k3x_cfg *c, const k3x_moe_w *w, int device,
             q = w->bank[e];
         }
         RCCHK(upload_expert(L, e, &q, stage));
-        L->special |= scale_flags(&q, (size_t)I * H / 32);
+        L->special |= scale_flags(&q, (size_t)I * X / 32);
     }
     hipFree(stage);
     *out = L;
@@ -267,7 +307,7 @@ int k3x_moe_layer_read_expert(const k3x_moe_layer *L, int e, unsigned char *p1,
                               unsigned char *p2, unsigned char *s2)
 {
     if (!L || e < 0 || e >= L->cfg.n_experts) return K3X_E_ARG;
-    const int H = L->cfg.hidden, I = L->cfg.moe_inter;
+    const int H = L->XL, I = L->cfg.moe_inter;
     const size_t pg = (size_t)I * H / 2, sg = (size_t)I * H / 32;
     const uint8_t *base = L->experts + (size_t)e * L->expert_bytes;
     uint8_t *st = NULL;
@@ -360,6 +400,22 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     if (T == 0) return 0;
     if (T <= L->tdec)
         return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, NULL, 0.0f, stream);
+    if (L->lat) {
+        /* the latent form has no grouped-GEMM pipeline yet: the decode path over groups of
+         * tdec tokens (results do not depend on the grouping) */
+        const size_t es = x_dtype == K3X_BF16 ? 2 : 4;
+        const int H = L->cfg.hidden, K = L->cfg.topk;
+        for (int t0 = 0; t0 < T; t0 += L->tdec) {
+            const int n = T - t0 < L->tdec ? T - t0 : L->tdec;
+            const int rc = k3x_dev_decode(L, out + (size_t)t0 * H,
+                                          (const char *)x + (size_t)t0 * H * es, x_dtype, n,
+                                          resid ? resid + (size_t)t0 * H : NULL,
+                                          idx ? idx + (size_t)t0 * K : NULL,
+                                          wt ? wt + (size_t)t0 * K : NULL, NULL, 0.0f, stream);
+            if (rc) return rc;
+        }
+        return 0;
+    }
     return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
 }
 
@@ -527,7 +583,7 @@ int k3x_synth_layer_create(const k3x_cfg *c, const k3x_synth_spec *s, int device
     k3x_moe_layer *L = NULL;
     int rc = new_layer(c, device, &L);
     if (rc) return rc;
-    const int H = c->hidden, E = c->n_experts, I = c->moe_inter, SI = L->SI;
+    const int H = c->hidden, E = c->n_experts, I = c->moe_inter, SI = L->SI, X = L->XL;
     float *hf = NULL;
     uint16_t *hb = NULL;
     hf = (float *)malloc((size_t)E * H * 4);
@@ -567,11 +623,33 @@ int k3x_synth_layer_create(const k3x_cfg *c, const k3x_synth_spec *s, int device
         free(hb);
         hb = NULL;
     }
+    if (L->lat || c->latent_norm) {
+        const size_t n = (size_t)X * H;
+        if (L->lat) {
+            hb = (uint16_t *)malloc(n * 2 * 2);
+            if (!hb) { rc = K3X_E_NOMEM; goto fail; }
+            k3x_synth_normal_bf16(hb, n, k3x_synth_key(s->seed, s->layer, K3X_STREAM_DOWN, 0),
+                                  0.0, s->trunk_sigma);
+            k3x_synth_normal_bf16(hb + n, n, k3x_synth_key(s->seed, s->layer, K3X_STREAM_UP, 0),
+                                  0.0, s->trunk_sigma);
+        }
+        if (c->latent_norm) {
+            hf = (float *)malloc((size_t)X * 4);
+            if (!hf) { rc = K3X_E_NOMEM; goto fail; }
+            k3x_synth_normal_f32(hf, (size_t)X, k3x_synth_key(s->seed, s->layer, K3X_STREAM_LNORM, 0),
+                                 1.0, 0.1);
+        }
+        RCCHK(upload_latent(L, hb, hb ? hb + n : NULL, hf));
+        free(hb);
+        hb = NULL;
+        free(hf);
+        hf = NULL;
+    }
     L->special = (s->scale_lo < 1 || s->scale_hi > 252) ? 7 : 0;
     for (int e = 0; e < E; e++) {
         uint8_t *base = L->experts + (size_t)e * L->expert_bytes;
         const struct { size_t off; int R, K, m; } mm[3] = {
-            {L->gate_off, I, H, 0}, {L->up_off, I, H, 1}, {L->down_off, H, I, 2}};
+            {L->gate_off, I, X, 0}, {L->up_off, I, X, 1}, {L->down_off, X, I, 2}};
         for (int i = 0; i < 3; i++)
             RCCHK(k3x_dev_synth_fp4(base + mm[i].off, mm[i].R, mm[i].K,
                                     k3x_synth_key(s->seed, s->layer, K3X_STREAM_CODES, 3 * e + mm[i].m),
@@ -642,7 +720,7 @@ static int stack_record(k3x_stack *S, float *h, int T)
     for (int l = 0; l < S->n && !rc; l++) {
         k3x_moe_layer *L = S->layers[l];
         const float *nw = S->norm_w[l];
-        if (T <= L->tdec && S->H <= 8192 && !((uintptr_t)nw & 15)) {
+        if (T <= L->tdec && !L->lat && S->H <= 8192 && !((uintptr_t)nw & 15)) {
             /* decode: the norm is worked out inside the router launch */
             rc = k3x_dev_decode(L, h, h, K3X_F32, T, h, NULL, NULL, nw, S->eps, S->cap);
         } else {

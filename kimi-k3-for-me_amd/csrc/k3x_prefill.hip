@@ -315,6 +315,7 @@ struct PfGemmArgs {
     int             arows;
     float          *y;          // down output rows [*][R] fp32
     int             out_base;   // output row = out_base + p
+    float           b1, b2;     // SiTU betas of the gate/up epilogue (0: uncapped)
 };
 
 template <bool FP4, int NMAT, int RT>
@@ -535,7 +536,7 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
                 uint32_t hi[4], lo[4];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const float yv = (w == 0.0f) ? 0.0f : w * swiglu(v0[j], v1[j]);
+                    const float yv = (w == 0.0f) ? 0.0f : w * situ(v0[j], v1[j], a.b1, a.b2);
                     split_bf16(yv, hi[j], lo[j]);
                 }
                 const size_t o = ((size_t)(r0 >> 3) * a.arows + (size_t)(a.out_base + p)) * 8 + (r0 & 7);
@@ -754,7 +755,7 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
                     uint32_t hi[4], lo[4];
 #pragma unroll
                     for (int b = 0; b < 4; b++) {
-                        const float yv = (w == 0.0f) ? 0.0f : w * swiglu(v0[b], v1[b]);
+                        const float yv = (w == 0.0f) ? 0.0f : w * situ(v0[b], v1[b], a.b1, a.b2);
                         split_bf16(yv, hi[b], lo[b]);
                     }
                     const size_t o = ((size_t)(r0 >> 3) * a.arows + (size_t)(a.out_base + p)) * 8 + (r0 & 7);
@@ -897,6 +898,7 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     g.R = I; g.K = H; g.desc = (const int4 *)B->desc_gu;
     g.bsrc = B->xp; g.brows = TK; g.perm = NULL; g.row_base = 0;
     g.pw = B->perm_w; g.act = B->act; g.arows = TK; g.out_base = 0;
+    g.b1 = L->b1; g.b2 = L->b2;
     const bool ex_gu = (L->special & 3) != 0;
     PfGemmArgs gb = g;
     g.ntile = B->tb_gu + E;
@@ -934,6 +936,7 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
         sg.R = SI; sg.K = H; sg.n0 = T;
         sg.bsrc = B->xhl; sg.brows = T; sg.row_base = 0;
         sg.act = B->act_sh; sg.arows = T; sg.out_base = 0;
+        sg.b1 = L->b1; sg.b2 = L->b2;
         const int tpb_sg = 4 * 16 / HLg, nrb_sg = cdiv(SI, (PF_NT / WAVE) * 1 * 16);
         const unsigned grid_sg = nrb_sg * cdiv(T, tpb_sg);
         if (HLg == 1)

@@ -5,9 +5,11 @@
  * k3_moe_gpu / k3_moe_prefill_gpu have the signatures of k3_moe / k3_moe_prefill
  * (include/k3/k3.h:629-637).  On first use of a layer they upload it through the
  * layer's own K3ExpertSrc (k3.h:521-544) and keep the handle; afterwards every call runs
- * on the GPU.  Only the K2-class form is accepted: latent == hidden with identity
- * down/up, latent_norm == 0, SiTU betas >= 2^64 (SwiGLU), bf16 shared weights; anything
- * else returns -1 so the caller keeps the CPU path (k3_ops.c:1862, :2008).
+ * on the GPU.  Accepted: bf16 trunk weights (wdt == K3_WBF16) and a streamed expert
+ * source, not a cache-only draft.  A layer with latent == hidden whose down/up are
+ * identity matrices (the K2-class emulation) is uploaded without projections; any other
+ * latent layer with its down/up projections, latent norm and SiTU betas.  Anything else
+ * returns -1 so the caller keeps the CPU path (k3_ops.c:1862, :2008).
  */
 #include "k3.h"
 #include "k3x_moe.h"
@@ -36,11 +38,21 @@ static int adapter_get(k3x_expert_src *self, int layer, int expert, k3x_expert_q
     return 0;
 }
 
-static int k2_form(const K3MoeW *w, const K3Cfg *c)
+static int gpu_form(const K3MoeW *w, const K3Cfg *c)
 {
-    return w->src && w->src->get && c->latent == c->hidden && !c->latent_norm &&
-           c->situ_b1 >= 0x1p64f && c->situ_b2 >= 0x1p64f && w->wdt == K3_WBF16 &&
-           !w->cache_only && w->layer >= 0 && w->layer < K3X_ADAPTER_MAX_LAYERS;
+    return w->src && w->src->get && w->wdt == K3_WBF16 && w->down && w->up &&
+           c->latent > 0 && !w->cache_only && w->layer >= 0 &&
+           w->layer < K3X_ADAPTER_MAX_LAYERS;
+}
+
+/* 1 when the bf16 [n][n] matrix m is the identity (1.0 = 0x3F80 on the diagonal, +0
+ * elsewhere): then the projection is exact and the layer needs none. */
+static int is_identity_bf16(const uint16_t *m, int n)
+{
+    for (size_t r = 0; r < (size_t)n; r++)
+        for (size_t k = 0; k < (size_t)n; k++)
+            if (m[r * n + k] != (r == k ? 0x3F80 : 0)) return 0;
+    return 1;
 }
 
 static k3x_moe_layer *layer_for(const K3MoeW *w, const K3Cfg *c)
@@ -56,6 +68,14 @@ static k3x_moe_layer *layer_for(const K3MoeW *w, const K3Cfg *c)
     kc.moe_renorm = c->moe_renorm;
     kc.routed_scale = c->routed_scale;
     kc.group = K3_MXFP4_GROUP;
+    const uint16_t *down = (const uint16_t *)w->down, *up = (const uint16_t *)w->up;
+    const int plain = c->latent == c->hidden && is_identity_bf16(down, c->hidden) &&
+                      is_identity_bf16(up, c->hidden);
+    kc.latent = plain ? 0 : c->latent;
+    kc.latent_norm = c->latent_norm;
+    kc.rms_eps = c->rms_eps;
+    kc.situ_b1 = c->situ_b1;
+    kc.situ_b2 = c->situ_b2;
     adapter_src as;
     memset(&as, 0, sizeof as);
     as.base.get = adapter_get;
@@ -69,6 +89,9 @@ static k3x_moe_layer *layer_for(const K3MoeW *w, const K3Cfg *c)
     kw.sh2 = (const uint16_t *)w->sh2;
     kw.src = &as.base;
     kw.layer = w->layer;
+    kw.down = plain ? NULL : down;
+    kw.up = plain ? NULL : up;
+    kw.latent_norm = w->latent_norm;
     k3x_moe_layer *L = NULL;
     const int rc = k3x_moe_layer_create(&kc, &kw, 0, &L);
     if (rc) {
@@ -88,7 +111,7 @@ int k3_moe_gpu(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int 
                float *wt, float *scratch)
 {
     (void)scratch;
-    if (!k2_form(w, c)) return -1;
+    if (!gpu_form(w, c)) return -1;
     k3x_moe_layer *L = layer_for(w, c);
     if (!L) return -1;
     return k3x_moe(L, out, x, T, idx, wt) == K3X_OK ? 0 : -1;
@@ -98,7 +121,7 @@ int k3_moe_prefill_gpu(float *out, const float *x, const K3MoeW *w, const K3Cfg 
                        int *idx, float *wt, float *scratch)
 {
     (void)scratch;
-    if (!k2_form(w, c)) return -1;
+    if (!gpu_form(w, c)) return -1;
     k3x_moe_layer *L = layer_for(w, c);
     if (!L) return -1;
     return k3x_moe_prefill(L, out, x, T, idx, wt) == K3X_OK ? 0 : -1;

@@ -20,7 +20,8 @@ K3X_F32 = 0
 K3X_BF16 = 1
 DECODE_MAX_T = 8
 
-STREAM_ROUTER, STREAM_BIAS, STREAM_X, STREAM_SH1, STREAM_SH3, STREAM_SH2, STREAM_NORM = range(7)
+(STREAM_ROUTER, STREAM_BIAS, STREAM_X, STREAM_SH1, STREAM_SH3, STREAM_SH2, STREAM_NORM,
+ STREAM_DOWN, STREAM_UP, STREAM_LNORM) = range(10)
 STREAM_CODES, STREAM_SCALES = 10, 11
 
 # the C-ABI surface declared in include/k3x_moe.h
@@ -43,7 +44,9 @@ class K3XError(RuntimeError):
 class Cfg(C.Structure):
     _fields_ = [("hidden", C.c_int), ("n_experts", C.c_int), ("topk", C.c_int),
                 ("moe_inter", C.c_int), ("n_shared", C.c_int), ("moe_renorm", C.c_int),
-                ("routed_scale", C.c_float), ("group", C.c_int)]
+                ("routed_scale", C.c_float), ("group", C.c_int), ("latent", C.c_int),
+                ("latent_norm", C.c_int), ("rms_eps", C.c_float), ("situ_b1", C.c_float),
+                ("situ_b2", C.c_float)]
 
 
 class ExpertQ(C.Structure):
@@ -61,14 +64,15 @@ ExpertSrc._fields_ = [("get", GET_FN), ("ctx", C.c_void_p)]
 class MoeW(C.Structure):
     _fields_ = [("gate", C.c_void_p), ("bias", C.c_void_p), ("sh1", C.c_void_p),
                 ("sh3", C.c_void_p), ("sh2", C.c_void_p), ("src", C.POINTER(ExpertSrc)),
-                ("bank", C.POINTER(ExpertQ)), ("layer", C.c_int)]
+                ("bank", C.POINTER(ExpertQ)), ("layer", C.c_int), ("down", C.c_void_p),
+                ("up", C.c_void_p), ("latent_norm", C.c_void_p)]
 
 
 class SynthSpec(C.Structure):
     _fields_ = [("seed", C.c_uint64), ("layer", C.c_int), ("router_sigma", C.c_double),
                 ("bias_sigma", C.c_double), ("zipf_alpha", C.c_double),
                 ("zipf_s", C.c_double), ("scale_lo", C.c_int), ("scale_hi", C.c_int),
-                ("shared_sigma", C.c_double)]
+                ("shared_sigma", C.c_double), ("trunk_sigma", C.c_double)]
 
 
 _lib = None
@@ -132,8 +136,11 @@ def expert_drops():
 
 
 def make_cfg(hidden, n_experts, topk, moe_inter, n_shared=1, moe_renorm=1, routed_scale=2.5,
-             group=32):
-    return Cfg(hidden, n_experts, topk, moe_inter, n_shared, moe_renorm, routed_scale, group)
+             group=32, latent=0, latent_norm=0, rms_eps=1e-5, situ_b1=0.0, situ_b2=0.0):
+    """K3Cfg's MoE fields.  latent > 0 selects the LatentMoE form; betas of 0 (or 2^64)
+    leave SiTU uncapped (SwiGLU)."""
+    return Cfg(hidden, n_experts, topk, moe_inter, n_shared, moe_renorm, routed_scale, group,
+               latent, latent_norm, rms_eps, situ_b1, situ_b2)
 
 
 def _vp(a):
@@ -149,9 +156,11 @@ class MoELayer:
 
     # -- construction -------------------------------------------------------------
     @classmethod
-    def from_bank(cls, cfg, gate, bias, experts, sh1=None, sh3=None, sh2=None, device=0):
-        """experts: list of dicts with numpy uint8 arrays p1,s1,p3,s3,p2,s2."""
-        keep = [gate, bias, sh1, sh3, sh2]
+    def from_bank(cls, cfg, gate, bias, experts, sh1=None, sh3=None, sh2=None, device=0,
+                  down=None, up=None, latent_norm=None):
+        """experts: list of dicts with numpy uint8 arrays p1,s1,p3,s3,p2,s2; down/up bf16
+        (uint16) and latent_norm fp32 numpy arrays for a latent layer."""
+        keep = [gate, bias, sh1, sh3, sh2, down, up, latent_norm]
         bank = (ExpertQ * cfg.n_experts)()
         for e, ex in enumerate(experts):
             for k in ("p1", "s1", "p3", "s3", "p2", "s2"):
@@ -159,7 +168,7 @@ class MoELayer:
                 keep.append(arr)
                 setattr(bank[e], k, arr.ctypes.data)
         w = MoeW(_vp(gate), _vp(bias), _vp(sh1), _vp(sh3), _vp(sh2), None,
-                 C.cast(bank, C.POINTER(ExpertQ)), 0)
+                 C.cast(bank, C.POINTER(ExpertQ)), 0, _vp(down), _vp(up), _vp(latent_norm))
         h = C.c_void_p()
         _check(lib().k3x_moe_layer_create(C.byref(cfg), C.byref(w), device, C.byref(h)),
                "k3x_moe_layer_create")
@@ -167,7 +176,7 @@ class MoELayer:
 
     @classmethod
     def from_source(cls, cfg, gate, bias, get, sh1=None, sh3=None, sh2=None, layer=0,
-                    device=0):
+                    device=0, down=None, up=None, latent_norm=None):
         """get(layer, expert) -> dict of numpy arrays, or None for a failed fetch."""
         hold = {}
 
@@ -185,7 +194,7 @@ class MoELayer:
         cb = GET_FN(_get)
         src = ExpertSrc(cb, None)
         w = MoeW(_vp(gate), _vp(bias), _vp(sh1), _vp(sh3), _vp(sh2), C.pointer(src), None,
-                 layer)
+                 layer, _vp(down), _vp(up), _vp(latent_norm))
         h = C.c_void_p()
         _check(lib().k3x_moe_layer_create(C.byref(cfg), C.byref(w), device, C.byref(h)),
                "k3x_moe_layer_create")
@@ -193,9 +202,10 @@ class MoELayer:
 
     @classmethod
     def synthetic(cls, cfg, seed=0, layer=0, router_sigma=0.02, bias_sigma=0.1, zipf_alpha=0.0,
-                  zipf_s=1.1, scale_lo=121, scale_hi=125, shared_sigma=0.02, device=0):
+                  zipf_s=1.1, scale_lo=121, scale_hi=125, shared_sigma=0.02, device=0,
+                  trunk_sigma=0.02):
         spec = SynthSpec(seed, layer, router_sigma, bias_sigma, zipf_alpha, zipf_s, scale_lo,
-                         scale_hi, shared_sigma)
+                         scale_hi, shared_sigma, trunk_sigma)
         h = C.c_void_p()
         _check(lib().k3x_synth_layer_create(C.byref(cfg), C.byref(spec), device, C.byref(h)),
                "k3x_synth_layer_create")
@@ -236,7 +246,10 @@ class MoELayer:
         return out, idx, wt
 
     def read_expert(self, e):
-        H, I = self.cfg.hidden, self.cfg.moe_inter
+        """Expert e in the reference's row-major layout; its width is the latent width in
+        the latent form."""
+        H = self.cfg.latent if self.cfg.latent > 0 else self.cfg.hidden
+        I = self.cfg.moe_inter
         d = {"p1": np.empty((I, H // 2), np.uint8), "s1": np.empty((I, H // 32), np.uint8),
              "p3": np.empty((I, H // 2), np.uint8), "s3": np.empty((I, H // 32), np.uint8),
              "p2": np.empty((H, I // 2), np.uint8), "s2": np.empty((H, I // 32), np.uint8)}

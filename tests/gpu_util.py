@@ -31,14 +31,21 @@ def dev_forward(torch, k3x, layer, x, bf16=False, resid=None):
     return out.cpu().numpy(), idx.cpu().numpy(), wt.cpu().numpy()
 
 
+def layer_cfg(k3x, L):
+    """k3x_cfg of a synth.Layer (betas of 2^64 are passed as they are: SwiGLU)."""
+    return k3x.make_cfg(L.H, L.E, L.K, L.I, L.n_shared, L.renorm, L.routed_scale,
+                        latent=L.latent, latent_norm=L.latent_norm, rms_eps=L.rms_eps,
+                        situ_b1=L.situ_b1, situ_b2=L.situ_b2)
+
+
 def bank_layer(k3x, L):
-    cfg = k3x.make_cfg(L.H, L.E, L.K, L.I, L.n_shared, L.renorm, L.routed_scale)
-    return k3x.MoELayer.from_bank(cfg, L.gate, L.bias, L.all_experts(), L.sh1, L.sh3, L.sh2)
+    return k3x.MoELayer.from_bank(layer_cfg(k3x, L), L.gate, L.bias, L.all_experts(), L.sh1,
+                                  L.sh3, L.sh2, down=L.down, up=L.up, latent_norm=L.lnorm)
 
 
 def synth_layer(k3x, L):
-    cfg = k3x.make_cfg(L.H, L.E, L.K, L.I, L.n_shared, L.renorm, L.routed_scale)
-    return k3x.MoELayer.synthetic(cfg, seed=L.seed, layer=L.layer, router_sigma=L.router_sigma,
-                                  bias_sigma=L.bias_sigma, zipf_alpha=L.zipf_alpha,
-                                  zipf_s=L.zipf_s, scale_lo=L.scale_lo, scale_hi=L.scale_hi,
-                                  shared_sigma=L.shared_sigma)
+    return k3x.MoELayer.synthetic(layer_cfg(k3x, L), seed=L.seed, layer=L.layer,
+                                  router_sigma=L.router_sigma, bias_sigma=L.bias_sigma,
+                                  zipf_alpha=L.zipf_alpha, zipf_s=L.zipf_s,
+                                  scale_lo=L.scale_lo, scale_hi=L.scale_hi,
+                                  shared_sigma=L.shared_sigma, trunk_sigma=L.trunk_sigma)

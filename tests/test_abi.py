@@ -54,7 +54,7 @@ def test_strerror(k3x):
 
 @pytest.mark.parametrize("bad", [
     dict(hidden=250), dict(moe_inter=100), dict(group=16), dict(topk=0), dict(topk=65),
-    dict(n_experts=2000), dict(topk=20, n_experts=16),
+    dict(n_experts=2000), dict(topk=20, n_experts=16), dict(latent=100), dict(latent=-128),
 ])
 def test_create_rejects_bad_cfg_before_device(k3x, bad):
     kw = dict(hidden=256, n_experts=16, topk=4, moe_inter=128)

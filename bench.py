@@ -9,7 +9,7 @@ over 4 layers of that shape, so every step reads its weights from HBM (a single 
 called back to back finds its router and shared expert, 99 MB, still in the 256 MB
 last-level cache; that figure is reported as warm_one_layer_us_per_token).  Weights are
 synthetic (seeded generator, random init).  The record also carries the 2048-token
-prefill leg and the 8-layer stack leg.
+prefill leg, the 8-layer stack leg and the K3 LatentMoE decode leg.
 
 Prints ONE JSON line (rank 0):
   value        microseconds per token for the whole layer (lower is better)
@@ -166,6 +166,93 @@ def stack_leg(torch, k3x):
             "outputs_finite": finite}
 
 
+# The K3 LatentMoE layer: hidden 7168, latent 3584, 896 experts top-16 of intermediate 3072
+# (MXFP4, at the latent width), two bf16 shared experts (intermediate 6144 together), SiTU
+# betas 4 and 25, the latent RMSNorm, routed_scale 1.
+K3_E, K3_K, K3_I, K3_L, K3_SI = 896, 16, 3072, 3584, 6144
+K3_KERNELS = ["k1_router_bset", "k1_zdown", "k2_gateup", "k3_down", "k4_up"]
+
+
+def k3_kernel_bytes(U, T):
+    """Algorithmic HBM bytes per launch of the latent decode kernels at one token (k4_up
+    works out the latent norm itself there): k1 the router, zdown the down projection, k2
+    the shared experts' and the unique experts' gate/up weights, k3 the unique experts'
+    down weights, k4 the up projection and the shared experts' down weights; activations
+    in and out included."""
+    xb = T * H * 2
+    ex = K3_I * K3_L // 2 + K3_I * K3_L // 32
+    return dict(zip(K3_KERNELS, (
+        K3_E * H * 4 + K3_E * 4 + xb,
+        K3_L * H * 2 + xb,
+        2 * K3_SI * H * 2 + U * 2 * ex + 2 * T * K3_E * 4,
+        U * ex + T * K3_L * 4,
+        H * K3_L * 2 + H * K3_SI * 2 + T * H * 4)))
+
+
+def k3_leg(torch, k3x, steps, warmup, nrot=2):
+    """Decode b=1 through the K3 LatentMoE layer shape (15.7 GB of experts per layer),
+    rotating over `nrot` layers so every call reads its weights from HBM; bf16 tokens from
+    a pool of 64.  Reports microseconds per token, the per-kernel HIP-event durations and
+    the dominant kernel's fraction of the HBM peak."""
+    cfg = k3x.make_cfg(H, K3_E, K3_K, K3_I, 2, 1, 1.0, latent=K3_L, latent_norm=1,
+                       rms_eps=1e-5, situ_b1=4.0, situ_b2=25.0)
+    layers = [k3x.MoELayer.synthetic(cfg, seed=40 + j) for j in range(nrot)]
+    n_pool = 64
+    xs = k3x.synth_normal_f32(n_pool * H, k3x.synth_key(40, 0, k3x.STREAM_X, 100))
+    xpool = torch.from_numpy(xs.reshape(n_pool, H)).cuda().to(torch.bfloat16).contiguous()
+    out = torch.empty((1, H), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.Stream()
+    sh = stream.cuda_stream
+    row = xpool.stride(0) * 2
+
+    def step(i):
+        layers[i % nrot].forward(out.data_ptr(), xpool.data_ptr() + (i % n_pool) * row, 1,
+                                 k3x.K3X_BF16, stream=sh)
+
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(warmup + i)
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    for l in layers:
+        l.set_timing(True)
+    per = {n: [] for n in K3_KERNELS}
+    with torch.cuda.stream(stream):
+        for i in range(steps):
+            step(i)
+            for n, v in zip(K3_KERNELS, layers[i % nrot].last_ms()):
+                per[n].append(v)
+    for l in layers:
+        l.set_timing(False)
+        l.check()
+    avg = {n: float(np.mean(v)) for n, v in per.items()}
+    kb = k3_kernel_bytes(U=K3_K, T=1)
+    dom = max(avg, key=lambda n: avg[n])
+    achieved = kb[dom] / (avg[dom] * 1e-3) / 1e9
+    total = sum(kb.values())
+    finite = bool(torch.isfinite(out).all().item())
+    for l in layers:
+        l.close()
+    del xpool, out
+    torch.cuda.empty_cache()
+    return {"workload": "K3 LatentMoE decode b=1: hidden 7168, latent 3584, 896 experts "
+                        "top-16, inter 3072 MXFP4, 2 bf16 shared experts, SiTU 4/25, "
+                        f"latent RMSNorm; {nrot} layers rotated",
+            "us_per_token": round(wall_ms * 1e3, 2),
+            "layer_bytes": total,
+            "layer_hbm_gbs": round(total / (wall_ms * 1e-3) / 1e9, 1),
+            "kernel_avg_us": {n: round(v * 1e3, 2) for n, v in avg.items()},
+            "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes_per_launch": kb[dom]},
+            "outputs_finite": finite, "steps": steps}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed counter summary (FETCH_SIZE and
     WRITE_SIZE runs scaled by a plain copy's readings), or None."""
@@ -261,6 +348,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 2048-token prefill leg")
     ap.add_argument("--no-stack", action="store_true", help="skip the 8-layer stack leg")
+    ap.add_argument("--no-k3", action="store_true", help="skip the K3 LatentMoE decode leg")
+    ap.add_argument("--k3-only", action="store_true",
+                    help="only run the K3 LatentMoE decode leg and print its record")
     ap.add_argument("--stack-only", action="store_true",
                     help="only run the 8-layer stack leg and print its record")
     ap.add_argument("--prefill-only", action="store_true",
@@ -286,6 +376,9 @@ def main():
         return
     if args.stack_only:
         print(json.dumps(stack_leg(torch, load_k3x())), flush=True)
+        return
+    if args.k3_only:
+        print(json.dumps(k3_leg(torch, load_k3x(), args.steps, args.warmup)), flush=True)
         return
     k3x = load_k3x()
     dev = torch.device("cuda:0")
@@ -382,6 +475,8 @@ def main():
         rec["prefill"] = prefill_leg(torch, k3x)
     if not args.no_stack:
         rec["stack"] = stack_leg(torch, k3x)
+    if not args.no_k3:
+        rec["k3_latent"] = k3_leg(torch, k3x, min(args.steps, 100), min(args.warmup, 10))
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(min_seconds=args.cpu_seconds)
     else:

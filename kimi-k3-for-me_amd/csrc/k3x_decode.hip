@@ -841,6 +841,9 @@ struct K3Args {
     int            T, H, I, K;     // H: the output rows (the latent width in that form)
     uint32_t       lds_bytes;      // LDS for the routed activation sets
     uint32_t       sh_lds;         // LDS for the shared activation set (after them), or 0
+    int            upp;            // unique experts per part: part blockIdx.y takes slots
+                                   // upp*y .. upp*y + upp - 1 (the latent form's split)
+    size_t         pstride;        // floats between parts' outputs (0: one part)
 };
 
 // A bf16 quad of the shared down matrix with its B fragments (read from the shared
@@ -855,7 +858,8 @@ struct QBB {
 // accumulator set.  Both rings are primed first, so the shared quads' loads are in
 // flight while the routed items stream.
 template <bool EXACT, bool LDSB, bool SHL>
-__device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int lane, int nu)
+__device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int lane, int u0,
+                                        int nu)
 {
     const int NW = NT3 / WAVE;
     const int NC = 2 * a.T;
@@ -864,9 +868,10 @@ __device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int
     const uint32_t slot = (uint32_t)nSI * 1024u * NC;
     const uint32_t tb = (uint32_t)fp4_tile_bytes(a.I);
     const int cnt = strided_count(wave, NW, nu * nSI);
-    const int nQS = a.sh_down ? a.SI >> 7 : 0;
+    const int nQS = (a.sh_down && blockIdx.y == 0) ? a.SI >> 7 : 0;
+    const uint16_t *actB = a.actB + (size_t)u0 * (slot / 2);   // this part's slots
     Stage<8> st;
-    if (LDSB) st.issue(a.actB, (uint32_t)nu * slot, NT3);
+    if (LDSB) st.issue(actB, (uint32_t)nu * slot, NT3);
     Stage<1> st2;
     if (SHL) st2.issue(a.shB, (uint32_t)nQS * 256u * NC, NT3);
     SQ ring[2];
@@ -874,7 +879,7 @@ __device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int
         const int it = wave + NW * k;
         const bool on = k < cnt;
         const int u = on ? it / nSI : 0, S = on ? it % nSI : 0;
-        const int e = on ? a.route->uniq[u] : 0;
+        const int e = on ? a.route->uniq[u0 + u] : 0;
         const rsrc_t r = make_rsrc(a.experts + (size_t)e * a.expert_bytes + a.down_off +
                                        (size_t)rt * tb, on ? tb : 0u);
         sq_load(ring[i], r, (uint32_t)S * SQ_BYTES, lane);
@@ -901,7 +906,7 @@ __device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int
     if (SHL) st2.commit(NT3, a.lds_bytes);
     if (LDSB || SHL) __syncthreads();
     BFrag<LDSB> bf;
-    bf.init(a.actB, (uint32_t)(a.T * a.K) * slot, NC, lane);
+    bf.init(actB, (uint32_t)nu * slot, NC, lane);
     ring_loop<2>(cnt, ld, [&](int i, int k) AI {
         const int it = wave + NW * k;
         sq_mfma<EXACT, LDSB>(d, ring[i], bf, (uint32_t)(it / nSI) * slot, it % nSI);
@@ -925,33 +930,39 @@ __global__ void __launch_bounds__(NT3) k3_down(K3Args a)
 {
     __shared__ float lds[(NT3 / WAVE - 1) * 4 * WAVE];
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
-    const int nu = a.route->nu;
+    const int nall = a.route->nu;
+    const int u0 = (int)blockIdx.y * a.upp;
+    const int nu = nall - u0 < a.upp ? (nall > u0 ? nall - u0 : 0) : a.upp;
     const int nSI = ((a.I >> 7) + 3) >> 2;
     const uint32_t slot = (uint32_t)nSI * 1024u * 2 * a.T;
     f32x4 d = {0.f, 0.f, 0.f, 0.f};
     // both activation sets in LDS when they fit, else both read through L2
     if ((uint32_t)nu * slot <= a.lds_bytes && a.sh_lds)
-        k3_body<EXACT, true, true>(a, d, wave, lane, nu);
+        k3_body<EXACT, true, true>(a, d, wave, lane, u0, nu);
     else
-        k3_body<EXACT, false, false>(a, d, wave, lane, nu);
+        k3_body<EXACT, false, false>(a, d, wave, lane, u0, nu);
     float acc[4] = {d[0], d[1], d[2], d[3]};
     wave_sum_lds<4, NT3 / WAVE>(acc, lds, wave, lane);
     if (wave != 0) return;
     const int rt = blockIdx.x;
+    float *out = a.out + blockIdx.y * a.pstride;
     per_token<4>(acc, 2 * a.T, lane, [&](int r0, int tok, const float (&v)[4]) AI {
         for (int i = 0; i < 4; i++) {
             const size_t o = (size_t)tok * a.H + rt * 16 + r0 + i;
-            a.out[o] = a.resid ? a.resid[o] + v[i] : v[i];
+            out[o] = a.resid ? a.resid[o] + v[i] : v[i];
         }
     });
 }
 
 // ------------------------------------------------------------------ K4 (latent form)
-// The routed aggregates' RMSNorm (k3_rmsnorm on the aggregate, k3_ops.c:1946) and their
-// B set for the up projection.  Every workgroup works out 1/rms of every token (a double
-// sum of squares, as the reference), then writes its share of the set.
+// The routed aggregates (the sum of k3's parts, in part order), their RMSNorm (k3_rmsnorm
+// on the aggregate, k3_ops.c:1946) and their B set for the up projection.  Every
+// workgroup works out 1/rms of every token (a double sum of squares, as the reference),
+// then writes its share of the set.
 struct KNArgs {
-    const float *acc;              // [T][XL]
+    const float *acc;              // [P][T][XL] partial aggregates, pstride floats apart
+    int          P;
+    size_t       pstride;
     const float *nw;               // [XL], or NULL: no norm
     float        eps;
     int          T, XL;
@@ -959,6 +970,13 @@ struct KNArgs {
 };
 
 #define NT4 256
+
+__device__ __forceinline__ float agg_at(const KNArgs &a, size_t i)
+{
+    float v = a.acc[i];
+    for (int p = 1; p < a.P; p++) v += a.acc[p * a.pstride + i];
+    return v;
+}
 
 __global__ void __launch_bounds__(NT4) k4_latent_norm(KNArgs a)
 {
@@ -969,7 +987,7 @@ __global__ void __launch_bounds__(NT4) k4_latent_norm(KNArgs a)
         for (int t = 0; t < a.T; t++) {
             double ss = 0.0;
             for (int i = threadIdx.x; i < a.XL; i += NT4) {
-                const double v = (double)a.acc[(size_t)t * a.XL + i];
+                const double v = (double)agg_at(a, (size_t)t * a.XL + i);
                 ss += v * v;
             }
             for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
@@ -983,44 +1001,123 @@ __global__ void __launch_bounds__(NT4) k4_latent_norm(KNArgs a)
         }
         __syncthreads();
     }
-    const int nS = ((a.XL >> 7) + 3) >> 2;
-    x_to_bset((uint8_t *)a.latB, a.acc, 0, a.XL, 2 * a.T, 4 * nS,
-              blockIdx.x * NT4 + threadIdx.x, gridDim.x * NT4, a.nw, a.nw ? s_inv : nullptr);
+    // entries of the compact set (whole super-quads; quads past XL/128 are zeros), as
+    // x_to_bset lays them out
+    const int NC = 2 * a.T, nQ = a.XL >> 7, nq = 4 * (((a.XL >> 7) + 3) >> 2);
+    const int ne = nq * 16 * NC;
+    for (int f = blockIdx.x * NT4 + threadIdx.x; f < ne; f += gridDim.x * NT4) {
+        const int n = f % NC, kq = (f / NC) & 3, t = (f / (NC * 4)) & 3, q = f / (NC * 16);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (q < nQ) {
+            const int c0 = q * 128 + kq * 32 + t * 8;
+            const size_t base = (size_t)(n >> 1) * a.XL + c0;
+            float xv[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) xv[j] = agg_at(a, base + j);
+            if (a.nw) {
+                const float inv = s_inv[n >> 1];
+#pragma unroll
+                for (int j = 0; j < 8; j++) xv[j] = a.nw[c0 + j] * xv[j] * inv;
+            }
+            v = bfrag_of(xv, n & 1);
+        }
+        *(u32x4 *)((uint8_t *)a.latB + (size_t)f * 16) = v;
+    }
 }
 
 // The up projection (k3_ops.c:1950) of the normalised aggregates and the shared expert's
 // down product (moe_shared, :1858) for 16 output rows: eight waves on interleaved bf16
 // quads of `up` and then of the shared down matrix, into two accumulator sets; out =
-// up + shared (:1859), plus the residual.  BL: both B sets staged in LDS (the aggregates'
-// at 0, the shared activation's after it), else each quad's B fragments are read from
-// global memory with its weights.
+// up + shared (:1859), plus the residual.
+//   FUSE: the workgroup works out the aggregates itself, while its first weights are in
+//         flight: the parts of k3 added in order into LDS (fp32), each token's 1/rms, and
+//         the normalised set's B fragments into LDS at 0 (else they come from
+//         k4_latent_norm's set in global memory, read with each quad's weights).
+//   SHL:  the shared activation's set staged in LDS after the aggregates' set (else read
+//         from global memory with each quad's weights).
 struct K4Args {
     const uint16_t *up;            // tiled bf16 [H][XL]
-    const uint16_t *latB;          // B set of the normalised aggregates
+    const uint16_t *latB;          // B set of the normalised aggregates (not FUSE)
+    KNArgs          kn;            // the parts and the norm (FUSE)
     const uint16_t *sh_down;       // tiled bf16 [H][SI], or NULL
     const uint16_t *shB;           // B set of the shared activation
     float          *out;
     const float    *resid;
     int             T, H, XL, SI;
-    uint32_t        lat_lds;       // bytes of the aggregates' set in LDS (BL)
 };
 
-#define K4_LDS_MAX 65536u          // both sets in LDS (with the static reduction area, two workgroups per CU)
+#define K4_LDS_MAX 65536u          // with the static reduction area, two workgroups per CU
 
-template <bool BL>
+__host__ __device__ inline uint32_t k4_lds_bytes(bool fuse, bool shl, int T, int XL, int SI)
+{
+    const uint32_t NC = 2u * (uint32_t)T;
+    return (fuse ? (uint32_t)(XL >> 7) * 256u * NC + (uint32_t)(T * XL) * 4u : 0u) +
+           (shl ? (uint32_t)(SI >> 7) * 256u * NC : 0u);
+}
+
+// FUSE's preamble: aggregates into LDS (agg), 1/rms per token, the normalised B set into
+// LDS at 0.  All NT3 threads; ends with a barrier.
+__device__ __forceinline__ void k4_fuse_norm(const KNArgs &a, float *agg, double (*dl)[K3X_DECODE_MAX_T],
+                                             float *s_inv)
+{
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int n4 = a.XL >> 2;
+    for (int t = 0; t < a.T; t++) {
+        double ss = 0.0;
+        for (int c = threadIdx.x; c < n4; c += NT3) {
+            const size_t o = (size_t)t * a.XL + 4 * c;
+            f32x4 v = *(const f32x4 *)(a.acc + o);
+            for (int p = 1; p < a.P; p++) {
+                const f32x4 w = *(const f32x4 *)(a.acc + p * a.pstride + o);
+                v[0] += w[0]; v[1] += w[1]; v[2] += w[2]; v[3] += w[3];
+            }
+            *(f32x4 *)(agg + o) = v;
+#pragma unroll
+            for (int k = 0; k < 4; k++) ss += (double)v[k] * (double)v[k];
+        }
+        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        if (lane == 0) dl[wave][t] = ss;
+    }
+    __syncthreads();
+    if (threadIdx.x < a.T) {
+        double tot = 0.0;
+        for (int w = 0; w < NT3 / WAVE; w++) tot += dl[w][threadIdx.x];
+        s_inv[threadIdx.x] = a.nw ? (float)(1.0 / sqrt(tot / (double)a.XL + (double)a.eps)) : 1.0f;
+    }
+    __syncthreads();
+    const int NC = 2 * a.T, ne = (a.XL >> 7) * 16 * NC;
+    for (int f = threadIdx.x; f < ne; f += NT3) {
+        const int n = f % NC, kq = (f / NC) & 3, t = (f / (NC * 4)) & 3, q = f / (NC * 16);
+        const int c0 = q * 128 + kq * 32 + t * 8;
+        const float *src = agg + (size_t)(n >> 1) * a.XL + c0;
+        float xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) xv[j] = src[j];
+        if (a.nw) {
+            const float inv = s_inv[n >> 1];
+            float wv[8];
+            load_x8(a.nw, 0, (size_t)c0, wv);
+#pragma unroll
+            for (int j = 0; j < 8; j++) xv[j] = wv[j] * xv[j] * inv;
+        }
+        *(u32x4 *)(dyn_lds + (size_t)f * 16) = bfrag_of(xv, n & 1);
+    }
+}
+
+template <bool FUSE, bool SHL>
 __global__ void __launch_bounds__(NT3) k4_up(K4Args a)
 {
     __shared__ float lds[(NT3 / WAVE - 1) * 8 * WAVE];
+    __shared__ double dl[NT3 / WAVE][K3X_DECODE_MAX_T];
+    __shared__ float s_inv[K3X_DECODE_MAX_T];
     constexpr int NW = NT3 / WAVE;
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int NC = 2 * a.T, rt = blockIdx.x;
     const int nQL = a.XL >> 7, nQS = a.sh_down ? a.SI >> 7 : 0;
     const uint32_t lbytes = (uint32_t)nQL * 256u * NC, sbytes = (uint32_t)nQS * 256u * NC;
-    Stage<4> st1, st2;
-    if (BL) {
-        st1.issue(a.latB, lbytes, NT3);
-        st2.issue(a.shB, sbytes, NT3);
-    }
+    const uint32_t sh_off = FUSE ? lbytes : 0u;            // the shared set's LDS offset
+    Stage<4> st2;
+    if (SHL) st2.issue(a.shB, sbytes, NT3);
     const int c1 = strided_count(wave, NW, nQL), c2 = strided_count(wave, NW, nQS);
     const rsrc_t rw1 = make_rsrc(a.up + (size_t)rt * 16 * a.XL, (uint32_t)nQL * 4096u);
     const rsrc_t rw2 = make_rsrc(nQS ? a.sh_down + (size_t)rt * 16 * a.SI : a.up,
@@ -1029,30 +1126,29 @@ __global__ void __launch_bounds__(NT3) k4_up(K4Args a)
     const int n = lane & 15, kq = lane >> 4;
     const uint32_t boff = (uint32_t)((kq * NC + (n < NC ? n : 0)) * 16);
     QBB r1[2], r2[2];
-    auto ldq = [&](QBB &it, rsrc_t rw, rsrc_t rb, int k, int cnt) AI {
+    auto ldq = [&](QBB &it, rsrc_t rw, rsrc_t rb, int k, int cnt, bool gb) AI {
         const bool on = k < cnt;
         const int q = wave + NW * k;
         qb_load(it.a, rw, on ? (uint32_t)q * 4096u : K3X_OOB, lane);
-        if (!BL) {
+        if (gb) {
 #pragma unroll
             for (int t = 0; t < 4; t++)
                 it.b[t] = bload16(rb, on ? boff + (uint32_t)(q * 256 * NC + t * 64 * NC) : K3X_OOB);
         }
     };
-    auto ld1 = [&](int i, int k) AI { ldq(r1[i], rw1, rb1, k, c1); };
-    auto ld2 = [&](int i, int k) AI { ldq(r2[i], rw2, rb2, k, c2); };
+    auto ld1 = [&](int i, int k) AI { ldq(r1[i], rw1, rb1, k, c1, !FUSE); };
+    auto ld2 = [&](int i, int k) AI { ldq(r2[i], rw2, rb2, k, c2, !SHL); };
     ring_prime<2>(ld1);
     ring_prime<2>(ld2);
-    if (BL) {
-        st1.commit(NT3);
-        st2.commit(NT3, a.lat_lds);
-        __syncthreads();
-    }
+    if (SHL) st2.commit(NT3, sh_off);
+    if (FUSE)
+        k4_fuse_norm(a.kn, (float *)(dyn_lds + sh_off + (SHL ? sbytes : 0u)), dl, s_inv);
+    if (FUSE || SHL) __syncthreads();
     BFrag<true> bf;
     bf.init(nullptr, 0u, NC, lane);
     f32x4 d1 = {0.f, 0.f, 0.f, 0.f}, d2 = {0.f, 0.f, 0.f, 0.f};
-    auto use = [&](f32x4 &d, const QBB &it, uint32_t sbase, int q) AI {
-        if (BL) {
+    auto use = [&](f32x4 &d, const QBB &it, bool inlds, uint32_t sbase, int q) AI {
+        if (inlds) {
             u32x4 b[4];
 #pragma unroll
             for (int t = 0; t < 4; t++) b[t] = bf.get(sbase, q, t);
@@ -1061,8 +1157,8 @@ __global__ void __launch_bounds__(NT3) k4_up(K4Args a)
             qb_mfma(d, it.a, it.b);
         }
     };
-    ring_loop<2>(c1, ld1, [&](int i, int k) AI { use(d1, r1[i], 0u, wave + NW * k); });
-    ring_loop<2>(c2, ld2, [&](int i, int k) AI { use(d2, r2[i], a.lat_lds, wave + NW * k); });
+    ring_loop<2>(c1, ld1, [&](int i, int k) AI { use(d1, r1[i], FUSE, 0u, wave + NW * k); });
+    ring_loop<2>(c2, ld2, [&](int i, int k) AI { use(d2, r2[i], SHL, sh_off, wave + NW * k); });
     float acc[8] = {d1[0], d1[1], d1[2], d1[3], d2[0], d2[1], d2[2], d2[3]};
     wave_sum_lds<8, NW>(acc, lds, wave, lane);
     if (wave != 0) return;
@@ -1170,32 +1266,49 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     // a shared expert here, an empty set)
     const uint32_t shb = a3.sh_down ? (uint32_t)(L->SI / 128) * 256u * NC : 0u;
     a3.sh_lds = (a3.lds_bytes && a3.lds_bytes + shb <= K3_LDS_MAX) ? (shb ? shb : 16u) : 0u;
+    // the latent form splits the unique experts into parts whose activation sets fit the
+    // LDS (at most K3X_DECODE_PARTS; k4_latent_norm adds the parts up); the K2 form writes
+    // its rows in one part
+    int parts = 1;
+    a3.upp = T * c->topk;
+    if (L->lat && a3.lds_bytes) {
+        parts = (T * c->topk + (int)(a3.lds_bytes / slot) - 1) / (int)(a3.lds_bytes / slot);
+        if (parts > K3X_DECODE_PARTS) parts = K3X_DECODE_PARTS;
+        a3.upp = (T * c->topk + parts - 1) / parts;     // balanced parts
+    }
+    a3.pstride = parts > 1 ? (size_t)K3X_DECODE_MAX_T * X : 0;
     const size_t l3 = (size_t)a3.lds_bytes + a3.sh_lds;
-    if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(X / 16), dim3(NT3), l3, s, a3);
-    else                hipLaunchKernelGGL(k3_down<false>, dim3(X / 16), dim3(NT3), l3, s, a3);
+    if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(X / 16, parts), dim3(NT3), l3, s, a3);
+    else                hipLaunchKernelGGL(k3_down<false>, dim3(X / 16, parts), dim3(NT3), l3, s, a3);
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, ev++, s))) return rc;
     if (!L->lat) return 0;
 
     KNArgs an;
-    an.acc = L->accL; an.nw = c->latent_norm ? L->lnw : NULL; an.eps = c->rms_eps;
+    an.acc = L->accL; an.P = parts; an.pstride = a3.pstride;
+    an.nw = c->latent_norm ? L->lnw : NULL; an.eps = c->rms_eps;
     an.T = T; an.XL = X; an.latB = L->latB;
-    const int nent = 4 * nSX * 16 * NC;
-    hipLaunchKernelGGL(k4_latent_norm, dim3((nent + 4 * NT4 - 1) / (4 * NT4)), dim3(NT4), 0, s, an);
-    if ((rc = launch_ok())) return rc;
-    if ((rc = record(L, ev++, s))) return rc;
-
     K4Args a4;
-    a4.up = L->lup; a4.latB = L->latB;
+    a4.up = L->lup; a4.latB = L->latB; a4.kn = an;
     a4.sh_down = L->SI > 0 ? L->sh_down : NULL; a4.shB = L->shB;
     a4.out = out; a4.resid = resid; a4.T = T; a4.H = H; a4.XL = X; a4.SI = L->SI;
-    const uint32_t lb = (uint32_t)(X / 128) * 256u * NC;
-    const uint32_t sb = a4.sh_down ? (uint32_t)(L->SI / 128) * 256u * NC : 0u;
-    a4.lat_lds = lb;
-    if (lb + sb <= K4_LDS_MAX)
-        hipLaunchKernelGGL(k4_up<true>, dim3(H / 16), dim3(NT3), (size_t)lb + sb, s, a4);
-    else
-        hipLaunchKernelGGL(k4_up<false>, dim3(H / 16), dim3(NT3), 0, s, a4);
+    // the norm inside k4 when its set (and the aggregates) fit the LDS, the shared set
+    // beside them when that fits too; otherwise the norm kernel writes the set first
+    const bool fuse = k4_lds_bytes(true, false, T, X, L->SI) <= K4_LDS_MAX;
+    const bool shl = k4_lds_bytes(fuse, true, T, X, L->SI) <= K4_LDS_MAX;
+    if (!fuse) {
+        const int nent = 4 * nSX * 16 * NC;
+        hipLaunchKernelGGL(k4_latent_norm, dim3((nent + 4 * NT4 - 1) / (4 * NT4)), dim3(NT4), 0,
+                           s, an);
+        if ((rc = launch_ok())) return rc;
+        if ((rc = record(L, ev++, s))) return rc;
+    }
+    const size_t l4 = k4_lds_bytes(fuse, shl, T, X, L->SI);
+    const dim3 g4(H / 16);
+    if (fuse && shl)  hipLaunchKernelGGL((k4_up<true, true>), g4, dim3(NT3), l4, s, a4);
+    else if (fuse)    hipLaunchKernelGGL((k4_up<true, false>), g4, dim3(NT3), l4, s, a4);
+    else if (shl)     hipLaunchKernelGGL((k4_up<false, true>), g4, dim3(NT3), l4, s, a4);
+    else              hipLaunchKernelGGL((k4_up<false, false>), g4, dim3(NT3), l4, s, a4);
     if ((rc = launch_ok())) return rc;
     return record(L, ev, s);
 }

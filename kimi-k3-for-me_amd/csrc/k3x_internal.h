@@ -48,6 +48,8 @@ extern "C" {
 #endif
 
 #define K3X_DECODE_MAX_T 8       /* tokens per call on the decode path (2 columns each) */
+#define K3X_DECODE_PARTS 8       /* latent form: parts the unique experts' down products
+                                    are split into (partial aggregates, added in order) */
 #define K3X_STAGE_MAX    65536   /* bytes of activation fragments a workgroup stages in LDS */
 #define K3X_MAX_TOPK     64      /* K3_MAX_TOPK, k3.h:857-864 */
 #define K3X_ROUTE_WAIT_DEFAULT 5000000ull  /* 50 ms at 100 MHz: decode's bound on the wait */
@@ -124,7 +126,8 @@ struct k3x_moe_layer {
                                      activation over whole super-quads of I */
     uint16_t *shB;                /* B set of the shared activation (SI/128 quads) */
     uint16_t *zB;                 /* latent: B set of z = down . x over whole super-quads */
-    float    *accL;               /* latent: [DECODE_MAX_T][XL] routed aggregates */
+    float    *accL;               /* latent: [DECODE_PARTS][DECODE_MAX_T][XL] partial
+                                     routed aggregates */
     uint16_t *latB;               /* latent: B set of the (normalised) aggregates */
     k3x_prefill_buf pf;
     size_t    bytes;

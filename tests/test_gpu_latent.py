@@ -86,6 +86,26 @@ def test_latent_variants(torch, k3x, norm, shared):
     layer.close()
 
 
+@pytest.mark.parametrize("H,LT,I,NS", [(2048, 2048, 128, 2), (512, 512, 1024, 2)])
+def test_latent_set_placements(torch, k3x, H, LT, I, NS):
+    """T = 8 on shapes whose up-projection sets take the other placements: the aggregates'
+    set too large for the LDS with the shared set staged (2048/2048/128), and the
+    aggregates' set worked out in the workgroup with the shared set read from memory
+    (512/512/1024)."""
+    say(f"case: latent layer H={H} latent={LT} I={I} shared={NS}, T=8")
+    L = synth.Layer(H=H, E=16, K=4, I=I, n_shared=NS, latent=LT, latent_norm=1,
+                    situ_b1=4.0, situ_b2=25.0, routed_scale=1.0, seed=11)
+    layer = bank_layer(k3x, L)
+    x = L.x(8, bf16=False)
+    o, idx, _, _ = L.oracle_moe(x)
+    out, i2, _ = dev_forward(torch, k3x, layer, x)
+    assert np.array_equal(i2, idx)
+    err = synth.rel_l2(out, o)
+    say(f"  rel_l2={err:.3e}")
+    assert err < TOL
+    layer.close()
+
+
 def test_latent_host_dropin(torch, k3x):
     say("case: tiny latent layer, host-pointer k3x_moe vs oracle")
     L = synth.tiny_latent(seed=7)
@@ -136,6 +156,18 @@ def test_k3_decode_b1(torch, k3x, k3_layer):
         err = synth.rel_l2(out, o[t:t + 1])
         say(f"  token {t}: rel_l2={err:.3e}")
         assert err < TOL
+
+
+def test_k3_decode_b2(torch, k3x, k3_layer):
+    say("case: K3 shape, T=2 in one call vs oracle")
+    L, layer = k3_layer
+    x = L.x(2, bf16=False, stream_sub=5)
+    o, idx, wt, _ = L.oracle_moe(x)
+    out, i2, w2 = dev_forward(torch, k3x, layer, x)
+    assert np.array_equal(i2, idx)
+    err = synth.rel_l2(out, o)
+    say(f"  rel_l2={err:.3e}")
+    assert err < TOL
 
 
 def test_k3_decode_b8(torch, k3x, k3_layer):

@@ -253,6 +253,57 @@ def k3_leg(torch, k3x, steps, warmup, nrot=2):
             "outputs_finite": finite, "steps": steps}
 
 
+def k3_prefill_leg(torch, k3x, reps=3):
+    """Prefill of one 2048-token chunk of bf16 N(0,1) activations through the K3 LatentMoE
+    shape with Zipf-skewed routing (alpha 1.0, s 1.1).  Algorithmic bytes: the weight bytes
+    of the experts the chunk uses, the shared experts, the latent projections and the
+    router, once, plus the activations in and out.  FLOPs: 2 per multiply-add of the
+    routed experts, the shared experts, the two projections and the router."""
+    T = PREFILL_T
+    cfg = k3x.make_cfg(H, K3_E, K3_K, K3_I, 2, 1, 1.0, latent=K3_L, latent_norm=1,
+                       rms_eps=1e-5, situ_b1=4.0, situ_b2=25.0)
+    layer = k3x.MoELayer.synthetic(cfg, seed=43, zipf_alpha=1.0)
+    xs = k3x.synth_normal_f32(T * H, k3x.synth_key(43, 0, k3x.STREAM_X, 5))
+    x = torch.from_numpy(xs.reshape(T, H)).cuda().to(torch.bfloat16).contiguous()
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    idx = torch.empty((T, K3_K), dtype=torch.int32, device="cuda")
+    wt = torch.empty((T, K3_K), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.Stream()
+    sh = stream.cuda_stream
+
+    def run():
+        layer.forward(out.data_ptr(), x.data_ptr(), T, k3x.K3X_BF16, 0, idx.data_ptr(),
+                      wt.data_ptr(), stream=sh)
+
+    with torch.cuda.stream(stream):
+        run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    used = int(torch.unique(idx).numel())
+    ex = 3 * (K3_I * K3_L // 2 + K3_I * K3_L // 32)
+    layer_bytes = (used * ex + 3 * K3_SI * H * 2 + 2 * K3_L * H * 2 + K3_E * H * 4 +
+                   T * H * 2 + T * H * 4)
+    flops = 2.0 * T * (K3_K * 3 * K3_I * K3_L + 3 * K3_SI * H + 2 * K3_L * H + K3_E * H)
+    finite = bool(torch.isfinite(out).all().item())
+    layer.close()
+    del x, out, idx, wt
+    torch.cuda.empty_cache()
+    return {"workload": f"K3 LatentMoE prefill {T} bf16 tokens, Zipf-skewed routing "
+                        "(alpha 1.0, s 1.1)",
+            "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_chunk": round(ms, 3),
+            "experts_used": used,
+            "hbm_gbs": round(layer_bytes / (ms * 1e-3) / 1e9, 1),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "mfma_frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / 2500.0, 4),
+            "outputs_finite": finite, "reps": reps}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed counter summary (FETCH_SIZE and
     WRITE_SIZE runs scaled by a plain copy's readings), or None."""
@@ -378,7 +429,11 @@ def main():
         print(json.dumps(stack_leg(torch, load_k3x())), flush=True)
         return
     if args.k3_only:
-        print(json.dumps(k3_leg(torch, load_k3x(), args.steps, args.warmup)), flush=True)
+        k = load_k3x()
+        rec = k3_leg(torch, k, args.steps, args.warmup)
+        if not args.no_prefill:
+            rec["prefill"] = k3_prefill_leg(torch, k)
+        print(json.dumps(rec), flush=True)
         return
     k3x = load_k3x()
     dev = torch.device("cuda:0")
@@ -477,6 +532,8 @@ def main():
         rec["stack"] = stack_leg(torch, k3x)
     if not args.no_k3:
         rec["k3_latent"] = k3_leg(torch, k3x, min(args.steps, 100), min(args.warmup, 10))
+        if not args.no_prefill:
+            rec["k3_latent"]["prefill"] = k3_prefill_leg(torch, k3x)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(min_seconds=args.cpu_seconds)
     else:

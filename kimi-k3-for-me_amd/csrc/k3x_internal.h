@@ -95,6 +95,10 @@ typedef struct k3x_prefill_buf {
     uint16_t *act;          /* [T*K][I/8][2][8] routed activations, hi/lo            */
     uint16_t *act_sh;       /* [T][SI/8][2][8] shared activations                    */
     float    *y;            /* [T*K + T][H] expert and shared output rows            */
+    /* latent form (X = latent width) */
+    float    *zf;           /* [T][X] z = down . x, then the routed aggregates        */
+    uint16_t *zhl;          /* [2][X/8][T][8] hi/lo planes of z, then of the normalised
+                               aggregates                                             */
 } k3x_prefill_buf;
 
 struct k3x_moe_layer {

@@ -336,8 +336,10 @@ int k3x_pf_reserve(k3x_moe_layer *L, int T)
     k3x_prefill_buf *B = &L->pf;
     if (T <= B->cap_T) return 0;
     const k3x_cfg *c = &L->cfg;
-    const size_t H = (size_t)c->hidden, E = (size_t)c->n_experts, K = (size_t)c->topk,
+    const size_t E = (size_t)c->n_experts, K = (size_t)c->topk,
                  I = (size_t)c->moe_inter, SI = (size_t)L->SI, t = (size_t)T;
+    /* rows of the widest activation (hidden, or a latent width above it) */
+    const size_t H = (size_t)(L->XL > c->hidden ? L->XL : c->hidden), X = (size_t)L->XL;
     const size_t sz[] = {
         t * H * 4,                 /* xhl     */
         t * E * 4, t * E * 4,      /* score, choice */
@@ -349,6 +351,8 @@ int k3x_pf_reserve(k3x_moe_layer *L, int T)
         (SI ? t * SI * 4 : 256),   /* act_sh  */
         (t * K + t) * H * 4,       /* y       */
         t * K * H * 4,             /* xp      */
+        L->lat ? t * X * 4 : 256,  /* zf      */
+        L->lat ? t * X * 4 : 256,  /* zhl     */
         0, 0,                      /* desc_gu, desc_dn (set below) */
     };
     enum { N = sizeof sz / sizeof sz[0] };
@@ -384,8 +388,9 @@ int k3x_pf_reserve(k3x_moe_layer *L, int T)
     B->act = (uint16_t *)(p + off[13]); B->act_sh = (uint16_t *)(p + off[14]);
     B->y = (float *)(p + off[15]);
     B->xp = (uint16_t *)(p + off[16]);
-    B->desc_gu = p + off[17]; B->ndesc_gu = ndg;
-    B->desc_dn = p + off[18]; B->ndesc_dn = ndd;
+    B->zf = (float *)(p + off[17]);     B->zhl = (uint16_t *)(p + off[18]);
+    B->desc_gu = p + off[19]; B->ndesc_gu = ndg;
+    B->desc_dn = p + off[20]; B->ndesc_dn = ndd;
     return 0;
 }
 
@@ -400,22 +405,6 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     if (T == 0) return 0;
     if (T <= L->tdec)
         return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, NULL, 0.0f, stream);
-    if (L->lat) {
-        /* the latent form has no grouped-GEMM pipeline yet: the decode path over groups of
-         * tdec tokens (results do not depend on the grouping) */
-        const size_t es = x_dtype == K3X_BF16 ? 2 : 4;
-        const int H = L->cfg.hidden, K = L->cfg.topk;
-        for (int t0 = 0; t0 < T; t0 += L->tdec) {
-            const int n = T - t0 < L->tdec ? T - t0 : L->tdec;
-            const int rc = k3x_dev_decode(L, out + (size_t)t0 * H,
-                                          (const char *)x + (size_t)t0 * H * es, x_dtype, n,
-                                          resid ? resid + (size_t)t0 * H : NULL,
-                                          idx ? idx + (size_t)t0 * K : NULL,
-                                          wt ? wt + (size_t)t0 * K : NULL, NULL, 0.0f, stream);
-            if (rc) return rc;
-        }
-        return 0;
-    }
     return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
 }
 

@@ -32,7 +32,7 @@
 __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int T, int H,
                                                   uint16_t *xg, int *counts, int E)
 {
-    if (blockIdx.x == 0)
+    if (blockIdx.x == 0 && counts)
         for (int e = threadIdx.x; e < E; e += PF_NT) counts[e] = 0;
     const size_t i = (size_t)blockIdx.x * PF_NT + threadIdx.x;     // (t, group) pairs
     const int G8 = H >> 3;
@@ -770,8 +770,58 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
     }
 }
 
+// ------------------------------------------------------------------ latent norm
+// The latent form's aggregates (agg [T][X], one workgroup per token): RMSNorm with the
+// latent norm weights (k3_rmsnorm, k3_ops.c:132-140 and :1946; double sum of squares, inv
+// rounded to float, w*x*inv), or none when nw is NULL, then the hi/lo planes
+// [2][X/8][T][8] for the up projection (pf_split's layout).
+__global__ void __launch_bounds__(PF_NT) pf_latnorm(const float *agg, const float *nw, float eps,
+                                                    int T, int X, uint16_t *hl)
+{
+    __shared__ double red[PF_NT / WAVE];
+    __shared__ float s_inv;
+    const int t = blockIdx.x, lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const float *row = agg + (size_t)t * X;
+    if (nw) {
+        double ss = 0.0;
+        for (int i = threadIdx.x; i < X; i += PF_NT) ss += (double)row[i] * (double)row[i];
+        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double tot = 0.0;
+            for (int w = 0; w < PF_NT / WAVE; w++) tot += red[w];
+            s_inv = (float)(1.0 / sqrt(tot / (double)X + (double)eps));
+        }
+        __syncthreads();
+    }
+    const int G8 = X >> 3;
+    for (int gi = threadIdx.x; gi < G8; gi += PF_NT) {
+        float v[8];
+        load_x8(row, 0, (size_t)gi * 8, v);
+        if (nw) {
+            float w[8];
+            load_x8(nw, 0, (size_t)gi * 8, w);
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = w[j] * v[j] * s_inv;
+        }
+        uint32_t hi[8], lo[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) split_bf16(v[j], hi[j], lo[j]);
+        u32x4 h, l;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            h[j] = hi[2 * j] | (hi[2 * j + 1] << 16);
+            l[j] = lo[2 * j] | (lo[2 * j + 1] << 16);
+        }
+        *(u32x4 *)(hl + ((size_t)gi * T + t) * 8) = h;
+        *(u32x4 *)(hl + ((size_t)(G8 + gi) * T + t) * 8) = l;
+    }
+}
+
 // ------------------------------------------------------------------ combine
-// out[t] = ((y[pos(t,0)] + y[pos(t,1)]) + ... ) + y_shared[t], then + resid.
+// out[t] = ((y[pos(t,0)] + y[pos(t,1)]) + ... ) + y_shared[t], then + resid (pos_of
+// NULL: K = 1 and row t).
 __global__ void __launch_bounds__(PF_NT) pf_combine(const float *y, const int *pos_of, int T, int K,
                                                     int H, int sh_row0, const float *resid,
                                                     float *out)
@@ -781,7 +831,10 @@ __global__ void __launch_bounds__(PF_NT) pf_combine(const float *y, const int *p
     if (i >= (size_t)T * h4) return;
     const int t = (int)(i / h4), h = (int)(i % h4) * 4;
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < K; j++) s += *(const f32x4 *)(y + (size_t)pos_of[(size_t)t * K + j] * H + h);
+    for (int j = 0; j < K; j++) {
+        const size_t row = pos_of ? (size_t)pos_of[(size_t)t * K + j] : (size_t)t;
+        s += *(const f32x4 *)(y + row * H + h);
+    }
     if (sh_row0 >= 0) s += *(const f32x4 *)(y + (size_t)(sh_row0 + t) * H + h);
     const size_t o = (size_t)t * H + h;
     if (resid) s += *(const f32x4 *)(resid + o);
@@ -834,9 +887,11 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     const k3x_cfg *c = &L->cfg;
     k3x_prefill_buf *B = &L->pf;
     const int H = c->hidden, E = c->n_experts, K = c->topk, I = c->moe_inter, SI = L->SI;
+    const int X = L->XL;                                 // the routed experts' width
     const int TK = T * K;
     const int x_bf16 = (x_dtype == K3X_BF16);
-    const int HLg = x_bf16 ? 1 : 2;                      // B columns per token, gate/up
+    const int HLg = x_bf16 ? 1 : 2;                      // B columns per token of x
+    const int HLr = L->lat ? 2 : HLg;                    // of the routed gate/up input
     int rc;
 
     hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (H / 8), PF_NT)), dim3(PF_NT), 0, s,
@@ -863,10 +918,10 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     PfScanArgs sa;
     sa.counts = B->counts; sa.E = E; sa.offsets = B->offsets; sa.cursor = B->cursor;
     sa.tb[0] = B->tb_gu; sa.tb[1] = B->tb_dn;
-    sa.tpb_s[0] = GU_CT32_S * 32 / HLg; sa.tpb_b[0] = GU_CT32_B * 32 / HLg;
+    sa.tpb_s[0] = GU_CT32_S * 32 / HLr; sa.tpb_b[0] = GU_CT32_B * 32 / HLr;
     sa.nrb_s[0] = cdiv(I, NW_S * GU_RT32 * 32); sa.nrb_b[0] = cdiv(I, NW_B * GU_RT32 * 32);
     sa.tpb_s[1] = DN_CT32_S * 32 / 2; sa.tpb_b[1] = DN_CT32_B * 32 / 2;
-    sa.nrb_s[1] = cdiv(H, NW_S * DN_RT32 * 32); sa.nrb_b[1] = cdiv(H, NW_B * DN_RT32 * 32);
+    sa.nrb_s[1] = cdiv(X, NW_S * DN_RT32 * 32); sa.nrb_b[1] = cdiv(X, NW_B * DN_RT32 * 32);
     hipLaunchKernelGGL(pf_scan, dim3(1), dim3(1024), 0, s, sa);
     if ((rc = launch_ok())) return rc;
     hipLaunchKernelGGL(pf_scatter, dim3(cdiv(TK, PF_NT)), dim3(PF_NT), 0, s, B->idx, B->wt, TK, K,
@@ -875,8 +930,27 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     hipLaunchKernelGGL(pf_tiles, dim3(E), dim3(PF_NT), 0, s, B->counts, B->offsets, sa,
                        (int4 *)B->desc_gu, (int4 *)B->desc_dn);
     if ((rc = launch_ok())) return rc;
-    hipLaunchKernelGGL(pf_permute, dim3(cdiv((size_t)HLg * (H / 8) * TK, PF_NT)), dim3(PF_NT), 0, s,
-                       B->xhl, T, H / 8, HLg, B->perm_tok, TK, B->xp);
+    const uint16_t *rsrc = B->xhl;        // the routed experts' input planes
+    if (L->lat) {
+        // z = down . x for every token (k3_mmw_batch, k3_ops.c:1871), then its hi/lo planes
+        PfGemmArgs zg;
+        memset(&zg, 0, sizeof zg);
+        zg.wm[0] = (const uint8_t *)L->ldown; zg.R = X; zg.K = H; zg.n0 = T;
+        zg.bsrc = B->xhl; zg.brows = T; zg.row_base = 0;
+        zg.y = B->zf; zg.out_base = 0;
+        const unsigned grid_z = cdiv(X, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 4 * 16 / HLg);
+        if (HLg == 1)
+            hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 1, false>), dim3(grid_z), dim3(PF_NT), 0, s, zg);
+        else
+            hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_z), dim3(PF_NT), 0, s, zg);
+        if ((rc = launch_ok())) return rc;
+        hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (X / 8), PF_NT)), dim3(PF_NT), 0, s,
+                           B->zf, 0, T, X, B->zhl, (int *)NULL, 0);
+        if ((rc = launch_ok())) return rc;
+        rsrc = B->zhl;
+    }
+    hipLaunchKernelGGL(pf_permute, dim3(cdiv((size_t)HLr * (X / 8) * TK, PF_NT)), dim3(PF_NT), 0, s,
+                       rsrc, T, X / 8, HLr, B->perm_tok, TK, B->xp);
     if ((rc = launch_ok())) return rc;
 
     // grids: upper bounds of each list (a small expert has one column block; large ones
@@ -895,7 +969,7 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     memset(&g, 0, sizeof g);
     g.wm[0] = L->experts + L->gate_off; g.wm[1] = L->experts + L->up_off;
     g.gstride = L->expert_bytes;
-    g.R = I; g.K = H; g.desc = (const int4 *)B->desc_gu;
+    g.R = I; g.K = X; g.desc = (const int4 *)B->desc_gu;
     g.bsrc = B->xp; g.brows = TK; g.perm = NULL; g.row_base = 0;
     g.pw = B->perm_w; g.act = B->act; g.arows = TK; g.out_base = 0;
     g.b1 = L->b1; g.b2 = L->b2;
@@ -904,10 +978,10 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     g.ntile = B->tb_gu + E;
     gb.ntile = B->tb_gu + 2 * E + 1; gb.dbase = B->tb_gu + E;
     if (ex_gu) {
-        if (HLg == 1) { launch_gu<true, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<true, 1, GU_CT32_S, NW_S>(g, grid_s[0], s); }
+        if (HLr == 1) { launch_gu<true, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<true, 1, GU_CT32_S, NW_S>(g, grid_s[0], s); }
         else          { launch_gu<true, 2, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<true, 2, GU_CT32_S, NW_S>(g, grid_s[0], s); }
     } else {
-        if (HLg == 1) { launch_gu<false, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<false, 1, GU_CT32_S, NW_S>(g, grid_s[0], s); }
+        if (HLr == 1) { launch_gu<false, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<false, 1, GU_CT32_S, NW_S>(g, grid_s[0], s); }
         else          { launch_gu<false, 2, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<false, 2, GU_CT32_S, NW_S>(g, grid_s[0], s); }
     }
     if ((rc = launch_ok())) return rc;
@@ -916,7 +990,7 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     PfGemmArgs d;
     memset(&d, 0, sizeof d);
     d.wm[0] = L->experts + L->down_off; d.gstride = L->expert_bytes;
-    d.R = H; d.K = I; d.desc = (const int4 *)B->desc_dn;
+    d.R = X; d.K = I; d.desc = (const int4 *)B->desc_dn;
     d.bsrc = B->act; d.brows = TK; d.perm = NULL; d.row_base = 0;
     d.y = B->y; d.out_base = 0;
     PfGemmArgs db = d;
@@ -926,7 +1000,30 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     else                { launch_dn<false, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<false, DN_CT32_S, NW_S>(d, grid_s[1], s); }
     if ((rc = launch_ok())) return rc;
 
-    int sh_row0 = -1;
+    int sh_row0 = -1, out_rows = TK;       // the shared rows follow the routed ones in y
+    const int *pos = B->pos_of;
+    int KC = K;
+    if (L->lat) {
+        // the routed aggregates in top-k order (:1941-1942), their RMSNorm and hi/lo
+        // planes (:1946), then the up projection (:1950) into y rows 0 .. T-1
+        hipLaunchKernelGGL(pf_combine, dim3(cdiv((size_t)T * (X / 4), PF_NT)), dim3(PF_NT), 0, s,
+                           B->y, B->pos_of, T, K, X, -1, (const float *)NULL, B->zf);
+        if ((rc = launch_ok())) return rc;
+        hipLaunchKernelGGL(pf_latnorm, dim3(T), dim3(PF_NT), 0, s, B->zf,
+                           c->latent_norm ? L->lnw : (const float *)NULL, c->rms_eps, T, X, B->zhl);
+        if ((rc = launch_ok())) return rc;
+        PfGemmArgs ug;
+        memset(&ug, 0, sizeof ug);
+        ug.wm[0] = (const uint8_t *)L->lup; ug.R = H; ug.K = X; ug.n0 = T;
+        ug.bsrc = B->zhl; ug.brows = T; ug.row_base = 0;
+        ug.y = B->y; ug.out_base = 0;
+        const unsigned grid_u = cdiv(H, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 32);
+        hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_u), dim3(PF_NT), 0, s, ug);
+        if ((rc = launch_ok())) return rc;
+        out_rows = T;
+        pos = NULL;
+        KC = 1;
+    }
     if (SI > 0) {
         // shared gate/up over every token (bf16 weights), then down; its output rows follow
         // the routed ones in y
@@ -948,16 +1045,16 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
         memset(&sd, 0, sizeof sd);
         sd.wm[0] = (const uint8_t *)L->sh_down; sd.R = H; sd.K = SI; sd.n0 = T;
         sd.bsrc = B->act_sh; sd.brows = T; sd.row_base = 0;
-        sd.y = B->y; sd.out_base = TK;
+        sd.y = B->y; sd.out_base = out_rows;
         const int nrb_sd = cdiv(H, (PF_NT / WAVE) * 2 * 16);
         const unsigned grid_sd = nrb_sd * cdiv(T, 32);
         hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_sd), dim3(PF_NT), 0, s, sd);
         if ((rc = launch_ok())) return rc;
-        sh_row0 = TK;
+        sh_row0 = out_rows;
     }
 
     hipLaunchKernelGGL(pf_combine, dim3(cdiv((size_t)T * (H / 4), PF_NT)), dim3(PF_NT), 0, s,
-                       B->y, B->pos_of, T, K, H, sh_row0, resid, out);
+                       B->y, pos, T, KC, H, sh_row0, resid, out);
     return launch_ok();
 }
 
@@ -969,7 +1066,8 @@ extern "C" int k3x_dev_prefill(k3x_moe_layer *L, float *out, const void *x, int 
     const int H = L->cfg.hidden, K = L->cfg.topk;
     const size_t es = (x_dtype == K3X_BF16) ? 2 : 4;
     // activation planes of one chunk stay under 1 GiB, so 32-bit buffer offsets hold
-    const size_t wide = (size_t)(H > L->cfg.moe_inter ? H : L->cfg.moe_inter);
+    size_t wide = (size_t)(H > L->cfg.moe_inter ? H : L->cfg.moe_inter);
+    if ((size_t)L->XL > wide) wide = (size_t)L->XL;
     int chunk = (int)(((size_t)1 << 30) / ((size_t)K * wide * 4));
     chunk = chunk < 1 ? 1 : (chunk > PF_CHUNK ? PF_CHUNK : chunk);
     int rc = k3x_pf_reserve(L, T < chunk ? T : chunk);

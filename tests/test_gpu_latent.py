@@ -181,3 +181,76 @@ def test_k3_decode_b8(torch, k3x, k3_layer):
     err = synth.rel_l2(out, o)
     say(f"  unique experts {len(np.unique(idx))}, rel_l2={err:.3e}")
     assert err < TOL
+
+
+# ------------------------------------------------------------------ prefill (T > 8)
+def decode_forward(torch, k3x, layer, x, bf16):
+    """The same tokens through the decode path, 8 at a time."""
+    outs, idxs = [], []
+    for t0 in range(0, x.shape[0], 8):
+        o, i, _ = dev_forward(torch, k3x, layer, x[t0:t0 + 8], bf16=bf16)
+        outs.append(o); idxs.append(i)
+    return np.concatenate(outs), np.concatenate(idxs)
+
+
+@pytest.mark.parametrize("T,bf16", [(9, False), (37, True), (130, False)])
+def test_latent_prefill_vs_oracle(torch, k3x, tiny_lat, T, bf16):
+    say(f"case: tiny latent layer prefill T={T} bf16={bf16} vs oracle")
+    L, layer = tiny_lat
+    x = L.x(T, bf16=bf16, stream_sub=50 + T)
+    o, idx, wt, _ = L.oracle_moe(x)
+    out, i2, w2 = dev_forward(torch, k3x, layer, x, bf16=bf16)
+    assert np.array_equal(i2, idx)
+    np.testing.assert_allclose(w2, wt, rtol=1e-6)
+    err = synth.rel_l2(out, o)
+    say(f"  rel_l2={err:.3e}")
+    assert err < TOL
+
+
+@pytest.mark.parametrize("norm,shared", [(0, 2), (1, 0)])
+def test_latent_prefill_variants(torch, k3x, norm, shared):
+    say(f"case: tiny latent layer prefill T=40, latent_norm={norm}, n_shared={shared}, resid")
+    L = synth.tiny_latent(seed=13, latent_norm=norm, n_shared=shared)
+    layer = bank_layer(k3x, L)
+    x = L.x(40, bf16=False)
+    r = L.x(40, bf16=False, stream_sub=70)
+    o, idx, _, _ = L.oracle_moe(x)
+    out, i2, _ = dev_forward(torch, k3x, layer, x, resid=r)
+    assert np.array_equal(i2, idx)
+    err = synth.rel_l2(out, o + r)
+    say(f"  rel_l2={err:.3e}")
+    assert err < TOL
+    layer.close()
+
+
+def test_k3_prefill_256(torch, k3x, k3_layer):
+    """The K3 shape, one call of 256 bf16 tokens: routing of every token against the
+    oracle's router, every token against the decode path, a sample against the oracle."""
+    import oracle_lib as ol
+    say("case: K3 shape prefill, 256 bf16 tokens")
+    L, layer = k3_layer
+    T = 256
+    x = L.x(T, bf16=True, stream_sub=6)
+    out, idx, wt = dev_forward(torch, k3x, layer, x, bf16=True)
+    ri = np.empty((T, L.K), np.int32)
+    rw = np.empty((T, L.K), np.float32)
+    for t in range(T):
+        xt = np.ascontiguousarray(x[t])
+        ol.oracle().ko_router(ol.ptr(ri[t], ol.I32P), ol.ptr(rw[t], ol.F32P),
+                              ol.ptr(xt, ol.F32P), ol.ptr(L.gate, ol.F32P),
+                              ol.ptr(L.bias, ol.F32P), L.H, L.E, L.K, 1, 1.0)
+    assert np.array_equal(idx, ri)
+    np.testing.assert_allclose(wt, rw, rtol=1e-6)
+    say(f"  routing of all {T} tokens equals the oracle's; experts used "
+        f"{len(np.unique(idx))}")
+    o2, i2 = decode_forward(torch, k3x, layer, x, True)
+    assert np.array_equal(idx, i2)
+    err = synth.rel_l2(out, o2)
+    say(f"  rel_l2(prefill, decode) over {T} tokens = {err:.3e}")
+    assert err < 1e-5
+    sample = [0, 100, 255]
+    o, oi, _, _ = L.oracle_moe(x[sample])
+    assert np.array_equal(idx[sample], oi)
+    err = synth.rel_l2(out[sample], o)
+    say(f"  rel_l2(prefill, oracle) on tokens {sample} = {err:.3e}")
+    assert err < TOL

@@ -419,10 +419,11 @@ struct K1Args {
     int         *ready;            // k2's routing flag, cleared here
     const float *norm_w;           // RMSNorm weights [H] (fp32 x), or NULL
     float        eps;
-    // latent form: z = down . x for the routed experts (k1_zdown)
+    // latent form: z = down . x for the routed experts, and the selection (k1_zdown)
     const uint16_t *ldown;         // tiled bf16 [XL][H], or NULL
     int          XL;
     uint16_t    *zB;               // compact B set of z over whole super-quads of XL
+    KSArgs       ks;
 };
 
 #define RWAVES 4                     // waves per expert row in the router
@@ -622,12 +623,22 @@ __device__ void k1_down(const K1Args &a, float *lds, int rt)
     });
 }
 
-// The latent form's z = down . x, 16 rows per workgroup.  A launch of its own: folded
-// into k1_router_bset's grid, the two paths' register allocation merges badly (spills).
+// The latent form's second launch: workgroup 0 selects each token's experts from the
+// router's scores and publishes the routing (ks_route), the others work out z = down . x,
+// 16 rows each.  The routed workgroups of k2_gateup then start on a published routing
+// instead of waiting inside their own launch, where the selection's few loads queue
+// behind the streaming workgroups' (about 14 us at the K3 shape).  A launch of its own:
+// folded into k1_router_bset's grid, the two paths' register allocation merges badly
+// (spills).
+template <int NE>
 __global__ void __launch_bounds__(NT1) k1_zdown(K1Args a)
 {
     __shared__ float lds[(NT1 / WAVE - 1) * 4 * WAVE];
-    k1_down(a, lds, blockIdx.x);
+    if (blockIdx.x == 0) {
+        ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true);
+        return;
+    }
+    k1_down(a, lds, blockIdx.x - 1);
 }
 
 // Router logits of NT1 / WAVE / RWAVES experts (of the RMSNorm of x when norm_w is given),
@@ -668,6 +679,9 @@ struct K2Args {
     const uint16_t *rB;            // the routed experts' input set: xB, or z's in the latent form
     int            XL;             // its width (H, or the latent width)
     float          b1, b2;         // SiTU betas (0: that half uncapped)
+    int            rtw;            // row tiles per routed workgroup (1, 2 or 4)
+    int            sel_done;       // 1: the routing was published by an earlier launch
+                                   // (k1_zdown): no selection here, no wait
 };
 
 // Shared expert gate and up products for rows 16*rt .. +15 over the full K: four waves on
@@ -733,15 +747,19 @@ __device__ void k2_shared(const K2Args &a, float *lds, int rt)
 // far above the selection's few microseconds): a workgroup that gives up sets the error
 // word (k3x_moe_layer_check reports it) and leaves without touching the expert weights.
 
-// Gate and up products of 16 rows of one unique expert: four waves on interleaved
-// super-quads; SiTU-GLU, the token's routing weight for this expert (0 where the token did
-// not choose it) and the bf16 hi/lo split into the expert's activation slot.
+// Gate and up products of rtw row tiles (16 rows each) of one unique expert: the waves
+// are dealt over the tiles (4/rtw waves per tile, on interleaved super-quads of it);
+// SiTU-GLU, the token's routing weight for this expert (0 where the token did not choose
+// it) and the bf16 hi/lo split into the expert's activation slot.  Several tiles per
+// workgroup when a tile has few super-quads (a narrow latent width), so that each wave
+// streams a run of items and the per-workgroup staging and waits are amortised.
 template <bool EXACT, bool LDSB, int NE>
 __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
 {
     __shared__ float lds[(NT / WAVE - 1) * 8 * WAVE];
     __shared__ int s_go;
     if (blockIdx.x == 0) {
+        if (a.sel_done) return;
         ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -756,9 +774,11 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int NW = NT / WAVE;
     const int NC = 2 * a.T;
-    const int nTiles = a.I >> 4;
+    const int RTW = a.rtw, WPT = NW / RTW;           // tiles per workgroup, waves per tile
+    const int tw = wave % RTW, sw = wave / RTW;      // this wave's tile, its rank on it
+    const int nGroups = (a.I >> 4) / RTW;
     const int blk = blockIdx.x - 1 - a.n_sh;
-    const int u = blk / nTiles, rt = blk % nTiles;
+    const int u = blk / nGroups, g0 = (blk % nGroups) * RTW, rt = g0 + tw;
     const int nS = ((a.XL >> 7) + 3) >> 2;
     const uint32_t bbytes = (uint32_t)nS * 1024u * NC;
     if (LDSB) {                        // the input's B set into LDS while the routing is worked out
@@ -769,7 +789,8 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     if (threadIdx.x == 0) {
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         int go = 1;
-        while (__hip_atomic_load(a.ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+        while (!a.sel_done &&
+               __hip_atomic_load(a.ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
             if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) {
                 __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 go = 0;
@@ -788,10 +809,10 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     const uint8_t *ex = a.experts + (size_t)e * a.expert_bytes + (size_t)rt * tb;
     const rsrc_t rg = make_rsrc(ex + a.gate_off, tb);
     const rsrc_t ru = make_rsrc(ex + a.up_off, tb);
-    const int cnt = strided_count(wave, NW, nS);
+    const int cnt = strided_count(sw, WPT, nS);
     SQ g[2], v[2];
     auto ld = [&](int i, int k) AI {
-        const uint32_t o = k < cnt ? (uint32_t)(wave + NW * k) * SQ_BYTES : K3X_OOB;
+        const uint32_t o = k < cnt ? (uint32_t)(sw + WPT * k) * SQ_BYTES : K3X_OOB;
         sq_load(g[i], rg, o, lane);
         sq_load(v[i], ru, o, lane);
     };
@@ -800,18 +821,24 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     bf.init(a.rB, bbytes, NC, lane);
     f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
     ring_loop<2>(cnt, ld, [&](int i, int k) AI {
-        sq_mfma2<EXACT, LDSB>(dg, du, g[i], v[i], bf, wave + NW * k);
+        sq_mfma2<EXACT, LDSB>(dg, du, g[i], v[i], bf, sw + WPT * k);
     });
     float acc[8] = {dg[0], dg[1], dg[2], dg[3], du[0], du[1], du[2], du[3]};
-    wave_sum_lds<8, NT / WAVE>(acc, lds, wave, lane);
+    // the waves of one tile summed into its rank-0 wave (waves tw + RTW*j)
+    if (sw != 0)
+        for (int i = 0; i < 8; i++) lds[((wave - 1) * 8 + i) * WAVE + lane] = acc[i];
+    __syncthreads();
+    if (sw == 0)
+        for (int j = 1; j < WPT; j++)
+            for (int i = 0; i < 8; i++) acc[i] += lds[((tw + RTW * j - 1) * 8 + i) * WAVE + lane];
     // the slot holds whole super-quads; its quads past I/128 stay zero
     const int nSI = ((a.I >> 7) + 3) >> 2;
     const uint32_t slot = (uint32_t)nSI * 1024u * NC;
     uint8_t *dst = (uint8_t *)a.actB + (size_t)u * slot;
-    if (rt == 0)
+    if (g0 == 0)
         for (uint32_t o = (uint32_t)(a.I >> 7) * 256u * NC + threadIdx.x * 16u; o < slot; o += NT * 16u)
             *(u32x4 *)(dst + o) = (u32x4){0u, 0u, 0u, 0u};
-    if (wave != 0) return;
+    if (sw != 0) return;
     uint16_t *d16 = (uint16_t *)dst;
     per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&s)[8]) AI {
         const float w = __hip_atomic_load(&rte->wtok[u][tok], __ATOMIC_RELAXED,
@@ -1216,17 +1243,26 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 1, s))) return rc;
     int ev = 2;                        // the next timing event
+    KSArgs ks;
+    ks.score = L->score; ks.choice = L->choice; ks.E = c->n_experts; ks.K = c->topk;
+    ks.renorm = c->moe_renorm; ks.routed_scale = c->routed_scale; ks.route = L->route;
+    ks.idx = L->idx; ks.wt = L->wt; ks.uidx = idx; ks.uwt = wt; ks.T = T;
     if (L->lat) {
-        hipLaunchKernelGGL(k1_zdown, dim3(X / 16), dim3(NT1), 0, s, a1);
+        a1.ks = ks;
+        const dim3 gz(1 + X / 16);
+        const size_t lz = sizeof(KSLds);
+        if (c->n_experts <= 128)      hipLaunchKernelGGL(k1_zdown<2>, gz, dim3(NT1), lz, s, a1);
+        else if (c->n_experts <= 256) hipLaunchKernelGGL(k1_zdown<4>, gz, dim3(NT1), lz, s, a1);
+        else if (c->n_experts <= 384) hipLaunchKernelGGL(k1_zdown<6>, gz, dim3(NT1), lz, s, a1);
+        else if (c->n_experts <= 512) hipLaunchKernelGGL(k1_zdown<8>, gz, dim3(NT1), lz, s, a1);
+        else                          hipLaunchKernelGGL(k1_zdown<16>, gz, dim3(NT1), lz, s, a1);
         if ((rc = launch_ok())) return rc;
         if ((rc = record(L, ev++, s))) return rc;
     }
 
     K2Args a2;
-    KSArgs &as = a2.ks;
-    as.score = L->score; as.choice = L->choice; as.E = c->n_experts; as.K = c->topk;
-    as.renorm = c->moe_renorm; as.routed_scale = c->routed_scale; as.route = L->route;
-    as.idx = L->idx; as.wt = L->wt; as.uidx = idx; as.uwt = wt; as.T = T;
+    a2.ks = ks;
+    a2.sel_done = L->lat;
     a2.route = L->route; a2.ready = &L->route->ready; a2.err = &L->route->err;
     a2.wait_ticks = L->wait_ticks; a2.publish = !L->no_publish;
     a2.experts = L->experts; a2.expert_bytes = L->expert_bytes;
@@ -1235,7 +1271,9 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a2.n_sh = L->SI > 0 ? L->SI / 16 : 0;
     a2.sh_gate = L->sh_gate; a2.sh_up = L->sh_up; a2.SI = L->SI; a2.shB = L->shB;
     a2.rB = L->lat ? L->zB : L->xB; a2.XL = X; a2.b1 = L->b1; a2.b2 = L->b2;
-    const int n_routed = T * c->topk * (I / 16);
+    // row tiles per routed workgroup: each wave streams at least a few super-quads
+    a2.rtw = nSX >= 12 ? 1 : (nSX >= 6 ? 2 : 4);
+    const int n_routed = T * c->topk * (I / 16) / a2.rtw;
     // the routed input's set and x's (the shared experts'): staged when both fit
     const uint32_t xset = (uint32_t)nS * 1024u * NC, rset = (uint32_t)nSX * 1024u * NC;
     const uint32_t bset = xset > rset ? xset : rset;

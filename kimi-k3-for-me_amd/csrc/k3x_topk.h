@@ -67,14 +67,19 @@ __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, 
                           int *out_e = nullptr, float *out_w = nullptr)
 {
     uint64_t pk[NE];
-    float sc[NE];
+    float sc[NE], cv[NE];
 #pragma unroll
     for (int c = 0; c < NE; c++) {
         const int e = lane * NE + c;
         const uint32_t o = e < E ? row_off + 4u * (uint32_t)e : K3X_OOB;
-        const float v = bload_f32<CP>(cr, o);
+        cv[c] = bload_f32<CP>(cr, o);
         sc[c] = bload_f32<CP>(sr, o);
-        const uint32_t k = choice_key(v);
+    }
+    SCHED_FENCE();      // both rows' loads in flight together: one memory round trip
+#pragma unroll
+    for (int c = 0; c < NE; c++) {
+        const int e = lane * NE + c;
+        const uint32_t k = choice_key(cv[c]);
         pk[c] = (e < E && k > K_NEG_INF) ? ((uint64_t)k << 32) | (uint64_t)(~(uint32_t)e) : 0ull;
     }
     uint64_t prev = ~0ull;        // the previous round's winner (none yet: above all)

@@ -1,0 +1,119 @@
+/* k3x_store.h - the checkpoint side of the MoE block: safetensors shards indexed by
+ * tensor name, routed experts resolved and read as whole byte runs, and a layer's experts
+ * streamed from the shards straight into its HBM arena.
+ *
+ * The reference reads its Kimi K3 checkpoint through
+ *
+ *     int  k3_st_open(K3St *s, const char *dir);                        k3_st.h:69
+ *     const K3Tensor *k3_st_find(const K3St *s, const char *name);      k3_st.h:75
+ *     int64_t k3_st_read(const K3St *s, const K3Tensor *t, void *buf);  k3_st.h:78
+ *     int  k3_expert_ref(const K3St *s, int layer, int expert, K3ExpertRef *r);
+ *     int64_t k3_expert_load(const K3St *s, const K3ExpertRef *r, unsigned char *buf);
+ *                                                                       k3_load.h:47-52
+ *
+ * and hands experts to the MoE block through a K3ExpertSrc (k3.h:521-544).  This header
+ * gives the same operations (plain C: pointers, sizes, status codes) plus the supplier
+ * over a store and a whole-layer upload from it.
+ *
+ * Format (safetensors): [8-byte little-endian header length N][N bytes of JSON][data];
+ * each JSON entry {"dtype", "shape", "data_offsets": [begin, end]} with offsets relative
+ * to the end of the header; "__metadata__" is skipped.  Every *.safetensors file of the
+ * directory is a shard, numbered in byte order of the file names.
+ *
+ * Expert tensors are named "language_model.model.layers.L.block_sparse_moe.experts.E.wM.
+ * weight_packed" / ".weight_scale" (M = 1 gate, 2 down, 3 up; k3_load.c:11), U8, 2-D,
+ * packed [rows][width/2], scales [rows][width/32].  When an expert's six tensors tile one
+ * contiguous span of a shard (w1 packed, w1 scale, w2 packed, ... in the released
+ * checkpoint, k3_load.h:3-22) the expert is read with one pread; otherwise six.
+ */
+#ifndef K3X_STORE_H
+#define K3X_STORE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "k3x_moe.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct k3x_store k3x_store;
+
+/* dtypes of K3Dtype (k3_st.h:34-35) the reader accepts */
+enum { K3X_DT_UNKNOWN = 0, K3X_DT_U8 = 1, K3X_DT_BF16 = 2, K3X_DT_F16 = 3, K3X_DT_F32 = 4 };
+
+/* One tensor, as K3Tensor (k3_st.h:37-45): off is the ABSOLUTE byte offset in its shard. */
+typedef struct k3x_tensor_info {
+    int     shard;
+    int     dtype;
+    int     ndim;
+    int64_t shape[4];
+    int64_t off;
+    int64_t nbytes;
+} k3x_tensor_info;
+
+/* Open and index every *.safetensors file of dir (k3_st_open).  Fails with K3X_E_ARG on a
+ * malformed header, an unsupported dtype, a tensor whose byte count does not match its
+ * shape or whose span leaves the file, or a name seen twice. */
+int  k3x_store_open(const char *dir, k3x_store **out);
+void k3x_store_close(k3x_store *s);
+int  k3x_store_count(const k3x_store *s);                 /* tensors indexed */
+int  k3x_store_shards(const k3x_store *s);                /* shard files     */
+
+/* O(1) lookup by name (k3_st_find): 0 and *info, or K3X_E_ARG when absent. */
+int  k3x_store_find(const k3x_store *s, const char *name, k3x_tensor_info *info);
+
+/* The raw bytes of a tensor (k3_st_read) into buf (cap bytes): the byte count, or a
+ * negative status (K3X_E_ARG: absent or cap too small; K3X_E_HIP is never returned). */
+int64_t k3x_store_read(const k3x_store *s, const char *name, void *buf, int64_t cap);
+
+/* One quantised matrix inside an expert's byte run (K3QMat, k3_load.h:30-35). */
+typedef struct k3x_qmat {
+    int64_t p_off, p_bytes;   /* packed nibbles, offset within the run */
+    int64_t s_off, s_bytes;   /* E8M0 scales, offset within the run    */
+    int     rows, pcols;      /* packed [rows][pcols]; width = 2 * pcols */
+    int     scols;            /* scales [rows][scols], scols = width / 32 */
+} k3x_qmat;
+
+/* An expert's six tensors (K3ExpertRef, k3_load.h:37-45): m[0] w1 (gate), m[1] w2
+ * (down), m[2] w3 (up). */
+typedef struct k3x_expert_ref {
+    int     layer, expert, shard;
+    int64_t off;              /* absolute offset of the run (contiguous) */
+    int64_t nbytes;           /* bytes of the run / of the packed buffer */
+    int     contiguous;       /* 1: one read                             */
+    k3x_qmat m[3];
+} k3x_expert_ref;
+
+/* Resolve and validate an expert (k3_expert_ref, k3_load.c:15-105): all six tensors
+ * present, U8, 2-D, packed and scale rows equal, 32 elements per scale, one shard.
+ * 0, or K3X_E_ARG (with the reason on stderr, as the reference). */
+int  k3x_store_expert_ref(const k3x_store *s, int layer, int expert, k3x_expert_ref *r);
+
+/* The expert's bytes into buf (r->nbytes): one read when contiguous, else six into the
+ * same layout (k3_expert_load, k3_load.c:107-135).  Bytes read, or a negative status. */
+int64_t k3x_store_expert_load(const k3x_store *s, const k3x_expert_ref *r, unsigned char *buf);
+
+/* A supplier over the store (the K3ExpertSrc seam): get(layer, expert) reads the expert
+ * into a buffer the supplier owns and points the k3x_expert_q into it (valid until the
+ * next get).  k3x_store_src_fetches() counts the reads. */
+int  k3x_store_src_create(k3x_store *s, k3x_expert_src **out);
+void k3x_store_src_destroy(k3x_expert_src *src);
+long k3x_store_src_fetches(const k3x_expert_src *src);
+
+/* A layer with its routed experts streamed from the store into HBM (no counterpart in
+ * the reference, which keeps experts on disk and reads them per token, k3_ops.c:1905-1931):
+ * each expert's run is read into one of two pinned host buffers, copied to the device
+ * and re-laid out there while the next run is read.  w supplies the router, bias, shared,
+ * latent weights as for k3x_moe_layer_create (w->src and w->bank are ignored).  Expert
+ * shapes are checked against c: w1/w3 [moe_inter][X], w2 [X][moe_inter], X the latent
+ * width (or hidden).  A missing or malformed expert counts in k3x_expert_drops and fails
+ * with K3X_E_DROP. */
+int  k3x_moe_layer_create_from_store(const k3x_cfg *c, const k3x_moe_w *w, k3x_store *s,
+                                     int layer, int device, k3x_moe_layer **out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

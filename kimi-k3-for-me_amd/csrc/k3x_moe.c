@@ -7,6 +7,7 @@
  * instead of abort()).
  */
 #include "k3x_internal.h"
+#include "../../include/k3x_store.h"
 
 #include <hip/hip_runtime_api.h>
 #include <math.h>
@@ -298,6 +299,88 @@ int k3x_moe_layer_create(const k3x_cfg *c, const k3x_moe_w *w, int device,
     return 0;
 fail:
     if (stage) hipFree(stage);
+    layer_free(L);
+    return rc;
+}
+
+/* ---------------------------------------------------------------- from a store ---- */
+/* An expert's matrices have the layer's shapes: w1 (gate) and w3 (up) [I][X], w2 (down)
+ * [X][I], X the experts' width. */
+static int store_shape_ok(const k3x_expert_ref *r, int I, int X)
+{
+    const int rows[3] = {I, X, I}, width[3] = {X, I, X};
+    for (int i = 0; i < 3; i++)
+        if (r->m[i].rows != rows[i] || r->m[i].pcols * 2 != width[i] || r->m[i].scols * 32 != width[i])
+            return 0;
+    return 1;
+}
+
+int k3x_moe_layer_create_from_store(const k3x_cfg *c, const k3x_moe_w *w, k3x_store *st,
+                                    int layer, int device, k3x_moe_layer **out)
+{
+    if (!c || !w || !st || !out || !w->gate) return K3X_E_ARG;
+    *out = NULL;
+    k3x_moe_layer *L = NULL;
+    int rc = new_layer(c, device, &L);
+    if (rc) return rc;
+    const int H = c->hidden, E = c->n_experts, I = c->moe_inter, X = L->XL;
+    const size_t run = 3 * ((size_t)I * X / 2 + (size_t)I * X / 32);
+    unsigned char *hb[2] = {NULL, NULL};
+    uint8_t *db[2] = {NULL, NULL};
+    hipEvent_t ev[2] = {NULL, NULL};
+    hipStream_t sm = NULL;
+    HIPCHK(hipMemcpy(L->router, w->gate, (size_t)E * H * 4, hipMemcpyHostToDevice));
+    if (w->bias) HIPCHK(hipMemcpy(L->bias, w->bias, (size_t)E * 4, hipMemcpyHostToDevice));
+    RCCHK(upload_shared(L, w->sh1, w->sh3, w->sh2));
+    RCCHK(upload_latent(L, w->down, w->up, w->latent_norm));
+    /* two pinned host buffers and two device staging areas in turn: run e is read from
+     * the shard while run e-1 is copied and re-laid out on the stream */
+    HIPCHK(hipStreamCreate(&sm));
+    for (int b = 0; b < 2; b++) {
+        HIPCHK(hipHostMalloc((void **)&hb[b], run, hipHostMallocDefault));
+        HIPCHK(hipMalloc((void **)&db[b], run));
+        HIPCHK(hipEventCreateWithFlags(&ev[b], hipEventDisableTiming));
+    }
+    for (int e = 0; e < E; e++) {
+        const int b = e & 1;
+        if (e >= 2) HIPCHK(hipEventSynchronize(ev[b]));
+        k3x_expert_ref r;
+        if (k3x_store_expert_ref(st, layer, e, &r) || !store_shape_ok(&r, I, X) ||
+            (size_t)r.nbytes > run || k3x_store_expert_load(st, &r, hb[b]) != r.nbytes) {
+            k3x_expert_drops++;
+            fprintf(stderr, "EXPERT DROP: layer %d expert %d could not be read from the store\n",
+                    layer, e);
+            rc = K3X_E_DROP;
+            goto fail;
+        }
+        const k3x_expert_q q = {hb[b] + r.m[0].p_off, hb[b] + r.m[0].s_off,
+                                hb[b] + r.m[2].p_off, hb[b] + r.m[2].s_off,
+                                hb[b] + r.m[1].p_off, hb[b] + r.m[1].s_off};
+        L->special |= scale_flags(&q, (size_t)I * X / 32);
+        uint8_t *base = L->experts + (size_t)e * L->expert_bytes;
+        HIPCHK(hipMemcpyAsync(db[b], hb[b], (size_t)r.nbytes, hipMemcpyHostToDevice, sm));
+        RCCHK(k3x_dev_tile_fp4(base + L->gate_off, db[b] + r.m[0].p_off, db[b] + r.m[0].s_off, I, X, sm));
+        RCCHK(k3x_dev_tile_fp4(base + L->up_off, db[b] + r.m[2].p_off, db[b] + r.m[2].s_off, I, X, sm));
+        RCCHK(k3x_dev_tile_fp4(base + L->down_off, db[b] + r.m[1].p_off, db[b] + r.m[1].s_off, X, I, sm));
+        HIPCHK(hipEventRecord(ev[b], sm));
+    }
+    HIPCHK(hipStreamSynchronize(sm));
+    for (int b = 0; b < 2; b++) {
+        hipEventDestroy(ev[b]);
+        hipFree(db[b]);
+        hipHostFree(hb[b]);
+    }
+    hipStreamDestroy(sm);
+    *out = L;
+    return 0;
+fail:
+    if (sm) hipStreamSynchronize(sm);
+    for (int b = 0; b < 2; b++) {
+        if (ev[b]) hipEventDestroy(ev[b]);
+        if (db[b]) hipFree(db[b]);
+        if (hb[b]) hipHostFree(hb[b]);
+    }
+    if (sm) hipStreamDestroy(sm);
     layer_free(L);
     return rc;
 }

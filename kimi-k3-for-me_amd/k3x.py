@@ -32,7 +32,14 @@ EXPORTS = [
     "k3x_synth_normal_f32", "k3x_synth_normal_bf16", "k3x_moe_layer_set_timing",
     "k3x_moe_layer_last_ms", "k3x_stack_create", "k3x_stack_forward", "k3x_stack_destroy",
     "k3x_moe_layer_check", "k3x_moe_layer_set_route_wait",
+    # include/k3x_store.h
+    "k3x_store_open", "k3x_store_close", "k3x_store_count", "k3x_store_shards",
+    "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
+    "k3x_store_src_create", "k3x_store_src_destroy", "k3x_store_src_fetches",
+    "k3x_moe_layer_create_from_store",
 ]
+
+DT_U8, DT_BF16, DT_F16, DT_F32 = 1, 2, 3, 4
 
 
 class K3XError(RuntimeError):
@@ -66,6 +73,23 @@ class MoeW(C.Structure):
                 ("sh3", C.c_void_p), ("sh2", C.c_void_p), ("src", C.POINTER(ExpertSrc)),
                 ("bank", C.POINTER(ExpertQ)), ("layer", C.c_int), ("down", C.c_void_p),
                 ("up", C.c_void_p), ("latent_norm", C.c_void_p)]
+
+
+class TensorInfo(C.Structure):
+    _fields_ = [("shard", C.c_int), ("dtype", C.c_int), ("ndim", C.c_int),
+                ("shape", C.c_int64 * 4), ("off", C.c_int64), ("nbytes", C.c_int64)]
+
+
+class QMat(C.Structure):
+    _fields_ = [("p_off", C.c_int64), ("p_bytes", C.c_int64), ("s_off", C.c_int64),
+                ("s_bytes", C.c_int64), ("rows", C.c_int), ("pcols", C.c_int),
+                ("scols", C.c_int)]
+
+
+class ExpertRef(C.Structure):
+    _fields_ = [("layer", C.c_int), ("expert", C.c_int), ("shard", C.c_int),
+                ("off", C.c_int64), ("nbytes", C.c_int64), ("contiguous", C.c_int),
+                ("m", QMat * 3)]
 
 
 class SynthSpec(C.Structure):
@@ -114,6 +138,24 @@ def lib():
         L.k3x_stack_forward.argtypes = [vp, vp, i, vp]
         L.k3x_stack_destroy.argtypes = [vp]
         L.k3x_stack_destroy.restype = None
+        L.k3x_store_open.argtypes = [C.c_char_p, C.POINTER(vp)]
+        L.k3x_store_close.argtypes = [vp]
+        L.k3x_store_close.restype = None
+        L.k3x_store_count.argtypes = [vp]
+        L.k3x_store_shards.argtypes = [vp]
+        L.k3x_store_find.argtypes = [vp, C.c_char_p, C.POINTER(TensorInfo)]
+        L.k3x_store_read.argtypes = [vp, C.c_char_p, vp, C.c_int64]
+        L.k3x_store_read.restype = C.c_int64
+        L.k3x_store_expert_ref.argtypes = [vp, i, i, C.POINTER(ExpertRef)]
+        L.k3x_store_expert_load.argtypes = [vp, C.POINTER(ExpertRef), vp]
+        L.k3x_store_expert_load.restype = C.c_int64
+        L.k3x_store_src_create.argtypes = [vp, C.POINTER(vp)]
+        L.k3x_store_src_destroy.argtypes = [vp]
+        L.k3x_store_src_destroy.restype = None
+        L.k3x_store_src_fetches.argtypes = [vp]
+        L.k3x_store_src_fetches.restype = C.c_long
+        L.k3x_moe_layer_create_from_store.argtypes = [C.POINTER(Cfg), C.POINTER(MoeW), vp, i, i,
+                                                      C.POINTER(vp)]
         _lib = L
     return _lib
 
@@ -198,6 +240,19 @@ class MoELayer:
         h = C.c_void_p()
         _check(lib().k3x_moe_layer_create(C.byref(cfg), C.byref(w), device, C.byref(h)),
                "k3x_moe_layer_create")
+        return cls(h.value, cfg)
+
+    @classmethod
+    def from_store(cls, cfg, gate, bias, store, layer, sh1=None, sh3=None, sh2=None, device=0,
+                   down=None, up=None, latent_norm=None):
+        """Routed experts streamed from a Store (k3x_moe_layer_create_from_store); the
+        other weights as numpy arrays."""
+        w = MoeW(_vp(gate), _vp(bias), _vp(sh1), _vp(sh3), _vp(sh2), None, None, layer,
+                 _vp(down), _vp(up), _vp(latent_norm))
+        h = C.c_void_p()
+        _check(lib().k3x_moe_layer_create_from_store(C.byref(cfg), C.byref(w), store.h, layer,
+                                                     device, C.byref(h)),
+               "k3x_moe_layer_create_from_store")
         return cls(h.value, cfg)
 
     @classmethod
@@ -325,3 +380,57 @@ class Stack:
             self.close()
         except Exception:
             pass
+
+
+class Store:
+    """A directory of safetensors shards (include/k3x_store.h), indexed by tensor name."""
+
+    def __init__(self, path):
+        self.h = C.c_void_p()
+        _check(lib().k3x_store_open(os.fsencode(path), C.byref(self.h)), "k3x_store_open")
+
+    def close(self):
+        if self.h:
+            lib().k3x_store_close(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def count(self):
+        return lib().k3x_store_count(self.h)
+
+    def shards(self):
+        return lib().k3x_store_shards(self.h)
+
+    def find(self, name):
+        t = TensorInfo()
+        if lib().k3x_store_find(self.h, name.encode(), C.byref(t)) != 0:
+            return None
+        return t
+
+    def read(self, name):
+        t = self.find(name)
+        if t is None:
+            raise K3XError(-1, f"k3x_store_read {name}")
+        buf = np.empty(t.nbytes, np.uint8)
+        _check(int(lib().k3x_store_read(self.h, name.encode(), buf.ctypes.data, t.nbytes)),
+               "k3x_store_read")
+        return buf
+
+    def expert_ref(self, layer, expert):
+        r = ExpertRef()
+        _check(lib().k3x_store_expert_ref(self.h, layer, expert, C.byref(r)),
+               "k3x_store_expert_ref")
+        return r
+
+    def expert_load(self, layer, expert):
+        """(ref, bytes of the expert's run in the ref's layout)."""
+        r = self.expert_ref(layer, expert)
+        buf = np.empty(r.nbytes, np.uint8)
+        _check(int(lib().k3x_store_expert_load(self.h, C.byref(r), buf.ctypes.data)),
+               "k3x_store_expert_load")
+        return r, buf

@@ -12,11 +12,12 @@ import pytest
 import synth
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "k3x_moe.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
 
 
 def declared():
-    txt = open(HEADER).read()
+    txt = "".join(open(h).read() for h in HEADERS)
     funcs = set(re.findall(r"\b(k3x_\w+)\s*\(", txt))
     data = set(re.findall(r"extern\s+long\s+(k3x_\w+)", txt))
     return funcs | data
@@ -38,7 +39,7 @@ def test_exports_every_declared_symbol(k3x):
 
 def test_header_compiles_as_c_and_cxx(tmp_path):
     src = tmp_path / "t.c"
-    src.write_text('#include "k3x_moe.h"\nint main(void){return K3X_OK;}\n')
+    src.write_text('#include "k3x_moe.h"\n#include "k3x_store.h"\nint main(void){return K3X_OK;}\n')
     inc = os.path.join(ROOT, "include")
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-I", inc, str(src)],
                    check=True)

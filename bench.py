@@ -9,7 +9,7 @@ over 4 layers of that shape, so every step reads its weights from HBM (a single 
 called back to back finds its router and shared expert, 99 MB, still in the 256 MB
 last-level cache; that figure is reported as warm_one_layer_us_per_token).  Weights are
 synthetic (seeded generator, random init).  The record also carries the 2048-token
-prefill leg, the 8-layer stack leg and the K3 LatentMoE decode leg.
+prefill leg, the 8-layer stack leg, the K3 LatentMoE decode leg and a trunk-product leg.
 
 Prints ONE JSON line (rank 0):
   value        microseconds per token for the whole layer (lower is better)
@@ -304,6 +304,53 @@ def k3_prefill_leg(torch, k3x, reps=3):
             "outputs_finite": finite, "reps": reps}
 
 
+def trunk_leg(torch, k3x, reps=48, nrot=4):
+    """bf16 trunk matrices of 7168 x 7168 (103 MB each, the size class of the K3 trunk's
+    projections; `nrot` of them used in turn so that no call finds its matrix in the
+    256 MB last-level cache) applied to 1 bf16 row (the GEMV: HBM-bound, bytes = the
+    matrix) and to 2048 rows (the GEMM: 2 * 2048 * 7168^2 FLOP; bf16 input is one B
+    column per row)."""
+    n = 7168
+    trs = []
+    for j in range(nrot):
+        w = k3x.synth_normal_bf16(n * n, k3x.synth_key(77, j, k3x.STREAM_SH1, 0), 0.0, 0.02)
+        trs.append(k3x.Trunk(w.reshape(n, n)))
+    rec = {"workload": f"bf16 trunk product, 7168 x 7168 weights, {nrot} matrices in turn"}
+    stream = torch.cuda.Stream()
+    for T in (1, 2048):
+        xs = k3x.synth_normal_f32(T * n, k3x.synth_key(77, 0, k3x.STREAM_X, T))
+        x = torch.from_numpy(xs.reshape(T, n)).cuda().to(torch.bfloat16).contiguous()
+        y = torch.empty((T, n), dtype=torch.float32, device="cuda")
+        r = reps if T == 1 else 8
+        with torch.cuda.stream(stream):
+            for i in range(nrot):
+                trs[i].apply(y.data_ptr(), n, x.data_ptr(), k3x.K3X_BF16, n, T, stream.cuda_stream)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(r):
+                trs[i % nrot].apply(y.data_ptr(), n, x.data_ptr(), k3x.K3X_BF16, n, T,
+                                    stream.cuda_stream)
+            e1.record(stream)
+            torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / r
+        if T == 1:
+            gbs = n * n * 2 / (us * 1e-6) / 1e9
+            rec["gemv_t1_us"] = round(us, 2)
+            rec["gemv_t1_gbs"] = round(gbs, 1)
+            rec["gemv_t1_hbm_frac"] = round(gbs / HBM_PEAK_GBS, 4)
+        else:
+            tf = 2.0 * T * n * n / (us * 1e-6) / 1e12
+            rec["gemm_t2048_us"] = round(us, 1)
+            rec["gemm_t2048_tflops"] = round(tf, 1)
+            rec["gemm_t2048_bf16_peak_frac"] = round(tf / 2500.0, 4)
+        del x, y
+    for tr in trs:
+        tr.close()
+    torch.cuda.empty_cache()
+    return rec
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed counter summary (FETCH_SIZE and
     WRITE_SIZE runs scaled by a plain copy's readings), or None."""
@@ -400,6 +447,9 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the 2048-token prefill leg")
     ap.add_argument("--no-stack", action="store_true", help="skip the 8-layer stack leg")
     ap.add_argument("--no-k3", action="store_true", help="skip the K3 LatentMoE decode leg")
+    ap.add_argument("--no-trunk", action="store_true", help="skip the trunk product leg")
+    ap.add_argument("--trunk-only", action="store_true",
+                    help="only run the trunk product leg and print its record")
     ap.add_argument("--k3-only", action="store_true",
                     help="only run the K3 LatentMoE decode leg and print its record")
     ap.add_argument("--stack-only", action="store_true",
@@ -427,6 +477,9 @@ def main():
         return
     if args.stack_only:
         print(json.dumps(stack_leg(torch, load_k3x())), flush=True)
+        return
+    if args.trunk_only:
+        print(json.dumps(trunk_leg(torch, load_k3x())), flush=True)
         return
     if args.k3_only:
         k = load_k3x()
@@ -534,6 +587,8 @@ def main():
         rec["k3_latent"] = k3_leg(torch, k3x, min(args.steps, 100), min(args.warmup, 10))
         if not args.no_prefill:
             rec["k3_latent"]["prefill"] = k3_prefill_leg(torch, k3x)
+    if not args.no_trunk:
+        rec["trunk"] = trunk_leg(torch, k3x)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(min_seconds=args.cpu_seconds)
     else:

@@ -543,19 +543,19 @@ __device__ void k1_router(const K1Args &a, float *lds, float *s_inv)
     }
 }
 
-// One quad of x's B fragments, raw: lane (n, kq) holds token n/2's elements 128q + 32kq +
+// One quad of x's B fragments, raw (x rows ldx elements apart): lane (n, kq) holds token n/2's elements 128q + 32kq +
 // 8t .. +7 for each product t (fp32: two float4; bf16: one 16-byte load, lo lanes zero).
 // Split into bf16 hi/lo only when used, so the loads stay in flight in a ring.
 struct XQ {
     f32x4 v[4][2];
 };
 
-__device__ __forceinline__ void xq_load(XQ &b, rsrc_t xr, int x_bf16, int H, int NC, int q,
+__device__ __forceinline__ void xq_load(XQ &b, rsrc_t xr, int x_bf16, int ldx, int NC, int q,
                                         bool on, int lane)
 {
     const int n0 = lane & 15, kq = lane >> 4;
     const int n = n0 < NC ? n0 : 0, tok = n >> 1, hl = n & 1;
-    const uint32_t e0 = (uint32_t)(tok * H + q * 128 + kq * 32);
+    const uint32_t e0 = (uint32_t)(tok * ldx + q * 128 + kq * 32);
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         if (x_bf16) {
@@ -576,35 +576,48 @@ __device__ __forceinline__ u32x4 xq_get(const XQ &b, int x_bf16, int t, int lane
     return bfrag_of(v, lane & 1);
 }
 
-// The latent down projection z = down . x (k3_mmw_batch, k3_ops.c:1871) for rows
-// 16*rt .. +15: four waves on interleaved bf16 quads, x's B fragments read from x with
-// each quad's weights; z's hi/lo B fragments into zB for k2's routed products.
-__device__ void k1_down(const K1Args &a, float *lds, int rt)
+// One 16-row tile of a tiled bf16 matrix (K columns) times the T activation rows of x
+// (row stride ldx elements, fp32 or bf16): four waves on interleaved quads, each quad's
+// B fragments read from x with its weights (x is small and stays in the caches).  The
+// workgroup's waves are summed in LDS; wave 0 ends with acc (per_token's layout).
+__device__ __forceinline__ void bf16_tile_x(const uint16_t *wtile, int K, const void *x,
+                                            int x_bf16, int ldx, int T, float *lds,
+                                            float (&acc)[4])
 {
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     constexpr int NW = NT1 / WAVE;
-    const int nQ = a.H >> 7, NC = 2 * a.T;
+    const int nQ = K >> 7, NC = 2 * T;
     const int cnt = strided_count(wave, NW, nQ);
-    const rsrc_t rw = make_rsrc(a.ldown + (size_t)rt * 16 * a.H, (uint32_t)nQ * 4096u);
-    const rsrc_t xr = make_rsrc(a.x, (uint32_t)(a.T * a.H * (a.x_bf16 ? 2 : 4)));
+    const rsrc_t rw = make_rsrc(wtile, (uint32_t)nQ * 4096u);
+    const rsrc_t xr = make_rsrc(x, (uint32_t)(((T - 1) * ldx + K) * (x_bf16 ? 2 : 4)));
     QB w[2];
     XQ b[2];
     auto ld = [&](int i, int k) AI {
         const bool on = k < cnt;
         const int q = wave + NW * k;
         qb_load(w[i], rw, on ? (uint32_t)q * 4096u : K3X_OOB, lane);
-        xq_load(b[i], xr, a.x_bf16, a.H, NC, q, on, lane);
+        xq_load(b[i], xr, x_bf16, ldx, NC, q, on, lane);
     };
     ring_prime<2>(ld);
     f32x4 d = {0.f, 0.f, 0.f, 0.f};
     ring_loop<2>(cnt, ld, [&](int i, int k) AI {
         u32x4 bb[4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) bb[t] = xq_get(b[i], a.x_bf16, t, lane);
+        for (int t = 0; t < 4; t++) bb[t] = xq_get(b[i], x_bf16, t, lane);
         qb_mfma(d, w[i], bb);
     });
-    float acc[4] = {d[0], d[1], d[2], d[3]};
+    acc[0] = d[0]; acc[1] = d[1]; acc[2] = d[2]; acc[3] = d[3];
     wave_sum_lds<4, NW>(acc, lds, wave, lane);
+}
+
+// The latent down projection z = down . x (k3_mmw_batch, k3_ops.c:1871) for rows
+// 16*rt .. +15, and z's hi/lo B fragments into zB for k2's routed products.
+__device__ void k1_down(const K1Args &a, float *lds, int rt)
+{
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    const int NC = 2 * a.T;
+    float acc[4];
+    bf16_tile_x(a.ldown + (size_t)rt * 16 * a.H, a.H, a.x, a.x_bf16, a.H, a.T, lds, acc);
     // z's set holds whole super-quads; its quads past XL/128 stay zero
     const int nSX = ((a.XL >> 7) + 3) >> 2;
     if (rt == 0)
@@ -1349,4 +1362,38 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     else              hipLaunchKernelGGL((k4_up<false, false>), g4, dim3(NT3), l4, s, a4);
     if ((rc = launch_ok())) return rc;
     return record(L, ev, s);
+}
+
+// ------------------------------------------------------------------ trunk products
+// A bf16 trunk matrix (tiled, [out][in]) times T <= 8 activation rows: one workgroup per
+// 16 output rows, Y[t*ldy + o] = W[o] . X[t*ldx] (k3_mmw_batch_ld, k3_ops.c:624-976).
+struct TrunkArgs {
+    const uint16_t *W;
+    int             in, out;
+    const void     *x;
+    int             x_bf16, ldx, T;
+    float          *y;
+    int             ldy;
+};
+
+__global__ void __launch_bounds__(NT1) trunk_gemv(TrunkArgs a)
+{
+    __shared__ float lds[(NT1 / WAVE - 1) * 4 * WAVE];
+    const int rt = blockIdx.x, lane = threadIdx.x % WAVE;
+    float acc[4];
+    bf16_tile_x(a.W + (size_t)rt * 16 * a.in, a.in, a.x, a.x_bf16, a.ldx, a.T, lds, acc);
+    if (wave_id() != 0) return;
+    per_token<4>(acc, 2 * a.T, lane, [&](int r0, int tok, const float (&v)[4]) AI {
+        for (int i = 0; i < 4; i++) a.y[(size_t)tok * a.ldy + rt * 16 + r0 + i] = v[i];
+    });
+}
+
+extern "C" int k3x_dev_trunk_gemv(const uint16_t *W, int in, int out, float *y, int ldy,
+                                  const void *x, int x_dtype, int ldx, int T, void *stream)
+{
+    TrunkArgs a;
+    a.W = W; a.in = in; a.out = out; a.x = x; a.x_bf16 = (x_dtype == K3X_BF16); a.ldx = ldx;
+    a.T = T; a.y = y; a.ldy = ldy;
+    hipLaunchKernelGGL(trunk_gemv, dim3(out / 16), dim3(NT1), 0, (hipStream_t)stream, a);
+    return launch_ok();
 }

@@ -165,6 +165,13 @@ int k3x_dev_decode(struct k3x_moe_layer *L, float *out, const void *x, int x_dty
 int k3x_dev_prefill(struct k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                     const float *resid, int *idx, float *wt, void *stream);
 int k3x_pf_reserve(struct k3x_moe_layer *L, int T);   /* k3x_moe.c */
+/* trunk products Y[t*ldy + o] = W[o] . X[t*ldx] over a tiled bf16 W [out][in]: T <= 8
+ * (GEMV on the matrix cores) and any T (hi/lo planes into `planes`, T*in*4 bytes, then
+ * the dense GEMM) */
+int k3x_dev_trunk_gemv(const uint16_t *W, int in, int out, float *y, int ldy, const void *x,
+                       int x_dtype, int ldx, int T, void *stream);
+int k3x_dev_trunk_gemm(const uint16_t *W, int in, int out, float *y, int ldy, const void *x,
+                       int x_dtype, int ldx, int T, uint16_t *planes, void *stream);
 int k3x_dev_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
                     void *stream);
 

@@ -25,12 +25,12 @@
 #define PF_CHUNK 4096          // tokens per pipeline run
 
 // ------------------------------------------------------------------ split
-// Activation planes, the GEMMs' B source: x [T][H] (bf16 or fp32) -> xg [2][H/8][T][8]
-// bf16, plane 0 the hi parts, plane 1 the lo parts, each k-group of 8 elements
-// token-major, so that one k-group of consecutive rows is contiguous.  Block 0 also
-// clears the expert histogram.
+// Activation planes, the GEMMs' B source: x [T][H] (bf16 or fp32, rows ldx elements
+// apart) -> xg [2][H/8][T][8] bf16, plane 0 the hi parts, plane 1 the lo parts, each
+// k-group of 8 elements token-major, so that one k-group of consecutive rows is
+// contiguous.  Block 0 also clears the expert histogram (when given).
 __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int T, int H,
-                                                  uint16_t *xg, int *counts, int E)
+                                                  int ldx, uint16_t *xg, int *counts, int E)
 {
     if (blockIdx.x == 0 && counts)
         for (int e = threadIdx.x; e < E; e += PF_NT) counts[e] = 0;
@@ -39,7 +39,7 @@ __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int
     if (i >= (size_t)T * G8) return;
     const int t = (int)(i / G8), gi = (int)(i % G8);
     float v[8];
-    load_x8(x, x_bf16, i * 8, v);
+    load_x8(x, x_bf16, (size_t)t * ldx + (size_t)gi * 8, v);
     uint32_t hi[8], lo[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) split_bf16(v[j], hi[j], lo[j]);
@@ -316,6 +316,7 @@ struct PfGemmArgs {
     float          *y;          // down output rows [*][R] fp32
     int             out_base;   // output row = out_base + p
     float           b1, b2;     // SiTU betas of the gate/up epilogue (0: uncapped)
+    int             ldy;        // floats between output rows (0: R)
 };
 
 template <bool FP4, int NMAT, int RT>
@@ -544,7 +545,7 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
                 *(u32x2 *)(a.act + o) = (u32x2){hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
                 *(u32x2 *)(a.act + plane + o) = (u32x2){lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
             } else {
-                float *dst = a.y + (size_t)(a.out_base + p) * a.R + r0;
+                float *dst = a.y + (size_t)(a.out_base + p) * (a.ldy ? a.ldy : a.R) + r0;
                 *(f32x4 *)dst = (f32x4){v0[0], v0[1], v0[2], v0[3]};
             }
         }
@@ -763,7 +764,7 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
                     *(u32x2 *)(a.act + o) = (u32x2){hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
                     *(u32x2 *)(a.act + plane + o) = (u32x2){lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
                 } else {
-                    float *dst = a.y + (size_t)(a.out_base + p) * a.R + r0;
+                    float *dst = a.y + (size_t)(a.out_base + p) * (a.ldy ? a.ldy : a.R) + r0;
                     *(f32x4 *)dst = (f32x4){v0[0], v0[1], v0[2], v0[3]};
                 }
             }
@@ -895,7 +896,7 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     int rc;
 
     hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (H / 8), PF_NT)), dim3(PF_NT), 0, s,
-                       x, x_bf16, T, H, B->xhl, B->counts, E);
+                       x, x_bf16, T, H, H, B->xhl, B->counts, E);
     if ((rc = launch_ok())) return rc;
 
     PfRouterArgs ar;
@@ -945,7 +946,7 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
             hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_z), dim3(PF_NT), 0, s, zg);
         if ((rc = launch_ok())) return rc;
         hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (X / 8), PF_NT)), dim3(PF_NT), 0, s,
-                           B->zf, 0, T, X, B->zhl, (int *)NULL, 0);
+                           B->zf, 0, T, X, X, B->zhl, (int *)NULL, 0);
         if ((rc = launch_ok())) return rc;
         rsrc = B->zhl;
     }
@@ -1080,4 +1081,30 @@ extern "C" int k3x_dev_prefill(k3x_moe_layer *L, float *out, const void *x, int 
         if (rc) return rc;
     }
     return 0;
+}
+
+// ------------------------------------------------------------------ trunk products
+// Y[t*ldy + o] = W[o] . X[t*ldx] for T activation rows (k3_mmw_batch_ld): X's hi/lo
+// planes into `planes` (T * in * 4 bytes), then the dense bf16 GEMM.
+extern "C" int k3x_dev_trunk_gemm(const uint16_t *W, int in, int out, float *y, int ldy,
+                                  const void *x, int x_dtype, int ldx, int T, uint16_t *planes,
+                                  void *stream)
+{
+    hipStream_t s = (hipStream_t)stream;
+    const int x_bf16 = (x_dtype == K3X_BF16), HL = x_bf16 ? 1 : 2;
+    hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (in / 8), PF_NT)), dim3(PF_NT), 0, s,
+                       x, x_bf16, T, in, ldx, planes, (int *)NULL, 0);
+    int rc = launch_ok();
+    if (rc) return rc;
+    PfGemmArgs g;
+    memset(&g, 0, sizeof g);
+    g.wm[0] = (const uint8_t *)W; g.R = out; g.K = in; g.n0 = T;
+    g.bsrc = planes; g.brows = T; g.row_base = 0;
+    g.y = y; g.out_base = 0; g.ldy = ldy;
+    const unsigned grid = cdiv(out, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 4 * 16 / HL);
+    if (HL == 1)
+        hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 1, false>), dim3(grid), dim3(PF_NT), 0, s, g);
+    else
+        hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid), dim3(PF_NT), 0, s, g);
+    return launch_ok();
 }

@@ -1,0 +1,105 @@
+/* k3x_trunk.c - host side of the trunk's bf16 products (include/k3x_trunk.h): upload and
+ * tiling of a matrix, argument checks, the workspace, the host-pointer form. */
+#include "k3x_internal.h"
+#include "../../include/k3x_trunk.h"
+
+#include <hip/hip_runtime_api.h>
+#include <stdlib.h>
+
+struct k3x_trunk {
+    int       device, in, out;
+    uint16_t *w;              /* tiled bf16 [out][in]                        */
+    uint16_t *planes;         /* workspace for T > K3X_DECODE_MAX_T           */
+    size_t    planes_bytes;
+    float    *hx, *hy;        /* device staging of the host-pointer form      */
+    size_t    hcap;           /* floats of each                               */
+};
+
+int k3x_trunk_create(const uint16_t *W, int in, int out, int device, k3x_trunk **t)
+{
+    if (!W || !t || in <= 0 || out <= 0) return K3X_E_ARG;
+    *t = NULL;
+    if (in % 128 || out % 16) return K3X_E_SHAPE;
+    int rc = k3x_dev_check(device);
+    if (rc) return rc;
+    if (hipSetDevice(device) != hipSuccess) return K3X_E_NODEV;
+    k3x_trunk *m = (k3x_trunk *)calloc(1, sizeof *m);
+    if (!m) return K3X_E_NOMEM;
+    m->device = device; m->in = in; m->out = out;
+    const size_t n = (size_t)in * out * 2;
+    void *stage = NULL;
+    rc = K3X_E_NOMEM;
+    if (hipMalloc((void **)&m->w, n) != hipSuccess || hipMalloc(&stage, n) != hipSuccess)
+        goto fail;
+    rc = K3X_E_HIP;
+    if (hipMemcpy(stage, W, n, hipMemcpyHostToDevice) != hipSuccess) goto fail;
+    if ((rc = k3x_dev_tile_bf16(m->w, (const uint16_t *)stage, out, in, NULL))) goto fail;
+    if (hipDeviceSynchronize() != hipSuccess) { rc = K3X_E_HIP; goto fail; }
+    hipFree(stage);
+    *t = m;
+    return 0;
+fail:
+    if (stage) hipFree(stage);
+    k3x_trunk_destroy(m);
+    return rc;
+}
+
+void k3x_trunk_destroy(k3x_trunk *t)
+{
+    if (!t) return;
+    hipSetDevice(t->device);
+    hipDeviceSynchronize();
+    if (t->w) hipFree(t->w);
+    if (t->planes) hipFree(t->planes);
+    if (t->hx) hipFree(t->hx);
+    if (t->hy) hipFree(t->hy);
+    free(t);
+}
+
+int k3x_trunk_apply(k3x_trunk *t, float *Y, int ldy, const void *X, int x_dtype, int ldx,
+                    int T, void *stream)
+{
+    if (!t || T < 0 || (T > 0 && (!Y || !X))) return K3X_E_ARG;
+    if (x_dtype != K3X_F32 && x_dtype != K3X_BF16) return K3X_E_ARG;
+    if (ldx < t->in || ldy < t->out || (ldx & 7) || ((uintptr_t)X & 15)) return K3X_E_ARG;
+    if (T == 0) return 0;
+    if (T <= K3X_DECODE_MAX_T)
+        return k3x_dev_trunk_gemv(t->w, t->in, t->out, Y, ldy, X, x_dtype, ldx, T, stream);
+    const size_t need = (size_t)T * t->in * 4;
+    if (need > ((size_t)1 << 31)) return K3X_E_SHAPE;      /* 32-bit buffer offsets */
+    if (need > t->planes_bytes) {
+        if (hipSetDevice(t->device) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+            return K3X_E_HIP;
+        if (t->planes) hipFree(t->planes);
+        t->planes = NULL;
+        t->planes_bytes = 0;
+        if (hipMalloc((void **)&t->planes, need) != hipSuccess) return K3X_E_NOMEM;
+        t->planes_bytes = need;
+    }
+    return k3x_dev_trunk_gemm(t->w, t->in, t->out, Y, ldy, X, x_dtype, ldx, T, t->planes,
+                              stream);
+}
+
+int k3x_trunk_apply_host(k3x_trunk *t, float *Y, const float *X, int T)
+{
+    if (!t || T < 0 || (T > 0 && (!Y || !X))) return K3X_E_ARG;
+    if (T == 0) return 0;
+    if (hipSetDevice(t->device) != hipSuccess) return K3X_E_HIP;
+    const size_t nx = (size_t)T * t->in, ny = (size_t)T * t->out;
+    const size_t need = nx > ny ? nx : ny;
+    if (need > t->hcap) {
+        if (t->hx) hipFree(t->hx);
+        if (t->hy) hipFree(t->hy);
+        t->hx = t->hy = NULL;
+        t->hcap = 0;
+        if (hipMalloc((void **)&t->hx, need * 4) != hipSuccess ||
+            hipMalloc((void **)&t->hy, need * 4) != hipSuccess)
+            return K3X_E_NOMEM;
+        t->hcap = need;
+    }
+    if (hipMemcpy(t->hx, X, nx * 4, hipMemcpyHostToDevice) != hipSuccess) return K3X_E_HIP;
+    int rc = k3x_trunk_apply(t, t->hy, t->out, t->hx, K3X_F32, t->in, T, NULL);
+    if (rc) return rc;
+    if (hipMemcpy(Y, t->hy, ny * 4, hipMemcpyDeviceToHost) != hipSuccess) return K3X_E_HIP;
+    return 0;
+}

@@ -37,6 +37,8 @@ EXPORTS = [
     "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
     "k3x_store_src_create", "k3x_store_src_destroy", "k3x_store_src_fetches",
     "k3x_moe_layer_create_from_store",
+    # include/k3x_trunk.h
+    "k3x_trunk_create", "k3x_trunk_destroy", "k3x_trunk_apply", "k3x_trunk_apply_host",
 ]
 
 DT_U8, DT_BF16, DT_F16, DT_F32 = 1, 2, 3, 4
@@ -156,6 +158,11 @@ def lib():
         L.k3x_store_src_fetches.restype = C.c_long
         L.k3x_moe_layer_create_from_store.argtypes = [C.POINTER(Cfg), C.POINTER(MoeW), vp, i, i,
                                                       C.POINTER(vp)]
+        L.k3x_trunk_create.argtypes = [vp, i, i, i, C.POINTER(vp)]
+        L.k3x_trunk_destroy.argtypes = [vp]
+        L.k3x_trunk_destroy.restype = None
+        L.k3x_trunk_apply.argtypes = [vp, vp, i, vp, i, i, i, vp]
+        L.k3x_trunk_apply_host.argtypes = [vp, vp, vp, i]
         _lib = L
     return _lib
 
@@ -434,3 +441,31 @@ class Store:
         _check(int(lib().k3x_store_expert_load(self.h, C.byref(r), buf.ctypes.data)),
                "k3x_store_expert_load")
         return r, buf
+
+
+class Trunk:
+    """A bf16 trunk matrix on the device (include/k3x_trunk.h): k3_mmw_batch_ld."""
+
+    def __init__(self, W, device=0):
+        W = np.ascontiguousarray(W, np.uint16)
+        self.out, self.inn = W.shape
+        self.h = C.c_void_p()
+        _check(lib().k3x_trunk_create(W.ctypes.data, self.inn, self.out, device,
+                                      C.byref(self.h)), "k3x_trunk_create")
+
+    def close(self):
+        if self.h:
+            lib().k3x_trunk_destroy(self.h)
+            self.h = C.c_void_p()
+
+    def apply(self, y, ldy, x, x_dtype, ldx, T, stream=0):
+        """Device pointers: Y[t*ldy + o] = W[o] . X[t*ldx] for t < T."""
+        _check(lib().k3x_trunk_apply(self.h, y, ldy, x, x_dtype, ldx, T, stream or None),
+               "k3x_trunk_apply")
+
+    def apply_host(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty((x.shape[0], self.out), np.float32)
+        _check(lib().k3x_trunk_apply_host(self.h, y.ctypes.data, x.ctypes.data, x.shape[0]),
+               "k3x_trunk_apply_host")
+        return y

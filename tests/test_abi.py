@@ -39,7 +39,7 @@ def test_exports_every_declared_symbol(k3x):
 
 def test_header_compiles_as_c_and_cxx(tmp_path):
     src = tmp_path / "t.c"
-    src.write_text('#include "k3x_moe.h"\n#include "k3x_store.h"\nint main(void){return K3X_OK;}\n')
+    src.write_text('#include "k3x_moe.h"\n#include "k3x_store.h"\n#include "k3x_trunk.h"\nint main(void){return K3X_OK;}\n')
     inc = os.path.join(ROOT, "include")
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-I", inc, str(src)],
                    check=True)
@@ -65,6 +65,14 @@ def test_create_rejects_bad_cfg_before_device(k3x, bad):
     spec = k3x.SynthSpec(0, 0, 0.02, 0.1, 0.0, 1.1, 121, 125, 0.02)
     rc = k3x.lib().k3x_synth_layer_create(C.byref(cfg), C.byref(spec), 0, C.byref(h))
     assert rc == -2 and not h.value
+
+
+@pytest.mark.parametrize("inn,out", [(100, 64), (256, 40), (0, 16)])
+def test_trunk_rejects_bad_shapes_before_device(k3x, inn, out):
+    W = np.zeros(max(inn * out, 1), np.uint16)
+    h = C.c_void_p()
+    rc = k3x.lib().k3x_trunk_create(W.ctypes.data, inn, out, 0, C.byref(h))
+    assert rc in (-1, -2) and not h.value
 
 
 def test_null_arguments(k3x):

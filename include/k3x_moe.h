@@ -200,6 +200,23 @@ void     k3x_synth_normal_f32(float *dst, size_t n, uint64_t key, double mu, dou
 void     k3x_synth_normal_bf16(uint16_t *dst, size_t n, uint64_t key, double mu,
                                double sigma);
 
+/* ---- decoder-layer glue ----------------------------------------------------------------
+ * Block attention-residual aggregation (k3_attn_res, k3_ops.c:1722-1753, gathered as in
+ * k3_decoder_layer_core, :2546-2555): for each of T rows the sources are blocks[t][0 ..
+ * nb-1] (rows of n floats, maxb of them per row t) followed by pref[t]; h[t] = sum_s p_s
+ * src_s, p the softmax over the sources of RMSNorm(src_s) . fold (fold = the norm weight
+ * times the projection, one vector).  nb + 1 <= 64.  Device pointers, on stream. */
+int  k3x_attn_res(float *h, const float *blocks, int maxb, int nb, const float *pref,
+                  const float *fold, int n, int T, float eps, void *stream);
+
+/* The MoE half of a decoder layer (k3_decoder_layer_core, k3_ops.c:2546-2589) on the
+ * device: h = attn_res(blocks, pref); hin = RMSNorm(h; post_norm, eps); pref += MoE(hin);
+ * h = pref.  hin is a caller workspace of T*hidden floats; all device pointers, 16-byte
+ * aligned; asynchronous on stream (kernels only, so it can be captured in a graph). */
+int  k3x_moe_half(k3x_moe_layer *L, float *h, float *pref, const float *blocks, int maxb,
+                  int nb, const float *fold, const float *post_norm, float eps, int T,
+                  float *hin, void *stream);
+
 /* ---- stacked layers ------------------------------------------------------------------
  * The MoE half of consecutive decoder layers (k3_decoder_layer_core, k3_ops.c:2547-2589,
  * without attention): for each layer l, h = h + MoE_l(RMSNorm(h; norm_w[l], eps)), the

@@ -514,6 +514,29 @@ int k3x_moe_layer_check(k3x_moe_layer *L)
     return K3X_E_WAIT;
 }
 
+int k3x_attn_res(float *h, const float *blocks, int maxb, int nb, const float *pref,
+                 const float *fold, int n, int T, float eps, void *stream)
+{
+    if (!h || !pref || !fold || n <= 0 || T < 0 || nb < 0 || (nb > 0 && (!blocks || maxb < nb)))
+        return K3X_E_ARG;
+    if (T == 0) return 0;
+    return k3x_dev_attn_res(h, blocks, maxb, nb, pref, fold, n, T, eps, stream);
+}
+
+int k3x_moe_half(k3x_moe_layer *L, float *h, float *pref, const float *blocks, int maxb,
+                 int nb, const float *fold, const float *post_norm, float eps, int T,
+                 float *hin, void *stream)
+{
+    if (!L || !post_norm || !hin || T < 0) return K3X_E_ARG;
+    if (T == 0) return 0;
+    const int H = L->cfg.hidden;
+    int rc = k3x_attn_res(h, blocks, maxb, nb, pref, fold, H, T, eps, stream);
+    if (!rc) rc = k3x_rmsnorm(hin, h, post_norm, H, T, eps, stream);
+    if (!rc) rc = k3x_moe_forward(L, pref, hin, K3X_F32, T, pref, NULL, NULL, stream);
+    if (!rc) rc = k3x_dev_copy_f32(h, pref, (size_t)T * H, stream);
+    return rc;
+}
+
 int k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
                 void *stream)
 {

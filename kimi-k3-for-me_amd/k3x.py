@@ -32,6 +32,7 @@ EXPORTS = [
     "k3x_synth_normal_f32", "k3x_synth_normal_bf16", "k3x_moe_layer_set_timing",
     "k3x_moe_layer_last_ms", "k3x_stack_create", "k3x_stack_forward", "k3x_stack_destroy",
     "k3x_moe_layer_check", "k3x_moe_layer_set_route_wait",
+    "k3x_attn_res", "k3x_moe_half",
     # include/k3x_store.h
     "k3x_store_open", "k3x_store_close", "k3x_store_count", "k3x_store_shards",
     "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
@@ -158,6 +159,8 @@ def lib():
         L.k3x_store_src_fetches.restype = C.c_long
         L.k3x_moe_layer_create_from_store.argtypes = [C.POINTER(Cfg), C.POINTER(MoeW), vp, i, i,
                                                       C.POINTER(vp)]
+        L.k3x_attn_res.argtypes = [vp, vp, i, i, vp, vp, i, i, f, vp]
+        L.k3x_moe_half.argtypes = [vp, vp, vp, vp, i, i, vp, vp, f, i, vp, vp]
         L.k3x_trunk_create.argtypes = [vp, i, i, i, C.POINTER(vp)]
         L.k3x_trunk_destroy.argtypes = [vp]
         L.k3x_trunk_destroy.restype = None
@@ -182,6 +185,12 @@ def _check(rc, what):
 
 def expert_drops():
     return C.c_long.in_dll(lib(), "k3x_expert_drops").value
+
+
+def attn_res(h, blocks, maxb, nb, pref, fold, n, T, eps=1e-5, stream=0):
+    """Block attention-residual aggregation on device pointers (k3x_attn_res)."""
+    _check(lib().k3x_attn_res(h, blocks or None, maxb, nb, pref, fold, n, T, eps,
+                              stream or None), "k3x_attn_res")
 
 
 def make_cfg(hidden, n_experts, topk, moe_inter, n_shared=1, moe_renorm=1, routed_scale=2.5,
@@ -319,6 +328,11 @@ class MoELayer:
                                                           ("p1", "s1", "p3", "s3", "p2", "s2")]),
                "k3x_moe_layer_read_expert")
         return d
+
+    def moe_half(self, h, pref, blocks, maxb, nb, fold, post_norm, eps, T, hin, stream=0):
+        """The MoE half of a decoder layer on device pointers (k3x_moe_half)."""
+        _check(lib().k3x_moe_half(self.h, h, pref, blocks or None, maxb, nb, fold, post_norm,
+                                  eps, T, hin, stream or None), "k3x_moe_half")
 
     def check(self):
         """Raise if a decode call since the last check had a workgroup give up waiting for

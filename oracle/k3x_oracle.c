@@ -18,6 +18,8 @@
  *                                     top-k with lower-index ties.
  *   ko_situ_glu                       situ_glu.json; closed form of SwiGLU at 2^64 betas.
  *   ko_rmsnorm                        rmsnorm.json.
+ *   ko_attn_res                       attnres.json; bitwise against oracle/_ref's
+ *                                     k3_attn_res; one source returns it unchanged.
  *   ko_moe / ko_moe_prefill           bitwise against the reference's k3_moe /
  *                                     k3_moe_prefill (oracle/_ref) on the same layer,
  *                                     expressed with identity latent projections.
@@ -487,6 +489,65 @@ long ko_stack_step(float *h, int T, int n_layers, const ko_cfg *c,
         for (size_t i = 0; i < (size_t)T * H; i++) h[i] += tmp[i];
     }
     free(hin); free(tmp); free(idx); free(wt);
+    return drops;
+}
+
+/* ------------------------------------------------------ decoder-layer glue ---- */
+/* k3_attn_res, k3_ops.c:1722-1753: the key of a source is its RMS-normalised row (inv
+ * rounded to float once, v*inv in float), dotted with fold (norm weight times projection,
+ * folded at load) in one double chain; the maximum subtracted, expf, the double sum z;
+ * p = (float)(e/z); out accumulated in float over sources in order, from 0. */
+void ko_attn_res(float *out, const float *src, const float *fold, int nsrc, int n, float eps)
+{
+    float *score = (float *)malloc((size_t)(nsrc > 0 ? nsrc : 1) * sizeof(float));
+    if (!score) abort();
+    for (int s = 0; s < nsrc; s++) {
+        const float *v = src + (size_t)s * n;
+        double ss = 0.0;
+        for (int i = 0; i < n; i++) ss += (double)v[i] * (double)v[i];
+        const float inv = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+        double acc = 0.0;
+        for (int i = 0; i < n; i++) acc += (double)(v[i] * inv) * (double)fold[i];
+        score[s] = (float)acc;
+    }
+    float m = score[0];
+    for (int s = 1; s < nsrc; s++) m = score[s] > m ? score[s] : m;
+    double z = 0.0;
+    for (int s = 0; s < nsrc; s++) {
+        score[s] = expf(score[s] - m);
+        z += score[s];
+    }
+    for (int i = 0; i < n; i++) out[i] = 0.0f;
+    for (int s = 0; s < nsrc; s++) {
+        const float p = (float)(score[s] / z);
+        const float *v = src + (size_t)s * n;
+        for (int i = 0; i < n; i++) out[i] += p * v[i];
+    }
+    free(score);
+}
+
+long ko_moe_half(float *h, float *pref, const float *blocks, int maxb, int nb,
+                 const float *fold, const float *post_norm, float eps, int T,
+                 const ko_cfg *c, const ko_weights *w)
+{
+    const int H = c->hidden, K = c->topk;
+    float *src = (float *)malloc((size_t)(nb + 1) * H * sizeof(float));
+    float *hin = (float *)malloc((size_t)T * H * sizeof(float));
+    float *tmp = (float *)malloc((size_t)T * H * sizeof(float));
+    int *idx = (int *)malloc((size_t)T * K * sizeof(int));
+    float *wt = (float *)malloc((size_t)T * K * sizeof(float));
+    if (!src || !hin || !tmp || !idx || !wt) abort();
+    for (int t = 0; t < T; t++) {
+        for (int b = 0; b < nb; b++)
+            memcpy(src + (size_t)b * H, blocks + ((size_t)t * maxb + b) * H, (size_t)H * sizeof(float));
+        memcpy(src + (size_t)nb * H, pref + (size_t)t * H, (size_t)H * sizeof(float));
+        ko_attn_res(h + (size_t)t * H, src, fold, nb + 1, H, eps);
+        ko_rmsnorm(hin + (size_t)t * H, h + (size_t)t * H, post_norm, H, eps);
+    }
+    const long drops = ko_moe(tmp, hin, T, c, w, idx, wt);
+    for (size_t i = 0; i < (size_t)T * H; i++) pref[i] += tmp[i];
+    memcpy(h, pref, (size_t)T * H * sizeof(float));
+    free(src); free(hin); free(tmp); free(idx); free(wt);
     return drops;
 }
 

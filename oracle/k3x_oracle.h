@@ -98,6 +98,18 @@ long ko_moe_prefill(float *out, const float *x, int T, const ko_cfg *c,
 long ko_stack_step(float *h, int T, int n_layers, const ko_cfg *c,
                    const ko_weights *const *w, const float *const *norm_w, float eps);
 
+/* Block attention-residual aggregation (k3_attn_res, k3_ops.c:1722-1753): per source s
+ * of nsrc rows of n, score_s = sum_i (v_i * inv_s) * fold_i in double (inv_s the row's
+ * 1/rms), softmax of the scores (expf, double sum), out = sum_s p_s * v_s in float. */
+void ko_attn_res(float *out, const float *src, const float *fold, int nsrc, int n, float eps);
+
+/* The MoE half of a decoder layer (k3_decoder_layer_core, k3_ops.c:2546-2589) for T
+ * rows: h[t] = attn_res(blocks[t][0 .. nb-1], pref[t]); hin = RMSNorm(h; post_norm);
+ * tmp = MoE(hin); pref += tmp; h = pref.  blocks [T][maxb][H]. */
+long ko_moe_half(float *h, float *pref, const float *blocks, int maxb, int nb,
+                 const float *fold, const float *post_norm, float eps, int T,
+                 const ko_cfg *c, const ko_weights *w);
+
 /* ---- synthetic inputs ---------------------------------------------------------- */
 /* The counter-based generator shared by the tests and the product's synthetic-layer
  * builder: value i of a stream depends only on (seed, layer, stream, sub, i). */

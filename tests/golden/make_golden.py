@@ -5,7 +5,7 @@ the reference tree; the GPU side only reads the .npz files).
    (data only): tests/fixtures/ops/{router,situ_glu,rmsnorm}.json and
    tests/fixtures/mxfp4.json (real checkpoint MXFP4 bytes with their exact dequant).
    tests/fixtures/ops/moe.json (the whole LatentMoE block, fp32 experts and trunk) goes
-   to ref_moe_latent.npz.
+   to ref_moe_latent.npz, tests/fixtures/ops/attnres.json to ref_attnres.npz.
 2. Whole-layer golden vectors of the K2-class layer computed by the COMPILED REFERENCE
    (oracle/_ref/libk3ref.so: the reference's k3_ops.c, k3_moe/k3_moe_prefill with
    identity latent projections and 2^64 SiTU betas) on seeded synthetic layers:
@@ -79,6 +79,14 @@ def convert_ops():
     rec["tol_abs"] = man["tolerance"]["fp32_abs"]
     rec["tol_rel"] = man["tolerance"]["fp32_rel"]
     np.savez_compressed(os.path.join(HERE, "ref_moe_latent.npz"), **rec)
+    a = json.load(open(os.path.join(FIX, "ops", "attnres.json")))
+    np.savez_compressed(os.path.join(HERE, "ref_attnres.npz"),
+                        prefix=arr(a["prefix_sum"]).astype(np.float32).reshape(a["prefix_sum"]["shape"]),
+                        blocks=arr(a["block_residual"]).astype(np.float32).reshape(a["block_residual"]["shape"]),
+                        fold=arr(a["fold_hint"]).astype(np.float32),
+                        out=arr(a["out"]).astype(np.float32).reshape(a["out"]["shape"]),
+                        eps=a["eps"], n_sources=a["n_sources"],
+                        tol_abs=man["tolerance"]["fp32_abs"], tol_rel=man["tolerance"]["fp32_rel"])
 
 
 def ref_moe(L, x, prefill=False):

@@ -1,0 +1,136 @@
+"""The decoder-layer glue on the device against the oracle: the block attention-residual
+aggregation (k3x_attn_res vs ko_attn_res, which is bitwise the reference's k3_attn_res),
+and the MoE half of a decoder layer (k3x_moe_half vs ko_moe_half), eagerly and replayed
+from a captured graph."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import synth
+from gpu_util import bank_layer, say
+from oracle_lib import F32P, oracle, ptr
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_attn_res(blocks, nb, pref, fold, eps):
+    T, n = pref.shape
+    out = np.empty_like(pref)
+    for t in range(T):
+        src = np.ascontiguousarray(np.concatenate([blocks[t, :nb], pref[t:t + 1]]), np.float32)
+        oracle().ko_attn_res(ptr(out[t], F32P), ptr(src, F32P), ptr(fold, F32P), nb + 1, n, eps)
+    return out
+
+
+@pytest.mark.parametrize("n,nb", [(256, 0), (7168, 3), (7168, 8)])
+def test_attn_res_vs_oracle(torch, k3x, n, nb):
+    say(f"case: attn_res n={n} nb={nb}, 5 rows")
+    T, maxb = 5, 9
+    rng = np.random.default_rng(n + nb)
+    blocks = (rng.standard_normal((T, maxb, n)) * rng.uniform(0.2, 5, (T, maxb, 1))).astype(np.float32)
+    pref = rng.standard_normal((T, n)).astype(np.float32)
+    fold = (rng.standard_normal(n) * 0.05).astype(np.float32)
+    bd, pd, fd = (torch.from_numpy(a).cuda() for a in (blocks, pref, fold))
+    hd = torch.empty_like(pd)
+    k3x.attn_res(hd.data_ptr(), bd.data_ptr(), maxb, nb, pd.data_ptr(), fd.data_ptr(), n, T, 1e-5,
+                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got, want = hd.cpu().numpy(), oracle_attn_res(blocks, nb, pref, fold, 1e-5)
+    same = float(np.mean(got.view(np.uint32) == want.view(np.uint32)))
+    err = synth.rel_l2(got, want)
+    say(f"  rel_l2={err:.3e}, bitwise-equal fraction {same:.4f}")
+    assert err < 1e-6
+
+
+def oracle_half(L, h, pref, blocks, nb, fold, post, eps):
+    cfg = L.ko_cfg()
+    w, cb, keep = L._weights()
+    T, H = pref.shape
+    h = h.copy(); p = pref.copy()
+    b = np.ascontiguousarray(blocks, np.float32)
+    oracle().ko_moe_half(ptr(h, F32P), ptr(p, F32P), ptr(b, F32P), b.shape[1], nb,
+                         ptr(fold, F32P), ptr(post, F32P), eps, T, C.byref(cfg), C.byref(w))
+    return h, p
+
+
+def half_inputs(L, T, maxb, seed):
+    rng = np.random.default_rng(seed)
+    H = L.H
+    blocks = (rng.standard_normal((T, maxb, H)) * 0.5).astype(np.float32)
+    pref = L.x(T, bf16=False, stream_sub=seed)
+    fold = (rng.standard_normal(H) * 0.05).astype(np.float32)
+    post = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    return blocks, pref, fold, post
+
+
+@pytest.mark.parametrize("latent,T", [(False, 1), (False, 12), (True, 4)])
+def test_moe_half_vs_oracle(torch, k3x, latent, T):
+    say(f"case: MoE half of a decoder layer, latent={latent}, T={T}, 3 block residuals")
+    L = synth.tiny_latent(seed=33) if latent else synth.tiny(seed=33)
+    layer = bank_layer(k3x, L)
+    nb, maxb = 3, 4
+    blocks, pref, fold, post = half_inputs(L, T, maxb, 7 + T)
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).cuda() for k, v in
+         (("b", blocks), ("p", pref), ("f", fold), ("n", post))}
+    h = torch.empty_like(d["p"]); hin = torch.empty_like(d["p"])
+    layer.moe_half(h.data_ptr(), d["p"].data_ptr(), d["b"].data_ptr(), maxb, nb,
+                   d["f"].data_ptr(), d["n"].data_ptr(), 1e-5, T, hin.data_ptr(),
+                   torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    layer.check()
+    wh, wp = oracle_half(L, np.zeros_like(pref), pref, blocks, nb, fold, post, 1e-5)
+    eh, ep = synth.rel_l2(h.cpu().numpy(), wh), synth.rel_l2(d["p"].cpu().numpy(), wp)
+    say(f"  rel_l2 h={eh:.3e} pref={ep:.3e}")
+    assert eh < 1e-3 and ep < 1e-3
+    assert torch.equal(h, d["p"])
+    layer.close()
+
+
+def test_moe_half_graph_replays(torch, k3x):
+    """One layer's glue + MoE captured once, replayed on new inputs with eager work and
+    synchronisations between the replays; every replay equals the eager result."""
+    say("case: MoE half captured in a graph, 4 replays with eager copies between")
+    L = synth.tiny(seed=34)
+    layer = bank_layer(k3x, L)
+    T, nb, maxb = 2, 2, 2
+    H = L.H
+    bd = torch.empty((T, maxb, H), dtype=torch.float32, device="cuda")
+    pd = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    fd = torch.empty((H,), dtype=torch.float32, device="cuda")
+    nd = torch.empty((H,), dtype=torch.float32, device="cuda")
+    h = torch.empty_like(pd); hin = torch.empty_like(pd)
+    s = torch.cuda.Stream()
+
+    def load(seed):
+        blocks, pref, fold, post = half_inputs(L, T, maxb, seed)
+        bd.copy_(torch.from_numpy(blocks)); pd.copy_(torch.from_numpy(pref))
+        fd.copy_(torch.from_numpy(fold)); nd.copy_(torch.from_numpy(post))
+
+    def run(stream):
+        layer.moe_half(h.data_ptr(), pd.data_ptr(), bd.data_ptr(), maxb, nb, fd.data_ptr(),
+                       nd.data_ptr(), 1e-5, T, hin.data_ptr(), stream)
+
+    load(100)
+    with torch.cuda.stream(s):
+        run(s.cuda_stream)                      # eager warm-up
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run(s.cuda_stream)
+    torch.cuda.synchronize()
+    for r in range(4):
+        load(200 + r)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got_h, got_p = h.clone(), pd.clone()
+        load(200 + r)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            run(s.cuda_stream)
+        torch.cuda.synchronize()
+        say(f"  replay {r}")
+        assert torch.equal(got_h, h) and torch.equal(got_p, pd)
+    layer.check()
+    layer.close()

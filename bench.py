@@ -8,8 +8,9 @@ pool of 64 distinct seeded bf16 N(0,1) activations resident in HBM, and the step
 over 4 layers of that shape, so every step reads its weights from HBM (a single layer
 called back to back finds its router and shared expert, 99 MB, still in the 256 MB
 last-level cache; that figure is reported as warm_one_layer_us_per_token).  Weights are
-synthetic (seeded generator, random init).  The record also carries the 2048-token
-prefill leg, the 8-layer stack leg, the K3 LatentMoE decode leg and a trunk-product leg.
+synthetic (seeded generator, random init).  The record also carries the T=8 verify leg,
+the 2048-token prefill leg, the 8-layer stack leg, the K3 LatentMoE decode leg and a
+trunk-product leg.
 
 Prints ONE JSON line (rank 0):
   value        microseconds per token for the whole layer (lower is better)
@@ -351,6 +352,55 @@ def trunk_leg(torch, k3x, reps=48, nrot=4):
     return rec
 
 
+def verify_leg(torch, k3x, steps=100, warmup=10, nrot=4):
+    """Speculative verification, T = 8 tokens per call, through the full-size K2-class
+    layer with Zipf-skewed routing (alpha 1.0, s 1.1): microseconds per call and the HBM
+    fraction of the call's algorithmic bytes (U unique experts x 23.4 MB + the shared
+    expert and the router), `nrot` layers in turn."""
+    T = 8
+    cfg = k3x.make_cfg(H, E, K, I, 1, 1, 2.5)
+    layers = [k3x.MoELayer.synthetic(cfg, seed=50 + j, zipf_alpha=1.0) for j in range(nrot)]
+    n_pool = 64
+    xs = k3x.synth_normal_f32(n_pool * T * H, k3x.synth_key(50, 0, k3x.STREAM_X, 8))
+    xpool = torch.from_numpy(xs.reshape(n_pool, T, H)).cuda().to(torch.bfloat16).contiguous()
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wt = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.Stream()
+    uniq = []
+
+    def step(i, routing=False):
+        layers[i % nrot].forward(out.data_ptr(), xpool[i % n_pool].data_ptr(), T, k3x.K3X_BF16,
+                                 0, idx.data_ptr() if routing else 0,
+                                 wt.data_ptr() if routing else 0, stream=stream.cuda_stream)
+
+    with torch.cuda.stream(stream):
+        for i in range(n_pool):                 # the pool's unique-expert counts
+            step(i, routing=True)
+            uniq.append(int(torch.unique(idx).numel()))
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(warmup + i)
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) * 1e6 / steps
+    for l in layers:
+        l.check()
+        l.close()
+    del xpool, out, idx, wt
+    torch.cuda.empty_cache()
+    u = float(np.mean([uniq[(warmup + i) % n_pool] for i in range(steps)]))
+    nbytes = u * B_EXPERT + B_SHARED + B_ROUTER + T * H * 2 + T * H * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"workload": "verify T=8 bf16 tokens per call, full-size K2-class layer, Zipf-skewed "
+                        f"routing (alpha 1.0, s 1.1), {nrot} layers in turn",
+            "us_per_call": round(us, 2), "unique_experts_mean": round(u, 2),
+            "algorithmic_mb_per_call": round(nbytes / 1e6, 1),
+            "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed counter summary (FETCH_SIZE and
     WRITE_SIZE runs scaled by a plain copy's readings), or None."""
@@ -448,6 +498,7 @@ def main():
     ap.add_argument("--no-stack", action="store_true", help="skip the 8-layer stack leg")
     ap.add_argument("--no-k3", action="store_true", help="skip the K3 LatentMoE decode leg")
     ap.add_argument("--no-trunk", action="store_true", help="skip the trunk product leg")
+    ap.add_argument("--no-verify", action="store_true", help="skip the T=8 verify leg")
     ap.add_argument("--trunk-only", action="store_true",
                     help="only run the trunk product leg and print its record")
     ap.add_argument("--k3-only", action="store_true",
@@ -579,6 +630,8 @@ def main():
         l.close()
     del xpool, out
     torch.cuda.empty_cache()
+    if not args.no_verify:
+        rec["verify"] = verify_leg(torch, k3x)
     if not args.no_prefill:
         rec["prefill"] = prefill_leg(torch, k3x)
     if not args.no_stack:

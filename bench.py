@@ -507,6 +507,8 @@ def main():
                     help="only run the 8-layer stack leg and print its record")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the prefill leg and print its record")
+    ap.add_argument("--verify-only", action="store_true",
+                    help="only run the T=8 verify leg and print its record")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only time a plain device copy of MIB MiB (the reference kernel for "
@@ -531,6 +533,9 @@ def main():
         return
     if args.trunk_only:
         print(json.dumps(trunk_leg(torch, load_k3x())), flush=True)
+        return
+    if args.verify_only:
+        print(json.dumps(verify_leg(torch, load_k3x())), flush=True)
         return
     if args.k3_only:
         k = load_k3x()

@@ -13,6 +13,8 @@
 //   k3_down           each unique expert's down product and the shared expert's (:1858)
 //                     into one accumulator set per 16 output rows (the weighted combine,
 //                     :1941-1942, plus the shared result, :1859), and an optional residual.
+//                     With two or more tokens, k3_down2 instead: two 16-row tiles a
+//                     workgroup, each B fragment read once for both.
 //
 // Each weight byte is read once per call.  Weights are dequantised in registers
 // (E2M1 x 2^(s-127) is exact in bf16) and multiplied on v_mfma_f32_16x16x32_bf16 against
@@ -994,6 +996,84 @@ __global__ void __launch_bounds__(NT3) k3_down(K3Args a)
     });
 }
 
+// Several tokens (K2 form): two 16-row tiles per workgroup, so that each B fragment read
+// from memory (the activation sets no longer fit the LDS) serves both tiles' products.
+template <bool EXACT>
+__global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
+{
+    __shared__ float lds[(NT3 / WAVE - 1) * 8 * WAVE];
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    constexpr int NW = NT3 / WAVE;
+    const int NC = 2 * a.T;
+    const int nu = a.route->nu;
+    const int nSI = ((a.I >> 7) + 3) >> 2;
+    const uint32_t slot = (uint32_t)nSI * 1024u * NC;
+    const uint32_t tb = (uint32_t)fp4_tile_bytes(a.I);
+    const int rt0 = 2 * blockIdx.x;
+    const int cnt = strided_count(wave, NW, nu * nSI);
+    const int nQS = a.sh_down ? a.SI >> 7 : 0;
+    SQ ring[2][2];
+    auto ld = [&](int i, int k) AI {
+        const int it = wave + NW * k;
+        const bool on = k < cnt;
+        const int u = on ? it / nSI : 0, S = on ? it % nSI : 0;
+        const int e = on ? a.route->uniq[u] : 0;
+        const rsrc_t r = make_rsrc(a.experts + (size_t)e * a.expert_bytes + a.down_off +
+                                       (size_t)rt0 * tb, on ? 2 * tb : 0u);
+        sq_load(ring[i][0], r, (uint32_t)S * SQ_BYTES, lane);
+        sq_load(ring[i][1], r, tb + (uint32_t)S * SQ_BYTES, lane);
+    };
+    ring_prime<2>(ld);
+    const int cs = strided_count(wave, NW, nQS);
+    const uint32_t sbytes = (uint32_t)nQS * 4096u;
+    const rsrc_t rw = make_rsrc(a.sh_down + (size_t)rt0 * 16 * a.SI, 2 * sbytes);
+    const rsrc_t rb = make_rsrc(a.shB, (uint32_t)nQS * 256u * NC);
+    const int n = lane & 15, kq = lane >> 4;
+    const uint32_t boff = (uint32_t)((kq * NC + (n < NC ? n : 0)) * 16);
+    QB w2[2][2];
+    u32x4 b2[2][4];
+    auto ld2 = [&](int i, int k) AI {
+        const bool on = k < cs;
+        const int q = wave + NW * k;
+        qb_load(w2[i][0], rw, on ? (uint32_t)q * 4096u : K3X_OOB, lane);
+        qb_load(w2[i][1], rw, on ? sbytes + (uint32_t)q * 4096u : K3X_OOB, lane);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            b2[i][t] = bload16(rb, on ? boff + (uint32_t)(q * 256 * NC + t * 64 * NC) : K3X_OOB);
+    };
+    ring_prime<2>(ld2);
+    BFrag<false> bf;
+    bf.init(a.actB, (uint32_t)nu * slot, NC, lane);
+    f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+    ring_loop<2>(cnt, ld, [&](int i, int k) AI {
+        const int it = wave + NW * k;
+        const uint32_t sb = (uint32_t)(it / nSI) * slot;
+        const int S = it % nSI;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const bf16x8 bv = as_bf16x8(bf.get(sb, 4 * S + j, t));
+                d0 = mfma(sq_a<EXACT>(ring[i][0], j, t), bv, d0);
+                d1 = mfma(sq_a<EXACT>(ring[i][1], j, t), bv, d1);
+            }
+    });
+    ring_loop<2>(cs, ld2, [&](int i, int k) AI {
+        qb_mfma(d0, w2[i][0], b2[i]);
+        qb_mfma(d1, w2[i][1], b2[i]);
+    });
+    float acc[8] = {d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3]};
+    wave_sum_lds<8, NW>(acc, lds, wave, lane);
+    if (wave != 0) return;
+    per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&v)[8]) AI {
+        for (int tt = 0; tt < 2; tt++)
+            for (int i = 0; i < 4; i++) {
+                const size_t o = (size_t)tok * a.H + (rt0 + tt) * 16 + r0 + i;
+                a.out[o] = a.resid ? a.resid[o] + v[4 * tt + i] : v[4 * tt + i];
+            }
+    });
+}
+
 // ------------------------------------------------------------------ K4 (latent form)
 // The routed aggregates (the sum of k3's parts, in part order), their RMSNorm (k3_rmsnorm
 // on the aggregate, k3_ops.c:1946) and their B set for the up projection.  Every
@@ -1331,7 +1411,10 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     }
     a3.pstride = parts > 1 ? (size_t)K3X_DECODE_MAX_T * X : 0;
     const size_t l3 = (size_t)a3.lds_bytes + a3.sh_lds;
-    if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(X / 16, parts), dim3(NT3), l3, s, a3);
+    if (!L->lat && T >= 2 && X % 32 == 0) {
+        if (L->special & 4) hipLaunchKernelGGL(k3_down2<true>, dim3(X / 32), dim3(NT3), 0, s, a3);
+        else                hipLaunchKernelGGL(k3_down2<false>, dim3(X / 32), dim3(NT3), 0, s, a3);
+    } else if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(X / 16, parts), dim3(NT3), l3, s, a3);
     else                hipLaunchKernelGGL(k3_down<false>, dim3(X / 16, parts), dim3(NT3), l3, s, a3);
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, ev++, s))) return rc;

@@ -695,6 +695,8 @@ struct K2Args {
     int            XL;             // its width (H, or the latent width)
     float          b1, b2;         // SiTU betas (0: that half uncapped)
     int            rtw;            // row tiles per routed workgroup (1, 2 or 4)
+    int            sb;             // 1 (with rtw 2 and the input's B set past the LDS): each
+                                   // super-quad's B fragments staged once for the four waves
     int            sel_done;       // 1: the routing was published by an earlier launch
                                    // (k1_zdown): no selection here, no wait
 };
@@ -824,20 +826,81 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     const uint8_t *ex = a.experts + (size_t)e * a.expert_bytes + (size_t)rt * tb;
     const rsrc_t rg = make_rsrc(ex + a.gate_off, tb);
     const rsrc_t ru = make_rsrc(ex + a.up_off, tb);
-    const int cnt = strided_count(sw, WPT, nS);
-    SQ g[2], v[2];
-    auto ld = [&](int i, int k) AI {
-        const uint32_t o = k < cnt ? (uint32_t)(sw + WPT * k) * SQ_BYTES : K3X_OOB;
-        sq_load(g[i], rg, o, lane);
-        sq_load(v[i], ru, o, lane);
-    };
-    ring_prime<2>(ld);
-    BFrag<LDSB> bf;
-    bf.init(a.rB, bbytes, NC, lane);
     f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
-    ring_loop<2>(cnt, ld, [&](int i, int k) AI {
-        sq_mfma2<EXACT, LDSB>(dg, du, g[i], v[i], bf, sw + WPT * k);
-    });
+    if (!LDSB && a.sb) {
+        // several tokens: wave (tw, sw) streams matrix sw (gate, up) of tile tw over every
+        // super-quad; each super-quad's B fragments are read once into LDS for the four
+        // waves (double buffered) instead of once per wave
+        const rsrc_t rw = sw ? ru : rg;
+        const uint32_t sqb = 1024u * (uint32_t)NC;
+        const rsrc_t rbB = make_rsrc(a.rB, bbytes);
+        SQ w[2];
+        auto ldw = [&](int i, int S) AI {
+            sq_load(w[i], rw, S < nS ? (uint32_t)S * SQ_BYTES : K3X_OOB, lane);
+        };
+        u32x4 breg[4];
+        auto bld = [&](int S) AI {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t o = threadIdx.x * 16u + (uint32_t)c * NT * 16u;
+                breg[c] = bload16(rbB, (S < nS && o < sqb) ? (uint32_t)S * sqb + o : K3X_OOB);
+            }
+        };
+        auto bst = [&](int buf) AI {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t o = threadIdx.x * 16u + (uint32_t)c * NT * 16u;
+                if (o < sqb) *(u32x4 *)(dyn_lds + (uint32_t)buf * sqb + o) = breg[c];
+            }
+        };
+        BFrag<true> bl;
+        bl.init(nullptr, 0u, NC, lane);
+        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+        auto mm = [&](const SQ &wq, int buf) AI {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    d = mfma(sq_a<EXACT>(wq, j, t), as_bf16x8(bl.get((uint32_t)buf * sqb, j, t)), d);
+        };
+        bld(0);
+        ring_prime<2>(ldw);
+        bst(0);
+        __syncthreads();
+        for (int S = 0; S < nS; S += 2) {
+            bld(S + 1);
+            mm(w[0], 0);
+            SCHED_FENCE();
+            ldw(0, S + 2);
+            SCHED_FENCE();
+            bst(1);
+            __syncthreads();
+            if (S + 1 >= nS) break;
+            bld(S + 2);
+            mm(w[1], 1);
+            SCHED_FENCE();
+            ldw(1, S + 3);
+            SCHED_FENCE();
+            bst(0);
+            __syncthreads();
+        }
+        if (sw) du = d;
+        else    dg = d;
+    } else {
+        const int cnt = strided_count(sw, WPT, nS);
+        SQ g[2], v[2];
+        auto ld = [&](int i, int k) AI {
+            const uint32_t o = k < cnt ? (uint32_t)(sw + WPT * k) * SQ_BYTES : K3X_OOB;
+            sq_load(g[i], rg, o, lane);
+            sq_load(v[i], ru, o, lane);
+        };
+        ring_prime<2>(ld);
+        BFrag<LDSB> bf;
+        bf.init(a.rB, bbytes, NC, lane);
+        ring_loop<2>(cnt, ld, [&](int i, int k) AI {
+            sq_mfma2<EXACT, LDSB>(dg, du, g[i], v[i], bf, sw + WPT * k);
+        });
+    }
     float acc[8] = {dg[0], dg[1], dg[2], dg[3], du[0], du[1], du[2], du[3]};
     // the waves of one tile summed into its rank-0 wave (waves tw + RTW*j)
     if (sw != 0)
@@ -1375,6 +1438,8 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     const bool ex2 = (L->special & 3) != 0, st2 = bset <= STAGE_MAX;
     size_t l2 = st2 ? bset : 0;
     if (l2 < sizeof(KSLds)) l2 = sizeof(KSLds);
+    a2.sb = (!st2 && a2.rtw == 2) ? 1 : 0;
+    if (a2.sb && l2 < (size_t)2048 * NC) l2 = (size_t)2048 * NC;
     const dim3 g2(1 + a2.n_sh + n_routed);
     if (c->n_experts <= 128)      launch_k2<2>(a2, ex2, st2, g2, l2, s);
     else if (c->n_experts <= 256) launch_k2<4>(a2, ex2, st2, g2, l2, s);

@@ -94,7 +94,7 @@ def test_synth_generator_matches_oracle(k3x):
 
 
 def test_integration_adapter_compiles_against_reference_header(tmp_path):
-    """The reference-side binding shown in INTEGRATION.md compiles against the
+    """The reference-side binding (k3x_ref_adapter.c) compiles against the
     reference's own k3.h and this library's header (build check only)."""
     if not os.path.isdir("/root/reference/include/k3"):
         pytest.skip("reference tree absent")

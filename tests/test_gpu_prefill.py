@@ -15,7 +15,7 @@ from gpu_util import bank_layer, dev_forward, say, synth_layer
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-3          # relative L2, from the north star
+TOL = 1e-3          # relative L2, the parity bar
 
 
 def decode_forward(torch, k3x, layer, x, bf16):

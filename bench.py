@@ -515,7 +515,7 @@ def main():
                          "the HBM byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
+        print("bench.py measures one GPU: this library has no multi-GPU path "
               "(collectives and sharding are out of scope); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)

@@ -2,7 +2,7 @@
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the product library links, loads or calls this
  * code; only tests/, the smoke check and the CPU-baseline leg of bench.py do, and only
- * as the checker (or, for the baseline, as the CPU path being timed beside the GPU).
+ * to check device results (or, for the baseline, as the CPU path timed beside the GPU).
  *
  * Every function restates one routine of the reference engine's numeric core
  * (src/core/k3_ops.c) with the same floating-point contract: the same accumulator

@@ -1,6 +1,6 @@
 """ctypes view of the oracle (oracle/k3x_oracle.c) and of the compiled reference.
 
-Test infrastructure only: the oracle is the checker.  The compiled reference
+Test infrastructure only: the oracle checks device results.  The compiled reference
 (oracle/_ref/libk3ref.so, built from the reference's own k3_ops.c) is optional and
 only pins the oracle; tests that need it skip when it was not built.
 """

@@ -1,4 +1,4 @@
-"""Pins the oracle (oracle/k3x_oracle.c) before it is trusted as the checker.
+"""Pins the oracle (oracle/k3x_oracle.c) before device results are checked against it.
 
 Three kinds of evidence, per function:
   * the reference's own fixtures (tests/golden/ref_*.npz, converted from the

@@ -113,6 +113,39 @@ long k3x_store_src_fetches(const k3x_expert_src *src);
 int  k3x_moe_layer_create_from_store(const k3x_cfg *c, const k3x_moe_w *w, k3x_store *s,
                                      int layer, int device, k3x_moe_layer **out);
 
+/* ---- expert cache: a layer with only part of its experts resident in HBM ----
+ *
+ * The reference streams its 1.45 TB of routed experts through a host-RAM cache
+ * (K3Cache, k3_cache.h:46-113; k3_cache_init :115, k3_cache_pin :121, stats :137-138)
+ * whose supplier k3_moe pulls from per token (k3_cache.c:394-563).  Here the arena is
+ * in HBM: a layer made by k3x_moe_layer_create_cached holds nslot experts; each decode
+ * call (k3x_moe_forward with T <= 8) first runs the selection, then makes the experts it
+ * names resident, reading a miss's run from the store (pinned buffer, copy, re-layout
+ * into the least recently used unpinned slot the call does not name), then runs the
+ * expert products through the slot table.  The results are those of a layer with every
+ * expert resident.  Cached layers serve decode calls only (prefill and the stacked
+ * graph return K3X_E_ARG) and a call whose tokens name more experts than there are slots
+ * returns K3X_E_SHAPE.  A miss that cannot be read counts in k3x_expert_drops and fails
+ * the call with K3X_E_DROP. */
+typedef struct k3x_cache_stat {
+    int                nslot;        /* slots in the arena                         */
+    int                resident;     /* slots holding an expert                    */
+    unsigned long long hits;         /* named experts found resident               */
+    unsigned long long misses;       /* named experts read from the store          */
+    unsigned long long evictions;    /* residents replaced                          */
+    unsigned long long bytes_read;   /* bytes of expert runs read from the store   */
+} k3x_cache_stat;
+
+/* nslot in [topk + 1, n_experts] (k3_cache_init refuses fewer than topk + 1 slots);
+ * w supplies the router, bias, shared and latent weights as for k3x_moe_layer_create;
+ * the cache starts empty. */
+int  k3x_moe_layer_create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store *s,
+                                 int layer, int nslot, int device, k3x_moe_layer **out);
+int  k3x_cache_stats(const k3x_moe_layer *L, k3x_cache_stat *st);
+/* pin = 1: make the expert resident (a miss) and never evict it; 0: release it.  At
+ * least topk slots stay unpinned (K3X_E_SHAPE otherwise). */
+int  k3x_cache_pin(k3x_moe_layer *L, int expert, int pin);
+
 #ifdef __cplusplus
 }
 #endif

@@ -697,6 +697,7 @@ struct K2Args {
     int            rtw;            // row tiles per routed workgroup (1, 2 or 4)
     int            sb;             // 1 (with rtw 2 and the input's B set past the LDS): each
                                    // super-quad's B fragments staged once for the four waves
+    const int     *slot;           // expert -> arena slot (expert cache), or NULL: identity
     int            sel_done;       // 1: the routing was published by an earlier launch
                                    // (k1_zdown): no selection here, no wait
 };
@@ -821,7 +822,8 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
     if (!s_go) return;
     const k3x_route *rte = a.route;
     if (u >= __hip_atomic_load(&rte->nu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
-    const int e = __hip_atomic_load(&rte->uniq[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int e = __hip_atomic_load(&rte->uniq[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.slot) e = a.slot[e];
     const uint32_t tb = (uint32_t)fp4_tile_bytes(a.XL);
     const uint8_t *ex = a.experts + (size_t)e * a.expert_bytes + (size_t)rt * tb;
     const rsrc_t rg = make_rsrc(ex + a.gate_off, tb);
@@ -949,6 +951,7 @@ struct K3Args {
     int            upp;            // unique experts per part: part blockIdx.y takes slots
                                    // upp*y .. upp*y + upp - 1 (the latent form's split)
     size_t         pstride;        // floats between parts' outputs (0: one part)
+    const int     *slot;           // expert -> arena slot (expert cache), or NULL: identity
 };
 
 // A bf16 quad of the shared down matrix with its B fragments (read from the shared
@@ -984,7 +987,8 @@ __device__ __forceinline__ void k3_body(const K3Args &a, f32x4 &d, int wave, int
         const int it = wave + NW * k;
         const bool on = k < cnt;
         const int u = on ? it / nSI : 0, S = on ? it % nSI : 0;
-        const int e = on ? a.route->uniq[u0 + u] : 0;
+        int e = on ? a.route->uniq[u0 + u] : 0;
+        if (a.slot) e = on ? a.slot[e] : 0;
         const rsrc_t r = make_rsrc(a.experts + (size_t)e * a.expert_bytes + a.down_off +
                                        (size_t)rt * tb, on ? tb : 0u);
         sq_load(ring[i], r, (uint32_t)S * SQ_BYTES, lane);
@@ -1080,7 +1084,8 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
         const int it = wave + NW * k;
         const bool on = k < cnt;
         const int u = on ? it / nSI : 0, S = on ? it % nSI : 0;
-        const int e = on ? a.route->uniq[u] : 0;
+        int e = on ? a.route->uniq[u] : 0;
+        if (a.slot) e = on ? a.slot[e] : 0;
         const rsrc_t r = make_rsrc(a.experts + (size_t)e * a.expert_bytes + a.down_off +
                                        (size_t)rt0 * tb, on ? 2 * tb : 0u);
         sq_load(ring[i][0], r, (uint32_t)S * SQ_BYTES, lane);
@@ -1435,17 +1440,31 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     // the routed input's set and x's (the shared experts'): staged when both fit
     const uint32_t xset = (uint32_t)nS * 1024u * NC, rset = (uint32_t)nSX * 1024u * NC;
     const uint32_t bset = xset > rset ? xset : rset;
-    const bool ex2 = (L->special & 3) != 0, st2 = bset <= STAGE_MAX;
+    const bool st2 = bset <= STAGE_MAX;
     size_t l2 = st2 ? bset : 0;
     if (l2 < sizeof(KSLds)) l2 = sizeof(KSLds);
     a2.sb = (!st2 && a2.rtw == 2) ? 1 : 0;
     if (a2.sb && l2 < (size_t)2048 * NC) l2 = (size_t)2048 * NC;
-    const dim3 g2(1 + a2.n_sh + n_routed);
-    if (c->n_experts <= 128)      launch_k2<2>(a2, ex2, st2, g2, l2, s);
-    else if (c->n_experts <= 256) launch_k2<4>(a2, ex2, st2, g2, l2, s);
-    else if (c->n_experts <= 384) launch_k2<6>(a2, ex2, st2, g2, l2, s);
-    else if (c->n_experts <= 512) launch_k2<8>(a2, ex2, st2, g2, l2, s);
-    else                          launch_k2<16>(a2, ex2, st2, g2, l2, s);
+    auto k2_launch = [&](bool ex, dim3 g) {
+        if (c->n_experts <= 128)      launch_k2<2>(a2, ex, st2, g, l2, s);
+        else if (c->n_experts <= 256) launch_k2<4>(a2, ex, st2, g, l2, s);
+        else if (c->n_experts <= 384) launch_k2<6>(a2, ex, st2, g, l2, s);
+        else if (c->n_experts <= 512) launch_k2<8>(a2, ex, st2, g, l2, s);
+        else                          launch_k2<16>(a2, ex, st2, g, l2, s);
+    };
+    a2.slot = L->nslot ? L->slot_dev : NULL;
+    if (L->nslot) {
+        // expert cache: the selection alone first (workgroup 0 of k2 on a grid of one, or
+        // k1_zdown's in the latent form), then the experts it names made resident
+        if (!L->lat) {
+            k2_launch(false, dim3(1));
+            if ((rc = launch_ok())) return rc;
+        }
+        if ((rc = k3x_cache_fill(L, s))) return rc;
+        a2.sel_done = 1;
+    }
+    const bool ex2 = (L->special & 3) != 0;
+    k2_launch(ex2, dim3(1 + a2.n_sh + n_routed));
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, ev++, s))) return rc;
 
@@ -1453,6 +1472,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     // or into the latent aggregates alone (latent form; the shared expert goes to k4)
     K3Args a3;
     a3.experts = L->experts; a3.expert_bytes = L->expert_bytes; a3.down_off = L->down_off;
+    a3.slot = L->nslot ? L->slot_dev : NULL;
     a3.route = L->route; a3.actB = L->actB;
     a3.sh_down = (L->SI > 0 && !L->lat) ? L->sh_down : NULL; a3.shB = L->shB; a3.SI = L->SI;
     a3.out = L->lat ? L->accL : out; a3.resid = L->lat ? NULL : resid;

@@ -146,7 +146,25 @@ struct k3x_moe_layer {
     /* host staging for the drop-in calls */
     void     *h_dev_x, *h_dev_out;
     size_t    h_cap;
+    /* expert cache (k3x_moe_layer_create_cached): nslot slots of the expert arena hold the
+     * resident experts; 0 when every expert sits at its own index */
+    int       nslot;
+    int      *slot_dev;           /* [E] slot of each expert, -1 when not resident   */
+    int      *slot_of;            /* host copy of slot_dev                            */
+    int      *key_of;             /* [nslot] expert held, -1 empty                    */
+    uint64_t *used_at;            /* [nslot] LRU stamp                                */
+    unsigned char *pinned;        /* [nslot] never evicted while set                  */
+    uint64_t  clock, hits, misses, evictions, bytes_read;
+    struct k3x_store *st;         /* where misses are read from                       */
+    int       st_layer;
+    unsigned char *c_hbuf;        /* pinned host buffer of one expert run             */
+    uint8_t  *c_dbuf;             /* device staging of one expert run                 */
+    int      *c_route;            /* pinned host copy of the routing summary's head   */
+    int       c_dirty;            /* slot_of changed since slot_dev was last written   */
 };
+
+/* expert cache: make the unique experts of the published routing resident (decode) */
+int k3x_cache_fill(k3x_moe_layer *L, void *stream);
 
 /* ---- launchers (k3x_kernels.hip), all return 0 or K3X_E_HIP ---------------------- */
 int k3x_dev_check(int device);

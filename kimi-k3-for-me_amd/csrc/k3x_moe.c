@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime_api.h>
 #include <math.h>
+#include <stddef.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -97,7 +98,8 @@ static int layer_alloc(k3x_moe_layer *L)
     size_t *b = &L->bytes;
     RCCHK(dmalloc((void **)&L->router, (size_t)E * H * 4, b));
     RCCHK(dmalloc((void **)&L->bias, (size_t)E * 4, b));
-    RCCHK(dmalloc((void **)&L->experts, (size_t)E * L->expert_bytes, b));
+    RCCHK(dmalloc((void **)&L->experts, (size_t)(L->nslot ? L->nslot : E) * L->expert_bytes, b));
+    if (L->nslot) RCCHK(dmalloc((void **)&L->slot_dev, (size_t)E * 4, b));
     if (L->SI > 0) {
         RCCHK(dmalloc((void **)&L->sh_gate, k3x_bf16_matrix_bytes(L->SI, H), b));
         RCCHK(dmalloc((void **)&L->sh_up, k3x_bf16_matrix_bytes(L->SI, H), b));
@@ -139,6 +141,11 @@ static void layer_free(k3x_moe_layer *L)
                  L->ldown, L->lup, L->lnw, L->zB, L->accL, L->latB};
     for (size_t i = 0; i < sizeof p / sizeof p[0]; i++)
         if (p[i]) hipFree(p[i]);
+    if (L->slot_dev) hipFree(L->slot_dev);
+    if (L->c_dbuf) hipFree(L->c_dbuf);
+    if (L->c_hbuf) hipHostFree(L->c_hbuf);
+    if (L->c_route) hipHostFree(L->c_route);
+    free(L->slot_of); free(L->key_of); free(L->used_at); free(L->pinned);
     for (int i = 0; i < 8; i++)
         if (L->ev[i]) hipEventDestroy((hipEvent_t)L->ev[i]);
     free(L);
@@ -154,7 +161,14 @@ void k3x_moe_layer_destroy(k3x_moe_layer *L)
 
 size_t k3x_moe_layer_bytes(const k3x_moe_layer *L) { return L ? L->bytes + L->pf.bytes : 0; }
 
+static int new_layer_slots(const k3x_cfg *c, int device, int nslot, k3x_moe_layer **out);
+
 static int new_layer(const k3x_cfg *c, int device, k3x_moe_layer **out)
+{
+    return new_layer_slots(c, device, 0, out);
+}
+
+static int new_layer_slots(const k3x_cfg *c, int device, int nslot, k3x_moe_layer **out)
 {
     int rc = cfg_ok(c);
     if (rc) return rc;
@@ -165,6 +179,7 @@ static int new_layer(const k3x_cfg *c, int device, k3x_moe_layer **out)
     L->cfg = *c;
     L->device = device;
     L->wait_ticks = K3X_ROUTE_WAIT_DEFAULT;
+    L->nslot = nslot;
     if ((rc = layer_alloc(L))) { layer_free(L); return rc; }
     *out = L;
     return 0;
@@ -385,14 +400,184 @@ fail:
     return rc;
 }
 
+/* ---------------------------------------------------------------- expert cache ---- */
+/* A layer whose expert arena holds nslot experts (k3_cache.c's K3Cache, with the arena in
+ * HBM instead of host RAM): after a decode call's selection the experts it names are made
+ * resident, a miss reading the expert's run from the store into a pinned buffer, copying
+ * it to the device and re-laying it out into a slot; victims are the least recently used
+ * unpinned slots not named by the call.  The kernels reach an expert through the slot
+ * table (slot_dev). */
+int k3x_moe_layer_create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store *st,
+                                int layer, int nslot, int device, k3x_moe_layer **out)
+{
+    if (!c || !w || !st || !out || !w->gate) return K3X_E_ARG;
+    *out = NULL;
+    if (nslot < c->topk + 1 || nslot > c->n_experts) return K3X_E_ARG;
+    k3x_moe_layer *L = NULL;
+    int rc = new_layer_slots(c, device, nslot, &L);
+    if (rc) return rc;
+    const int H = c->hidden, E = c->n_experts, I = c->moe_inter, X = L->XL;
+    const size_t run = 3 * ((size_t)I * X / 2 + (size_t)I * X / 32);
+    L->st = st; L->st_layer = layer;
+    L->slot_of = (int *)malloc((size_t)E * sizeof(int));
+    L->key_of = (int *)malloc((size_t)nslot * sizeof(int));
+    L->used_at = (uint64_t *)calloc((size_t)nslot, sizeof(uint64_t));
+    L->pinned = (unsigned char *)calloc((size_t)nslot, 1);
+    if (!L->slot_of || !L->key_of || !L->used_at || !L->pinned) { rc = K3X_E_NOMEM; goto fail; }
+    for (int e = 0; e < E; e++) L->slot_of[e] = -1;
+    for (int i = 0; i < nslot; i++) L->key_of[i] = -1;
+    HIPCHK(hipHostMalloc((void **)&L->c_hbuf, run, hipHostMallocDefault));
+    HIPCHK(hipHostMalloc((void **)&L->c_route, sizeof(k3x_route), hipHostMallocDefault));
+    HIPCHK(hipMalloc((void **)&L->c_dbuf, run));
+    HIPCHK(hipMemcpy(L->slot_dev, L->slot_of, (size_t)E * 4, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(L->router, w->gate, (size_t)E * H * 4, hipMemcpyHostToDevice));
+    if (w->bias) HIPCHK(hipMemcpy(L->bias, w->bias, (size_t)E * 4, hipMemcpyHostToDevice));
+    RCCHK(upload_shared(L, w->sh1, w->sh3, w->sh2));
+    RCCHK(upload_latent(L, w->down, w->up, w->latent_norm));
+    *out = L;
+    return 0;
+fail:
+    layer_free(L);
+    return rc;
+}
+
+/* expert e into a slot (a miss): the least recently used unpinned slot whose expert the
+ * current call does not name (want[key] == 0), empty slots first */
+static int cache_load(k3x_moe_layer *L, int e, const unsigned char *want, hipStream_t s)
+{
+    const int I = L->cfg.moe_inter, X = L->XL;
+    const size_t run = 3 * ((size_t)I * X / 2 + (size_t)I * X / 32);
+    int v = -1;
+    for (int i = 0; i < L->nslot; i++) {
+        if (L->pinned[i]) continue;
+        const int k = L->key_of[i];
+        if (k >= 0 && want && want[k]) continue;
+        if (k < 0) { v = i; break; }
+        if (v < 0 || L->used_at[i] < L->used_at[v]) v = i;
+    }
+    if (v < 0) return K3X_E_SHAPE;              /* every slot pinned or in use */
+    k3x_expert_ref r;
+    if (k3x_store_expert_ref(L->st, L->st_layer, e, &r) || !store_shape_ok(&r, I, X) ||
+        (size_t)r.nbytes > run || k3x_store_expert_load(L->st, &r, L->c_hbuf) != r.nbytes) {
+        k3x_expert_drops++;
+        fprintf(stderr, "EXPERT DROP: layer %d expert %d could not be read from the store\n",
+                L->st_layer, e);
+        return K3X_E_DROP;
+    }
+    const k3x_expert_q q = {L->c_hbuf + r.m[0].p_off, L->c_hbuf + r.m[0].s_off,
+                            L->c_hbuf + r.m[2].p_off, L->c_hbuf + r.m[2].s_off,
+                            L->c_hbuf + r.m[1].p_off, L->c_hbuf + r.m[1].s_off};
+    L->special |= scale_flags(&q, (size_t)I * X / 32);
+    if (L->key_of[v] >= 0) {
+        L->slot_of[L->key_of[v]] = -1;
+        L->key_of[v] = -1;
+        L->c_dirty = 1;
+        L->evictions++;
+    }
+    uint8_t *base = L->experts + (size_t)v * L->expert_bytes;
+    uint8_t *db = L->c_dbuf;
+    int rc = 0;
+    HIPCHK(hipMemcpyAsync(db, L->c_hbuf, (size_t)r.nbytes, hipMemcpyHostToDevice, s));
+    RCCHK(k3x_dev_tile_fp4(base + L->gate_off, db + r.m[0].p_off, db + r.m[0].s_off, I, X, s));
+    RCCHK(k3x_dev_tile_fp4(base + L->up_off, db + r.m[2].p_off, db + r.m[2].s_off, I, X, s));
+    RCCHK(k3x_dev_tile_fp4(base + L->down_off, db + r.m[1].p_off, db + r.m[1].s_off, X, I, s));
+    /* the pinned buffer and the staging area are reused by the next miss */
+    HIPCHK(hipStreamSynchronize(s));
+    L->key_of[v] = e;
+    L->slot_of[e] = v;
+    L->c_dirty = 1;
+    L->used_at[v] = ++L->clock;
+    L->bytes_read += (uint64_t)r.nbytes;
+    L->misses++;
+    return 0;
+fail:
+    return rc;
+}
+
+int k3x_cache_fill(k3x_moe_layer *L, void *stream)
+{
+    hipStream_t s = (hipStream_t)stream;
+    const size_t head = offsetof(k3x_route, uniq) + sizeof(((k3x_route *)0)->uniq);
+    int rc = 0;
+    HIPCHK(hipMemcpyAsync(L->c_route, L->route, head, hipMemcpyDeviceToHost, s));
+    HIPCHK(hipStreamSynchronize(s));
+    const k3x_route *r = (const k3x_route *)L->c_route;
+    const int nu = r->nu, E = L->cfg.n_experts;
+    if (nu < 0 || nu > K3X_DECODE_MAX_T * K3X_MAX_TOPK) return K3X_E_HIP;
+    if (nu > L->nslot) return K3X_E_SHAPE;      /* more experts than slots in one call */
+    unsigned char *want = (unsigned char *)calloc((size_t)E, 1);
+    if (!want) return K3X_E_NOMEM;
+    for (int u = 0; u < nu; u++) {
+        const int e = r->uniq[u];
+        if (e < 0 || e >= E) { free(want); return K3X_E_HIP; }
+        want[e] = 1;
+    }
+    for (int u = 0; u < nu && !rc; u++) {
+        const int e = r->uniq[u];
+        if (L->slot_of[e] >= 0) {
+            L->hits++;
+            L->used_at[L->slot_of[e]] = ++L->clock;
+        } else {
+            rc = cache_load(L, e, want, s);
+        }
+    }
+    free(want);
+    if (rc) return rc;
+    if (L->c_dirty) {
+        HIPCHK(hipMemcpyAsync(L->slot_dev, L->slot_of, (size_t)E * 4, hipMemcpyHostToDevice, s));
+        L->c_dirty = 0;
+    }
+    return 0;
+fail:
+    return rc;
+}
+
+int k3x_cache_stats(const k3x_moe_layer *L, k3x_cache_stat *st)
+{
+    if (!L || !st) return K3X_E_ARG;
+    memset(st, 0, sizeof *st);
+    st->nslot = L->nslot;
+    for (int i = 0; i < L->nslot; i++) st->resident += L->key_of[i] >= 0;
+    st->hits = L->hits; st->misses = L->misses;
+    st->evictions = L->evictions; st->bytes_read = L->bytes_read;
+    return 0;
+}
+
+int k3x_cache_pin(k3x_moe_layer *L, int expert, int pin)
+{
+    if (!L || !L->nslot || expert < 0 || expert >= L->cfg.n_experts) return K3X_E_ARG;
+    int rc = 0;
+    if (hipSetDevice(L->device) != hipSuccess) return K3X_E_NODEV;
+    if (L->slot_of[expert] < 0) {
+        if (!pin) return 0;
+        int np = 0;
+        for (int i = 0; i < L->nslot; i++) np += L->pinned[i];
+        if (np + 1 > L->nslot - L->cfg.topk) return K3X_E_SHAPE;   /* keep topk slots free */
+        hipStream_t s = NULL;
+        HIPCHK(hipStreamCreate(&s));
+        rc = cache_load(L, expert, NULL, s);
+        if (!rc && hipMemcpyAsync(L->slot_dev, L->slot_of, (size_t)L->cfg.n_experts * 4,
+                                  hipMemcpyHostToDevice, s) != hipSuccess) rc = K3X_E_HIP;
+        if (!rc && hipStreamSynchronize(s) != hipSuccess) rc = K3X_E_HIP;
+        if (!rc) L->c_dirty = 0;
+        hipStreamDestroy(s);
+        if (rc) return rc;
+    }
+    L->pinned[L->slot_of[expert]] = pin ? 1 : 0;
+    return 0;
+fail:
+    return rc;
+}
+
 int k3x_moe_layer_read_expert(const k3x_moe_layer *L, int e, unsigned char *p1,
                               unsigned char *s1, unsigned char *p3, unsigned char *s3,
                               unsigned char *p2, unsigned char *s2)
 {
     if (!L || e < 0 || e >= L->cfg.n_experts) return K3X_E_ARG;
+    if (L->nslot && L->slot_of[e] < 0) return K3X_E_ARG;        /* not resident */
     const int H = L->XL, I = L->cfg.moe_inter;
     const size_t pg = (size_t)I * H / 2, sg = (size_t)I * H / 32;
-    const uint8_t *base = L->experts + (size_t)e * L->expert_bytes;
+    const uint8_t *base = L->experts + (size_t)(L->nslot ? L->slot_of[e] : e) * L->expert_bytes;
     uint8_t *st = NULL;
     int rc = 0;
     HIPCHK(hipSetDevice(L->device));
@@ -488,6 +673,7 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     if (T == 0) return 0;
     if (T <= L->tdec)
         return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, NULL, 0.0f, stream);
+    if (L->nslot) return K3X_E_ARG;           /* a cached layer serves decode calls only */
     return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
 }
 
@@ -786,7 +972,7 @@ int k3x_stack_create(k3x_moe_layer *const *layers, const float *const *norm_w, i
     for (int l = 0; l < n_layers; l++) {
         if (!layers[l] || !norm_w[l]) return K3X_E_ARG;
         if (layers[l]->cfg.hidden != H || layers[l]->device != dev) return K3X_E_SHAPE;
-        if (layers[l]->timing) return K3X_E_ARG;
+        if (layers[l]->timing || layers[l]->nslot) return K3X_E_ARG;
     }
     k3x_stack *S = (k3x_stack *)calloc(1, sizeof *S);
     if (!S) return K3X_E_NOMEM;

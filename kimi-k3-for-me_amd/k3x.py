@@ -38,6 +38,9 @@ EXPORTS = [
     "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
     "k3x_store_src_create", "k3x_store_src_destroy", "k3x_store_src_fetches",
     "k3x_moe_layer_create_from_store",
+    "k3x_moe_layer_create_cached",
+    "k3x_cache_stats",
+    "k3x_cache_pin",
     # include/k3x_trunk.h
     "k3x_trunk_create", "k3x_trunk_destroy", "k3x_trunk_apply", "k3x_trunk_apply_host",
 ]
@@ -159,6 +162,10 @@ def lib():
         L.k3x_store_src_fetches.restype = C.c_long
         L.k3x_moe_layer_create_from_store.argtypes = [C.POINTER(Cfg), C.POINTER(MoeW), vp, i, i,
                                                       C.POINTER(vp)]
+        L.k3x_moe_layer_create_cached.argtypes = [C.POINTER(Cfg), C.POINTER(MoeW), vp, i, i, i,
+                                                  C.POINTER(vp)]
+        L.k3x_cache_stats.argtypes = [vp, C.POINTER(CacheStat)]
+        L.k3x_cache_pin.argtypes = [vp, i, i]
         L.k3x_attn_res.argtypes = [vp, vp, i, i, vp, vp, i, i, f, vp]
         L.k3x_moe_half.argtypes = [vp, vp, vp, vp, i, i, vp, vp, f, i, vp, vp]
         L.k3x_trunk_create.argtypes = [vp, i, i, i, C.POINTER(vp)]
@@ -270,6 +277,30 @@ class MoELayer:
                                                      device, C.byref(h)),
                "k3x_moe_layer_create_from_store")
         return cls(h.value, cfg)
+
+    @classmethod
+    def from_store_cached(cls, cfg, gate, bias, store, layer, nslot, sh1=None, sh3=None,
+                          sh2=None, device=0, down=None, up=None, latent_norm=None):
+        """A layer with an HBM expert cache of nslot slots over a Store
+        (k3x_moe_layer_create_cached); decode calls only."""
+        w = MoeW(_vp(gate), _vp(bias), _vp(sh1), _vp(sh3), _vp(sh2), None, None, layer,
+                 _vp(down), _vp(up), _vp(latent_norm))
+        h = C.c_void_p()
+        _check(lib().k3x_moe_layer_create_cached(C.byref(cfg), C.byref(w), store.h, layer,
+                                                 nslot, device, C.byref(h)),
+               "k3x_moe_layer_create_cached")
+        obj = cls(h.value, cfg)
+        obj.store = store                       # the cache reads misses from it
+        return obj
+
+    def cache_stats(self):
+        """k3x_cache_stats as a dict."""
+        st = CacheStat()
+        _check(lib().k3x_cache_stats(self.h, C.byref(st)), "k3x_cache_stats")
+        return {f: int(getattr(st, f)) for f, _ in CacheStat._fields_}
+
+    def cache_pin(self, expert, pin=True):
+        _check(lib().k3x_cache_pin(self.h, expert, 1 if pin else 0), "k3x_cache_pin")
 
     @classmethod
     def synthetic(cls, cfg, seed=0, layer=0, router_sigma=0.02, bias_sigma=0.1, zipf_alpha=0.0,
@@ -401,6 +432,13 @@ class Stack:
             self.close()
         except Exception:
             pass
+
+
+class CacheStat(C.Structure):
+    """k3x_cache_stat (include/k3x_store.h)."""
+    _fields_ = [("nslot", C.c_int), ("resident", C.c_int), ("hits", C.c_ulonglong),
+                ("misses", C.c_ulonglong), ("evictions", C.c_ulonglong),
+                ("bytes_read", C.c_ulonglong)]
 
 
 class Store:

@@ -56,3 +56,85 @@ def test_missing_expert_is_a_drop(torch, k3x, tmp_path):
     assert ei.value.status == -5
     assert k3x.expert_drops() == d0 + 1
     st.close()
+
+
+def run_bytes(L):
+    return 3 * (L.I * L.XL // 2 + L.I * L.XL // 32)
+
+
+@pytest.mark.parametrize("latent", [False, True])
+def test_cached_layer_equals_resident(torch, k3x, tmp_path, latent):
+    """A layer with an HBM expert cache of topk + 2 slots over the shards, token by token and
+    in T = 2 calls, against the same layer with every expert resident: identical indices and
+    bitwise equal outputs; the counters add up (hits + misses = experts named, bytes read =
+    misses x run, evictions = misses - resident)."""
+    say(f"case: expert cache of topk+2 slots (latent={latent}) vs every expert resident")
+    L = synth.tiny_latent(seed=23) if latent else synth.tiny(seed=23)
+    write_layer(tmp_path, L, layer=3)
+    st = k3x.Store(str(tmp_path))
+    cfg = layer_cfg(k3x, L)
+    kw = dict(down=L.down, up=L.up, latent_norm=L.lnorm)
+    full = k3x.MoELayer.from_store(cfg, L.gate, L.bias, st, 3, L.sh1, L.sh3, L.sh2, **kw)
+    nslot = cfg.topk + 2
+    cache = k3x.MoELayer.from_store_cached(cfg, L.gate, L.bias, st, 3, nslot, L.sh1, L.sh3,
+                                           L.sh2, **kw)
+    x = L.x(12, bf16=False, stream_sub=3)
+    named, seen = 0, set()
+    for t in range(12):
+        of, i_f, _ = dev_forward(torch, k3x, full, x[t:t + 1])
+        oc, i_c, _ = dev_forward(torch, k3x, cache, x[t:t + 1])
+        assert np.array_equal(i_f, i_c), t
+        assert np.array_equal(of.view(np.uint32), oc.view(np.uint32)), t
+        named += len(np.unique(i_c))
+        seen |= set(np.unique(i_c).tolist())
+    for t in range(0, 6, 2):
+        of, i_f, _ = dev_forward(torch, k3x, full, x[t:t + 2])
+        if len(np.unique(i_f)) > nslot:
+            continue
+        oc, i_c, _ = dev_forward(torch, k3x, cache, x[t:t + 2])
+        assert np.array_equal(i_f, i_c)
+        assert np.array_equal(of.view(np.uint32), oc.view(np.uint32))
+        named += len(np.unique(i_c))
+    s = cache.cache_stats()
+    say(f"  stats {s}, distinct experts {len(seen)}")
+    assert s["nslot"] == nslot
+    assert s["hits"] + s["misses"] == named
+    assert s["bytes_read"] == s["misses"] * run_bytes(L)
+    assert s["resident"] == min(nslot, s["misses"])
+    assert s["evictions"] == s["misses"] - s["resident"]
+    assert s["misses"] >= len(seen) and s["evictions"] > 0
+    o, _, _, _ = L.oracle_moe(x[:1])
+    of, _, _ = dev_forward(torch, k3x, cache, x[:1])
+    assert synth.rel_l2(of, o) < 1e-3
+    cache.close(); full.close(); st.close()
+
+
+def test_cache_pin_prefill_and_capacity(torch, k3x, tmp_path):
+    """A pinned expert stays resident through later tokens; a prefill call on a cached
+    layer is refused (K3X_E_ARG); a call naming more experts than slots returns
+    K3X_E_SHAPE and the layer keeps working."""
+    say("case: expert cache pinning, prefill refusal, capacity")
+    L = synth.tiny(seed=24)
+    write_layer(tmp_path, L, layer=0)
+    st = k3x.Store(str(tmp_path))
+    cfg = layer_cfg(k3x, L)
+    cache = k3x.MoELayer.from_store_cached(cfg, L.gate, L.bias, st, 0, cfg.topk + 1, L.sh1,
+                                           L.sh3, L.sh2)
+    cache.cache_pin(7)
+    x = L.x(16, bf16=False, stream_sub=5)
+    for t in range(8):
+        dev_forward(torch, k3x, cache, x[t:t + 1])
+    assert np.array_equal(cache.read_expert(7)["p1"], L.expert(7)["p1"])
+    with pytest.raises(k3x.K3XError) as ei:
+        dev_forward(torch, k3x, cache, x)                 # T = 16: the prefill path
+    assert ei.value.status == -1
+    _, idx8, _, _ = L.oracle_moe(x[:8])
+    assert len(np.unique(idx8)) > cfg.topk + 1
+    with pytest.raises(k3x.K3XError) as ei:
+        dev_forward(torch, k3x, cache, x[:8])             # more experts than slots
+    assert ei.value.status == -2
+    o, _, _, _ = L.oracle_moe(x[:1])
+    of, _, _ = dev_forward(torch, k3x, cache, x[:1])
+    assert synth.rel_l2(of, o) < 1e-3
+    cache.cache_pin(7, False)
+    cache.close(); st.close()

@@ -246,3 +246,17 @@ def test_real_checkpoint_bytes_through_an_expert_run(k3x, tmp_path):
     oracle().ko_mxfp4_dequant(ptr(y, F32P), ptr(packed, U8P), ptr(scales, U8P), 64, X // 2, 32)
     assert np.array_equal(y, g["expected"])
     st.close()
+
+
+@pytest.mark.parametrize("nslot", [0, 4, 17])
+def test_cached_layer_slot_bounds(k3x, shards, nslot):
+    """k3x_moe_layer_create_cached refuses fewer than topk + 1 slots or more slots than
+    experts before it touches a device (k3_cache_init's lower bound)."""
+    path, _, _ = shards
+    st = k3x.Store(str(path))
+    cfg = k3x.make_cfg(256, 16, 4, 128, 1, 1, 2.5)
+    gate = np.zeros((16, 256), np.float32)
+    with pytest.raises(k3x.K3XError) as ei:
+        k3x.MoELayer.from_store_cached(cfg, gate, None, st, 1, nslot)
+    assert ei.value.status == -1
+    st.close()

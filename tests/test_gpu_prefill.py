@@ -118,3 +118,49 @@ def test_full_prefill_2048_zipf(torch, k3x):
     say(f"  rel_l2(prefill, oracle) on tokens {sample} = {err:.3e}")
     assert err < TOL
     layer.close()
+
+
+def test_prefill_graph_replays(torch, k3x):
+    """A prefill chunk (T = 40) captured once into a HIP graph and replayed on new inputs,
+    with eager work and synchronisations between the replays: every replay equals the eager
+    call bit for bit (routing, permute, grouped GEMMs and combine are all kernels with
+    host-computed grids, so the per-layer sequence captures)."""
+    say("case: prefill T=40 captured in a graph, 3 replays with eager copies between")
+    L = synth.tiny(seed=35)
+    layer = bank_layer(k3x, L)
+    T, H, K = 40, L.H, L.K
+    xd = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+    wt = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+
+    def run():
+        layer.forward(out.data_ptr(), xd.data_ptr(), T, k3x.K3X_F32, 0, idx.data_ptr(),
+                      wt.data_ptr(), stream=s.cuda_stream)
+
+    xd.copy_(torch.from_numpy(L.x(T, bf16=False, stream_sub=20)))
+    with torch.cuda.stream(s):
+        run()                                   # eager: reserves the chunk buffers
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run()
+    torch.cuda.synchronize()
+    for r in range(3):
+        x = L.x(T, bf16=False, stream_sub=21 + r)
+        xd.copy_(torch.from_numpy(x))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        go, gi = out.clone(), idx.clone()
+        with torch.cuda.stream(s):
+            run()
+        torch.cuda.synchronize()
+        say(f"  replay {r}")
+        assert torch.equal(gi, idx) and torch.equal(go, out)
+        o, i_ref, _, _ = L.oracle_moe(x)
+        assert np.array_equal(gi.cpu().numpy(), i_ref)
+        assert synth.rel_l2(go.cpu().numpy(), o) < TOL
+    layer.check()
+    layer.close()

@@ -1072,19 +1072,22 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     constexpr int NW = NT3 / WAVE;
     const int NC = 2 * a.T;
-    const int nu = a.route->nu;
+    const int nall = a.route->nu;
+    const int u0 = (int)blockIdx.y * a.upp;         // this part's unique experts
+    const int nu = nall - u0 < a.upp ? (nall > u0 ? nall - u0 : 0) : a.upp;
     const int nSI = ((a.I >> 7) + 3) >> 2;
     const uint32_t slot = (uint32_t)nSI * 1024u * NC;
     const uint32_t tb = (uint32_t)fp4_tile_bytes(a.I);
     const int rt0 = 2 * blockIdx.x;
     const int cnt = strided_count(wave, NW, nu * nSI);
-    const int nQS = a.sh_down ? a.SI >> 7 : 0;
+    const int nQS = (a.sh_down && blockIdx.y == 0) ? a.SI >> 7 : 0;
+    const uint16_t *actB = a.actB + (size_t)u0 * (slot / 2);
     SQ ring[2][2];
     auto ld = [&](int i, int k) AI {
         const int it = wave + NW * k;
         const bool on = k < cnt;
         const int u = on ? it / nSI : 0, S = on ? it % nSI : 0;
-        int e = on ? a.route->uniq[u] : 0;
+        int e = on ? a.route->uniq[u0 + u] : 0;
         if (a.slot) e = on ? a.slot[e] : 0;
         const rsrc_t r = make_rsrc(a.experts + (size_t)e * a.expert_bytes + a.down_off +
                                        (size_t)rt0 * tb, on ? 2 * tb : 0u);
@@ -1111,7 +1114,7 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
     };
     ring_prime<2>(ld2);
     BFrag<false> bf;
-    bf.init(a.actB, (uint32_t)nu * slot, NC, lane);
+    bf.init(actB, (uint32_t)nu * slot, NC, lane);
     f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
     ring_loop<2>(cnt, ld, [&](int i, int k) AI {
         const int it = wave + NW * k;
@@ -1133,11 +1136,12 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
     float acc[8] = {d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3]};
     wave_sum_lds<8, NW>(acc, lds, wave, lane);
     if (wave != 0) return;
+    float *out = a.out + blockIdx.y * a.pstride;
     per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&v)[8]) AI {
         for (int tt = 0; tt < 2; tt++)
             for (int i = 0; i < 4; i++) {
                 const size_t o = (size_t)tok * a.H + (rt0 + tt) * 16 + r0 + i;
-                a.out[o] = a.resid ? a.resid[o] + v[4 * tt + i] : v[4 * tt + i];
+                out[o] = a.resid ? a.resid[o] + v[4 * tt + i] : v[4 * tt + i];
             }
     });
 }
@@ -1489,16 +1493,22 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     // its rows in one part
     int parts = 1;
     a3.upp = T * c->topk;
+    // latent form with the activation sets past the LDS: two row tiles a workgroup
+    // (k3_down2, each B fragment read once for both) and parts for parallelism
+    const bool lat2 = L->lat && !a3.lds_bytes && T >= 2 && X % 32 == 0;
     if (L->lat && a3.lds_bytes) {
         parts = (T * c->topk + (int)(a3.lds_bytes / slot) - 1) / (int)(a3.lds_bytes / slot);
         if (parts > K3X_DECODE_PARTS) parts = K3X_DECODE_PARTS;
         a3.upp = (T * c->topk + parts - 1) / parts;     // balanced parts
+    } else if (lat2) {
+        parts = T * c->topk < K3X_DECODE_PARTS ? T * c->topk : K3X_DECODE_PARTS;
+        a3.upp = (T * c->topk + parts - 1) / parts;
     }
     a3.pstride = parts > 1 ? (size_t)K3X_DECODE_MAX_T * X : 0;
     const size_t l3 = (size_t)a3.lds_bytes + a3.sh_lds;
-    if (!L->lat && T >= 2 && X % 32 == 0) {
-        if (L->special & 4) hipLaunchKernelGGL(k3_down2<true>, dim3(X / 32), dim3(NT3), 0, s, a3);
-        else                hipLaunchKernelGGL(k3_down2<false>, dim3(X / 32), dim3(NT3), 0, s, a3);
+    if ((!L->lat && T >= 2 && X % 32 == 0) || lat2) {
+        if (L->special & 4) hipLaunchKernelGGL(k3_down2<true>, dim3(X / 32, parts), dim3(NT3), 0, s, a3);
+        else                hipLaunchKernelGGL(k3_down2<false>, dim3(X / 32, parts), dim3(NT3), 0, s, a3);
     } else if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(X / 16, parts), dim3(NT3), l3, s, a3);
     else                hipLaunchKernelGGL(k3_down<false>, dim3(X / 16, parts), dim3(NT3), l3, s, a3);
     if ((rc = launch_ok())) return rc;

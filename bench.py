@@ -352,6 +352,38 @@ def trunk_leg(torch, k3x, reps=48, nrot=4):
     return rec
 
 
+def k3_multi_leg(torch, k3x, tokens=(2, 4, 8), steps=60, warmup=10, nrot=2):
+    """Decode calls of several bf16 tokens through the K3 LatentMoE layer shape with
+    Zipf-skewed routing (alpha 1.0, s 1.1), `nrot` layers in turn: microseconds per call
+    for each token count."""
+    cfg = k3x.make_cfg(H, K3_E, K3_K, K3_I, 2, 1, 1.0, latent=K3_L, latent_norm=1,
+                       rms_eps=1e-5, situ_b1=4.0, situ_b2=25.0)
+    layers = [k3x.MoELayer.synthetic(cfg, seed=60 + j, zipf_alpha=1.0) for j in range(nrot)]
+    n_pool = 64
+    rec = {"workload": "K3 LatentMoE decode, several bf16 tokens a call, Zipf-skewed routing "
+                       f"(alpha 1.0, s 1.1), {nrot} layers in turn", "us_per_call": {}}
+    stream = torch.cuda.Stream()
+    for T in tokens:
+        xs = k3x.synth_normal_f32(n_pool * T * H, k3x.synth_key(60, 0, k3x.STREAM_X, T))
+        xpool = torch.from_numpy(xs.reshape(n_pool, T, H)).cuda().to(torch.bfloat16).contiguous()
+        out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+        with torch.cuda.stream(stream):
+            for i in range(warmup + steps):
+                if i == warmup:
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                layers[i % nrot].forward(out.data_ptr(), xpool[i % n_pool].data_ptr(), T,
+                                         k3x.K3X_BF16, stream=stream.cuda_stream)
+            torch.cuda.synchronize()
+        rec["us_per_call"][str(T)] = round((time.perf_counter() - t0) * 1e6 / steps, 1)
+        del xpool, out
+    for l in layers:
+        l.check()
+        l.close()
+    torch.cuda.empty_cache()
+    return rec
+
+
 def verify_leg(torch, k3x, steps=100, warmup=10, nrot=4):
     """Speculative verification, T = 8 tokens per call, through the full-size K2-class
     layer with Zipf-skewed routing (alpha 1.0, s 1.1): microseconds per call and the HBM
@@ -507,6 +539,8 @@ def main():
                     help="only run the 8-layer stack leg and print its record")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the prefill leg and print its record")
+    ap.add_argument("--k3-multi-only", action="store_true",
+                    help="only run the K3 LatentMoE several-token decode leg")
     ap.add_argument("--verify-only", action="store_true",
                     help="only run the T=8 verify leg and print its record")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -533,6 +567,9 @@ def main():
         return
     if args.trunk_only:
         print(json.dumps(trunk_leg(torch, load_k3x())), flush=True)
+        return
+    if args.k3_multi_only:
+        print(json.dumps(k3_multi_leg(torch, load_k3x())), flush=True)
         return
     if args.verify_only:
         print(json.dumps(verify_leg(torch, load_k3x())), flush=True)
@@ -645,6 +682,7 @@ def main():
         rec["k3_latent"] = k3_leg(torch, k3x, min(args.steps, 100), min(args.warmup, 10))
         if not args.no_prefill:
             rec["k3_latent"]["prefill"] = k3_prefill_leg(torch, k3x)
+        rec["k3_latent"]["multi"] = k3_multi_leg(torch, k3x)
     if not args.no_trunk:
         rec["trunk"] = trunk_leg(torch, k3x)
     if not args.no_cpu_baseline:

@@ -1170,6 +1170,17 @@ __device__ __forceinline__ float agg_at(const KNArgs &a, size_t i)
     return v;
 }
 
+// four consecutive aggregates (i a multiple of 4), each added over the parts in order
+__device__ __forceinline__ f32x4 agg4(const KNArgs &a, size_t i)
+{
+    f32x4 v = *(const f32x4 *)(a.acc + i);
+    for (int p = 1; p < a.P; p++) {
+        const f32x4 w = *(const f32x4 *)(a.acc + p * a.pstride + i);
+        v[0] += w[0]; v[1] += w[1]; v[2] += w[2]; v[3] += w[3];
+    }
+    return v;
+}
+
 __global__ void __launch_bounds__(NT4) k4_latent_norm(KNArgs a)
 {
     __shared__ double dl[NT4 / WAVE][K3X_DECODE_MAX_T];
@@ -1178,9 +1189,10 @@ __global__ void __launch_bounds__(NT4) k4_latent_norm(KNArgs a)
     if (a.nw) {
         for (int t = 0; t < a.T; t++) {
             double ss = 0.0;
-            for (int i = threadIdx.x; i < a.XL; i += NT4) {
-                const double v = (double)agg_at(a, (size_t)t * a.XL + i);
-                ss += v * v;
+            for (int i = threadIdx.x * 4; i < a.XL; i += NT4 * 4) {
+                const f32x4 v = agg4(a, (size_t)t * a.XL + i);
+                ss += (double)v[0] * (double)v[0] + (double)v[1] * (double)v[1] +
+                      (double)v[2] * (double)v[2] + (double)v[3] * (double)v[3];
             }
             for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
             if (lane == 0) dl[wave][t] = ss;
@@ -1204,8 +1216,9 @@ __global__ void __launch_bounds__(NT4) k4_latent_norm(KNArgs a)
             const int c0 = q * 128 + kq * 32 + t * 8;
             const size_t base = (size_t)(n >> 1) * a.XL + c0;
             float xv[8];
+            const f32x4 v0 = agg4(a, base), v1 = agg4(a, base + 4);
 #pragma unroll
-            for (int j = 0; j < 8; j++) xv[j] = agg_at(a, base + j);
+            for (int j = 0; j < 4; j++) { xv[j] = v0[j]; xv[4 + j] = v1[j]; }
             if (a.nw) {
                 const float inv = s_inv[n >> 1];
 #pragma unroll

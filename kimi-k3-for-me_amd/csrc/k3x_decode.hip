@@ -1187,15 +1187,25 @@ __global__ void __launch_bounds__(NT4) k4_latent_norm(KNArgs a)
     __shared__ float s_inv[K3X_DECODE_MAX_T];
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     if (a.nw) {
-        for (int t = 0; t < a.T; t++) {
-            double ss = 0.0;
-            for (int i = threadIdx.x * 4; i < a.XL; i += NT4 * 4) {
+        // every token's loads of a step in flight together
+        double ss[K3X_DECODE_MAX_T];
+#pragma unroll
+        for (int t = 0; t < K3X_DECODE_MAX_T; t++) ss[t] = 0.0;
+        for (int i = threadIdx.x * 4; i < a.XL; i += NT4 * 4) {
+#pragma unroll
+            for (int t = 0; t < K3X_DECODE_MAX_T; t++) {
+                if (t >= a.T) break;
                 const f32x4 v = agg4(a, (size_t)t * a.XL + i);
-                ss += (double)v[0] * (double)v[0] + (double)v[1] * (double)v[1] +
-                      (double)v[2] * (double)v[2] + (double)v[3] * (double)v[3];
+                ss[t] += (double)v[0] * (double)v[0] + (double)v[1] * (double)v[1] +
+                         (double)v[2] * (double)v[2] + (double)v[3] * (double)v[3];
             }
-            for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-            if (lane == 0) dl[wave][t] = ss;
+        }
+#pragma unroll
+        for (int t = 0; t < K3X_DECODE_MAX_T; t++) {
+            if (t >= a.T) break;
+            double v = ss[t];
+            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0) dl[wave][t] = v;
         }
         __syncthreads();
         if (threadIdx.x < a.T) {

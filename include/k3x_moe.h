@@ -124,6 +124,15 @@ void k3x_moe_layer_destroy(k3x_moe_layer *L);
 /* Bytes of device memory the layer holds (weights plus its working buffers). */
 size_t k3x_moe_layer_bytes(const k3x_moe_layer *L);
 
+/* Reserve the prefill working buffers for calls of up to max_T tokens (no-op for the
+ * decode path's T <= 8 and for cached layers).  A forward call with more tokens than are
+ * reserved grows the buffers itself, except while its stream is being captured into a
+ * graph: then it returns K3X_E_SHAPE, so a caller that captures prefill calls reserves
+ * first.  Growing never frees the old buffers (a graph recorded over them stays valid);
+ * they are released with the layer.  No counterpart in the reference (k3_moe_scratch,
+ * k3.h:574, sizes the caller's scratch instead). */
+int  k3x_moe_layer_reserve(k3x_moe_layer *L, int max_T);
+
 /* Read expert e back from the device in the reference's row-major layout (host
  * buffers sized as in k3x_expert_q).  For checking and for handing experts back. */
 int  k3x_moe_layer_read_expert(const k3x_moe_layer *L, int e, unsigned char *p1,

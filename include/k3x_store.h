@@ -99,6 +99,12 @@ int64_t k3x_store_expert_load(const k3x_store *s, const k3x_expert_ref *r, unsig
  * into a buffer the supplier owns and points the k3x_expert_q into it (valid until the
  * next get).  k3x_store_src_fetches() counts the reads. */
 int  k3x_store_src_create(k3x_store *s, k3x_expert_src **out);
+/* The same supplier for a layer whose experts are gate/up [moe_inter][width] and down
+ * [width][moe_inter] (width: the latent width, or hidden): get() fails, so the layer
+ * counts a drop, for an expert of any other shape instead of handing out arrays shorter
+ * than the upload reads.  (The plain supplier checks only that an expert's three
+ * matrices agree with one another.) */
+int  k3x_store_src_create_for(k3x_store *s, int moe_inter, int width, k3x_expert_src **out);
 void k3x_store_src_destroy(k3x_expert_src *src);
 long k3x_store_src_fetches(const k3x_expert_src *src);
 

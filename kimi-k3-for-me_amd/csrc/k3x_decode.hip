@@ -761,7 +761,9 @@ __device__ void k2_shared(const K2Args &a, float *lds, int rt)
 // call).  Next come the shared expert's workgroups, which need no routing and stream
 // meanwhile; then the routed ones, which wait for the flag.  Workgroups are dispatched
 // in order, so workgroup 0 is resident before any routed one waits, and it waits on
-// nothing.  The wait is still bounded (wait_ticks of the 100 MHz clock, by default 50 ms,
+// nothing.  The flag is stored with release semantics and read by a relaxed spin followed
+// by an acquire fence, both at agent scope, so the routing's visibility rests on the
+// memory model.  The wait is still bounded (wait_ticks of the 100 MHz clock, by default 50 ms,
 // far above the selection's few microseconds): a workgroup that gives up sets the error
 // word (k3x_moe_layer_check reports it) and leaves without touching the expert weights.
 
@@ -781,8 +783,10 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
         ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        // release at agent scope: every store of the routing (all waves', ordered before
+        // this one by the barrier) is visible to a workgroup that acquires the flag
         if (threadIdx.x == 0 && a.publish)
-            __hip_atomic_store(a.ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     if ((int)blockIdx.x <= a.n_sh) {
@@ -816,6 +820,9 @@ __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
             }
             __builtin_amdgcn_s_sleep(2);
         }
+        // the relaxed spin read the released flag: this acquire fence makes the routing
+        // stored before it visible (one cache invalidation, not one per spin)
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         s_go = go;
     }
     __syncthreads();

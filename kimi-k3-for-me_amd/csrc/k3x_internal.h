@@ -53,6 +53,7 @@ extern "C" {
 #define K3X_STAGE_MAX    65536   /* bytes of activation fragments a workgroup stages in LDS */
 #define K3X_MAX_TOPK     64      /* K3_MAX_TOPK, k3.h:857-864 */
 #define K3X_ROUTE_WAIT_DEFAULT 5000000ull  /* 50 ms at 100 MHz: decode's bound on the wait */
+#define K3X_PF_CHUNK     4096    /* prefill: most tokens per pipeline run */
 /* byte sizes of the tiled formats */
 static inline size_t k3x_fp4_tile_bytes(int K)
 {
@@ -74,10 +75,17 @@ typedef struct k3x_route {
 } k3x_route;
 
 /* prefill working buffers (one allocation), sized for cap_T tokens per pipeline run */
+#define K3X_PF_RETIRED 24      /* earlier prefill allocations kept until the layer ends */
 typedef struct k3x_prefill_buf {
     int       cap_T;
     void     *base;
     size_t    bytes;
+    /* allocations replaced by a larger one: a HIP graph recorded over them may still be
+     * replayed, so they stay allocated until the layer is destroyed (growth at least
+     * doubles the capacity, so there are few) */
+    void     *retired[K3X_PF_RETIRED];
+    int       nretired;
+    size_t    retired_bytes;
     uint16_t *xhl;          /* [T][H/8][2][8] bf16 hi/lo activation rows            */
     float    *score, *choice; /* [T][E]                                             */
     int      *idx;          /* [T][K]                                                */
@@ -182,7 +190,18 @@ int k3x_dev_decode(struct k3x_moe_layer *L, float *out, const void *x, int x_dty
                    void *stream);
 int k3x_dev_prefill(struct k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                     const float *resid, int *idx, float *wt, void *stream);
-int k3x_pf_reserve(struct k3x_moe_layer *L, int T);   /* k3x_moe.c */
+/* prefill working buffers for runs of min(T, the chunk) tokens; refuses to grow while
+ * `stream` is being captured (k3x_moe.c) */
+int k3x_pf_reserve(struct k3x_moe_layer *L, int T, void *stream);
+/* tokens per prefill pipeline run: at most K3X_PF_CHUNK, and the widest activation
+ * planes of a run (T*K rows) stay under 1 GiB so 32-bit buffer offsets hold */
+static inline int k3x_pf_chunk_tokens(const struct k3x_moe_layer *L)
+{
+    size_t wide = (size_t)(L->cfg.hidden > L->cfg.moe_inter ? L->cfg.hidden : L->cfg.moe_inter);
+    if ((size_t)L->XL > wide) wide = (size_t)L->XL;
+    size_t chunk = ((size_t)1 << 30) / ((size_t)L->cfg.topk * wide * 4);
+    return chunk < 1 ? 1 : (chunk > K3X_PF_CHUNK ? K3X_PF_CHUNK : (int)chunk);
+}
 /* trunk products Y[t*ldy + o] = W[o] . X[t*ldx] over a tiled bf16 W [out][in]: T <= 8
  * (GEMV on the matrix cores) and any T (hi/lo planes into `planes`, T*in*4 bytes, then
  * the dense GEMM) */

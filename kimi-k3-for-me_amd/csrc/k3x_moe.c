@@ -141,6 +141,7 @@ static void layer_free(k3x_moe_layer *L)
                  L->ldown, L->lup, L->lnw, L->zB, L->accL, L->latB};
     for (size_t i = 0; i < sizeof p / sizeof p[0]; i++)
         if (p[i]) hipFree(p[i]);
+    for (int i = 0; i < L->pf.nretired; i++) hipFree(L->pf.retired[i]);
     if (L->slot_dev) hipFree(L->slot_dev);
     if (L->c_dbuf) hipFree(L->c_dbuf);
     if (L->c_hbuf) hipHostFree(L->c_hbuf);
@@ -159,7 +160,18 @@ void k3x_moe_layer_destroy(k3x_moe_layer *L)
     layer_free(L);
 }
 
-size_t k3x_moe_layer_bytes(const k3x_moe_layer *L) { return L ? L->bytes + L->pf.bytes : 0; }
+size_t k3x_moe_layer_bytes(const k3x_moe_layer *L)
+{
+    return L ? L->bytes + L->pf.bytes + L->pf.retired_bytes : 0;
+}
+
+int k3x_moe_layer_reserve(k3x_moe_layer *L, int max_T)
+{
+    if (!L || max_T < 0) return K3X_E_ARG;
+    if (max_T <= L->tdec || L->nslot) return 0;
+    if (hipSetDevice(L->device) != hipSuccess) return K3X_E_HIP;
+    return k3x_pf_reserve(L, max_T, NULL);
+}
 
 static int new_layer_slots(const k3x_cfg *c, int device, int nslot, k3x_moe_layer **out);
 
@@ -597,12 +609,27 @@ fail:
     return rc;
 }
 
-/* Prefill working buffers for T tokens per pipeline run: one allocation, carved into
- * 256-byte-aligned regions; grown (never shrunk) when a larger T arrives. */
-int k3x_pf_reserve(k3x_moe_layer *L, int T)
+/* Prefill working buffers for min(T, the chunk) tokens per pipeline run: one
+ * allocation, carved into 256-byte-aligned regions.  Grown, to at least twice the old
+ * capacity, when a larger T arrives; the old allocation is not freed (a graph recorded
+ * over it may still be replayed) but kept until the layer is destroyed.  Growing
+ * allocates, so it is refused while `stream` is being captured: a caller that captures
+ * prefill calls reserves first (k3x_moe_layer_reserve). */
+int k3x_pf_reserve(k3x_moe_layer *L, int T, void *stream)
 {
     k3x_prefill_buf *B = &L->pf;
+    const int chunk = k3x_pf_chunk_tokens(L);
+    if (T > chunk) T = chunk;
     if (T <= B->cap_T) return 0;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) return K3X_E_HIP;
+    if (cs != hipStreamCaptureStatusNone) {
+        fprintf(stderr, "k3x: prefill of %d tokens needs its buffers reserved before capture "
+                        "(k3x_moe_layer_reserve); %d reserved\n", T, B->cap_T);
+        return K3X_E_SHAPE;
+    }
+    if (B->nretired == K3X_PF_RETIRED) return K3X_E_NOMEM;
+    if (B->base && T < 2 * B->cap_T) T = 2 * B->cap_T < chunk ? 2 * B->cap_T : chunk;
     const k3x_cfg *c = &L->cfg;
     const size_t E = (size_t)c->n_experts, K = (size_t)c->topk,
                  I = (size_t)c->moe_inter, SI = (size_t)L->SI, t = (size_t)T;
@@ -640,8 +667,8 @@ int k3x_pf_reserve(k3x_moe_layer *L, int T)
     if (hipSetDevice(L->device) != hipSuccess) return K3X_E_HIP;
     if (hipMalloc(&base, total) != hipSuccess) return K3X_E_NOMEM;
     if (B->base) {
-        if (hipDeviceSynchronize() != hipSuccess) { hipFree(base); return K3X_E_HIP; }
-        hipFree(B->base);
+        B->retired[B->nretired++] = B->base;
+        B->retired_bytes += B->bytes;
     }
     char *p = (char *)base;
     B->base = base; B->bytes = total; B->cap_T = T;
@@ -756,7 +783,10 @@ static int host_call(k3x_moe_layer *L, float *out, const float *x, int T, int *i
         float *dwt = (float *)((char *)didx + ((nr + 255) & ~(size_t)255));
         HIPCHK(hipMemcpy(dx, x, n, hipMemcpyHostToDevice));
         RCCHK(k3x_moe_forward(L, (float *)L->h_dev_out, dx, K3X_F32, T, NULL, didx, dwt, NULL));
-        HIPCHK(hipDeviceSynchronize());
+        /* synchronises, then reports (and clears) a decode workgroup that gave up its
+         * bounded wait: that call's output is not valid, and the caller has no other way
+         * to learn of it */
+        RCCHK(k3x_moe_layer_check(L));
         HIPCHK(hipMemcpy(out, L->h_dev_out, n, hipMemcpyDeviceToHost));
         if (idx) {
             const size_t last = (size_t)(T - 1) * c->topk;
@@ -984,7 +1014,7 @@ int k3x_stack_create(k3x_moe_layer *const *layers, const float *const *norm_w, i
     HIPCHK(hipStreamCreateWithFlags(&S->cap, hipStreamNonBlocking));
     /* every allocation a call can make happens here, never while recording */
     if (max_T > K3X_DECODE_MAX_T)
-        for (int l = 0; l < n_layers; l++) RCCHK(k3x_pf_reserve(layers[l], max_T));
+        for (int l = 0; l < n_layers; l++) RCCHK(k3x_pf_reserve(layers[l], max_T, NULL));
     *out = S;
     return 0;
 fail:

@@ -22,7 +22,6 @@
 #include <string.h>
 
 #define PF_NT 256
-#define PF_CHUNK 4096          // tokens per pipeline run
 
 // ------------------------------------------------------------------ split
 // Activation planes, the GEMMs' B source: x [T][H] (bf16 or fp32, rows ldx elements
@@ -1059,19 +1058,15 @@ static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     return launch_ok();
 }
 
-// Prefill: the pipeline over chunks of up to PF_CHUNK tokens.  Each token's result
+// Prefill: the pipeline over chunks of up to K3X_PF_CHUNK tokens.  Each token's result
 // depends only on its own routing, so the chunking changes no result.
 extern "C" int k3x_dev_prefill(k3x_moe_layer *L, float *out, const void *x, int x_dtype,
                                int T, const float *resid, int *idx, float *wt, void *stream)
 {
     const int H = L->cfg.hidden, K = L->cfg.topk;
     const size_t es = (x_dtype == K3X_BF16) ? 2 : 4;
-    // activation planes of one chunk stay under 1 GiB, so 32-bit buffer offsets hold
-    size_t wide = (size_t)(H > L->cfg.moe_inter ? H : L->cfg.moe_inter);
-    if ((size_t)L->XL > wide) wide = (size_t)L->XL;
-    int chunk = (int)(((size_t)1 << 30) / ((size_t)K * wide * 4));
-    chunk = chunk < 1 ? 1 : (chunk > PF_CHUNK ? PF_CHUNK : chunk);
-    int rc = k3x_pf_reserve(L, T < chunk ? T : chunk);
+    const int chunk = k3x_pf_chunk_tokens(L);
+    int rc = k3x_pf_reserve(L, T, stream);
     if (rc) return rc;
     for (int t0 = 0; t0 < T; t0 += chunk) {
         const int n = T - t0 < chunk ? T - t0 : chunk;

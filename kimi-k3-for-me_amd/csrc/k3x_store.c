@@ -334,11 +334,15 @@ static int scan_shard(k3x_store *s, int shard)
                 }
             }
             if (!have_dt || !have_shape || !have_off || b0 < 0 || b1 < b0) goto bad;
-            int64_t numel = 1;
-            for (int d = 0; d < t.ndim; d++) numel *= t.shape[d];
-            t.off = data0 + b0;
+            /* every product and sum checked: a crafted header must not wrap around */
+            int64_t numel = 1, want = 0, end = 0;
+            int ovf = 0;
+            for (int d = 0; d < t.ndim; d++) ovf |= __builtin_mul_overflow(numel, t.shape[d], &numel);
+            ovf |= __builtin_mul_overflow(numel, (int64_t)dtype_size(t.dtype), &want);
+            ovf |= __builtin_add_overflow(data0, b0, &t.off);
             t.nbytes = b1 - b0;
-            if (numel * dtype_size(t.dtype) != t.nbytes || t.off + t.nbytes > s->fsize[shard]) {
+            ovf |= __builtin_add_overflow(t.off, t.nbytes, &end);
+            if (ovf || want != t.nbytes || end > s->fsize[shard]) {
                 fprintf(stderr, "k3x_store: %s: %s has %lld bytes for its shape or leaves the file\n",
                         s->path[shard], name, (long long)t.nbytes);
                 goto out;
@@ -551,13 +555,33 @@ typedef struct {
     unsigned char *buf;
     int64_t        cap;
     long           fetches;
+    int            inter, width;  /* the layer's expert shape, or 0: not checked */
 } store_src;
+
+/* w1/w3 [I][X] and w2 [X][I] with one scale per 32 elements, for some I and X (or the
+ * supplier's I and X when it has them) */
+static int expert_shape_ok(const store_src *ss, const k3x_expert_ref *r)
+{
+    const int I = ss->inter ? ss->inter : r->m[0].rows;
+    const int X = ss->width ? ss->width : r->m[0].pcols * 2;
+    const int rows[3] = {I, X, I}, width[3] = {X, I, X};
+    for (int i = 0; i < 3; i++)
+        if (r->m[i].rows != rows[i] || r->m[i].pcols * 2 != width[i] ||
+            r->m[i].scols * 32 != width[i])
+            return 0;
+    return 1;
+}
 
 static int store_get(k3x_expert_src *self, int layer, int expert, k3x_expert_q *q)
 {
     store_src *ss = (store_src *)self;
     k3x_expert_ref r;
     if (k3x_store_expert_ref(ss->s, layer, expert, &r)) return -1;
+    if (!expert_shape_ok(ss, &r)) {
+        fprintf(stderr, "k3x_store: layer %d expert %d has matrices of the wrong shape\n",
+                layer, expert);
+        return -1;
+    }
     if (r.nbytes > ss->cap) {
         unsigned char *nb = (unsigned char *)realloc(ss->buf, (size_t)r.nbytes);
         if (!nb) return -1;
@@ -572,16 +596,23 @@ static int store_get(k3x_expert_src *self, int layer, int expert, k3x_expert_q *
     return 0;
 }
 
-int k3x_store_src_create(k3x_store *s, k3x_expert_src **out)
+int k3x_store_src_create_for(k3x_store *s, int moe_inter, int width, k3x_expert_src **out)
 {
-    if (!s || !out) return K3X_E_ARG;
+    if (!s || !out || moe_inter < 0 || width < 0) return K3X_E_ARG;
     store_src *ss = (store_src *)calloc(1, sizeof *ss);
     if (!ss) return K3X_E_NOMEM;
     ss->base.get = store_get;
     ss->base.ctx = ss;
     ss->s = s;
+    ss->inter = moe_inter;
+    ss->width = width;
     *out = &ss->base;
     return 0;
+}
+
+int k3x_store_src_create(k3x_store *s, k3x_expert_src **out)
+{
+    return k3x_store_src_create_for(s, 0, 0, out);
 }
 
 void k3x_store_src_destroy(k3x_expert_src *src)

@@ -32,11 +32,12 @@ EXPORTS = [
     "k3x_synth_normal_f32", "k3x_synth_normal_bf16", "k3x_moe_layer_set_timing",
     "k3x_moe_layer_last_ms", "k3x_stack_create", "k3x_stack_forward", "k3x_stack_destroy",
     "k3x_moe_layer_check", "k3x_moe_layer_set_route_wait",
-    "k3x_attn_res", "k3x_moe_half",
+    "k3x_attn_res", "k3x_moe_half", "k3x_moe_layer_reserve",
     # include/k3x_store.h
     "k3x_store_open", "k3x_store_close", "k3x_store_count", "k3x_store_shards",
     "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
-    "k3x_store_src_create", "k3x_store_src_destroy", "k3x_store_src_fetches",
+    "k3x_store_src_create", "k3x_store_src_create_for", "k3x_store_src_destroy",
+    "k3x_store_src_fetches",
     "k3x_moe_layer_create_from_store",
     "k3x_moe_layer_create_cached",
     "k3x_cache_stats",
@@ -124,6 +125,7 @@ def lib():
         L.k3x_moe_layer_bytes.argtypes = [vp]
         L.k3x_moe_layer_bytes.restype = C.c_size_t
         L.k3x_moe_layer_read_expert.argtypes = [vp, i] + [vp] * 6
+        L.k3x_moe_layer_reserve.argtypes = [vp, i]
         L.k3x_moe_forward.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
         L.k3x_rmsnorm.argtypes = [vp, vp, vp, i, i, f, vp]
         L.k3x_moe.argtypes = [vp, vp, vp, i, vp, vp]
@@ -156,6 +158,7 @@ def lib():
         L.k3x_store_expert_load.argtypes = [vp, C.POINTER(ExpertRef), vp]
         L.k3x_store_expert_load.restype = C.c_int64
         L.k3x_store_src_create.argtypes = [vp, C.POINTER(vp)]
+        L.k3x_store_src_create_for.argtypes = [vp, i, i, C.POINTER(vp)]
         L.k3x_store_src_destroy.argtypes = [vp]
         L.k3x_store_src_destroy.restype = None
         L.k3x_store_src_fetches.argtypes = [vp]
@@ -327,6 +330,10 @@ class MoELayer:
     # -- calls --------------------------------------------------------------------
     def nbytes(self):
         return lib().k3x_moe_layer_bytes(self.h)
+
+    def reserve(self, max_T):
+        """Prefill buffers for calls of up to max_T tokens (needed before capturing one)."""
+        _check(lib().k3x_moe_layer_reserve(self.h, max_T), "k3x_moe_layer_reserve")
 
     def forward(self, out_ptr, x_ptr, T, x_dtype=K3X_F32, resid_ptr=0, idx_ptr=0, wt_ptr=0,
                 stream=0):

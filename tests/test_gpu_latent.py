@@ -170,6 +170,23 @@ def test_k3_decode_b2(torch, k3x, k3_layer):
     assert err < TOL
 
 
+@pytest.mark.parametrize("T", [3, 4, 6])
+def test_k3_decode_multi(torch, k3x, k3_layer, T):
+    """T = 3..5 take the down products over parts without the activation sets in LDS,
+    T = 6..7 take k3_down2 with parts; both feed k4_latent_norm (the aggregates past the
+    LDS) at this shape."""
+    say(f"case: K3 shape, T={T} in one call vs oracle")
+    L, layer = k3_layer
+    x = L.x(T, bf16=True, stream_sub=80 + T)
+    o, idx, wt, _ = L.oracle_moe(x)
+    out, i2, w2 = dev_forward(torch, k3x, layer, x, bf16=True)
+    assert np.array_equal(i2, idx)
+    np.testing.assert_allclose(w2, wt, rtol=1e-6)
+    err = synth.rel_l2(out, o)
+    say(f"  unique experts {len(np.unique(idx))}, rel_l2={err:.3e}")
+    assert err < TOL
+
+
 def test_k3_decode_b8(torch, k3x, k3_layer):
     say("case: K3 shape, T=8 in one call vs oracle")
     L, layer = k3_layer

@@ -164,3 +164,53 @@ def test_prefill_graph_replays(torch, k3x):
         assert synth.rel_l2(go.cpu().numpy(), o) < TOL
     layer.check()
     layer.close()
+
+
+def test_prefill_graph_survives_growth(torch, k3x):
+    """A prefill graph recorded over the layer's buffers stays valid after an eager call
+    with more tokens grows them (the old buffers are kept, not freed), and a capture that
+    would need to grow them is refused with K3X_E_SHAPE instead of allocating inside the
+    capture."""
+    say("case: prefill T=24 graph, eager T=100 grows the buffers, replay still exact")
+    L = synth.tiny(seed=36)
+    layer = bank_layer(k3x, L)
+    layer.reserve(24)
+    T, H, K = 24, L.H, L.K
+    xd = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        layer.forward(out.data_ptr(), xd.data_ptr(), T, k3x.K3X_F32, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    n0 = layer.nbytes()
+    xb = L.x(100, bf16=False, stream_sub=30)
+    ob, ib, _ = dev_forward(torch, k3x, layer, xb)       # grows the prefill buffers
+    assert layer.nbytes() > n0
+    o, i_ref, _, _ = L.oracle_moe(xb)
+    assert np.array_equal(ib, i_ref) and synth.rel_l2(ob, o) < TOL
+    for r in range(2):
+        x = L.x(T, bf16=False, stream_sub=31 + r)
+        xd.copy_(torch.from_numpy(x))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        o, _, _, _ = L.oracle_moe(x)
+        say(f"  replay {r}")
+        assert synth.rel_l2(out.cpu().numpy(), o) < TOL
+    # capturing a call that needs more than is reserved is refused
+    big = layer.nbytes()
+    T2 = 4000
+    x2 = torch.zeros((T2, H), dtype=torch.float32, device="cuda")
+    o2 = torch.empty((T2, H), dtype=torch.float32, device="cuda")
+    s2 = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with pytest.raises(k3x.K3XError) as ei:
+        g2 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g2, stream=s2):
+            layer.forward(o2.data_ptr(), x2.data_ptr(), T2, k3x.K3X_F32, stream=s2.cuda_stream)
+    assert ei.value.status == -2
+    torch.cuda.synchronize()
+    assert layer.nbytes() == big
+    layer.check()
+    layer.close()

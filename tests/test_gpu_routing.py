@@ -86,3 +86,24 @@ def test_wait_bound_reports_and_recovers(torch, k3x):
     assert np.array_equal(i2, idx)
     assert synth.rel_l2(out2, o) < TOL
     layer.close()
+
+
+def test_wait_bound_host_call_returns_wait(torch, k3x):
+    """The host-pointer drop-in (k3x_moe, behind the reference binding's k3_moe_gpu) must
+    not return success on a call whose routed workgroups gave up waiting: with the flag
+    withheld it raises K3X_E_WAIT, and the next call with the defaults is valid."""
+    say("case: host-pointer k3x_moe with the decode wait forced, then restored")
+    L = synth.tiny(seed=35)
+    layer = bank_layer(k3x, L)
+    x = L.x(3, bf16=False, stream_sub=13)
+    o, idx, _, _ = L.oracle_moe(x)
+    layer.set_route_wait(200, publish=False)
+    with pytest.raises(k3x.K3XError) as ei:
+        layer.moe(x)
+    assert ei.value.status == -7, str(ei.value)
+    layer.check()                           # the host call cleared the word
+    layer.set_route_wait(5000000, publish=True)
+    out, il, _ = layer.moe(x)
+    assert np.array_equal(il, idx[-1])
+    assert synth.rel_l2(out, o) < TOL
+    layer.close()

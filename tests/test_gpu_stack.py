@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 import synth
-from gpu_util import bank_layer, say
+from gpu_util import bank_layer, say, synth_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -101,4 +101,66 @@ def test_stack_rejects_too_many_tokens(torch, k3x, tiny_stack):
     h = torch.zeros((3, Ls[0].H), dtype=torch.float32, device="cuda")
     with pytest.raises(k3x.K3XError):
         S.forward(h.data_ptr(), 3, torch.cuda.current_stream().cuda_stream)
+    S.close()
+
+
+# ------------------------------------------------------------------ the full width
+@pytest.fixture(scope="module")
+def full_stack(torch, k3x):
+    """Three full-size K2-class layers (H 7168, 384 experts top-8, I 2048; seeds 10 + l),
+    generated on the device, with RMSNorm weights 1 + N(0, 0.1)."""
+    say("building 3 full-size synthetic layers (27 GB) on the device")
+    Ls = [synth.full(seed=10 + l, layer=l) for l in range(3)]
+    rng = np.random.default_rng(6)
+    norms = [(1 + 0.1 * rng.standard_normal(Ls[0].H)).astype(np.float32) for _ in Ls]
+    layers = [synth_layer(k3x, L) for L in Ls]
+    nd = [torch.from_numpy(w).cuda() for w in norms]
+    yield Ls, norms, layers, nd
+    for l in layers:
+        l.close()
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_full_stack_graph_vs_oracle(torch, k3x, full_stack, T):
+    """The stacked-layer sequence at the benchmark's full width (H 7168): the first call
+    records the graph, the next two replay it on new tokens; every call against the oracle
+    applying ko_rmsnorm, the oracle MoE of each layer and the residual add on the host
+    (k3_decoder_layer_core's MoE half, k3_ops.c:2559-2589)."""
+    Ls, norms, layers, nd = full_stack
+    S = k3x.Stack(layers, [w.data_ptr() for w in nd], eps=EPS, max_T=8)
+    h = torch.empty((T, Ls[0].H), dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream()
+    for r in range(3):
+        say(f"case: 3 full-size layers stacked, T={T}, call {r} ({'record' if r == 0 else 'replay'})")
+        h0 = Ls[0].x(T, bf16=False, stream_sub=110 + 10 * T + r) * 2.0
+        h.copy_(torch.from_numpy(h0).cuda())
+        S.forward(h.data_ptr(), T, s.cuda_stream)
+        torch.cuda.synchronize()
+        for l in layers:
+            l.check()
+        want = oracle_stack(Ls, norms, h0)
+        err = synth.rel_l2(h.cpu().numpy(), want)
+        say(f"  rel_l2={err:.3e}")
+        assert err < TOL
+    S.close()
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_full_stack_fused_norm_bitwise(torch, k3x, full_stack, T):
+    """At H 7168 the RMSNorm worked out inside the router launch gives bitwise what a
+    separate k3x_rmsnorm followed by the MoE call gives, layer after layer."""
+    say(f"case: 3 full-size layers, T={T}, fused norm vs k3x_rmsnorm + forward, bitwise")
+    Ls, norms, layers, nd = full_stack
+    S = k3x.Stack(layers, [w.data_ptr() for w in nd], eps=EPS, max_T=8)
+    h0 = Ls[0].x(T, bf16=False, stream_sub=150 + T) * 3.0
+    h = torch.from_numpy(h0).cuda()
+    s = torch.cuda.current_stream().cuda_stream
+    S.forward(h.data_ptr(), T, s)
+    ref = torch.from_numpy(h0).cuda()
+    y = torch.empty_like(ref)
+    for L, w in zip(layers, nd):
+        k3x.rmsnorm(y.data_ptr(), ref.data_ptr(), w.data_ptr(), Ls[0].H, T, EPS, s)
+        L.forward(ref.data_ptr(), y.data_ptr(), T, k3x.K3X_F32, ref.data_ptr(), 0, 0, s)
+    torch.cuda.synchronize()
+    assert torch.equal(h, ref)
     S.close()

@@ -195,6 +195,52 @@ def test_malformed_shards_rejected(k3x, tmp_path, what):
         k3x.Store(str(tmp_path))
 
 
+@pytest.mark.parametrize("shape,nbytes", [([2 ** 62 + 1], 4), ([2 ** 61 + 1, 2], 8)])
+def test_overflowing_shape_rejected(k3x, tmp_path, shape, nbytes):
+    """A header whose element count times 4 wraps around to the tensor's byte count
+    (2^64 + nbytes) is rejected, not indexed."""
+    raw = np.zeros(nbytes, np.uint8).tobytes()
+    write_shard(tmp_path / "m.safetensors", [("a", "F32", tuple(shape), raw)])
+    with pytest.raises(k3x.K3XError):
+        k3x.Store(str(tmp_path))
+
+
+def test_huge_offsets_rejected(k3x, tmp_path):
+    """data_offsets near 2^63 (their sum with the header length would wrap) are rejected."""
+    p = tmp_path / "m.safetensors"
+    big = 2 ** 63 - 4
+    hdr = ('{"a": {"dtype": "U8", "shape": [4], "data_offsets": [%d, %d]}}' % (big, big + 4)).encode()
+    if big + 4 >= 2 ** 63:
+        hdr = ('{"a": {"dtype": "U8", "shape": [4], "data_offsets": [%d, %d]}}'
+               % (big - 4, big)).encode()
+    p.write_bytes(struct.pack("<Q", len(hdr)) + hdr + b"\0" * 4)
+    with pytest.raises(k3x.K3XError):
+        k3x.Store(str(tmp_path))
+
+
+def test_supplier_refuses_wrong_shaped_expert(k3x, tmp_path):
+    """A supplier made for a layer's expert shape fails get() (a drop for the layer) for an
+    expert of another shape, instead of pointing the upload at short arrays; the plain
+    supplier still refuses an expert whose three matrices disagree."""
+    rng = np.random.default_rng(4)
+    write_shard(tmp_path / "m.safetensors",
+                expert_tensors(0, 0, small_expert(rng, I=64, X=128)) +
+                expert_tensors(0, 1, small_expert(rng, I=32, X=128)))
+    st = k3x.Store(str(tmp_path))
+    q = k3x.ExpertQ()
+    h = C.c_void_p()
+    assert k3x.lib().k3x_store_src_create_for(st.h, 64, 128, C.byref(h)) == 0
+    src = C.cast(h, C.POINTER(k3x.ExpertSrc))
+    assert src.contents.get(src, 0, 0, C.byref(q)) == 0
+    assert src.contents.get(src, 0, 1, C.byref(q)) != 0        # 32 rows, not 64
+    k3x.lib().k3x_store_src_destroy(h)
+    assert k3x.lib().k3x_store_src_create(st.h, C.byref(h)) == 0
+    src = C.cast(h, C.POINTER(k3x.ExpertSrc))
+    assert src.contents.get(src, 0, 1, C.byref(q)) == 0        # consistent on its own
+    k3x.lib().k3x_store_src_destroy(h)
+    st.close()
+
+
 def test_empty_directory_rejected(k3x, tmp_path):
     with pytest.raises(k3x.K3XError):
         k3x.Store(str(tmp_path))

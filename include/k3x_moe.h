@@ -133,6 +133,13 @@ size_t k3x_moe_layer_bytes(const k3x_moe_layer *L);
  * k3.h:574, sizes the caller's scratch instead). */
 int  k3x_moe_layer_reserve(k3x_moe_layer *L, int max_T);
 
+/* Matrix m (0 gate, 1 up, 2 down) of expert e, as the device's product kernels
+ * dequantise it, into out (host, fp32 row-major [rows][width]): k3_mxfp4_dequant
+ * (k3.h:866-867, k3_ops.c:3778-3808) of the layer's resident bytes, E8M0 byte 255 -> 0,
+ * byte 0 -> 2^-127.  Every such value is a bf16 (or an infinity), so this is what the
+ * matrix cores multiply.  For checking. */
+int  k3x_moe_layer_dequant(const k3x_moe_layer *L, int e, int m, float *out);
+
 /* Read expert e back from the device in the reference's row-major layout (host
  * buffers sized as in k3x_expert_q).  For checking and for handing experts back. */
 int  k3x_moe_layer_read_expert(const k3x_moe_layer *L, int e, unsigned char *p1,
@@ -163,9 +170,12 @@ int  k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float e
 /* ---- host-pointer drop-ins with the reference's semantics ---------------------------
  * k3x_moe mirrors k3_moe (k3.h:629-630): out [T][hidden] overwritten, x [T][hidden]
  * fp32, idx/wt [topk] left holding the LAST token's routing.  k3x_moe_prefill mirrors
- * k3_moe_prefill (k3.h:636-637); on this device both run the same pipeline, whose
- * results do not depend on how tokens are grouped into calls.  Synchronous.  The
- * reference's scratch argument has no counterpart: working memory lives in the layer. */
+ * k3_moe_prefill (k3.h:636-637): with T > 1 it leaves idx/wt untouched, as the
+ * reference's batched path does (k3_ops.c:2018-2053); with T == 1 it writes them as
+ * k3_moe.  On this device both run the same pipeline, whose results do not depend on how
+ * tokens are grouped into calls.  Synchronous; K3X_E_WAIT when a decode workgroup gave
+ * up its wait (the output is then not valid).  The reference's scratch argument has no
+ * counterpart: working memory lives in the layer. */
 int  k3x_moe(k3x_moe_layer *L, float *out, const float *x, int T, int *idx, float *wt);
 int  k3x_moe_prefill(k3x_moe_layer *L, float *out, const float *x, int T, int *idx,
                      float *wt);

@@ -181,6 +181,8 @@ int k3x_dev_tile_fp4(uint8_t *dst, const uint8_t *packed, const uint8_t *scales,
 int k3x_dev_tile_bf16(uint16_t *dst, const uint16_t *src, int R, int K, void *stream);
 int k3x_dev_untile_fp4(uint8_t *packed, uint8_t *scales, const uint8_t *src, int R, int K,
                        void *stream);
+int k3x_dev_dequant_fp4(float *out, const uint8_t *src, int R, int K, int exact,
+                        void *stream);
 int k3x_dev_synth_fp4(uint8_t *dst, int R, int K, uint64_t code_key, uint64_t scale_key,
                       int lo, int hi, void *stream);
 /* norm_w != NULL: the MoE input is the RMSNorm of x (fp32, 16-byte aligned, hidden <=

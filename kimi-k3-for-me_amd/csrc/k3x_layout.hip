@@ -59,6 +59,41 @@ __global__ void untile_fp4_kernel(uint8_t *packed, uint8_t *scales, const uint8_
     }
 }
 
+// A tiled fp4 matrix dequantised to fp32 rows (k3_mxfp4_dequant, k3_ops.c:3778-3808)
+// through the product kernels' own conversion: each lane's dword t of quad j goes
+// through dq8 (scale bytes 1..252) or, when the layer takes the exact path for this
+// matrix, dq8_exact, and the 8 bf16 results are widened.
+__global__ void dequant_fp4_kernel(float *out, const uint8_t *src, int R, int K, int exact)
+{
+    const int nQ = K >> 7, nS = (nQ + 3) >> 2, tiles = R >> 4;
+    const size_t tb = fp4_tile_bytes(K);
+    const long total = (long)tiles * nS * 64;
+    for (long f = blockIdx.x * (long)blockDim.x + threadIdx.x; f < total;
+         f += (long)gridDim.x * blockDim.x) {
+        const int l = f & 63;
+        const int S = (f >> 6) % nS;
+        const int rt = (int)((f >> 6) / nS);
+        const int m = l & 15, kq = l >> 4;
+        const int row = rt * 16 + m;
+        const int nq = min(4, nQ - 4 * S);
+        const uint8_t *so = src + (size_t)rt * tb + (size_t)S * 4352;
+        const uint32_t sw = *(const uint32_t *)(so + 4096 + l * 4);
+        for (int j = 0; j < nq; j++) {
+            const u32x4 c = *(const u32x4 *)(so + j * 1024 + l * 16);
+            const uint32_t sb = (sw >> (8 * j)) & 255u;
+            for (int t = 0; t < 4; t++) {
+                const bf16x8 v = exact ? dq8_exact(c[t], sb) : dq8(c[t], e8m0_scale(sb));
+                const u32x4 u = __builtin_bit_cast(u32x4, v);
+                float *d = out + (size_t)row * K + 128 * (4 * S + j) + 32 * kq + 8 * t;
+                for (int i = 0; i < 4; i++) {
+                    d[2 * i] = bf2f(u[i] & 0xFFFFu);
+                    d[2 * i + 1] = bf2f(u[i] >> 16);
+                }
+            }
+        }
+    }
+}
+
 __global__ void tile_bf16_kernel(uint16_t *dst, const uint16_t *src, int R, int K)
 {
     const int nQ = K >> 7;
@@ -217,6 +252,15 @@ extern "C" int k3x_dev_untile_fp4(uint8_t *packed, uint8_t *scales, const uint8_
     const long total = (long)(R >> 4) * (((K >> 7) + 3) >> 2) * 64;
     hipLaunchKernelGGL(untile_fp4_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
                        (hipStream_t)stream, packed, scales, src, R, K);
+    return launch_ok();
+}
+
+extern "C" int k3x_dev_dequant_fp4(float *out, const uint8_t *src, int R, int K, int exact,
+                                   void *stream)
+{
+    const long total = (long)(R >> 4) * (((K >> 7) + 3) >> 2) * 64;
+    hipLaunchKernelGGL(dequant_fp4_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+                       (hipStream_t)stream, out, src, R, K, exact);
     return launch_ok();
 }
 

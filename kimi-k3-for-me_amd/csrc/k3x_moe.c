@@ -609,6 +609,27 @@ fail:
     return rc;
 }
 
+int k3x_moe_layer_dequant(const k3x_moe_layer *L, int e, int m, float *out)
+{
+    if (!L || !out || e < 0 || e >= L->cfg.n_experts || m < 0 || m > 2) return K3X_E_ARG;
+    if (L->nslot && L->slot_of[e] < 0) return K3X_E_ARG;        /* not resident */
+    const int X = L->XL, I = L->cfg.moe_inter;
+    const int R = m == 2 ? X : I, K = m == 2 ? I : X;
+    const size_t off[3] = {L->gate_off, L->up_off, L->down_off};
+    const uint8_t *src = L->experts + (size_t)(L->nslot ? L->slot_of[e] : e) * L->expert_bytes +
+                         off[m];
+    float *d = NULL;
+    int rc = 0;
+    HIPCHK(hipSetDevice(L->device));
+    HIPCHK(hipMalloc((void **)&d, (size_t)R * K * 4));
+    RCCHK(k3x_dev_dequant_fp4(d, src, R, K, (L->special >> m) & 1, NULL));
+    HIPCHK(hipDeviceSynchronize());
+    HIPCHK(hipMemcpy(out, d, (size_t)R * K * 4, hipMemcpyDeviceToHost));
+fail:
+    if (d) hipFree(d);
+    return rc;
+}
+
 /* Prefill working buffers for min(T, the chunk) tokens per pipeline run: one
  * allocation, carved into 256-byte-aligned regions.  Grown, to at least twice the old
  * capacity, when a larger T arrives; the old allocation is not freed (a graph recorded
@@ -757,10 +778,14 @@ int k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float ep
     return k3x_dev_rmsnorm(y, x, w, n, T, eps, stream);
 }
 
-/* Host-pointer drop-ins: stage x and out through device buffers held by the layer. */
+/* Host-pointer drop-ins: stage x and out through device buffers held by the layer.
+ * idx/wt receive the last token's routing, except for a prefill call of several tokens,
+ * which leaves them as they were: k3_moe_prefill's batched path routes into buffers of
+ * its own (k3_ops.c:2018-2053) and only its one-token fallback, k3_moe, writes them. */
 static int host_call(k3x_moe_layer *L, float *out, const float *x, int T, int *idx,
-                     float *wt)
+                     float *wt, int prefill)
 {
+    if (prefill && T > 1) idx = NULL, wt = NULL;
     if (!L || (T > 0 && (!out || !x))) return K3X_E_ARG;
     if (T <= 0) return T < 0 ? K3X_E_ARG : 0;
     const k3x_cfg *c = &L->cfg;
@@ -803,13 +828,13 @@ fail:
 
 int k3x_moe(k3x_moe_layer *L, float *out, const float *x, int T, int *idx, float *wt)
 {
-    return host_call(L, out, x, T, idx, wt);
+    return host_call(L, out, x, T, idx, wt, 0);
 }
 
 int k3x_moe_prefill(k3x_moe_layer *L, float *out, const float *x, int T, int *idx,
                     float *wt)
 {
-    return host_call(L, out, x, T, idx, wt);
+    return host_call(L, out, x, T, idx, wt, 1);
 }
 
 /* ---------------------------------------------------------------- timing ---- */

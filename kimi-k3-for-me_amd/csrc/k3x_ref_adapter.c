@@ -3,13 +3,20 @@
  * reference's k3.h); it is not part of libk3x.so.
  *
  * k3_moe_gpu / k3_moe_prefill_gpu have the signatures of k3_moe / k3_moe_prefill
- * (include/k3/k3.h:629-637).  On first use of a layer they upload it through the
- * layer's own K3ExpertSrc (k3.h:521-544) and keep the handle; afterwards every call runs
- * on the GPU.  Accepted: bf16 trunk weights (wdt == K3_WBF16) and a streamed expert
- * source, not a cache-only draft.  A layer with latent == hidden whose down/up are
- * identity matrices (the K2-class emulation) is uploaded without projections; any other
- * latent layer with its down/up projections, latent norm and SiTU betas.  Anything else
- * returns -1 so the caller keeps the CPU path (k3_ops.c:1862, :2008).
+ * (include/k3/k3.h:629-637) and return 0 when the call ran on the GPU, -1 when the
+ * caller must run its CPU path instead (k3_ops.c:1862, :2008).  On first use of a layer
+ * they upload it through the layer's own K3ExpertSrc (k3.h:521-544) and keep the handle;
+ * afterwards every call runs on the GPU.
+ *
+ * Accepted: bf16 trunk weights (wdt == K3_WBF16) and a streamed expert source, not a
+ * cache-only draft (k3.h:568: its routing depends on the host cache's residency, which
+ * the device copy of the layer does not share).  A layer with latent == hidden whose
+ * down/up are identity matrices (the K2-class emulation) is uploaded without
+ * projections; any other latent layer with its down/up projections, latent norm and
+ * SiTU betas.  An expert that cannot be fetched at upload counts in k3_expert_drops (as
+ * k3_ops.c:1916-1926 counts a per-token drop) and the call returns -1; a device call
+ * that fails (k3x status, including a decode workgroup that gave up its wait) returns -1
+ * without counting a drop.
  */
 #include "k3.h"
 #include "k3x_moe.h"
@@ -19,8 +26,16 @@
 
 #define K3X_ADAPTER_MAX_LAYERS 128
 
-static k3x_moe_layer *g_layers[K3X_ADAPTER_MAX_LAYERS];
-static const K3MoeW *g_owner[K3X_ADAPTER_MAX_LAYERS];
+/* A layer is reused while the K3MoeW it was built from is the same object with the
+ * same weights and shape; anything else uploads it again. */
+typedef struct {
+    k3x_moe_layer *L;
+    const K3MoeW  *w;
+    const void    *gate, *sh1, *down, *src;
+    int            hidden, n_experts, topk, moe_inter, latent;
+} adapter_slot;
+
+static adapter_slot g_slots[K3X_ADAPTER_MAX_LAYERS];
 
 typedef struct {
     k3x_expert_src  base;   /* first member: the callback casts back */
@@ -31,6 +46,7 @@ static int adapter_get(k3x_expert_src *self, int layer, int expert, k3x_expert_q
 {
     adapter_src *a = (adapter_src *)self;
     K3ExpertQ q;
+    memset(&q, 0, sizeof q);
     if (a->src->get(a->src, layer, expert, &q) != 0) return -1;
     out->p1 = q.p1; out->s1 = q.s1;
     out->p3 = q.p3; out->s3 = q.s3;
@@ -55,9 +71,18 @@ static int is_identity_bf16(const uint16_t *m, int n)
     return 1;
 }
 
+static int slot_matches(const adapter_slot *s, const K3MoeW *w, const K3Cfg *c)
+{
+    return s->L && s->w == w && s->gate == (const void *)w->gate && s->sh1 == w->sh1 &&
+           s->down == w->down && s->src == (const void *)w->src && s->hidden == c->hidden &&
+           s->n_experts == c->n_experts && s->topk == c->topk &&
+           s->moe_inter == c->moe_inter && s->latent == c->latent;
+}
+
 static k3x_moe_layer *layer_for(const K3MoeW *w, const K3Cfg *c)
 {
-    if (g_layers[w->layer] && g_owner[w->layer] == w) return g_layers[w->layer];
+    adapter_slot *s = &g_slots[w->layer];
+    if (slot_matches(s, w, c)) return s->L;
     k3x_cfg kc;
     memset(&kc, 0, sizeof kc);
     kc.hidden = c->hidden;
@@ -101,28 +126,60 @@ static k3x_moe_layer *layer_for(const K3MoeW *w, const K3Cfg *c)
         fprintf(stderr, "k3x: layer %d upload failed: %s\n", w->layer, k3x_strerror(rc));
         return NULL;
     }
-    if (g_layers[w->layer]) k3x_moe_layer_destroy(g_layers[w->layer]);
-    g_layers[w->layer] = L;
-    g_owner[w->layer] = w;
+    if (s->L) k3x_moe_layer_destroy(s->L);
+    s->L = L;
+    s->w = w;
+    s->gate = w->gate; s->sh1 = w->sh1; s->down = w->down; s->src = w->src;
+    s->hidden = c->hidden; s->n_experts = c->n_experts; s->topk = c->topk;
+    s->moe_inter = c->moe_inter; s->latent = c->latent;
     return L;
+}
+
+static int run(int prefill, float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
+               int T, int *idx, float *wt)
+{
+    if (!gpu_form(w, c)) return -1;
+    k3x_moe_layer *L = layer_for(w, c);
+    if (!L) return -1;
+    const int rc = prefill ? k3x_moe_prefill(L, out, x, T, idx, wt)
+                           : k3x_moe(L, out, x, T, idx, wt);
+    if (rc) {
+        fprintf(stderr, "k3x: layer %d call failed: %s\n", w->layer, k3x_strerror(rc));
+        return -1;
+    }
+    return 0;
 }
 
 int k3_moe_gpu(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T, int *idx,
                float *wt, float *scratch)
 {
     (void)scratch;
-    if (!gpu_form(w, c)) return -1;
-    k3x_moe_layer *L = layer_for(w, c);
-    if (!L) return -1;
-    return k3x_moe(L, out, x, T, idx, wt) == K3X_OK ? 0 : -1;
+    return run(0, out, x, w, c, T, idx, wt);
 }
 
 int k3_moe_prefill_gpu(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T,
                        int *idx, float *wt, float *scratch)
 {
     (void)scratch;
-    if (!gpu_form(w, c)) return -1;
-    k3x_moe_layer *L = layer_for(w, c);
-    if (!L) return -1;
-    return k3x_moe_prefill(L, out, x, T, idx, wt) == K3X_OK ? 0 : -1;
+    return run(1, out, x, w, c, T, idx, wt);
+}
+
+/* k3_moe_scratch's counterpart (k3.h:574): the device path keeps its working memory in
+ * the layer and needs no caller scratch, so 0 floats.  A caller still sizes the scratch
+ * it passes with k3_moe_scratch, for the CPU path it runs when a call returns -1. */
+size_t k3_moe_gpu_scratch(const K3Cfg *c, int T)
+{
+    (void)c;
+    (void)T;
+    return 0;
+}
+
+/* Drops every uploaded layer (a model's teardown, or before its weights are replaced in
+ * place). */
+void k3_moe_gpu_release(void)
+{
+    for (int l = 0; l < K3X_ADAPTER_MAX_LAYERS; l++) {
+        if (g_slots[l].L) k3x_moe_layer_destroy(g_slots[l].L);
+        memset(&g_slots[l], 0, sizeof g_slots[l]);
+    }
 }

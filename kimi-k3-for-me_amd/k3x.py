@@ -32,7 +32,7 @@ EXPORTS = [
     "k3x_synth_normal_f32", "k3x_synth_normal_bf16", "k3x_moe_layer_set_timing",
     "k3x_moe_layer_last_ms", "k3x_stack_create", "k3x_stack_forward", "k3x_stack_destroy",
     "k3x_moe_layer_check", "k3x_moe_layer_set_route_wait",
-    "k3x_attn_res", "k3x_moe_half", "k3x_moe_layer_reserve",
+    "k3x_attn_res", "k3x_moe_half", "k3x_moe_layer_reserve", "k3x_moe_layer_dequant",
     # include/k3x_store.h
     "k3x_store_open", "k3x_store_close", "k3x_store_count", "k3x_store_shards",
     "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
@@ -126,6 +126,7 @@ def lib():
         L.k3x_moe_layer_bytes.restype = C.c_size_t
         L.k3x_moe_layer_read_expert.argtypes = [vp, i] + [vp] * 6
         L.k3x_moe_layer_reserve.argtypes = [vp, i]
+        L.k3x_moe_layer_dequant.argtypes = [vp, i, i, vp]
         L.k3x_moe_forward.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
         L.k3x_rmsnorm.argtypes = [vp, vp, vp, i, i, f, vp]
         L.k3x_moe.argtypes = [vp, vp, vp, i, vp, vp]
@@ -366,6 +367,16 @@ class MoELayer:
                                                           ("p1", "s1", "p3", "s3", "p2", "s2")]),
                "k3x_moe_layer_read_expert")
         return d
+
+    def dequant(self, e, m):
+        """Matrix m (0 gate, 1 up, 2 down) of expert e as the device dequantises it
+        (fp32 [rows][width])."""
+        X = self.cfg.latent if self.cfg.latent > 0 else self.cfg.hidden
+        I = self.cfg.moe_inter
+        out = np.empty((X, I) if m == 2 else (I, X), np.float32)
+        _check(lib().k3x_moe_layer_dequant(self.h, e, m, out.ctypes.data),
+               "k3x_moe_layer_dequant")
+        return out
 
     def moe_half(self, h, pref, blocks, maxb, nb, fold, post_norm, eps, T, hin, stream=0):
         """The MoE half of a decoder layer on device pointers (k3x_moe_half)."""

@@ -25,6 +25,7 @@ typedef struct {
     const drv_expert *bank;
     int               n;
     const int        *fail;    /* optional [n]: 1 makes get() fail (a forced drop) */
+    const int        *res;     /* optional [n]: resident() reports res[e] != 0 */
     long              gets;
 } drv_src;
 
@@ -39,6 +40,19 @@ static int drv_get(K3ExpertSrc *self, int layer, int e, K3ExpertQ *out)
     out->p3 = s->bank[e].p3; out->s3 = s->bank[e].s3;
     out->p2 = s->bank[e].p2; out->s2 = s->bank[e].s2;
     return 0;
+}
+
+static int drv_resident(K3ExpertSrc *self, int layer, int e, K3ExpertQ *out)
+{
+    drv_src *s = (drv_src *)self;
+    (void)layer;
+    if (e < 0 || e >= s->n || (s->res && !s->res[e])) return 0;
+    if (out) {
+        out->p1 = s->bank[e].p1; out->s1 = s->bank[e].s1;
+        out->p3 = s->bank[e].p3; out->s3 = s->bank[e].s3;
+        out->p2 = s->bank[e].p2; out->s2 = s->bank[e].s2;
+    }
+    return 1;
 }
 
 static uint16_t *identity_bf16(int n)
@@ -212,4 +226,90 @@ long refdrv_k2_tokens(float *out, const float *x, int T, int H, int E, int K, in
     }
     free(gu); free(act); free(edn); free(sgu); free(sdn);
     return 0;
+}
+
+#ifdef K3X_ADAPTER
+/* The reference-side binding of libk3x (kimi-k3-for-me_amd/csrc/k3x_ref_adapter.c). */
+int    k3_moe_gpu(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T,
+                  int *idx, float *wt, float *scratch);
+int    k3_moe_prefill_gpu(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T,
+                          int *idx, float *wt, float *scratch);
+size_t k3_moe_gpu_scratch(const K3Cfg *c, int T);
+void   k3_moe_gpu_release(void);
+
+void refdrv_gpu_release(void) { k3_moe_gpu_release(); }
+#endif
+
+/* One call of the layer in general form through a chosen entry point: mode 0 k3_moe,
+ * 1 k3_moe_prefill (the reference's CPU path), 2 k3_moe_gpu, 3 k3_moe_prefill_gpu (the
+ * GPU binding, in the library built with it; elsewhere *status = -2).  cache_only sets
+ * K3MoeW.cache_only with a resident() reporting res[e] != 0 (every expert when res is
+ * NULL); trunk_f32 tags the trunk matrices fp32.  *status receives the GPU entry's
+ * return (0 or -1; 0 for the CPU modes), *gets the supplier's get() calls.  Returns the
+ * change in k3_expert_drops. */
+long refdrv_moe_entry(float *out, const float *x, int T, const drv_cfg *dc, const float *gate,
+                      const float *bias, const drv_expert *bank, const int *fail,
+                      const void *down, const void *up, const float *lnorm, const void *sh1,
+                      const void *sh3, const void *sh2, int trunk_f32, int mode,
+                      int cache_only, const int *res, int *idx, float *wt, int *status,
+                      long *gets)
+{
+    K3Cfg c;
+    memset(&c, 0, sizeof c);
+    c.hidden = dc->hidden;
+    c.latent = dc->latent;
+    c.n_experts = dc->n_experts;
+    c.topk = dc->topk;
+    c.moe_inter = dc->inter;
+    c.n_shared = dc->n_shared;
+    c.routed_scale = dc->routed_scale;
+    c.moe_renorm = dc->renorm;
+    c.latent_norm = dc->latent_norm;
+    c.situ_b1 = dc->situ_b1;
+    c.situ_b2 = dc->situ_b2;
+    c.rms_eps = dc->rms_eps;
+
+    static drv_src s;          /* outlives the call: the binding keeps the layer */
+    memset(&s, 0, sizeof s);
+    s.src.get = drv_get;
+    s.src.resident = drv_resident;
+    s.bank = bank;
+    s.n = dc->n_experts;
+    s.fail = fail;
+    s.res = res;
+
+    static K3MoeW w;
+    memset(&w, 0, sizeof w);
+    w.gate = gate;
+    w.bias = bias;
+    w.down = down;
+    w.up = up;
+    w.latent_norm = lnorm;
+    w.sh1 = sh1;
+    w.sh3 = sh3;
+    w.sh2 = sh2;
+    w.wdt = trunk_f32 ? K3_WF32 : K3_WBF16;
+    w.src = &s.src;
+    w.layer = 0;
+    w.cache_only = cache_only;
+
+    *status = 0;
+    const long d0 = k3_expert_drops;
+    if (mode <= 1) {
+        float *scratch = (float *)malloc(k3_moe_scratch(&c, T) * sizeof(float));
+        if (!scratch) return -1000000;
+        if (mode == 1) k3_moe_prefill(out, x, &w, &c, T, idx, wt, scratch);
+        else           k3_moe(out, x, &w, &c, T, idx, wt, scratch);
+        free(scratch);
+    } else {
+#ifdef K3X_ADAPTER
+        if (k3_moe_gpu_scratch(&c, T) != 0) { *status = -3; return 0; }
+        *status = mode == 3 ? k3_moe_prefill_gpu(out, x, &w, &c, T, idx, wt, NULL)
+                            : k3_moe_gpu(out, x, &w, &c, T, idx, wt, NULL);
+#else
+        *status = -2;
+#endif
+    }
+    if (gets) *gets = s.gets;
+    return k3_expert_drops - d0;
 }

@@ -162,6 +162,19 @@ int  k3x_moe_layer_read_expert(const k3x_moe_layer *L, int e, unsigned char *p1,
 int  k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                      const float *resid, int *idx, float *wt, void *stream);
 
+/* The prefill path of k3x_moe_forward (8 < T tokens) for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops): same arguments and
+ * results (bit for bit), but the working buffers come from a static device array of
+ * 64 MiB that each GPU holds until the process ends, instead of the layer's buffers that
+ * k3x_moe_forward may grow.  Calls no allocating routine.  One call's buffers must fit
+ * the array (about 590 KB per token at the K2 shape: T <= 111 there); larger T, or
+ * T <= 8 (k3x_moe_forward's decode path allocates nothing), returns K3X_E_SHAPE.  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU race, so order
+ * them on one stream.  No counterpart in the reference; for callers that cannot
+ * allocate. */
+int  k3x_moe_prefill_noalloc(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
+                             const float *resid, int *idx, float *wt, void *stream);
+
 /* RMSNorm of T rows on the device: y = w * x * inv, inv = 1/sqrt(mean(x^2) + eps)
  * (k3_rmsnorm, k3_ops.c:132-140).  x, y fp32 [T][n], w fp32 [n], device pointers. */
 int  k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,

@@ -54,6 +54,7 @@ extern "C" {
 #define K3X_MAX_TOPK     64      /* K3_MAX_TOPK, k3.h:857-864 */
 #define K3X_ROUTE_WAIT_DEFAULT 5000000ull  /* 50 ms at 100 MHz: decode's bound on the wait */
 #define K3X_PF_CHUNK     4096    /* prefill: most tokens per pipeline run */
+#define K3X_NOALLOC_BYTES (64u << 20)  /* the no-allocation prefill's static device array */
 /* byte sizes of the tiled formats */
 static inline size_t k3x_fp4_tile_bytes(int K)
 {
@@ -195,6 +196,13 @@ int k3x_dev_prefill(struct k3x_moe_layer *L, float *out, const void *x, int x_dt
 /* prefill working buffers for runs of min(T, the chunk) tokens; refuses to grow while
  * `stream` is being captured (k3x_moe.c) */
 int k3x_pf_reserve(struct k3x_moe_layer *L, int T, void *stream);
+/* The prefill buffers of runs of T tokens carved from p (256-byte aligned regions) into
+ * B; returns the bytes they take (with p or B NULL, only that) (k3x_moe.c) */
+size_t k3x_pf_layout(const struct k3x_moe_layer *L, int T, char *p, k3x_prefill_buf *B);
+/* the prefill pipeline over one run of T <= the chunk tokens with its working buffers
+ * in the static device array, never allocating (k3x_prefill.hip) */
+int k3x_dev_prefill_noalloc(struct k3x_moe_layer *L, float *out, const void *x, int x_dtype,
+                            int T, const float *resid, int *idx, float *wt, void *stream);
 /* tokens per prefill pipeline run: at most K3X_PF_CHUNK, and the widest activation
  * planes of a run (T*K rows) stay under 1 GiB so 32-bit buffer offsets hold */
 static inline int k3x_pf_chunk_tokens(const struct k3x_moe_layer *L)

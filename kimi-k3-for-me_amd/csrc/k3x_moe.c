@@ -651,11 +651,29 @@ int k3x_pf_reserve(k3x_moe_layer *L, int T, void *stream)
     }
     if (B->nretired == K3X_PF_RETIRED) return K3X_E_NOMEM;
     if (B->base && T < 2 * B->cap_T) T = 2 * B->cap_T < chunk ? 2 * B->cap_T : chunk;
+    const size_t total = k3x_pf_layout(L, T, NULL, NULL);
+    void *base = NULL;
+    if (hipSetDevice(L->device) != hipSuccess) return K3X_E_HIP;
+    if (hipMalloc(&base, total) != hipSuccess) return K3X_E_NOMEM;
+    if (B->base) {
+        B->retired[B->nretired++] = B->base;
+        B->retired_bytes += B->bytes;
+    }
+    k3x_pf_layout(L, T, (char *)base, B);
+    B->base = base;
+    return 0;
+}
+
+size_t k3x_pf_layout(const k3x_moe_layer *L, int T, char *p, k3x_prefill_buf *B)
+{
     const k3x_cfg *c = &L->cfg;
     const size_t E = (size_t)c->n_experts, K = (size_t)c->topk,
                  I = (size_t)c->moe_inter, SI = (size_t)L->SI, t = (size_t)T;
     /* rows of the widest activation (hidden, or a latent width above it) */
     const size_t H = (size_t)(L->XL > c->hidden ? L->XL : c->hidden), X = (size_t)L->XL;
+    /* GEMM tiles: at most ceil(rows/64) row blocks by (T*K/16 + E + 1) column blocks */
+    const int ndg = (int)(((I + 63) / 64) * (t * K / 16 + E + 1));
+    const int ndd = (int)(((H + 63) / 64) * (t * K / 16 + E + 1));
     const size_t sz[] = {
         t * H * 4,                 /* xhl     */
         t * E * 4, t * E * 4,      /* score, choice */
@@ -669,30 +687,17 @@ int k3x_pf_reserve(k3x_moe_layer *L, int T, void *stream)
         t * K * H * 4,             /* xp      */
         L->lat ? t * X * 4 : 256,  /* zf      */
         L->lat ? t * X * 4 : 256,  /* zhl     */
-        0, 0,                      /* desc_gu, desc_dn (set below) */
+        (size_t)ndg * 16,          /* desc_gu */
+        (size_t)ndd * 16,          /* desc_dn */
     };
     enum { N = sizeof sz / sizeof sz[0] };
-    /* GEMM tiles: at most ceil(rows/64) row blocks by (T*K/16 + E + 1) column blocks */
-    const int ndg = (int)(((I + 63) / 64) * (t * K / 16 + E + 1));
-    const int ndd = (int)(((H + 63) / 64) * (t * K / 16 + E + 1));
-    size_t szs[N];
-    for (int i = 0; i < N; i++) szs[i] = sz[i];
-    szs[N - 2] = (size_t)ndg * 16;
-    szs[N - 1] = (size_t)ndd * 16;
     size_t off[N], total = 0;
     for (int i = 0; i < N; i++) {
         off[i] = total;
-        total += (szs[i] + 255) & ~(size_t)255;
+        total += (sz[i] + 255) & ~(size_t)255;
     }
-    void *base = NULL;
-    if (hipSetDevice(L->device) != hipSuccess) return K3X_E_HIP;
-    if (hipMalloc(&base, total) != hipSuccess) return K3X_E_NOMEM;
-    if (B->base) {
-        B->retired[B->nretired++] = B->base;
-        B->retired_bytes += B->bytes;
-    }
-    char *p = (char *)base;
-    B->base = base; B->bytes = total; B->cap_T = T;
+    if (!p || !B) return total;
+    B->bytes = total; B->cap_T = T;
     B->xhl = (uint16_t *)(p + off[0]);
     B->score = (float *)(p + off[1]);   B->choice = (float *)(p + off[2]);
     B->idx = (int *)(p + off[3]);       B->wt = (float *)(p + off[4]);
@@ -707,7 +712,7 @@ int k3x_pf_reserve(k3x_moe_layer *L, int T, void *stream)
     B->zf = (float *)(p + off[17]);     B->zhl = (uint16_t *)(p + off[18]);
     B->desc_gu = p + off[19]; B->ndesc_gu = ndg;
     B->desc_dn = p + off[20]; B->ndesc_dn = ndd;
-    return 0;
+    return total;
 }
 
 /* ---------------------------------------------------------------- forward ---- */
@@ -723,6 +728,17 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
         return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, NULL, 0.0f, stream);
     if (L->nslot) return K3X_E_ARG;           /* a cached layer serves decode calls only */
     return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
+}
+
+int k3x_moe_prefill_noalloc(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
+                            const float *resid, int *idx, float *wt, void *stream)
+{
+    if (!L || !out || !x || T < 0 || (x_dtype != K3X_F32 && x_dtype != K3X_BF16)) return K3X_E_ARG;
+    if (((uintptr_t)x & 15) || ((uintptr_t)out & 15) || ((uintptr_t)resid & 15)) return K3X_E_ARG;
+    if ((idx == NULL) != (wt == NULL)) return K3X_E_ARG;
+    if (L->nslot) return K3X_E_ARG;           /* a cached layer serves decode calls only */
+    if (T <= L->tdec) return K3X_E_SHAPE;     /* the decode path: k3x_moe_forward */
+    return k3x_dev_prefill_noalloc(L, out, x, x_dtype, T, resid, idx, wt, stream);
 }
 
 int k3x_moe_layer_set_route_wait(k3x_moe_layer *L, unsigned long long ticks, int publish)

@@ -19,7 +19,10 @@
 #include "k3x_device.h"
 #include "k3x_topk.h"
 
+#include <stdio.h>
 #include <string.h>
+
+#include <mutex>
 
 #define PF_NT 256
 
@@ -881,11 +884,11 @@ static void launch_dn(const PfGemmArgs &a, unsigned grid, hipStream_t s)
 
 static inline unsigned round8(size_t n) { return (unsigned)((n + 7) & ~(size_t)7); }
 
-static int pf_chunk(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
-                    const float *resid, int *uidx, float *uwt, hipStream_t s)
+static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, const void *x,
+                    int x_dtype, int T, const float *resid, int *uidx, float *uwt,
+                    hipStream_t s)
 {
     const k3x_cfg *c = &L->cfg;
-    k3x_prefill_buf *B = &L->pf;
     const int H = c->hidden, E = c->n_experts, K = c->topk, I = c->moe_inter, SI = L->SI;
     const int X = L->XL;                                 // the routed experts' width
     const int TK = T * K;
@@ -1070,12 +1073,63 @@ extern "C" int k3x_dev_prefill(k3x_moe_layer *L, float *out, const void *x, int 
     if (rc) return rc;
     for (int t0 = 0; t0 < T; t0 += chunk) {
         const int n = T - t0 < chunk ? T - t0 : chunk;
-        rc = pf_chunk(L, out + (size_t)t0 * H, (const char *)x + (size_t)t0 * H * es, x_dtype, n,
+        rc = pf_chunk(L, &L->pf, out + (size_t)t0 * H, (const char *)x + (size_t)t0 * H * es, x_dtype, n,
                       resid ? resid + (size_t)t0 * H : NULL, idx ? idx + (size_t)t0 * K : NULL,
                       wt ? wt + (size_t)t0 * K : NULL, (hipStream_t)stream);
         if (rc) return rc;
     }
     return 0;
+}
+
+// ------------------------------------------------------------------ without allocation
+// The prefill pipeline for callers that cannot allocate (graph capture, serving loops):
+// its working buffers come from this static device array instead of the layer's. Each
+// device holds its own copy at its own address, found once per device by
+// hipGetSymbolAddress; host code uses that address, never the array's name.  Every call
+// on a device shares the device's copy (calls that overlap on one device race); no
+// kernel needs it to start cleared (the histogram is zeroed by pf_split each run).
+static __device__ __align__(256) uint8_t scratch[K3X_NOALLOC_BYTES];
+
+#define K3X_MAX_DEVICES 64
+static void *g_scratch[K3X_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+static void *scratch_ptr(int device)
+{
+    if (device < 0 || device >= K3X_MAX_DEVICES) return NULL;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[device]) {
+        void *p = NULL;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fprintf(stderr, "k3x: hipGetSymbolAddress(scratch) on device %d failed: %s\n",
+                    device, hipGetErrorString(e));
+            return NULL;
+        }
+        g_scratch[device] = p;
+    }
+    return g_scratch[device];
+}
+
+extern "C" int k3x_dev_prefill_noalloc(k3x_moe_layer *L, float *out, const void *x, int x_dtype,
+                                       int T, const float *resid, int *idx, float *wt,
+                                       void *stream)
+{
+    const int chunk = k3x_pf_chunk_tokens(L);
+    const size_t need = k3x_pf_layout(L, T, NULL, NULL);
+    if (T > chunk || need > K3X_NOALLOC_BYTES) {
+        fprintf(stderr, "k3x: a prefill of %d tokens needs %zu bytes of working memory; the "
+                        "static array holds %u (and one run at most %d tokens)\n",
+                T, need, K3X_NOALLOC_BYTES, chunk);
+        return K3X_E_SHAPE;
+    }
+    if (hipSetDevice(L->device) != hipSuccess) return K3X_E_HIP;
+    void *p = scratch_ptr(L->device);
+    if (!p) return K3X_E_HIP;
+    k3x_prefill_buf B;
+    memset(&B, 0, sizeof B);
+    k3x_pf_layout(L, T, (char *)p, &B);
+    return pf_chunk(L, &B, out, x, x_dtype, T, resid, idx, wt, (hipStream_t)stream);
 }
 
 // ------------------------------------------------------------------ trunk products

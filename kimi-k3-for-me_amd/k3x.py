@@ -33,6 +33,7 @@ EXPORTS = [
     "k3x_moe_layer_last_ms", "k3x_stack_create", "k3x_stack_forward", "k3x_stack_destroy",
     "k3x_moe_layer_check", "k3x_moe_layer_set_route_wait",
     "k3x_attn_res", "k3x_moe_half", "k3x_moe_layer_reserve", "k3x_moe_layer_dequant",
+    "k3x_moe_prefill_noalloc",
     # include/k3x_store.h
     "k3x_store_open", "k3x_store_close", "k3x_store_count", "k3x_store_shards",
     "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
@@ -128,6 +129,7 @@ def lib():
         L.k3x_moe_layer_reserve.argtypes = [vp, i]
         L.k3x_moe_layer_dequant.argtypes = [vp, i, i, vp]
         L.k3x_moe_forward.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
+        L.k3x_moe_prefill_noalloc.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
         L.k3x_rmsnorm.argtypes = [vp, vp, vp, i, i, f, vp]
         L.k3x_moe.argtypes = [vp, vp, vp, i, vp, vp]
         L.k3x_moe_prefill.argtypes = [vp, vp, vp, i, vp, vp]
@@ -342,6 +344,15 @@ class MoELayer:
         _check(lib().k3x_moe_forward(self.h, out_ptr, x_ptr, x_dtype, T, resid_ptr or None,
                                      idx_ptr or None, wt_ptr or None, stream or None),
                "k3x_moe_forward")
+
+    def prefill_noalloc(self, out_ptr, x_ptr, T, x_dtype=K3X_F32, resid_ptr=0, idx_ptr=0,
+                        wt_ptr=0, stream=0):
+        """k3x_moe_prefill_noalloc: the prefill path with its buffers in the static device
+        array (device pointers; asynchronous on `stream`)."""
+        _check(lib().k3x_moe_prefill_noalloc(self.h, out_ptr, x_ptr, x_dtype, T,
+                                             resid_ptr or None, idx_ptr or None,
+                                             wt_ptr or None, stream or None),
+               "k3x_moe_prefill_noalloc")
 
     def moe(self, x, prefill=False):
         """Host call with k3_moe semantics: returns (out, idx_last, wt_last)."""

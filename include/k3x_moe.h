@@ -281,6 +281,13 @@ int  k3x_moe_layer_check(k3x_moe_layer *L);
  * so are not valid; restore with (5000000, 1).  No counterpart in the reference. */
 int  k3x_moe_layer_set_route_wait(k3x_moe_layer *L, unsigned long long ticks, int publish);
 int  k3x_moe_layer_set_timing(k3x_moe_layer *L, int on);
+/* Diagnostics (a layer created with K3X_TRACE=1 in the environment): per workgroup of
+ * decode kernel k (0 the router, 1 the gate/up products, 2 the down products, which is
+ * traced when it runs as one part) of the last decode call, three words: the workgroup
+ * index | XCD << 28 | hardware ids << 32, its start and its end (100 MHz clock).
+ * Returns the number of workgroups copied (0 without the trace).  No counterpart in the
+ * reference. */
+int  k3x_moe_layer_trace(k3x_moe_layer *L, int kernel, unsigned long long *out, int max_wg);
 int  k3x_moe_layer_last_ms(k3x_moe_layer *L, float *ms);
 
 #ifdef __cplusplus

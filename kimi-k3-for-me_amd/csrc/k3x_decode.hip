@@ -269,6 +269,30 @@ __device__ __forceinline__ void per_token(const float (&acc)[NV], int NC, int la
     if ((n & 1) == 0 && n < NC) f(4 * kq, n >> 1, v);
 }
 
+// ------------------------------------------------------------------ diagnostics
+// Optional per-workgroup trace (a layer made with K3X_TRACE=1): thread 0 writes
+// {workgroup | XCD << 28 | hardware ids << 32, start, end} (100 MHz clock) at rec.
+struct WgTrace {
+    unsigned long long *rec;       // [grid][3] for this launch, or NULL
+    uint64_t            t0;
+    __device__ __forceinline__ void start(unsigned long long *r)
+    {
+        rec = r;
+        if (rec && threadIdx.x == 0) t0 = __builtin_amdgcn_s_memrealtime();
+    }
+    __device__ __forceinline__ void end()
+    {
+        if (!rec || threadIdx.x != 0) return;
+        const uint32_t hw = __builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11));   // HW_ID
+        const uint32_t xcc = __builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11));  // XCC_ID
+        unsigned long long *p = rec + (size_t)blockIdx.x * 3;
+        p[0] = (unsigned long long)blockIdx.x | ((unsigned long long)hw << 32) |
+               ((unsigned long long)(xcc & 15) << 28);
+        p[1] = t0;
+        p[2] = __builtin_amdgcn_s_memrealtime();
+    }
+};
+
 // ------------------------------------------------------------------ selection
 struct KSArgs {
     const float   *score, *choice;
@@ -426,6 +450,7 @@ struct K1Args {
     int          XL;
     uint16_t    *zB;               // compact B set of z over whole super-quads of XL
     KSArgs       ks;
+    unsigned long long *trace;     // diagnostics, or NULL
 };
 
 #define RWAVES 4                     // waves per expert row in the router
@@ -472,7 +497,7 @@ __device__ void k1_norm_inv(const K1Args &a, float *lds, float *s_inv)
 // reference's single chain), then score = sigmoid((float)logit), choice = score + bias.
 // With a.norm_w, x[i] is the normalised nw[i] * x[i] * inv (float, the reference's order);
 // the expert's weights are in flight while the norm is worked out.
-__device__ void k1_router(const K1Args &a, float *lds, float *s_inv)
+__device__ void k1_router(const K1Args &a, float *lds, float *s_inv, bool bset)
 {
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int grp = wave / RWAVES, wq = wave % RWAVES;          // expert slot, quarter
@@ -499,6 +524,14 @@ __device__ void k1_router(const K1Args &a, float *lds, float *s_inv)
                 const int f = tl + RWAVES * WAVE * c;
                 nw[c] = f < nf4 ? *(const f32x4 *)(a.norm_w + 4 * f) : (f32x4){0.f, 0.f, 0.f, 0.f};
             }
+        }
+        if (bset && f0 == 0) {
+            // this workgroup's share of x's B set (of the normalised rows with norm_w),
+            // while the router's weights are in flight
+            const int nS = ((a.H >> 7) + 3) >> 2;
+            const int tid = threadIdx.x * a.n_rwg + blockIdx.x, nth = a.n_rwg * NT1;
+            x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS, tid, nth, a.norm_w,
+                      s_inv);
         }
 #pragma unroll
         for (int t = 0; t < K3X_DECODE_MAX_T; t++) {
@@ -662,16 +695,13 @@ __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
 {
     __shared__ float lds[(NT1 / WAVE - 1) * 8 * WAVE];
     __shared__ float s_inv[K3X_DECODE_MAX_T];
+    WgTrace tr;
+    tr.start(a.trace);
     if (blockIdx.x == 0 && threadIdx.x == 0) *a.ready = 0;
-    // the B set's entries dealt across the workgroups (a few per workgroup), converted
-    // before the router's weights are requested when no norm is needed
-    const int nS = ((a.H >> 7) + 3) >> 2;
-    const int tid = threadIdx.x * a.n_rwg + blockIdx.x, nth = a.n_rwg * NT1;
-    if (!a.norm_w)
-        x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS, tid, nth);
-    k1_router(a, lds, s_inv);
-    if (a.norm_w)
-        x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS, tid, nth, a.norm_w, s_inv);
+    // the B set's entries are dealt across the workgroups (a few per workgroup) and
+    // converted while the router's weights are in flight
+    k1_router(a, lds, s_inv, true);
+    tr.end();
 }
 
 // ------------------------------------------------------------------ K2
@@ -700,6 +730,7 @@ struct K2Args {
     const int     *slot;           // expert -> arena slot (expert cache), or NULL: identity
     int            sel_done;       // 1: the routing was published by an earlier launch
                                    // (k1_zdown): no selection here, no wait
+    unsigned long long *trace;     // diagnostics, or NULL
 };
 
 // Shared expert gate and up products for rows 16*rt .. +15 over the full K: four waves on
@@ -774,10 +805,23 @@ __device__ void k2_shared(const K2Args &a, float *lds, int rt)
 // workgroup when a tile has few super-quads (a narrow latent width), so that each wave
 // streams a run of items and the per-workgroup staging and waits are amortised.
 template <bool EXACT, bool LDSB, int NE>
+__device__ void k2_gateup_body(const K2Args &a, float *lds, int *s_go_p);
+
+template <bool EXACT, bool LDSB, int NE>
 __global__ void __launch_bounds__(NT) k2_gateup(K2Args a)
 {
     __shared__ float lds[(NT / WAVE - 1) * 8 * WAVE];
     __shared__ int s_go;
+    WgTrace tr;
+    tr.start(a.trace);
+    k2_gateup_body<EXACT, LDSB, NE>(a, lds, &s_go);
+    tr.end();
+}
+
+template <bool EXACT, bool LDSB, int NE>
+__device__ void k2_gateup_body(const K2Args &a, float *lds, int *s_go_p)
+{
+    int &s_go = *s_go_p;
     if (blockIdx.x == 0) {
         if (a.sel_done) return;
         ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true);
@@ -959,6 +1003,7 @@ struct K3Args {
                                    // upp*y .. upp*y + upp - 1 (the latent form's split)
     size_t         pstride;        // floats between parts' outputs (0: one part)
     const int     *slot;           // expert -> arena slot (expert cache), or NULL: identity
+    unsigned long long *trace;     // diagnostics, or NULL
 };
 
 // A bf16 quad of the shared down matrix with its B fragments (read from the shared
@@ -1045,6 +1090,8 @@ template <bool EXACT>
 __global__ void __launch_bounds__(NT3) k3_down(K3Args a)
 {
     __shared__ float lds[(NT3 / WAVE - 1) * 4 * WAVE];
+    WgTrace tr;
+    tr.start(a.trace);
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int nall = a.route->nu;
     const int u0 = (int)blockIdx.y * a.upp;
@@ -1068,6 +1115,7 @@ __global__ void __launch_bounds__(NT3) k3_down(K3Args a)
             out[o] = a.resid ? a.resid[o] + v[i] : v[i];
         }
     });
+    tr.end();
 }
 
 // Several tokens (K2 form): two 16-row tiles per workgroup, so that each B fragment read
@@ -1433,6 +1481,9 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     if (norm_w && (L->lat || x_dtype == K3X_BF16 || H > RCH * NT1 * 4 || ((uintptr_t)x & 15) ||
                    ((uintptr_t)norm_w & 15)))
         return K3X_E_ARG;
+    unsigned long long *trb = L->tr;
+    a1.trace = (trb && a1.n_rwg <= L->tr_cap) ? trb : NULL;
+    if (trb) L->tr_n[0] = a1.trace ? a1.n_rwg : 0;
     if ((rc = record(L, 0, s))) return rc;
     hipLaunchKernelGGL(k1_router_bset, dim3(a1.n_rwg), dim3(NT1), 0, s, a1);
     if ((rc = launch_ok())) return rc;
@@ -1456,6 +1507,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     }
 
     K2Args a2;
+    a2.trace = NULL;
     a2.ks = ks;
     a2.sel_done = L->lat;
     a2.route = L->route; a2.ready = &L->route->ready; a2.err = &L->route->err;
@@ -1498,7 +1550,10 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
         a2.sel_done = 1;
     }
     const bool ex2 = (L->special & 3) != 0;
-    k2_launch(ex2, dim3(1 + a2.n_sh + n_routed));
+    const int g2 = 1 + a2.n_sh + n_routed;
+    a2.trace = (trb && g2 <= L->tr_cap) ? trb + (size_t)L->tr_cap * 3 : NULL;
+    if (trb) L->tr_n[1] = a2.trace ? g2 : 0;
+    k2_launch(ex2, dim3(g2));
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, ev++, s))) return rc;
 
@@ -1511,6 +1566,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a3.sh_down = (L->SI > 0 && !L->lat) ? L->sh_down : NULL; a3.shB = L->shB; a3.SI = L->SI;
     a3.out = L->lat ? L->accL : out; a3.resid = L->lat ? NULL : resid;
     a3.T = T; a3.H = X; a3.I = I; a3.K = c->topk;
+    a3.trace = NULL;
     const uint32_t slot = (uint32_t)nSI * 1024u * NC;
     const size_t all = (size_t)T * c->topk * slot;
     a3.lds_bytes = slot <= STAGE_MAX ? (uint32_t)(all < STAGE_MAX ? all : (STAGE_MAX / slot) * slot) : 0u;
@@ -1536,7 +1592,14 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     }
     a3.pstride = parts > 1 ? (size_t)K3X_DECODE_MAX_T * X : 0;
     const size_t l3 = (size_t)a3.lds_bytes + a3.sh_lds;
-    if ((!L->lat && T >= 2 && X % 32 == 0) || lat2) {
+    const bool use2 = (!L->lat && T >= 2 && X % 32 == 0) || lat2;
+    if (trb) {
+        // k3_down's workgroups when they are one part (k3_down2 is not traced)
+        const bool on = parts == 1 && !use2 && X / 16 <= L->tr_cap;
+        a3.trace = on ? trb + (size_t)L->tr_cap * 6 : NULL;
+        L->tr_n[2] = on ? X / 16 : 0;
+    }
+    if (use2) {
         if (L->special & 4) hipLaunchKernelGGL(k3_down2<true>, dim3(X / 32, parts), dim3(NT3), 0, s, a3);
         else                hipLaunchKernelGGL(k3_down2<false>, dim3(X / 32, parts), dim3(NT3), 0, s, a3);
     } else if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(X / 16, parts), dim3(NT3), l3, s, a3);

@@ -142,6 +142,10 @@ struct k3x_moe_layer {
     float    *accL;               /* latent: [DECODE_PARTS][DECODE_MAX_T][XL] partial
                                      routed aggregates */
     uint16_t *latB;               /* latent: B set of the (normalised) aggregates */
+    /* diagnostics (K3X_TRACE=1 at creation): per-workgroup {id | ids, start, end} of the
+     * last decode call's k1, k2 and k3, tr_cap records each */
+    unsigned long long *tr;
+    int       tr_cap, tr_n[3];
     k3x_prefill_buf pf;
     size_t    bytes;
     /* decode: bound on the routed workgroups' wait for the published selection (ticks of

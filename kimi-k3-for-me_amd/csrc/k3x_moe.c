@@ -122,6 +122,14 @@ static int layer_alloc(k3x_moe_layer *L)
     }
     if (c->latent_norm) RCCHK(dmalloc((void **)&L->lnw, (size_t)L->XL * 4, b));
     if (hipMemset(L->route, 0, sizeof(k3x_route)) != hipSuccess) return K3X_E_HIP;
+    {
+        const char *tr = getenv("K3X_TRACE");
+        if (tr && tr[0] == '1') {
+            L->tr_cap = E + L->SI / 16 + 1 + K3X_DECODE_MAX_T * K * (I / 16) +
+                        K3X_DECODE_PARTS * (L->XL / 16);
+            RCCHK(dmalloc((void **)&L->tr, (size_t)3 * L->tr_cap * 24, b));
+        }
+    }
     /* B sets of 2*DECODE_MAX_T columns over whole super-quads (512 elements) */
     const size_t hs = (size_t)(H + 511) / 512 * 512, is = (size_t)(I + 511) / 512 * 512;
     RCCHK(dmalloc((void **)&L->xB, hs * 2 * K3X_DECODE_MAX_T * 2, b));
@@ -138,7 +146,7 @@ static void layer_free(k3x_moe_layer *L)
     void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shB,
                  L->score, L->choice, L->idx, L->wt, L->route,
                  L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out,
-                 L->ldown, L->lup, L->lnw, L->zB, L->accL, L->latB};
+                 L->ldown, L->lup, L->lnw, L->zB, L->accL, L->latB, L->tr};
     for (size_t i = 0; i < sizeof p / sizeof p[0]; i++)
         if (p[i]) hipFree(p[i]);
     for (int i = 0; i < L->pf.nretired; i++) hipFree(L->pf.retired[i]);
@@ -739,6 +747,18 @@ int k3x_moe_prefill_noalloc(k3x_moe_layer *L, float *out, const void *x, int x_d
     if (L->nslot) return K3X_E_ARG;           /* a cached layer serves decode calls only */
     if (T <= L->tdec) return K3X_E_SHAPE;     /* the decode path: k3x_moe_forward */
     return k3x_dev_prefill_noalloc(L, out, x, x_dtype, T, resid, idx, wt, stream);
+}
+
+int k3x_moe_layer_trace(k3x_moe_layer *L, int kernel, unsigned long long *out, int max_wg)
+{
+    if (!L || !out || kernel < 0 || kernel > 2 || max_wg < 0) return K3X_E_ARG;
+    if (!L->tr) return 0;
+    const int n = L->tr_n[kernel] < max_wg ? L->tr_n[kernel] : max_wg;
+    if (hipSetDevice(L->device) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(out, L->tr + (size_t)kernel * L->tr_cap * 3, (size_t)n * 24,
+                  hipMemcpyDeviceToHost) != hipSuccess)
+        return K3X_E_HIP;
+    return n;
 }
 
 int k3x_moe_layer_set_route_wait(k3x_moe_layer *L, unsigned long long ticks, int publish)

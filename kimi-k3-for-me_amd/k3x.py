@@ -33,7 +33,7 @@ EXPORTS = [
     "k3x_moe_layer_last_ms", "k3x_stack_create", "k3x_stack_forward", "k3x_stack_destroy",
     "k3x_moe_layer_check", "k3x_moe_layer_set_route_wait",
     "k3x_attn_res", "k3x_moe_half", "k3x_moe_layer_reserve", "k3x_moe_layer_dequant",
-    "k3x_moe_prefill_noalloc",
+    "k3x_moe_prefill_noalloc", "k3x_moe_layer_trace",
     # include/k3x_store.h
     "k3x_store_open", "k3x_store_close", "k3x_store_count", "k3x_store_shards",
     "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
@@ -130,6 +130,7 @@ def lib():
         L.k3x_moe_layer_dequant.argtypes = [vp, i, i, vp]
         L.k3x_moe_forward.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
         L.k3x_moe_prefill_noalloc.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
+        L.k3x_moe_layer_trace.argtypes = [vp, i, vp, i]
         L.k3x_rmsnorm.argtypes = [vp, vp, vp, i, i, f, vp]
         L.k3x_moe.argtypes = [vp, vp, vp, i, vp, vp]
         L.k3x_moe_prefill.argtypes = [vp, vp, vp, i, vp, vp]
@@ -404,6 +405,15 @@ class MoELayer:
         withholds the selection's flag (calls made so are not valid)."""
         _check(lib().k3x_moe_layer_set_route_wait(self.h, ticks, 1 if publish else 0),
                "k3x_moe_layer_set_route_wait")
+
+    def trace(self, kernel, max_wg=1 << 16):
+        """Per-workgroup trace of decode kernel 0/1/2 of the last call ([n][3] uint64: id |
+        XCD << 28 | hardware ids << 32, start, end at 100 MHz), or None (a layer made
+        without K3X_TRACE=1)."""
+        buf = np.zeros((max_wg, 3), np.uint64)
+        n = _check(lib().k3x_moe_layer_trace(self.h, kernel, buf.ctypes.data, max_wg),
+                   "k3x_moe_layer_trace")
+        return buf[:n] if n else None
 
     def set_timing(self, on):
         _check(lib().k3x_moe_layer_set_timing(self.h, 1 if on else 0), "set_timing")

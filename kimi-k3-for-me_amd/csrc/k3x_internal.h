@@ -147,6 +147,10 @@ struct k3x_moe_layer {
     unsigned long long *tr;
     int       tr_cap, tr_n[3];
     k3x_prefill_buf pf;
+    /* prefill: the shared expert's GEMMs run on a stream of their own, forked from the
+     * caller's stream after the activation split and joined before the combine (events
+     * 0 and 1); NULL when the layer has no shared expert */
+    void     *pf_side, *pf_ev[2];
     size_t    bytes;
     /* decode: bound on the routed workgroups' wait for the published selection (ticks of
      * the 100 MHz clock), and a failure-injection switch that withholds the flag */

@@ -105,6 +105,13 @@ static int layer_alloc(k3x_moe_layer *L)
         RCCHK(dmalloc((void **)&L->sh_up, k3x_bf16_matrix_bytes(L->SI, H), b));
         RCCHK(dmalloc((void **)&L->sh_down, k3x_bf16_matrix_bytes(H, L->SI), b));
         RCCHK(dmalloc((void **)&L->shB, (size_t)L->SI * 2 * K3X_DECODE_MAX_T * 2, b));
+        if (hipStreamCreateWithFlags((hipStream_t *)&L->pf_side, hipStreamNonBlocking) !=
+                hipSuccess ||
+            hipEventCreateWithFlags((hipEvent_t *)&L->pf_ev[0], hipEventDisableTiming) !=
+                hipSuccess ||
+            hipEventCreateWithFlags((hipEvent_t *)&L->pf_ev[1], hipEventDisableTiming) !=
+                hipSuccess)
+            return K3X_E_HIP;
     }
     RCCHK(dmalloc((void **)&L->score, (size_t)K3X_DECODE_MAX_T * E * 4, b));
     RCCHK(dmalloc((void **)&L->choice, (size_t)K3X_DECODE_MAX_T * E * 4, b));
@@ -157,6 +164,9 @@ static void layer_free(k3x_moe_layer *L)
     free(L->slot_of); free(L->key_of); free(L->used_at); free(L->pinned);
     for (int i = 0; i < 8; i++)
         if (L->ev[i]) hipEventDestroy((hipEvent_t)L->ev[i]);
+    for (int i = 0; i < 2; i++)
+        if (L->pf_ev[i]) hipEventDestroy((hipEvent_t)L->pf_ev[i]);
+    if (L->pf_side) hipStreamDestroy((hipStream_t)L->pf_side);
     free(L);
 }
 

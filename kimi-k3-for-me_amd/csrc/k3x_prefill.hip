@@ -56,14 +56,23 @@ __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int
 }
 
 // ------------------------------------------------------------------ router
-// Logits of a 32-token x 64-expert tile; thread (ty, tx) owns tokens 2ty, 2ty+1 and
-// experts 4tx .. 4tx+3 and runs their eight chains in double over i = 0 .. H-1 in order
-// (a product of two floats is exact in double, so each chain equals the reference's
-// fma-free loop).  K is staged 64 at a time: activations as double, weights as float
-// (widened at use); the next chunk is fetched into registers during the current one.
-#define RT_TOK 32
-#define RT_EXP 64
-#define RT_KC  64
+// Logits of every (token, expert) pair in double, each one sequential chain over
+// i = 0 .. H-1 in the reference's order (k3_router, k3_ops.c:1666-1688), on the FP64
+// matrix cores.  v_mfma_f64_16x16x4f64 adds its four k terms to each output one after
+// another, k in lane-group order, each a fused multiply-add (held bitwise against a
+// sequential fma chain on wide-exponent cancelling data); a product of two floats is
+// exact in double, so the chain equals the reference's fma-free loop bit for bit.  A
+// chain cannot be split over k, so the parallelism is the number of 16x16 output tiles:
+// a workgroup takes 48 experts x 64 tokens (each wave 16 tokens, three expert tiles,
+// 12 tiles per CU at 2048 tokens x 384 experts).  K is staged 64 at a time in LDS as
+// float, element k of a chunk at (k % 4) * 16 + k / 4 of its row, so that one 16-byte
+// read gives a lane its operands of four consecutive MFMA steps; the next chunk is
+// fetched into registers during the current one.  Workgroups are dealt expert block
+// fastest, so that with 8 expert blocks each XCD keeps one block's router rows in L2.
+#define RM_E  48
+#define RM_T  64
+#define RM_KC 64
+#define RM_S  (RM_KC + 4)
 
 struct PfRouterArgs {
     const void  *x;
@@ -73,65 +82,83 @@ struct PfRouterArgs {
     float       *score, *choice;
 };
 
-typedef __attribute__((__vector_size__(2 * sizeof(double)))) double f64x2;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
 
 __global__ void __launch_bounds__(PF_NT) pf_router(PfRouterArgs a)
 {
-    __shared__ __attribute__((aligned(16))) double xs[RT_KC][RT_TOK];
-    __shared__ __attribute__((aligned(16))) float ws[RT_KC][RT_EXP];
-    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-    const int tok0 = blockIdx.x * RT_TOK, e0 = blockIdx.y * RT_EXP;
-    double acc[2][4];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = 0.0;
-    // staging roles, so that a wave's LDS stores are contiguous: x: token tid%32, k from
-    // (tid/32)*8; W: expert tid%64, k from (tid/64)*16
-    const int xt = threadIdx.x % RT_TOK, xk = (threadIdx.x / RT_TOK) * 8;
-    const int we = threadIdx.x % RT_EXP, wk = (threadIdx.x / RT_EXP) * 16;
-    const bool xon = tok0 + xt < a.T, won = e0 + we < a.E;
-    const float *wrow = a.W + (size_t)(won ? e0 + we : 0) * a.H + wk;
-    const size_t xrow = (size_t)(xon ? tok0 + xt : 0) * a.H + xk;
-    float xv[8];
-    f32x4 wv[4];
+    __shared__ __attribute__((aligned(16))) float lds[2][RM_E + RM_T][RM_S];
+    const int nEB = (a.E + RM_E - 1) / RM_E;
+    const int e0 = (blockIdx.x % nEB) * RM_E, t0 = (blockIdx.x / nEB) * RM_T;
+    const int tid = threadIdx.x, wave = tid / WAVE, r = tid % 16, g = (tid % WAVE) / 16;
+    // staging roles: W rows tid/16 + 16c (c < 3), k 4*(tid%16) .. +3; x rows tid/8 + 32c
+    // (c < 2), k 8*(tid%8) .. +7
+    const int wk = 4 * (tid % 16), xk = 8 * (tid % 8);
+    f32x4 wv[3];
+    float xv[2][8];
     auto fetch = [&](int k0) AI {
-        if (xon) load_x8(a.x, a.x_bf16, xrow + k0, xv);
-        else for (int j = 0; j < 8; j++) xv[j] = 0.f;
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-            wv[c] = won ? *(const f32x4 *)(wrow + k0 + 4 * c) : (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < 3; c++) {
+            const int e = e0 + tid / 16 + 16 * c;
+            wv[c] = e < a.E ? *(const f32x4 *)(a.W + (size_t)e * a.H + k0 + wk)
+                            : (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int t = t0 + tid / 8 + 32 * c;
+            if (t < a.T) load_x8(a.x, a.x_bf16, (size_t)t * a.H + k0 + xk, xv[c]);
+            else
+#pragma unroll
+                for (int q = 0; q < 8; q++) xv[c][q] = 0.f;
+        }
     };
+    auto stage = [&](int b) AI {
+#pragma unroll
+        for (int c = 0; c < 3; c++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) lds[b][tid / 16 + 16 * c][q * 16 + tid % 16] = wv[c][q];
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                lds[b][RM_E + tid / 8 + 32 * c][(q % 4) * 16 + xk / 4 + q / 4] = xv[c][q];
+    };
+    f64x4 acc[3];
+#pragma unroll
+    for (int m = 0; m < 3; m++) acc[m] = (f64x4){0.0, 0.0, 0.0, 0.0};
     fetch(0);
-    for (int k0 = 0; k0 < a.H; k0 += RT_KC) {
-        __syncthreads();
+    stage(0);
+    __syncthreads();
+    const int nk = a.H / RM_KC;
+    for (int kc = 0; kc < nk; kc++) {
+        const int b = kc & 1;
+        if (kc + 1 < nk) fetch((kc + 1) * RM_KC);
 #pragma unroll
-        for (int j = 0; j < 8; j++) xs[xk + j][xt] = (double)xv[j];
+        for (int j0 = 0; j0 < RM_KC / 4; j0 += 4) {
+            const f32x4 xq = *(const f32x4 *)&lds[b][RM_E + 16 * wave + r][g * 16 + j0];
+            f32x4 wq[3];
 #pragma unroll
-        for (int c = 0; c < 4; c++)
+            for (int m = 0; m < 3; m++) wq[m] = *(const f32x4 *)&lds[b][16 * m + r][g * 16 + j0];
 #pragma unroll
-            for (int j = 0; j < 4; j++) ws[wk + 4 * c + j][we] = wv[c][j];
-        __syncthreads();
-        if (k0 + RT_KC < a.H) fetch(k0 + RT_KC);
-#pragma unroll 8
-        for (int k = 0; k < RT_KC; k++) {
-            const f64x2 x2 = *(const f64x2 *)&xs[k][2 * ty];
-            const f32x4 w4 = *(const f32x4 *)&ws[k][4 * tx];
+            for (int jj = 0; jj < 4; jj++) {
+                const double xd = (double)xq[jj];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const double wd = (double)w4[j];
-                acc[0][j] = __fma_rn(x2[0], wd, acc[0][j]);
-                acc[1][j] = __fma_rn(x2[1], wd, acc[1][j]);
+                for (int m = 0; m < 3; m++)
+                    acc[m] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)wq[m][jj], xd, acc[m], 0, 0, 0);
             }
         }
+        if (kc + 1 < nk) stage(b ^ 1);
+        __syncthreads();
     }
+    // output tile m, element i of lane (r, g): expert 16m + g + 4i, token 16*wave + r
+    const int t = t0 + 16 * wave + r;
+    if (t >= a.T) return;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int m = 0; m < 3; m++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int t = tok0 + 2 * ty + i, e = e0 + 4 * tx + j;
-            if (t < a.T && e < a.E) {
-                const float sc = sigmoid_ref((float)acc[i][j]);
+        for (int i = 0; i < 4; i++) {
+            const int e = e0 + 16 * m + g + 4 * i;
+            if (e < a.E) {
+                const float sc = sigmoid_ref((float)acc[m][i]);
                 a.score[(size_t)t * a.E + e] = sc;
                 a.choice[(size_t)t * a.E + e] = sc + a.bias[e];
             }
@@ -375,10 +402,12 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
     int g = 0, rb, ntok, p0;
     const int tile = blockIdx.x;
     if (a.desc) {
-        const int ntiles = *a.ntile;
+        // scalar registers (readfirstlane), so that the weight resources are uniform
+        const int ntiles = __builtin_amdgcn_readfirstlane(*a.ntile);
         if (tile >= ntiles) return;
         const int4 d = a.desc[tile];
-        g = d.x; rb = d.y; p0 = d.z; ntok = d.w;
+        g = __builtin_amdgcn_readfirstlane(d.x); rb = __builtin_amdgcn_readfirstlane(d.y);
+        p0 = __builtin_amdgcn_readfirstlane(d.z); ntok = __builtin_amdgcn_readfirstlane(d.w);
     } else {
         const int nc = (a.n0 + TPB - 1) / TPB;
         if (tile >= nrb * nc) return;
@@ -589,13 +618,18 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
         // contiguous runs instead (XCD x takes tiles x*per .. x*per + per-1 in order), so
         // the column blocks of one weight row block run back to back on one XCD and
         // re-read the weights from its L2.  The grid is a multiple of 8.
-        const int ntiles = a.desc ? *a.ntile : nrb * ((a.n0 + TPB - 1) / TPB);
+        // the descriptor words are read into scalar registers (readfirstlane): the
+        // weight resources built from them must be wave-uniform, or every buffer load
+        // becomes a loop over distinct descriptors
+        const int ntiles = a.desc ? __builtin_amdgcn_readfirstlane(*a.ntile)
+                                  : nrb * ((a.n0 + TPB - 1) / TPB);
         const int per = (ntiles + 7) >> 3;
         const int k = blockIdx.x >> 3, tile = (blockIdx.x & 7) * per + k;
         if (k >= per || tile >= ntiles) return;
         if (a.desc) {
-            const int4 d = a.desc[(a.dbase ? *a.dbase : 0) + tile];
-            g = d.x; rb = d.y; p0 = d.z; ntok = d.w;
+            const int4 d = a.desc[(a.dbase ? __builtin_amdgcn_readfirstlane(*a.dbase) : 0) + tile];
+            g = __builtin_amdgcn_readfirstlane(d.x); rb = __builtin_amdgcn_readfirstlane(d.y);
+            p0 = __builtin_amdgcn_readfirstlane(d.z); ntok = __builtin_amdgcn_readfirstlane(d.w);
         } else {
             const int nc = (a.n0 + TPB - 1) / TPB;
             rb = tile / nc;
@@ -616,7 +650,9 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
     for (int i = 0; i < RT32; i++) {
         const int t16 = ((rb * NW + wave) * RT32 + i) * 2;
         tp16[i] = t16;
-        const int ntl = R16 - t16 < 0 ? 0 : (R16 - t16 > 2 ? 2 : R16 - t16);
+        // readfirstlane: the clamp is a VALU med3, whose result would make the weight
+        // resource a vector operand
+        const int ntl = __builtin_amdgcn_readfirstlane(R16 - t16 < 0 ? 0 : (R16 - t16 > 2 ? 2 : R16 - t16));
 #pragma unroll
         for (int m = 0; m < NMAT; m++)
             ra[m][i] = make_rsrc(a.wm[m] + (size_t)g * a.gstride + (size_t)t16 * tbytes,
@@ -901,11 +937,56 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
                        x, x_bf16, T, H, H, B->xhl, B->counts, E);
     if ((rc = launch_ok())) return rc;
 
+    if (SI > 0) {
+        // the shared expert (bf16 weights, every token) needs only the split activations:
+        // its gate/up and down run on the layer's side stream while the router, the
+        // dispatch and the routed GEMMs run on s.  Its T rows follow the TK routed rows
+        // in y, which nothing on s writes.
+        hipStream_t side = (hipStream_t)L->pf_side;
+        if (hipEventRecord((hipEvent_t)L->pf_ev[0], s) != hipSuccess ||
+            hipStreamWaitEvent(side, (hipEvent_t)L->pf_ev[0], 0) != hipSuccess)
+            return K3X_E_HIP;
+        PfGemmArgs sg;
+        memset(&sg, 0, sizeof sg);
+        sg.wm[0] = (const uint8_t *)L->sh_gate; sg.wm[1] = (const uint8_t *)L->sh_up;
+        sg.R = SI; sg.K = H; sg.n0 = T;
+        sg.bsrc = B->xhl; sg.brows = T; sg.row_base = 0;
+        sg.act = B->act_sh; sg.arows = T; sg.out_base = 0;
+        sg.b1 = L->b1; sg.b2 = L->b2;
+        const int tpb_sg = 4 * 16 / HLg, nrb_sg = cdiv(SI, (PF_NT / WAVE) * 1 * 16);
+        const unsigned grid_sg = nrb_sg * cdiv(T, tpb_sg);
+        if (HLg == 1)
+            hipLaunchKernelGGL((pf_gemm<false, false, 2, 1, 4, 1, true>), dim3(grid_sg), dim3(PF_NT), 0, side, sg);
+        else
+            hipLaunchKernelGGL((pf_gemm<false, false, 2, 1, 4, 2, true>), dim3(grid_sg), dim3(PF_NT), 0, side, sg);
+        rc = launch_ok();
+        PfGemmArgs sd;
+        memset(&sd, 0, sizeof sd);
+        sd.wm[0] = (const uint8_t *)L->sh_down; sd.R = H; sd.K = SI; sd.n0 = T;
+        sd.bsrc = B->act_sh; sd.brows = T; sd.row_base = 0;
+        sd.y = B->y; sd.out_base = TK;
+        const int nrb_sd = cdiv(H, (PF_NT / WAVE) * 2 * 16);
+        const unsigned grid_sd = nrb_sd * cdiv(T, 32);
+        if (!rc) {
+            hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_sd), dim3(PF_NT), 0, side, sd);
+            rc = launch_ok();
+        }
+        // recorded even after a failed launch, so that s can always join the side stream
+        if (hipEventRecord((hipEvent_t)L->pf_ev[1], side) != hipSuccess) return K3X_E_HIP;
+        if (rc) {
+            (void)hipStreamWaitEvent(s, (hipEvent_t)L->pf_ev[1], 0);
+            return rc;
+        }
+    }
+    // from here on, a failed launch joins the side stream before it returns
+#define PF_RET(e) do { const int e_ = (e); \
+        if (SI > 0) (void)hipStreamWaitEvent(s, (hipEvent_t)L->pf_ev[1], 0); return e_; } while (0)
+
     PfRouterArgs ar;
     ar.x = x; ar.x_bf16 = x_bf16; ar.W = L->router; ar.bias = L->bias;
     ar.T = T; ar.H = H; ar.E = E; ar.score = B->score; ar.choice = B->choice;
-    hipLaunchKernelGGL(pf_router, dim3(cdiv(T, RT_TOK), cdiv(E, RT_EXP)), dim3(PF_NT), 0, s, ar);
-    if ((rc = launch_ok())) return rc;
+    hipLaunchKernelGGL(pf_router, dim3(cdiv(T, RM_T) * cdiv(E, RM_E)), dim3(PF_NT), 0, s, ar);
+    if ((rc = launch_ok())) PF_RET(rc);
 
     PfTopkArgs at;
     at.score = B->score; at.choice = B->choice; at.T = T; at.E = E; at.K = K;
@@ -916,7 +997,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     else if (E <= 384) launch_topk<6>(at, s);
     else if (E <= 512) launch_topk<8>(at, s);
     else               launch_topk<16>(at, s);
-    if ((rc = launch_ok())) return rc;
+    if ((rc = launch_ok())) PF_RET(rc);
 
     PfScanArgs sa;
     sa.counts = B->counts; sa.E = E; sa.offsets = B->offsets; sa.cursor = B->cursor;
@@ -926,13 +1007,13 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     sa.tpb_s[1] = DN_CT32_S * 32 / 2; sa.tpb_b[1] = DN_CT32_B * 32 / 2;
     sa.nrb_s[1] = cdiv(X, NW_S * DN_RT32 * 32); sa.nrb_b[1] = cdiv(X, NW_B * DN_RT32 * 32);
     hipLaunchKernelGGL(pf_scan, dim3(1), dim3(1024), 0, s, sa);
-    if ((rc = launch_ok())) return rc;
+    if ((rc = launch_ok())) PF_RET(rc);
     hipLaunchKernelGGL(pf_scatter, dim3(cdiv(TK, PF_NT)), dim3(PF_NT), 0, s, B->idx, B->wt, TK, K,
                        B->offsets, B->cursor, B->perm_tok, B->perm_w, B->pos_of);
-    if ((rc = launch_ok())) return rc;
+    if ((rc = launch_ok())) PF_RET(rc);
     hipLaunchKernelGGL(pf_tiles, dim3(E), dim3(PF_NT), 0, s, B->counts, B->offsets, sa,
                        (int4 *)B->desc_gu, (int4 *)B->desc_dn);
-    if ((rc = launch_ok())) return rc;
+    if ((rc = launch_ok())) PF_RET(rc);
     const uint16_t *rsrc = B->xhl;        // the routed experts' input planes
     if (L->lat) {
         // z = down . x for every token (k3_mmw_batch, k3_ops.c:1871), then its hi/lo planes
@@ -946,15 +1027,15 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
             hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 1, false>), dim3(grid_z), dim3(PF_NT), 0, s, zg);
         else
             hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_z), dim3(PF_NT), 0, s, zg);
-        if ((rc = launch_ok())) return rc;
+        if ((rc = launch_ok())) PF_RET(rc);
         hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (X / 8), PF_NT)), dim3(PF_NT), 0, s,
                            B->zf, 0, T, X, X, B->zhl, (int *)NULL, 0);
-        if ((rc = launch_ok())) return rc;
+        if ((rc = launch_ok())) PF_RET(rc);
         rsrc = B->zhl;
     }
     hipLaunchKernelGGL(pf_permute, dim3(cdiv((size_t)HLr * (X / 8) * TK, PF_NT)), dim3(PF_NT), 0, s,
                        rsrc, T, X / 8, HLr, B->perm_tok, TK, B->xp);
-    if ((rc = launch_ok())) return rc;
+    if ((rc = launch_ok())) PF_RET(rc);
 
     // grids: upper bounds of each list (a small expert has one column block; large ones
     // number at most TK / (tpb_s + 1)); surplus workgroups leave at once
@@ -965,7 +1046,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         grid_b[m] = round8((size_t)sa.nrb_b[m] * (cdiv(TK, sa.tpb_b[m]) + (nbig < (size_t)E ? nbig : (size_t)E)));
     }
     if (grid_s[0] + grid_b[0] > (unsigned)B->ndesc_gu || grid_s[1] + grid_b[1] > (unsigned)B->ndesc_dn)
-        return K3X_E_SHAPE;
+        PF_RET(K3X_E_SHAPE);
 
     // routed gate/up: B rows are the permuted activation rows
     PfGemmArgs g;
@@ -987,7 +1068,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         if (HLr == 1) { launch_gu<false, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<false, 1, GU_CT32_S, NW_S>(g, grid_s[0], s); }
         else          { launch_gu<false, 2, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<false, 2, GU_CT32_S, NW_S>(g, grid_s[0], s); }
     }
-    if ((rc = launch_ok())) return rc;
+    if ((rc = launch_ok())) PF_RET(rc);
 
     // routed down: B rows are the activation rows, in permuted order
     PfGemmArgs d;
@@ -1001,9 +1082,9 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     db.ntile = B->tb_dn + 2 * E + 1; db.dbase = B->tb_dn + E;
     if (L->special & 4) { launch_dn<true, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<true, DN_CT32_S, NW_S>(d, grid_s[1], s); }
     else                { launch_dn<false, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<false, DN_CT32_S, NW_S>(d, grid_s[1], s); }
-    if ((rc = launch_ok())) return rc;
+    if ((rc = launch_ok())) PF_RET(rc);
 
-    int sh_row0 = -1, out_rows = TK;       // the shared rows follow the routed ones in y
+    int sh_row0 = -1;
     const int *pos = B->pos_of;
     int KC = K;
     if (L->lat) {
@@ -1011,10 +1092,10 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         // planes (:1946), then the up projection (:1950) into y rows 0 .. T-1
         hipLaunchKernelGGL(pf_combine, dim3(cdiv((size_t)T * (X / 4), PF_NT)), dim3(PF_NT), 0, s,
                            B->y, B->pos_of, T, K, X, -1, (const float *)NULL, B->zf);
-        if ((rc = launch_ok())) return rc;
+        if ((rc = launch_ok())) PF_RET(rc);
         hipLaunchKernelGGL(pf_latnorm, dim3(T), dim3(PF_NT), 0, s, B->zf,
                            c->latent_norm ? L->lnw : (const float *)NULL, c->rms_eps, T, X, B->zhl);
-        if ((rc = launch_ok())) return rc;
+        if ((rc = launch_ok())) PF_RET(rc);
         PfGemmArgs ug;
         memset(&ug, 0, sizeof ug);
         ug.wm[0] = (const uint8_t *)L->lup; ug.R = H; ug.K = X; ug.n0 = T;
@@ -1022,44 +1103,21 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         ug.y = B->y; ug.out_base = 0;
         const unsigned grid_u = cdiv(H, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 32);
         hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_u), dim3(PF_NT), 0, s, ug);
-        if ((rc = launch_ok())) return rc;
-        out_rows = T;
+        if ((rc = launch_ok())) PF_RET(rc);
         pos = NULL;
         KC = 1;
     }
     if (SI > 0) {
-        // shared gate/up over every token (bf16 weights), then down; its output rows follow
-        // the routed ones in y
-        PfGemmArgs sg;
-        memset(&sg, 0, sizeof sg);
-        sg.wm[0] = (const uint8_t *)L->sh_gate; sg.wm[1] = (const uint8_t *)L->sh_up;
-        sg.R = SI; sg.K = H; sg.n0 = T;
-        sg.bsrc = B->xhl; sg.brows = T; sg.row_base = 0;
-        sg.act = B->act_sh; sg.arows = T; sg.out_base = 0;
-        sg.b1 = L->b1; sg.b2 = L->b2;
-        const int tpb_sg = 4 * 16 / HLg, nrb_sg = cdiv(SI, (PF_NT / WAVE) * 1 * 16);
-        const unsigned grid_sg = nrb_sg * cdiv(T, tpb_sg);
-        if (HLg == 1)
-            hipLaunchKernelGGL((pf_gemm<false, false, 2, 1, 4, 1, true>), dim3(grid_sg), dim3(PF_NT), 0, s, sg);
-        else
-            hipLaunchKernelGGL((pf_gemm<false, false, 2, 1, 4, 2, true>), dim3(grid_sg), dim3(PF_NT), 0, s, sg);
-        if ((rc = launch_ok())) return rc;
-        PfGemmArgs sd;
-        memset(&sd, 0, sizeof sd);
-        sd.wm[0] = (const uint8_t *)L->sh_down; sd.R = H; sd.K = SI; sd.n0 = T;
-        sd.bsrc = B->act_sh; sd.brows = T; sd.row_base = 0;
-        sd.y = B->y; sd.out_base = out_rows;
-        const int nrb_sd = cdiv(H, (PF_NT / WAVE) * 2 * 16);
-        const unsigned grid_sd = nrb_sd * cdiv(T, 32);
-        hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_sd), dim3(PF_NT), 0, s, sd);
-        if ((rc = launch_ok())) return rc;
-        sh_row0 = out_rows;
+        // the shared rows are in y: join the shared stream
+        if (hipStreamWaitEvent(s, (hipEvent_t)L->pf_ev[1], 0) != hipSuccess) return K3X_E_HIP;
+        sh_row0 = TK;
     }
 
     hipLaunchKernelGGL(pf_combine, dim3(cdiv((size_t)T * (H / 4), PF_NT)), dim3(PF_NT), 0, s,
                        B->y, pos, T, KC, H, sh_row0, resid, out);
     return launch_ok();
 }
+#undef PF_RET
 
 // Prefill: the pipeline over chunks of up to K3X_PF_CHUNK tokens.  Each token's result
 // depends only on its own routing, so the chunking changes no result.

@@ -107,3 +107,48 @@ def test_wait_bound_host_call_returns_wait(torch, k3x):
     assert np.array_equal(il, idx[-1])
     assert synth.rel_l2(out, o) < TOL
     layer.close()
+
+
+def test_prefill_router_sequential_chain_bitwise(torch, k3x):
+    """The prefill router's logits are the reference's single double chain over
+    i = 0 .. H-1 (k3_ops.c:1666-1688) bit for bit.  The router rows are equal at columns
+    p and p+1 and every token carries +2^40 and -2^40 there, so the pair cancels but first
+    rounds away low bits of the partial sum it meets, which depends on the summation order.
+    With renorm off and scale 1 the routing weights are the sigmoid scores themselves and
+    are compared bitwise with the oracle's.  E = 100 and T = 70 are not multiples of the
+    router's 48-expert and 64-token blocks.  Teeth: on the same data a four-chain order
+    changes the float logits of most pairs."""
+    import oracle_lib as ol
+    say("case: prefill router on cancelling data, E=100 H=1024 T=70, weights bitwise")
+    H, E, K, T, p = 1024, 100, 8, 70, 512
+    L = synth.Layer(H=H, E=E, K=K, I=128, seed=41, renorm=0, routed_scale=1.0)
+    L.gate[:, p + 1] = L.gate[:, p]
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    sgn = np.where(rng.integers(0, 2, T) == 1, 1.0, -1.0).astype(np.float32)
+    x[:, p] = sgn * np.float32(2.0 ** 40)
+    x[:, p + 1] = -sgn * np.float32(2.0 ** 40)
+    # teeth (CPU): the sequential chain against a four-chain order
+    W64, X64 = L.gate.astype(np.float64), x.astype(np.float64)
+    seq = np.zeros((T, E))
+    ch = np.zeros((4, T, E))
+    for i in range(H):
+        term = X64[:, i:i + 1] * W64[:, i][None, :]
+        seq = seq + term
+        ch[i % 4] = ch[i % 4] + term
+    four = ((ch[0] + ch[1]) + ch[2]) + ch[3]
+    differ = np.mean(seq.astype(np.float32) != four.astype(np.float32))
+    say(f"  float logits that a four-chain order changes: {differ:.1%}")
+    assert differ > 0.2
+    layer = bank_layer(k3x, L)
+    _, idx, wt = dev_forward(torch, k3x, layer, x)
+    ri = np.empty((T, K), np.int32)
+    rw = np.empty((T, K), np.float32)
+    for t in range(T):
+        xt = np.ascontiguousarray(x[t])
+        ol.oracle().ko_router(ol.ptr(ri[t], ol.I32P), ol.ptr(rw[t], ol.F32P),
+                              ol.ptr(xt, ol.F32P), ol.ptr(L.gate, ol.F32P),
+                              ol.ptr(L.bias, ol.F32P), H, E, K, 0, 1.0)
+    assert np.array_equal(idx, ri)
+    assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+    layer.close()

@@ -85,32 +85,51 @@ def prefill_leg(torch, k3x, reps=5):
         layer.forward(out.data_ptr(), x.data_ptr(), T, k3x.K3X_BF16, 0, idx.data_ptr(),
                       wt.data_ptr(), stream=sh)
 
-    with torch.cuda.stream(stream):
-        run()
-        run()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
+    def timed():
+        with torch.cuda.stream(stream):
             run()
-        e1.record(stream)
-        torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
-    used = int(torch.unique(idx).numel())
-    layer_bytes = used * B_EXPERT + B_SHARED + B_ROUTER + T * H * 2 + T * H * 4
-    flops = 2.0 * T * (K * 3 * I * H + 3 * I * H + E * H)
+            run()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                run()
+            e1.record(stream)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    def rates(ms):
+        used = int(torch.unique(idx).numel())
+        layer_bytes = used * B_EXPERT + B_SHARED + B_ROUTER + T * H * 2 + T * H * 4
+        flops = 2.0 * T * (K * 3 * I * H + 3 * I * H + E * H)
+        return {"tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_chunk": round(ms, 3),
+                "experts_used": used,
+                "hbm_gbs": round(layer_bytes / (ms * 1e-3) / 1e9, 1),
+                "hbm_frac": round(layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                "mfma_frac_mxfp4_peak": round(flops / (ms * 1e-3) / 1e12 / 10100.0, 4),
+                "mfma_frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / 2500.0, 4)}
+
+    ms = timed()
+    rec = {"workload": f"prefill {T} bf16 tokens, Zipf-skewed routing (alpha 1.0, s 1.1)"}
+    rec.update(rates(ms))
+    rec["reps"] = reps
+    # the opt-in MXFP8-activation mode on the same layer and input: scaled matrix cores
+    # for the routed products; its distance from the exact mode is reported beside it
+    exact_out, exact_idx = out.clone(), idx.clone()
+    layer.set_prefill_mode(k3x.K3X_PREFILL_MXFP8)
+    ms_mx = timed()
+    mx = {"mode": "K3X_PREFILL_MXFP8 (opt-in): routed products on v_mfma_scale_f32_32x32x64_f8f6f4, "
+                  "activations quantised to MXFP8"}
+    mx.update(rates(ms_mx))
+    d = (out.double() - exact_out.double()).norm() / exact_out.double().norm()
+    mx["rel_l2_vs_exact_mode"] = float(f"{float(d):.3e}")
+    mx["same_experts_as_exact_mode"] = bool(torch.equal(idx, exact_idx))
+    rec["mxfp8"] = mx
     layer.close()
-    del x, out, idx, wt
+    del x, out, idx, wt, exact_out, exact_idx
     torch.cuda.empty_cache()
-    return {"workload": f"prefill {T} bf16 tokens, Zipf-skewed routing (alpha 1.0, s 1.1)",
-            "tokens_per_s": round(T / (ms * 1e-3), 1), "ms_per_chunk": round(ms, 3),
-            "experts_used": used,
-            "hbm_gbs": round(layer_bytes / (ms * 1e-3) / 1e9, 1),
-            "hbm_frac": round(layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
-            "mfma_frac_mxfp4_peak": round(flops / (ms * 1e-3) / 1e12 / 10100.0, 4),
-            "mfma_frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / 2500.0, 4),
-            "reps": reps}
+    return rec
 
 
 STACK_LAYERS, STACK_TOKENS = 8, 256

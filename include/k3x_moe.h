@@ -175,6 +175,24 @@ int  k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, i
 int  k3x_moe_prefill_noalloc(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                              const float *resid, int *idx, float *wt, void *stream);
 
+/* Prefill arithmetic of a layer (calls with more than 8 tokens; the decode path is always
+ * exact).  K3X_PREFILL_EXACT (the default): the routed products take the activations as
+ * bf16 hi + lo pairs against the exactly dequantised MXFP4 weights, within the parity bar
+ * of the reference's fp32 path (k3_matmul_mxfp4, k3_ops.c:3323-3776).
+ * K3X_PREFILL_MXFP8 (opt-in): the routed gate/up and down products run on the scaled
+ * matrix cores with the weights as stored and the activations quantised to MXFP8 (E4M3
+ * elements, one E8M0 scale per 32 consecutive k; the scale 2^X is the least power of two
+ * with max|v| <= 448 * 2^X over the block's finite values, elements rounded to nearest,
+ * ties to even; the routing weight is folded into the gate/up output before it is
+ * quantised).  Router, shared expert and latent projections stay exact.  Results then
+ * differ from the reference by the quantisation (about 1-3% relative L2 on N(0,1)
+ * activations).  No counterpart in the reference.  Returns K3X_E_SHAPE for a layer
+ * holding an E8M0 scale byte outside 1..252 (the matrix cores read 255 as NaN where the
+ * reference reads zero) and K3X_E_ARG for an unknown mode. */
+#define K3X_PREFILL_EXACT 0
+#define K3X_PREFILL_MXFP8 1
+int  k3x_moe_layer_set_prefill_mode(k3x_moe_layer *L, int mode);
+
 /* RMSNorm of T rows on the device: y = w * x * inv, inv = 1/sqrt(mean(x^2) + eps)
  * (k3_rmsnorm, k3_ops.c:132-140).  x, y fp32 [T][n], w fp32 [n], device pointers. */
 int  k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,

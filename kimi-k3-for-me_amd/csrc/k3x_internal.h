@@ -151,6 +151,7 @@ struct k3x_moe_layer {
      * caller's stream after the activation split and joined before the combine (events
      * 0 and 1); NULL when the layer has no shared expert */
     void     *pf_side, *pf_ev[2];
+    int       pf_mode;            /* K3X_PREFILL_EXACT or K3X_PREFILL_MXFP8 */
     size_t    bytes;
     /* decode: bound on the routed workgroups' wait for the published selection (ticks of
      * the 100 MHz clock), and a failure-injection switch that withholds the flag */

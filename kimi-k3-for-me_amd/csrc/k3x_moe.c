@@ -883,6 +883,14 @@ int k3x_moe_prefill(k3x_moe_layer *L, float *out, const float *x, int T, int *id
     return host_call(L, out, x, T, idx, wt, 1);
 }
 
+int k3x_moe_layer_set_prefill_mode(k3x_moe_layer *L, int mode)
+{
+    if (!L || (mode != K3X_PREFILL_EXACT && mode != K3X_PREFILL_MXFP8)) return K3X_E_ARG;
+    if (mode == K3X_PREFILL_MXFP8 && L->special) return K3X_E_SHAPE;
+    L->pf_mode = mode;
+    return 0;
+}
+
 /* ---------------------------------------------------------------- timing ---- */
 int k3x_moe_layer_set_timing(k3x_moe_layer *L, int on)
 {

@@ -346,6 +346,12 @@ struct PfGemmArgs {
     int             out_base;   // output row = out_base + p
     float           b1, b2;     // SiTU betas of the gate/up epilogue (0: uncapped)
     int             ldy;        // floats between output rows (0: R)
+    // MXFP8 mode (pf_gemm_mx): B codes [K/16][brows][16] bytes and scales [K/128][brows]
+    // dwords (byte b = the 32-k block 4q + b); the gate/up output in the same two forms
+    // over R, arows rows
+    const uint8_t  *b8;
+    const uint32_t *b8s;
+    uint8_t        *o8, *o8s;
 };
 
 template <bool FP4, int NMAT, int RT>
@@ -809,6 +815,318 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
     }
 }
 
+// ------------------------------------------------------------------ MXFP8 mode
+// The opt-in prefill mode K3X_PREFILL_MXFP8: the routed expert products on the scaled
+// matrix cores (v_mfma_scale_f32_32x32x64_f8f6f4), the weights as stored (E2M1 codes,
+// E8M0 scale per 32 k, applied by the matrix core), the activations quantised to MXFP8:
+// blocks of 32 k sharing an E8M0 scale 2^X, X the least integer with max|v| <= 448 * 2^X
+// over the block's finite values (clamped to [-127, 127]; -127 for a block with no
+// non-zero finite value), each finite value v * 2^-X rounded to the nearest E4M3 (FN
+// encoding) value, ties to the even code, a non-finite one the NaN code.  The gate/up
+// input is the token's row (x, or z in a LatentMoE layer); the down input is the
+// gate/up output w * SiTU(gate, up), quantised in the gate/up epilogue.
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// E8M0 byte of a block whose largest finite magnitude is m
+__device__ __forceinline__ int mx8_scale(float m)
+{
+    if (!(m > 0.0f)) return 0;
+    const uint32_t b = __float_as_uint(m);
+    int X = (int)((b >> 23) & 255u) - 127 - 8 + ((b & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+    X = X < -127 ? -127 : (X > 127 ? 127 : X);
+    return X + 127;
+}
+
+// v (finite, |v| <= 448) to its E4M3 code, nearest value, ties to the even code
+__device__ __forceinline__ uint32_t e4m3_rne(float v)
+{
+    const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
+    const float a = fabsf(v);
+    if (a < 0x1p-6f) return sign | (uint32_t)rintf(a * 512.0f);     // steps of 2^-9
+    const int E = (int)((__float_as_uint(a) >> 23) & 255u) - 127;     // -6 .. 8
+    const uint32_t m = (uint32_t)rintf(a * __uint_as_float((uint32_t)(127 + 3 - E) << 23));
+    return sign | (m == 16u ? (uint32_t)(E + 8) << 3 : ((uint32_t)(E + 7) << 3) | (m - 8u));
+}
+
+// SiTU out of line: its capped form evaluates tanh in double, whose inlined expansion
+// over the sixteen values of a quantisation block would take the registers the
+// accumulators need
+__device__ __attribute__((noinline)) float situ_call(float g, float u, float b1, float b2)
+{
+    return situ(g, u, b1, b2);
+}
+
+// the code of v in a block of scale byte sb (inv = 2^-X)
+__device__ __forceinline__ uint32_t mx8_code(float v, float inv)
+{
+    if (!isfinite(v)) return ((__float_as_uint(v) >> 24) & 0x80u) | 0x7Fu;
+    return e4m3_rne(v * inv);
+}
+
+__device__ __forceinline__ float mx8_inv(int sb) { return __uint_as_float((uint32_t)(254 - sb) << 23); }
+
+// The routed experts' MXFP8 input in permuted order: one thread per (row p, 32-k block):
+// src row perm_tok[p] (bf16 or fp32, rows ld elements apart), X elements -> codes
+// [X/16][TK][16], scales [X/128][TK] dwords.
+__global__ void __launch_bounds__(PF_NT) pf_mx8_rows(const void *src, int bf16, int ld, int X,
+                                                     const int *perm_tok, int TK,
+                                                     uint8_t *codes, uint8_t *scales)
+{
+    const size_t i = (size_t)blockIdx.x * PF_NT + threadIdx.x;      // blk * TK + p
+    if (i >= (size_t)TK * (X / 32)) return;
+    const int p = (int)(i % TK), blk = (int)(i / TK);
+    const size_t base = (size_t)perm_tok[p] * ld + (size_t)blk * 32;
+    float v[4][8];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        load_x8(src, bf16, base + 8 * j, v[j]);
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            if (isfinite(v[j][e])) m = fmaxf(m, fabsf(v[j][e]));
+    }
+    const int sb = mx8_scale(m);
+    const float inv = mx8_inv(sb);
+    uint32_t w[8];
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+        uint32_t r = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) r |= mx8_code(v[d / 2][(d % 2) * 4 + e], inv) << (8 * e);
+        w[d] = r;
+    }
+    *(u32x4 *)(codes + ((size_t)(2 * blk) * TK + p) * 16) = (u32x4){w[0], w[1], w[2], w[3]};
+    *(u32x4 *)(codes + ((size_t)(2 * blk + 1) * TK + p) * 16) = (u32x4){w[4], w[5], w[6], w[7]};
+    scales[((size_t)(blk >> 2) * TK + p) * 4 + (blk & 3)] = (uint8_t)sb;
+}
+
+// Grouped GEMM on v_mfma_scale_f32_32x32x64_f8f6f4 (A fp4, B fp8 E4M3).  Operand layout
+// of the instruction (64 k a step): A lane l holds row l%32, k = 32*(l/32) .. +31 (16
+// bytes, low nibble first) with that 32-k group's scale byte; B lane l holds column l%32,
+// bytes 0-15 = k 16*(l/32) .. +15 and bytes 16-31 = k 32 + 16*(l/32) .. +15, and lane
+// (j + 32b) gives column j's scale of 32-k group b; D as the 32x32x16 bf16 form.  A quad
+// of 128 k is two steps whose A operands are pf_gemm32's two code loads and scale dwords
+// (k groups 2*step + h).  Tile lists, XCD dealing, ring and barrier protocol as
+// pf_gemm32; the B block in LDS: entry gq*NCOL + col = k16-group gq of the quad, column
+// col; each lane keeps its column's scale dword per quad in registers.  The gate/up
+// epilogue forms w * SiTU(gate, up) and quantises each 32-row block of a column (16
+// values in each of two lanes) to MXFP8 codes and a scale byte.
+template <int NMAT, int RT32, int CT, bool GU, int NW>
+__global__ void __launch_bounds__(NW * WAVE) pf_gemm_mx(PfGemmArgs a)
+{
+    constexpr int NTH = NW * WAVE;
+    constexpr int NCOL = CT * 32;
+    constexpr int RPB = NW * RT32 * 32;
+    constexpr int QB = 8 * NCOL * 16;
+    constexpr int NJ = QB / (NTH * 16);
+    constexpr int RING = 4;
+    constexpr int LPI = NMAT * RT32 * 4 + NJ + CT;
+    static_assert(NJ * NTH * 16 == QB, "B quad must split evenly");
+    static_assert((RING - 2) * LPI < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) uint8_t sB[RING * QB];
+
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    const int nrb = (a.R + RPB - 1) / RPB;
+    int g = 0, rb, ntok, p0;
+    {
+        const int ntiles = a.desc ? __builtin_amdgcn_readfirstlane(*a.ntile)
+                                  : nrb * ((a.n0 + NCOL - 1) / NCOL);
+        const int per = (ntiles + 7) >> 3;
+        const int k = blockIdx.x >> 3, tile = (blockIdx.x & 7) * per + k;
+        if (k >= per || tile >= ntiles) return;
+        if (a.desc) {
+            const int4 d = a.desc[(a.dbase ? __builtin_amdgcn_readfirstlane(*a.dbase) : 0) + tile];
+            g = __builtin_amdgcn_readfirstlane(d.x); rb = __builtin_amdgcn_readfirstlane(d.y);
+            p0 = __builtin_amdgcn_readfirstlane(d.z); ntok = __builtin_amdgcn_readfirstlane(d.w);
+        } else {
+            const int nc = (a.n0 + NCOL - 1) / NCOL;
+            rb = tile / nc;
+            p0 = (tile % nc) * NCOL;
+            ntok = min(NCOL, a.n0 - p0);
+        }
+    }
+    const int nQ = a.K >> 7;
+
+    const uint32_t tbytes = (uint32_t)fp4_tile_bytes(a.K);
+    const int R16 = a.R >> 4;
+    const int Rl = lane & 31, h = lane >> 5;
+    rsrc_t ra[NMAT][RT32];
+    int tp16[RT32];
+#pragma unroll
+    for (int i = 0; i < RT32; i++) {
+        const int t16 = ((rb * NW + wave) * RT32 + i) * 2;
+        tp16[i] = t16;
+        const int ntl = __builtin_amdgcn_readfirstlane(R16 - t16 < 0 ? 0 : (R16 - t16 > 2 ? 2 : R16 - t16));
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+            ra[m][i] = make_rsrc(a.wm[m] + (size_t)g * a.gstride + (size_t)t16 * tbytes,
+                                 (uint32_t)ntl * tbytes);
+    }
+    const uint32_t lc = (uint32_t)(Rl >> 4) * tbytes + (uint32_t)((Rl & 15) + 16 * h) * 16u;
+    const uint32_t ls = (uint32_t)(Rl >> 4) * tbytes + 4096u + (uint32_t)((Rl & 15) + 16 * h) * 4u;
+
+    // ---- B: entry e = (wave*NJ + j)*64 + lane = gq*NCOL + col
+    const rsrc_t rbc = make_rsrc(a.b8, (uint32_t)((size_t)a.K * a.brows));
+    const rsrc_t rbsc = make_rsrc(a.b8s, (uint32_t)((size_t)(a.K >> 7) * a.brows * 4));
+    const uint32_t qstep = (uint32_t)a.brows * 128u, sstep = (uint32_t)a.brows * 4u;
+    uint32_t boff[NJ], soff[CT];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int e = (wave * NJ + j) * WAVE + lane;
+        const int gq = e / NCOL, col = e % NCOL;
+        boff[j] = col < ntok ? ((uint32_t)gq * (uint32_t)a.brows + (uint32_t)(a.row_base + p0 + col)) * 16u
+                             : K3X_OOB;
+    }
+#pragma unroll
+    for (int c = 0; c < CT; c++) {
+        const int col = c * 32 + Rl;
+        soff[c] = col < ntok ? (uint32_t)(a.row_base + p0 + col) * 4u : K3X_OOB;
+    }
+
+    struct AQ {
+        u32x4    c[NMAT][RT32][2];
+        uint32_t s[NMAT][RT32][2];
+        uint32_t bs[CT];
+    };
+    AQ A[RING];
+    auto ld = [&](int slot, int q) AI {
+        const bool on = q < nQ;
+        const uint32_t qc = (uint32_t)(q >> 2) * 4352u + (uint32_t)(q & 3) * 1024u;
+        const uint32_t qs = (uint32_t)(q >> 2) * 4352u;
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int i = 0; i < RT32; i++)
+#pragma unroll
+                for (int gl = 0; gl < 2; gl++) {
+                    A[slot].c[m][i][gl] = wld16(ra[m][i], on ? lc + qc + 512u * gl : K3X_OOB);
+                    A[slot].s[m][i][gl] = wld4(ra[m][i], on ? ls + qs + 128u * gl : K3X_OOB);
+                }
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+            A[slot].bs[c] = __builtin_amdgcn_raw_buffer_load_b32(
+                rbsc, on && soff[c] != K3X_OOB ? soff[c] + (uint32_t)q * sstep : K3X_OOB, 0, 0);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const uint32_t o = boff[j] == K3X_OOB || !on ? K3X_OOB : boff[j] + (uint32_t)q * qstep;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rbc, (lds_void *)(sB + slot * QB + (wave * NJ + j) * 1024), 16, o, 0, 0, 0);
+        }
+    };
+
+    f32x16 acc[NMAT][RT32][CT];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int i = 0; i < RT32; i++)
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[m][i][c][v] = 0.f;
+
+    auto compute = [&](int slot, int q) AI {
+        const uint8_t *bb = sB + slot * QB;
+        const int sh = 8 * (q & 3);
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+            i32x8 bv[CT];
+            int sbv[CT];
+#pragma unroll
+            for (int c = 0; c < CT; c++) {
+                const u32x4 b0 = *(const u32x4 *)(bb + ((4 * st + h) * NCOL + c * 32 + Rl) * 16);
+                const u32x4 b1 = *(const u32x4 *)(bb + ((4 * st + 2 + h) * NCOL + c * 32 + Rl) * 16);
+                bv[c] = (i32x8){(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
+                                (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+                sbv[c] = (int)((A[slot].bs[c] >> (8 * (2 * st + h))) & 255u);
+            }
+#pragma unroll
+            for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                for (int i = 0; i < RT32; i++) {
+                    const u32x4 cw = A[slot].c[m][i][st];
+                    const i32x8 av = {(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3], 0, 0, 0, 0};
+                    const int sa = (int)((A[slot].s[m][i][st] >> sh) & 255u);
+#pragma unroll
+                    for (int c = 0; c < CT; c++)
+                        acc[m][i][c] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            av, bv[c], acc[m][i][c], 4, 0, 0, sa, 0, sbv[c]);
+                }
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < RING - 1; s++) {
+        SCHED_FENCE();
+        ld(s, s);
+    }
+    SCHED_FENCE();
+    int q = 0;
+    for (; q + RING <= nQ; q += RING) {
+#pragma unroll
+        for (int s = 0; s < RING; s++) {
+            meet<(RING - 2) * LPI>();
+            SCHED_FENCE();
+            ld((s + RING - 1) % RING, q + s + RING - 1);
+            SCHED_FENCE();
+            compute(s, q + s);
+        }
+    }
+    static_assert(RING == 4, "tail written for a ring of 4");
+    if (q < nQ)     { meet<2 * LPI>(); compute(0, q); }
+    if (q + 1 < nQ) { meet<LPI>();     compute(1, q + 1); }
+    if (q + 2 < nQ) { meet<0>();       compute(2, q + 2); }
+    WAIT_VMCNT_LGKM0(0);
+
+    // ---- epilogue: lane holds column Rl of each column tile, rows 8a + 4h + b
+#pragma unroll
+    for (int c = 0; c < CT; c++) {
+        const int tl = c * 32 + Rl;
+        const bool writer = tl < ntok;
+        const int p = p0 + tl;
+#pragma unroll
+        for (int i = 0; i < RT32; i++) {
+            const int rt = tp16[i] * 16;              // first row of the 32-row tile
+            if (GU) {
+                const float w = writer && a.pw ? a.pw[p] : 1.0f;
+                float yv[16];
+                float m = 0.0f;
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    yv[v] = (w == 0.0f) ? 0.0f : w * situ_call(acc[0][i][c][v], acc[NMAT - 1][i][c][v], a.b1, a.b2);
+                    if (isfinite(yv[v])) m = fmaxf(m, fabsf(yv[v]));
+                }
+                m = fmaxf(m, __shfl_xor(m, 32));
+                if (!writer || rt >= a.R) continue;
+                const int sb = mx8_scale(m);
+                const float inv = mx8_inv(sb);
+#pragma unroll
+                for (int aa = 0; aa < 4; aa++) {
+                    const int r0 = rt + 8 * aa + 4 * h;
+                    uint32_t wd = 0;
+#pragma unroll
+                    for (int b = 0; b < 4; b++) wd |= mx8_code(yv[4 * aa + b], inv) << (8 * b);
+                    *(uint32_t *)(a.o8 + ((size_t)(r0 >> 4) * a.arows + (size_t)(a.out_base + p)) * 16 + (r0 & 15)) = wd;
+                }
+                if (h == 0) {
+                    const int r32 = rt >> 5;
+                    a.o8s[((size_t)(r32 >> 2) * a.arows + (size_t)(a.out_base + p)) * 4 + (r32 & 3)] = (uint8_t)sb;
+                }
+            } else {
+                if (!writer) continue;
+#pragma unroll
+                for (int aa = 0; aa < 4; aa++) {
+                    const int r0 = rt + 8 * aa + 4 * h;
+                    if (r0 >= a.R) continue;
+                    float *dst = a.y + (size_t)(a.out_base + p) * (a.ldy ? a.ldy : a.R) + r0;
+                    *(f32x4 *)dst = (f32x4){acc[0][i][c][4 * aa], acc[0][i][c][4 * aa + 1],
+                                            acc[0][i][c][4 * aa + 2], acc[0][i][c][4 * aa + 3]};
+                }
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ latent norm
 // The latent form's aggregates (agg [T][X], one workgroup per token): RMSNorm with the
 // latent norm weights (k3_rmsnorm, k3_ops.c:132-140 and :1946; double sum of squares, inv
@@ -918,6 +1236,12 @@ static void launch_dn(const PfGemmArgs &a, unsigned grid, hipStream_t s)
                        dim3(NW * WAVE), 0, s, a);
 }
 
+// MXFP8 mode tiles: small class 32 tokens, large class 64; four waves a workgroup, gate/up
+// 128 rows (one 32-row tile a wave), down 256 (two)
+#define MX_CT_S 1
+#define MX_CT_B 2
+#define MX_NW   4
+
 static inline unsigned round8(size_t n) { return (unsigned)((n + 7) & ~(size_t)7); }
 
 static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, const void *x,
@@ -1002,10 +1326,15 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     PfScanArgs sa;
     sa.counts = B->counts; sa.E = E; sa.offsets = B->offsets; sa.cursor = B->cursor;
     sa.tb[0] = B->tb_gu; sa.tb[1] = B->tb_dn;
-    sa.tpb_s[0] = GU_CT32_S * 32 / HLr; sa.tpb_b[0] = GU_CT32_B * 32 / HLr;
-    sa.nrb_s[0] = cdiv(I, NW_S * GU_RT32 * 32); sa.nrb_b[0] = cdiv(I, NW_B * GU_RT32 * 32);
-    sa.tpb_s[1] = DN_CT32_S * 32 / 2; sa.tpb_b[1] = DN_CT32_B * 32 / 2;
-    sa.nrb_s[1] = cdiv(X, NW_S * DN_RT32 * 32); sa.nrb_b[1] = cdiv(X, NW_B * DN_RT32 * 32);
+    const bool mx = L->pf_mode == K3X_PREFILL_MXFP8;
+    sa.tpb_s[0] = mx ? MX_CT_S * 32 : GU_CT32_S * 32 / HLr;
+    sa.tpb_b[0] = mx ? MX_CT_B * 32 : GU_CT32_B * 32 / HLr;
+    sa.nrb_s[0] = cdiv(I, NW_S * GU_RT32 * 32);
+    sa.nrb_b[0] = cdiv(I, (mx ? MX_NW : NW_B) * GU_RT32 * 32);
+    sa.tpb_s[1] = mx ? MX_CT_S * 32 : DN_CT32_S * 32 / 2;
+    sa.tpb_b[1] = mx ? MX_CT_B * 32 : DN_CT32_B * 32 / 2;
+    sa.nrb_s[1] = cdiv(X, NW_S * DN_RT32 * 32);
+    sa.nrb_b[1] = cdiv(X, (mx ? MX_NW : NW_B) * DN_RT32 * 32);
     hipLaunchKernelGGL(pf_scan, dim3(1), dim3(1024), 0, s, sa);
     if ((rc = launch_ok())) PF_RET(rc);
     hipLaunchKernelGGL(pf_scatter, dim3(cdiv(TK, PF_NT)), dim3(PF_NT), 0, s, B->idx, B->wt, TK, K,
@@ -1028,13 +1357,25 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         else
             hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_z), dim3(PF_NT), 0, s, zg);
         if ((rc = launch_ok())) PF_RET(rc);
-        hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (X / 8), PF_NT)), dim3(PF_NT), 0, s,
-                           B->zf, 0, T, X, X, B->zhl, (int *)NULL, 0);
-        if ((rc = launch_ok())) PF_RET(rc);
+        if (!mx) {
+            hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (X / 8), PF_NT)), dim3(PF_NT), 0, s,
+                               B->zf, 0, T, X, X, B->zhl, (int *)NULL, 0);
+            if ((rc = launch_ok())) PF_RET(rc);
+        }
         rsrc = B->zhl;
     }
-    hipLaunchKernelGGL(pf_permute, dim3(cdiv((size_t)HLr * (X / 8) * TK, PF_NT)), dim3(PF_NT), 0, s,
-                       rsrc, T, X / 8, HLr, B->perm_tok, TK, B->xp);
+    // MXFP8 mode: the routed input quantised in permuted order, codes then scales in xp;
+    // the gate/up output's codes then scales in act
+    uint8_t *xq8 = (uint8_t *)B->xp, *xs8 = xq8 + (((size_t)TK * X + 255) & ~(size_t)255);
+    uint8_t *aq8 = (uint8_t *)B->act, *as8 = aq8 + (((size_t)TK * I + 255) & ~(size_t)255);
+    if (mx) {
+        const void *src = L->lat ? (const void *)B->zf : x;
+        hipLaunchKernelGGL(pf_mx8_rows, dim3(cdiv((size_t)TK * (X / 32), PF_NT)), dim3(PF_NT), 0, s,
+                           src, L->lat ? 0 : x_bf16, X, X, B->perm_tok, TK, xq8, xs8);
+    } else {
+        hipLaunchKernelGGL(pf_permute, dim3(cdiv((size_t)HLr * (X / 8) * TK, PF_NT)), dim3(PF_NT), 0, s,
+                           rsrc, T, X / 8, HLr, B->perm_tok, TK, B->xp);
+    }
     if ((rc = launch_ok())) PF_RET(rc);
 
     // grids: upper bounds of each list (a small expert has one column block; large ones
@@ -1058,10 +1399,16 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     g.pw = B->perm_w; g.act = B->act; g.arows = TK; g.out_base = 0;
     g.b1 = L->b1; g.b2 = L->b2;
     const bool ex_gu = (L->special & 3) != 0;
+    if (mx) {
+        g.b8 = xq8; g.b8s = (const uint32_t *)xs8; g.o8 = aq8; g.o8s = as8;
+    }
     PfGemmArgs gb = g;
     g.ntile = B->tb_gu + E;
     gb.ntile = B->tb_gu + 2 * E + 1; gb.dbase = B->tb_gu + E;
-    if (ex_gu) {
+    if (mx) {
+        hipLaunchKernelGGL((pf_gemm_mx<2, GU_RT32, MX_CT_B, true, MX_NW>), dim3(grid_b[0]), dim3(MX_NW * WAVE), 0, s, gb);
+        hipLaunchKernelGGL((pf_gemm_mx<2, GU_RT32, MX_CT_S, true, MX_NW>), dim3(grid_s[0]), dim3(MX_NW * WAVE), 0, s, g);
+    } else if (ex_gu) {
         if (HLr == 1) { launch_gu<true, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<true, 1, GU_CT32_S, NW_S>(g, grid_s[0], s); }
         else          { launch_gu<true, 2, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<true, 2, GU_CT32_S, NW_S>(g, grid_s[0], s); }
     } else {
@@ -1077,10 +1424,14 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     d.R = X; d.K = I; d.desc = (const int4 *)B->desc_dn;
     d.bsrc = B->act; d.brows = TK; d.perm = NULL; d.row_base = 0;
     d.y = B->y; d.out_base = 0;
+    if (mx) { d.b8 = aq8; d.b8s = (const uint32_t *)as8; }
     PfGemmArgs db = d;
     d.ntile = B->tb_dn + E;
     db.ntile = B->tb_dn + 2 * E + 1; db.dbase = B->tb_dn + E;
-    if (L->special & 4) { launch_dn<true, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<true, DN_CT32_S, NW_S>(d, grid_s[1], s); }
+    if (mx) {
+        hipLaunchKernelGGL((pf_gemm_mx<1, DN_RT32, MX_CT_B, false, MX_NW>), dim3(grid_b[1]), dim3(MX_NW * WAVE), 0, s, db);
+        hipLaunchKernelGGL((pf_gemm_mx<1, DN_RT32, MX_CT_S, false, MX_NW>), dim3(grid_s[1]), dim3(MX_NW * WAVE), 0, s, d);
+    } else if (L->special & 4) { launch_dn<true, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<true, DN_CT32_S, NW_S>(d, grid_s[1], s); }
     else                { launch_dn<false, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<false, DN_CT32_S, NW_S>(d, grid_s[1], s); }
     if ((rc = launch_ok())) PF_RET(rc);
 

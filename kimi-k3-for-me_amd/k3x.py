@@ -18,6 +18,9 @@ LIB_PATH = os.path.join(HERE, "lib", "libk3x.so")
 
 K3X_F32 = 0
 K3X_BF16 = 1
+# prefill arithmetic (k3x_moe_layer_set_prefill_mode)
+K3X_PREFILL_EXACT = 0
+K3X_PREFILL_MXFP8 = 1
 DECODE_MAX_T = 8
 
 (STREAM_ROUTER, STREAM_BIAS, STREAM_X, STREAM_SH1, STREAM_SH3, STREAM_SH2, STREAM_NORM,
@@ -33,7 +36,7 @@ EXPORTS = [
     "k3x_moe_layer_last_ms", "k3x_stack_create", "k3x_stack_forward", "k3x_stack_destroy",
     "k3x_moe_layer_check", "k3x_moe_layer_set_route_wait",
     "k3x_attn_res", "k3x_moe_half", "k3x_moe_layer_reserve", "k3x_moe_layer_dequant",
-    "k3x_moe_prefill_noalloc", "k3x_moe_layer_trace",
+    "k3x_moe_prefill_noalloc", "k3x_moe_layer_trace", "k3x_moe_layer_set_prefill_mode",
     # include/k3x_store.h
     "k3x_store_open", "k3x_store_close", "k3x_store_count", "k3x_store_shards",
     "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
@@ -127,6 +130,7 @@ def lib():
         L.k3x_moe_layer_bytes.restype = C.c_size_t
         L.k3x_moe_layer_read_expert.argtypes = [vp, i] + [vp] * 6
         L.k3x_moe_layer_reserve.argtypes = [vp, i]
+        L.k3x_moe_layer_set_prefill_mode.argtypes = [vp, i]
         L.k3x_moe_layer_dequant.argtypes = [vp, i, i, vp]
         L.k3x_moe_forward.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
         L.k3x_moe_prefill_noalloc.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
@@ -334,6 +338,10 @@ class MoELayer:
     # -- calls --------------------------------------------------------------------
     def nbytes(self):
         return lib().k3x_moe_layer_bytes(self.h)
+
+    def set_prefill_mode(self, mode):
+        """K3X_PREFILL_EXACT (default) or the opt-in K3X_PREFILL_MXFP8."""
+        _check(lib().k3x_moe_layer_set_prefill_mode(self.h, mode), "k3x_moe_layer_set_prefill_mode")
 
     def reserve(self, max_T):
         """Prefill buffers for calls of up to max_T tokens (needed before capturing one)."""

@@ -661,3 +661,154 @@ int ko_threads(void)
     return 1;
 #endif
 }
+
+/* ------------------------------------------- MXFP8-activation prefill mode ---- */
+/* The opt-in prefill mode of the device library (K3X_PREFILL_MXFP8) has no counterpart
+ * in the reference, whose expert products take fp32 activations.  Its oracle is the
+ * reference's MoE arithmetic (k3_moe, k3_ops.c:1862-1952) with one documented change:
+ * every activation row entering a routed expert product is first quantised to MXFP8
+ * (OCP Microscaling Formats v1.0: blocks of 32 consecutive elements sharing one E8M0
+ * scale 2^X, elements in FP8 E4M3, the "FN" encoding: bias 7, no infinities, 448 the
+ * largest finite value, 0x7F/0xFF NaN), and the expert products are the exact
+ * products of the MXFP4 weights (E2M1 x E8M0 as stored) with those elements, summed in
+ * double and rounded to float once.  The quantisation:
+ *   - X is the least integer with max|v| <= 448 * 2^X over the block's finite elements
+ *     (max|v| = f * 2^E with f in [1, 2): X = E - 8, or E - 7 when f > 1.75), clamped
+ *     to [-127, 127]; a block without a non-zero finite element has X = -127;
+ *   - each finite element is v * 2^-X (exact) rounded to the nearest E4M3 value, ties
+ *     to the even code; a non-finite element is the NaN code 0x7F (sign kept);
+ *   - the scale byte is X + 127.
+ * Where the quantisation happens: the routed experts' input (x, or z = down . x in a
+ * LatentMoE layer) per token, and each expert's activation h = w_j * SiTU(gate, up)
+ * with the routing weight w_j folded in before quantising (the device applies it in
+ * the gate/up epilogue); the down products are then summed in float in top-k order
+ * without a further weight.  Router, shared expert and latent projections are the
+ * exact path's.  Pinned in tests/test_oracle_mx.py: the E4M3 rounding against a
+ * brute-force nearest search over all 253 finite codes, the scale rule against its
+ * definition, the product against dequantise-then-float64-dot, the identity on inputs
+ * that MXFP8 represents exactly (the layer then equals ko_moe to float rounding). */
+
+float ko_e4m3(int code)
+{
+    const int s = code & 0x80, e = (code >> 3) & 15, m = code & 7;
+    float v;
+    if (e == 15 && m == 7) return s ? -NAN : NAN;
+    if (e == 0) v = ldexpf((float)m, -9);
+    else        v = ldexpf((float)(8 + m), e - 10);
+    return s ? -v : v;
+}
+
+/* |v| <= 448 (finite) to the nearest E4M3 value, ties to the even code. */
+int ko_e4m3_rne(float v)
+{
+    const int sign = signbit(v) ? 0x80 : 0;
+    const float a = fabsf(v);
+    if (a < 0x1p-6f) {                              /* subnormal steps of 2^-9 */
+        const int m = (int)nearbyintf(a * 512.0f);  /* 0 .. 8; 8 is 2^-6, code 0x08 */
+        return sign | m;
+    }
+    int E;
+    frexpf(a, &E);
+    E -= 1;                                         /* a = f * 2^E, f in [1, 2) */
+    const int m = (int)nearbyintf(ldexpf(a, 3 - E)); /* 8 .. 16 */
+    if (m == 16) return sign | ((E + 8) << 3);
+    return sign | ((E + 7) << 3) | (m - 8);
+}
+
+int ko_mx8_scale(const float *v, int n)
+{
+    float amax = 0.0f;
+    for (int i = 0; i < n; i++)
+        if (isfinite(v[i]) && fabsf(v[i]) > amax) amax = fabsf(v[i]);
+    if (amax == 0.0f) return 0;
+    uint32_t b;
+    memcpy(&b, &amax, 4);
+    int X = (int)((b >> 23) & 255u) - 127 - 8 + ((b & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+    if (X < -127) X = -127;
+    if (X > 127) X = 127;
+    return X + 127;
+}
+
+void ko_mx8_quant(uint8_t *codes, uint8_t *scales, const float *x, int n)
+{
+    for (int b = 0; b < n / 32; b++) {
+        const float *v = x + 32 * b;
+        const int sb = ko_mx8_scale(v, 32);
+        scales[b] = (uint8_t)sb;
+        for (int i = 0; i < 32; i++) {
+            if (!isfinite(v[i])) { codes[32 * b + i] = (uint8_t)((signbit(v[i]) ? 0x80 : 0) | 0x7F); continue; }
+            codes[32 * b + i] = (uint8_t)ko_e4m3_rne(ldexpf(v[i], 127 - sb));
+        }
+    }
+}
+
+void ko_mx8_dequant(double *y, const uint8_t *codes, const uint8_t *scales, int n)
+{
+    for (int i = 0; i < n; i++) y[i] = ldexp((double)ko_e4m3(codes[i]), (int)scales[i / 32] - 127);
+}
+
+/* y[r] = sum_i W[r][i] * xq[i], exact products summed in double (ascending i), rounded
+ * to float once; W MXFP4 (E2M1 codes, E8M0 scale per 32), xq MXFP8 (n % 32 == 0). */
+void ko_matmul_mx(float *y, const uint8_t *xc, const uint8_t *xs, const uint8_t *packed,
+                  const uint8_t *wscales, int in, int rows)
+{
+    double *xd = (double *)malloc((size_t)in * sizeof(double));
+    if (!xd) abort();
+    ko_mx8_dequant(xd, xc, xs, in);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) if (rows > 64)
+#endif
+    for (int r = 0; r < rows; r++) {
+        const uint8_t *pr = packed + (size_t)r * (in / 2), *sr = wscales + (size_t)r * (in / 32);
+        double acc = 0.0;
+        for (int i = 0; i < in; i++) {
+            const int by = pr[i >> 1];
+            const int nib = (i & 1) ? (by >> 4) : (by & 15);
+            const double wv = ldexp((double)E2M1[nib], (int)sr[i / 32] - 127);
+            acc += wv * xd[i];
+        }
+        y[r] = (float)acc;
+    }
+    free(xd);
+}
+
+long ko_moe_mx(float *out, const float *x, int T, const ko_cfg *c, const ko_weights *w,
+               int *idx, float *wt)
+{
+    const int H = c->hidden, K = c->topk, L = latent_of(c), I = c->moe_inter;
+    if (!w->get || c->group != 32 || L % 32 || I % 32) return -1;
+    long drops = 0;
+    moe_tmp m;
+    uint8_t *zc = (uint8_t *)malloc((size_t)L), *zs = (uint8_t *)malloc((size_t)L / 32);
+    uint8_t *hc = (uint8_t *)malloc((size_t)I), *hs = (uint8_t *)malloc((size_t)I / 32);
+    if (!zc || !zs || !hc || !hs || moe_tmp_alloc(&m, c)) abort();
+    for (int t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * H;
+        float *ot = out + (size_t)t * H;
+        float *acc = c->latent > 0 ? m.acc : ot;
+        int *it = idx + (size_t)t * K;
+        float *wtt = wt + (size_t)t * K;
+        const float *z = latent_in(xt, c, w, m.z);
+        ko_mx8_quant(zc, zs, z, L);
+        ko_router(it, wtt, xt, w->gate, w->bias, H, c->n_experts, K, c->renorm,
+                  c->routed_scale);
+        for (int i = 0; i < L; i++) acc[i] = 0.0f;
+        for (int j = 0; j < K; j++) {
+            ko_expert q;
+            if (expert_get(w, it[j], &q) != 0) { drops++; continue; }
+            ko_matmul_mx(m.gu,     zc, zs, q.p1, q.s1, L, I);
+            ko_matmul_mx(m.gu + I, zc, zs, q.p3, q.s3, L, I);
+            ko_situ_glu(m.act, m.gu, I, c->situ_b1, c->situ_b2);
+            const float wj = wtt[j];
+            for (int i = 0; i < I; i++) m.act[i] = wj == 0.0f ? 0.0f : wj * m.act[i];
+            ko_mx8_quant(hc, hs, m.act, I);
+            ko_matmul_mx(m.edn, hc, hs, q.p2, q.s2, I, L);
+            for (int i = 0; i < L; i++) acc[i] += m.edn[i];
+        }
+        latent_out(ot, acc, c, w);
+        shared_add(ot, xt, c, w, &m);
+    }
+    moe_tmp_free(&m);
+    free(zc); free(zs); free(hc); free(hs);
+    return drops;
+}

@@ -113,6 +113,20 @@ long ko_moe_half(float *h, float *pref, const float *blocks, int maxb, int nb,
 /* ---- synthetic inputs ---------------------------------------------------------- */
 /* The counter-based generator shared by the tests and the product's synthetic-layer
  * builder: value i of a stream depends only on (seed, layer, stream, sub, i). */
+/* The opt-in MXFP8-activation prefill mode (no reference counterpart; the definition
+ * is at the top of its section in k3x_oracle.c): E4M3 decode and round-to-nearest-even
+ * (|v| <= 448), the block scale byte, MXFP8 quantisation and dequantisation of n % 32 == 0
+ * elements, the MXFP4 x MXFP8 product, and the whole layer (drops counted as ko_moe). */
+float ko_e4m3(int code);
+int   ko_e4m3_rne(float v);
+int   ko_mx8_scale(const float *v, int n);
+void  ko_mx8_quant(uint8_t *codes, uint8_t *scales, const float *x, int n);
+void  ko_mx8_dequant(double *y, const uint8_t *codes, const uint8_t *scales, int n);
+void  ko_matmul_mx(float *y, const uint8_t *xc, const uint8_t *xs, const uint8_t *packed,
+                   const uint8_t *wscales, int in, int rows);
+long  ko_moe_mx(float *out, const float *x, int T, const ko_cfg *c, const ko_weights *w,
+                int *idx, float *wt);
+
 uint64_t ko_mix64(uint64_t z);
 uint64_t ko_key(uint64_t seed, int layer, int stream, int sub);
 uint64_t ko_draw(uint64_t key, uint64_t i);

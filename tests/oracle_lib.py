@@ -93,6 +93,16 @@ def oracle():
         lib.ko_moe_prefill.argtypes = [F32P, F32P, C.c_int, C.POINTER(KoCfg),
                                        C.POINTER(KoWeights), I32P, F32P,
                                        C.POINTER(C.c_long)]
+        lib.ko_e4m3.restype = C.c_float
+        lib.ko_e4m3.argtypes = [C.c_int]
+        lib.ko_e4m3_rne.argtypes = [C.c_float]
+        lib.ko_mx8_scale.argtypes = [F32P, C.c_int]
+        lib.ko_mx8_quant.argtypes = [U8P, U8P, F32P, C.c_int]
+        lib.ko_mx8_dequant.argtypes = [C.POINTER(C.c_double), U8P, U8P, C.c_int]
+        lib.ko_matmul_mx.argtypes = [F32P, U8P, U8P, U8P, U8P, C.c_int, C.c_int]
+        lib.ko_moe_mx.restype = C.c_long
+        lib.ko_moe_mx.argtypes = [F32P, F32P, C.c_int, C.POINTER(KoCfg), C.POINTER(KoWeights),
+                                  I32P, F32P]
         lib.ko_attn_res.argtypes = [F32P, F32P, F32P, C.c_int, C.c_int, C.c_float]
         lib.ko_moe_half.restype = C.c_long
         lib.ko_moe_half.argtypes = [F32P, F32P, F32P, C.c_int, C.c_int, F32P, F32P, C.c_float,

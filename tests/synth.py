@@ -189,6 +189,19 @@ class Layer:
                                 ptr(idx, I32P), ptr(wt, F32P))
         return out, idx, wt, drops
 
+    def oracle_moe_mx(self, x, fail=None):
+        """The oracle of the MXFP8-activation prefill mode (ko_moe_mx)."""
+        x = np.ascontiguousarray(x, np.float32)
+        T = x.shape[0]
+        out = np.empty_like(x)
+        idx = np.empty((T, self.K), np.int32)
+        wt = np.empty((T, self.K), np.float32)
+        cfg = self.ko_cfg()
+        w, cb, keep = self._weights(fail)
+        drops = oracle().ko_moe_mx(ptr(out, F32P), ptr(x, F32P), T, C.byref(cfg), C.byref(w),
+                                   ptr(idx, I32P), ptr(wt, F32P))
+        return out, idx, wt, drops
+
     def all_experts(self):
         return [self.expert(e) for e in range(self.E)]
 

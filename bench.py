@@ -512,7 +512,10 @@ def cpu_baseline(n_tokens=24, min_seconds=10.0):
 
     L = synth.full(seed=1)
     x = L.x(n_tokens, bf16=True, stream_sub=7)
-    ref = ol.ref()
+    # the reference's best build for this host: its AVX-512 paths where the host has
+    # x86-64-v4 (what its -march=native build selects there), else the AVX2 build
+    isa = "x86-64-v4" if ol.ref("x86-64-v4") is not None else "x86-64-v3"
+    ref = ol.ref(isa)
     kind = "reference" if ref is not None else "port"
     # route once to know which experts the sample needs, then generate only those
     idx = np.empty((n_tokens, K), np.int32)
@@ -552,7 +555,22 @@ def cpu_baseline(n_tokens=24, min_seconds=10.0):
             break
     us = float(np.median(times) * 1e6)
     cores = int(ol.oracle().ko_threads())
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    import platform
+    libc = platform.libc_ver()
     return {"value": round(us, 1), "unit": "us/token", "cores": cores, "kind": kind,
+            "isa": isa if kind == "reference" else "x86-64-v3 (oracle port)",
+            "build": "gcc -O3 -fopenmp -ffp-contract=off -march=" + isa
+                     + " (oracle/Makefile, the reference's flags but -march)",
+            "cpu_model": cpu_model, "glibc": f"{libc[0]} {libc[1]}",
             "sample": f"{len(times)} layer calls over {n_tokens} distinct bf16 tokens of the "
                       f"same seeded layer ({len(need)} experts generated), median per token, "
                       f"OpenMP threads {cores}"}

@@ -12,6 +12,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "libk3x_oracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libk3ref.so")
+REF_V4_SO = os.path.join(ROOT, "oracle", "_ref", "libk3ref_v4.so")
 
 F32P = C.POINTER(C.c_float)
 U8P = C.POINTER(C.c_uint8)
@@ -132,14 +133,33 @@ def oracle():
     return _oracle
 
 
-_ref = None
+_ref = {}
+
+AVX512 = ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl")
 
 
-def ref():
-    """The compiled reference, or None when oracle/_ref was not built."""
-    global _ref
-    if _ref is None:
-        lib = _load(REF_SO)
+def host_has_x86_64_v4():
+    """The host CPU has the AVX-512 subsets x86-64-v4 requires (from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    fl = set(line.split(":", 1)[1].split())
+                    return all(x in fl for x in AVX512)
+    except OSError:
+        pass
+    return False
+
+
+def ref(isa="x86-64-v3"):
+    """The compiled reference, or None when oracle/_ref was not built: the x86-64-v3
+    build (AVX2 + FMA), or with isa="x86-64-v4" the AVX-512 build (None where the
+    host lacks AVX-512)."""
+    path = REF_V4_SO if isa == "x86-64-v4" else REF_SO
+    if isa == "x86-64-v4" and not host_has_x86_64_v4():
+        return None
+    if path not in _ref:
+        lib = _load(path)
         if lib is None:
             return None
         lib.k3_router.argtypes = [I32P, F32P, F32P, F32P, F32P, C.c_int, C.c_int, C.c_int,
@@ -164,5 +184,5 @@ def ref():
         lib.refdrv_k2_tokens.argtypes = [F32P, F32P, C.c_int, C.c_int, C.c_int, C.c_int,
                                          C.c_int, C.c_int, C.c_float, C.c_int, F32P, F32P,
                                          C.POINTER(KoExpert), U16P, U16P, U16P, I32P, F32P]
-        _ref = lib
-    return _ref
+        _ref[path] = lib
+    return _ref[path]

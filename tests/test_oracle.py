@@ -445,3 +445,28 @@ def test_generator_reproducible():
     cd = synth.codes(100000, synth.key(1, 0, 10, 0))
     nib = np.concatenate([cd & 15, cd >> 4])
     assert np.bincount(nib, minlength=16).min() > 100000 * 2 / 16 * 0.9
+
+
+def test_reference_avx512_build_bitwise():
+    """The reference compiled for x86-64-v4 (its AVX-512 paths, k3_ops.c:457, :2752,
+    :3134, the build the CPU baseline uses on such hosts) gives the same bits as the
+    oracle: the GEMV on cancelling data and the whole tiny layer, decode and prefill."""
+    import oracle_lib as ol
+    r4 = ol.ref("x86-64-v4")
+    if r4 is None:
+        pytest.skip("no AVX-512 host, or oracle/_ref not built")
+    rng = np.random.default_rng(9)
+    rows, n = 96, 3584
+    p = cancelling_codes(rng.integers(0, 256, (rows, n // 2), dtype=np.uint8), n)
+    s = rng.integers(118, 130, (rows, n // 32), dtype=np.uint8)
+    x = cancelling(rows, n, rng)
+    y = mx_gemv(x, p, s)
+    r = np.empty(rows, np.float32)
+    r4.k3_matmul_mxfp4(ptr(r, F32P), ptr(x, F32P), ptr(p, U8P), ptr(s, U8P), n, rows, 32)
+    assert np.array_equal(y.view(np.uint32), r.view(np.uint32))
+    L = synth.tiny(seed=2)
+    xt = L.x(70, bf16=False)
+    for prefill in (False, True):
+        o, _, _, _ = L.oracle_moe(xt, prefill=prefill)[:4]
+        ro, _, _, rd, _ = ref_moe(r4, L, xt, prefill=prefill)
+        assert rd == 0 and np.array_equal(o.view(np.uint32), ro.view(np.uint32))

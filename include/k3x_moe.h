@@ -84,12 +84,22 @@ typedef struct k3x_expert_q {
     const unsigned char *p2, *s2;
 } k3x_expert_q;
 
-/* ---- expert supplier: the get() half of K3ExpertSrc (k3.h:521-544) -----------------
+/* ---- expert supplier: K3ExpertSrc (k3.h:521-544) ----------------------------------
  * get() returns 0 and fills *out, or non-zero when the expert cannot be fetched. The
- * pointers need stay valid only until get() is called again. */
+ * pointers need stay valid only until get() is called again.
+ * getmany() (optional, may be NULL; k3.h:527-539): bring experts[0 .. n-1] resident with
+ *   their reads issued together; returns how many are resident, or -1.  A short return
+ *   is not an error: get() then fetches the rest itself.  Called before the get()s of a
+ *   batch of experts (a layer's upload, 16 at a time).
+ * resident() (optional, may be NULL; k3.h:540-542): 1 when the expert is resident (get()
+ *   would read nothing), filling *out when out != NULL.
+ * Zero the struct before setting what you have: the two optional members come last, so
+ * a caller written for get/ctx alone stays valid when it zeroes the struct. */
 typedef struct k3x_expert_src {
     int  (*get)(struct k3x_expert_src *self, int layer, int expert, k3x_expert_q *out);
     void *ctx;
+    int  (*getmany)(struct k3x_expert_src *self, int layer, const int *experts, int n);
+    int  (*resident)(struct k3x_expert_src *self, int layer, int expert, k3x_expert_q *out);
 } k3x_expert_src;
 
 /* ---- a layer's weights: K3MoeW (k3.h:546-569) with bf16 trunk matrices --------------
@@ -189,6 +199,19 @@ int  k3x_moe_prefill_noalloc(k3x_moe_layer *L, float *out, const void *x, int x_
  * activations).  No counterpart in the reference.  Returns K3X_E_SHAPE for a layer
  * holding an E8M0 scale byte outside 1..252 (the matrix cores read 255 as NaN where the
  * reference reads zero) and K3X_E_ARG for an unknown mode. */
+/* Cache-only (draft) routing, K3MoeW.cache_only (k3.h:564-568, k3_ops.c:1884-1926):
+ * on = 1 makes every later forward call keep, per token, only those of its top-k experts
+ * that are resident, in top-k order, with their weights divided by their float sum (so a
+ * draft reads no expert bytes that are not already in place); idx/wt then hold the kept
+ * experts first and the router's entries after them, as the reference leaves its arrays.
+ * resident: a host array [n_experts] (copied; non-zero = resident), or NULL: for a cached
+ * layer the experts in its HBM slots at each call, for a resident layer every expert
+ * (which keeps the routing and renormalises the weights to sum 1).  Calls run the decode
+ * path in groups of up to 8 tokens with a host step after each selection, as the
+ * reference runs such calls token by token (:2018); k3x_moe_prefill_noalloc and the
+ * stacked graph refuse such a layer (K3X_E_ARG).  on = 0 restores the exact routing. */
+int  k3x_moe_layer_set_cache_only(k3x_moe_layer *L, int on, const unsigned char *resident);
+
 #define K3X_PREFILL_EXACT 0
 #define K3X_PREFILL_MXFP8 1
 int  k3x_moe_layer_set_prefill_mode(k3x_moe_layer *L, int mode);

@@ -129,10 +129,11 @@ int  k3x_moe_layer_create_from_store(const k3x_cfg *c, const k3x_moe_w *w, k3x_s
  * names resident, reading a miss's run from the store (pinned buffer, copy, re-layout
  * into the least recently used unpinned slot the call does not name), then runs the
  * expert products through the slot table.  The results are those of a layer with every
- * expert resident.  Cached layers serve decode calls only (prefill and the stacked
- * graph return K3X_E_ARG) and a call whose tokens name more experts than there are slots
- * returns K3X_E_SHAPE.  A miss that cannot be read counts in k3x_expert_drops and fails
- * the call with K3X_E_DROP. */
+ * expert resident.  Cached layers run a prefill call as decode-path calls of 8 tokens
+ * (k3x_moe_prefill_noalloc and the stacked graph return K3X_E_ARG), and a call whose
+ * tokens name more experts than there are slots returns K3X_E_SHAPE.  The misses of a
+ * call are read together (as k3x_cache_getmany).  A miss that cannot be read counts in
+ * k3x_expert_drops and fails the call with K3X_E_DROP. */
 typedef struct k3x_cache_stat {
     int                nslot;        /* slots in the arena                         */
     int                resident;     /* slots holding an expert                    */
@@ -151,6 +152,16 @@ int  k3x_cache_stats(const k3x_moe_layer *L, k3x_cache_stat *st);
 /* pin = 1: make the expert resident (a miss) and never evict it; 0: release it.  At
  * least topk slots stay unpinned (K3X_E_SHAPE otherwise). */
 int  k3x_cache_pin(k3x_moe_layer *L, int expert, int pin);
+/* cache_getmany's counterpart (k3_cache.c:394-512): make experts[0 .. n-1] resident, the
+ * misses read from the store together (up to 8 at once, each by its own thread into its
+ * own pinned buffer), evicting least recently used unpinned slots that the list does not
+ * name.  Returns the number of listed experts now resident, K3X_E_SHAPE when n exceeds
+ * the slots, or K3X_E_DROP when a run could not be read (the others are loaded).
+ * Synchronous. */
+int  k3x_cache_getmany(k3x_moe_layer *L, const int *experts, int n);
+/* 1 when the expert is resident in the layer's HBM (every expert of a layer made without
+ * a cache), 0 when not: the resident() of the reference's supplier (k3.h:540-542). */
+int  k3x_cache_resident(const k3x_moe_layer *L, int expert);
 
 #ifdef __cplusplus
 }

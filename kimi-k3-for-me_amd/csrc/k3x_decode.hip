@@ -1539,14 +1539,15 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
         else                          launch_k2<16>(a2, ex, st2, g, l2, s);
     };
     a2.slot = L->nslot ? L->slot_dev : NULL;
-    if (L->nslot) {
-        // expert cache: the selection alone first (workgroup 0 of k2 on a grid of one, or
-        // k1_zdown's in the latent form), then the experts it names made resident
+    if (L->nslot || L->cache_only) {
+        // expert cache or cache-only routing: the selection alone first (workgroup 0 of
+        // k2 on a grid of one, or k1_zdown's in the latent form), then the host's part:
+        // the draft filter, and the experts it names made resident
         if (!L->lat) {
             k2_launch(false, dim3(1));
             if ((rc = launch_ok())) return rc;
         }
-        if ((rc = k3x_cache_fill(L, s))) return rc;
+        if ((rc = k3x_route_host(L, s, T, idx, wt))) return rc;
         a2.sel_done = 1;
     }
     const bool ex2 = (L->special & 3) != 0;

@@ -55,6 +55,7 @@ extern "C" {
 #define K3X_ROUTE_WAIT_DEFAULT 5000000ull  /* 50 ms at 100 MHz: decode's bound on the wait */
 #define K3X_PF_CHUNK     4096    /* prefill: most tokens per pipeline run */
 #define K3X_NOALLOC_BYTES (64u << 20)  /* the no-allocation prefill's static device array */
+#define K3X_CACHE_IO     8       /* expert-cache misses read from the store concurrently */
 /* byte sizes of the tiled formats */
 static inline size_t k3x_fp4_tile_bytes(int K)
 {
@@ -175,14 +176,24 @@ struct k3x_moe_layer {
     uint64_t  clock, hits, misses, evictions, bytes_read;
     struct k3x_store *st;         /* where misses are read from                       */
     int       st_layer;
-    unsigned char *c_hbuf;        /* pinned host buffer of one expert run             */
-    uint8_t  *c_dbuf;             /* device staging of one expert run                 */
-    int      *c_route;            /* pinned host copy of the routing summary's head   */
+    unsigned char *c_hbuf[K3X_CACHE_IO];  /* pinned host buffers, one expert run each  */
+    uint8_t  *c_dbuf[K3X_CACHE_IO];       /* device staging, one expert run each        */
+    int       c_nio;              /* staging pairs: misses read together               */
+    int      *c_route;            /* pinned host copy of the routing summary (head,
+                                     unique list, per-token weights)                 */
     int       c_dirty;            /* slot_of changed since slot_dev was last written   */
+    /* cache-only (draft) routing: each token keeps its top-k experts that are resident */
+    int       cache_only;
+    unsigned char *res_mask;      /* [E] resident experts, or NULL: the HBM slots of a
+                                     cached layer (every expert of a resident layer)   */
+    int      *c_sel;              /* pinned [2][DECODE_MAX_T * topk]: the selection's
+                                     indices, then its weights' bits                  */
 };
 
-/* expert cache: make the unique experts of the published routing resident (decode) */
-int k3x_cache_fill(k3x_moe_layer *L, void *stream);
+/* After a decode call's selection (published in the route): with cache-only routing,
+ * filter each token's experts to the resident ones and rewrite the route and the
+ * caller's idx/wt; for a cached layer, make the named experts resident. */
+int k3x_route_host(k3x_moe_layer *L, void *stream, int T, int *uidx, float *uwt);
 
 /* ---- launchers (k3x_kernels.hip), all return 0 or K3X_E_HIP ---------------------- */
 int k3x_dev_check(int device);

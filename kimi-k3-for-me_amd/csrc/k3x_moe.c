@@ -158,8 +158,12 @@ static void layer_free(k3x_moe_layer *L)
         if (p[i]) hipFree(p[i]);
     for (int i = 0; i < L->pf.nretired; i++) hipFree(L->pf.retired[i]);
     if (L->slot_dev) hipFree(L->slot_dev);
-    if (L->c_dbuf) hipFree(L->c_dbuf);
-    if (L->c_hbuf) hipHostFree(L->c_hbuf);
+    for (int i = 0; i < K3X_CACHE_IO; i++) {
+        if (L->c_dbuf[i]) hipFree(L->c_dbuf[i]);
+        if (L->c_hbuf[i]) hipHostFree(L->c_hbuf[i]);
+    }
+    if (L->c_sel) hipHostFree(L->c_sel);
+    free(L->res_mask);
     if (L->c_route) hipHostFree(L->c_route);
     free(L->slot_of); free(L->key_of); free(L->used_at); free(L->pinned);
     for (int i = 0; i < 8; i++)
@@ -324,6 +328,14 @@ int k3x_moe_layer_create(const k3x_cfg *c, const k3x_moe_w *w, int device,
     HIPCHK(hipMalloc((void **)&stage, 3 * ((size_t)I * X / 2 + (size_t)I * X / 32)));
     for (int e = 0; e < E; e++) {
         k3x_expert_q q;
+        if (w->src && w->src->getmany && e % 16 == 0) {
+            /* the next 16 experts' reads issued together (k3_ops.c:1905-1906); a short
+             * or failed return only means that get() reads the rest itself */
+            int batch[16];
+            const int nb = E - e < 16 ? E - e : 16;
+            for (int i = 0; i < nb; i++) batch[i] = e + i;
+            (void)w->src->getmany(w->src, w->layer, batch, nb);
+        }
         if (w->src) {
             memset(&q, 0, sizeof q);
             if (w->src->get(w->src, w->layer, e, &q) != 0) {
@@ -433,10 +445,16 @@ fail:
 /* ---------------------------------------------------------------- expert cache ---- */
 /* A layer whose expert arena holds nslot experts (k3_cache.c's K3Cache, with the arena in
  * HBM instead of host RAM): after a decode call's selection the experts it names are made
- * resident, a miss reading the expert's run from the store into a pinned buffer, copying
- * it to the device and re-laying it out into a slot; victims are the least recently used
- * unpinned slots not named by the call.  The kernels reach an expert through the slot
- * table (slot_dev). */
+ * resident; the misses are read from the store together (K3X_CACHE_IO at a time, each
+ * into its own pinned buffer, as cache_getmany issues its preads together,
+ * k3_cache.c:394-512), then copied to the device and re-laid out into slots; victims are
+ * the least recently used unpinned slots not named by the call.  The kernels reach an
+ * expert through the slot table (slot_dev). */
+static size_t expert_run_bytes(const k3x_moe_layer *L)
+{
+    return 3 * ((size_t)L->cfg.moe_inter * L->XL / 2 + (size_t)L->cfg.moe_inter * L->XL / 32);
+}
+
 int k3x_moe_layer_create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store *st,
                                 int layer, int nslot, int device, k3x_moe_layer **out)
 {
@@ -446,8 +464,8 @@ int k3x_moe_layer_create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store 
     k3x_moe_layer *L = NULL;
     int rc = new_layer_slots(c, device, nslot, &L);
     if (rc) return rc;
-    const int H = c->hidden, E = c->n_experts, I = c->moe_inter, X = L->XL;
-    const size_t run = 3 * ((size_t)I * X / 2 + (size_t)I * X / 32);
+    const int H = c->hidden, E = c->n_experts;
+    const size_t run = expert_run_bytes(L);
     L->st = st; L->st_layer = layer;
     L->slot_of = (int *)malloc((size_t)E * sizeof(int));
     L->key_of = (int *)malloc((size_t)nslot * sizeof(int));
@@ -456,9 +474,12 @@ int k3x_moe_layer_create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store 
     if (!L->slot_of || !L->key_of || !L->used_at || !L->pinned) { rc = K3X_E_NOMEM; goto fail; }
     for (int e = 0; e < E; e++) L->slot_of[e] = -1;
     for (int i = 0; i < nslot; i++) L->key_of[i] = -1;
-    HIPCHK(hipHostMalloc((void **)&L->c_hbuf, run, hipHostMallocDefault));
+    L->c_nio = nslot < K3X_CACHE_IO ? nslot : K3X_CACHE_IO;
+    for (int i = 0; i < L->c_nio; i++) {
+        HIPCHK(hipHostMalloc((void **)&L->c_hbuf[i], run, hipHostMallocDefault));
+        HIPCHK(hipMalloc((void **)&L->c_dbuf[i], run));
+    }
     HIPCHK(hipHostMalloc((void **)&L->c_route, sizeof(k3x_route), hipHostMallocDefault));
-    HIPCHK(hipMalloc((void **)&L->c_dbuf, run));
     HIPCHK(hipMemcpy(L->slot_dev, L->slot_of, (size_t)E * 4, hipMemcpyHostToDevice));
     HIPCHK(hipMemcpy(L->router, w->gate, (size_t)E * H * 4, hipMemcpyHostToDevice));
     if (w->bias) HIPCHK(hipMemcpy(L->bias, w->bias, (size_t)E * 4, hipMemcpyHostToDevice));
@@ -471,94 +492,253 @@ fail:
     return rc;
 }
 
-/* expert e into a slot (a miss): the least recently used unpinned slot whose expert the
- * current call does not name (want[key] == 0), empty slots first */
-static int cache_load(k3x_moe_layer *L, int e, const unsigned char *want, hipStream_t s)
+/* The least recently used unpinned slot whose expert the call does not name (want[key]
+ * == 0) and that no other miss of the batch took (taken[slot]), empty slots first. */
+static int cache_victim(const k3x_moe_layer *L, const unsigned char *want,
+                        const unsigned char *taken)
 {
-    const int I = L->cfg.moe_inter, X = L->XL;
-    const size_t run = 3 * ((size_t)I * X / 2 + (size_t)I * X / 32);
     int v = -1;
     for (int i = 0; i < L->nslot; i++) {
-        if (L->pinned[i]) continue;
+        if (L->pinned[i] || taken[i]) continue;
         const int k = L->key_of[i];
         if (k >= 0 && want && want[k]) continue;
-        if (k < 0) { v = i; break; }
+        if (k < 0) return i;
         if (v < 0 || L->used_at[i] < L->used_at[v]) v = i;
     }
-    if (v < 0) return K3X_E_SHAPE;              /* every slot pinned or in use */
-    k3x_expert_ref r;
-    if (k3x_store_expert_ref(L->st, L->st_layer, e, &r) || !store_shape_ok(&r, I, X) ||
-        (size_t)r.nbytes > run || k3x_store_expert_load(L->st, &r, L->c_hbuf) != r.nbytes) {
-        k3x_expert_drops++;
-        fprintf(stderr, "EXPERT DROP: layer %d expert %d could not be read from the store\n",
-                L->st_layer, e);
-        return K3X_E_DROP;
-    }
-    const k3x_expert_q q = {L->c_hbuf + r.m[0].p_off, L->c_hbuf + r.m[0].s_off,
-                            L->c_hbuf + r.m[2].p_off, L->c_hbuf + r.m[2].s_off,
-                            L->c_hbuf + r.m[1].p_off, L->c_hbuf + r.m[1].s_off};
-    L->special |= scale_flags(&q, (size_t)I * X / 32);
-    if (L->key_of[v] >= 0) {
-        L->slot_of[L->key_of[v]] = -1;
-        L->key_of[v] = -1;
-        L->c_dirty = 1;
-        L->evictions++;
-    }
-    uint8_t *base = L->experts + (size_t)v * L->expert_bytes;
-    uint8_t *db = L->c_dbuf;
-    int rc = 0;
-    HIPCHK(hipMemcpyAsync(db, L->c_hbuf, (size_t)r.nbytes, hipMemcpyHostToDevice, s));
-    RCCHK(k3x_dev_tile_fp4(base + L->gate_off, db + r.m[0].p_off, db + r.m[0].s_off, I, X, s));
-    RCCHK(k3x_dev_tile_fp4(base + L->up_off, db + r.m[2].p_off, db + r.m[2].s_off, I, X, s));
-    RCCHK(k3x_dev_tile_fp4(base + L->down_off, db + r.m[1].p_off, db + r.m[1].s_off, X, I, s));
-    /* the pinned buffer and the staging area are reused by the next miss */
-    HIPCHK(hipStreamSynchronize(s));
-    L->key_of[v] = e;
-    L->slot_of[e] = v;
-    L->c_dirty = 1;
-    L->used_at[v] = ++L->clock;
-    L->bytes_read += (uint64_t)r.nbytes;
-    L->misses++;
-    return 0;
-fail:
-    return rc;
+    return v;
 }
 
-int k3x_cache_fill(k3x_moe_layer *L, void *stream)
+/* Experts miss[0 .. n-1] (distinct, none resident) into slots: per batch of c_nio, the
+ * victims are chosen, the runs read from the store concurrently (one thread and one
+ * pinned buffer each), then copied and re-laid out on s, one synchronisation a batch.
+ * A run that cannot be read counts in k3x_expert_drops; the others are still loaded. */
+static int cache_load_many(k3x_moe_layer *L, const int *miss, int n, const unsigned char *want,
+                           hipStream_t s)
 {
-    hipStream_t s = (hipStream_t)stream;
-    const size_t head = offsetof(k3x_route, uniq) + sizeof(((k3x_route *)0)->uniq);
-    int rc = 0;
-    HIPCHK(hipMemcpyAsync(L->c_route, L->route, head, hipMemcpyDeviceToHost, s));
-    HIPCHK(hipStreamSynchronize(s));
-    const k3x_route *r = (const k3x_route *)L->c_route;
-    const int nu = r->nu, E = L->cfg.n_experts;
-    if (nu < 0 || nu > K3X_DECODE_MAX_T * K3X_MAX_TOPK) return K3X_E_HIP;
-    if (nu > L->nslot) return K3X_E_SHAPE;      /* more experts than slots in one call */
-    unsigned char *want = (unsigned char *)calloc((size_t)E, 1);
-    if (!want) return K3X_E_NOMEM;
-    for (int u = 0; u < nu; u++) {
-        const int e = r->uniq[u];
-        if (e < 0 || e >= E) { free(want); return K3X_E_HIP; }
-        want[e] = 1;
+    const int I = L->cfg.moe_inter, X = L->XL;
+    const size_t run = expert_run_bytes(L);
+    unsigned char *taken = (unsigned char *)calloc((size_t)L->nslot, 1);
+    if (!taken) return K3X_E_NOMEM;
+    int rc = 0, dropped = 0;
+    for (int b0 = 0; b0 < n && !rc; b0 += L->c_nio) {
+        const int nb = n - b0 < L->c_nio ? n - b0 : L->c_nio;
+        int vic[K3X_CACHE_IO], ok[K3X_CACHE_IO];
+        k3x_expert_ref ref[K3X_CACHE_IO];
+        memset(taken, 0, (size_t)L->nslot);
+        for (int i = 0; i < nb; i++) {
+            vic[i] = cache_victim(L, want, taken);
+            if (vic[i] < 0) { rc = K3X_E_SHAPE; break; }    /* every slot pinned or in use */
+            taken[vic[i]] = 1;
+        }
+        if (rc) break;
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(nb) schedule(static, 1)
+#endif
+        for (int i = 0; i < nb; i++) {
+            k3x_expert_ref *r = &ref[i];
+            ok[i] = !k3x_store_expert_ref(L->st, L->st_layer, miss[b0 + i], r) &&
+                    store_shape_ok(r, I, X) && (size_t)r->nbytes <= run &&
+                    k3x_store_expert_load(L->st, r, L->c_hbuf[i]) == r->nbytes;
+        }
+        for (int i = 0; i < nb; i++) {
+            const int e = miss[b0 + i], v = vic[i];
+            if (!ok[i]) {
+                k3x_expert_drops++;
+                dropped = 1;
+                fprintf(stderr, "EXPERT DROP: layer %d expert %d could not be read from the store\n",
+                        L->st_layer, e);
+                continue;
+            }
+            const k3x_expert_ref *r = &ref[i];
+            unsigned char *hb = L->c_hbuf[i];
+            const k3x_expert_q q = {hb + r->m[0].p_off, hb + r->m[0].s_off,
+                                    hb + r->m[2].p_off, hb + r->m[2].s_off,
+                                    hb + r->m[1].p_off, hb + r->m[1].s_off};
+            L->special |= scale_flags(&q, (size_t)I * X / 32);
+            if (L->key_of[v] >= 0) {
+                L->slot_of[L->key_of[v]] = -1;
+                L->key_of[v] = -1;
+                L->evictions++;
+            }
+            uint8_t *base = L->experts + (size_t)v * L->expert_bytes, *db = L->c_dbuf[i];
+            if (hipMemcpyAsync(db, hb, (size_t)r->nbytes, hipMemcpyHostToDevice, s) != hipSuccess ||
+                k3x_dev_tile_fp4(base + L->gate_off, db + r->m[0].p_off, db + r->m[0].s_off, I, X, s) ||
+                k3x_dev_tile_fp4(base + L->up_off, db + r->m[2].p_off, db + r->m[2].s_off, I, X, s) ||
+                k3x_dev_tile_fp4(base + L->down_off, db + r->m[1].p_off, db + r->m[1].s_off, X, I, s)) {
+                rc = K3X_E_HIP;
+                break;
+            }
+            L->key_of[v] = e;
+            L->slot_of[e] = v;
+            L->used_at[v] = ++L->clock;
+            L->bytes_read += (uint64_t)r->nbytes;
+            L->misses++;
+        }
+        L->c_dirty = 1;
+        /* the pinned buffers and the staging areas are reused by the next batch */
+        if (hipStreamSynchronize(s) != hipSuccess && !rc) rc = K3X_E_HIP;
     }
-    for (int u = 0; u < nu && !rc; u++) {
-        const int e = r->uniq[u];
+    free(taken);
+    return rc ? rc : (dropped ? K3X_E_DROP : 0);
+}
+
+static int cache_publish(k3x_moe_layer *L, hipStream_t s)
+{
+    if (!L->c_dirty) return 0;
+    if (hipMemcpyAsync(L->slot_dev, L->slot_of, (size_t)L->cfg.n_experts * 4,
+                       hipMemcpyHostToDevice, s) != hipSuccess)
+        return K3X_E_HIP;
+    L->c_dirty = 0;
+    return 0;
+}
+
+/* Make experts e[0 .. n-1] resident (the named ones: hits refresh their stamp, misses
+ * are read together). */
+static int cache_make_resident(k3x_moe_layer *L, const int *ex, int n, hipStream_t s)
+{
+    const int E = L->cfg.n_experts;
+    if (n > L->nslot) return K3X_E_SHAPE;       /* more experts than slots in one call */
+    unsigned char *want = (unsigned char *)calloc((size_t)E, 1);
+    int *miss = (int *)malloc((size_t)(n > 0 ? n : 1) * sizeof(int));
+    if (!want || !miss) { free(want); free(miss); return K3X_E_NOMEM; }
+    for (int u = 0; u < n; u++) {
+        if (ex[u] < 0 || ex[u] >= E) { free(want); free(miss); return K3X_E_ARG; }
+        want[ex[u]] = 1;
+    }
+    int nm = 0;
+    for (int u = 0; u < n; u++) {
+        const int e = ex[u];
         if (L->slot_of[e] >= 0) {
             L->hits++;
             L->used_at[L->slot_of[e]] = ++L->clock;
-        } else {
-            rc = cache_load(L, e, want, s);
+        } else if (want[e] == 1) {
+            want[e] = 2;                          /* listed once */
+            miss[nm++] = e;
         }
     }
+    int rc = nm ? cache_load_many(L, miss, nm, want, s) : 0;
     free(want);
+    free(miss);
+    const int rp = cache_publish(L, s);
+    return rc ? rc : rp;
+}
+
+int k3x_cache_getmany(k3x_moe_layer *L, const int *experts, int n)
+{
+    if (!L || !L->nslot || n < 0 || (n && !experts)) return K3X_E_ARG;
+    if (hipSetDevice(L->device) != hipSuccess) return K3X_E_NODEV;
+    hipStream_t s = NULL;
+    if (hipStreamCreate(&s) != hipSuccess) return K3X_E_HIP;
+    int rc = cache_make_resident(L, experts, n, s);
+    if (hipStreamSynchronize(s) != hipSuccess && !rc) rc = K3X_E_HIP;
+    hipStreamDestroy(s);
     if (rc) return rc;
-    if (L->c_dirty) {
-        HIPCHK(hipMemcpyAsync(L->slot_dev, L->slot_of, (size_t)E * 4, hipMemcpyHostToDevice, s));
-        L->c_dirty = 0;
+    int got = 0;
+    for (int i = 0; i < n; i++) got += L->slot_of[experts[i]] >= 0;
+    return got;
+}
+
+int k3x_cache_resident(const k3x_moe_layer *L, int expert)
+{
+    if (!L || expert < 0 || expert >= L->cfg.n_experts) return K3X_E_ARG;
+    return L->nslot ? L->slot_of[expert] >= 0 : 1;
+}
+
+/* ---------------------------------------------------------- cache-only routing ---- */
+int k3x_moe_layer_set_cache_only(k3x_moe_layer *L, int on, const unsigned char *resident)
+{
+    if (!L || (on != 0 && on != 1)) return K3X_E_ARG;
+    const int E = L->cfg.n_experts, K = L->cfg.topk;
+    if (hipSetDevice(L->device) != hipSuccess) return K3X_E_NODEV;
+    if (on && !L->c_sel &&
+        hipHostMalloc((void **)&L->c_sel, (size_t)2 * K3X_DECODE_MAX_T * K * sizeof(int),
+                      hipHostMallocDefault) != hipSuccess)
+        return K3X_E_NOMEM;
+    if (on && !L->c_route &&
+        hipHostMalloc((void **)&L->c_route, sizeof(k3x_route), hipHostMallocDefault) != hipSuccess)
+        return K3X_E_NOMEM;
+    if (on && resident) {
+        if (!L->res_mask && !(L->res_mask = (unsigned char *)malloc((size_t)E))) return K3X_E_NOMEM;
+        for (int e = 0; e < E; e++) L->res_mask[e] = resident[e] ? 1 : 0;
+    } else {
+        free(L->res_mask);
+        L->res_mask = NULL;
     }
+    L->cache_only = on;
     return 0;
-fail:
+}
+
+static int is_resident(const k3x_moe_layer *L, int e)
+{
+    if (e < 0 || e >= L->cfg.n_experts) return 0;
+    if (L->res_mask) return L->res_mask[e];
+    return L->nslot ? L->slot_of[e] >= 0 : 1;
+}
+
+/* The draft's routing (k3_ops.c:1887-1896) applied to T tokens' selections sel_i/sel_w
+ * [T][K]: each token's resident experts compacted to the front in top-k order, their
+ * weights divided by their float sum when positive, the router's entries left after them
+ * (as the reference's in-place loop leaves them).  The route is rebuilt over the kept
+ * experts as the selection would have built it: unique experts in first-seen order over
+ * (token, slot), each token's weight for an expert the sum of its kept slots' weights in
+ * slot order. */
+static void cache_only_filter(const k3x_moe_layer *L, int T, int *sel_i, float *sel_w,
+                              k3x_route *r)
+{
+    const int K = L->cfg.topk;
+    int nu = 0;
+    for (int t = 0; t < T; t++) {
+        int *it = sel_i + (size_t)t * K;
+        float *wt = sel_w + (size_t)t * K;
+        int m = 0;
+        float wsum = 0.0f;
+        for (int j = 0; j < K; j++)
+            if (is_resident(L, it[j])) { it[m] = it[j]; wt[m] = wt[j]; wsum += wt[j]; m++; }
+        if (wsum > 0.0f) for (int j = 0; j < m; j++) wt[j] /= wsum;
+        for (int j = 0; j < m; j++) {
+            int u = 0;
+            while (u < nu && r->uniq[u] != it[j]) u++;
+            if (u == nu) {
+                r->uniq[nu++] = it[j];
+                for (int tt = 0; tt < K3X_DECODE_MAX_T; tt++) r->wtok[u][tt] = 0.0f;
+            }
+            r->wtok[u][t] += wt[j];
+        }
+    }
+    r->nu = nu;
+}
+
+int k3x_route_host(k3x_moe_layer *L, void *stream, int T, int *uidx, float *uwt)
+{
+    hipStream_t s = (hipStream_t)stream;
+    const int K = L->cfg.topk, TK = T * K;
+    k3x_route *r = (k3x_route *)L->c_route;
+    const size_t head = offsetof(k3x_route, uniq) + sizeof(r->uniq);
+    int *sel_i = L->c_sel;
+    float *sel_w = L->c_sel ? (float *)(L->c_sel + (size_t)K3X_DECODE_MAX_T * K) : NULL;
+    if (hipMemcpyAsync(r, L->route, head, hipMemcpyDeviceToHost, s) != hipSuccess) return K3X_E_HIP;
+    if (L->cache_only &&
+        (hipMemcpyAsync(sel_i, L->idx, (size_t)TK * 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+         hipMemcpyAsync(sel_w, L->wt, (size_t)TK * 4, hipMemcpyDeviceToHost, s) != hipSuccess))
+        return K3X_E_HIP;
+    if (hipStreamSynchronize(s) != hipSuccess) return K3X_E_HIP;
+    if (r->nu < 0 || r->nu > K3X_DECODE_MAX_T * K3X_MAX_TOPK) return K3X_E_HIP;
+    if (L->cache_only) {
+        cache_only_filter(L, T, sel_i, sel_w, r);
+        if (hipMemcpyAsync(&L->route->nu, &r->nu, sizeof(int), hipMemcpyHostToDevice, s) != hipSuccess ||
+            (r->nu && (hipMemcpyAsync(L->route->uniq, r->uniq, (size_t)r->nu * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+                       hipMemcpyAsync(L->route->wtok, r->wtok, (size_t)r->nu * sizeof(r->wtok[0]),
+                                      hipMemcpyHostToDevice, s) != hipSuccess)))
+            return K3X_E_HIP;
+        if (uidx && (hipMemcpyAsync(uidx, sel_i, (size_t)TK * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+                     hipMemcpyAsync(uwt, sel_w, (size_t)TK * 4, hipMemcpyHostToDevice, s) != hipSuccess))
+            return K3X_E_HIP;
+    }
+    int rc = 0;
+    if (L->nslot) rc = cache_make_resident(L, r->uniq, r->nu, s);
+    /* the copies above read the pinned host buffers, which the next call (perhaps on
+     * another stream) rewrites */
+    if (!rc && L->cache_only && hipStreamSynchronize(s) != hipSuccess) rc = K3X_E_HIP;
     return rc;
 }
 
@@ -585,11 +765,9 @@ int k3x_cache_pin(k3x_moe_layer *L, int expert, int pin)
         if (np + 1 > L->nslot - L->cfg.topk) return K3X_E_SHAPE;   /* keep topk slots free */
         hipStream_t s = NULL;
         HIPCHK(hipStreamCreate(&s));
-        rc = cache_load(L, expert, NULL, s);
-        if (!rc && hipMemcpyAsync(L->slot_dev, L->slot_of, (size_t)L->cfg.n_experts * 4,
-                                  hipMemcpyHostToDevice, s) != hipSuccess) rc = K3X_E_HIP;
+        rc = cache_load_many(L, &expert, 1, NULL, s);
+        if (!rc) rc = cache_publish(L, s);
         if (!rc && hipStreamSynchronize(s) != hipSuccess) rc = K3X_E_HIP;
-        if (!rc) L->c_dirty = 0;
         hipStreamDestroy(s);
         if (rc) return rc;
     }
@@ -744,7 +922,22 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     if (T == 0) return 0;
     if (T <= L->tdec)
         return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, NULL, 0.0f, stream);
-    if (L->nslot) return K3X_E_ARG;           /* a cached layer serves decode calls only */
+    if (L->nslot || L->cache_only) {
+        /* a cached layer, or cache-only routing: decode-path calls of tdec tokens (each
+         * token's result depends on its own routing only; the reference runs such calls
+         * token by token, k3_ops.c:2018) */
+        const size_t es = (x_dtype == K3X_BF16) ? 2 : 4;
+        const int H = L->cfg.hidden, K = L->cfg.topk;
+        for (int t0 = 0; t0 < T; t0 += L->tdec) {
+            const int n = T - t0 < L->tdec ? T - t0 : L->tdec;
+            const int rc = k3x_dev_decode(L, out + (size_t)t0 * H, (const char *)x + (size_t)t0 * H * es,
+                                          x_dtype, n, resid ? resid + (size_t)t0 * H : NULL,
+                                          idx ? idx + (size_t)t0 * K : NULL,
+                                          wt ? wt + (size_t)t0 * K : NULL, NULL, 0.0f, stream);
+            if (rc) return rc;
+        }
+        return 0;
+    }
     return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
 }
 
@@ -754,7 +947,7 @@ int k3x_moe_prefill_noalloc(k3x_moe_layer *L, float *out, const void *x, int x_d
     if (!L || !out || !x || T < 0 || (x_dtype != K3X_F32 && x_dtype != K3X_BF16)) return K3X_E_ARG;
     if (((uintptr_t)x & 15) || ((uintptr_t)out & 15) || ((uintptr_t)resid & 15)) return K3X_E_ARG;
     if ((idx == NULL) != (wt == NULL)) return K3X_E_ARG;
-    if (L->nslot) return K3X_E_ARG;           /* a cached layer serves decode calls only */
+    if (L->nslot || L->cache_only) return K3X_E_ARG;  /* host work between the kernels */
     if (T <= L->tdec) return K3X_E_SHAPE;     /* the decode path: k3x_moe_forward */
     return k3x_dev_prefill_noalloc(L, out, x, x_dtype, T, resid, idx, wt, stream);
 }
@@ -827,12 +1020,13 @@ int k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float ep
 /* Host-pointer drop-ins: stage x and out through device buffers held by the layer.
  * idx/wt receive the last token's routing, except for a prefill call of several tokens,
  * which leaves them as they were: k3_moe_prefill's batched path routes into buffers of
- * its own (k3_ops.c:2018-2053) and only its one-token fallback, k3_moe, writes them. */
+ * its own (k3_ops.c:2018-2053) and only its per-token fallback, k3_moe (for one token,
+ * or for cache-only routing), writes them. */
 static int host_call(k3x_moe_layer *L, float *out, const float *x, int T, int *idx,
                      float *wt, int prefill)
 {
-    if (prefill && T > 1) idx = NULL, wt = NULL;
     if (!L || (T > 0 && (!out || !x))) return K3X_E_ARG;
+    if (prefill && T > 1 && !L->cache_only) idx = NULL, wt = NULL;
     if (T <= 0) return T < 0 ? K3X_E_ARG : 0;
     const k3x_cfg *c = &L->cfg;
     const size_t n = (size_t)T * c->hidden * 4;
@@ -1081,7 +1275,7 @@ int k3x_stack_create(k3x_moe_layer *const *layers, const float *const *norm_w, i
     for (int l = 0; l < n_layers; l++) {
         if (!layers[l] || !norm_w[l]) return K3X_E_ARG;
         if (layers[l]->cfg.hidden != H || layers[l]->device != dev) return K3X_E_SHAPE;
-        if (layers[l]->timing || layers[l]->nslot) return K3X_E_ARG;
+        if (layers[l]->timing || layers[l]->nslot || layers[l]->cache_only) return K3X_E_ARG;
     }
     k3x_stack *S = (k3x_stack *)calloc(1, sizeof *S);
     if (!S) return K3X_E_NOMEM;

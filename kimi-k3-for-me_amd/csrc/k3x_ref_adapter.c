@@ -8,20 +8,24 @@
  * they upload it through the layer's own K3ExpertSrc (k3.h:521-544) and keep the handle;
  * afterwards every call runs on the GPU.
  *
- * Accepted: bf16 trunk weights (wdt == K3_WBF16) and a streamed expert source, not a
- * cache-only draft (k3.h:568: its routing depends on the host cache's residency, which
- * the device copy of the layer does not share).  A layer with latent == hidden whose
- * down/up are identity matrices (the K2-class emulation) is uploaded without
- * projections; any other latent layer with its down/up projections, latent norm and
- * SiTU betas.  An expert that cannot be fetched at upload counts in k3_expert_drops (as
- * k3_ops.c:1916-1926 counts a per-token drop) and the call returns -1; a device call
- * that fails (k3x status, including a decode workgroup that gave up its wait) returns -1
- * without counting a drop.
+ * Accepted: bf16 trunk weights (wdt == K3_WBF16) and a streamed expert source.  A layer
+ * with latent == hidden whose down/up are identity matrices (the K2-class emulation) is
+ * uploaded without projections; any other latent layer with its down/up projections,
+ * latent norm and SiTU betas.  The upload hands the source's getmany (when it has one)
+ * each batch of experts before their get() calls.  A cache-only draft (k3.h:564-568)
+ * routes over the experts the source's resident() reports, asked for every expert at
+ * each call (the host cache's residency, which the device copy does not share), with
+ * the reference's renormalisation (k3_ops.c:1887-1896); a source without resident() is
+ * refused (-1), as the reference's draft loop needs it.  An expert that cannot be
+ * fetched at upload counts in k3_expert_drops (as k3_ops.c:1916-1926 counts a per-token
+ * drop) and the call returns -1; a device call that fails (k3x status, including a
+ * decode workgroup that gave up its wait) returns -1 without counting a drop.
  */
 #include "k3.h"
 #include "k3x_moe.h"
 
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define K3X_ADAPTER_MAX_LAYERS 128
@@ -42,6 +46,12 @@ typedef struct {
     K3ExpertSrc    *src;
 } adapter_src;
 
+static int adapter_getmany(k3x_expert_src *self, int layer, const int *experts, int n)
+{
+    adapter_src *a = (adapter_src *)self;
+    return a->src->getmany(a->src, layer, experts, n);
+}
+
 static int adapter_get(k3x_expert_src *self, int layer, int expert, k3x_expert_q *out)
 {
     adapter_src *a = (adapter_src *)self;
@@ -57,7 +67,7 @@ static int adapter_get(k3x_expert_src *self, int layer, int expert, k3x_expert_q
 static int gpu_form(const K3MoeW *w, const K3Cfg *c)
 {
     return w->src && w->src->get && w->wdt == K3_WBF16 && w->down && w->up &&
-           c->latent > 0 && !w->cache_only && w->layer >= 0 &&
+           c->latent > 0 && (!w->cache_only || w->src->resident) && w->layer >= 0 &&
            w->layer < K3X_ADAPTER_MAX_LAYERS;
 }
 
@@ -104,6 +114,7 @@ static k3x_moe_layer *layer_for(const K3MoeW *w, const K3Cfg *c)
     adapter_src as;
     memset(&as, 0, sizeof as);
     as.base.get = adapter_get;
+    if (w->src->getmany) as.base.getmany = adapter_getmany;
     as.src = w->src;
     k3x_moe_w kw;
     memset(&kw, 0, sizeof kw);
@@ -141,8 +152,18 @@ static int run(int prefill, float *out, const float *x, const K3MoeW *w, const K
     if (!gpu_form(w, c)) return -1;
     k3x_moe_layer *L = layer_for(w, c);
     if (!L) return -1;
-    const int rc = prefill ? k3x_moe_prefill(L, out, x, T, idx, wt)
-                           : k3x_moe(L, out, x, T, idx, wt);
+    int rc = 0;
+    if (w->cache_only) {
+        unsigned char *res = (unsigned char *)malloc((size_t)c->n_experts);
+        if (!res) return -1;
+        for (int e = 0; e < c->n_experts; e++)
+            res[e] = w->src->resident(w->src, w->layer, e, NULL) ? 1 : 0;
+        rc = k3x_moe_layer_set_cache_only(L, 1, res);
+        free(res);
+    }
+    if (!rc)
+        rc = prefill ? k3x_moe_prefill(L, out, x, T, idx, wt) : k3x_moe(L, out, x, T, idx, wt);
+    if (w->cache_only) k3x_moe_layer_set_cache_only(L, 0, NULL);
     if (rc) {
         fprintf(stderr, "k3x: layer %d call failed: %s\n", w->layer, k3x_strerror(rc));
         return -1;

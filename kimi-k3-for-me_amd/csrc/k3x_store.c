@@ -596,12 +596,40 @@ static int store_get(k3x_expert_src *self, int layer, int expert, k3x_expert_q *
     return 0;
 }
 
+/* getmany: the experts' byte ranges handed to the kernel's read-ahead together
+ * (POSIX_FADV_WILLNEED), so that the get() calls that follow find them in the page
+ * cache; returns n, or -1 when a range cannot be found. */
+static int store_getmany(k3x_expert_src *self, int layer, const int *experts, int n)
+{
+    store_src *ss = (store_src *)self;
+    char name[256];
+    for (int i = 0; i < n; i++) {
+        k3x_expert_ref r;
+        if (k3x_store_expert_ref(ss->s, layer, experts[i], &r)) return -1;
+        const int fd = ss->s->fd[r.shard];
+        if (r.contiguous) {
+            (void)posix_fadvise(fd, (off_t)r.off, (off_t)r.nbytes, POSIX_FADV_WILLNEED);
+            continue;
+        }
+        for (int m = 0; m < 3; m++)
+            for (int k = 0; k < 2; k++) {
+                snprintf(name, sizeof name, EXPERT_NAME, layer, experts[i], m + 1,
+                         k ? "weight_scale" : "weight_packed");
+                const st_ent *e = lookup(ss->s, name);
+                if (!e) return -1;
+                (void)posix_fadvise(fd, (off_t)e->t.off, (off_t)e->t.nbytes, POSIX_FADV_WILLNEED);
+            }
+    }
+    return n;
+}
+
 int k3x_store_src_create_for(k3x_store *s, int moe_inter, int width, k3x_expert_src **out)
 {
     if (!s || !out || moe_inter < 0 || width < 0) return K3X_E_ARG;
     store_src *ss = (store_src *)calloc(1, sizeof *ss);
     if (!ss) return K3X_E_NOMEM;
     ss->base.get = store_get;
+    ss->base.getmany = store_getmany;
     ss->base.ctx = ss;
     ss->s = s;
     ss->inter = moe_inter;

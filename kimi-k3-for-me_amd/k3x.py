@@ -45,7 +45,7 @@ EXPORTS = [
     "k3x_moe_layer_create_from_store",
     "k3x_moe_layer_create_cached",
     "k3x_cache_stats",
-    "k3x_cache_pin",
+    "k3x_cache_pin", "k3x_cache_getmany", "k3x_cache_resident", "k3x_moe_layer_set_cache_only",
     # include/k3x_trunk.h
     "k3x_trunk_create", "k3x_trunk_destroy", "k3x_trunk_apply", "k3x_trunk_apply_host",
 ]
@@ -76,7 +76,11 @@ class ExpertSrc(C.Structure):
 
 
 GET_FN = C.CFUNCTYPE(C.c_int, C.POINTER(ExpertSrc), C.c_int, C.c_int, C.POINTER(ExpertQ))
-ExpertSrc._fields_ = [("get", GET_FN), ("ctx", C.c_void_p)]
+GETMANY_FN = C.CFUNCTYPE(C.c_int, C.POINTER(ExpertSrc), C.c_int, C.POINTER(C.c_int), C.c_int)
+RESIDENT_FN = C.CFUNCTYPE(C.c_int, C.POINTER(ExpertSrc), C.c_int, C.c_int, C.POINTER(ExpertQ))
+# get and ctx, then the two optional members (NULL unless set)
+ExpertSrc._fields_ = [("get", GET_FN), ("ctx", C.c_void_p), ("getmany", GETMANY_FN),
+                      ("resident", RESIDENT_FN)]
 
 
 class MoeW(C.Structure):
@@ -177,6 +181,9 @@ def lib():
                                                   C.POINTER(vp)]
         L.k3x_cache_stats.argtypes = [vp, C.POINTER(CacheStat)]
         L.k3x_cache_pin.argtypes = [vp, i, i]
+        L.k3x_cache_getmany.argtypes = [vp, C.POINTER(C.c_int), i]
+        L.k3x_cache_resident.argtypes = [vp, i]
+        L.k3x_moe_layer_set_cache_only.argtypes = [vp, i, C.c_void_p]
         L.k3x_attn_res.argtypes = [vp, vp, i, i, vp, vp, i, i, f, vp]
         L.k3x_moe_half.argtypes = [vp, vp, vp, vp, i, i, vp, vp, f, i, vp, vp]
         L.k3x_trunk_create.argtypes = [vp, i, i, i, C.POINTER(vp)]
@@ -252,8 +259,9 @@ class MoELayer:
 
     @classmethod
     def from_source(cls, cfg, gate, bias, get, sh1=None, sh3=None, sh2=None, layer=0,
-                    device=0, down=None, up=None, latent_norm=None):
-        """get(layer, expert) -> dict of numpy arrays, or None for a failed fetch."""
+                    device=0, down=None, up=None, latent_norm=None, getmany=None):
+        """get(layer, expert) -> dict of numpy arrays, or None for a failed fetch;
+        getmany(layer, experts) -> how many are now resident (optional)."""
         hold = {}
 
         def _get(src, lay, e, out):
@@ -269,6 +277,12 @@ class MoELayer:
 
         cb = GET_FN(_get)
         src = ExpertSrc(cb, None)
+        if getmany is not None:
+            def _getmany(src_, lay, ex, n):
+                return int(getmany(lay, [ex[i] for i in range(n)]))
+            cbm = GETMANY_FN(_getmany)
+            src.getmany = cbm
+            hold["getmany"] = cbm
         w = MoeW(_vp(gate), _vp(bias), _vp(sh1), _vp(sh3), _vp(sh2), C.pointer(src), None,
                  layer, _vp(down), _vp(up), _vp(latent_norm))
         h = C.c_void_p()
@@ -312,6 +326,24 @@ class MoELayer:
 
     def cache_pin(self, expert, pin=True):
         _check(lib().k3x_cache_pin(self.h, expert, 1 if pin else 0), "k3x_cache_pin")
+
+    def cache_getmany(self, experts):
+        """k3x_cache_getmany: experts made resident together; returns how many are."""
+        a = (C.c_int * len(experts))(*[int(e) for e in experts])
+        return _check(lib().k3x_cache_getmany(self.h, a, len(experts)), "k3x_cache_getmany")
+
+    def cache_resident(self, expert):
+        return _check(lib().k3x_cache_resident(self.h, expert), "k3x_cache_resident")
+
+    def set_cache_only(self, on, resident=None):
+        """Cache-only (draft) routing over the experts resident[e] != 0 marks (numpy array
+        of n_experts), or over the layer's own residency when resident is None."""
+        keep = None
+        if resident is not None:
+            keep = np.ascontiguousarray(np.asarray(resident) != 0, dtype=np.uint8)
+        _check(lib().k3x_moe_layer_set_cache_only(self.h, 1 if on else 0,
+                                                  keep.ctypes.data if keep is not None else None),
+               "k3x_moe_layer_set_cache_only")
 
     @classmethod
     def synthetic(cls, cfg, seed=0, layer=0, router_sigma=0.02, bias_sigma=0.1, zipf_alpha=0.0,

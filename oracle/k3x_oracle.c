@@ -392,6 +392,52 @@ long ko_moe(float *out, const float *x, int T, const ko_cfg *c, const ko_weights
     return drops;
 }
 
+/* k3_moe with cache_only set (the draft model's routing, k3_ops.c:1884-1896, :1905-1926):
+ * each token's top-k is filtered to the experts res[] marks resident, in top-k order,
+ * compacted to the front of idx/wt (the slots past the kept count keep the router's
+ * values), the kept weights divided by their float sum (when it is positive); only the
+ * kept experts are computed, no getmany, and a kept expert is applied without get() (the
+ * cache serves it) -- a failed fetch is skipped without a drop.  k3_moe_prefill with
+ * cache_only runs this per-token path for every T (:2018). */
+long ko_moe_cache_only(float *out, const float *x, int T, const ko_cfg *c,
+                       const ko_weights *w, const int *res, int *idx, float *wt)
+{
+    const int H = c->hidden, K = c->topk, L = latent_of(c);
+    moe_tmp m;
+    if (moe_tmp_alloc(&m, c)) abort();
+    for (int t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * H;
+        float *ot = out + (size_t)t * H;
+        float *acc = c->latent > 0 ? m.acc : ot;
+        int *it = idx + (size_t)t * K;
+        float *wtt = wt + (size_t)t * K;
+        const float *z = latent_in(xt, c, w, m.z);
+        ko_router(it, wtt, xt, w->gate, w->bias, H, c->n_experts, K, c->renorm,
+                  c->routed_scale);
+        int nk = 0;
+        float wsum = 0.0f;
+        for (int j = 0; j < K; j++) {
+            const int e = it[j];
+            if (e >= 0 && e < c->n_experts && res[e]) {
+                it[nk] = it[j]; wtt[nk] = wtt[j]; wsum += wtt[j]; nk++;
+            }
+        }
+        if (wsum > 0.0f) for (int j = 0; j < nk; j++) wtt[j] /= wsum;
+        for (int i = 0; i < L; i++) acc[i] = 0.0f;
+        for (int j = 0; j < nk; j++) {
+            ko_expert q;
+            if (expert_get(w, it[j], &q) != 0) continue;
+            expert_apply(m.edn, z, it[j], &q, c, w, &m);
+            const float wj = wtt[j];
+            for (int i = 0; i < L; i++) acc[i] += wj * m.edn[i];
+        }
+        latent_out(ot, acc, c, w);
+        shared_add(ot, xt, c, w, &m);
+    }
+    moe_tmp_free(&m);
+    return 0;
+}
+
 /* k3_moe_prefill / moe_prefill_routed, k3_ops.c:2008-2132: per 64-token sub-chunk
  * (MOE_DEDUP_CHUNK, :1993) route every token, collect unique experts in first-seen order,
  * apply each once to every (token, slot) that chose it, then sum each token's

@@ -113,6 +113,12 @@ long ko_moe_half(float *h, float *pref, const float *blocks, int maxb, int nb,
 /* ---- synthetic inputs ---------------------------------------------------------- */
 /* The counter-based generator shared by the tests and the product's synthetic-layer
  * builder: value i of a stream depends only on (seed, layer, stream, sub, i). */
+/* k3_moe / k3_moe_prefill with K3MoeW.cache_only (k3_ops.c:1884-1926, :2018): each
+ * token's top-k filtered to the experts with res[e] != 0, weights renormalised over them;
+ * idx/wt [T][K] hold the kept experts first and the router's values after them. */
+long ko_moe_cache_only(float *out, const float *x, int T, const ko_cfg *c,
+                       const ko_weights *w, const int *res, int *idx, float *wt);
+
 /* The opt-in MXFP8-activation prefill mode (no reference counterpart; the definition
  * is at the top of its section in k3x_oracle.c): E4M3 decode and round-to-nearest-even
  * (|v| <= 448), the block scale byte, MXFP8 quantisation and dequantisation of n % 32 == 0

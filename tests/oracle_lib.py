@@ -101,6 +101,9 @@ def oracle():
         lib.ko_mx8_quant.argtypes = [U8P, U8P, F32P, C.c_int]
         lib.ko_mx8_dequant.argtypes = [C.POINTER(C.c_double), U8P, U8P, C.c_int]
         lib.ko_matmul_mx.argtypes = [F32P, U8P, U8P, U8P, U8P, C.c_int, C.c_int]
+        lib.ko_moe_cache_only.restype = C.c_long
+        lib.ko_moe_cache_only.argtypes = [F32P, F32P, C.c_int, C.POINTER(KoCfg),
+                                          C.POINTER(KoWeights), I32P, I32P, F32P]
         lib.ko_moe_mx.restype = C.c_long
         lib.ko_moe_mx.argtypes = [F32P, F32P, C.c_int, C.POINTER(KoCfg), C.POINTER(KoWeights),
                                   I32P, F32P]

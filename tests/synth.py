@@ -189,6 +189,20 @@ class Layer:
                                 ptr(idx, I32P), ptr(wt, F32P))
         return out, idx, wt, drops
 
+    def oracle_moe_cache_only(self, x, res):
+        """The oracle of cache-only (draft) routing over the experts res marks resident."""
+        x = np.ascontiguousarray(x, np.float32)
+        T = x.shape[0]
+        out = np.empty_like(x)
+        idx = np.empty((T, self.K), np.int32)
+        wt = np.empty((T, self.K), np.float32)
+        cfg = self.ko_cfg()
+        w, cb, keep = self._weights(None)
+        r = np.ascontiguousarray(res, np.int32)
+        oracle().ko_moe_cache_only(ptr(out, F32P), ptr(x, F32P), T, C.byref(cfg), C.byref(w),
+                                   ptr(r, I32P), ptr(idx, I32P), ptr(wt, F32P))
+        return out, idx, wt
+
     def oracle_moe_mx(self, x, fail=None):
         """The oracle of the MXFP8-activation prefill mode (ko_moe_mx)."""
         x = np.ascontiguousarray(x, np.float32)

@@ -10,9 +10,9 @@ k3_decoder_layer_core would use (k3_ops.c:2562-2567).
 
 Branches: the K2-class emulation (identity latent, 2^64 betas: uploaded without
 projections) and a LatentMoE layer, decode and prefill, against the reference and the
-committed golden vectors; a cache-only draft and fp32 trunk weights refused (-1, the
-caller keeps its CPU path); an expert that fails to load at upload counted in
-k3_expert_drops; the scratch query.
+committed golden vectors; a cache-only draft over the source's resident() against the
+reference's draft path; fp32 trunk weights refused (-1, the caller keeps its CPU path);
+an expert that fails to load at upload counted in k3_expert_drops; the scratch query.
 """
 import ctypes as C
 import os
@@ -21,6 +21,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as ol
+import refcall
 import synth
 from gpu_util import say
 
@@ -35,13 +36,7 @@ ADAPTER_SO = os.path.join(ol.ROOT, "oracle", "_ref", "libk3adapter.so")
 def adl(torch, k3x):
     if not os.path.exists(ADAPTER_SO):
         pytest.skip("oracle/_ref/libk3adapter.so not built (needs the reference tree)")
-    lib = C.CDLL(ADAPTER_SO)
-    lib.refdrv_moe_entry.restype = C.c_long
-    lib.refdrv_moe_entry.argtypes = [
-        ol.F32P, ol.F32P, C.c_int, C.POINTER(ol.DrvCfg), ol.F32P, ol.F32P,
-        C.POINTER(ol.KoExpert), ol.I32P, C.c_void_p, C.c_void_p, ol.F32P, C.c_void_p,
-        C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, ol.I32P, ol.I32P, ol.F32P,
-        C.POINTER(C.c_int), C.POINTER(C.c_long)]
+    lib = refcall.bind(C.CDLL(ADAPTER_SO))
     lib.refdrv_gpu_release.restype = None
     lib.k3_moe_gpu_scratch.restype = C.c_size_t
     lib.k3_moe_gpu_scratch.argtypes = [C.c_void_p, C.c_int]
@@ -49,51 +44,7 @@ def adl(torch, k3x):
     lib.refdrv_gpu_release()
 
 
-def identity_bf16(n):
-    m = np.zeros((n, n), np.uint16)
-    m[np.arange(n), np.arange(n)] = 0x3F80
-    return m
-
-
-class Call:
-    """The layer's arrays in the reference's types, kept alive across calls."""
-
-    def __init__(self, L, k2_emulation):
-        self.L = L
-        self.bank = (ol.KoExpert * L.E)()
-        self.keep = []
-        for e in range(L.E):
-            d = L.expert(e)
-            self.keep.append(d)
-            for k in ("p1", "s1", "p3", "s3", "p2", "s2"):
-                setattr(self.bank[e], k, d[k].ctypes.data_as(ol.U8P))
-        if k2_emulation:
-            # K2 through the reference's own types: latent = hidden, identity down/up,
-            # latent norm off, SiTU betas 2^64 (SwiGLU)
-            self.down = self.up = identity_bf16(L.H)
-            self.dc = ol.DrvCfg(L.H, L.H, L.E, L.K, L.I, L.n_shared, L.renorm, 0,
-                                L.routed_scale, L.rms_eps, 2.0 ** 64, 2.0 ** 64)
-        else:
-            self.down, self.up = L.down, L.up
-            self.dc = ol.DrvCfg(L.H, L.latent, L.E, L.K, L.I, L.n_shared, L.renorm,
-                                L.latent_norm, L.routed_scale, L.rms_eps, L.situ_b1, L.situ_b2)
-
-    def __call__(self, adl, x, mode, fail=None, cache_only=0, trunk_f32=0):
-        L = self.L
-        x = np.ascontiguousarray(x, np.float32)
-        out = np.full_like(x, np.float32(7.0))
-        idx = np.full(L.K, -9, np.int32)
-        wt = np.zeros(L.K, np.float32)
-        st = C.c_int(99)
-        gets = C.c_long(0)
-        fa = None if fail is None else np.ascontiguousarray(fail, np.int32)
-        drops = adl.refdrv_moe_entry(
-            ol.ptr(out, ol.F32P), ol.ptr(x, ol.F32P), x.shape[0], C.byref(self.dc),
-            ol.ptr(L.gate, ol.F32P), ol.ptr(L.bias, ol.F32P), self.bank, ol.ptr(fa, ol.I32P),
-            ol.vptr(self.down), ol.vptr(self.up), ol.ptr(L.lnorm, ol.F32P), ol.vptr(L.sh1),
-            ol.vptr(L.sh3), ol.vptr(L.sh2), trunk_f32, mode, cache_only, None,
-            ol.ptr(idx, ol.I32P), ol.ptr(wt, ol.F32P), C.byref(st), C.byref(gets))
-        return out, idx, wt, drops, st.value
+Call = refcall.Call
 
 
 @pytest.mark.parametrize("T,mode", [(1, 2), (8, 2), (8, 3), (40, 3)])
@@ -147,17 +98,41 @@ def test_latent_layer_through_binding(adl, T, mode):
     assert synth.rel_l2(go[:n], g["out"][:n]) < TOL
 
 
+@pytest.mark.parametrize("T,mode", [(1, 2), (5, 2), (20, 3)])
+def test_cache_only_draft_through_binding(adl, T, mode):
+    """A cache-only draft (K3MoeW.cache_only with the source's resident() reporting a
+    mask) through the binding, against the reference's CPU path with the same source:
+    the last token's indices exact and weights to float rounding, outputs within the
+    parity bar."""
+    say(f"case: binding, cache-only draft over a half-resident source, T={T}, mode {mode}")
+    adl.refdrv_gpu_release()
+    L = synth.tiny(seed=9)
+    c = Call(L, k2_emulation=True)
+    res = (np.random.default_rng(T).random(L.E) < 0.5).astype(np.int32)
+    x = L.x(T, bf16=False)
+    go, gi, gw, gd, gs = c(adl, x, mode, cache_only=1, res=res)
+    ro, ri, rw, rd, rs = c(adl, x, mode - 2, cache_only=1, res=res)
+    assert gs == 0 and rs == 0 and gd == 0 and rd == 0
+    assert np.array_equal(gi, ri)
+    np.testing.assert_allclose(gw, rw, rtol=1e-6)
+    err = synth.rel_l2(go, ro)
+    say(f"  rel_l2 vs the reference's CPU path = {err:.3e}")
+    assert err < TOL
+    o, oi, _ = L.oracle_moe_cache_only(x, res)
+    assert np.array_equal(gi, oi[-1]) and synth.rel_l2(go, o) < TOL
+
+
 def test_binding_refusals_and_drops(adl, k3x):
     """What the binding does not run returns -1 with the output untouched (the caller
-    keeps its CPU path): a cache-only draft, fp32 trunk weights.  An expert whose fetch
-    fails at upload counts once in k3_expert_drops (and in k3x_expert_drops), the call
-    returns -1; the next call with a working source uploads and runs."""
-    say("case: binding refusals (cache_only, fp32 trunk) and an upload drop")
+    keeps its CPU path): fp32 trunk weights.  An expert whose fetch fails at upload
+    counts once in k3_expert_drops (and in k3x_expert_drops), the call returns -1; the
+    next call with a working source uploads and runs."""
+    say("case: binding refusal (fp32 trunk) and an upload drop")
     adl.refdrv_gpu_release()
     L = synth.tiny(seed=3)
     c = Call(L, k2_emulation=True)
     x = L.x(2, bf16=False)
-    for kw in ({"cache_only": 1}, {"trunk_f32": 1}):
+    for kw in ({"trunk_f32": 1},):
         o, i, w, d, s = c(adl, x, 2, **kw)
         assert s == -1 and d == 0, kw
         assert np.all(o == np.float32(7.0)) and np.all(i == -9), kw

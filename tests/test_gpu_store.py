@@ -110,9 +110,9 @@ def test_cached_layer_equals_resident(torch, k3x, tmp_path, latent):
 
 
 def test_cache_pin_prefill_and_capacity(torch, k3x, tmp_path):
-    """A pinned expert stays resident through later tokens; a prefill call on a cached
-    layer is refused (K3X_E_ARG); a call naming more experts than slots returns
-    K3X_E_SHAPE and the layer keeps working."""
+    """A pinned expert stays resident through later tokens; a call naming more experts
+    than slots returns K3X_E_SHAPE (a 16-token call runs as 8-token decode calls, whose
+    first group names more than topk + 1) and the layer keeps working."""
     say("case: expert cache pinning, prefill refusal, capacity")
     L = synth.tiny(seed=24)
     write_layer(tmp_path, L, layer=0)
@@ -125,10 +125,10 @@ def test_cache_pin_prefill_and_capacity(torch, k3x, tmp_path):
     for t in range(8):
         dev_forward(torch, k3x, cache, x[t:t + 1])
     assert np.array_equal(cache.read_expert(7)["p1"], L.expert(7)["p1"])
-    with pytest.raises(k3x.K3XError) as ei:
-        dev_forward(torch, k3x, cache, x)                 # T = 16: the prefill path
-    assert ei.value.status == -1
     _, idx8, _, _ = L.oracle_moe(x[:8])
+    with pytest.raises(k3x.K3XError) as ei:
+        dev_forward(torch, k3x, cache, x)                 # T = 16: groups of 8 tokens
+    assert ei.value.status == -2
     assert len(np.unique(idx8)) > cfg.topk + 1
     with pytest.raises(k3x.K3XError) as ei:
         dev_forward(torch, k3x, cache, x[:8])             # more experts than slots

@@ -148,6 +148,18 @@ typedef struct k3x_cache_stat {
  * the cache starts empty. */
 int  k3x_moe_layer_create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store *s,
                                  int layer, int nslot, int device, k3x_moe_layer **out);
+/* The same cache with its misses fetched through the layer's supplier w->src instead of
+ * a store (the reference's K3ExpertSrc behind a binding): for each batch of a call's
+ * misses, the supplier's getmany() when it has one, then get() one expert at a time, its
+ * arrays (the layer's shapes) copied into a pinned buffer.  A failed get() counts in
+ * k3x_expert_drops and fails the call with K3X_E_DROP.  The supplier must outlive the
+ * layer. */
+int  k3x_moe_layer_create_cached_src(const k3x_cfg *c, const k3x_moe_w *w, int nslot,
+                                     int device, k3x_moe_layer **out);
+/* Expert slots that fit in `fraction` (0 < fraction <= 1) of the device's free memory
+ * beside one layer's other weights of shape c (at most n_experts): the nslot to give a
+ * cache when the whole layer does not fit. */
+int  k3x_cache_slots_fit(const k3x_cfg *c, int device, double fraction);
 int  k3x_cache_stats(const k3x_moe_layer *L, k3x_cache_stat *st);
 /* pin = 1: make the expert resident (a miss) and never evict it; 0: release it.  At
  * least topk slots stay unpinned (K3X_E_SHAPE otherwise). */

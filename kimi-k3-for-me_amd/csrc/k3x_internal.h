@@ -174,8 +174,9 @@ struct k3x_moe_layer {
     uint64_t *used_at;            /* [nslot] LRU stamp                                */
     unsigned char *pinned;        /* [nslot] never evicted while set                  */
     uint64_t  clock, hits, misses, evictions, bytes_read;
-    struct k3x_store *st;         /* where misses are read from                       */
+    struct k3x_store *st;         /* where misses are read from, or NULL: from c_src   */
     int       st_layer;
+    k3x_expert_src *c_src;        /* the supplier misses are fetched through (no store) */
     unsigned char *c_hbuf[K3X_CACHE_IO];  /* pinned host buffers, one expert run each  */
     uint8_t  *c_dbuf[K3X_CACHE_IO];       /* device staging, one expert run each        */
     int       c_nio;              /* staging pairs: misses read together               */

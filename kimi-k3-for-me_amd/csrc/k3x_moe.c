@@ -455,10 +455,10 @@ static size_t expert_run_bytes(const k3x_moe_layer *L)
     return 3 * ((size_t)L->cfg.moe_inter * L->XL / 2 + (size_t)L->cfg.moe_inter * L->XL / 32);
 }
 
-int k3x_moe_layer_create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store *st,
-                                int layer, int nslot, int device, k3x_moe_layer **out)
+static int create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store *st,
+                         k3x_expert_src *src, int layer, int nslot, int device,
+                         k3x_moe_layer **out)
 {
-    if (!c || !w || !st || !out || !w->gate) return K3X_E_ARG;
     *out = NULL;
     if (nslot < c->topk + 1 || nslot > c->n_experts) return K3X_E_ARG;
     k3x_moe_layer *L = NULL;
@@ -466,7 +466,7 @@ int k3x_moe_layer_create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store 
     if (rc) return rc;
     const int H = c->hidden, E = c->n_experts;
     const size_t run = expert_run_bytes(L);
-    L->st = st; L->st_layer = layer;
+    L->st = st; L->st_layer = layer; L->c_src = src;
     L->slot_of = (int *)malloc((size_t)E * sizeof(int));
     L->key_of = (int *)malloc((size_t)nslot * sizeof(int));
     L->used_at = (uint64_t *)calloc((size_t)nslot, sizeof(uint64_t));
@@ -490,6 +490,50 @@ int k3x_moe_layer_create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store 
 fail:
     layer_free(L);
     return rc;
+}
+
+int k3x_moe_layer_create_cached(const k3x_cfg *c, const k3x_moe_w *w, k3x_store *st,
+                                int layer, int nslot, int device, k3x_moe_layer **out)
+{
+    if (!c || !w || !st || !out || !w->gate) return K3X_E_ARG;
+    return create_cached(c, w, st, NULL, layer, nslot, device, out);
+}
+
+int k3x_moe_layer_create_cached_src(const k3x_cfg *c, const k3x_moe_w *w, int nslot,
+                                    int device, k3x_moe_layer **out)
+{
+    if (!c || !w || !out || !w->gate || !w->src || !w->src->get) return K3X_E_ARG;
+    return create_cached(c, w, NULL, w->src, w->layer, nslot, device, out);
+}
+
+/* A miss through the supplier: its getmany() (when it has one) for the batch, then, one
+ * expert at a time (get()'s pointers last until the next get()), the six arrays copied
+ * into the pinned buffer as a run laid out [p1 s1 p3 s3 p2 s2]; ok[i] = 0 for a failed
+ * fetch. */
+static void src_fetch(k3x_moe_layer *L, const int *miss, int nb, int *ok, k3x_expert_ref *ref)
+{
+    const size_t I = (size_t)L->cfg.moe_inter, X = (size_t)L->XL;
+    const int64_t pb = (int64_t)(I * X / 2), sb = (int64_t)(I * X / 32);
+    k3x_expert_src *src = L->c_src;
+    if (src->getmany) (void)src->getmany(src, L->st_layer, miss, nb);
+    for (int i = 0; i < nb; i++) {
+        k3x_expert_q q;
+        memset(&q, 0, sizeof q);
+        ok[i] = src->get(src, L->st_layer, miss[i], &q) == 0 && q.p1 && q.s1 && q.p3 &&
+                q.s3 && q.p2 && q.s2;
+        if (!ok[i]) continue;
+        k3x_expert_ref *r = &ref[i];
+        memset(r, 0, sizeof *r);
+        /* m[0] gate (w1), m[1] down (w2), m[2] up (w3), as the store's runs */
+        r->m[0].p_off = 0;           r->m[0].s_off = pb;
+        r->m[2].p_off = pb + sb;     r->m[2].s_off = 2 * pb + sb;
+        r->m[1].p_off = 2 * pb + 2 * sb; r->m[1].s_off = 3 * pb + 2 * sb;
+        r->nbytes = 3 * (pb + sb);
+        unsigned char *hb = L->c_hbuf[i];
+        memcpy(hb + r->m[0].p_off, q.p1, (size_t)pb); memcpy(hb + r->m[0].s_off, q.s1, (size_t)sb);
+        memcpy(hb + r->m[2].p_off, q.p3, (size_t)pb); memcpy(hb + r->m[2].s_off, q.s3, (size_t)sb);
+        memcpy(hb + r->m[1].p_off, q.p2, (size_t)pb); memcpy(hb + r->m[1].s_off, q.s2, (size_t)sb);
+    }
 }
 
 /* The least recently used unpinned slot whose expert the call does not name (want[key]
@@ -531,22 +575,26 @@ static int cache_load_many(k3x_moe_layer *L, const int *miss, int n, const unsig
             taken[vic[i]] = 1;
         }
         if (rc) break;
+        if (!L->st) {
+            src_fetch(L, miss + b0, nb, ok, ref);
+        } else {
 #ifdef _OPENMP
 #pragma omp parallel for num_threads(nb) schedule(static, 1)
 #endif
-        for (int i = 0; i < nb; i++) {
-            k3x_expert_ref *r = &ref[i];
-            ok[i] = !k3x_store_expert_ref(L->st, L->st_layer, miss[b0 + i], r) &&
-                    store_shape_ok(r, I, X) && (size_t)r->nbytes <= run &&
-                    k3x_store_expert_load(L->st, r, L->c_hbuf[i]) == r->nbytes;
+            for (int i = 0; i < nb; i++) {
+                k3x_expert_ref *r = &ref[i];
+                ok[i] = !k3x_store_expert_ref(L->st, L->st_layer, miss[b0 + i], r) &&
+                        store_shape_ok(r, I, X) && (size_t)r->nbytes <= run &&
+                        k3x_store_expert_load(L->st, r, L->c_hbuf[i]) == r->nbytes;
+            }
         }
         for (int i = 0; i < nb; i++) {
             const int e = miss[b0 + i], v = vic[i];
             if (!ok[i]) {
                 k3x_expert_drops++;
                 dropped = 1;
-                fprintf(stderr, "EXPERT DROP: layer %d expert %d could not be read from the store\n",
-                        L->st_layer, e);
+                fprintf(stderr, "EXPERT DROP: layer %d expert %d could not be %s\n",
+                        L->st_layer, e, L->st ? "read from the store" : "fetched");
                 continue;
             }
             const k3x_expert_ref *r = &ref[i];
@@ -621,6 +669,25 @@ static int cache_make_resident(k3x_moe_layer *L, const int *ex, int n, hipStream
     free(miss);
     const int rp = cache_publish(L, s);
     return rc ? rc : rp;
+}
+
+int k3x_cache_slots_fit(const k3x_cfg *c, int device, double fraction)
+{
+    if (!c || fraction <= 0.0 || fraction > 1.0 || c->hidden <= 0 || c->moe_inter <= 0)
+        return K3X_E_ARG;
+    const int X = c->latent > 0 ? c->latent : c->hidden, I = c->moe_inter;
+    const size_t per = 2 * k3x_fp4_matrix_bytes(I, X) + k3x_fp4_matrix_bytes(X, I);
+    size_t fr = 0, tot = 0;
+    if (hipSetDevice(device) != hipSuccess || hipMemGetInfo(&fr, &tot) != hipSuccess)
+        return K3X_E_NODEV;
+    /* the layer's other weights (router, shared expert, projections) and its buffers */
+    const size_t SI = (size_t)I * c->n_shared;
+    const size_t fixed = (size_t)c->n_experts * c->hidden * 4 + 3 * SI * c->hidden * 2 +
+                         (c->latent > 0 ? 2 * (size_t)X * c->hidden * 2 : 0) + ((size_t)256 << 20);
+    const double room = (double)fr * fraction - (double)fixed;
+    if (room <= 0.0) return 0;
+    const double n = room / (double)per;
+    return n > (double)c->n_experts ? c->n_experts : (int)n;
 }
 
 int k3x_cache_getmany(k3x_moe_layer *L, const int *experts, int n)

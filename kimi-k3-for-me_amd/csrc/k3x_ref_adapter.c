@@ -23,6 +23,7 @@
  */
 #include "k3.h"
 #include "k3x_moe.h"
+#include "k3x_store.h"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -30,21 +31,23 @@
 
 #define K3X_ADAPTER_MAX_LAYERS 128
 
+typedef struct {
+    k3x_expert_src  base;   /* first member: the callback casts back */
+    K3ExpertSrc    *src;
+} adapter_src;
+
 /* A layer is reused while the K3MoeW it was built from is the same object with the
- * same weights and shape; anything else uploads it again. */
+ * same weights and shape; anything else uploads it again.  A layer kept as an HBM expert
+ * cache fetches its misses through as, which lives as long as the layer. */
 typedef struct {
     k3x_moe_layer *L;
     const K3MoeW  *w;
     const void    *gate, *sh1, *down, *src;
     int            hidden, n_experts, topk, moe_inter, latent;
+    adapter_src    as;
 } adapter_slot;
 
 static adapter_slot g_slots[K3X_ADAPTER_MAX_LAYERS];
-
-typedef struct {
-    k3x_expert_src  base;   /* first member: the callback casts back */
-    K3ExpertSrc    *src;
-} adapter_src;
 
 static int adapter_getmany(k3x_expert_src *self, int layer, const int *experts, int n)
 {
@@ -116,6 +119,11 @@ static k3x_moe_layer *layer_for(const K3MoeW *w, const K3Cfg *c)
     as.base.get = adapter_get;
     if (w->src->getmany) as.base.getmany = adapter_getmany;
     as.src = w->src;
+    if (s->L) {                 /* the old layer (and the supplier it holds) goes first */
+        k3x_moe_layer_destroy(s->L);
+        memset(s, 0, sizeof *s);
+    }
+    s->as = as;
     k3x_moe_w kw;
     memset(&kw, 0, sizeof kw);
     kw.gate = w->gate;
@@ -123,13 +131,25 @@ static k3x_moe_layer *layer_for(const K3MoeW *w, const K3Cfg *c)
     kw.sh1 = (const uint16_t *)w->sh1;
     kw.sh3 = (const uint16_t *)w->sh3;
     kw.sh2 = (const uint16_t *)w->sh2;
-    kw.src = &as.base;
+    kw.src = &s->as.base;
     kw.layer = w->layer;
     kw.down = plain ? NULL : down;
     kw.up = plain ? NULL : up;
     kw.latent_norm = w->latent_norm;
     k3x_moe_layer *L = NULL;
-    const int rc = k3x_moe_layer_create(&kc, &kw, 0, &L);
+    /* the whole layer in HBM; when it does not fit (or K3X_ADAPTER_SLOTS asks for it),
+     * an HBM expert cache of that many slots, or of the slots that fit in three quarters
+     * of the free device memory (at least 8 * topk + 1, so that a call of 8 tokens fits),
+     * whose misses come through the same source */
+    const char *forced = getenv("K3X_ADAPTER_SLOTS");
+    int rc = forced ? K3X_E_NOMEM : k3x_moe_layer_create(&kc, &kw, 0, &L);
+    if (rc == K3X_E_NOMEM) {
+        int nslot = forced ? atoi(forced) : k3x_cache_slots_fit(&kc, 0, 0.75);
+        if (!forced && nslot < 8 * kc.topk + 1) nslot = 8 * kc.topk + 1;
+        if (nslot < kc.topk + 1) nslot = kc.topk + 1;
+        if (nslot > kc.n_experts) nslot = kc.n_experts;
+        rc = k3x_moe_layer_create_cached_src(&kc, &kw, nslot, 0, &L);
+    }
     if (rc) {
         /* a failed fetch was counted in k3x_expert_drops; mirror it for the CLI check
          * (k3_run.c:1027-1031) */
@@ -137,7 +157,6 @@ static k3x_moe_layer *layer_for(const K3MoeW *w, const K3Cfg *c)
         fprintf(stderr, "k3x: layer %d upload failed: %s\n", w->layer, k3x_strerror(rc));
         return NULL;
     }
-    if (s->L) k3x_moe_layer_destroy(s->L);
     s->L = L;
     s->w = w;
     s->gate = w->gate; s->sh1 = w->sh1; s->down = w->down; s->src = w->src;
@@ -165,6 +184,8 @@ static int run(int prefill, float *out, const float *x, const K3MoeW *w, const K
         rc = prefill ? k3x_moe_prefill(L, out, x, T, idx, wt) : k3x_moe(L, out, x, T, idx, wt);
     if (w->cache_only) k3x_moe_layer_set_cache_only(L, 0, NULL);
     if (rc) {
+        /* an expert the cache could not fetch: counted like the reference's per-token drop */
+        if (rc == K3X_E_DROP) k3_expert_drops++;
         fprintf(stderr, "k3x: layer %d call failed: %s\n", w->layer, k3x_strerror(rc));
         return -1;
     }

@@ -46,6 +46,7 @@ EXPORTS = [
     "k3x_moe_layer_create_cached",
     "k3x_cache_stats",
     "k3x_cache_pin", "k3x_cache_getmany", "k3x_cache_resident", "k3x_moe_layer_set_cache_only",
+    "k3x_moe_layer_create_cached_src", "k3x_cache_slots_fit",
     # include/k3x_trunk.h
     "k3x_trunk_create", "k3x_trunk_destroy", "k3x_trunk_apply", "k3x_trunk_apply_host",
 ]
@@ -184,6 +185,9 @@ def lib():
         L.k3x_cache_getmany.argtypes = [vp, C.POINTER(C.c_int), i]
         L.k3x_cache_resident.argtypes = [vp, i]
         L.k3x_moe_layer_set_cache_only.argtypes = [vp, i, C.c_void_p]
+        L.k3x_moe_layer_create_cached_src.argtypes = [C.POINTER(Cfg), C.POINTER(MoeW), i, i,
+                                                      C.POINTER(vp)]
+        L.k3x_cache_slots_fit.argtypes = [C.POINTER(Cfg), i, C.c_double]
         L.k3x_attn_res.argtypes = [vp, vp, i, i, vp, vp, i, i, f, vp]
         L.k3x_moe_half.argtypes = [vp, vp, vp, vp, i, i, vp, vp, f, i, vp, vp]
         L.k3x_trunk_create.argtypes = [vp, i, i, i, C.POINTER(vp)]
@@ -206,6 +210,11 @@ def _check(rc, what):
     if rc < 0:
         raise K3XError(rc, what)
     return rc
+
+
+def cache_slots_fit(cfg, device=0, fraction=0.75):
+    """k3x_cache_slots_fit: expert slots that fit in that fraction of free device memory."""
+    return _check(lib().k3x_cache_slots_fit(C.byref(cfg), device, fraction), "k3x_cache_slots_fit")
 
 
 def expert_drops():
@@ -289,6 +298,45 @@ class MoELayer:
         _check(lib().k3x_moe_layer_create(C.byref(cfg), C.byref(w), device, C.byref(h)),
                "k3x_moe_layer_create")
         return cls(h.value, cfg)
+
+    @classmethod
+    def from_source_cached(cls, cfg, gate, bias, get, nslot, sh1=None, sh3=None, sh2=None,
+                           layer=0, device=0, down=None, up=None, latent_norm=None,
+                           getmany=None):
+        """An HBM expert cache of nslot slots whose misses come through get (and getmany)
+        as in from_source (k3x_moe_layer_create_cached_src); the callbacks are kept alive
+        with the layer."""
+        hold = {}
+
+        def _get(src, lay, e, out):
+            ex = get(lay, e)
+            if ex is None:
+                return -1
+            arrs = {k: np.ascontiguousarray(ex[k], dtype=np.uint8)
+                    for k in ("p1", "s1", "p3", "s3", "p2", "s2")}
+            hold["cur"] = arrs
+            for k, a in arrs.items():
+                setattr(out.contents, k, a.ctypes.data)
+            return 0
+
+        cb = GET_FN(_get)
+        src = ExpertSrc(cb, None)
+        hold["get"] = cb
+        if getmany is not None:
+            def _getmany(src_, lay, ex, n):
+                return int(getmany(lay, [ex[i] for i in range(n)]))
+            hold["getmany"] = GETMANY_FN(_getmany)
+            src.getmany = hold["getmany"]
+        hold["src"] = src
+        w = MoeW(_vp(gate), _vp(bias), _vp(sh1), _vp(sh3), _vp(sh2), C.pointer(src), None,
+                 layer, _vp(down), _vp(up), _vp(latent_norm))
+        h = C.c_void_p()
+        _check(lib().k3x_moe_layer_create_cached_src(C.byref(cfg), C.byref(w), nslot, device,
+                                                     C.byref(h)),
+               "k3x_moe_layer_create_cached_src")
+        layer_ = cls(h.value, cfg)
+        layer_._hold = hold
+        return layer_
 
     @classmethod
     def from_store(cls, cfg, gate, bias, store, layer, sh1=None, sh3=None, sh2=None, device=0,

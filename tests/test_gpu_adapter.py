@@ -147,3 +147,31 @@ def test_binding_refusals_and_drops(adl, k3x):
     assert s == 0 and d == 0 and np.array_equal(i, ri)
     assert synth.rel_l2(o, ro) < TOL
     assert adl.k3_moe_gpu_scratch(None, 8) == 0
+
+
+@pytest.mark.parametrize("slots,T,mode", [("6", 1, 2), ("12", 3, 2), ("16", 20, 3)])
+def test_binding_over_an_expert_cache(adl, slots, T, mode, monkeypatch):
+    """K3X_ADAPTER_SLOTS makes the binding keep the layer as an HBM expert cache fed by
+    the reference's own source (what it does when a whole layer does not fit): against
+    the reference's CPU path with the same source.  A call whose tokens name more experts
+    than the slots returns -1 (the caller's CPU path runs it)."""
+    say(f"case: binding over an expert cache of {slots} slots, T={T}, mode {mode}")
+    monkeypatch.setenv("K3X_ADAPTER_SLOTS", slots)
+    adl.refdrv_gpu_release()
+    L = synth.tiny(seed=10)
+    c = Call(L, k2_emulation=True)
+    x = L.x(T, bf16=False)
+    go, gi, gw, gd, gs = c(adl, x, mode)
+    ro, ri, rw, rd, rs = c(adl, x, mode - 2)
+    assert gs == 0 and rs == 0 and gd == 0 and rd == 0
+    assert np.array_equal(gi, ri)
+    err = synth.rel_l2(go, ro)
+    say(f"  rel_l2 vs the reference's CPU path = {err:.3e}")
+    assert err < TOL
+    if slots == "6":
+        x3 = L.x(3, bf16=False)
+        _, i3, _, _ = L.oracle_moe(x3)
+        assert len(np.unique(i3)) > 6
+        o, i, w, d, s = c(adl, x3, 2)
+        assert s == -1 and d == 0 and np.all(o == np.float32(7.0))
+    adl.refdrv_gpu_release()

@@ -147,3 +147,46 @@ def test_cache_only_cached_layer_reads_nothing(torch, k3x, tmp_path):
     assert np.array_equal(idx, oi)
     assert synth.rel_l2(out, o) < TOL
     c.close(); st.close()
+
+
+def test_cached_layer_over_a_supplier(torch, k3x):
+    """A cache whose misses come through get() (k3x_moe_layer_create_cached_src), the
+    getmany() of each batch of misses called first: equal bit for bit to the resident
+    layer, the getmany calls naming exactly the misses; a failing get() is a drop
+    (K3X_E_DROP, counted) and the layer keeps working."""
+    say("case: expert cache over a get()/getmany() supplier, 7 slots")
+    L = synth.tiny(seed=46)
+    cfg = layer_cfg(k3x, L)
+    asked, fail = [], set()
+
+    def get(lay, e):
+        return None if e in fail else L.expert(e)
+
+    def getmany(lay, ex):
+        asked.append(list(ex))
+        return len(ex)
+
+    c = k3x.MoELayer.from_source_cached(cfg, L.gate, L.bias, get, cfg.topk + 3, L.sh1, L.sh3,
+                                        L.sh2, getmany=getmany)
+    full = bank_layer(k3x, L)
+    x = L.x(10, bf16=False, stream_sub=9)
+    for t in range(10):
+        of, i_f, _ = dev_forward(torch, k3x, full, x[t:t + 1])
+        oc, i_c, _ = dev_forward(torch, k3x, c, x[t:t + 1])
+        assert np.array_equal(i_f, i_c)
+        assert np.array_equal(of.view(np.uint32), oc.view(np.uint32))
+    s = c.cache_stats()
+    assert sum(len(a) for a in asked) == s["misses"] and s["evictions"] > 0
+    _, inext, _, _ = L.oracle_moe(x[:1])
+    victim = next(e for e in inext[0] if not c.cache_resident(int(e)))
+    fail.add(int(victim))
+    d0 = k3x.expert_drops()
+    with pytest.raises(k3x.K3XError) as ei:
+        dev_forward(torch, k3x, c, x[:1])
+    assert ei.value.status == -5 and k3x.expert_drops() == d0 + 1
+    fail.clear()
+    oc, _, _ = dev_forward(torch, k3x, c, x[:1])
+    of, _, _ = dev_forward(torch, k3x, full, x[:1])
+    assert np.array_equal(oc.view(np.uint32), of.view(np.uint32))
+    assert k3x.cache_slots_fit(cfg) > 0
+    c.close(); full.close()

@@ -611,9 +611,13 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
     constexpr int QB = NCOL * 128 * 2;
     constexpr int NJ = QB / (NTH * 16);
     constexpr int RING = 4;
-    constexpr int LPI = NMAT * RT32 * 4 + NJ;       // 2 code + 2 scale loads per 32 rows
+    // vector loads a quad issues per wave: 2 code loads per 32 rows and the B pieces, plus
+    // (the first quad of a super-quad) 2 scale dwords per 32 rows, which hold the scale
+    // bytes of the super-quad's four quads
+    constexpr int LPI = NMAT * RT32 * 2 + NJ;
+    constexpr int LPS = LPI + NMAT * RT32 * 2;
     static_assert(NJ * NTH * 16 == QB, "B quad must split evenly");
-    static_assert((RING - 2) * LPI < 64, "vmcnt range");
+    static_assert(LPI + LPS < 64, "vmcnt range");
     __shared__ __attribute__((aligned(16))) uint8_t sB[RING * QB];
 
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
@@ -690,9 +694,12 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
 
     struct AQ {
         u32x4    c[NMAT][RT32][2];
-        uint32_t s[NMAT][RT32][2];
     };
     AQ A[RING];
+    // scale dwords: sn is loaded with the first quad of a super-quad (slot 0: quad q is
+    // always computed from slot q % 4), and copied to sc before that quad is computed,
+    // while the three other quads of the previous super-quad still read sc
+    uint32_t sn[NMAT][RT32][2], sc[NMAT][RT32][2];
     auto ld = [&](int slot, int q) AI {
         const bool on = q < nQ;
         const uint32_t qc = (uint32_t)(q >> 2) * 4352u + (uint32_t)(q & 3) * 1024u;
@@ -704,7 +711,7 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
 #pragma unroll
                 for (int gl = 0; gl < 2; gl++) {
                     A[slot].c[m][i][gl] = wld16(ra[m][i], on ? lc + qc + 512u * gl : K3X_OOB);
-                    A[slot].s[m][i][gl] = wld4(ra[m][i], on ? ls + qs + 128u * gl : K3X_OOB);
+                    if (slot == 0) sn[m][i][gl] = wld4(ra[m][i], on ? ls + qs + 128u * gl : K3X_OOB);
                 }
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
@@ -727,6 +734,14 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
     auto compute = [&](int slot, int q) AI {
         const uint8_t *bb = sB + slot * QB;
         const int sh = 8 * (q & 3);
+        if (slot == 0) {
+#pragma unroll
+            for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                for (int i = 0; i < RT32; i++)
+#pragma unroll
+                    for (int gl = 0; gl < 2; gl++) sc[m][i][gl] = sn[m][i][gl];
+        }
 #pragma unroll
         for (int gl = 0; gl < 2; gl++)
 #pragma unroll
@@ -739,7 +754,7 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
                 for (int m = 0; m < NMAT; m++)
 #pragma unroll
                     for (int i = 0; i < RT32; i++) {
-                        const uint32_t sb = (A[slot].s[m][i][gl] >> sh) & 255u;
+                        const uint32_t sb = (sc[m][i][gl] >> sh) & 255u;
                         const bf16x8 av = EXACT ? dq8_exact(A[slot].c[m][i][gl][d], sb)
                                                 : dq8(A[slot].c[m][i][gl][d], e8m0_scale(sb));
 #pragma unroll
@@ -755,17 +770,16 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm32(PfGemmArgs a)
     }
     SCHED_FENCE();
     int q = 0;
+    // meet quad q + s once the loads issued after its own are all that remain: those of
+    // quads q + s + 1 and q + s + 2, of which q + 4 (the next super-quad's first) also
+    // loads the scale dwords
+    static_assert(RING == 4, "written for a ring of 4");
     for (; q + RING <= nQ; q += RING) {
-#pragma unroll
-        for (int s = 0; s < RING; s++) {
-            meet<(RING - 2) * LPI>();
-            SCHED_FENCE();
-            ld((s + RING - 1) % RING, q + s + RING - 1);
-            SCHED_FENCE();
-            compute(s, q + s);
-        }
+        meet<2 * LPI>();       SCHED_FENCE(); ld(3, q + 3); SCHED_FENCE(); compute(0, q);
+        meet<2 * LPI>();       SCHED_FENCE(); ld(0, q + 4); SCHED_FENCE(); compute(1, q + 1);
+        meet<LPI + LPS>();     SCHED_FENCE(); ld(1, q + 5); SCHED_FENCE(); compute(2, q + 2);
+        meet<LPS + LPI>();     SCHED_FENCE(); ld(2, q + 6); SCHED_FENCE(); compute(3, q + 3);
     }
-    static_assert(RING == 4, "tail written for a ring of 4");
     if (q < nQ)     { meet<2 * LPI>(); compute(0, q); }
     if (q + 1 < nQ) { meet<LPI>();     compute(1, q + 1); }
     if (q + 2 < nQ) { meet<0>();       compute(2, q + 2); }
@@ -921,9 +935,11 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm_mx(PfGemmArgs a)
     constexpr int QB = 8 * NCOL * 16;
     constexpr int NJ = QB / (NTH * 16);
     constexpr int RING = 4;
-    constexpr int LPI = NMAT * RT32 * 4 + NJ + CT;
+    // loads a quad issues per wave (as pf_gemm32's, plus a scale dword per column tile)
+    constexpr int LPI = NMAT * RT32 * 2 + NJ + CT;
+    constexpr int LPS = LPI + NMAT * RT32 * 2;
     static_assert(NJ * NTH * 16 == QB, "B quad must split evenly");
-    static_assert((RING - 2) * LPI < 64, "vmcnt range");
+    static_assert(LPI + LPS < 64, "vmcnt range");
     __shared__ __attribute__((aligned(16))) uint8_t sB[RING * QB];
 
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
@@ -986,10 +1002,10 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm_mx(PfGemmArgs a)
 
     struct AQ {
         u32x4    c[NMAT][RT32][2];
-        uint32_t s[NMAT][RT32][2];
         uint32_t bs[CT];
     };
     AQ A[RING];
+    uint32_t sn[NMAT][RT32][2], sc[NMAT][RT32][2];     // as in pf_gemm32
     auto ld = [&](int slot, int q) AI {
         const bool on = q < nQ;
         const uint32_t qc = (uint32_t)(q >> 2) * 4352u + (uint32_t)(q & 3) * 1024u;
@@ -1001,7 +1017,7 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm_mx(PfGemmArgs a)
 #pragma unroll
                 for (int gl = 0; gl < 2; gl++) {
                     A[slot].c[m][i][gl] = wld16(ra[m][i], on ? lc + qc + 512u * gl : K3X_OOB);
-                    A[slot].s[m][i][gl] = wld4(ra[m][i], on ? ls + qs + 128u * gl : K3X_OOB);
+                    if (slot == 0) sn[m][i][gl] = wld4(ra[m][i], on ? ls + qs + 128u * gl : K3X_OOB);
                 }
 #pragma unroll
         for (int c = 0; c < CT; c++)
@@ -1028,6 +1044,14 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm_mx(PfGemmArgs a)
     auto compute = [&](int slot, int q) AI {
         const uint8_t *bb = sB + slot * QB;
         const int sh = 8 * (q & 3);
+        if (slot == 0) {
+#pragma unroll
+            for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                for (int i = 0; i < RT32; i++)
+#pragma unroll
+                    for (int gl = 0; gl < 2; gl++) sc[m][i][gl] = sn[m][i][gl];
+        }
 #pragma unroll
         for (int st = 0; st < 2; st++) {
             i32x8 bv[CT];
@@ -1046,7 +1070,7 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm_mx(PfGemmArgs a)
                 for (int i = 0; i < RT32; i++) {
                     const u32x4 cw = A[slot].c[m][i][st];
                     const i32x8 av = {(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3], 0, 0, 0, 0};
-                    const int sa = (int)((A[slot].s[m][i][st] >> sh) & 255u);
+                    const int sa = (int)((sc[m][i][st] >> sh) & 255u);
 #pragma unroll
                     for (int c = 0; c < CT; c++)
                         acc[m][i][c] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
@@ -1062,17 +1086,16 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm_mx(PfGemmArgs a)
     }
     SCHED_FENCE();
     int q = 0;
+    // meet quad q + s once the loads issued after its own are all that remain: those of
+    // quads q + s + 1 and q + s + 2, of which q + 4 (the next super-quad's first) also
+    // loads the scale dwords
+    static_assert(RING == 4, "written for a ring of 4");
     for (; q + RING <= nQ; q += RING) {
-#pragma unroll
-        for (int s = 0; s < RING; s++) {
-            meet<(RING - 2) * LPI>();
-            SCHED_FENCE();
-            ld((s + RING - 1) % RING, q + s + RING - 1);
-            SCHED_FENCE();
-            compute(s, q + s);
-        }
+        meet<2 * LPI>();       SCHED_FENCE(); ld(3, q + 3); SCHED_FENCE(); compute(0, q);
+        meet<2 * LPI>();       SCHED_FENCE(); ld(0, q + 4); SCHED_FENCE(); compute(1, q + 1);
+        meet<LPI + LPS>();     SCHED_FENCE(); ld(1, q + 5); SCHED_FENCE(); compute(2, q + 2);
+        meet<LPS + LPI>();     SCHED_FENCE(); ld(2, q + 6); SCHED_FENCE(); compute(3, q + 3);
     }
-    static_assert(RING == 4, "tail written for a ring of 4");
     if (q < nQ)     { meet<2 * LPI>(); compute(0, q); }
     if (q + 1 < nQ) { meet<LPI>();     compute(1, q + 1); }
     if (q + 2 < nQ) { meet<0>();       compute(2, q + 2); }

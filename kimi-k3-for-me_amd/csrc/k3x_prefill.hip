@@ -63,16 +63,18 @@ __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int
 // sequential fma chain on wide-exponent cancelling data); a product of two floats is
 // exact in double, so the chain equals the reference's fma-free loop bit for bit.  A
 // chain cannot be split over k, so the parallelism is the number of 16x16 output tiles:
-// a workgroup takes 48 experts x 64 tokens (each wave 16 tokens, three expert tiles,
-// 12 tiles per CU at 2048 tokens x 384 experts).  K is staged 64 at a time in LDS as
-// float, element k of a chunk at (k % 4) * 16 + k / 4 of its row, so that one 16-byte
-// read gives a lane its operands of four consecutive MFMA steps; the next chunk is
-// fetched into registers during the current one.  Workgroups are dealt expert block
-// fastest, so that with 8 expert blocks each XCD keeps one block's router rows in L2.
+// a workgroup takes 48 experts x 64 tokens as twelve waves of one tile each (three waves
+// a SIMD, whose independent chains keep its matrix core fed; 12 tiles per CU at 2048
+// tokens x 384 experts).  K is staged 64 at a time in LDS as float, element k of a chunk
+// at (k % 4) * 16 + k / 4 of its row, so that one 16-byte read gives a lane its operands
+// of four consecutive MFMA steps; the next chunk is fetched into registers during the
+// current one.  Workgroups are dealt expert block fastest, so that with 8 expert blocks
+// each XCD keeps one block's router rows in L2.
 #define RM_E  48
 #define RM_T  64
 #define RM_KC 64
 #define RM_S  (RM_KC + 4)
+#define RM_NT 768
 
 struct PfRouterArgs {
     const void  *x;
@@ -84,47 +86,39 @@ struct PfRouterArgs {
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-__global__ void __launch_bounds__(PF_NT) pf_router(PfRouterArgs a)
+__global__ void __launch_bounds__(RM_NT) pf_router(PfRouterArgs a)
 {
     __shared__ __attribute__((aligned(16))) float lds[2][RM_E + RM_T][RM_S];
     const int nEB = (a.E + RM_E - 1) / RM_E;
     const int e0 = (blockIdx.x % nEB) * RM_E, t0 = (blockIdx.x / nEB) * RM_T;
     const int tid = threadIdx.x, wave = tid / WAVE, r = tid % 16, g = (tid % WAVE) / 16;
-    // staging roles: W rows tid/16 + 16c (c < 3), k 4*(tid%16) .. +3; x rows tid/8 + 32c
-    // (c < 2), k 8*(tid%8) .. +7
+    const int et = wave % 3, tt = wave / 3;          // this wave's expert and token tiles
+    // staging roles: W row tid/16 (48 rows), k 4*(tid%16) .. +3; x (threads below 512) row
+    // tid/8, k 8*(tid%8) .. +7
     const int wk = 4 * (tid % 16), xk = 8 * (tid % 8);
-    f32x4 wv[3];
-    float xv[2][8];
+    const bool xst = tid < RM_T * 8;
+    f32x4 wv;
+    float xv[8];
     auto fetch = [&](int k0) AI {
-#pragma unroll
-        for (int c = 0; c < 3; c++) {
-            const int e = e0 + tid / 16 + 16 * c;
-            wv[c] = e < a.E ? *(const f32x4 *)(a.W + (size_t)e * a.H + k0 + wk)
-                            : (f32x4){0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int t = t0 + tid / 8 + 32 * c;
-            if (t < a.T) load_x8(a.x, a.x_bf16, (size_t)t * a.H + k0 + xk, xv[c]);
+        const int e = e0 + tid / 16;
+        wv = e < a.E ? *(const f32x4 *)(a.W + (size_t)e * a.H + k0 + wk) : (f32x4){0.f, 0.f, 0.f, 0.f};
+        if (xst) {
+            const int t = t0 + tid / 8;
+            if (t < a.T) load_x8(a.x, a.x_bf16, (size_t)t * a.H + k0 + xk, xv);
             else
 #pragma unroll
-                for (int q = 0; q < 8; q++) xv[c][q] = 0.f;
+                for (int q = 0; q < 8; q++) xv[q] = 0.f;
         }
     };
     auto stage = [&](int b) AI {
 #pragma unroll
-        for (int c = 0; c < 3; c++)
-#pragma unroll
-            for (int q = 0; q < 4; q++) lds[b][tid / 16 + 16 * c][q * 16 + tid % 16] = wv[c][q];
-#pragma unroll
-        for (int c = 0; c < 2; c++)
+        for (int q = 0; q < 4; q++) lds[b][tid / 16][q * 16 + tid % 16] = wv[q];
+        if (xst)
 #pragma unroll
             for (int q = 0; q < 8; q++)
-                lds[b][RM_E + tid / 8 + 32 * c][(q % 4) * 16 + xk / 4 + q / 4] = xv[c][q];
+                lds[b][RM_E + tid / 8][(q % 4) * 16 + xk / 4 + q / 4] = xv[q];
     };
-    f64x4 acc[3];
-#pragma unroll
-    for (int m = 0; m < 3; m++) acc[m] = (f64x4){0.0, 0.0, 0.0, 0.0};
+    f64x4 acc = {0.0, 0.0, 0.0, 0.0};
     fetch(0);
     stage(0);
     __syncthreads();
@@ -134,35 +128,27 @@ __global__ void __launch_bounds__(PF_NT) pf_router(PfRouterArgs a)
         if (kc + 1 < nk) fetch((kc + 1) * RM_KC);
 #pragma unroll
         for (int j0 = 0; j0 < RM_KC / 4; j0 += 4) {
-            const f32x4 xq = *(const f32x4 *)&lds[b][RM_E + 16 * wave + r][g * 16 + j0];
-            f32x4 wq[3];
+            const f32x4 xq = *(const f32x4 *)&lds[b][RM_E + 16 * tt + r][g * 16 + j0];
+            const f32x4 wq = *(const f32x4 *)&lds[b][16 * et + r][g * 16 + j0];
 #pragma unroll
-            for (int m = 0; m < 3; m++) wq[m] = *(const f32x4 *)&lds[b][16 * m + r][g * 16 + j0];
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const double xd = (double)xq[jj];
-#pragma unroll
-                for (int m = 0; m < 3; m++)
-                    acc[m] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)wq[m][jj], xd, acc[m], 0, 0, 0);
-            }
+            for (int jj = 0; jj < 4; jj++)
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)wq[jj], (double)xq[jj], acc, 0, 0, 0);
         }
         if (kc + 1 < nk) stage(b ^ 1);
         __syncthreads();
     }
-    // output tile m, element i of lane (r, g): expert 16m + g + 4i, token 16*wave + r
-    const int t = t0 + 16 * wave + r;
+    // element i of lane (r, g): expert 16 et + g + 4i, token 16 tt + r
+    const int t = t0 + 16 * tt + r;
     if (t >= a.T) return;
 #pragma unroll
-    for (int m = 0; m < 3; m++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = e0 + 16 * m + g + 4 * i;
-            if (e < a.E) {
-                const float sc = sigmoid_ref((float)acc[m][i]);
-                a.score[(size_t)t * a.E + e] = sc;
-                a.choice[(size_t)t * a.E + e] = sc + a.bias[e];
-            }
+    for (int i = 0; i < 4; i++) {
+        const int e = e0 + 16 * et + g + 4 * i;
+        if (e < a.E) {
+            const float sc = sigmoid_ref((float)acc[i]);
+            a.score[(size_t)t * a.E + e] = sc;
+            a.choice[(size_t)t * a.E + e] = sc + a.bias[e];
         }
+    }
 }
 
 // ------------------------------------------------------------------ top-k
@@ -1332,7 +1318,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     PfRouterArgs ar;
     ar.x = x; ar.x_bf16 = x_bf16; ar.W = L->router; ar.bias = L->bias;
     ar.T = T; ar.H = H; ar.E = E; ar.score = B->score; ar.choice = B->choice;
-    hipLaunchKernelGGL(pf_router, dim3(cdiv(T, RM_T) * cdiv(E, RM_E)), dim3(PF_NT), 0, s, ar);
+    hipLaunchKernelGGL(pf_router, dim3(cdiv(T, RM_T) * cdiv(E, RM_E)), dim3(RM_NT), 0, s, ar);
     if ((rc = launch_ok())) PF_RET(rc);
 
     PfTopkArgs at;

@@ -401,10 +401,16 @@ __global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
         g = __builtin_amdgcn_readfirstlane(d.x); rb = __builtin_amdgcn_readfirstlane(d.y);
         p0 = __builtin_amdgcn_readfirstlane(d.z); ntok = __builtin_amdgcn_readfirstlane(d.w);
     } else {
-        const int nc = (a.n0 + TPB - 1) / TPB;
-        if (tile >= nrb * nc) return;
-        rb = tile / nc;
-        const int cb = tile % nc;
+        // one dense product: the tiles are dealt to the 8 XCDs in contiguous runs (the
+        // workgroups go round-robin), so that the column blocks of a row block run back
+        // to back on one XCD and read its weights from that XCD's L2.  The grid is a
+        // multiple of 8; surplus workgroups leave at once.
+        const int nc = (a.n0 + TPB - 1) / TPB, ntiles = nrb * nc;
+        const int per = (ntiles + 7) >> 3;
+        const int k = tile >> 3, dt = (tile & 7) * per + k;
+        if (k >= per || dt >= ntiles) return;
+        rb = dt / nc;
+        const int cb = dt % nc;
         p0 = cb * TPB;
         ntok = min(TPB, a.n0 - p0);
     }
@@ -1287,7 +1293,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         sg.act = B->act_sh; sg.arows = T; sg.out_base = 0;
         sg.b1 = L->b1; sg.b2 = L->b2;
         const int tpb_sg = 4 * 16 / HLg, nrb_sg = cdiv(SI, (PF_NT / WAVE) * 1 * 16);
-        const unsigned grid_sg = nrb_sg * cdiv(T, tpb_sg);
+        const unsigned grid_sg = round8((size_t)nrb_sg * cdiv(T, tpb_sg));
         if (HLg == 1)
             hipLaunchKernelGGL((pf_gemm<false, false, 2, 1, 4, 1, true>), dim3(grid_sg), dim3(PF_NT), 0, side, sg);
         else
@@ -1299,7 +1305,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         sd.bsrc = B->act_sh; sd.brows = T; sd.row_base = 0;
         sd.y = B->y; sd.out_base = TK;
         const int nrb_sd = cdiv(H, (PF_NT / WAVE) * 2 * 16);
-        const unsigned grid_sd = nrb_sd * cdiv(T, 32);
+        const unsigned grid_sd = round8((size_t)nrb_sd * cdiv(T, 32));
         if (!rc) {
             hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_sd), dim3(PF_NT), 0, side, sd);
             rc = launch_ok();
@@ -1360,7 +1366,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         zg.wm[0] = (const uint8_t *)L->ldown; zg.R = X; zg.K = H; zg.n0 = T;
         zg.bsrc = B->xhl; zg.brows = T; zg.row_base = 0;
         zg.y = B->zf; zg.out_base = 0;
-        const unsigned grid_z = cdiv(X, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 4 * 16 / HLg);
+        const unsigned grid_z = round8((size_t)cdiv(X, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 4 * 16 / HLg));
         if (HLg == 1)
             hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 1, false>), dim3(grid_z), dim3(PF_NT), 0, s, zg);
         else
@@ -1461,7 +1467,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         ug.wm[0] = (const uint8_t *)L->lup; ug.R = H; ug.K = X; ug.n0 = T;
         ug.bsrc = B->zhl; ug.brows = T; ug.row_base = 0;
         ug.y = B->y; ug.out_base = 0;
-        const unsigned grid_u = cdiv(H, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 32);
+        const unsigned grid_u = round8((size_t)cdiv(H, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 32));
         hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_u), dim3(PF_NT), 0, s, ug);
         if ((rc = launch_ok())) PF_RET(rc);
         pos = NULL;
@@ -1568,7 +1574,7 @@ extern "C" int k3x_dev_trunk_gemm(const uint16_t *W, int in, int out, float *y, 
     g.wm[0] = (const uint8_t *)W; g.R = out; g.K = in; g.n0 = T;
     g.bsrc = planes; g.brows = T; g.row_base = 0;
     g.y = y; g.out_base = 0; g.ldy = ldy;
-    const unsigned grid = cdiv(out, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 4 * 16 / HL);
+    const unsigned grid = round8((size_t)cdiv(out, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 4 * 16 / HL));
     if (HL == 1)
         hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 1, false>), dim3(grid), dim3(PF_NT), 0, s, g);
     else

@@ -239,6 +239,36 @@ def _vp(a):
     return None if a is None else a.ctypes.data
 
 
+def _supplier(get, getmany=None):
+    """A k3x_expert_src over Python callables: get(layer, expert) -> dict of the six
+    uint8 arrays (p1, s1, p3, s3, p2, s2) or None for a failed fetch; getmany(layer,
+    experts) -> how many are now resident (optional).  Returns the struct and a dict
+    that keeps the callbacks and the last expert's arrays alive: hold it as long as the
+    library may call the supplier."""
+    hold = {}
+
+    def _get(src, lay, e, out):
+        ex = get(lay, e)
+        if ex is None:
+            return -1
+        arrs = {k: np.ascontiguousarray(ex[k], dtype=np.uint8)
+                for k in ("p1", "s1", "p3", "s3", "p2", "s2")}
+        hold["cur"] = arrs
+        for k, a in arrs.items():
+            setattr(out.contents, k, a.ctypes.data)
+        return 0
+
+    hold["get"] = GET_FN(_get)
+    src = ExpertSrc(hold["get"], None)
+    if getmany is not None:
+        def _getmany(src_, lay, ex, n):
+            return int(getmany(lay, [ex[i] for i in range(n)]))
+        hold["getmany"] = GETMANY_FN(_getmany)
+        src.getmany = hold["getmany"]
+    hold["src"] = src
+    return src, hold
+
+
 class MoELayer:
     """A device-resident MoE layer (k3x_moe_layer)."""
 
@@ -271,27 +301,7 @@ class MoELayer:
                     device=0, down=None, up=None, latent_norm=None, getmany=None):
         """get(layer, expert) -> dict of numpy arrays, or None for a failed fetch;
         getmany(layer, experts) -> how many are now resident (optional)."""
-        hold = {}
-
-        def _get(src, lay, e, out):
-            ex = get(lay, e)
-            if ex is None:
-                return -1
-            arrs = {k: np.ascontiguousarray(ex[k], dtype=np.uint8)
-                    for k in ("p1", "s1", "p3", "s3", "p2", "s2")}
-            hold["cur"] = arrs
-            for k, a in arrs.items():
-                setattr(out.contents, k, a.ctypes.data)
-            return 0
-
-        cb = GET_FN(_get)
-        src = ExpertSrc(cb, None)
-        if getmany is not None:
-            def _getmany(src_, lay, ex, n):
-                return int(getmany(lay, [ex[i] for i in range(n)]))
-            cbm = GETMANY_FN(_getmany)
-            src.getmany = cbm
-            hold["getmany"] = cbm
+        src, _hold = _supplier(get, getmany)
         w = MoeW(_vp(gate), _vp(bias), _vp(sh1), _vp(sh3), _vp(sh2), C.pointer(src), None,
                  layer, _vp(down), _vp(up), _vp(latent_norm))
         h = C.c_void_p()
@@ -306,28 +316,7 @@ class MoELayer:
         """An HBM expert cache of nslot slots whose misses come through get (and getmany)
         as in from_source (k3x_moe_layer_create_cached_src); the callbacks are kept alive
         with the layer."""
-        hold = {}
-
-        def _get(src, lay, e, out):
-            ex = get(lay, e)
-            if ex is None:
-                return -1
-            arrs = {k: np.ascontiguousarray(ex[k], dtype=np.uint8)
-                    for k in ("p1", "s1", "p3", "s3", "p2", "s2")}
-            hold["cur"] = arrs
-            for k, a in arrs.items():
-                setattr(out.contents, k, a.ctypes.data)
-            return 0
-
-        cb = GET_FN(_get)
-        src = ExpertSrc(cb, None)
-        hold["get"] = cb
-        if getmany is not None:
-            def _getmany(src_, lay, ex, n):
-                return int(getmany(lay, [ex[i] for i in range(n)]))
-            hold["getmany"] = GETMANY_FN(_getmany)
-            src.getmany = hold["getmany"]
-        hold["src"] = src
+        src, hold = _supplier(get, getmany)
         w = MoeW(_vp(gate), _vp(bias), _vp(sh1), _vp(sh3), _vp(sh2), C.pointer(src), None,
                  layer, _vp(down), _vp(up), _vp(latent_norm))
         h = C.c_void_p()

@@ -314,6 +314,12 @@ __device__ __forceinline__ void pub_f(float *p, float v)
 {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A tagged word of the in-launch handoff: (seq << 32) | v in one 64-bit atomic store.
+__device__ __forceinline__ void pub_t(unsigned long long *p, unsigned seq, uint32_t v)
+{
+    __hip_atomic_store(p, ((unsigned long long)seq << 32) | v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // A workgroup's view of the routing, in LDS.
 struct KSLds {
@@ -338,9 +344,10 @@ __device__ __forceinline__ float ks_weight(const KSLds &l, int K, int t, int e)
 // order over (token, slot), built in parallel: each expert's first item by an LDS
 // minimum, the first items' slots by ballots.  Returns the number of unique experts.
 // With `publish`, also writes the indices and weights, and the unique list and each
-// unique expert's weight per token (written through) for the routed workgroups and k3.
+// unique expert's weight per token (written through) for k3 and the host.  With seq != 0,
+// also the tagged copies that k2's routed workgroups read in the same launch.
 template <int NE>
-__device__ int ks_route(const KSArgs &a, KSLds &l, bool publish)
+__device__ int ks_route(const KSArgs &a, KSLds &l, bool publish, unsigned seq = 0u)
 {
     constexpr int NW = NT / WAVE;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -378,8 +385,15 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish)
                 pub_i(&a.route->uniq[slot], ex);
                 pub_f(&a.route->wtok[slot][0], wsum);
                 for (int t = 1; t < K3X_DECODE_MAX_T; t++) pub_f(&a.route->wtok[slot][t], 0.0f);
+                if (seq) {
+                    pub_t(&a.route->tuniq[slot], seq, (uint32_t)ex);
+                    pub_t(&a.route->twtok[slot][0], seq, __float_as_uint(wsum));
+                }
             }
-            if (lane == 0) pub_i(&a.route->nu, nu);
+            if (lane == 0) {
+                pub_i(&a.route->nu, nu);
+                if (seq) pub_t(&a.route->tnu, seq, (uint32_t)nu);
+            }
         }
         return nu;
     }
@@ -418,6 +432,7 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish)
             const int slot = off + lanes_below(m);
             l.uq[slot] = ex;
             if (publish) pub_i(&a.route->uniq[slot], ex);
+            if (publish && seq) pub_t(&a.route->tuniq[slot], seq, (uint32_t)ex);
         }
         base += tot;
         __syncthreads();
@@ -425,9 +440,14 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish)
     if (publish) {
         for (int f = threadIdx.x; f < base * K3X_DECODE_MAX_T; f += NT) {
             const int slot = f / K3X_DECODE_MAX_T, t = f % K3X_DECODE_MAX_T;
-            pub_f(&a.route->wtok[slot][t], t < a.T ? ks_weight(l, a.K, t, l.uq[slot]) : 0.0f);
+            const float w = t < a.T ? ks_weight(l, a.K, t, l.uq[slot]) : 0.0f;
+            pub_f(&a.route->wtok[slot][t], w);
+            if (seq && t < a.T) pub_t(&a.route->twtok[slot][t], seq, __float_as_uint(w));
         }
-        if (threadIdx.x == 0) pub_i(&a.route->nu, base);
+        if (threadIdx.x == 0) {
+            pub_i(&a.route->nu, base);
+            if (seq) pub_t(&a.route->tnu, seq, (uint32_t)base);
+        }
     }
     return base;
 }
@@ -442,7 +462,7 @@ struct K1Args {
     float       *score, *choice;   // [T][E]
     uint16_t    *xB;               // compact B set of x over whole super-quads
     int          n_rwg;            // workgroups
-    int         *ready;            // k2's routing flag, cleared here
+    unsigned    *seq;              // the call sequence, advanced here
     const float *norm_w;           // RMSNorm weights [H] (fp32 x), or NULL
     float        eps;
     // latent form: z = down . x for the routed experts, and the selection (k1_zdown)
@@ -697,7 +717,10 @@ __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
     __shared__ float s_inv[K3X_DECODE_MAX_T];
     WgTrace tr;
     tr.start(a.trace);
-    if (blockIdx.x == 0 && threadIdx.x == 0) *a.ready = 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const unsigned q = *a.seq + 1u;
+        *a.seq = q ? q : 1u;                 // 0 tags nothing
+    }
     // the B set's entries are dealt across the workgroups (a few per workgroup) and
     // converted while the router's weights are in flight
     k1_router(a, lds, s_inv, true);
@@ -707,8 +730,8 @@ __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
 // ------------------------------------------------------------------ K2
 struct K2Args {
     KSArgs         ks;             // the routing, worked out by workgroup 0
-    const k3x_route *route;
-    int           *ready;          // set by workgroup 0 once the routing is out
+    const k3x_route *route;        // tnu / tuniq / twtok: the tagged routing of this launch
+    const unsigned *seq;           // this call's sequence (advanced by k1)
     int           *err;            // set by a routed workgroup that gave up waiting
     uint64_t       wait_ticks;     // the routed workgroups' bound on the wait
     int            publish;        // 0 only to exercise the bound (failure-handling test)
@@ -787,16 +810,20 @@ __device__ void k2_shared(const K2Args &a, float *lds, int rt)
     });
 }
 
-// Workgroup 0 works out the routing (ks_route) and publishes it: the unique list and
-// weights written through, waited for, then the ready flag (cleared by k1 of the same
-// call).  Next come the shared expert's workgroups, which need no routing and stream
-// meanwhile; then the routed ones, which wait for the flag.  Workgroups are dispatched
-// in order, so workgroup 0 is resident before any routed one waits, and it waits on
-// nothing.  The flag is stored with release semantics and read by a relaxed spin followed
-// by an acquire fence, both at agent scope, so the routing's visibility rests on the
-// memory model.  The wait is still bounded (wait_ticks of the 100 MHz clock, by default 50 ms,
-// far above the selection's few microseconds): a workgroup that gives up sets the error
-// word (k3x_moe_layer_check reports it) and leaves without touching the expert weights.
+// Workgroup 0 works out the routing (ks_route) and publishes it.  Next come the shared
+// expert's workgroups, which need no routing and stream meanwhile; then the routed ones,
+// which wait for it.  Workgroups are dispatched in order, so workgroup 0 is resident
+// before any routed one waits, and it waits on nothing.  The handoff needs no ordering
+// between memory locations: every word a routed workgroup reads (the unique count, its
+// slot's expert, the slot's weight per token) is a 64-bit word (seq << 32) | value,
+// written and read by relaxed atomic operations at agent scope, with seq the call's
+// sequence number (advanced by k1 of the same call).  Atomic operations on one location
+// are coherent, so a word read with this call's seq holds the value workgroup 0 stored
+// in this call, and the reader needs neither a release/acquire pair nor the cache
+// invalidation of an acquire fence (measured: 1.85 us of k2 at b = 1).  The wait is
+// bounded (wait_ticks of the 100 MHz clock, by default 50 ms, far above the selection's
+// few microseconds): a workgroup that gives up sets the error word (k3x_moe_layer_check
+// reports it) and leaves without touching the expert weights.
 
 // Gate and up products of rtw row tiles (16 rows each) of one unique expert: the waves
 // are dealt over the tiles (4/rtw waves per tile, on interleaved super-quads of it);
@@ -824,13 +851,9 @@ __device__ void k2_gateup_body(const K2Args &a, float *lds, int *s_go_p)
     int &s_go = *s_go_p;
     if (blockIdx.x == 0) {
         if (a.sel_done) return;
-        ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        // release at agent scope: every store of the routing (all waves', ordered before
-        // this one by the barrier) is visible to a workgroup that acquires the flag
-        if (threadIdx.x == 0 && a.publish)
-            __hip_atomic_store(a.ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        // publish = 0 (the failure-handling test) leaves the tagged words unwritten, so
+        // that the routed workgroups' bound runs out
+        ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true, a.publish ? *a.seq : 0u);
         return;
     }
     if ((int)blockIdx.x <= a.n_sh) {
@@ -852,28 +875,52 @@ __device__ void k2_gateup_body(const K2Args &a, float *lds, int *s_go_p)
         st.issue(a.rB, bbytes, NT);
         st.commit(NT);
     }
+    // thread 0 reads the routing words this workgroup needs: the unique count, its slot's
+    // expert and the slot's weight per token (into s_w); after an earlier launch's
+    // selection (sel_done) the plain words, written before this launch began
+    __shared__ float s_w[K3X_DECODE_MAX_T];
+    __shared__ int s_e;
+    const k3x_route *rte = a.route;
     if (threadIdx.x == 0) {
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        int go = 1;
-        while (!a.sel_done &&
-               __hip_atomic_load(a.ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-            if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) {
+        int go = 1, e = 0;
+        if (a.sel_done) {
+            if (u >= rte->nu) go = 0;
+            else {
+                e = rte->uniq[u];
+                for (int t = 0; t < a.T; t++) s_w[t] = rte->wtok[u][t];
+            }
+        } else {
+            const unsigned seq = *a.seq;
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            // the word at p once it carries this call's tag; false when the bound ran out
+            auto take = [&](const unsigned long long *p, uint32_t &v) -> bool {
+                for (;;) {
+                    const unsigned long long w =
+                        __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if ((unsigned)(w >> 32) == seq) { v = (uint32_t)w; return true; }
+                    if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) return false;
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            };
+            uint32_t v = 0;
+            bool ok = take(&rte->tnu, v);
+            if (ok && u >= (int)v) go = 0;
+            else if (ok && (ok = take(&rte->tuniq[u], v))) {
+                e = (int)v;
+                for (int t = 0; ok && t < a.T; t++)
+                    if ((ok = take(&rte->twtok[u][t], v))) s_w[t] = __uint_as_float(v);
+            }
+            if (!ok) {
                 __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 go = 0;
-                break;
             }
-            __builtin_amdgcn_s_sleep(2);
         }
-        // the relaxed spin read the released flag: this acquire fence makes the routing
-        // stored before it visible (one cache invalidation, not one per spin)
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         s_go = go;
+        s_e = e;
     }
     __syncthreads();
     if (!s_go) return;
-    const k3x_route *rte = a.route;
-    if (u >= __hip_atomic_load(&rte->nu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;
-    int e = __hip_atomic_load(&rte->uniq[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int e = s_e;
     if (a.slot) e = a.slot[e];
     const uint32_t tb = (uint32_t)fp4_tile_bytes(a.XL);
     const uint8_t *ex = a.experts + (size_t)e * a.expert_bytes + (size_t)rt * tb;
@@ -972,8 +1019,7 @@ __device__ void k2_gateup_body(const K2Args &a, float *lds, int *s_go_p)
     if (sw != 0) return;
     uint16_t *d16 = (uint16_t *)dst;
     per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&s)[8]) AI {
-        const float w = __hip_atomic_load(&rte->wtok[u][tok], __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
+        const float w = s_w[tok];
         for (int i = 0; i < 4; i++) {
             const float y = (w == 0.0f) ? 0.0f : w * situ(s[i], s[4 + i], a.b1, a.b2);
             uint32_t hi, lo;
@@ -1475,7 +1521,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a1.T = T; a1.H = H; a1.E = c->n_experts;
     a1.score = L->score; a1.choice = L->choice; a1.xB = L->xB;
     a1.n_rwg = (c->n_experts + NT1 / WAVE / RWAVES - 1) / (NT1 / WAVE / RWAVES);
-    a1.ready = &L->route->ready;
+    a1.seq = &L->route->seq;
     a1.norm_w = norm_w; a1.eps = eps;
     a1.ldown = L->lat ? L->ldown : NULL; a1.XL = X; a1.zB = L->zB;
     if (norm_w && (L->lat || x_dtype == K3X_BF16 || H > RCH * NT1 * 4 || ((uintptr_t)x & 15) ||
@@ -1510,7 +1556,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a2.trace = NULL;
     a2.ks = ks;
     a2.sel_done = L->lat;
-    a2.route = L->route; a2.ready = &L->route->ready; a2.err = &L->route->err;
+    a2.route = L->route; a2.seq = &L->route->seq; a2.err = &L->route->err;
     a2.wait_ticks = L->wait_ticks; a2.publish = !L->no_publish;
     a2.experts = L->experts; a2.expert_bytes = L->expert_bytes;
     a2.gate_off = L->gate_off; a2.up_off = L->up_off;

@@ -68,12 +68,18 @@ static inline size_t k3x_bf16_matrix_bytes(int R, int K) { return (size_t)R * K 
 /* routing summary written by the router, read by the expert kernels */
 typedef struct k3x_route {
     int   nu;                                   /* unique experts in this call        */
-    int   ready;                                /* selection published (k2); cleared
-                                                   by k1 of the same call              */
+    unsigned seq;                               /* call sequence (advanced by k1, never
+                                                   0 after the first call)            */
     int   err;                                  /* a routed workgroup gave up waiting */
     int   pad[61];
     int   uniq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];        /* first-seen order           */
     float wtok[K3X_DECODE_MAX_T * K3X_MAX_TOPK][K3X_DECODE_MAX_T]; /* [u][token], 0 = not chosen */
+    /* the same routing as k2's routed workgroups read it inside the launch that works it
+       out: each word (seq << 32) | value, so that a word read with this call's seq holds
+       this call's value whatever the order in which the words became visible */
+    unsigned long long tnu;
+    unsigned long long tuniq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];
+    unsigned long long twtok[K3X_DECODE_MAX_T * K3X_MAX_TOPK][K3X_DECODE_MAX_T];
 } k3x_route;
 
 /* prefill working buffers (one allocation), sized for cap_T tokens per pipeline run */

@@ -7,13 +7,15 @@
 //   pf_topk     each token's top-k by one wave (:1700-1716) and the per-expert histogram
 //   pf_scan     per-expert offsets (prefix sum) and the GEMM tile lists
 //   pf_scatter  each (token, slot) to its row in its expert's segment
-//   pf_gemm     grouped GEMMs: gate/up of every expert segment with SwiGLU and the
+//   pf_gemm32   grouped GEMMs: gate/up of every expert segment with SwiGLU and the
 //               routing weight (k3_matmul_mxfp4 :3323-3776, k3_situ_glu :148-161), then
-//               down; the shared expert (bf16, :1848-1860) through the same kernel
+//               down (pf_gemm_mx in the MXFP8 mode)
+//   pf_dense    the shared expert's bf16 products (:1848-1860), the latent projections
+//               and the trunk matrices
 //   pf_combine  per token, the K expert rows summed in top-k order (:1941-1942), plus
 //               the shared row (:1951), plus an optional residual
 //
-// The GEMMs run on v_mfma_f32_16x16x32_bf16 with MXFP4 weights dequantised exactly in
+// The GEMMs run on v_mfma_f32_32x32x16_bf16 with MXFP4 weights dequantised exactly in
 // registers; the activations are bf16 hi + lo pairs (hi only when the input is bf16,
 // whose lo part is zero), so products are exact and only the fp32 accumulation rounds.
 #include "k3x_device.h"
@@ -293,21 +295,18 @@ __global__ void __launch_bounds__(PF_NT) pf_tiles(const int *counts, const int *
     }
 }
 
-// ------------------------------------------------------------------ grouped GEMM
-// Y[p][r] = sum_k W_g[r][k] B[p][k] over the permuted rows p of group g (an expert's
-// segment, or all tokens for the shared expert).  A workgroup computes a tile of
-// NW*RT*16 weight rows (NMAT matrices: gate and up together) by one column block of
-// CT*16 B columns (TPB tokens; HL columns per token: hi, or hi and lo); its four waves
-// own RT row tiles each and share the column block.
+// ------------------------------------------------------------------ GEMMs
+// Y[p][r] = sum_k W_g[r][k] B[p][k] over the rows p of group g: an expert's segment of
+// permuted rows (the grouped GEMMs, pf_gemm32 and pf_gemm_mx), or all rows of one dense
+// product (pf_dense).
 //
-// K advances one 128-wide quad per step through a ring of RING slots: a slot holds the
-// quad's weights for this wave's tiles (registers, range-checked buffer loads) and the
-// quad's B block (LDS, filled by buffer loads straight to LDS: lane i of a load writes
-// 16 bytes at the load's LDS base + 16 i; rows past the block's tokens read out of range
-// and land as zeros).  Each step waits for its own slot's loads, meets the other waves
-// at one barrier (after which every wave's share of the B block is in LDS and the slot
-// used by the previous step is free), refills that slot RING-1 quads ahead and runs the
-// quad's MFMAs.
+// K advances through a ring of slots: a slot holds one step's weights (registers,
+// range-checked buffer loads, or LDS) and its B block (LDS, filled by buffer loads
+// straight to LDS: lane i of a load writes 16 bytes at the load's LDS base + 16 i; rows
+// past the block's tokens read out of range and land as zeros).  Each step waits for its
+// own slot's loads, meets the other waves at one barrier (after which every wave's share
+// of the block is in LDS and the slot used by the previous step is free), refills that
+// slot and runs the step's MFMAs.
 //
 // B sources are activation planes [2][K/8][rows][8] bf16 (hi, lo; each k-group
 // row-major over rows), so the 16-byte pieces of one k-group over consecutive rows are
@@ -340,20 +339,6 @@ struct PfGemmArgs {
     uint8_t        *o8, *o8s;
 };
 
-template <bool FP4, int NMAT, int RT>
-struct AQuad;
-
-template <int NMAT, int RT>
-struct AQuad<true, NMAT, RT> {              // fp4: 16 code bytes + the scale dword per tile
-    u32x4    c[NMAT][RT];
-    uint32_t s[NMAT][RT];
-};
-
-template <int NMAT, int RT>
-struct AQuad<false, NMAT, RT> {             // bf16: 4 x 16 bytes per tile
-    u32x4 c[NMAT][RT][4];
-};
-
 typedef __attribute__((address_space(3))) void lds_void;
 
 // s_waitcnt vmcnt(n) lgkmcnt(0) (expcnt left at its maximum), gfx9 encoding
@@ -373,218 +358,202 @@ __device__ __forceinline__ void meet()
     asm volatile("" ::: "memory");
 }
 
-template <bool FP4, bool EXACT, int NMAT, int RT, int CT, int HL, bool GU>
-__global__ void __launch_bounds__(PF_NT, 2) pf_gemm(PfGemmArgs a)
+// ------------------------------------------------------------------ dense GEMM
+// One dense product Y[p][r] = sum_k W[r][k] B[p][k] with bf16 weights (the shared
+// experts, the latent projections, the trunk matrices): W in the 16-row tile layout
+// (per 128-k quad, 16-byte runs at t*1024 + (row + 16*kq)*16 for k = 32kq + 8t .. +7), B
+// the activation planes.  Both operands go through LDS, fetched by loads straight to LDS,
+// so that every weight byte a workgroup reads serves all of its columns and every B byte
+// all of its rows; the four waves (2 x 2) take RW x CW tiles of 32 x 32 each (NMAT
+// matrices: gate and up of the same rows together) on v_mfma_f32_32x32x16_bf16.
+//
+// K advances 64 at a time through a ring of NS stages.  A stage holds the workgroup's
+// A block as [matrix][k-group g][row][8] and its B block as [g][column][8] (16-byte runs),
+// so that the 32 lanes of an MFMA operand that share a k-group read 512 consecutive
+// bytes.  Each step waits for its stage (the loads issued after it are the NS - 2 stages
+// ahead: stages past the end load out of range, which reads nothing and keeps the count
+// exact), meets the other waves, refills the stage freed by the previous step and runs
+// its 16 k-steps' MFMAs.
+template <int NMAT, int RW, int CW, int HL, bool GU, int NS>
+__global__ void __launch_bounds__(PF_NT) pf_dense(PfGemmArgs a)
 {
-    constexpr int NW = PF_NT / WAVE;
-    constexpr int NCOL = CT * 16;
-    constexpr int TPB = NCOL / HL;
-    constexpr int RPB = NW * RT * 16;
-    constexpr int QB = NCOL * 128 * 2;             // B bytes per quad
-    constexpr int NJ = QB / (PF_NT * 16);          // LDS loads per wave per quad
-    constexpr int RING = 4;
-    constexpr int LPI = NMAT * RT * (FP4 ? 2 : 4) + NJ;   // vector loads per slot per wave
-    static_assert(NJ * PF_NT * 16 == QB, "B quad must split evenly");
-    static_assert((RING - 2) * LPI < 64, "vmcnt range");
-    __shared__ __attribute__((aligned(16))) uint8_t sB[RING * QB];
+    constexpr int BM = 2 * RW * 32;                // rows of each matrix per workgroup
+    constexpr int BN = 2 * CW * 32;                // B columns per workgroup
+    constexpr int TPB = BN / HL;                   // tokens per workgroup
+    constexpr int SA = NMAT * BM * 128;            // A bytes per stage (64 k)
+    constexpr int SB = BN * 128;
+    constexpr int SS = SA + SB;
+    constexpr int NJA = SA / (PF_NT * 16), NJB = SB / (PF_NT * 16);
+    constexpr int LPS = NJA + NJB;                 // vector loads per stage per wave
+    static_assert(NJA * PF_NT * 16 == SA && NJB * PF_NT * 16 == SB, "stage must split evenly");
+    static_assert(NS >= 2 && (NS - 2) * LPS < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) uint8_t sm[NS * SS];
 
-    const int wave = wave_id(), lane = threadIdx.x % WAVE;
-    const int nrb = (a.R + RPB - 1) / RPB;
-    // ---- which tile
-    int g = 0, rb, ntok, p0;
-    const int tile = blockIdx.x;
-    if (a.desc) {
-        // scalar registers (readfirstlane), so that the weight resources are uniform
-        const int ntiles = __builtin_amdgcn_readfirstlane(*a.ntile);
-        if (tile >= ntiles) return;
-        const int4 d = a.desc[tile];
-        g = __builtin_amdgcn_readfirstlane(d.x); rb = __builtin_amdgcn_readfirstlane(d.y);
-        p0 = __builtin_amdgcn_readfirstlane(d.z); ntok = __builtin_amdgcn_readfirstlane(d.w);
-    } else {
-        // one dense product: the tiles are dealt to the 8 XCDs in contiguous runs (the
-        // workgroups go round-robin), so that the column blocks of a row block run back
-        // to back on one XCD and read its weights from that XCD's L2.  The grid is a
-        // multiple of 8; surplus workgroups leave at once.
-        const int nc = (a.n0 + TPB - 1) / TPB, ntiles = nrb * nc;
+    const int wave = wave_id(), lane = threadIdx.x % WAVE, tid = threadIdx.x;
+    const int wr = wave >> 1, wc = wave & 1;
+    int rb, p0, ntok;
+    {
+        // tiles dealt to the 8 XCDs in contiguous runs (workgroups go round-robin), so
+        // that the column blocks of a row block run back to back on one XCD and read its
+        // weights from that XCD's L2; the grid is a multiple of 8, surplus workgroups
+        // leave at once
+        const int nrb = (a.R + BM - 1) / BM, nc = (a.n0 + TPB - 1) / TPB, ntiles = nrb * nc;
         const int per = (ntiles + 7) >> 3;
-        const int k = tile >> 3, dt = (tile & 7) * per + k;
+        const int k = blockIdx.x >> 3, dt = (blockIdx.x & 7) * per + k;
         if (k >= per || dt >= ntiles) return;
         rb = dt / nc;
-        const int cb = dt % nc;
-        p0 = cb * TPB;
+        p0 = (dt % nc) * TPB;
         ntok = min(TPB, a.n0 - p0);
     }
-    const int nQ = a.K >> 7;
+    const int nst = a.K >> 6;
 
-    // ---- this wave's weight tiles
-    const uint32_t tbytes = FP4 ? (uint32_t)fp4_tile_bytes(a.K) : (uint32_t)a.K * 32u;
-    rsrc_t ra[NMAT][RT];
-    bool rvalid[RT];
+    // ---- A: the row block's weights of each matrix; rows past R read out of range
+    const uint32_t tbytes = (uint32_t)a.K * 32u;
+    const int t16 = rb * (BM / 16), R16 = a.R >> 4;
+    const uint32_t ntl = (uint32_t)(R16 - t16 < BM / 16 ? R16 - t16 : BM / 16);
+    rsrc_t ra[NMAT];
 #pragma unroll
-    for (int i = 0; i < RT; i++) {
-        const int rt = (rb * NW + wave) * RT + i;
-        rvalid[i] = rt < (a.R >> 4);
+    for (int m = 0; m < NMAT; m++)
+        ra[m] = make_rsrc(a.wm[m] + (size_t)t16 * tbytes, ntl * tbytes);
+    // load j of a stage: 16-byte run c = j*256 + tid -> (matrix, g, row) of the A block,
+    // or (g, column) of the B block; its offset in the stage's source, less the stage's
+    // own step (A: (st>>1)*4096 + (st&1)*512, B: st*8 k-groups)
+    uint32_t aoff[NJA], boff[NJB];
 #pragma unroll
-        for (int m = 0; m < NMAT; m++)
-            ra[m][i] = make_rsrc(a.wm[m] + (size_t)g * a.gstride + (size_t)rt * tbytes,
-                                 rvalid[i] ? tbytes : 0u);
+    for (int j = 0; j < NJA; j++) {
+        const int c = j * PF_NT + tid;
+        const int rem = c % (BM * 8), g = rem / BM, r = rem % BM;
+        aoff[j] = (uint32_t)(r >> 4) * tbytes + (uint32_t)(g & 3) * 1024u +
+                  (uint32_t)((r & 15) + 16 * (g >> 2)) * 16u;
     }
-    // ---- this lane's B pieces: entry e = (wave*NJ + j)*64 + lane of each quad's block,
-    // e = (t*4 + kq)*NCOL + col, col = tok*HL + hl; k-group g8 = kq*4 + t of the quad
     const int G8 = a.K >> 3;
-    const rsrc_t rbs = make_rsrc(a.bsrc, (uint32_t)((size_t)2 * G8 * a.brows * 16));
-    const uint32_t qstep = (uint32_t)a.brows * 256u;               // 16 k-groups
-    uint32_t boff[NJ];
+    const rsrc_t rbs = make_rsrc(a.bsrc, (uint32_t)((size_t)HL * G8 * a.brows * 16));
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int e = (wave * NJ + j) * WAVE + lane;
-        const int tk = e / NCOL, col = e % NCOL;
-        const int t = tk >> 2, kq = tk & 3, tok = col / HL, hl = col % HL;
-        if (tok < ntok) {
-            const int row = a.perm ? a.perm[p0 + tok] : a.row_base + p0 + tok;
-            boff[j] = ((uint32_t)(hl * G8 + kq * 4 + t) * (uint32_t)a.brows + (uint32_t)row) * 16u;
-        } else {
-            boff[j] = K3X_OOB;
-        }
+    for (int j = 0; j < NJB; j++) {
+        const int c = j * PF_NT + tid;
+        const int g = c / BN, col = c % BN, tok = col / HL, hl = col % HL;
+        boff[j] = tok < ntok ? ((uint32_t)(hl * G8 + g) * (uint32_t)a.brows +
+                                (uint32_t)(a.row_base + p0 + tok)) * 16u
+                             : K3X_OOB;
     }
+    const uint32_t bstep = (uint32_t)a.brows * 128u;          // 8 k-groups of B
 
-    AQuad<FP4, NMAT, RT> A[RING];
-    auto ld = [&](int slot, int q) AI {
-        const bool on = q < nQ;
+    auto ld = [&](int slot, int st) AI {
+        const bool on = st < nst;
+        const uint32_t sa = (uint32_t)(st >> 1) * 4096u + (uint32_t)(st & 1) * 512u;
+        uint8_t *base = sm + slot * SS;
 #pragma unroll
-        for (int m = 0; m < NMAT; m++)
-#pragma unroll
-            for (int i = 0; i < RT; i++) {
-                if constexpr (FP4) {
-                    const uint32_t sq = (uint32_t)(q >> 2) * 4352u;
-                    const uint32_t oc = on ? sq + (uint32_t)(q & 3) * 1024u + lane * 16u : K3X_OOB;
-                    const uint32_t os = on ? sq + 4096u + lane * 4u : K3X_OOB;
-                    A[slot].c[m][i] = wld16(ra[m][i], oc);
-                    A[slot].s[m][i] = wld4(ra[m][i], os);
-                } else {
-                    const uint32_t o = on ? (uint32_t)q * 4096u + lane * 16u : K3X_OOB;
-#pragma unroll
-                    for (int t = 0; t < 4; t++) A[slot].c[m][i][t] = wld16(ra[m][i], o + 1024u * t);
-                }
-            }
-        // no select here: an out-of-range base stays out of range (bases < 2^30, steps
-        // < 2^30), and a quad past the end loads bytes that are never used
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const uint32_t o = boff[j] + (uint32_t)q * qstep;
+        for (int j = 0; j < NJA; j++) {
+            const int m = (j * PF_NT) / (BM * 8);            // uniform per load
+            // (resource and offset through locals: the host pass of this template
+            // rejects a captured array element as the builtin's operand)
+            const rsrc_t r = ra[m];
+            const uint32_t o = on ? aoff[j] + sa : K3X_OOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rbs, (lds_void *)(sB + slot * QB + (wave * NJ + j) * 1024), 16, o, 0, 0, 0);
+                r, (lds_void *)(base + (j * PF_NT + wave * WAVE) * 16), 16, o, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < NJB; j++) {
+            const uint32_t o = on ? boff[j] + (uint32_t)st * bstep : K3X_OOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rbs, (lds_void *)(base + SA + (j * PF_NT + wave * WAVE) * 16), 16, o, 0, 0, 0);
         }
     };
 
-    f32x4 acc[NMAT][RT][CT];
+    f32x16 acc[NMAT][RW][CW];
 #pragma unroll
     for (int m = 0; m < NMAT; m++)
 #pragma unroll
-        for (int i = 0; i < RT; i++)
+        for (int i = 0; i < RW; i++)
 #pragma unroll
-            for (int c = 0; c < CT; c++) acc[m][i][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            for (int c = 0; c < CW; c++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[m][i][c][v] = 0.f;
 
-    const int n16 = lane & 15, kq = lane >> 4;
-    auto compute = [&](int slot, int q) AI {
-        const uint8_t *bb = sB + slot * QB;
+    const int l32 = lane & 31, h = lane >> 5;
+    auto compute = [&](int slot) AI {
+        const uint8_t *base = sm + slot * SS;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            bf16x8 bf[CT];
+        for (int s4 = 0; s4 < 4; s4++) {
+            const int g = 2 * s4 + h;
+            bf16x8 bf[CW];
 #pragma unroll
-            for (int c = 0; c < CT; c++)
-                bf[c] = as_bf16x8(*(const u32x4 *)(bb + ((t * 4 + kq) * NCOL + c * 16 + n16) * 16));
+            for (int c = 0; c < CW; c++)
+                bf[c] = as_bf16x8(*(const u32x4 *)(base + SA + (g * BN + (wc * CW + c) * 32 + l32) * 16));
 #pragma unroll
             for (int m = 0; m < NMAT; m++)
 #pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    bf16x8 av;
-                    if constexpr (FP4) {
-                        const uint32_t sb = (A[slot].s[m][i] >> (8 * (q & 3))) & 255u;
-                        av = EXACT ? dq8_exact(A[slot].c[m][i][t], sb)
-                                   : dq8(A[slot].c[m][i][t], e8m0_scale(sb));
-                    } else {
-                        av = as_bf16x8(A[slot].c[m][i][t]);
-                    }
+                for (int i = 0; i < RW; i++) {
+                    const bf16x8 av = as_bf16x8(
+                        *(const u32x4 *)(base + ((m * 8 + g) * BM + (wr * RW + i) * 32 + l32) * 16));
 #pragma unroll
-                    for (int c = 0; c < CT; c++) acc[m][i][c] = mfma(av, bf[c], acc[m][i][c]);
+                    for (int c = 0; c < CW; c++) acc[m][i][c] = mfma32(av, bf[c], acc[m][i][c]);
                 }
         }
     };
 
 #pragma unroll
-    for (int s = 0; s < RING - 1; s++) {
+    for (int s = 0; s < NS - 1; s++) {
         SCHED_FENCE();
         ld(s, s);
     }
     SCHED_FENCE();
-    int q = 0;
-    for (; q + RING <= nQ; q += RING) {
-#pragma unroll
-        for (int s = 0; s < RING; s++) {
-            meet<(RING - 2) * LPI>();
-            SCHED_FENCE();
-            ld((s + RING - 1) % RING, q + s + RING - 1);
-            SCHED_FENCE();
-            compute(s, q + s);
-        }
+    for (int st = 0; st < nst; st++) {
+        meet<(NS - 2) * LPS>();
+        SCHED_FENCE();
+        ld((st + NS - 1) % NS, st + NS - 1);
+        SCHED_FENCE();
+        compute(st % NS);
     }
-    // the last quads: their loads are all in flight already and nothing more is issued
-    // (a refill here would be dead, and the compiler drops the dead register loads, so
-    // the wait counts below count only what the loop and the prime issued)
-    static_assert(RING == 4, "tail written for a ring of 4");
-    if (q < nQ)     { meet<2 * LPI>(); compute(0, q); }
-    if (q + 1 < nQ) { meet<LPI>();     compute(1, q + 1); }
-    if (q + 2 < nQ) { meet<0>();       compute(2, q + 2); }
     // no load to LDS may still be landing when the workgroup ends
     WAIT_VMCNT_LGKM0(0);
 
-    // ---- epilogue: lane (n16, kq) holds rows 4*kq .. 4*kq+3 of each row tile, column n16
+    // ---- epilogue: lane holds column l32 of each column tile, rows 8aa + 4h + b
     const int G8o = a.R >> 3;
 #pragma unroll
-    for (int c = 0; c < CT; c++) {
-        const int col = c * 16 + n16;
+    for (int c = 0; c < CW; c++) {
+        const int col = (wc * CW + c) * 32 + l32;
         const int tl = col / HL;
         const bool writer = (HL == 1 || (col & 1) == 0) && tl < ntok;
         const int p = p0 + tl;
 #pragma unroll
-        for (int i = 0; i < RT; i++) {
-            const int r0 = ((rb * NW + wave) * RT + i) * 16 + 4 * kq;
-            float v0[4], v1[4];
+        for (int i = 0; i < RW; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                v0[j] = acc[0][i][c][j];
-                if (HL == 2) v0[j] += __shfl_xor(v0[j], 1);
-                if (NMAT == 2) {
-                    v1[j] = acc[NMAT - 1][i][c][j];
-                    if (HL == 2) v1[j] += __shfl_xor(v1[j], 1);
+            for (int aa = 0; aa < 4; aa++) {
+                const int r0 = rb * BM + (wr * RW + i) * 32 + 8 * aa + 4 * h;
+                float v0[4], v1[4];
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    v0[b] = acc[0][i][c][4 * aa + b];
+                    if (HL == 2) v0[b] += __shfl_xor(v0[b], 1);
+                    if (NMAT == 2) {
+                        v1[b] = acc[NMAT - 1][i][c][4 * aa + b];
+                        if (HL == 2) v1[b] += __shfl_xor(v1[b], 1);
+                    }
+                }
+                if (!writer || r0 >= a.R) continue;
+                if (GU) {
+                    uint32_t hi[4], lo[4];
+#pragma unroll
+                    for (int b = 0; b < 4; b++) split_bf16(situ(v0[b], v1[b], a.b1, a.b2), hi[b], lo[b]);
+                    const size_t o = ((size_t)(r0 >> 3) * a.arows + (size_t)(a.out_base + p)) * 8 + (r0 & 7);
+                    const size_t plane = (size_t)G8o * a.arows * 8;
+                    *(u32x2 *)(a.act + o) = (u32x2){hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+                    *(u32x2 *)(a.act + plane + o) = (u32x2){lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+                } else {
+                    float *dst = a.y + (size_t)(a.out_base + p) * (a.ldy ? a.ldy : a.R) + r0;
+                    *(f32x4 *)dst = (f32x4){v0[0], v0[1], v0[2], v0[3]};
                 }
             }
-            if (!writer || !rvalid[i]) continue;
-            if (GU) {
-                const float w = a.pw ? a.pw[p] : 1.0f;
-                uint32_t hi[4], lo[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float yv = (w == 0.0f) ? 0.0f : w * situ(v0[j], v1[j], a.b1, a.b2);
-                    split_bf16(yv, hi[j], lo[j]);
-                }
-                const size_t o = ((size_t)(r0 >> 3) * a.arows + (size_t)(a.out_base + p)) * 8 + (r0 & 7);
-                const size_t plane = (size_t)G8o * a.arows * 8;
-                *(u32x2 *)(a.act + o) = (u32x2){hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
-                *(u32x2 *)(a.act + plane + o) = (u32x2){lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
-            } else {
-                float *dst = a.y + (size_t)(a.out_base + p) * (a.ldy ? a.ldy : a.R) + r0;
-                *(f32x4 *)dst = (f32x4){v0[0], v0[1], v0[2], v0[3]};
-            }
-        }
     }
 }
 
 // ------------------------------------------------------------------ grouped GEMM, 32x32
-// The routed GEMMs (MXFP4 weights) on v_mfma_f32_32x32x16_bf16.  Same tiling, ring and
-// barrier protocol as pf_gemm; a wave owns RT32 row tiles of 32 rows (two 16-row tiles of
-// the fp4 layout) and the workgroup CT32 column tiles of 32 B columns.
+// The routed GEMMs (MXFP4 weights) on v_mfma_f32_32x32x16_bf16.  A workgroup computes
+// NW*RT32*32 weight rows (NMAT matrices: gate and up together) by CT32 column tiles of 32
+// B columns (HL columns per token: hi, or hi and lo); a wave owns RT32 row tiles of 32
+// rows (two 16-row tiles of the fp4 layout), its weights held in registers through a
+// ring of 4 quads of 128 k, and the waves share each quad's B block in LDS.
 //
 // K order.  Within a quad, lane L (row R = L%32, h = L/32) loads two 16-byte scale
 // groups of row R: group kq = h (load 0) and kq = 2 + h (load 1).  Dword d of load g
@@ -1228,7 +1197,8 @@ static void launch_topk(const PfTopkArgs &a, hipStream_t s)
 // workgroup and CT32 32-column tiles; a small shape for experts of at most one small
 // column block of tokens (little padding, more workgroups per CU) and a large one for the
 // others (fewer re-reads of their weights and activations).
-#define NW_S      4
+#define NW_GS     4
+#define NW_DS     4
 #define NW_B      8
 #define GU_RT32   1
 #define GU_CT32_S 1
@@ -1259,6 +1229,24 @@ static void launch_dn(const PfGemmArgs &a, unsigned grid, hipStream_t s)
 
 static inline unsigned round8(size_t n) { return (unsigned)((n + 7) & ~(size_t)7); }
 
+// stages of the dense GEMM's LDS ring (32 KB each): two, so that two workgroups share a
+// CU (measured at 2048 x 7168 x 7168: 325 us, against 371 with three stages and 365 with
+// four, one workgroup a CU)
+#define DENSE_NS 2
+
+// A dense product on pf_dense: NMAT matrices of R rows over a.n0 B rows, HL B columns per
+// row (1: bf16 activations, 2: hi and lo parts of fp32 ones)
+template <int NMAT, int RW, int CW, bool GU>
+static void launch_dense(const PfGemmArgs &a, int HL, hipStream_t s)
+{
+    const int BM = 2 * RW * 32, BN = 2 * CW * 32;
+    const unsigned grid = round8((size_t)cdiv(a.R, BM) * cdiv(a.n0, BN / HL));
+    if (HL == 1)
+        hipLaunchKernelGGL((pf_dense<NMAT, RW, CW, 1, GU, DENSE_NS>), dim3(grid), dim3(PF_NT), 0, s, a);
+    else
+        hipLaunchKernelGGL((pf_dense<NMAT, RW, CW, 2, GU, DENSE_NS>), dim3(grid), dim3(PF_NT), 0, s, a);
+}
+
 static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, const void *x,
                     int x_dtype, int T, const float *resid, int *uidx, float *uwt,
                     hipStream_t s)
@@ -1276,11 +1264,15 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
                        x, x_bf16, T, H, H, B->xhl, B->counts, E);
     if ((rc = launch_ok())) return rc;
 
-    if (SI > 0) {
-        // the shared expert (bf16 weights, every token) needs only the split activations:
-        // its gate/up and down run on the layer's side stream while the router, the
-        // dispatch and the routed GEMMs run on s.  Its T rows follow the TK routed rows
-        // in y, which nothing on s writes.
+    // The shared expert (bf16 weights, every token) needs only the split activations: its
+    // gate/up and down run on the layer's side stream, forked right after the split, beside
+    // the router, the dispatch and the routed GEMMs on s (measured against forking after
+    // the dispatch, after the large experts' gate/up or after all routed gate/up: 3.83
+    // against 3.83, 3.88 and 3.91 ms at 2048 tokens).  Its T rows follow the TK routed rows
+    // in y, which nothing on s writes.
+    bool forked = false;
+    auto fork_shared = [&]() -> int {
+        if (SI <= 0) return 0;
         hipStream_t side = (hipStream_t)L->pf_side;
         if (hipEventRecord((hipEvent_t)L->pf_ev[0], s) != hipSuccess ||
             hipStreamWaitEvent(side, (hipEvent_t)L->pf_ev[0], 0) != hipSuccess)
@@ -1292,34 +1284,30 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         sg.bsrc = B->xhl; sg.brows = T; sg.row_base = 0;
         sg.act = B->act_sh; sg.arows = T; sg.out_base = 0;
         sg.b1 = L->b1; sg.b2 = L->b2;
-        const int tpb_sg = 4 * 16 / HLg, nrb_sg = cdiv(SI, (PF_NT / WAVE) * 1 * 16);
-        const unsigned grid_sg = round8((size_t)nrb_sg * cdiv(T, tpb_sg));
-        if (HLg == 1)
-            hipLaunchKernelGGL((pf_gemm<false, false, 2, 1, 4, 1, true>), dim3(grid_sg), dim3(PF_NT), 0, side, sg);
-        else
-            hipLaunchKernelGGL((pf_gemm<false, false, 2, 1, 4, 2, true>), dim3(grid_sg), dim3(PF_NT), 0, side, sg);
-        rc = launch_ok();
+        launch_dense<2, 1, 2, true>(sg, HLg, side);
+        int r = launch_ok();
         PfGemmArgs sd;
         memset(&sd, 0, sizeof sd);
         sd.wm[0] = (const uint8_t *)L->sh_down; sd.R = H; sd.K = SI; sd.n0 = T;
         sd.bsrc = B->act_sh; sd.brows = T; sd.row_base = 0;
         sd.y = B->y; sd.out_base = TK;
-        const int nrb_sd = cdiv(H, (PF_NT / WAVE) * 2 * 16);
-        const unsigned grid_sd = round8((size_t)nrb_sd * cdiv(T, 32));
-        if (!rc) {
-            hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_sd), dim3(PF_NT), 0, side, sd);
-            rc = launch_ok();
+        if (!r) {
+            launch_dense<1, 2, 2, false>(sd, 2, side);
+            r = launch_ok();
         }
         // recorded even after a failed launch, so that s can always join the side stream
         if (hipEventRecord((hipEvent_t)L->pf_ev[1], side) != hipSuccess) return K3X_E_HIP;
-        if (rc) {
+        if (r) {
             (void)hipStreamWaitEvent(s, (hipEvent_t)L->pf_ev[1], 0);
-            return rc;
+            return r;
         }
-    }
-    // from here on, a failed launch joins the side stream before it returns
+        forked = true;
+        return 0;
+    };
+    // from the fork on, a failed launch joins the side stream before it returns
 #define PF_RET(e) do { const int e_ = (e); \
-        if (SI > 0) (void)hipStreamWaitEvent(s, (hipEvent_t)L->pf_ev[1], 0); return e_; } while (0)
+        if (forked) (void)hipStreamWaitEvent(s, (hipEvent_t)L->pf_ev[1], 0); return e_; } while (0)
+    if ((rc = fork_shared())) return rc;
 
     PfRouterArgs ar;
     ar.x = x; ar.x_bf16 = x_bf16; ar.W = L->router; ar.bias = L->bias;
@@ -1344,11 +1332,11 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     const bool mx = L->pf_mode == K3X_PREFILL_MXFP8;
     sa.tpb_s[0] = mx ? MX_CT_S * 32 : GU_CT32_S * 32 / HLr;
     sa.tpb_b[0] = mx ? MX_CT_B * 32 : GU_CT32_B * 32 / HLr;
-    sa.nrb_s[0] = cdiv(I, NW_S * GU_RT32 * 32);
+    sa.nrb_s[0] = cdiv(I, (mx ? MX_NW : NW_GS) * GU_RT32 * 32);
     sa.nrb_b[0] = cdiv(I, (mx ? MX_NW : NW_B) * GU_RT32 * 32);
     sa.tpb_s[1] = mx ? MX_CT_S * 32 : DN_CT32_S * 32 / 2;
     sa.tpb_b[1] = mx ? MX_CT_B * 32 : DN_CT32_B * 32 / 2;
-    sa.nrb_s[1] = cdiv(X, NW_S * DN_RT32 * 32);
+    sa.nrb_s[1] = cdiv(X, (mx ? MX_NW : NW_DS) * DN_RT32 * 32);
     sa.nrb_b[1] = cdiv(X, (mx ? MX_NW : NW_B) * DN_RT32 * 32);
     hipLaunchKernelGGL(pf_scan, dim3(1), dim3(1024), 0, s, sa);
     if ((rc = launch_ok())) PF_RET(rc);
@@ -1366,11 +1354,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         zg.wm[0] = (const uint8_t *)L->ldown; zg.R = X; zg.K = H; zg.n0 = T;
         zg.bsrc = B->xhl; zg.brows = T; zg.row_base = 0;
         zg.y = B->zf; zg.out_base = 0;
-        const unsigned grid_z = round8((size_t)cdiv(X, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 4 * 16 / HLg));
-        if (HLg == 1)
-            hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 1, false>), dim3(grid_z), dim3(PF_NT), 0, s, zg);
-        else
-            hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_z), dim3(PF_NT), 0, s, zg);
+        launch_dense<1, 2, 2, false>(zg, HLg, s);
         if ((rc = launch_ok())) PF_RET(rc);
         if (!mx) {
             hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (X / 8), PF_NT)), dim3(PF_NT), 0, s,
@@ -1420,15 +1404,25 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     PfGemmArgs gb = g;
     g.ntile = B->tb_gu + E;
     gb.ntile = B->tb_gu + 2 * E + 1; gb.dbase = B->tb_gu + E;
+    // the large-expert tiles first, then the small ones
     if (mx) {
         hipLaunchKernelGGL((pf_gemm_mx<2, GU_RT32, MX_CT_B, true, MX_NW>), dim3(grid_b[0]), dim3(MX_NW * WAVE), 0, s, gb);
+    } else if (ex_gu) {
+        if (HLr == 1) launch_gu<true, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s);
+        else          launch_gu<true, 2, GU_CT32_B, NW_B>(gb, grid_b[0], s);
+    } else {
+        if (HLr == 1) launch_gu<false, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s);
+        else          launch_gu<false, 2, GU_CT32_B, NW_B>(gb, grid_b[0], s);
+    }
+    if ((rc = launch_ok())) PF_RET(rc);
+    if (mx) {
         hipLaunchKernelGGL((pf_gemm_mx<2, GU_RT32, MX_CT_S, true, MX_NW>), dim3(grid_s[0]), dim3(MX_NW * WAVE), 0, s, g);
     } else if (ex_gu) {
-        if (HLr == 1) { launch_gu<true, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<true, 1, GU_CT32_S, NW_S>(g, grid_s[0], s); }
-        else          { launch_gu<true, 2, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<true, 2, GU_CT32_S, NW_S>(g, grid_s[0], s); }
+        if (HLr == 1) launch_gu<true, 1, GU_CT32_S, NW_GS>(g, grid_s[0], s);
+        else          launch_gu<true, 2, GU_CT32_S, NW_GS>(g, grid_s[0], s);
     } else {
-        if (HLr == 1) { launch_gu<false, 1, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<false, 1, GU_CT32_S, NW_S>(g, grid_s[0], s); }
-        else          { launch_gu<false, 2, GU_CT32_B, NW_B>(gb, grid_b[0], s); launch_gu<false, 2, GU_CT32_S, NW_S>(g, grid_s[0], s); }
+        if (HLr == 1) launch_gu<false, 1, GU_CT32_S, NW_GS>(g, grid_s[0], s);
+        else          launch_gu<false, 2, GU_CT32_S, NW_GS>(g, grid_s[0], s);
     }
     if ((rc = launch_ok())) PF_RET(rc);
 
@@ -1446,8 +1440,8 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     if (mx) {
         hipLaunchKernelGGL((pf_gemm_mx<1, DN_RT32, MX_CT_B, false, MX_NW>), dim3(grid_b[1]), dim3(MX_NW * WAVE), 0, s, db);
         hipLaunchKernelGGL((pf_gemm_mx<1, DN_RT32, MX_CT_S, false, MX_NW>), dim3(grid_s[1]), dim3(MX_NW * WAVE), 0, s, d);
-    } else if (L->special & 4) { launch_dn<true, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<true, DN_CT32_S, NW_S>(d, grid_s[1], s); }
-    else                { launch_dn<false, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<false, DN_CT32_S, NW_S>(d, grid_s[1], s); }
+    } else if (L->special & 4) { launch_dn<true, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<true, DN_CT32_S, NW_DS>(d, grid_s[1], s); }
+    else                { launch_dn<false, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<false, DN_CT32_S, NW_DS>(d, grid_s[1], s); }
     if ((rc = launch_ok())) PF_RET(rc);
 
     int sh_row0 = -1;
@@ -1467,13 +1461,12 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         ug.wm[0] = (const uint8_t *)L->lup; ug.R = H; ug.K = X; ug.n0 = T;
         ug.bsrc = B->zhl; ug.brows = T; ug.row_base = 0;
         ug.y = B->y; ug.out_base = 0;
-        const unsigned grid_u = round8((size_t)cdiv(H, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 32));
-        hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid_u), dim3(PF_NT), 0, s, ug);
+        launch_dense<1, 2, 2, false>(ug, 2, s);
         if ((rc = launch_ok())) PF_RET(rc);
         pos = NULL;
         KC = 1;
     }
-    if (SI > 0) {
+    if (forked) {
         // the shared rows are in y: join the shared stream
         if (hipStreamWaitEvent(s, (hipEvent_t)L->pf_ev[1], 0) != hipSuccess) return K3X_E_HIP;
         sh_row0 = TK;
@@ -1574,10 +1567,6 @@ extern "C" int k3x_dev_trunk_gemm(const uint16_t *W, int in, int out, float *y, 
     g.wm[0] = (const uint8_t *)W; g.R = out; g.K = in; g.n0 = T;
     g.bsrc = planes; g.brows = T; g.row_base = 0;
     g.y = y; g.out_base = 0; g.ldy = ldy;
-    const unsigned grid = round8((size_t)cdiv(out, (PF_NT / WAVE) * 2 * 16) * cdiv(T, 4 * 16 / HL));
-    if (HL == 1)
-        hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 1, false>), dim3(grid), dim3(PF_NT), 0, s, g);
-    else
-        hipLaunchKernelGGL((pf_gemm<false, false, 1, 2, 4, 2, false>), dim3(grid), dim3(PF_NT), 0, s, g);
+    launch_dense<1, 2, 2, false>(g, HL, s);
     return launch_ok();
 }

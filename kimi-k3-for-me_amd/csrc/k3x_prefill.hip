@@ -454,6 +454,8 @@ __global__ void __launch_bounds__(PF_NT) pf_dense(PfGemmArgs a)
         }
 #pragma unroll
         for (int j = 0; j < NJB; j++) {
+            // (a column past the tokens keeps an out-of-range offset: K3X_OOB plus at most
+            // K/64 steps of brows*128 bytes stays below 2^32 and past the planes)
             const uint32_t o = on ? boff[j] + (uint32_t)st * bstep : K3X_OOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rbs, (lds_void *)(base + SA + (j * PF_NT + wave * WAVE) * 16), 16, o, 0, 0, 0);
@@ -983,10 +985,12 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm_mx(PfGemmArgs a)
 #pragma unroll
         for (int c = 0; c < CT; c++)
             A[slot].bs[c] = __builtin_amdgcn_raw_buffer_load_b32(
-                rbsc, on && soff[c] != K3X_OOB ? soff[c] + (uint32_t)q * sstep : K3X_OOB, 0, 0);
+                rbsc, (!on | (soff[c] == K3X_OOB)) ? K3X_OOB : soff[c] + (uint32_t)q * sstep, 0, 0);
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
-            const uint32_t o = boff[j] == K3X_OOB || !on ? K3X_OOB : boff[j] + (uint32_t)q * qstep;
+            // (bitwise, not short-circuit: a branch on the uniform `on` would split the
+            // step into blocks, and the MFMAs would then sink past the next barriers)
+            const uint32_t o = ((boff[j] == K3X_OOB) | !on) ? K3X_OOB : boff[j] + (uint32_t)q * qstep;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rbc, (lds_void *)(sB + slot * QB + (wave * NJ + j) * 1024), 16, o, 0, 0, 0);
         }
@@ -1233,6 +1237,12 @@ static inline unsigned round8(size_t n) { return (unsigned)((n + 7) & ~(size_t)7
 // CU (measured at 2048 x 7168 x 7168: 325 us, against 371 with three stages and 365 with
 // four, one workgroup a CU)
 #define DENSE_NS 2
+// wave tiles (32 x 32 MFMA tiles per wave, four waves as 2 x 2): the gate/up products,
+// and the single-matrix ones
+#define DENSE_GU_RW 1
+#define DENSE_GU_CW 2
+#define DENSE_RW    2
+#define DENSE_CW    2
 
 // A dense product on pf_dense: NMAT matrices of R rows over a.n0 B rows, HL B columns per
 // row (1: bf16 activations, 2: hi and lo parts of fp32 ones)
@@ -1284,7 +1294,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         sg.bsrc = B->xhl; sg.brows = T; sg.row_base = 0;
         sg.act = B->act_sh; sg.arows = T; sg.out_base = 0;
         sg.b1 = L->b1; sg.b2 = L->b2;
-        launch_dense<2, 1, 2, true>(sg, HLg, side);
+        launch_dense<2, DENSE_GU_RW, DENSE_GU_CW, true>(sg, HLg, side);
         int r = launch_ok();
         PfGemmArgs sd;
         memset(&sd, 0, sizeof sd);
@@ -1292,7 +1302,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         sd.bsrc = B->act_sh; sd.brows = T; sd.row_base = 0;
         sd.y = B->y; sd.out_base = TK;
         if (!r) {
-            launch_dense<1, 2, 2, false>(sd, 2, side);
+            launch_dense<1, DENSE_RW, DENSE_CW, false>(sd, 2, side);
             r = launch_ok();
         }
         // recorded even after a failed launch, so that s can always join the side stream
@@ -1354,7 +1364,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         zg.wm[0] = (const uint8_t *)L->ldown; zg.R = X; zg.K = H; zg.n0 = T;
         zg.bsrc = B->xhl; zg.brows = T; zg.row_base = 0;
         zg.y = B->zf; zg.out_base = 0;
-        launch_dense<1, 2, 2, false>(zg, HLg, s);
+        launch_dense<1, DENSE_RW, DENSE_CW, false>(zg, HLg, s);
         if ((rc = launch_ok())) PF_RET(rc);
         if (!mx) {
             hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (X / 8), PF_NT)), dim3(PF_NT), 0, s,
@@ -1461,7 +1471,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         ug.wm[0] = (const uint8_t *)L->lup; ug.R = H; ug.K = X; ug.n0 = T;
         ug.bsrc = B->zhl; ug.brows = T; ug.row_base = 0;
         ug.y = B->y; ug.out_base = 0;
-        launch_dense<1, 2, 2, false>(ug, 2, s);
+        launch_dense<1, DENSE_RW, DENSE_CW, false>(ug, 2, s);
         if ((rc = launch_ok())) PF_RET(rc);
         pos = NULL;
         KC = 1;
@@ -1567,6 +1577,6 @@ extern "C" int k3x_dev_trunk_gemm(const uint16_t *W, int in, int out, float *y, 
     g.wm[0] = (const uint8_t *)W; g.R = out; g.K = in; g.n0 = T;
     g.bsrc = planes; g.brows = T; g.row_base = 0;
     g.y = y; g.out_base = 0; g.ldy = ldy;
-    launch_dense<1, 2, 2, false>(g, HL, s);
+    launch_dense<1, DENSE_RW, DENSE_CW, false>(g, HL, s);
     return launch_ok();
 }

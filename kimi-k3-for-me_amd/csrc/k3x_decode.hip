@@ -727,6 +727,143 @@ __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
     tr.end();
 }
 
+// Router logits of several tokens without the RMSNorm: RM_EPW experts per workgroup,
+// x's rows (raw, bf16 or fp32) staged once in LDS for all of them, TG tokens at a time.
+// Each expert's 256 threads take the chunks, the per-thread order and the reduction tree
+// of k1_router, so every logit is bitwise the single-expert kernel's.  k1_router reads
+// every token's x from L2 in each expert's workgroup, a load and its use at a time (8
+// tokens of the K2 shape: 44 MB of 8-byte loads a call, 21 us a workgroup); staged once
+// per two experts, a workgroup takes 12 us, most of it the double-precision products.
+#define RM_EPW 2
+#define RM_XLDS (120 * 1024)         // LDS for staged x rows
+
+template <int TT, int TG, bool XBF>
+__global__ void __launch_bounds__(NT1 * RM_EPW) k1_router_mt(K1Args a)
+{
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+    __shared__ double dl[RM_EPW * RWAVES][K3X_DECODE_MAX_T];
+    WgTrace tr;
+    tr.start(a.trace);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const unsigned q = *a.seq + 1u;
+        *a.seq = q ? q : 1u;                 // 0 tags nothing
+    }
+    constexpr int XB = XBF ? 2 : 4;          // bytes per x element
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int grp = threadIdx.x / NT1, tl = threadIdx.x % NT1;
+    const int e = blockIdx.x * RM_EPW + grp;
+    const int nf4 = a.H >> 2;
+    const float *row = a.router + (size_t)(e < a.E ? e : 0) * a.H;
+    f32x4 w[RCH];
+#pragma unroll
+    for (int c = 0; c < RCH; c++) {
+        const int f = tl + NT1 * c;
+        w[c] = (f < nf4 && e < a.E) ? __builtin_nontemporal_load((const f32x4 *)(row + 4 * f))
+                                    : (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    {
+        // this workgroup's share of x's B set, as k1_router deals it over 256-thread groups
+        const int nS = ((a.H >> 7) + 3) >> 2;
+        const int tid = threadIdx.x * (int)gridDim.x + blockIdx.x, nth = (int)gridDim.x * NT1 * RM_EPW;
+        x_to_bset((uint8_t *)a.xB, a.x, a.x_bf16, a.H, 2 * a.T, 4 * nS, tid, nth);
+    }
+    for (int t0 = 0; t0 < TT; t0 += TG) {
+        const int ng = TT - t0 < TG ? TT - t0 : TG;
+        // rows t0 .. t0 + ng - 1 into LDS, 16 bytes a thread at a time
+        const size_t rowb = (size_t)a.H * XB;
+        const uint8_t *src = (const uint8_t *)a.x + (size_t)t0 * rowb;
+        const int n16 = (int)((size_t)ng * rowb / 16);
+        if (t0) __syncthreads();             // the previous group's reads are done
+        // eight loads in flight per thread before their stores (one at a time, each
+        // would wait out its own latency)
+        constexpr int NB = NT1 * RM_EPW, UNR = 8;
+        for (int i0 = 0; i0 < n16; i0 += NB * UNR) {
+            u32x4 r[UNR];
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                const int i = i0 + u * NB + (int)threadIdx.x;
+                r[u] = i < n16 ? *(const u32x4 *)(src + (size_t)i * 16) : (u32x4){0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                const int i = i0 + u * NB + (int)threadIdx.x;
+                if (i < n16) *(u32x4 *)(xs + (size_t)i * 16) = r[u];
+            }
+        }
+        __syncthreads();
+        // one token at a time (a loop, not unrolled: unrolled, every token's widened x
+        // would be live at once): this thread's chain, then the wave's sum
+#pragma unroll 1
+        for (int g = 0; g < ng; g++) {
+            double v = 0.0;
+#pragma unroll
+            for (int c = 0; c < RCH; c++) {
+                const int f = tl + NT1 * c;
+                float xv[4] = {0.f, 0.f, 0.f, 0.f};
+                if (f < nf4) {
+                    const uint8_t *px = xs + ((size_t)g * a.H + 4 * f) * XB;
+                    if (XBF) {
+                        const u32x2 r = *(const u32x2 *)px;
+                        xv[0] = bf2f(r[0] & 0xFFFFu); xv[1] = bf2f(r[0] >> 16);
+                        xv[2] = bf2f(r[1] & 0xFFFFu); xv[3] = bf2f(r[1] >> 16);
+                    } else {
+                        const f32x4 r = *(const f32x4 *)px;
+                        xv[0] = r[0]; xv[1] = r[1]; xv[2] = r[2]; xv[3] = r[3];
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) v += (double)w[c][k] * (double)xv[k];
+            }
+            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0) dl[wave][t0 + g] = v;
+        }
+    }
+    __syncthreads();
+    const int wq = wave % RWAVES;
+    if (wq == 0 && lane < TT && e < a.E) {
+        const int t = lane, w0 = grp * RWAVES;
+        const double v = (dl[w0][t] + dl[w0 + 1][t]) + (dl[w0 + 2][t] + dl[w0 + 3][t]);
+        const float sc = sigmoid_ref((float)v);
+        a.score[(size_t)t * a.E + e] = sc;
+        a.choice[(size_t)t * a.E + e] = sc + a.bias[e];
+    }
+    tr.end();
+}
+
+// The router launch: the multi-token kernel for 2 .. 8 tokens without the RMSNorm when a
+// group of at least two rows fits the LDS, else k1_router_bset.  Returns the grid.
+static unsigned launch_k1(const K1Args &a1, hipStream_t s)
+{
+    const int T = a1.T;
+    const size_t rowb = (size_t)a1.H * (a1.x_bf16 ? 2 : 4);
+    const int fit = (int)(RM_XLDS / rowb);
+    if (T >= 2 && !a1.norm_w && fit >= 2 && a1.H <= RCH * NT1 * 4) {
+        const dim3 g((unsigned)((a1.E + RM_EPW - 1) / RM_EPW)), b(NT1 * RM_EPW);
+        const int tg = T <= fit ? T : (fit >= 4 ? 4 : 2);
+        const size_t lds = (size_t)(tg < T ? tg : T) * rowb;
+#define K1MT(TT_) \
+        if (a1.x_bf16) { if (tg >= TT_) hipLaunchKernelGGL((k1_router_mt<TT_, TT_, true>), g, b, lds, s, a1); \
+                         else if (tg >= 4) hipLaunchKernelGGL((k1_router_mt<TT_, (TT_ < 4 ? TT_ : 4), true>), g, b, lds, s, a1); \
+                         else hipLaunchKernelGGL((k1_router_mt<TT_, 2, true>), g, b, lds, s, a1); } \
+        else           { if (tg >= TT_) hipLaunchKernelGGL((k1_router_mt<TT_, TT_, false>), g, b, lds, s, a1); \
+                         else if (tg >= 4) hipLaunchKernelGGL((k1_router_mt<TT_, (TT_ < 4 ? TT_ : 4), false>), g, b, lds, s, a1); \
+                         else hipLaunchKernelGGL((k1_router_mt<TT_, 2, false>), g, b, lds, s, a1); }
+        switch (T) {
+        case 2: K1MT(2) break;
+        case 3: K1MT(3) break;
+        case 4: K1MT(4) break;
+        case 5: K1MT(5) break;
+        case 6: K1MT(6) break;
+        case 7: K1MT(7) break;
+        default: K1MT(8) break;
+        }
+#undef K1MT
+        return g.x;
+    }
+    hipLaunchKernelGGL(k1_router_bset, dim3(a1.n_rwg), dim3(NT1), 0, s, a1);
+    return (unsigned)a1.n_rwg;
+}
+
 // ------------------------------------------------------------------ K2
 struct K2Args {
     KSArgs         ks;             // the routing, worked out by workgroup 0
@@ -1529,9 +1666,9 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
         return K3X_E_ARG;
     unsigned long long *trb = L->tr;
     a1.trace = (trb && a1.n_rwg <= L->tr_cap) ? trb : NULL;
-    if (trb) L->tr_n[0] = a1.trace ? a1.n_rwg : 0;
     if ((rc = record(L, 0, s))) return rc;
-    hipLaunchKernelGGL(k1_router_bset, dim3(a1.n_rwg), dim3(NT1), 0, s, a1);
+    const unsigned g1 = launch_k1(a1, s);
+    if (trb) L->tr_n[0] = a1.trace ? (int)g1 : 0;
     if ((rc = launch_ok())) return rc;
     if ((rc = record(L, 1, s))) return rc;
     int ev = 2;                        // the next timing event

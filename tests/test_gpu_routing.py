@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import synth
-from gpu_util import bank_layer, dev_forward, say
+from gpu_util import bank_layer, dev_forward, say, synth_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -151,4 +151,26 @@ def test_prefill_router_sequential_chain_bitwise(torch, k3x):
                               ol.ptr(L.bias, ol.F32P), H, E, K, 0, 1.0)
     assert np.array_equal(idx, ri)
     assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+    layer.close()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("H,E", [(1024, 100), (7168, 384)])
+def test_decode_router_same_bits_for_any_token_count(torch, k3x, bf16, H, E):
+    """The decode router's logits do not depend on how many tokens a call carries: a call
+    of T = 2 .. 8 tokens (the multi-token kernel, x staged in LDS, several experts a
+    workgroup) gives each token the routing weights of its own T = 1 call (k1_router_bset)
+    bit for bit, and the same experts.  Renorm off and scale 1, so the weights are the
+    sigmoid scores themselves.  E = 100 is not a multiple of the experts per workgroup."""
+    say(f"case: decode router, T=1 calls against T=2..8 calls, H={H} E={E} bf16={bf16}")
+    L = synth.Layer(H=H, E=E, K=8, I=128, seed=51, renorm=0, routed_scale=1.0)
+    layer = synth_layer(k3x, L)
+    x = L.x(8, bf16=bf16, stream_sub=12)
+    ones = [dev_forward(torch, k3x, layer, x[t:t + 1], bf16=bf16) for t in range(8)]
+    i1 = np.concatenate([o[1] for o in ones])
+    w1 = np.concatenate([o[2] for o in ones])
+    for T in (2, 3, 5, 8):
+        _, iT, wT = dev_forward(torch, k3x, layer, x[:T], bf16=bf16)
+        assert np.array_equal(iT, i1[:T]), T
+        assert np.array_equal(wT.view(np.uint32), w1[:T].view(np.uint32)), T
     layer.close()

@@ -32,29 +32,57 @@
 // Activation planes, the GEMMs' B source: x [T][H] (bf16 or fp32, rows ldx elements
 // apart) -> xg [2][H/8][T][8] bf16, plane 0 the hi parts, plane 1 the lo parts, each
 // k-group of 8 elements token-major, so that one k-group of consecutive rows is
-// contiguous.  Block 0 also clears the expert histogram (when given).
+// contiguous.  For bf16 rows the lo parts are zero and no GEMM reads plane 1 (they take
+// one column per token, HL = 1): it is not written.  A workgroup transposes a tile of
+// SP_T tokens by SP_G k-groups through LDS, so that both its reads (along the rows) and
+// its writes (along the tokens of a k-group) are contiguous.  Block 0 also clears the
+// expert histogram (when given).
+#define SP_T 32
+#define SP_G 32
+
+static inline unsigned pf_split_grid(int T, int H)
+{
+    return (unsigned)(((T + SP_T - 1) / SP_T) * (((H >> 3) + SP_G - 1) / SP_G));
+}
+
 __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int T, int H,
                                                   int ldx, uint16_t *xg, int *counts, int E)
 {
+    __shared__ u32x4 sh[2][SP_G][SP_T + 1];
     if (blockIdx.x == 0 && counts)
         for (int e = threadIdx.x; e < E; e += PF_NT) counts[e] = 0;
-    const size_t i = (size_t)blockIdx.x * PF_NT + threadIdx.x;     // (t, group) pairs
-    const int G8 = H >> 3;
-    if (i >= (size_t)T * G8) return;
-    const int t = (int)(i / G8), gi = (int)(i % G8);
-    float v[8];
-    load_x8(x, x_bf16, (size_t)t * ldx + (size_t)gi * 8, v);
-    uint32_t hi[8], lo[8];
+    const int G8 = H >> 3, ntg = (G8 + SP_G - 1) / SP_G;
+    const int t0 = (blockIdx.x / ntg) * SP_T, g0 = (blockIdx.x % ntg) * SP_G;
 #pragma unroll
-    for (int j = 0; j < 8; j++) split_bf16(v[j], hi[j], lo[j]);
-    u32x4 h, l;
+    for (int j = 0; j < SP_T * SP_G / PF_NT; j++) {
+        const int i = j * PF_NT + threadIdx.x, r = i / SP_G, g = i % SP_G;
+        const int t = t0 + r, gi = g0 + g;
+        u32x4 h = {0u, 0u, 0u, 0u}, l = {0u, 0u, 0u, 0u};
+        if (t < T && gi < G8) {
+            float v[8];
+            load_x8(x, x_bf16, (size_t)t * ldx + (size_t)gi * 8, v);
+            uint32_t hi[8], lo[8];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        h[j] = hi[2 * j] | (hi[2 * j + 1] << 16);
-        l[j] = lo[2 * j] | (lo[2 * j + 1] << 16);
+            for (int k = 0; k < 8; k++) split_bf16(v[k], hi[k], lo[k]);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                h[k] = hi[2 * k] | (hi[2 * k + 1] << 16);
+                l[k] = lo[2 * k] | (lo[2 * k + 1] << 16);
+            }
+        }
+        sh[0][g][r] = h;
+        sh[1][g][r] = l;
     }
-    *(u32x4 *)(xg + ((size_t)gi * T + t) * 8) = h;
-    *(u32x4 *)(xg + ((size_t)(G8 + gi) * T + t) * 8) = l;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < SP_T * SP_G / PF_NT; j++) {
+        const int i = j * PF_NT + threadIdx.x, g = i / SP_T, r = i % SP_T;
+        const int t = t0 + r, gi = g0 + g;
+        if (t < T && gi < G8) {
+            *(u32x4 *)(xg + ((size_t)gi * T + t) * 8) = sh[0][g][r];
+            if (!x_bf16) *(u32x4 *)(xg + ((size_t)(G8 + gi) * T + t) * 8) = sh[1][g][r];
+        }
+    }
 }
 
 // ------------------------------------------------------------------ router
@@ -1270,7 +1298,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     const int HLr = L->lat ? 2 : HLg;                    // of the routed gate/up input
     int rc;
 
-    hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (H / 8), PF_NT)), dim3(PF_NT), 0, s,
+    hipLaunchKernelGGL(pf_split, dim3(pf_split_grid(T, H)), dim3(PF_NT), 0, s,
                        x, x_bf16, T, H, H, B->xhl, B->counts, E);
     if ((rc = launch_ok())) return rc;
 
@@ -1367,7 +1395,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         launch_dense<1, DENSE_RW, DENSE_CW, false>(zg, HLg, s);
         if ((rc = launch_ok())) PF_RET(rc);
         if (!mx) {
-            hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (X / 8), PF_NT)), dim3(PF_NT), 0, s,
+            hipLaunchKernelGGL(pf_split, dim3(pf_split_grid(T, X)), dim3(PF_NT), 0, s,
                                B->zf, 0, T, X, X, B->zhl, (int *)NULL, 0);
             if ((rc = launch_ok())) PF_RET(rc);
         }
@@ -1568,7 +1596,7 @@ extern "C" int k3x_dev_trunk_gemm(const uint16_t *W, int in, int out, float *y, 
 {
     hipStream_t s = (hipStream_t)stream;
     const int x_bf16 = (x_dtype == K3X_BF16), HL = x_bf16 ? 1 : 2;
-    hipLaunchKernelGGL(pf_split, dim3(cdiv((size_t)T * (in / 8), PF_NT)), dim3(PF_NT), 0, s,
+    hipLaunchKernelGGL(pf_split, dim3(pf_split_grid(T, in)), dim3(PF_NT), 0, s,
                        x, x_bf16, T, in, ldx, planes, (int *)NULL, 0);
     int rc = launch_ok();
     if (rc) return rc;

@@ -113,7 +113,7 @@ typedef struct k3x_prefill_buf {
     float    *y;            /* [T*K + T][H] expert and shared output rows            */
     /* latent form (X = latent width) */
     float    *zf;           /* [T][X] z = down . x, then the routed aggregates        */
-    uint16_t *zhl;          /* [2][X/8][T][8] hi/lo planes of z, then of the normalised
+    uint16_t *zhl;          /* [2][X/8][T][8] hi/lo planes of the normalised
                                aggregates                                             */
 } k3x_prefill_buf;
 

@@ -7,6 +7,7 @@
 //   pf_topk     each token's top-k by one wave (:1700-1716) and the per-expert histogram
 //   pf_scan     per-expert offsets (prefix sum) and the GEMM tile lists
 //   pf_scatter  each (token, slot) to its row in its expert's segment
+//               (pf_split again, with the rows in that order: the routed input's planes)
 //   pf_gemm32   grouped GEMMs: gate/up of every expert segment with SwiGLU and the
 //               routing weight (k3_matmul_mxfp4 :3323-3776, k3_situ_glu :148-161), then
 //               down (pf_gemm_mx in the MXFP8 mode)
@@ -32,7 +33,9 @@
 // Activation planes, the GEMMs' B source: x [T][H] (bf16 or fp32, rows ldx elements
 // apart) -> xg [2][H/8][T][8] bf16, plane 0 the hi parts, plane 1 the lo parts, each
 // k-group of 8 elements token-major, so that one k-group of consecutive rows is
-// contiguous.  For bf16 rows the lo parts are zero and no GEMM reads plane 1 (they take
+// contiguous.  With a row map, output row t is x's row rowmap[t] (the routed experts'
+// input in permuted order, from the rows themselves rather than from their planes,
+// whose 16-byte pieces of one row lie T*16 bytes apart).  For bf16 rows the lo parts are zero and no GEMM reads plane 1 (they take
 // one column per token, HL = 1): it is not written.  A workgroup transposes a tile of
 // SP_T tokens by SP_G k-groups through LDS, so that both its reads (along the rows) and
 // its writes (along the tokens of a k-group) are contiguous.  Block 0 also clears the
@@ -46,7 +49,8 @@ static inline unsigned pf_split_grid(int T, int H)
 }
 
 __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int T, int H,
-                                                  int ldx, uint16_t *xg, int *counts, int E)
+                                                  int ldx, uint16_t *xg, int *counts, int E,
+                                                  const int *rowmap)
 {
     __shared__ u32x4 sh[2][SP_G][SP_T + 1];
     if (blockIdx.x == 0 && counts)
@@ -58,9 +62,12 @@ __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int
         const int i = j * PF_NT + threadIdx.x, r = i / SP_G, g = i % SP_G;
         const int t = t0 + r, gi = g0 + g;
         u32x4 h = {0u, 0u, 0u, 0u}, l = {0u, 0u, 0u, 0u};
-        if (t < T && gi < G8) {
+        const size_t src = (size_t)(t < T && rowmap ? rowmap[t] : t) * ldx + (size_t)gi * 8;
+        if (t < T && gi < G8 && x_bf16) {
+            h = *(const u32x4 *)((const uint16_t *)x + src);        // bf16: hi = x, lo = 0
+        } else if (t < T && gi < G8) {
             float v[8];
-            load_x8(x, x_bf16, (size_t)t * ldx + (size_t)gi * 8, v);
+            load_x8(x, 0, src, v);
             uint32_t hi[8], lo[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) split_bf16(v[k], hi[k], lo[k]);
@@ -287,19 +294,6 @@ __global__ void __launch_bounds__(PF_NT) pf_scatter(const int *idx, const float 
     perm_tok[p] = i / K;
     perm_w[p] = wt[i];
     pos_of[i] = p;
-}
-
-// ------------------------------------------------------------------ permute
-// The gate/up B source in permuted order: xp [HL][H/8][T*K][8] = xg rows perm_tok[p], so
-// that one k-group of an expert's segment is contiguous.
-__global__ void __launch_bounds__(PF_NT) pf_permute(const uint16_t *xg, int T, int G8, int HL,
-                                                    const int *perm_tok, int TK, uint16_t *xp)
-{
-    const size_t i = (size_t)blockIdx.x * PF_NT + threadIdx.x;    // ((hl*G8 + g)*TK + p)
-    if (i >= (size_t)HL * G8 * TK) return;
-    const int p = (int)(i % TK);
-    const size_t hg = i / TK;
-    *(u32x4 *)(xp + i * 8) = *(const u32x4 *)(xg + (hg * T + perm_tok[p]) * 8);
 }
 
 // ------------------------------------------------------------------ tile tables
@@ -1299,7 +1293,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     int rc;
 
     hipLaunchKernelGGL(pf_split, dim3(pf_split_grid(T, H)), dim3(PF_NT), 0, s,
-                       x, x_bf16, T, H, H, B->xhl, B->counts, E);
+                       x, x_bf16, T, H, H, B->xhl, B->counts, E, (const int *)NULL);
     if ((rc = launch_ok())) return rc;
 
     // The shared expert (bf16 weights, every token) needs only the split activations: its
@@ -1384,7 +1378,6 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     hipLaunchKernelGGL(pf_tiles, dim3(E), dim3(PF_NT), 0, s, B->counts, B->offsets, sa,
                        (int4 *)B->desc_gu, (int4 *)B->desc_dn);
     if ((rc = launch_ok())) PF_RET(rc);
-    const uint16_t *rsrc = B->xhl;        // the routed experts' input planes
     if (L->lat) {
         // z = down . x for every token (k3_mmw_batch, k3_ops.c:1871), then its hi/lo planes
         PfGemmArgs zg;
@@ -1394,12 +1387,6 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         zg.y = B->zf; zg.out_base = 0;
         launch_dense<1, DENSE_RW, DENSE_CW, false>(zg, HLg, s);
         if ((rc = launch_ok())) PF_RET(rc);
-        if (!mx) {
-            hipLaunchKernelGGL(pf_split, dim3(pf_split_grid(T, X)), dim3(PF_NT), 0, s,
-                               B->zf, 0, T, X, X, B->zhl, (int *)NULL, 0);
-            if ((rc = launch_ok())) PF_RET(rc);
-        }
-        rsrc = B->zhl;
     }
     // MXFP8 mode: the routed input quantised in permuted order, codes then scales in xp;
     // the gate/up output's codes then scales in act
@@ -1410,8 +1397,11 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         hipLaunchKernelGGL(pf_mx8_rows, dim3(cdiv((size_t)TK * (X / 32), PF_NT)), dim3(PF_NT), 0, s,
                            src, L->lat ? 0 : x_bf16, X, X, B->perm_tok, TK, xq8, xs8);
     } else {
-        hipLaunchKernelGGL(pf_permute, dim3(cdiv((size_t)HLr * (X / 8) * TK, PF_NT)), dim3(PF_NT), 0, s,
-                           rsrc, T, X / 8, HLr, B->perm_tok, TK, B->xp);
+        // the routed input's planes in permuted order, from x's rows (z's in the latent
+        // form), so that one k-group of an expert's segment is contiguous
+        const void *src = L->lat ? (const void *)B->zf : x;
+        hipLaunchKernelGGL(pf_split, dim3(pf_split_grid(TK, X)), dim3(PF_NT), 0, s,
+                           src, L->lat ? 0 : x_bf16, TK, X, X, B->xp, (int *)NULL, 0, B->perm_tok);
     }
     if ((rc = launch_ok())) PF_RET(rc);
 
@@ -1597,7 +1587,7 @@ extern "C" int k3x_dev_trunk_gemm(const uint16_t *W, int in, int out, float *y, 
     hipStream_t s = (hipStream_t)stream;
     const int x_bf16 = (x_dtype == K3X_BF16), HL = x_bf16 ? 1 : 2;
     hipLaunchKernelGGL(pf_split, dim3(pf_split_grid(T, in)), dim3(PF_NT), 0, s,
-                       x, x_bf16, T, in, ldx, planes, (int *)NULL, 0);
+                       x, x_bf16, T, in, ldx, planes, (int *)NULL, 0, (const int *)NULL);
     int rc = launch_ok();
     if (rc) return rc;
     PfGemmArgs g;

@@ -865,39 +865,63 @@ __device__ __forceinline__ uint32_t mx8_code(float v, float inv)
 
 __device__ __forceinline__ float mx8_inv(int sb) { return __uint_as_float((uint32_t)(254 - sb) << 23); }
 
-// The routed experts' MXFP8 input in permuted order: one thread per (row p, 32-k block):
-// src row perm_tok[p] (bf16 or fp32, rows ld elements apart), X elements -> codes
-// [X/16][TK][16], scales [X/128][TK] dwords.
+// The routed experts' MXFP8 input in permuted order: src row perm_tok[p] (bf16 or fp32,
+// rows ld elements apart), X elements -> codes [X/16][TK][16], scales [X/128][TK] dwords.
+// A workgroup takes MX_R rows by one 128-k quad, one thread per (row, 32-k block); the
+// codes go through LDS so that the stores run along the rows of a k16-group (1 KB
+// contiguous) and each row's four scale bytes are one dword.
+#define MX_R 64
+
+static inline unsigned pf_mx8_grid(int TK, int X) { return (unsigned)(((TK + MX_R - 1) / MX_R) * (X / 128)); }
+
 __global__ void __launch_bounds__(PF_NT) pf_mx8_rows(const void *src, int bf16, int ld, int X,
                                                      const int *perm_tok, int TK,
                                                      uint8_t *codes, uint8_t *scales)
 {
-    const size_t i = (size_t)blockIdx.x * PF_NT + threadIdx.x;      // blk * TK + p
-    if (i >= (size_t)TK * (X / 32)) return;
-    const int p = (int)(i % TK), blk = (int)(i / TK);
-    const size_t base = (size_t)perm_tok[p] * ld + (size_t)blk * 32;
-    float v[4][8];
-    float m = 0.0f;
+    static_assert(MX_R * 4 == PF_NT, "a thread per (row, block)");
+    __shared__ u32x4 sc[8][MX_R + 1];          // [k16-group of the quad][row]
+    __shared__ uint32_t ss[MX_R];
+    const int nq = X / 128;
+    const int q = blockIdx.x % nq, p0 = (blockIdx.x / nq) * MX_R;
+    const int r = threadIdx.x >> 2, b = threadIdx.x & 3, p = p0 + r;
+    uint32_t w[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    int sb = 0;
+    if (p < TK) {
+        const size_t base = (size_t)perm_tok[p] * ld + (size_t)q * 128 + (size_t)b * 32;
+        float v[4][8];
+        float m = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        load_x8(src, bf16, base + 8 * j, v[j]);
+        for (int j = 0; j < 4; j++) {
+            load_x8(src, bf16, base + 8 * j, v[j]);
 #pragma unroll
-        for (int e = 0; e < 8; e++)
-            if (isfinite(v[j][e])) m = fmaxf(m, fabsf(v[j][e]));
+            for (int e = 0; e < 8; e++)
+                if (isfinite(v[j][e])) m = fmaxf(m, fabsf(v[j][e]));
+        }
+        sb = mx8_scale(m);
+        const float inv = mx8_inv(sb);
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            uint32_t c = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) c |= mx8_code(v[d / 2][(d % 2) * 4 + e], inv) << (8 * e);
+            w[d] = c;
+        }
     }
-    const int sb = mx8_scale(m);
-    const float inv = mx8_inv(sb);
-    uint32_t w[8];
+    sc[2 * b][r] = (u32x4){w[0], w[1], w[2], w[3]};
+    sc[2 * b + 1][r] = (u32x4){w[4], w[5], w[6], w[7]};
+    // the row's four scale bytes, block b at byte b, gathered by its lane group of four
+    uint32_t sw = (uint32_t)sb << (8 * b);
+    sw |= __shfl_xor(sw, 1);
+    sw |= __shfl_xor(sw, 2);
+    if (b == 0) ss[r] = sw;
+    __syncthreads();
 #pragma unroll
-    for (int d = 0; d < 8; d++) {
-        uint32_t r = 0;
-#pragma unroll
-        for (int e = 0; e < 4; e++) r |= mx8_code(v[d / 2][(d % 2) * 4 + e], inv) << (8 * e);
-        w[d] = r;
+    for (int j = 0; j < 2; j++) {
+        const int i = j * PF_NT + threadIdx.x, g = i / MX_R, rr = i % MX_R, pp = p0 + rr;
+        if (pp < TK) *(u32x4 *)(codes + ((size_t)(8 * q + g) * TK + pp) * 16) = sc[g][rr];
     }
-    *(u32x4 *)(codes + ((size_t)(2 * blk) * TK + p) * 16) = (u32x4){w[0], w[1], w[2], w[3]};
-    *(u32x4 *)(codes + ((size_t)(2 * blk + 1) * TK + p) * 16) = (u32x4){w[4], w[5], w[6], w[7]};
-    scales[((size_t)(blk >> 2) * TK + p) * 4 + (blk & 3)] = (uint8_t)sb;
+    if (threadIdx.x < MX_R && p0 + (int)threadIdx.x < TK)
+        *(uint32_t *)(scales + ((size_t)q * TK + p0 + threadIdx.x) * 4) = ss[threadIdx.x];
 }
 
 // Grouped GEMM on v_mfma_scale_f32_32x32x64_f8f6f4 (A fp4, B fp8 E4M3).  Operand layout
@@ -1394,7 +1418,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     uint8_t *aq8 = (uint8_t *)B->act, *as8 = aq8 + (((size_t)TK * I + 255) & ~(size_t)255);
     if (mx) {
         const void *src = L->lat ? (const void *)B->zf : x;
-        hipLaunchKernelGGL(pf_mx8_rows, dim3(cdiv((size_t)TK * (X / 32), PF_NT)), dim3(PF_NT), 0, s,
+        hipLaunchKernelGGL(pf_mx8_rows, dim3(pf_mx8_grid(TK, X)), dim3(PF_NT), 0, s,
                            src, L->lat ? 0 : x_bf16, X, X, B->perm_tok, TK, xq8, xs8);
     } else {
         // the routed input's planes in permuted order, from x's rows (z's in the latent

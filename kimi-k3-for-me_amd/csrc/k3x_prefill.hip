@@ -1251,23 +1251,25 @@ static void launch_topk(const PfTopkArgs &a, hipStream_t s)
 #define NW_DS     4
 #define NW_B      8
 #define GU_RT32   1
+#define GU_RT32_S 2
 #define GU_CT32_S 1
 #define GU_CT32_B 3
 #define DN_RT32   2
+#define DN_RT32_S 2
 #define DN_CT32_S 2
 #define DN_CT32_B 3
 
-template <bool EXACT, int HL, int CT32, int NW>
+template <bool EXACT, int HL, int CT32, int NW, int RT32 = GU_RT32>
 static void launch_gu(const PfGemmArgs &a, unsigned grid, hipStream_t s)
 {
-    hipLaunchKernelGGL((pf_gemm32<EXACT, 2, GU_RT32, CT32, HL, true, NW>), dim3(grid),
+    hipLaunchKernelGGL((pf_gemm32<EXACT, 2, RT32, CT32, HL, true, NW>), dim3(grid),
                        dim3(NW * WAVE), 0, s, a);
 }
 
-template <bool EXACT, int CT32, int NW>
+template <bool EXACT, int CT32, int NW, int RT32 = DN_RT32>
 static void launch_dn(const PfGemmArgs &a, unsigned grid, hipStream_t s)
 {
-    hipLaunchKernelGGL((pf_gemm32<EXACT, 1, DN_RT32, CT32, 2, false, NW>), dim3(grid),
+    hipLaunchKernelGGL((pf_gemm32<EXACT, 1, RT32, CT32, 2, false, NW>), dim3(grid),
                        dim3(NW * WAVE), 0, s, a);
 }
 
@@ -1388,11 +1390,11 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     const bool mx = L->pf_mode == K3X_PREFILL_MXFP8;
     sa.tpb_s[0] = mx ? MX_CT_S * 32 : GU_CT32_S * 32 / HLr;
     sa.tpb_b[0] = mx ? MX_CT_B * 32 : GU_CT32_B * 32 / HLr;
-    sa.nrb_s[0] = cdiv(I, (mx ? MX_NW : NW_GS) * GU_RT32 * 32);
+    sa.nrb_s[0] = cdiv(I, mx ? MX_NW * GU_RT32 * 32 : NW_GS * GU_RT32_S * 32);
     sa.nrb_b[0] = cdiv(I, (mx ? MX_NW : NW_B) * GU_RT32 * 32);
     sa.tpb_s[1] = mx ? MX_CT_S * 32 : DN_CT32_S * 32 / 2;
     sa.tpb_b[1] = mx ? MX_CT_B * 32 : DN_CT32_B * 32 / 2;
-    sa.nrb_s[1] = cdiv(X, (mx ? MX_NW : NW_DS) * DN_RT32 * 32);
+    sa.nrb_s[1] = cdiv(X, mx ? MX_NW * DN_RT32 * 32 : NW_DS * DN_RT32_S * 32);
     sa.nrb_b[1] = cdiv(X, (mx ? MX_NW : NW_B) * DN_RT32 * 32);
     hipLaunchKernelGGL(pf_scan, dim3(1), dim3(1024), 0, s, sa);
     if ((rc = launch_ok())) PF_RET(rc);
@@ -1470,11 +1472,11 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     if (mx) {
         hipLaunchKernelGGL((pf_gemm_mx<2, GU_RT32, MX_CT_S, true, MX_NW>), dim3(grid_s[0]), dim3(MX_NW * WAVE), 0, s, g);
     } else if (ex_gu) {
-        if (HLr == 1) launch_gu<true, 1, GU_CT32_S, NW_GS>(g, grid_s[0], s);
-        else          launch_gu<true, 2, GU_CT32_S, NW_GS>(g, grid_s[0], s);
+        if (HLr == 1) launch_gu<true, 1, GU_CT32_S, NW_GS, GU_RT32_S>(g, grid_s[0], s);
+        else          launch_gu<true, 2, GU_CT32_S, NW_GS, GU_RT32_S>(g, grid_s[0], s);
     } else {
-        if (HLr == 1) launch_gu<false, 1, GU_CT32_S, NW_GS>(g, grid_s[0], s);
-        else          launch_gu<false, 2, GU_CT32_S, NW_GS>(g, grid_s[0], s);
+        if (HLr == 1) launch_gu<false, 1, GU_CT32_S, NW_GS, GU_RT32_S>(g, grid_s[0], s);
+        else          launch_gu<false, 2, GU_CT32_S, NW_GS, GU_RT32_S>(g, grid_s[0], s);
     }
     if ((rc = launch_ok())) PF_RET(rc);
 
@@ -1492,8 +1494,8 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     if (mx) {
         hipLaunchKernelGGL((pf_gemm_mx<1, DN_RT32, MX_CT_B, false, MX_NW>), dim3(grid_b[1]), dim3(MX_NW * WAVE), 0, s, db);
         hipLaunchKernelGGL((pf_gemm_mx<1, DN_RT32, MX_CT_S, false, MX_NW>), dim3(grid_s[1]), dim3(MX_NW * WAVE), 0, s, d);
-    } else if (L->special & 4) { launch_dn<true, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<true, DN_CT32_S, NW_DS>(d, grid_s[1], s); }
-    else                { launch_dn<false, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<false, DN_CT32_S, NW_DS>(d, grid_s[1], s); }
+    } else if (L->special & 4) { launch_dn<true, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<true, DN_CT32_S, NW_DS, DN_RT32_S>(d, grid_s[1], s); }
+    else                { launch_dn<false, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<false, DN_CT32_S, NW_DS, DN_RT32_S>(d, grid_s[1], s); }
     if ((rc = launch_ok())) PF_RET(rc);
 
     int sh_row0 = -1;

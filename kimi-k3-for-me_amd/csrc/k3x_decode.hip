@@ -968,6 +968,11 @@ __device__ void k2_shared(const K2Args &a, float *lds, int rt)
 // it) and the bf16 hi/lo split into the expert's activation slot.  Several tiles per
 // workgroup when a tile has few super-quads (a narrow latent width), so that each wave
 // streams a run of items and the per-workgroup staging and waits are amortised.
+#ifndef K2SB_R
+#define K2SB_R 2                       // stages of the shared-B path (super-quads)
+#endif
+#define K2SB_BL 4                      // its B loads per thread and super-quad (16 KB)
+#define K2SB_STAGE (1024u * 2 * K3X_DECODE_MAX_T)   // LDS bytes of a stage's B
 template <bool EXACT, bool LDSB, int NE>
 __device__ void k2_gateup_body(const K2Args &a, float *lds, int *s_go_p);
 
@@ -1066,61 +1071,58 @@ __device__ void k2_gateup_body(const K2Args &a, float *lds, int *s_go_p)
     f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
     if (!LDSB && a.sb) {
         // several tokens: wave (tw, sw) streams matrix sw (gate, up) of tile tw over every
-        // super-quad; each super-quad's B fragments are read once into LDS for the four
-        // waves (double buffered) instead of once per wave
+        // super-quad; each super-quad's B fragments come straight into an LDS stage, once
+        // for the four waves, with its weights.  K2SB_R stages: a wave has K2SB_R - 1
+        // super-quads' loads in flight while it multiplies one.
         const rsrc_t rw = sw ? ru : rg;
-        const uint32_t sqb = 1024u * (uint32_t)NC;
+        const uint32_t sqb = 1024u * (uint32_t)NC;           // B bytes of a super-quad
         const rsrc_t rbB = make_rsrc(a.rB, bbytes);
-        SQ w[2];
-        auto ldw = [&](int i, int S) AI {
-            sq_load(w[i], rw, S < nS ? (uint32_t)S * SQ_BYTES : K3X_OOB, lane);
-        };
-        u32x4 breg[4];
-        auto bld = [&](int S) AI {
+        constexpr int LPI = 5 + K2SB_BL;                      // vector loads per super-quad
+        SQ w[K2SB_R];
+        auto ld = [&](int i, int S) AI {
+            const bool on = S < nS;
+            sq_load(w[i], rw, on ? (uint32_t)S * SQ_BYTES : K3X_OOB, lane);
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
+            for (int c = 0; c < K2SB_BL; c++) {
                 const uint32_t o = threadIdx.x * 16u + (uint32_t)c * NT * 16u;
-                breg[c] = bload16(rbB, (S < nS && o < sqb) ? (uint32_t)S * sqb + o : K3X_OOB);
-            }
-        };
-        auto bst = [&](int buf) AI {
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const uint32_t o = threadIdx.x * 16u + (uint32_t)c * NT * 16u;
-                if (o < sqb) *(u32x4 *)(dyn_lds + (uint32_t)buf * sqb + o) = breg[c];
+                const uint32_t go = (on && o < sqb) ? (uint32_t)S * sqb + o : K3X_OOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rbB, (lds_void *)(dyn_lds + (uint32_t)i * K2SB_STAGE + (uint32_t)c * NT * 16u +
+                                      (uint32_t)wave * WAVE * 16u), 16, go, 0, 0, 0);
             }
         };
         BFrag<true> bl;
         bl.init(nullptr, 0u, NC, lane);
         f32x4 d = {0.f, 0.f, 0.f, 0.f};
-        auto mm = [&](const SQ &wq, int buf) AI {
+        auto mm = [&](const SQ &wq, int i) AI {
 #pragma unroll
             for (int j = 0; j < 4; j++)
 #pragma unroll
                 for (int t = 0; t < 4; t++)
-                    d = mfma(sq_a<EXACT>(wq, j, t), as_bf16x8(bl.get((uint32_t)buf * sqb, j, t)), d);
+                    d = mfma(sq_a<EXACT>(wq, j, t), as_bf16x8(bl.get((uint32_t)i * K2SB_STAGE, j, t)), d);
         };
-        bld(0);
-        ring_prime<2>(ldw);
-        bst(0);
-        __syncthreads();
-        for (int S = 0; S < nS; S += 2) {
-            bld(S + 1);
-            mm(w[0], 0);
+#pragma unroll
+        for (int i = 0; i < K2SB_R - 1; i++) {
             SCHED_FENCE();
-            ldw(0, S + 2);
-            SCHED_FENCE();
-            bst(1);
-            __syncthreads();
-            if (S + 1 >= nS) break;
-            bld(S + 2);
-            mm(w[1], 1);
-            SCHED_FENCE();
-            ldw(1, S + 3);
-            SCHED_FENCE();
-            bst(0);
-            __syncthreads();
+            ld(i, i);
         }
+        SCHED_FENCE();
+        // super-quad S + i: wait for its loads (those of the K2SB_R - 2 after it remain),
+        // meet the other waves (so that stage i - 1 is no longer read), refill that stage
+        // with super-quad S + i + K2SB_R - 1, multiply
+        for (int S = 0; S < nS; S += K2SB_R) {
+#pragma unroll
+            for (int i = 0; i < K2SB_R; i++) {
+                if (S + i < nS) {
+                    meet<(K2SB_R - 2) * LPI>();
+                    SCHED_FENCE();
+                    ld((i + K2SB_R - 1) % K2SB_R, S + i + K2SB_R - 1);
+                    SCHED_FENCE();
+                    mm(w[i], i);
+                }
+            }
+        }
+        WAIT_VMCNT_LGKM0(0);
         if (sw) du = d;
         else    dg = d;
     } else {
@@ -1187,6 +1189,7 @@ struct K3Args {
     size_t         pstride;        // floats between parts' outputs (0: one part)
     const int     *slot;           // expert -> arena slot (expert cache), or NULL: identity
     unsigned long long *trace;     // diagnostics, or NULL
+    float         *pacc;           // k3_down_wide: part sums, [part][DECODE_MAX_T][H]
 };
 
 // A bf16 quad of the shared down matrix with its B fragments (read from the shared
@@ -1303,6 +1306,12 @@ __global__ void __launch_bounds__(NT3) k3_down(K3Args a)
 
 // Several tokens (K2 form): two 16-row tiles per workgroup, so that each B fragment read
 // from memory (the activation sets no longer fit the LDS) serves both tiles' products.
+#ifndef K3D2_R
+#define K3D2_R 2
+#endif
+#ifndef K3D2_BPF
+#define K3D2_BPF 1
+#endif
 template <bool EXACT>
 __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
 {
@@ -1320,7 +1329,13 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
     const int cnt = strided_count(wave, NW, nu * nSI);
     const int nQS = (a.sh_down && blockIdx.y == 0) ? a.SI >> 7 : 0;
     const uint16_t *actB = a.actB + (size_t)u0 * (slot / 2);
-    SQ ring[2][2];
+    const int n = lane & 15, kq = lane >> 4;
+    const uint32_t boff = (uint32_t)((kq * NC + (n < NC ? n : 0)) * 16);
+    // an item's B fragments travel with its weights: a read of them at use would leave
+    // its L2 latency in front of every item's products
+    const rsrc_t ra = make_rsrc(actB, (uint32_t)nu * slot);
+    SQ ring[K3D2_R][2];
+    u32x4 bb[K3D2_BPF ? K3D2_R : 1][16];
     auto ld = [&](int i, int k) AI {
         const int it = wave + NW * k;
         const bool on = k < cnt;
@@ -1331,14 +1346,41 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
                                        (size_t)rt0 * tb, on ? 2 * tb : 0u);
         sq_load(ring[i][0], r, (uint32_t)S * SQ_BYTES, lane);
         sq_load(ring[i][1], r, tb + (uint32_t)S * SQ_BYTES, lane);
+#if K3D2_BPF
+        const uint32_t bo = (uint32_t)u * slot + (uint32_t)(4 * S) * 256u * NC + boff;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                bb[i][4 * j + t] = bload16(ra, on ? bo + (uint32_t)(j * 256 * NC + t * 64 * NC) : K3X_OOB);
+#endif
     };
-    ring_prime<2>(ld);
+    ring_prime<K3D2_R>(ld);
+    f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+    ring_loop<K3D2_R>(cnt, ld, [&](int i, int k) AI {
+#if !K3D2_BPF
+        const int it = wave + NW * k;
+        const uint32_t bo = (uint32_t)(it / nSI) * slot + (uint32_t)(4 * (it % nSI)) * 256u * NC + boff;
+#endif
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+#if K3D2_BPF
+                const bf16x8 bv = as_bf16x8(bb[i][4 * j + t]);
+#else
+                const bf16x8 bv = as_bf16x8(bload16(ra, bo + (uint32_t)(j * 256 * NC + t * 64 * NC)));
+#endif
+                d0 = mfma(sq_a<EXACT>(ring[i][0], j, t), bv, d0);
+                d1 = mfma(sq_a<EXACT>(ring[i][1], j, t), bv, d1);
+            }
+    });
+    // then the shared expert's quads (two per wave at SI = 2048), their ring primed once
+    // the routed one has drained, so that the two never hold registers together
     const int cs = strided_count(wave, NW, nQS);
     const uint32_t sbytes = (uint32_t)nQS * 4096u;
     const rsrc_t rw = make_rsrc(a.sh_down + (size_t)rt0 * 16 * a.SI, 2 * sbytes);
     const rsrc_t rb = make_rsrc(a.shB, (uint32_t)nQS * 256u * NC);
-    const int n = lane & 15, kq = lane >> 4;
-    const uint32_t boff = (uint32_t)((kq * NC + (n < NC ? n : 0)) * 16);
     QB w2[2][2];
     u32x4 b2[2][4];
     auto ld2 = [&](int i, int k) AI {
@@ -1351,22 +1393,6 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
             b2[i][t] = bload16(rb, on ? boff + (uint32_t)(q * 256 * NC + t * 64 * NC) : K3X_OOB);
     };
     ring_prime<2>(ld2);
-    BFrag<false> bf;
-    bf.init(actB, (uint32_t)nu * slot, NC, lane);
-    f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-    ring_loop<2>(cnt, ld, [&](int i, int k) AI {
-        const int it = wave + NW * k;
-        const uint32_t sb = (uint32_t)(it / nSI) * slot;
-        const int S = it % nSI;
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const bf16x8 bv = as_bf16x8(bf.get(sb, 4 * S + j, t));
-                d0 = mfma(sq_a<EXACT>(ring[i][0], j, t), bv, d0);
-                d1 = mfma(sq_a<EXACT>(ring[i][1], j, t), bv, d1);
-            }
-    });
     ring_loop<2>(cs, ld2, [&](int i, int k) AI {
         qb_mfma(d0, w2[i][0], b2[i]);
         qb_mfma(d1, w2[i][1], b2[i]);
@@ -1382,6 +1408,178 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
                 out[o] = a.resid ? a.resid[o] + v[4 * tt + i] : v[4 * tt + i];
             }
     });
+}
+
+// Several tokens, K2 form, H a multiple of 256: the down products of 256 output rows a
+// workgroup (wave w: row tiles 2w, 2w + 1 of the group).  Workgroups blockIdx.y <
+// gridDim.y - 1 each take one part of the (unique expert, super-quad) items, dealt in
+// runs of equal length; the last row of workgroups takes the shared expert's bf16 quads.
+// All eight waves take the same item at once, so that its B fragments (16 KB at eight
+// tokens) come straight into an LDS stage once for the workgroup, beside the waves'
+// weights, through a ring of K3W_R stages: a wave has K3W_R - 1 items of weights in
+// flight while it multiplies one.  Every workgroup writes its part sums, which k3_reduce
+// adds up in part order (the shared expert's last).
+#define K3W_R 4
+#ifndef K3W_ON
+#define K3W_ON 1
+#endif
+#define K3W_STAGE (1024u * 2 * K3X_DECODE_MAX_T)   // LDS bytes of a stage's B
+#define K3W_LPI 12                                 // vector loads per item and wave
+
+// The ring over n items: ld(i, k) issues item k's loads into stage i (K3W_LPI of them,
+// any k; k >= n loads nothing), use(i) multiplies stage i.
+template <class LD, class USE>
+__device__ __forceinline__ void k3w_ring(int n, LD ld, USE use)
+{
+#pragma unroll
+    for (int i = 0; i < K3W_R - 1; i++) {
+        SCHED_FENCE();
+        ld(i, i);
+    }
+    SCHED_FENCE();
+    // item k + i: wait for its loads (those of the K3W_R - 2 items after it remain), meet
+    // the other waves (stage i - 1 is then no longer read), refill that stage with item
+    // k + i + K3W_R - 1, multiply
+    int k = 0;
+    for (; k + K3W_R <= n; k += K3W_R) {
+#pragma unroll
+        for (int i = 0; i < K3W_R; i++) {
+            meet<(K3W_R - 2) * K3W_LPI>();
+            SCHED_FENCE();
+            ld((i + K3W_R - 1) % K3W_R, k + i + K3W_R - 1);
+            SCHED_FENCE();
+            use(i);
+        }
+    }
+    // the last n - k items (fewer than K3W_R), without refills
+#pragma unroll
+    for (int i = 0; i < K3W_R - 1; i++) {
+        if (k + i < n) {
+            WAIT_VMCNT_LGKM0(0);
+            __builtin_amdgcn_s_barrier();
+            use(i);
+        }
+    }
+    WAIT_VMCNT_LGKM0(0);
+}
+
+template <bool EXACT>
+__global__ void __launch_bounds__(NT3) k3_down_wide(K3Args a)
+{
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    const int NC = 2 * a.T;
+    const int rg = blockIdx.x, p = blockIdx.y, P = gridDim.y - 1;
+    const int rt0 = rg * 16 + 2 * wave;
+    const uint32_t stB = (uint32_t)wave * WAVE * 16u;
+    BFrag<true> bl;
+    bl.init(nullptr, 0u, NC, lane);
+    f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+    SQ w[K3W_R][2];
+    if (p < P) {
+        const int nu = __builtin_amdgcn_readfirstlane(a.route->nu);
+        const int nSI = ((a.I >> 7) + 3) >> 2;
+        const uint32_t sqb = 1024u * (uint32_t)NC;      // B bytes of a super-quad
+        const uint32_t slot = (uint32_t)nSI * sqb;      // B bytes of an expert
+        const int nit = nu * nSI;
+        const int ipp = (nit + P - 1) / P;
+        const int i0 = p * ipp < nit ? p * ipp : nit;
+        const int cnt = (i0 + ipp < nit ? i0 + ipp : nit) - i0;
+        const uint32_t tb = (uint32_t)fp4_tile_bytes(a.I);
+        const rsrc_t ra = make_rsrc(a.actB, (uint32_t)nu * slot);
+        // the unique experts' arena slots in LDS, so that the loads of an item need no
+        // load of their own (a global one would be waited for in front of every item's)
+        __shared__ int s_ue[K3X_DECODE_MAX_T * K3X_MAX_TOPK];
+        for (int u = threadIdx.x; u < nu; u += NT3) {
+            const int e = a.route->uniq[u];
+            s_ue[u] = a.slot ? a.slot[e] : e;
+        }
+        __syncthreads();
+        // (expert, super-quad) of the next item: ld is called for k = 0, 1, 2, ...
+        int cu = i0 / nSI, cS = i0 % nSI;
+        k3w_ring(cnt, [&](int i, int k) AI {
+            const bool on = k < cnt;
+            const int e = __builtin_amdgcn_readfirstlane(s_ue[on ? cu : 0]);
+            const rsrc_t r = make_rsrc(a.experts + (size_t)e * a.expert_bytes + a.down_off +
+                                           (size_t)rt0 * tb, on ? 2 * tb : 0u);
+            sq_load(w[i][0], r, (uint32_t)cS * SQ_BYTES, lane);
+            sq_load(w[i][1], r, tb + (uint32_t)cS * SQ_BYTES, lane);
+            const uint32_t gb = (uint32_t)cu * slot + (uint32_t)cS * sqb;
+            const int wrap = cS + 1 == nSI;
+            cu += wrap;
+            cS = wrap ? 0 : cS + 1;
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const uint32_t o = threadIdx.x * 16u + (uint32_t)c * NT3 * 16u;
+                const uint32_t go = (on & (o < sqb)) ? gb + o : K3X_OOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ra, (lds_void *)(dyn_lds + (uint32_t)i * K3W_STAGE + (uint32_t)c * NT3 * 16u + stB),
+                    16, go, 0, 0, 0);
+            }
+        }, [&](int i) AI {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const bf16x8 bv = as_bf16x8(bl.get((uint32_t)i * K3W_STAGE, j, t));
+                    d0 = mfma(sq_a<EXACT>(w[i][0], j, t), bv, d0);
+                    d1 = mfma(sq_a<EXACT>(w[i][1], j, t), bv, d1);
+                }
+        });
+    } else {
+        // the shared expert: quad q's two 16-row runs a wave (four 16-byte loads each, as
+        // an fp4 super-quad's codes, plus two scale-slot loads that read nothing)
+        const int nQS = a.sh_down ? a.SI >> 7 : 0;
+        const uint32_t sbytes = (uint32_t)nQS * 4096u;  // a tile's bytes
+        const uint32_t qbB = 256u * (uint32_t)NC;       // B bytes of a quad
+        const rsrc_t r = make_rsrc(a.sh_down + (size_t)rt0 * 16 * a.SI, 2 * sbytes);
+        const rsrc_t rsb = make_rsrc(a.shB, (uint32_t)nQS * qbB);
+        k3w_ring(nQS, [&](int i, int q) AI {
+            const bool on = q < nQS;
+            const uint32_t b0 = on ? (uint32_t)q * 4096u : K3X_OOB;
+            sq_load(w[i][0], r, b0, lane);
+            sq_load(w[i][1], r, on ? sbytes + b0 : K3X_OOB, lane);
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const uint32_t o = threadIdx.x * 16u + (uint32_t)c * NT3 * 16u;
+                const uint32_t go = (on & (o < qbB)) ? (uint32_t)q * qbB + o : K3X_OOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rsb, (lds_void *)(dyn_lds + (uint32_t)i * K3W_STAGE + (uint32_t)c * NT3 * 16u + stB),
+                    16, go, 0, 0, 0);
+            }
+        }, [&](int i) AI {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const bf16x8 bv = as_bf16x8(bl.get((uint32_t)i * K3W_STAGE, 0, t));
+                d0 = mfma(as_bf16x8(w[i][0].c[t]), bv, d0);
+                d1 = mfma(as_bf16x8(w[i][1].c[t]), bv, d1);
+            }
+        });
+    }
+    const float acc[8] = {d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3]};
+    float *dst = a.pacc + (size_t)p * K3X_DECODE_MAX_T * a.H;
+    per_token<8>(acc, NC, lane, [&](int r0, int tok, const float (&v)[8]) AI {
+        for (int tt = 0; tt < 2; tt++)
+            for (int i = 0; i < 4; i++)
+                dst[(size_t)tok * a.H + (rt0 + tt) * 16 + r0 + i] = v[4 * tt + i];
+    });
+}
+
+// out = resid + the parts' sums of k3_down_wide, added in part order, over [T][H].
+__global__ void __launch_bounds__(256) k3_reduce(const float *pacc, int P, const float *resid,
+                                                  float *out, int n, int H)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const size_t ps = (size_t)K3X_DECODE_MAX_T * H;
+    float v[K3X_WIDE_PMAX];
+#pragma unroll
+    for (int q = 0; q < K3X_WIDE_PMAX; q++)
+        if (q < P) v[q] = pacc[q * ps + i];
+    float s = v[0];
+#pragma unroll
+    for (int q = 1; q < K3X_WIDE_PMAX; q++)
+        if (q < P) s += v[q];
+    out[i] = resid ? resid[i] + s : s;
 }
 
 // ------------------------------------------------------------------ K4 (latent form)
@@ -1713,7 +1911,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     size_t l2 = st2 ? bset : 0;
     if (l2 < sizeof(KSLds)) l2 = sizeof(KSLds);
     a2.sb = (!st2 && a2.rtw == 2) ? 1 : 0;
-    if (a2.sb && l2 < (size_t)2048 * NC) l2 = (size_t)2048 * NC;
+    if (a2.sb && l2 < (size_t)K2SB_R * K2SB_STAGE) l2 = (size_t)K2SB_R * K2SB_STAGE;
     auto k2_launch = [&](bool ex, dim3 g) {
         if (c->n_experts <= 128)      launch_k2<2>(a2, ex, st2, g, l2, s);
         else if (c->n_experts <= 256) launch_k2<4>(a2, ex, st2, g, l2, s);
@@ -1783,7 +1981,24 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
         a3.trace = on ? trb + (size_t)L->tr_cap * 6 : NULL;
         L->tr_n[2] = on ? X / 16 : 0;
     }
-    if (use2) {
+    a3.pacc = L->pacc;
+    // K2 form, several tokens: 256 rows a workgroup over parts of the items, about one
+    // workgroup per CU
+    const bool wide = !L->lat && T >= 2 && X % 256 == 0 && L->pacc && K3W_ON;
+    if (wide) {
+        // routed parts and one shared part: about one workgroup per CU
+        int pw = 256 / (X / 256);
+        if (pw < 2) pw = 2;
+        if (pw > K3X_WIDE_PMAX) pw = K3X_WIDE_PMAX;
+        const dim3 gw(X / 256, pw);
+        const size_t lw = (size_t)K3W_R * K3W_STAGE;
+        if (L->special & 4) hipLaunchKernelGGL(k3_down_wide<true>, gw, dim3(NT3), lw, s, a3);
+        else                hipLaunchKernelGGL(k3_down_wide<false>, gw, dim3(NT3), lw, s, a3);
+        if ((rc = launch_ok())) return rc;
+        const int n = T * X;
+        hipLaunchKernelGGL(k3_reduce, dim3((n + 255) / 256), dim3(256), 0, s,
+                           (const float *)L->pacc, pw, resid, out, n, X);
+    } else if (use2) {
         if (L->special & 4) hipLaunchKernelGGL(k3_down2<true>, dim3(X / 32, parts), dim3(NT3), 0, s, a3);
         else                hipLaunchKernelGGL(k3_down2<false>, dim3(X / 32, parts), dim3(NT3), 0, s, a3);
     } else if (L->special & 4) hipLaunchKernelGGL(k3_down<true>, dim3(X / 16, parts), dim3(NT3), l3, s, a3);

@@ -172,6 +172,25 @@ __device__ __forceinline__ uint32_t wld4(rsrc_t r, uint32_t off)
 
 #define SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (expcnt left at its maximum), gfx9 encoding
+#define WAIT_VMCNT_LGKM0(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4))
+
+// Meet the other waves once this wave's loads of a stage are in (N = vector loads issued
+// after the stage's; exact, since the wait is what makes LDS data written by loads
+// straight to LDS safe to read) and its LDS reads of the previous stage are done.  A bare
+// s_barrier: __syncthreads' release fence would wait for every load in flight; the empty
+// asm keeps the compiler from moving LDS accesses across it.
+template <int N>
+__device__ __forceinline__ void meet()
+{
+    WAIT_VMCNT_LGKM0(N);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // ------------------------------------------------------------------ layout offsets
 __device__ __forceinline__ size_t fp4_tile_bytes(int K)
 {

@@ -48,6 +48,7 @@ extern "C" {
 #endif
 
 #define K3X_DECODE_MAX_T 8       /* tokens per call on the decode path (2 columns each) */
+#define K3X_WIDE_PMAX 12         /* K2 form, 2+ tokens: parts of the down products */
 #define K3X_DECODE_PARTS 8       /* latent form: parts the unique experts' down products
                                     are split into (partial aggregates, added in order) */
 #define K3X_STAGE_MAX    65536   /* bytes of activation fragments a workgroup stages in LDS */
@@ -149,6 +150,8 @@ struct k3x_moe_layer {
     float    *accL;               /* latent: [DECODE_PARTS][DECODE_MAX_T][XL] partial
                                      routed aggregates */
     uint16_t *latB;               /* latent: B set of the (normalised) aggregates */
+    float    *pacc;               /* K2 form, 2+ tokens: [K3X_WIDE_PMAX][DECODE_MAX_T][H]
+                                     part sums of k3_down_wide */
     /* diagnostics (K3X_TRACE=1 at creation): per-workgroup {id | ids, start, end} of the
      * last decode call's k1, k2 and k3, tr_cap records each */
     unsigned long long *tr;

@@ -118,6 +118,8 @@ static int layer_alloc(k3x_moe_layer *L)
     RCCHK(dmalloc((void **)&L->idx, (size_t)K3X_DECODE_MAX_T * K * 4, b));
     RCCHK(dmalloc((void **)&L->wt, (size_t)K3X_DECODE_MAX_T * K * 4, b));
     RCCHK(dmalloc((void **)&L->route, sizeof(k3x_route), b));
+    if (!L->lat && H % 256 == 0)
+        RCCHK(dmalloc((void **)&L->pacc, (size_t)K3X_WIDE_PMAX * K3X_DECODE_MAX_T * H * 4, b));
     if (L->lat) {
         const int X = L->XL;
         const size_t xs = (size_t)(X + 511) / 512 * 512;
@@ -153,7 +155,8 @@ static void layer_free(k3x_moe_layer *L)
     void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shB,
                  L->score, L->choice, L->idx, L->wt, L->route,
                  L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out,
-                 L->ldown, L->lup, L->lnw, L->zB, L->accL, L->latB, L->tr};
+                 L->ldown, L->lup, L->lnw, L->zB, L->accL, L->latB, L->tr,
+                 L->pacc};
     for (size_t i = 0; i < sizeof p / sizeof p[0]; i++)
         if (p[i]) hipFree(p[i]);
     for (int i = 0; i < L->pf.nretired; i++) hipFree(L->pf.retired[i]);

@@ -361,24 +361,6 @@ struct PfGemmArgs {
     uint8_t        *o8, *o8s;
 };
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// s_waitcnt vmcnt(n) lgkmcnt(0) (expcnt left at its maximum), gfx9 encoding
-#define WAIT_VMCNT_LGKM0(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4))
-
-// Meet the other waves once this wave's loads of a quad are in (N = vector loads issued
-// after the quad's; exact, since the wait is what makes LDS data written by loads safe to
-// read) and its LDS reads of the previous quad are done.  A bare s_barrier:
-// __syncthreads' release fence would wait for every load in flight; the empty asm keeps
-// the compiler from moving LDS accesses across it.
-template <int N>
-__device__ __forceinline__ void meet()
-{
-    WAIT_VMCNT_LGKM0(N);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
 
 // ------------------------------------------------------------------ dense GEMM
 // One dense product Y[p][r] = sum_k W[r][k] B[p][k] with bf16 weights (the shared

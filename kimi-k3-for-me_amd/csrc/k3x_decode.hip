@@ -1190,6 +1190,8 @@ struct K3Args {
     const int     *slot;           // expert -> arena slot (expert cache), or NULL: identity
     unsigned long long *trace;     // diagnostics, or NULL
     float         *pacc;           // k3_down_wide: part sums, [part][DECODE_MAX_T][H]
+    int            pr;             // k3_down_wide: parts of the routed items (the rest of
+                                   // blockIdx.y: parts of the shared expert's quads)
 };
 
 // A bf16 quad of the shared down matrix with its B fragments (read from the shared
@@ -1411,17 +1413,21 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
 }
 
 // Several tokens, K2 form, H a multiple of 256: the down products of 256 output rows a
-// workgroup (wave w: row tiles 2w, 2w + 1 of the group).  Workgroups blockIdx.y <
-// gridDim.y - 1 each take one part of the (unique expert, super-quad) items, dealt in
-// runs of equal length; the last row of workgroups takes the shared expert's bf16 quads.
+// workgroup (wave w: row tiles 2w, 2w + 1 of the group).  Workgroups blockIdx.y < pr
+// each take one part of the (unique expert, super-quad) items, dealt in runs of equal
+// length; the other rows take the shared expert's bf16 quads, quad q to the row q mod
+// (gridDim.y - pr).
 // All eight waves take the same item at once, so that its B fragments (16 KB at eight
 // tokens) come straight into an LDS stage once for the workgroup, beside the waves'
 // weights, through a ring of K3W_R stages: a wave has K3W_R - 1 items of weights in
 // flight while it multiplies one.  Every workgroup writes its part sums, which k3_reduce
-// adds up in part order (the shared expert's last).
+// adds up in part order (the shared expert's parts last).
 #define K3W_R 4
 #ifndef K3W_ON
 #define K3W_ON 1
+#endif
+#ifndef K3W_TMIN
+#define K3W_TMIN 2                                 // fewest tokens taking k3_down_wide
 #endif
 #define K3W_STAGE (1024u * 2 * K3X_DECODE_MAX_T)   // LDS bytes of a stage's B
 #define K3W_LPI 12                                 // vector loads per item and wave
@@ -1468,7 +1474,7 @@ __global__ void __launch_bounds__(NT3) k3_down_wide(K3Args a)
 {
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int NC = 2 * a.T;
-    const int rg = blockIdx.x, p = blockIdx.y, P = gridDim.y - 1;
+    const int rg = blockIdx.x, p = blockIdx.y, P = a.pr;
     const int rt0 = rg * 16 + 2 * wave;
     const uint32_t stB = (uint32_t)wave * WAVE * 16u;
     BFrag<true> bl;
@@ -1529,12 +1535,15 @@ __global__ void __launch_bounds__(NT3) k3_down_wide(K3Args a)
         // the shared expert: quad q's two 16-row runs a wave (four 16-byte loads each, as
         // an fp4 super-quad's codes, plus two scale-slot loads that read nothing)
         const int nQS = a.sh_down ? a.SI >> 7 : 0;
+        const int ps = p - P, PS = gridDim.y - P;
+        const int cs = ps < nQS ? (nQS - 1 - ps) / PS + 1 : 0;
         const uint32_t sbytes = (uint32_t)nQS * 4096u;  // a tile's bytes
         const uint32_t qbB = 256u * (uint32_t)NC;       // B bytes of a quad
         const rsrc_t r = make_rsrc(a.sh_down + (size_t)rt0 * 16 * a.SI, 2 * sbytes);
         const rsrc_t rsb = make_rsrc(a.shB, (uint32_t)nQS * qbB);
-        k3w_ring(nQS, [&](int i, int q) AI {
-            const bool on = q < nQS;
+        k3w_ring(cs, [&](int i, int k) AI {
+            const bool on = k < cs;
+            const int q = ps + PS * k;
             const uint32_t b0 = on ? (uint32_t)q * 4096u : K3X_OOB;
             sq_load(w[i][0], r, b0, lane);
             sq_load(w[i][1], r, on ? sbytes + b0 : K3X_OOB, lane);
@@ -1984,12 +1993,20 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a3.pacc = L->pacc;
     // K2 form, several tokens: 256 rows a workgroup over parts of the items, about one
     // workgroup per CU
-    const bool wide = !L->lat && T >= 2 && X % 256 == 0 && L->pacc && K3W_ON;
+    const bool wide = !L->lat && T >= K3W_TMIN && X % 256 == 0 && L->pacc && K3W_ON;
     if (wide) {
-        // routed parts and one shared part: about one workgroup per CU
+        // about one workgroup per CU, the parts shared between the routed items (by the
+        // unique experts a call can have) and the shared expert's quads in proportion
         int pw = 256 / (X / 256);
         if (pw < 2) pw = 2;
         if (pw > K3X_WIDE_PMAX) pw = K3X_WIDE_PMAX;
+        const int nQS = a3.sh_down ? L->SI / 128 : 0;
+        const int ue = T * c->topk < c->n_experts ? T * c->topk : c->n_experts;
+        const int nit = ue * nSI;
+        int pr = (int)(((long)pw * nit * 2 + (nit + nQS)) / (2L * (nit + nQS)));
+        if (pr > pw - (nQS > 0)) pr = pw - (nQS > 0);
+        if (pr < 1) pr = 1;
+        a3.pr = pr;
         const dim3 gw(X / 256, pw);
         const size_t lw = (size_t)K3W_R * K3W_STAGE;
         if (L->special & 4) hipLaunchKernelGGL(k3_down_wide<true>, gw, dim3(NT3), lw, s, a3);

@@ -1017,48 +1017,57 @@ __device__ void k2_gateup_body(const K2Args &a, float *lds, int *s_go_p)
         st.issue(a.rB, bbytes, NT);
         st.commit(NT);
     }
-    // thread 0 reads the routing words this workgroup needs: the unique count, its slot's
-    // expert and the slot's weight per token (into s_w); after an earlier launch's
-    // selection (sel_done) the plain words, written before this launch began
+    // the routing words this workgroup needs: the unique count, its slot's expert and the
+    // slot's weight per token (into s_w); after an earlier launch's selection (sel_done)
+    // the plain words, written before this launch began, else their tagged copies
     __shared__ float s_w[K3X_DECODE_MAX_T];
     __shared__ int s_e;
     const k3x_route *rte = a.route;
-    if (threadIdx.x == 0) {
-        int go = 1, e = 0;
-        if (a.sel_done) {
+    if (a.sel_done) {
+        if (threadIdx.x == 0) {
+            int go = 1, e = 0;
             if (u >= rte->nu) go = 0;
             else {
                 e = rte->uniq[u];
                 for (int t = 0; t < a.T; t++) s_w[t] = rte->wtok[u][t];
             }
-        } else {
-            const unsigned seq = *a.seq;
-            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-            // the word at p once it carries this call's tag; false when the bound ran out
-            auto take = [&](const unsigned long long *p, uint32_t &v) -> bool {
-                for (;;) {
-                    const unsigned long long w =
-                        __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if ((unsigned)(w >> 32) == seq) { v = (uint32_t)w; return true; }
-                    if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) return false;
-                    __builtin_amdgcn_s_sleep(2);
-                }
-            };
-            uint32_t v = 0;
-            bool ok = take(&rte->tnu, v);
-            if (ok && u >= (int)v) go = 0;
-            else if (ok && (ok = take(&rte->tuniq[u], v))) {
-                e = (int)v;
-                for (int t = 0; ok && t < a.T; t++)
-                    if ((ok = take(&rte->twtok[u][t], v))) s_w[t] = __uint_as_float(v);
-            }
-            if (!ok) {
-                __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                go = 0;
-            }
+            s_go = go;
+            s_e = e;
         }
-        s_go = go;
-        s_e = e;
+    } else if (wave == 0) {
+        // lane 0 reads the unique count, lane 1 its slot's expert, lanes 2 .. T + 1 the
+        // slot's weight per token, all at once, until each carries this call's tag (or
+        // the count does and this slot is past it); the bound ends the wait with an error
+        const unsigned seq = *a.seq;
+        const int nw = 2 + a.T;
+        const unsigned long long *p = lane == 0 ? &rte->tnu
+                                    : lane == 1 ? &rte->tuniq[u]
+                                                : &rte->twtok[u][lane < nw ? lane - 2 : 0];
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        int go = 0, e = 0;
+        for (;;) {
+            const unsigned long long wv =
+                lane < nw ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                          : (unsigned long long)seq << 32;
+            const uint32_t v = (uint32_t)wv;
+            const uint64_t ok = __ballot((unsigned)(wv >> 32) == seq);
+            if ((ok & 1ull) && u >= (int)__shfl(v, 0)) break;
+            if (ok == ~0ull) {
+                go = 1;
+                e = (int)__shfl(v, 1);
+                if (lane >= 2 && lane < nw) s_w[lane - 2] = __uint_as_float(v);
+                break;
+            }
+            if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) {
+                if (lane == 0) __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (lane == 0) {
+            s_go = go;
+            s_e = e;
+        }
     }
     __syncthreads();
     if (!s_go) return;

@@ -397,9 +397,16 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish, unsigned seq = 
         }
         return nu;
     }
-    for (int t = wave; t < a.T; t += NW)
-        wave_topk<NE, 0>(cr, sr, (uint32_t)(t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
-                      l.idx[t], l.w[t], lane);
+    // tokens wave and wave + NW together (at most eight tokens over four waves)
+    static_assert(K3X_DECODE_MAX_T <= 2 * NW, "two tokens a wave at most");
+    if (wave < a.T) {
+        const int t1 = wave + NW < a.T ? wave + NW : wave;
+        const uint32_t ro[2] = {(uint32_t)(wave * a.E * 4), (uint32_t)(t1 * a.E * 4)};
+        int *const si[2] = {l.idx[wave], l.idx[t1]};
+        float *const sw[2] = {l.w[wave], l.w[t1]};
+        wave_topk_n<NE, 0, 2>(cr, sr, ro, wave + NW < a.T ? 2 : 1, a.E, a.K, a.renorm,
+                              a.routed_scale, si, sw, lane);
+    }
     for (int e = threadIdx.x; e < a.E; e += NT) l.first[e] = 0x7FFFFFFF;
     __syncthreads();
     const int TK = a.T * a.K;

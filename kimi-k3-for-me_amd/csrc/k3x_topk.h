@@ -124,4 +124,87 @@ __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, 
     if (out_e) { *out_e = mine_e; *out_w = wgt; }
 }
 
+// wave_topk for N tokens of one wave together (tokens past ntok load nothing and store
+// nothing): every token's rows are loaded at once (one memory round trip for all), and
+// each round runs for every token before the next, so that one token's wave maximum
+// fills the other's latency.  Per token, the same operations in the same order as
+// wave_topk, so the same results.
+template <int NE, int CP, int N>
+__device__ void wave_topk_n(rsrc_t cr, rsrc_t sr, const uint32_t (&row_off)[N], int ntok, int E,
+                            int K, int renorm, float routed_scale, int *const (&s_idx)[N],
+                            float *const (&s_w)[N], int lane)
+{
+    uint64_t pk[N][NE];
+    float sc[N][NE], cv[N][NE];
+#pragma unroll
+    for (int r = 0; r < N; r++)
+#pragma unroll
+        for (int c = 0; c < NE; c++) {
+            const int e = lane * NE + c;
+            const uint32_t o = (e < E && r < ntok) ? row_off[r] + 4u * (uint32_t)e : K3X_OOB;
+            cv[r][c] = bload_f32<CP>(cr, o);
+            sc[r][c] = bload_f32<CP>(sr, o);
+        }
+    SCHED_FENCE();
+#pragma unroll
+    for (int r = 0; r < N; r++)
+#pragma unroll
+        for (int c = 0; c < NE; c++) {
+            const int e = lane * NE + c;
+            const uint32_t k = choice_key(cv[r][c]);
+            pk[r][c] = (e < E && k > K_NEG_INF) ? ((uint64_t)k << 32) | (uint64_t)(~(uint32_t)e) : 0ull;
+        }
+    uint64_t prev[N];
+    int mine_e[N];
+    float mine_s[N];
+#pragma unroll
+    for (int r = 0; r < N; r++) {
+        prev[r] = ~0ull;
+        mine_e[r] = 0;
+        mine_s[r] = 0.0f;
+    }
+    for (int j = 0; j < K; j++) {
+#pragma unroll
+        for (int r = 0; r < N; r++) {
+            uint64_t best = 0ull;
+            float bs = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NE; c++) {
+                const uint64_t v = pk[r][c] < prev[r] ? pk[r][c] : 0ull;
+                const bool gt = v > best;
+                best = gt ? v : best;
+                bs = gt ? sc[r][c] : bs;
+            }
+            const uint32_t bk = (uint32_t)(best >> 32);
+            const uint32_t m = wave_max_u32(bk);
+            const uint64_t holders = __ballot(m != 0u && bk == m);
+            if (holders == 0ull) {                  // nothing left (uniform)
+                if (lane == j) { mine_e[r] = 0; mine_s[r] = 0.0f; }
+                continue;
+            }
+            const int w = (int)__builtin_ctzll(holders);
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)best, w);
+            const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs), w));
+            prev[r] = ((uint64_t)m << 32) | lo;
+            if (lane == j) { mine_e[r] = (int)~lo; mine_s[r] = ws; }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < N; r++) {
+        float wgt = mine_s[r];
+        if (renorm && K > 1) {
+            double sum = 0.0;
+            for (int j = 0; j < K; j++)
+                sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine_s[r]), j));
+            const float inv = (float)(1.0 / (sum + 1e-20));
+            wgt *= inv;
+        }
+        wgt *= routed_scale;
+        if (r < ntok && lane < K) {
+            s_idx[r][lane] = mine_e[r];
+            s_w[r][lane] = wgt;
+        }
+    }
+}
+
 #endif

@@ -1442,6 +1442,9 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
 #ifndef K3W_ON
 #define K3W_ON 1
 #endif
+#ifndef K3W_LAT_TMAX
+#define K3W_LAT_TMAX 4                             // most tokens of the latent form taking it
+#endif
 #ifndef K3W_TMIN
 #define K3W_TMIN 2                                 // fewest tokens taking k3_down_wide
 #endif
@@ -2006,10 +2009,14 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
         a3.trace = on ? trb + (size_t)L->tr_cap * 6 : NULL;
         L->tr_n[2] = on ? X / 16 : 0;
     }
-    a3.pacc = L->pacc;
-    // K2 form, several tokens: 256 rows a workgroup over parts of the items, about one
-    // workgroup per CU
-    const bool wide = !L->lat && T >= K3W_TMIN && X % 256 == 0 && L->pacc && K3W_ON;
+    // several tokens, X a multiple of 256: 256 rows a workgroup over parts of the items,
+    // about one workgroup per CU; the parts' sums go to the K2 form's part buffer (added up
+    // by k3_reduce) or to the latent form's partial aggregates (added up by k4_latent_norm)
+    a3.pacc = L->lat ? L->accL : L->pacc;
+    // (the latent form up to four tokens: past that, k4_latent_norm's sum over the parts
+    // of every token outweighs the gain, 632 us against 587 at eight)
+    const bool wide = T >= K3W_TMIN && X % 256 == 0 && a3.pacc && K3W_ON &&
+                      (!L->lat || T <= K3W_LAT_TMAX);
     if (wide) {
         // about one workgroup per CU, the parts shared between the routed items (by the
         // unique experts a call can have) and the shared expert's quads in proportion
@@ -2023,14 +2030,20 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
         if (pr > pw - (nQS > 0)) pr = pw - (nQS > 0);
         if (pr < 1) pr = 1;
         a3.pr = pr;
+        if (L->lat) {
+            parts = pw;
+            a3.pstride = (size_t)K3X_DECODE_MAX_T * X;
+        }
         const dim3 gw(X / 256, pw);
         const size_t lw = (size_t)K3W_R * K3W_STAGE;
         if (L->special & 4) hipLaunchKernelGGL(k3_down_wide<true>, gw, dim3(NT3), lw, s, a3);
         else                hipLaunchKernelGGL(k3_down_wide<false>, gw, dim3(NT3), lw, s, a3);
-        if ((rc = launch_ok())) return rc;
-        const int n = T * X;
-        hipLaunchKernelGGL(k3_reduce, dim3((n + 255) / 256), dim3(256), 0, s,
-                           (const float *)L->pacc, pw, resid, out, n, X);
+        if (!L->lat) {
+            if ((rc = launch_ok())) return rc;
+            const int n = T * X;
+            hipLaunchKernelGGL(k3_reduce, dim3((n + 255) / 256), dim3(256), 0, s,
+                               (const float *)L->pacc, pw, resid, out, n, X);
+        }
     } else if (use2) {
         if (L->special & 4) hipLaunchKernelGGL(k3_down2<true>, dim3(X / 32, parts), dim3(NT3), 0, s, a3);
         else                hipLaunchKernelGGL(k3_down2<false>, dim3(X / 32, parts), dim3(NT3), 0, s, a3);

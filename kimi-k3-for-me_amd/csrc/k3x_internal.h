@@ -48,7 +48,7 @@ extern "C" {
 #endif
 
 #define K3X_DECODE_MAX_T 8       /* tokens per call on the decode path (2 columns each) */
-#define K3X_WIDE_PMAX 12         /* K2 form, 2+ tokens: parts of the down products */
+#define K3X_WIDE_PMAX 20         /* 2+ tokens: parts of the down products (k3_down_wide) */
 #define K3X_DECODE_PARTS 8       /* latent form: parts the unique experts' down products
                                     are split into (partial aggregates, added in order) */
 #define K3X_STAGE_MAX    65536   /* bytes of activation fragments a workgroup stages in LDS */
@@ -147,7 +147,7 @@ struct k3x_moe_layer {
                                      activation over whole super-quads of I */
     uint16_t *shB;                /* B set of the shared activation (SI/128 quads) */
     uint16_t *zB;                 /* latent: B set of z = down . x over whole super-quads */
-    float    *accL;               /* latent: [DECODE_PARTS][DECODE_MAX_T][XL] partial
+    float    *accL;               /* latent: [max(DECODE_PARTS, WIDE_PMAX)][DECODE_MAX_T][XL] partial
                                      routed aggregates */
     uint16_t *latB;               /* latent: B set of the (normalised) aggregates */
     float    *pacc;               /* K2 form, 2+ tokens: [K3X_WIDE_PMAX][DECODE_MAX_T][H]

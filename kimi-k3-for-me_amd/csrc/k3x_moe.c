@@ -126,7 +126,8 @@ static int layer_alloc(k3x_moe_layer *L)
         RCCHK(dmalloc((void **)&L->ldown, k3x_bf16_matrix_bytes(X, H), b));
         RCCHK(dmalloc((void **)&L->lup, k3x_bf16_matrix_bytes(H, X), b));
         RCCHK(dmalloc((void **)&L->zB, xs * 2 * K3X_DECODE_MAX_T * 2, b));
-        RCCHK(dmalloc((void **)&L->accL, (size_t)K3X_DECODE_PARTS * K3X_DECODE_MAX_T * X * 4, b));
+        const size_t np = K3X_WIDE_PMAX > K3X_DECODE_PARTS ? K3X_WIDE_PMAX : K3X_DECODE_PARTS;
+        RCCHK(dmalloc((void **)&L->accL, np * K3X_DECODE_MAX_T * X * 4, b));
         RCCHK(dmalloc((void **)&L->latB, xs * 2 * K3X_DECODE_MAX_T * 2, b));
     }
     if (c->latent_norm) RCCHK(dmalloc((void **)&L->lnw, (size_t)L->XL * 4, b));

@@ -1625,7 +1625,7 @@ struct KNArgs {
     uint16_t    *latB;
 };
 
-#define NT4 256
+#define NT4 1024                  // k4_latent_norm: 16 waves, 1024 set entries a workgroup
 
 __device__ __forceinline__ float agg_at(const KNArgs &a, size_t i)
 {
@@ -1634,15 +1634,33 @@ __device__ __forceinline__ float agg_at(const KNArgs &a, size_t i)
     return v;
 }
 
+// Four consecutive floats at o of each of P parts (pstride floats apart), added in part
+// order.  The loads go out eight parts at a time (a part past P loads the last part again
+// and is not added), not one part's load and add after another's.
+__device__ __forceinline__ f32x4 parts_sum4(const float *acc, int P, size_t pstride, size_t o)
+{
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    for (int p0 = 0; p0 < P; p0 += 8) {
+        f32x4 w[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int p = p0 + j < P ? p0 + j : P - 1;
+            w[j] = *(const f32x4 *)(acc + p * pstride + o);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (p0 + j >= P) break;
+            if (p0 + j == 0) v = w[j];
+            else { v[0] += w[j][0]; v[1] += w[j][1]; v[2] += w[j][2]; v[3] += w[j][3]; }
+        }
+    }
+    return v;
+}
+
 // four consecutive aggregates (i a multiple of 4), each added over the parts in order
 __device__ __forceinline__ f32x4 agg4(const KNArgs &a, size_t i)
 {
-    f32x4 v = *(const f32x4 *)(a.acc + i);
-    for (int p = 1; p < a.P; p++) {
-        const f32x4 w = *(const f32x4 *)(a.acc + p * a.pstride + i);
-        v[0] += w[0]; v[1] += w[1]; v[2] += w[2]; v[3] += w[3];
-    }
-    return v;
+    return parts_sum4(a.acc, a.P, a.pstride, i);
 }
 
 __global__ void __launch_bounds__(NT4) k4_latent_norm(KNArgs a)
@@ -2067,7 +2085,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     const bool shl = k4_lds_bytes(fuse, true, T, X, L->SI) <= K4_LDS_MAX;
     if (!fuse) {
         const int nent = 4 * nSX * 16 * NC;
-        hipLaunchKernelGGL(k4_latent_norm, dim3((nent + 4 * NT4 - 1) / (4 * NT4)), dim3(NT4), 0,
+        hipLaunchKernelGGL(k4_latent_norm, dim3((nent + NT4 - 1) / NT4), dim3(NT4), 0,
                            s, an);
         if ((rc = launch_ok())) return rc;
         if ((rc = record(L, ev++, s))) return rc;

@@ -1442,9 +1442,6 @@ __global__ void __launch_bounds__(NT3) k3_down2(K3Args a)
 #ifndef K3W_ON
 #define K3W_ON 1
 #endif
-#ifndef K3W_LAT_TMAX
-#define K3W_LAT_TMAX 4                             // most tokens of the latent form taking it
-#endif
 #ifndef K3W_TMIN
 #define K3W_TMIN 2                                 // fewest tokens taking k3_down_wide
 #endif
@@ -2031,10 +2028,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     // about one workgroup per CU; the parts' sums go to the K2 form's part buffer (added up
     // by k3_reduce) or to the latent form's partial aggregates (added up by k4_latent_norm)
     a3.pacc = L->lat ? L->accL : L->pacc;
-    // (the latent form up to four tokens: past that, k4_latent_norm's sum over the parts
-    // of every token outweighs the gain, 632 us against 587 at eight)
-    const bool wide = T >= K3W_TMIN && X % 256 == 0 && a3.pacc && K3W_ON &&
-                      (!L->lat || T <= K3W_LAT_TMAX);
+    const bool wide = T >= K3W_TMIN && X % 256 == 0 && a3.pacc && K3W_ON;
     if (wide) {
         // about one workgroup per CU, the parts shared between the routed items (by the
         // unique experts a call can have) and the shared expert's quads in proportion

@@ -1760,11 +1760,7 @@ __device__ __forceinline__ void k4_fuse_norm(const KNArgs &a, float *agg, double
         double ss = 0.0;
         for (int c = threadIdx.x; c < n4; c += NT3) {
             const size_t o = (size_t)t * a.XL + 4 * c;
-            f32x4 v = *(const f32x4 *)(a.acc + o);
-            for (int p = 1; p < a.P; p++) {
-                const f32x4 w = *(const f32x4 *)(a.acc + p * a.pstride + o);
-                v[0] += w[0]; v[1] += w[1]; v[2] += w[2]; v[3] += w[3];
-            }
+            const f32x4 v = parts_sum4(a.acc, a.P, a.pstride, o);
             *(f32x4 *)(agg + o) = v;
 #pragma unroll
             for (int k = 0; k < 4; k++) ss += (double)v[k] * (double)v[k];

@@ -13,8 +13,12 @@
 //   k3_down           each unique expert's down product and the shared expert's (:1858)
 //                     into one accumulator set per 16 output rows (the weighted combine,
 //                     :1941-1942, plus the shared result, :1859), and an optional residual.
-//                     With two or more tokens, k3_down2 instead: two 16-row tiles a
-//                     workgroup, each B fragment read once for both.
+//                     With two or more tokens and 256 | H, k3_down_wide instead: 256 rows
+//                     a workgroup over parts of the items, each item's B fragments loaded
+//                     into LDS once for the workgroup; k3_reduce (K2 form) or
+//                     k4_latent_norm (latent form) adds the parts in order.  Otherwise
+//                     k3_down2: two 16-row tiles a workgroup, each B fragment read once
+//                     for both.
 //
 // Each weight byte is read once per call.  Weights are dequantised in registers
 // (E2M1 x 2^(s-127) is exact in bf16) and multiplied on v_mfma_f32_16x16x32_bf16 against

@@ -1593,6 +1593,28 @@ __global__ void __launch_bounds__(NT3) k3_down_wide(K3Args a)
     });
 }
 
+// The same, four outputs a thread (16-byte aligned out, resid and parts, H % 4 == 0).
+__global__ void __launch_bounds__(256) k3_reduce4(const float *pacc, int P, const float *resid,
+                                                   float *out, int n4, int H)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const size_t o = (size_t)i * 4, ps = (size_t)K3X_DECODE_MAX_T * H;
+    f32x4 v[K3X_WIDE_PMAX];
+#pragma unroll
+    for (int q = 0; q < K3X_WIDE_PMAX; q++)
+        if (q < P) v[q] = *(const f32x4 *)(pacc + q * ps + o);
+    f32x4 s = v[0];
+#pragma unroll
+    for (int q = 1; q < K3X_WIDE_PMAX; q++)
+        if (q < P) { s[0] += v[q][0]; s[1] += v[q][1]; s[2] += v[q][2]; s[3] += v[q][3]; }
+    if (resid) {
+        const f32x4 r = *(const f32x4 *)(resid + o);
+        s[0] = r[0] + s[0]; s[1] = r[1] + s[1]; s[2] = r[2] + s[2]; s[3] = r[3] + s[3];
+    }
+    *(f32x4 *)(out + o) = s;
+}
+
 // out = resid + the parts' sums of k3_down_wide, added in part order, over [T][H].
 __global__ void __launch_bounds__(256) k3_reduce(const float *pacc, int P, const float *resid,
                                                   float *out, int n, int H)
@@ -2053,8 +2075,13 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
         if (!L->lat) {
             if ((rc = launch_ok())) return rc;
             const int n = T * X;
-            hipLaunchKernelGGL(k3_reduce, dim3((n + 255) / 256), dim3(256), 0, s,
-                               (const float *)L->pacc, pw, resid, out, n, X);
+            const bool v4 = X % 4 == 0 && ((uintptr_t)out % 16 | (uintptr_t)resid % 16) == 0;
+            if (v4)
+                hipLaunchKernelGGL(k3_reduce4, dim3((n / 4 + 255) / 256), dim3(256), 0, s,
+                                   (const float *)L->pacc, pw, resid, out, n / 4, X);
+            else
+                hipLaunchKernelGGL(k3_reduce, dim3((n + 255) / 256), dim3(256), 0, s,
+                                   (const float *)L->pacc, pw, resid, out, n, X);
         }
     } else if (use2) {
         if (L->special & 4) hipLaunchKernelGGL(k3_down2<true>, dim3(X / 32, parts), dim3(NT3), 0, s, a3);

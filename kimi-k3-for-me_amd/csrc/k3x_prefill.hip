@@ -1260,6 +1260,12 @@ static void launch_dn(const PfGemmArgs &a, unsigned grid, hipStream_t s)
 #define MX_CT_S 1
 #define MX_CT_B 2
 #define MX_NW   4
+#ifndef MX_GU_RT32_S
+#define MX_GU_RT32_S 1     // 32-row tiles a wave, small-class gate/up
+#endif
+#ifndef MX_DN_RT32_S
+#define MX_DN_RT32_S 2     // the same, small-class down
+#endif
 
 static inline unsigned round8(size_t n) { return (unsigned)((n + 7) & ~(size_t)7); }
 
@@ -1372,11 +1378,11 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     const bool mx = L->pf_mode == K3X_PREFILL_MXFP8;
     sa.tpb_s[0] = mx ? MX_CT_S * 32 : GU_CT32_S * 32 / HLr;
     sa.tpb_b[0] = mx ? MX_CT_B * 32 : GU_CT32_B * 32 / HLr;
-    sa.nrb_s[0] = cdiv(I, mx ? MX_NW * GU_RT32 * 32 : NW_GS * GU_RT32_S * 32);
+    sa.nrb_s[0] = cdiv(I, mx ? MX_NW * MX_GU_RT32_S * 32 : NW_GS * GU_RT32_S * 32);
     sa.nrb_b[0] = cdiv(I, (mx ? MX_NW : NW_B) * GU_RT32 * 32);
     sa.tpb_s[1] = mx ? MX_CT_S * 32 : DN_CT32_S * 32 / 2;
     sa.tpb_b[1] = mx ? MX_CT_B * 32 : DN_CT32_B * 32 / 2;
-    sa.nrb_s[1] = cdiv(X, mx ? MX_NW * DN_RT32 * 32 : NW_DS * DN_RT32_S * 32);
+    sa.nrb_s[1] = cdiv(X, mx ? MX_NW * MX_DN_RT32_S * 32 : NW_DS * DN_RT32_S * 32);
     sa.nrb_b[1] = cdiv(X, (mx ? MX_NW : NW_B) * DN_RT32 * 32);
     hipLaunchKernelGGL(pf_scan, dim3(1), dim3(1024), 0, s, sa);
     if ((rc = launch_ok())) PF_RET(rc);
@@ -1452,7 +1458,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     }
     if ((rc = launch_ok())) PF_RET(rc);
     if (mx) {
-        hipLaunchKernelGGL((pf_gemm_mx<2, GU_RT32, MX_CT_S, true, MX_NW>), dim3(grid_s[0]), dim3(MX_NW * WAVE), 0, s, g);
+        hipLaunchKernelGGL((pf_gemm_mx<2, MX_GU_RT32_S, MX_CT_S, true, MX_NW>), dim3(grid_s[0]), dim3(MX_NW * WAVE), 0, s, g);
     } else if (ex_gu) {
         if (HLr == 1) launch_gu<true, 1, GU_CT32_S, NW_GS, GU_RT32_S>(g, grid_s[0], s);
         else          launch_gu<true, 2, GU_CT32_S, NW_GS, GU_RT32_S>(g, grid_s[0], s);
@@ -1475,7 +1481,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     db.ntile = B->tb_dn + 2 * E + 1; db.dbase = B->tb_dn + E;
     if (mx) {
         hipLaunchKernelGGL((pf_gemm_mx<1, DN_RT32, MX_CT_B, false, MX_NW>), dim3(grid_b[1]), dim3(MX_NW * WAVE), 0, s, db);
-        hipLaunchKernelGGL((pf_gemm_mx<1, DN_RT32, MX_CT_S, false, MX_NW>), dim3(grid_s[1]), dim3(MX_NW * WAVE), 0, s, d);
+        hipLaunchKernelGGL((pf_gemm_mx<1, MX_DN_RT32_S, MX_CT_S, false, MX_NW>), dim3(grid_s[1]), dim3(MX_NW * WAVE), 0, s, d);
     } else if (L->special & 4) { launch_dn<true, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<true, DN_CT32_S, NW_DS, DN_RT32_S>(d, grid_s[1], s); }
     else                { launch_dn<false, DN_CT32_B, NW_B>(db, grid_b[1], s); launch_dn<false, DN_CT32_S, NW_DS, DN_RT32_S>(d, grid_s[1], s); }
     if ((rc = launch_ok())) PF_RET(rc);

@@ -195,8 +195,9 @@ def test_full_verify_b8_zipf(torch, k3x):
 @pytest.mark.parametrize("T,bf16", [(3, False), (5, True)])
 def test_full_decode_multi_token(torch, k3x, full_normal, T, bf16):
     """T = 3 and 5 at the full shape: the several-token kernels (each super-quad's B
-    fragments staged once for the gate/up waves, two row tiles per down workgroup) with
-    B sets of 6 and 10 columns, which fill the staging chunks only in part."""
+    fragments staged once for the gate/up waves; the down products in 256-row workgroups
+    over parts of the items, the parts added by k3_reduce) with B sets of 6 and 10
+    columns, which fill the staging chunks only in part."""
     say(f"case: full-size decode T={T} ({'bf16' if bf16 else 'fp32'} tokens) vs oracle")
     L, layer = full_normal
     x = L.x(T, bf16=bf16, stream_sub=6 + T)
@@ -206,4 +207,26 @@ def test_full_decode_multi_token(torch, k3x, full_normal, T, bf16):
     np.testing.assert_allclose(w2, wt, rtol=1e-6)
     err = synth.rel_l2(out, o)
     say(f"  rel_l2={err:.3e}")
+    assert err < TOL
+
+
+def test_full_repeated_token_columns(torch, k3x, full_normal):
+    """Eight copies of one token in a T = 8 call: every column goes through the same
+    products and the same part sums, so the eight outputs are equal bit for bit, within
+    the parity bar of the single-token call, and a second identical call gives the same
+    bits (the down products' parts are added in a fixed order)."""
+    say("case: full-size T=8 call of one token repeated, columns and repeat bitwise")
+    L, layer = full_normal
+    x1 = L.x(1, bf16=True, stream_sub=11)
+    x = np.repeat(x1, 8, axis=0)
+    out, idx, _ = dev_forward(torch, k3x, layer, x, bf16=True)
+    for t in range(1, 8):
+        assert np.array_equal(idx[t], idx[0])
+        assert np.array_equal(out[t].view(np.uint32), out[0].view(np.uint32)), t
+    out2, _, _ = dev_forward(torch, k3x, layer, x, bf16=True)
+    assert np.array_equal(out2.view(np.uint32), out.view(np.uint32))
+    o1, i1, _ = dev_forward(torch, k3x, layer, x1, bf16=True)
+    assert np.array_equal(i1[0], idx[0])
+    err = synth.rel_l2(out[:1], o1)
+    say(f"  rel_l2 against the single-token call {err:.3e}")
     assert err < TOL

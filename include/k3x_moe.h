@@ -226,8 +226,11 @@ int  k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float e
  * fp32, idx/wt [topk] left holding the LAST token's routing.  k3x_moe_prefill mirrors
  * k3_moe_prefill (k3.h:636-637): with T > 1 it leaves idx/wt untouched, as the
  * reference's batched path does (k3_ops.c:2018-2053); with T == 1 it writes them as
- * k3_moe.  On this device both run the same pipeline, whose results do not depend on how
- * tokens are grouped into calls.  Synchronous; K3X_E_WAIT when a decode workgroup gave
+ * k3_moe.  On this device both run the same pipeline.  Identical calls repeat bit for
+ * bit; one token's output in calls that group tokens differently (one token against
+ * eight, decode against prefill) agrees within the parity bar but not bit for bit, since
+ * the fp32 accumulation order of the products follows the call's shape (its token count
+ * and its unique experts).  Synchronous; K3X_E_WAIT when a decode workgroup gave
  * up its wait (the output is then not valid).  The reference's scratch argument has no
  * counterpart: working memory lives in the layer. */
 int  k3x_moe(k3x_moe_layer *L, float *out, const float *x, int T, int *idx, float *wt);
@@ -289,6 +292,22 @@ int  k3x_attn_res(float *h, const float *blocks, int maxb, int nb, const float *
 int  k3x_moe_half(k3x_moe_layer *L, float *h, float *pref, const float *blocks, int maxb,
                   int nb, const float *fold, const float *post_norm, float eps, int T,
                   float *hin, void *stream);
+
+/* The same two calls with a block count per row, as k3_decoder_layer_core takes them
+ * (k3_ops.c:2481-2483: token t's count is nbv[t * nbs], nbs 0 for one count shared by
+ * every token, 1 for one per token; used per token at :2493 and :2549; the speculative
+ * caller k3_decoder_layer_inc_logv, :2606-2613, passes nbs 1).  nbv is a DEVICE int
+ * array read by the kernel when it runs, so a captured graph replays with the counts the
+ * array then holds.  Rows with equal counts compute the same floats as k3x_attn_res /
+ * k3x_moe_half.  A count outside 0 .. min(maxb, 63) (or above 0 with blocks NULL) fills
+ * that row of h with quiet NaNs, which the MoE half carries to its outputs: the
+ * reference reads past its block stack there. */
+int  k3x_attn_res_v(float *h, const float *blocks, int maxb, const int *nbv, int nbs,
+                    const float *pref, const float *fold, int n, int T, float eps,
+                    void *stream);
+int  k3x_moe_half_v(k3x_moe_layer *L, float *h, float *pref, const float *blocks, int maxb,
+                    const int *nbv, int nbs, const float *fold, const float *post_norm,
+                    float eps, int T, float *hin, void *stream);
 
 /* ---- stacked layers ------------------------------------------------------------------
  * The MoE half of consecutive decoder layers (k3_decoder_layer_core, k3_ops.c:2547-2589,

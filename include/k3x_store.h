@@ -97,7 +97,9 @@ int64_t k3x_store_expert_load(const k3x_store *s, const k3x_expert_ref *r, unsig
 
 /* A supplier over the store (the K3ExpertSrc seam): get(layer, expert) reads the expert
  * into a buffer the supplier owns and points the k3x_expert_q into it (valid until the
- * next get).  k3x_store_src_fetches() counts the reads. */
+ * next get).  Its getmany() only advises the kernel to read the experts' ranges ahead and
+ * returns 0 (none made resident: get() still reads each).  k3x_store_src_fetches()
+ * counts the reads. */
 int  k3x_store_src_create(k3x_store *s, k3x_expert_src **out);
 /* The same supplier for a layer whose experts are gate/up [moe_inter][width] and down
  * [width][moe_inter] (width: the latent width, or hidden): get() fails, so the layer

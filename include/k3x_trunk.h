@@ -37,10 +37,19 @@ void k3x_trunk_destroy(k3x_trunk *t);
 /* Y[t*ldy + o] = W[o] . X[t*ldx] for t < T (k3_mmw_batch_ld), device pointers, X fp32
  * (K3X_F32) or bf16 (K3X_BF16), ldx >= in, ldy >= out, X 16-byte aligned with ldx a
  * multiple of 8; asynchronous on `stream`.  T > 8 uses a workspace of T*in*4 bytes held
- * by the handle, grown (with an allocation and a device synchronisation) when a larger T
- * arrives; two calls on one handle must be ordered on one stream. */
+ * by the handle, grown (an allocation, at least doubling) when a larger T arrives; two
+ * calls on one handle must be ordered on one stream.
+ * Graph capture: a call may be captured once the workspace covers its T (reserve first
+ * with k3x_trunk_reserve); a call that would grow it on a stream under capture returns
+ * K3X_E_SHAPE and enqueues nothing.  An outgrown workspace is kept until
+ * k3x_trunk_destroy (a graph captured over it stays valid); after 16 growths a further
+ * one returns K3X_E_NOMEM. */
 int  k3x_trunk_apply(k3x_trunk *t, float *Y, int ldy, const void *X, int x_dtype, int ldx,
                      int T, void *stream);
+
+/* Grow the workspace for calls of up to max_T rows now (outside capture).  No
+ * counterpart in the reference, whose products need no workspace. */
+int  k3x_trunk_reserve(k3x_trunk *t, int max_T);
 
 /* The host-pointer form with k3_mmw_batch's semantics (synchronous): Y [T][out] and
  * X [T][in] fp32 in host memory. */

@@ -22,8 +22,8 @@
 //
 // Each weight byte is read once per call.  Weights are dequantised in registers
 // (E2M1 x 2^(s-127) is exact in bf16) and multiplied on v_mfma_f32_16x16x32_bf16 against
-// activations split into bf16 hi + lo columns: every product is exact and only the fp32
-// accumulation rounds.
+// activations split into bf16 hi + lo columns (16 significant bits: a bf16 activation
+// exactly, an fp32 one within 2^-17): the products of the pair are exact, the sums fp32.
 //
 // Streaming.  A workgroup's weights are cut into wave-uniform items (an fp4 super-quad,
 // 4352 bytes per 16 rows, or a bf16 quad, 4096 bytes) that its waves take interleaved,
@@ -1915,6 +1915,13 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     const int H = c->hidden, I = c->moe_inter, NC = 2 * T, X = L->XL;
     const int nQ = H / 128, nS = (nQ + 3) / 4, nSI = (I / 128 + 3) / 4, nSX = (X / 128 + 3) / 4;
     int rc;
+    if (L->nslot || L->cache_only) {
+        // such a call reads the selection back to the host and synchronises, which a
+        // stream under capture cannot do: refused before anything is enqueued
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &cs) != hipSuccess) return K3X_E_HIP;
+        if (cs != hipStreamCaptureStatusNone) return K3X_E_ARG;
+    }
 
     K1Args a1;
     a1.router = L->router; a1.bias = L->bias; a1.x = x; a1.x_bf16 = (x_dtype == K3X_BF16);
@@ -1988,7 +1995,8 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     if (L->nslot || L->cache_only) {
         // expert cache or cache-only routing: the selection alone first (workgroup 0 of
         // k2 on a grid of one, or k1_zdown's in the latent form), then the host's part:
-        // the draft filter, and the experts it names made resident
+        // the draft filter, and the experts it names made resident (refused under
+        // capture, before the first launch)
         if (!L->lat) {
             k2_launch(false, dim3(1));
             if ((rc = launch_ok())) return rc;

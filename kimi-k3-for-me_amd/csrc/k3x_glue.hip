@@ -1,5 +1,6 @@
 // k3x_glue.hip - the decoder layer's glue around the MoE block: the block attention-
-// residual aggregation (k3_attn_res, k3_ops.c:1722-1753) and a float row copy.
+// residual aggregation (k3_attn_res, k3_ops.c:1722-1753, with a block count per call or
+// per row as k3_decoder_layer_core takes them, :2481-2493) and a float row copy.
 #include "k3x_device.h"
 
 #define AR_NT 256
@@ -24,19 +25,30 @@ __device__ __forceinline__ double ar_sum(double v, double *red)
     return tot;
 }
 
-// One workgroup per row t: the sources are blocks[t][0 .. nb-1] then pref[t].  Each
-// source's key is its RMS-normalised row (inv rounded to float, v*inv in float) dotted
-// with fold in double; softmax with exp evaluated in double and rounded to float (the
-// reference's expf), the double sum z; p = (float)(e/z); h = sum_s p_s v_s in float, in
-// source order from 0 (the raw rows are the values).
+// One workgroup per row t: the sources are blocks[t][0 .. nb-1] then pref[t], nb = row
+// t's block count: nbv[t * nbs] when nbv is given (device memory; nbs 0 for one count
+// shared by every row, 1 for a count per row: K3_NB(t), k3_ops.c:2481-2483, 2493), else
+// nb0.  Each source's key is its RMS-normalised row (inv rounded to float, v*inv in
+// float) dotted with fold in double; softmax with exp evaluated in double and rounded to
+// float (the reference's expf), the double sum z; p = (float)(e/z); h = sum_s p_s v_s in
+// float, in source order from 0 (the raw rows are the values).  A device count outside
+// 0 .. min(maxb, AR_MAXSRC - 1) (or above 0 without blocks) fills row t with quiet NaNs
+// instead: the reference reads past its stack there.
 __global__ void __launch_bounds__(AR_NT) attn_res_kernel(float *h, const float *blocks, int maxb,
-                                                         int nb, const float *pref,
+                                                         int nb0, const int *nbv, int nbs,
+                                                         const float *pref,
                                                          const float *fold, int n, float eps)
 {
     __shared__ double red[AR_NT / WAVE];
     __shared__ float p[AR_MAXSRC];
     __shared__ float sc[AR_MAXSRC];
-    const int t = blockIdx.x, nsrc = nb + 1;
+    const int t = blockIdx.x;
+    const int nb = nbv ? nbv[(size_t)t * nbs] : nb0;
+    if (nb < 0 || nb > maxb || nb + 1 > AR_MAXSRC || (nb > 0 && !blocks)) {
+        for (int i = threadIdx.x; i < n; i += AR_NT) h[(size_t)t * n + i] = __int_as_float(0x7FC00000);
+        return;
+    }
+    const int nsrc = nb + 1;
     for (int s = 0; s < nsrc; s++) {
         const float *v = ar_src(blocks, maxb, nb, pref, n, t, s);
         double ss = 0.0;
@@ -73,13 +85,15 @@ __global__ void __launch_bounds__(AR_NT) copy_f32x4(float *dst, const float *src
     if (i < n4) ((f32x4 *)dst)[i] = ((const f32x4 *)src)[i];
 }
 
-extern "C" int k3x_dev_attn_res(float *h, const float *blocks, int maxb, int nb,
-                                const float *pref, const float *fold, int n, int T, float eps,
-                                void *stream)
+// nbv == NULL: the count nb for every row (checked here); else the rows' counts are read
+// on the device from nbv[t * nbs] (nb unused).
+extern "C" int k3x_dev_attn_res(float *h, const float *blocks, int maxb, int nb, const int *nbv,
+                                int nbs, const float *pref, const float *fold, int n, int T,
+                                float eps, void *stream)
 {
-    if (nb + 1 > AR_MAXSRC) return K3X_E_SHAPE;
+    if (!nbv && nb + 1 > AR_MAXSRC) return K3X_E_SHAPE;
     hipLaunchKernelGGL(attn_res_kernel, dim3(T), dim3(AR_NT), 0, (hipStream_t)stream, h, blocks,
-                       maxb, nb, pref, fold, n, eps);
+                       maxb, nb, nbv, nbs, pref, fold, n, eps);
     return hipGetLastError() == hipSuccess ? 0 : K3X_E_HIP;
 }
 

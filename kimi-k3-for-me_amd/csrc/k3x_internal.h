@@ -246,8 +246,9 @@ static inline int k3x_pf_chunk_tokens(const struct k3x_moe_layer *L)
  * (GEMV on the matrix cores) and any T (hi/lo planes into `planes`, T*in*4 bytes, then
  * the dense GEMM) */
 /* decoder-layer glue (k3x_glue.hip) */
-int k3x_dev_attn_res(float *h, const float *blocks, int maxb, int nb, const float *pref,
-                     const float *fold, int n, int T, float eps, void *stream);
+int k3x_dev_attn_res(float *h, const float *blocks, int maxb, int nb, const int *nbv, int nbs,
+                     const float *pref, const float *fold, int n, int T, float eps,
+                     void *stream);
 int k3x_dev_copy_f32(float *dst, const float *src, size_t n, void *stream);
 int k3x_dev_trunk_gemv(const uint16_t *W, int in, int out, float *y, int ldy, const void *x,
                        int x_dtype, int ldx, int T, void *stream);

@@ -995,8 +995,9 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
         return k3x_dev_decode(L, out, x, x_dtype, T, resid, idx, wt, NULL, 0.0f, stream);
     if (L->nslot || L->cache_only) {
         /* a cached layer, or cache-only routing: decode-path calls of tdec tokens (each
-         * token's result depends on its own routing only; the reference runs such calls
-         * token by token, k3_ops.c:2018) */
+         * token's routing is its own; its output bits follow the sub-call's shape, within
+         * the parity bar of any other grouping; the reference runs such calls token by
+         * token, k3_ops.c:2018) */
         const size_t es = (x_dtype == K3X_BF16) ? 2 : 4;
         const int H = L->cfg.hidden, K = L->cfg.topk;
         for (int t0 = 0; t0 < T; t0 += L->tdec) {
@@ -1064,21 +1065,50 @@ int k3x_attn_res(float *h, const float *blocks, int maxb, int nb, const float *p
     if (!h || !pref || !fold || n <= 0 || T < 0 || nb < 0 || (nb > 0 && (!blocks || maxb < nb)))
         return K3X_E_ARG;
     if (T == 0) return 0;
-    return k3x_dev_attn_res(h, blocks, maxb, nb, pref, fold, n, T, eps, stream);
+    return k3x_dev_attn_res(h, blocks, maxb, nb, NULL, 0, pref, fold, n, T, eps, stream);
+}
+
+int k3x_attn_res_v(float *h, const float *blocks, int maxb, const int *nbv, int nbs,
+                   const float *pref, const float *fold, int n, int T, float eps, void *stream)
+{
+    if (!h || !pref || !fold || !nbv || n <= 0 || T < 0 || maxb < 0 || (nbs != 0 && nbs != 1))
+        return K3X_E_ARG;
+    if (T == 0) return 0;
+    return k3x_dev_attn_res(h, blocks, maxb, 0, nbv, nbs, pref, fold, n, T, eps, stream);
+}
+
+/* The MoE half with the rows' block counts either one host value (nbv NULL) or read on
+ * the device (nbv[t * nbs]). */
+static int moe_half(k3x_moe_layer *L, float *h, float *pref, const float *blocks, int maxb,
+                    int nb, const int *nbv, int nbs, const float *fold,
+                    const float *post_norm, float eps, int T, float *hin, void *stream)
+{
+    if (!L || !post_norm || !hin || T < 0) return K3X_E_ARG;
+    if (T == 0) return 0;
+    const int H = L->cfg.hidden;
+    int rc = nbv ? k3x_attn_res_v(h, blocks, maxb, nbv, nbs, pref, fold, H, T, eps, stream)
+                 : k3x_attn_res(h, blocks, maxb, nb, pref, fold, H, T, eps, stream);
+    if (!rc) rc = k3x_rmsnorm(hin, h, post_norm, H, T, eps, stream);
+    if (!rc) rc = k3x_moe_forward(L, pref, hin, K3X_F32, T, pref, NULL, NULL, stream);
+    if (!rc) rc = k3x_dev_copy_f32(h, pref, (size_t)T * H, stream);
+    return rc;
 }
 
 int k3x_moe_half(k3x_moe_layer *L, float *h, float *pref, const float *blocks, int maxb,
                  int nb, const float *fold, const float *post_norm, float eps, int T,
                  float *hin, void *stream)
 {
-    if (!L || !post_norm || !hin || T < 0) return K3X_E_ARG;
-    if (T == 0) return 0;
-    const int H = L->cfg.hidden;
-    int rc = k3x_attn_res(h, blocks, maxb, nb, pref, fold, H, T, eps, stream);
-    if (!rc) rc = k3x_rmsnorm(hin, h, post_norm, H, T, eps, stream);
-    if (!rc) rc = k3x_moe_forward(L, pref, hin, K3X_F32, T, pref, NULL, NULL, stream);
-    if (!rc) rc = k3x_dev_copy_f32(h, pref, (size_t)T * H, stream);
-    return rc;
+    return moe_half(L, h, pref, blocks, maxb, nb, NULL, 0, fold, post_norm, eps, T, hin,
+                    stream);
+}
+
+int k3x_moe_half_v(k3x_moe_layer *L, float *h, float *pref, const float *blocks, int maxb,
+                   const int *nbv, int nbs, const float *fold, const float *post_norm,
+                   float eps, int T, float *hin, void *stream)
+{
+    if (!nbv) return K3X_E_ARG;
+    return moe_half(L, h, pref, blocks, maxb, 0, nbv, nbs, fold, post_norm, eps, T, hin,
+                    stream);
 }
 
 int k3x_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,

@@ -598,7 +598,8 @@ static int store_get(k3x_expert_src *self, int layer, int expert, k3x_expert_q *
 
 /* getmany: the experts' byte ranges handed to the kernel's read-ahead together
  * (POSIX_FADV_WILLNEED), so that the get() calls that follow find them in the page
- * cache; returns n, or -1 when a range cannot be found. */
+ * cache.  Advisory: nothing is made resident in this supplier (get() still reads), so
+ * it returns 0 experts resident, or -1 when a range cannot be found. */
 static int store_getmany(k3x_expert_src *self, int layer, const int *experts, int n)
 {
     store_src *ss = (store_src *)self;
@@ -620,7 +621,7 @@ static int store_getmany(k3x_expert_src *self, int layer, const int *experts, in
                 (void)posix_fadvise(fd, (off_t)e->t.off, (off_t)e->t.nbytes, POSIX_FADV_WILLNEED);
             }
     }
-    return n;
+    return 0;
 }
 
 int k3x_store_src_create_for(k3x_store *s, int moe_inter, int width, k3x_expert_src **out)

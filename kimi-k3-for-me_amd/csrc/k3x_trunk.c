@@ -6,14 +6,49 @@
 #include <hip/hip_runtime_api.h>
 #include <stdlib.h>
 
+#define TRUNK_RETIRED 16   /* workspaces outgrown, kept until destroy */
+
 struct k3x_trunk {
     int       device, in, out;
     uint16_t *w;              /* tiled bf16 [out][in]                        */
     uint16_t *planes;         /* workspace for T > K3X_DECODE_MAX_T           */
     size_t    planes_bytes;
+    uint16_t *retired[TRUNK_RETIRED];   /* earlier workspaces: a graph recorded over
+                                           one of them still reads it            */
+    int       nretired;
     float    *hx, *hy;        /* device staging of the host-pointer form      */
     size_t    hcap;           /* floats of each                               */
 };
+
+/* The workspace for `need` bytes: grown (at least doubled, so few generations exist)
+ * outside capture only; the outgrown one is retired, not freed, since a graph captured
+ * over it may replay later. */
+static int trunk_workspace(k3x_trunk *t, size_t need, void *stream)
+{
+    if (need <= t->planes_bytes) return 0;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) return K3X_E_HIP;
+    if (cs != hipStreamCaptureStatusNone) return K3X_E_SHAPE;
+    if (t->planes && t->nretired == TRUNK_RETIRED) return K3X_E_NOMEM;
+    if (need < 2 * t->planes_bytes) need = 2 * t->planes_bytes;
+    if (need > ((size_t)1 << 31)) need = (size_t)1 << 31;
+    if (hipSetDevice(t->device) != hipSuccess) return K3X_E_HIP;
+    uint16_t *p = NULL;
+    if (hipMalloc((void **)&p, need) != hipSuccess) return K3X_E_NOMEM;
+    if (t->planes) t->retired[t->nretired++] = t->planes;
+    t->planes = p;
+    t->planes_bytes = need;
+    return 0;
+}
+
+int k3x_trunk_reserve(k3x_trunk *t, int max_T)
+{
+    if (!t || max_T < 0) return K3X_E_ARG;
+    if (max_T <= K3X_DECODE_MAX_T) return 0;
+    const size_t need = (size_t)max_T * t->in * 4;
+    if (need > ((size_t)1 << 31)) return K3X_E_SHAPE;      /* 32-bit buffer offsets */
+    return trunk_workspace(t, need, NULL);
+}
 
 int k3x_trunk_create(const uint16_t *W, int in, int out, int device, k3x_trunk **t)
 {
@@ -51,6 +86,7 @@ void k3x_trunk_destroy(k3x_trunk *t)
     hipDeviceSynchronize();
     if (t->w) hipFree(t->w);
     if (t->planes) hipFree(t->planes);
+    for (int i = 0; i < t->nretired; i++) hipFree(t->retired[i]);
     if (t->hx) hipFree(t->hx);
     if (t->hy) hipFree(t->hy);
     free(t);
@@ -67,15 +103,8 @@ int k3x_trunk_apply(k3x_trunk *t, float *Y, int ldy, const void *X, int x_dtype,
         return k3x_dev_trunk_gemv(t->w, t->in, t->out, Y, ldy, X, x_dtype, ldx, T, stream);
     const size_t need = (size_t)T * t->in * 4;
     if (need > ((size_t)1 << 31)) return K3X_E_SHAPE;      /* 32-bit buffer offsets */
-    if (need > t->planes_bytes) {
-        if (hipSetDevice(t->device) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
-            return K3X_E_HIP;
-        if (t->planes) hipFree(t->planes);
-        t->planes = NULL;
-        t->planes_bytes = 0;
-        if (hipMalloc((void **)&t->planes, need) != hipSuccess) return K3X_E_NOMEM;
-        t->planes_bytes = need;
-    }
+    const int rc = trunk_workspace(t, need, stream);
+    if (rc) return rc;
     return k3x_dev_trunk_gemm(t->w, t->in, t->out, Y, ldy, X, x_dtype, ldx, T, t->planes,
                               stream);
 }

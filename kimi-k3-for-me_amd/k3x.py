@@ -35,7 +35,8 @@ EXPORTS = [
     "k3x_synth_normal_f32", "k3x_synth_normal_bf16", "k3x_moe_layer_set_timing",
     "k3x_moe_layer_last_ms", "k3x_stack_create", "k3x_stack_forward", "k3x_stack_destroy",
     "k3x_moe_layer_check", "k3x_moe_layer_set_route_wait",
-    "k3x_attn_res", "k3x_moe_half", "k3x_moe_layer_reserve", "k3x_moe_layer_dequant",
+    "k3x_attn_res", "k3x_moe_half", "k3x_attn_res_v", "k3x_moe_half_v",
+    "k3x_moe_layer_reserve", "k3x_moe_layer_dequant",
     "k3x_moe_prefill_noalloc", "k3x_moe_layer_trace", "k3x_moe_layer_set_prefill_mode",
     # include/k3x_store.h
     "k3x_store_open", "k3x_store_close", "k3x_store_count", "k3x_store_shards",
@@ -49,6 +50,7 @@ EXPORTS = [
     "k3x_moe_layer_create_cached_src", "k3x_cache_slots_fit",
     # include/k3x_trunk.h
     "k3x_trunk_create", "k3x_trunk_destroy", "k3x_trunk_apply", "k3x_trunk_apply_host",
+    "k3x_trunk_reserve",
 ]
 
 DT_U8, DT_BF16, DT_F16, DT_F32 = 1, 2, 3, 4
@@ -190,11 +192,14 @@ def lib():
         L.k3x_cache_slots_fit.argtypes = [C.POINTER(Cfg), i, C.c_double]
         L.k3x_attn_res.argtypes = [vp, vp, i, i, vp, vp, i, i, f, vp]
         L.k3x_moe_half.argtypes = [vp, vp, vp, vp, i, i, vp, vp, f, i, vp, vp]
+        L.k3x_attn_res_v.argtypes = [vp, vp, i, vp, i, vp, vp, i, i, f, vp]
+        L.k3x_moe_half_v.argtypes = [vp, vp, vp, vp, i, vp, i, vp, vp, f, i, vp, vp]
         L.k3x_trunk_create.argtypes = [vp, i, i, i, C.POINTER(vp)]
         L.k3x_trunk_destroy.argtypes = [vp]
         L.k3x_trunk_destroy.restype = None
         L.k3x_trunk_apply.argtypes = [vp, vp, i, vp, i, i, i, vp]
         L.k3x_trunk_apply_host.argtypes = [vp, vp, vp, i]
+        L.k3x_trunk_reserve.argtypes = [vp, i]
         _lib = L
     return _lib
 
@@ -225,6 +230,13 @@ def attn_res(h, blocks, maxb, nb, pref, fold, n, T, eps=1e-5, stream=0):
     """Block attention-residual aggregation on device pointers (k3x_attn_res)."""
     _check(lib().k3x_attn_res(h, blocks or None, maxb, nb, pref, fold, n, T, eps,
                               stream or None), "k3x_attn_res")
+
+
+def attn_res_v(h, blocks, maxb, nbv, nbs, pref, fold, n, T, eps=1e-5, stream=0):
+    """The same with row t's block count nbv[t * nbs] read on the device (nbv a device
+    int32 pointer; k3x_attn_res_v)."""
+    _check(lib().k3x_attn_res_v(h, blocks or None, maxb, nbv, nbs, pref, fold, n, T, eps,
+                                stream or None), "k3x_attn_res_v")
 
 
 def make_cfg(hidden, n_experts, topk, moe_inter, n_shared=1, moe_renorm=1, routed_scale=2.5,
@@ -472,6 +484,13 @@ class MoELayer:
         _check(lib().k3x_moe_half(self.h, h, pref, blocks or None, maxb, nb, fold, post_norm,
                                   eps, T, hin, stream or None), "k3x_moe_half")
 
+    def moe_half_v(self, h, pref, blocks, maxb, nbv, nbs, fold, post_norm, eps, T, hin,
+                   stream=0):
+        """The MoE half with row t's block count nbv[t * nbs] read on the device
+        (k3x_moe_half_v)."""
+        _check(lib().k3x_moe_half_v(self.h, h, pref, blocks or None, maxb, nbv, nbs, fold,
+                                    post_norm, eps, T, hin, stream or None), "k3x_moe_half_v")
+
     def check(self):
         """Raise if a decode call since the last check had a workgroup give up waiting for
         the published selection (K3X_E_WAIT)."""
@@ -625,6 +644,10 @@ class Trunk:
         if self.h:
             lib().k3x_trunk_destroy(self.h)
             self.h = C.c_void_p()
+
+    def reserve(self, max_T):
+        """Grow the workspace for calls of up to max_T rows (before a graph capture)."""
+        _check(lib().k3x_trunk_reserve(self.h, max_T), "k3x_trunk_reserve")
 
     def apply(self, y, ldy, x, x_dtype, ldx, T, stream=0):
         """Device pointers: Y[t*ldy + o] = W[o] . X[t*ldx] for t < T."""

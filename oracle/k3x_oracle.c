@@ -20,6 +20,11 @@
  *   ko_rmsnorm                        rmsnorm.json.
  *   ko_attn_res                       attnres.json; bitwise against oracle/_ref's
  *                                     k3_attn_res; one source returns it unchanged.
+ *   ko_moe_half / ko_moe_half_v       bitwise against the reference's k3_attn_res,
+ *                                     k3_rmsnorm and k3_moe_prefill composed as the
+ *                                     decoder layer's MLP half (oracle/ref_driver.c,
+ *                                     refdrv_moe_half_v) with per-row block counts; with
+ *                                     no block residual, one ko_stack_step.
  *   ko_moe / ko_moe_prefill           bitwise against the reference's k3_moe /
  *                                     k3_moe_prefill (oracle/_ref) on the same layer,
  *                                     expressed with identity latent projections.
@@ -570,6 +575,40 @@ void ko_attn_res(float *out, const float *src, const float *fold, int nsrc, int 
         for (int i = 0; i < n; i++) out[i] += p * v[i];
     }
     free(score);
+}
+
+/* k3_decoder_layer_core's MLP half, k3_ops.c:2546-2589: row t's count is nbv[t * nbs]
+ * (K3_NB, :2493), its sources gathered as :2548-2557. */
+long ko_moe_half_v(float *h, float *pref, const float *blocks, int maxb, const int *nbv,
+                   int nbs, const float *fold, const float *post_norm, float eps, int T,
+                   const ko_cfg *c, const ko_weights *w)
+{
+    const int H = c->hidden, K = c->topk;
+    int nbmax = 0;
+    for (int t = 0; t < T; t++) {
+        const int nb = nbv[(size_t)t * nbs];
+        if (nb < 0 || nb > maxb) abort();
+        nbmax = nb > nbmax ? nb : nbmax;
+    }
+    float *src = (float *)malloc((size_t)(nbmax + 1) * H * sizeof(float));
+    float *hin = (float *)malloc((size_t)T * H * sizeof(float));
+    float *tmp = (float *)malloc((size_t)T * H * sizeof(float));
+    int *idx = (int *)malloc((size_t)T * K * sizeof(int));
+    float *wt = (float *)malloc((size_t)T * K * sizeof(float));
+    if (!src || !hin || !tmp || !idx || !wt) abort();
+    for (int t = 0; t < T; t++) {
+        const int nb = nbv[(size_t)t * nbs];
+        for (int b = 0; b < nb; b++)
+            memcpy(src + (size_t)b * H, blocks + ((size_t)t * maxb + b) * H, (size_t)H * sizeof(float));
+        memcpy(src + (size_t)nb * H, pref + (size_t)t * H, (size_t)H * sizeof(float));
+        ko_attn_res(h + (size_t)t * H, src, fold, nb + 1, H, eps);
+        ko_rmsnorm(hin + (size_t)t * H, h + (size_t)t * H, post_norm, H, eps);
+    }
+    const long drops = ko_moe(tmp, hin, T, c, w, idx, wt);
+    for (size_t i = 0; i < (size_t)T * H; i++) pref[i] += tmp[i];
+    memcpy(h, pref, (size_t)T * H * sizeof(float));
+    free(src); free(hin); free(tmp); free(idx); free(wt);
+    return drops;
 }
 
 long ko_moe_half(float *h, float *pref, const float *blocks, int maxb, int nb,

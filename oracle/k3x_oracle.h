@@ -109,6 +109,11 @@ void ko_attn_res(float *out, const float *src, const float *fold, int nsrc, int 
 long ko_moe_half(float *h, float *pref, const float *blocks, int maxb, int nb,
                  const float *fold, const float *post_norm, float eps, int T,
                  const ko_cfg *c, const ko_weights *w);
+/* The same with row t's block count nbv[t * nbs] (nbs 0: one shared count, 1: one per
+ * row; k3_ops.c:2481-2493), as the speculative caller passes them (:2606-2613). */
+long ko_moe_half_v(float *h, float *pref, const float *blocks, int maxb, const int *nbv,
+                   int nbs, const float *fold, const float *post_norm, float eps, int T,
+                   const ko_cfg *c, const ko_weights *w);
 
 /* ---- synthetic inputs ---------------------------------------------------------- */
 /* The counter-based generator shared by the tests and the product's synthetic-layer

@@ -183,6 +183,57 @@ long refdrv_moe_cfg(float *out, const float *x, int T, const drv_cfg *dc, const 
     return dd;
 }
 
+/* The decoder layer's MLP half (k3_decoder_layer_core, k3_ops.c:2546-2589) with the
+ * reference's own k3_attn_res, k3_rmsnorm and k3_moe_prefill, for rows whose block counts
+ * are nbv[t * nbs] (K3_NB, :2493): per row the sources are its nb block residuals then
+ * pref (:2548-2557), h = AttnRes of them; hin = RMSNorm(h; post_norm); tmp = MoE(hin);
+ * pref += tmp; h = pref.  The layer as refdrv_moe_cfg takes it; dc->latent == 0 is the
+ * K2 form, expressed as refdrv_moe does (identity bf16 projections at the hidden width,
+ * 2^64 betas, no latent norm).  Returns the change in k3_expert_drops. */
+long refdrv_moe_half_v(float *h, float *pref, const float *blocks, int maxb, const int *nbv,
+                       int nbs, const float *fold, const float *post_norm, float eps, int T,
+                       const drv_cfg *dc, const float *gate, const float *bias,
+                       const drv_expert *bank, const void *down, const void *up,
+                       const float *lnorm, const void *sh1, const void *sh3, const void *sh2)
+{
+    const int E = dc->hidden;
+    drv_cfg kc = *dc;
+    uint16_t *eye = NULL;
+    if (dc->latent == 0) {
+        eye = identity_bf16(E);
+        if (!eye) return -1000000;
+        kc.latent = E;
+        kc.latent_norm = 0;
+        kc.situ_b1 = kc.situ_b2 = 0x1p64f;
+        down = up = eye;
+        lnorm = NULL;
+    }
+    int nbmax = 0;
+    for (int t = 0; t < T; t++) nbmax = nbv[(size_t)t * nbs] > nbmax ? nbv[(size_t)t * nbs] : nbmax;
+    float *src = (float *)malloc((size_t)(nbmax + 1) * E * sizeof(float));
+    float *hin = (float *)malloc((size_t)T * E * sizeof(float));
+    float *tmp = (float *)malloc((size_t)T * E * sizeof(float));
+    if (!src || !hin || !tmp) { free(eye); free(src); free(hin); free(tmp); return -1000000; }
+    for (int t = 0; t < T; t++) {
+        const int nb = nbv[(size_t)t * nbs];
+        for (int b = 0; b < nb; b++)
+            memcpy(src + (size_t)b * E, blocks + ((size_t)t * maxb + b) * E,
+                   (size_t)E * sizeof(float));
+        memcpy(src + (size_t)nb * E, pref + (size_t)t * E, (size_t)E * sizeof(float));
+        k3_attn_res(h + (size_t)t * E, src, fold, nb + 1, E, eps);
+    }
+    for (int t = 0; t < T; t++)
+        k3_rmsnorm(hin + (size_t)t * E, h + (size_t)t * E, post_norm, E, eps);
+    int idx[K3_MAX_TOPK];
+    float wt[K3_MAX_TOPK];
+    const long dd = refdrv_moe_cfg(tmp, hin, T, &kc, gate, bias, bank, NULL, down, up, lnorm,
+                                   sh1, sh3, sh2, 0, 1, idx, wt, NULL);
+    for (size_t i = 0; i < (size_t)T * E; i++) pref[i] += tmp[i];
+    memcpy(h, pref, (size_t)T * E * sizeof(float));
+    free(eye); free(src); free(hin); free(tmp);
+    return dd;
+}
+
 /* One K2-class layer over T tokens with the reference's own kernels and nothing else:
  * k3_router, then per selected expert 3 x k3_matmul_mxfp4 + k3_situ_glu and the float
  * combine in top-k order (k3_ops.c:1879-1942), then the shared expert with

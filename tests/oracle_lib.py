@@ -111,6 +111,10 @@ def oracle():
         lib.ko_moe_half.restype = C.c_long
         lib.ko_moe_half.argtypes = [F32P, F32P, F32P, C.c_int, C.c_int, F32P, F32P, C.c_float,
                                     C.c_int, C.POINTER(KoCfg), C.POINTER(KoWeights)]
+        lib.ko_moe_half_v.restype = C.c_long
+        lib.ko_moe_half_v.argtypes = [F32P, F32P, F32P, C.c_int, I32P, C.c_int, F32P, F32P,
+                                      C.c_float, C.c_int, C.POINTER(KoCfg),
+                                      C.POINTER(KoWeights)]
         lib.ko_stack_step.restype = C.c_long
         lib.ko_stack_step.argtypes = [F32P, C.c_int, C.c_int, C.POINTER(KoCfg),
                                       C.POINTER(C.POINTER(KoWeights)),
@@ -183,6 +187,11 @@ def ref(isa="x86-64-v3"):
                                        F32P, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
                                        C.c_int, I32P, F32P, C.POINTER(C.c_long)]
         lib.k3_attn_res.argtypes = [F32P, F32P, F32P, C.c_int, C.c_int, C.c_float]
+        lib.refdrv_moe_half_v.restype = C.c_long
+        lib.refdrv_moe_half_v.argtypes = [F32P, F32P, F32P, C.c_int, I32P, C.c_int, F32P,
+                                          F32P, C.c_float, C.c_int, C.POINTER(DrvCfg), F32P,
+                                          F32P, C.POINTER(KoExpert), C.c_void_p, C.c_void_p,
+                                          F32P, C.c_void_p, C.c_void_p, C.c_void_p]
         lib.refdrv_k2_tokens.restype = C.c_long
         lib.refdrv_k2_tokens.argtypes = [F32P, F32P, C.c_int, C.c_int, C.c_int, C.c_int,
                                          C.c_int, C.c_int, C.c_float, C.c_int, F32P, F32P,

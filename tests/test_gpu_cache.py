@@ -190,3 +190,32 @@ def test_cached_layer_over_a_supplier(torch, k3x):
     assert np.array_equal(oc.view(np.uint32), of.view(np.uint32))
     assert k3x.cache_slots_fit(cfg) > 0
     c.close(); full.close()
+
+
+def test_cache_only_forward_refuses_capture(torch, k3x):
+    """A decode call that must read the selection back to the host (cache-only routing,
+    or an expert cache) returns K3X_E_ARG on a stream under capture, enqueuing nothing;
+    the layer then runs eagerly as before."""
+    say("case: cache-only decode call under graph capture is refused")
+    L = synth.tiny(seed=44)
+    res = (np.random.default_rng(5).random(L.E) < 0.5).astype(np.int32)
+    layer = bank_layer(k3x, L)
+    layer.set_cache_only(True, res)
+    x = L.x(2, bf16=False, stream_sub=8)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty_like(xd)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    err = None
+    with torch.cuda.graph(g, stream=s):
+        try:
+            layer.forward(out.data_ptr(), xd.data_ptr(), 2, k3x.K3X_F32, 0, 0, 0, s.cuda_stream)
+        except k3x.K3XError as e:
+            err = e
+    torch.cuda.synchronize()
+    assert err is not None and err.status == -1, err            # K3X_E_ARG
+    got, idx, wt = dev_forward(torch, k3x, layer, x)
+    o, oi, ow = L.oracle_moe_cache_only(x, res)
+    assert np.array_equal(idx, oi) and synth.rel_l2(got, o) < TOL
+    layer.close()

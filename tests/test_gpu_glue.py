@@ -134,3 +134,141 @@ def test_moe_half_graph_replays(torch, k3x):
         assert torch.equal(got_h, h) and torch.equal(got_p, pd)
     layer.check()
     layer.close()
+
+
+def oracle_half_v(L, pref, blocks, nbv, nbs, fold, post, eps=1e-5):
+    from oracle_lib import I32P
+    cfg = L.ko_cfg()
+    w, cb, keep = L._weights()
+    T = pref.shape[0]
+    h = np.zeros_like(pref); p = pref.copy()
+    b = np.ascontiguousarray(blocks, np.float32)
+    nbv = np.ascontiguousarray(nbv, np.int32)
+    oracle().ko_moe_half_v(ptr(h, F32P), ptr(p, F32P), ptr(b, F32P), b.shape[1], ptr(nbv, I32P),
+                           nbs, ptr(fold, F32P), ptr(post, F32P), eps, T, C.byref(cfg),
+                           C.byref(w))
+    return h, p
+
+
+def test_attn_res_v_per_row_counts(torch, k3x):
+    """Block counts read per row from a device array (k3_ops.c:2481-2493, nbs 1): each row
+    against the oracle with its own count; a count past maxb gives a NaN row; nbs 0 is
+    one count for every row."""
+    n, T, maxb = 7168, 6, 5
+    say(f"case: attn_res_v n={n}, {T} rows, per-row counts")
+    rng = np.random.default_rng(11)
+    blocks = (rng.standard_normal((T, maxb, n)) * rng.uniform(0.2, 5, (T, maxb, 1))).astype(np.float32)
+    pref = rng.standard_normal((T, n)).astype(np.float32)
+    fold = (rng.standard_normal(n) * 0.05).astype(np.float32)
+    bd, pd, fd = (torch.from_numpy(a).cuda() for a in (blocks, pref, fold))
+    hd = torch.empty_like(pd)
+    st = torch.cuda.current_stream().cuda_stream
+    counts = [3, 0, 5, 1, 4, 2]
+    nbd = torch.tensor(counts, dtype=torch.int32, device="cuda")
+    k3x.attn_res_v(hd.data_ptr(), bd.data_ptr(), maxb, nbd.data_ptr(), 1, pd.data_ptr(),
+                   fd.data_ptr(), n, T, 1e-5, st)
+    torch.cuda.synchronize()
+    got = hd.cpu().numpy()
+    for t, nb in enumerate(counts):
+        want = oracle_attn_res(blocks[t:t + 1], nb, pref[t:t + 1], fold, 1e-5)[0]
+        err = synth.rel_l2(got[t], want)
+        say(f"  row {t} nb={nb}: rel_l2={err:.3e}")
+        assert err < 1e-6
+    # one shared count (nbs 0) equals the host-count entry point bit for bit
+    k3x.attn_res_v(hd.data_ptr(), bd.data_ptr(), maxb, nbd.data_ptr() + 4 * 4, 0, pd.data_ptr(),
+                   fd.data_ptr(), n, T, 1e-5, st)
+    h2 = torch.empty_like(pd)
+    k3x.attn_res(h2.data_ptr(), bd.data_ptr(), maxb, 4, pd.data_ptr(), fd.data_ptr(), n, T, 1e-5, st)
+    torch.cuda.synchronize()
+    assert torch.equal(hd, h2)
+    # a count past maxb: that row is NaN, the others are computed
+    bad = torch.tensor([1, maxb + 1, 2, -1, 0, 3], dtype=torch.int32, device="cuda")
+    k3x.attn_res_v(hd.data_ptr(), bd.data_ptr(), maxb, bad.data_ptr(), 1, pd.data_ptr(),
+                   fd.data_ptr(), n, T, 1e-5, st)
+    torch.cuda.synchronize()
+    g = hd.cpu().numpy()
+    assert np.isnan(g[1]).all() and np.isnan(g[3]).all()
+    assert np.isfinite(g[[0, 2, 4, 5]]).all()
+
+
+@pytest.mark.parametrize("latent,T", [(False, 5), (True, 3), (False, 12)])
+def test_moe_half_v_vs_oracle(torch, k3x, latent, T):
+    """The MoE half with a block count per row, against ko_moe_half_v (itself bitwise the
+    reference's functions composed as the decoder layer's MLP half)."""
+    say(f"case: MoE half with per-row counts, latent={latent}, T={T}")
+    L = synth.tiny_latent(seed=35) if latent else synth.tiny(seed=35)
+    layer = bank_layer(k3x, L)
+    maxb = 4
+    counts = [(3 * t + 1) % (maxb + 1) for t in range(T)]
+    blocks, pref, fold, post = half_inputs(L, T, maxb, 21 + T)
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).cuda() for k, v in
+         (("b", blocks), ("p", pref), ("f", fold), ("n", post))}
+    nbd = torch.tensor(counts, dtype=torch.int32, device="cuda")
+    h = torch.empty_like(d["p"]); hin = torch.empty_like(d["p"])
+    layer.moe_half_v(h.data_ptr(), d["p"].data_ptr(), d["b"].data_ptr(), maxb, nbd.data_ptr(), 1,
+                     d["f"].data_ptr(), d["n"].data_ptr(), 1e-5, T, hin.data_ptr(),
+                     torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    layer.check()
+    wh, wp = oracle_half_v(L, pref, blocks, counts, 1, fold, post)
+    eh, ep = synth.rel_l2(h.cpu().numpy(), wh), synth.rel_l2(d["p"].cpu().numpy(), wp)
+    say(f"  counts {counts}: rel_l2 h={eh:.3e} pref={ep:.3e}")
+    assert eh < 1e-3 and ep < 1e-3
+    assert torch.equal(h, d["p"])
+    layer.close()
+
+
+def test_moe_half_v_graph_replays(torch, k3x):
+    """The per-row form captured once; each replay runs with counts and inputs changed on
+    the device in between (the counts are read when the graph runs), and equals the eager
+    call on the same counts and inputs."""
+    say("case: MoE half with per-row counts captured in a graph, 4 replays, counts changed")
+    L = synth.tiny(seed=36)
+    layer = bank_layer(k3x, L)
+    T, maxb = 3, 3
+    H = L.H
+    bd = torch.empty((T, maxb, H), dtype=torch.float32, device="cuda")
+    pd = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    fd = torch.empty((H,), dtype=torch.float32, device="cuda")
+    nd = torch.empty((H,), dtype=torch.float32, device="cuda")
+    nbd = torch.zeros((T,), dtype=torch.int32, device="cuda")
+    h = torch.empty_like(pd); hin = torch.empty_like(pd)
+    s = torch.cuda.Stream()
+
+    def load(seed, counts):
+        blocks, pref, fold, post = half_inputs(L, T, maxb, seed)
+        bd.copy_(torch.from_numpy(blocks)); pd.copy_(torch.from_numpy(pref))
+        fd.copy_(torch.from_numpy(fold)); nd.copy_(torch.from_numpy(post))
+        nbd.copy_(torch.tensor(counts, dtype=torch.int32))
+        return blocks, pref, fold, post
+
+    def run(stream):
+        layer.moe_half_v(h.data_ptr(), pd.data_ptr(), bd.data_ptr(), maxb, nbd.data_ptr(), 1,
+                         fd.data_ptr(), nd.data_ptr(), 1e-5, T, hin.data_ptr(), stream)
+
+    load(300, [1, 2, 0])
+    with torch.cuda.stream(s):
+        run(s.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run(s.cuda_stream)
+    torch.cuda.synchronize()
+    for r, counts in enumerate(([0, 3, 1], [2, 2, 2], [3, 0, 2], [1, 1, 3])):
+        blocks, pref, fold, post = load(400 + r, counts)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got_h, got_p = h.clone(), pd.clone()
+        load(400 + r, counts)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            run(s.cuda_stream)
+        torch.cuda.synchronize()
+        wh, _ = oracle_half_v(L, pref, blocks, counts, 1, fold, post)
+        err = synth.rel_l2(got_h.cpu().numpy(), wh)
+        say(f"  replay {r} counts {counts}: rel_l2 vs oracle {err:.3e}")
+        assert torch.equal(got_h, h) and torch.equal(got_p, pd)
+        assert err < 1e-3
+    layer.check()
+    layer.close()

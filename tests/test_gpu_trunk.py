@@ -68,3 +68,53 @@ def test_trunk_strides_and_host_form(torch, k3x, T):
     yh = tr.apply_host(Xp[:, :inn])
     assert np.array_equal(yh, y[:, :out])
     tr.close()
+
+
+def test_trunk_graph_capture_and_growth(torch, k3x):
+    """A product of 40 rows captured after a reserve, replayed on new inputs; a larger
+    call under capture is refused (K3X_E_SHAPE) without enqueuing; an eager call that
+    outgrows the workspace afterwards leaves the captured graph valid (its workspace is
+    retired, not freed): every replay equals the eager product of the same rows."""
+    say("case: trunk GEMM captured after reserve, refused growth, replays after growth")
+    inn, out, T = 1024, 512, 40
+    rng = np.random.default_rng(77)
+    W = synth.f32_to_bf16((rng.standard_normal((out, inn)) * 0.05).astype(np.float32))
+    tr = k3x.Trunk(W)
+    tr.reserve(T)
+    xd = torch.empty((T, inn), dtype=torch.float32, device="cuda")
+    yd = torch.empty((T, out), dtype=torch.float32, device="cuda")
+    big_x = torch.zeros((4 * T, inn), dtype=torch.float32, device="cuda")
+    big_y = torch.empty((4 * T, out), dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    refused = None
+    with torch.cuda.graph(g, stream=s):
+        tr.apply(yd.data_ptr(), out, xd.data_ptr(), k3x.K3X_F32, inn, T, s.cuda_stream)
+        try:
+            tr.apply(big_y.data_ptr(), out, big_x.data_ptr(), k3x.K3X_F32, inn, 4 * T,
+                     s.cuda_stream)
+        except k3x.K3XError as e:
+            refused = e
+    torch.cuda.synchronize()
+    assert refused is not None and refused.status == -2        # K3X_E_SHAPE
+    for r in range(3):
+        X = rng.standard_normal((T, inn)).astype(np.float32)
+        xd.copy_(torch.from_numpy(X))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = yd.cpu().numpy()
+        if r == 1:
+            # outgrow the workspace eagerly between replays
+            tr.apply(big_y.data_ptr(), out, big_x.data_ptr(), k3x.K3X_F32, inn, 4 * T)
+            torch.cuda.synchronize()
+        tr.apply(yd.data_ptr(), out, xd.data_ptr(), k3x.K3X_F32, inn, T)
+        torch.cuda.synchronize()
+        say(f"  replay {r}")
+        assert np.array_equal(got, yd.cpu().numpy())
+        assert synth.rel_l2(got, oracle_rows(W, X)) < 2e-5
+    g.replay()
+    torch.cuda.synchronize()
+    assert np.array_equal(yd.cpu().numpy(), got)
+    tr.close()

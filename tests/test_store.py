@@ -121,6 +121,13 @@ def test_supplier_get(k3x, shards):
             assert got.tobytes() == d[k].tobytes(), (e, k)
     assert src.contents.get(src, 1, 7, C.byref(q)) != 0           # absent expert
     assert k3x.lib().k3x_store_src_fetches(h) == 2
+    # getmany only advises read-ahead: nothing is made resident (0), get() still reads;
+    # an absent expert is an error
+    ids = (C.c_int * 2)(0, 2)
+    assert src.contents.getmany(src, 1, ids, 2) == 0
+    assert k3x.lib().k3x_store_src_fetches(h) == 2
+    bad = (C.c_int * 1)(7)
+    assert src.contents.getmany(src, 1, bad, 1) < 0
     k3x.lib().k3x_store_src_destroy(h)
     st.close()
 

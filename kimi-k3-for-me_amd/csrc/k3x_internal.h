@@ -69,8 +69,8 @@ static inline size_t k3x_bf16_matrix_bytes(int R, int K) { return (size_t)R * K 
 /* routing summary written by the router, read by the expert kernels */
 typedef struct k3x_route {
     int   nu;                                   /* unique experts in this call        */
-    unsigned seq;                               /* call sequence (advanced by k1, never
-                                                   0 after the first call)            */
+    unsigned seq;                               /* call sequence: 1 at creation, never
+                                                   0; advanced by k1 before its use    */
     int   err;                                  /* a routed workgroup gave up waiting */
     int   pad[61];
     int   uniq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];        /* first-seen order           */

@@ -133,6 +133,12 @@ static int layer_alloc(k3x_moe_layer *L)
     if (c->latent_norm) RCCHK(dmalloc((void **)&L->lnw, (size_t)L->XL * 4, b));
     if (hipMemset(L->route, 0, sizeof(k3x_route)) != hipSuccess) return K3X_E_HIP;
     {
+        /* the call tag starts at 1: words tagged 0 (the zeroed buffers) match no call */
+        const unsigned one = 1u;
+        if (hipMemcpy(&L->route->seq, &one, sizeof one, hipMemcpyHostToDevice) != hipSuccess)
+            return K3X_E_HIP;
+    }
+    {
         const char *tr = getenv("K3X_TRACE");
         if (tr && tr[0] == '1') {
             L->tr_cap = E + L->SI / 16 + 1 + K3X_DECODE_MAX_T * K * (I / 16) +

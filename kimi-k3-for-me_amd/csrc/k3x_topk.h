@@ -60,22 +60,14 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 // Branch-free.  NaN and -inf are never taken; a round with nothing left gives index 0,
 // weight 0.  Weights are the unbiased scores, renormalised through a double sum in slot
 // order and a float reciprocal, then scaled (:1710-1716).  Results in s_idx/s_w, and
-// lane j's (slot j's) in out_e/out_w when given.
-template <int NE, int CP>
-__device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, int renorm,
-                          float routed_scale, int *s_idx, float *s_w, int lane,
-                          int *out_e = nullptr, float *out_w = nullptr)
+// lane j's (slot j's) in out_e/out_w when given.  This form takes the choices and
+// scores in registers (lane l: experts l*NE + c); wave_topk below loads them first.
+template <int NE>
+__device__ void wave_topk_vals(const float (&cv)[NE], const float (&sc)[NE], int E, int K,
+                               int renorm, float routed_scale, int *s_idx, float *s_w,
+                               int lane, int *out_e = nullptr, float *out_w = nullptr)
 {
     uint64_t pk[NE];
-    float sc[NE], cv[NE];
-#pragma unroll
-    for (int c = 0; c < NE; c++) {
-        const int e = lane * NE + c;
-        const uint32_t o = e < E ? row_off + 4u * (uint32_t)e : K3X_OOB;
-        cv[c] = bload_f32<CP>(cr, o);
-        sc[c] = bload_f32<CP>(sr, o);
-    }
-    SCHED_FENCE();      // both rows' loads in flight together: one memory round trip
 #pragma unroll
     for (int c = 0; c < NE; c++) {
         const int e = lane * NE + c;
@@ -122,6 +114,23 @@ __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, 
         s_w[lane] = wgt;
     }
     if (out_e) { *out_e = mine_e; *out_w = wgt; }
+}
+
+template <int NE, int CP>
+__device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, int renorm,
+                          float routed_scale, int *s_idx, float *s_w, int lane,
+                          int *out_e = nullptr, float *out_w = nullptr)
+{
+    float sc[NE], cv[NE];
+#pragma unroll
+    for (int c = 0; c < NE; c++) {
+        const int e = lane * NE + c;
+        const uint32_t o = e < E ? row_off + 4u * (uint32_t)e : K3X_OOB;
+        cv[c] = bload_f32<CP>(cr, o);
+        sc[c] = bload_f32<CP>(sr, o);
+    }
+    SCHED_FENCE();      // both rows' loads in flight together: one memory round trip
+    wave_topk_vals<NE>(cv, sc, E, K, renorm, routed_scale, s_idx, s_w, lane, out_e, out_w);
 }
 
 // wave_topk for N tokens of one wave together (tokens past ntok load nothing and store

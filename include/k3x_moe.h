@@ -336,9 +336,9 @@ void k3x_stack_destroy(k3x_stack *S);
  * No counterpart in the reference (its CPU path has no cross-workgroup wait). */
 int  k3x_moe_layer_check(k3x_moe_layer *L);
 /* Failure injection for tests of the check above: sets the decode wait's bound (ticks of
- * the 100 MHz clock; the default is 5,000,000 = 50 ms) and, with publish = 0, withholds
+ * the 100 MHz clock; the default is 100,000,000 = 1 s) and, with publish = 0, withholds
  * the flag, so that every routed workgroup gives up after `ticks` and leaves.  Calls made
- * so are not valid; restore with (5000000, 1).  No counterpart in the reference. */
+ * so are not valid; restore with (100000000, 1).  No counterpart in the reference. */
 int  k3x_moe_layer_set_route_wait(k3x_moe_layer *L, unsigned long long ticks, int publish);
 int  k3x_moe_layer_set_timing(k3x_moe_layer *L, int on);
 /* Diagnostics (a layer created with K3X_TRACE=1 in the environment): per workgroup of
@@ -348,6 +348,17 @@ int  k3x_moe_layer_set_timing(k3x_moe_layer *L, int on);
  * Returns the number of workgroups copied (0 without the trace).  No counterpart in the
  * reference. */
 int  k3x_moe_layer_trace(k3x_moe_layer *L, int kernel, unsigned long long *out, int max_wg);
+/* Diagnostics: waits for the layer's work and stores in *n how many (token, expert)
+ * router logits the last decode-path selection worked out again as the reference's
+ * single double chain (k3_ops.c:1666-1688), because the parallel sum's float logit was
+ * not proven equal to it and could change the selection or a selected weight.  No
+ * counterpart in the reference (its router is that chain). */
+int  k3x_moe_layer_exact_count(k3x_moe_layer *L, int *n);
+/* Diagnostics: waits for the layer's work and copies the routing of the last decode-path
+ * call on L (1 <= T <= 8 tokens, as that call carried; also the calls that the stacked
+ * layers make): idx and wt [T][topk], as k3x_moe_forward returns them.  For callers that
+ * do not see the selection, such as k3x_stack_forward.  No counterpart in the reference. */
+int  k3x_moe_layer_last_route(k3x_moe_layer *L, int T, int *idx, float *wt);
 int  k3x_moe_layer_last_ms(k3x_moe_layer *L, float *ms);
 
 #ifdef __cplusplus

@@ -47,13 +47,20 @@
 
 // ------------------------------------------------------------------ selection
 struct KSArgs {
-    const float   *score, *choice;
+    float         *score, *choice; // [T][E], from k1 (entries resolved below are rewritten)
+    float         *slack;          // [T][E] choice slack from k1 (0: proven the reference's)
+    unsigned      *hkey;           // [T] largest slack_key of each token's row (0: none)
     int            E, K, renorm;
     float          routed_scale;
     k3x_route     *route;          // unique experts and per-(expert, token) weights, for k2/k3
     int           *idx;  float *wt;        // internal [T][K]
     int           *uidx; float *uwt;       // optional caller copies
     int            T;
+    // the router's inputs, for the logits worked out again as the reference's chain
+    const float   *router, *bias;  // [E][H], [E]
+    const void    *x;              // [T][H] raw rows (fp32 or bf16)
+    int            x_bf16, H;
+    const float   *norm_w, *ninv;  // RMSNorm weights [H] and each row's 1/rms, or NULL
 };
 
 // Stores of the published routing: written through to the device-coherent level, since
@@ -73,14 +80,171 @@ __device__ __forceinline__ void pub_t(unsigned long long *p, unsigned seq, uint3
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// A workgroup's view of the routing, in LDS.
+// A workgroup's view of the routing, in LDS, and each wave's buffer for the products of
+// a chain (ks_chain).
+#define KS_CH 256            // elements of a chain chunk: four a lane
+#define KS_CR 2              // chain chunks in flight per wave
+#define KS_LIST 64           // experts worked out per pass of ks_resolve
 struct KSLds {
-    int   idx[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
-    float w[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
-    int   first[1024];                          // per expert: its first (token, slot) item
-    int   uq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];  // unique experts, first-seen order
-    int   wc[NT / WAVE];
+    int    idx[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
+    float  w[K3X_DECODE_MAX_T][K3X_MAX_TOPK];
+    int    first[1024];                          // per expert: its first (token, slot) item
+    int    uq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];  // unique experts, first-seen order
+    int    wc[NT / WAVE];
+    int    need[K3X_DECODE_MAX_T];               // token's selection needs ks_resolve
+    int    list[KS_LIST], nlist;                 // ks_resolve's experts of a pass
+    alignas(16) double pl[NT / WAVE][KS_CH];     // ks_chain's products
 };
+
+// The choice key (choice_key's order) just above choice + slack: an upper bound of the
+// reference's choice for an expert whose logit is not proven.
+__device__ __forceinline__ uint32_t slack_key(float choice, float slack)
+{
+    const uint32_t k = choice_key((float)((double)choice + (double)slack));
+    return (k != 0u && k < 0xFF800000u) ? k + 1u : k;
+}
+
+// Whether an expert not proven could change a selection whose K-th choice is ck, or one
+// of its weights: its choice may reach ck (hk: the token's largest slack_key, 0 = none).
+// Every selected expert's choice is at least ck, so a selected one not proven counts.
+__device__ __forceinline__ bool slack_reaches(uint32_t hk, float ck)
+{
+    return hk != 0u && hk >= choice_key(ck);
+}
+
+// The logit of (token t, expert e) as the reference computes it: one double chain
+// acc += (double)W[e][i] * (double)x[i] for i = 0 .. H-1 in order (k3_ops.c:1666-1688),
+// with x the row the router read (nw[i] * x[i] * inv for the RMSNorm of x).  The whole
+// workgroup: in step g, wave w forms the products of chunk 4g + w (KS_CH elements, four a
+// lane; exact in double, -0.0, the identity of the sum, past H) in its LDS buffer, with
+// its next chunks' loads in flight (a ring of KS_CR); then thread 0 adds the step's
+// 4 KS_CH products in order.  The value in thread 0 (every thread must call).
+__device__ double ks_chain(const KSArgs &a, KSLds &l, int t, int e)
+{
+    constexpr int NW = NT / WAVE;
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    const uint32_t H = (uint32_t)a.H, xb = a.x_bf16 ? 2u : 4u;
+    const rsrc_t rw = make_rsrc(a.router + (size_t)e * H, H * 4u);
+    const rsrc_t rx = make_rsrc((const uint8_t *)a.x + (size_t)t * H * xb, H * xb);
+    const bool nrm = a.norm_w != nullptr;
+    const rsrc_t rn = make_rsrc(nrm ? a.norm_w : a.router, nrm ? H * 4u : 0u);
+    const float inv = nrm ? a.ninv[t] : 1.0f;
+    const int steps = (int)((H + NW * KS_CH - 1) / (NW * KS_CH));
+    double *pl = l.pl[wave];
+    u32x4 w[KS_CR], nw[KS_CR];
+    u32x2 xv[KS_CR][2];
+    auto ld = [&](int i, int k) AI {
+        const uint32_t el = (uint32_t)(k * NW + wave) * KS_CH + 4u * (uint32_t)lane;
+        const bool on = k < steps;
+        w[i] = bload16(rw, on ? el * 4u : K3X_OOB);
+        // x in two 8-byte pieces (bf16: the first holds all four, the second loads
+        // nothing), so that no load reaches past the row
+        xv[i][0] = __builtin_amdgcn_raw_buffer_load_b64(rx, on ? el * xb : K3X_OOB, 0, 0);
+        xv[i][1] = __builtin_amdgcn_raw_buffer_load_b64(rx, on && xb == 4u ? el * 4u + 8u : K3X_OOB,
+                                                        0, 0);
+        nw[i] = bload16(rn, on && nrm ? el * 4u : K3X_OOB);
+    };
+    double acc = 0.0;
+    ring_prime<KS_CR>(ld);
+    ring_loop<KS_CR>(steps, ld, [&](int i, int k) AI {
+        const uint32_t el = (uint32_t)(k * NW + wave) * KS_CH + 4u * (uint32_t)lane;
+        float xf[4];
+        if (a.x_bf16) {
+            xf[0] = bf2f(xv[i][0][0] & 0xFFFFu); xf[1] = bf2f(xv[i][0][0] >> 16);
+            xf[2] = bf2f(xv[i][0][1] & 0xFFFFu); xf[3] = bf2f(xv[i][0][1] >> 16);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) xf[q] = __uint_as_float(xv[i][q >> 1][q & 1]);
+        }
+        double p[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float xq = nrm ? __uint_as_float(nw[i][q]) * xf[q] * inv : xf[q];
+            p[q] = el + q < H ? (double)__uint_as_float(w[i][q]) * (double)xq : -0.0;
+        }
+        *(f64x2 *)(pl + 4 * lane) = (f64x2){p[0], p[1]};
+        *(f64x2 *)(pl + 4 * lane + 2) = (f64x2){p[2], p[3]};
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const double *q = &l.pl[0][0];
+            double s = acc;
+#pragma unroll 4
+            for (int j = 0; j < NW * KS_CH; j += 2) {
+                const f64x2 v = *(const f64x2 *)(q + j);
+                s += v[0];
+                s += v[1];
+            }
+            acc = s;
+        }
+        __syncthreads();
+    });
+    return acc;
+}
+
+// Token t's selection where an expert whose logit is not proven may reach it
+// (slack_reaches): wave 0 selects again from the rows in memory and lists the experts
+// whose slack_key reaches the K-th choice (up to KS_LIST a pass, lowest index first); the
+// workgroup works out each one's logit as the reference's chain (ks_chain) and stores
+// its score, its choice and a slack of 0; until a pass lists none.  Each pass resolves
+// at least one expert, so the loop ends.  Then every selected expert's choice and score
+// are the reference's and every expert not proven lies below the K-th choice, as in the
+// reference: the selection and its weights are the reference's.  Every thread calls;
+// results as wave_topk's in s_idx/s_w, and in wave 0's out_e/out_w.  Returns the number
+// of logits worked out again.
+template <int NE>
+__device__ int ks_resolve(const KSArgs &a, KSLds &l, int t, int *s_idx, float *s_w,
+                          int *out_e = nullptr, float *out_w = nullptr)
+{
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    const uint32_t bytes = (uint32_t)(a.T * a.E * 4), ro = (uint32_t)(t * a.E * 4);
+    const rsrc_t cr = make_rsrc(a.choice, bytes), sr = make_rsrc(a.score, bytes);
+    const rsrc_t lr = make_rsrc(a.slack, bytes);
+    int nex = 0;
+    for (int pass = 0; pass <= a.E; pass++) {
+        __threadfence();              // the stores below reach the loads of the next pass
+        if (wave == 0) {
+            float ck;
+            wave_topk<NE, 0>(cr, sr, ro, a.E, a.K, a.renorm, a.routed_scale, s_idx, s_w, lane,
+                             out_e, out_w, &ck);
+            const uint32_t kk = choice_key(ck);
+            uint32_t crit = 0u;
+#pragma unroll
+            for (int c = 0; c < NE; c++) {
+                const int e = lane * NE + c;
+                const uint32_t o = e < a.E ? ro + 4u * (uint32_t)e : K3X_OOB;
+                const float sl = bload_f32<0>(lr, o);
+                if (sl > 0.0f && slack_key(bload_f32<0>(cr, o), sl) >= kk) crit |= 1u << c;
+            }
+            int n = 0;
+            for (; n < KS_LIST; n++) {             // lowest index first
+                const uint64_t m = __ballot(crit != 0u);
+                if (m == 0ull) break;
+                const int l0 = (int)__builtin_ctzll(m);
+                const int c = __builtin_ctz((uint32_t)__builtin_amdgcn_readlane((int)crit, l0));
+                if (lane == l0) crit &= crit - 1u;
+                if (lane == 0) l.list[n] = l0 * NE + c;
+            }
+            if (lane == 0) l.nlist = n;
+        }
+        __syncthreads();
+        const int n = l.nlist;
+        if (n == 0) break;
+        for (int i = 0; i < n; i++) {
+            const int e = l.list[i];
+            const double v = ks_chain(a, l, t, e);
+            if (threadIdx.x == 0) {
+                const float sv = sigmoid_ref((float)v);
+                const size_t o = (size_t)t * a.E + e;
+                a.score[o] = sv;
+                a.choice[o] = sv + a.bias[e];
+                a.slack[o] = 0.0f;
+            }
+        }
+        nex += n;
+        __syncthreads();              // l.nlist is read before wave 0 writes it again
+    }
+    return nex;
+}
 
 // Token t's weight for expert e: the sum of its slots' weights for e (0 where not
 // chosen; a slot repeated by a round that found nothing adds 0).
@@ -106,14 +270,25 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish, unsigned seq = 
     const rsrc_t cr = make_rsrc(a.choice, (uint32_t)(a.T * a.E * 4));
     const rsrc_t sr = make_rsrc(a.score, (uint32_t)(a.T * a.E * 4));
     if (a.T == 1) {
-        // one token, all in wave 0 and its registers: lane j holds slot j; the unique
+        // one token, selected by wave 0 in its registers: lane j holds slot j; the unique
         // experts are the slots whose expert no lower slot holds, each with the sum of
-        // its slots' weights in slot order
+        // its slots' weights in slot order.  The other waves stay for ks_resolve.
+        int ex = 0;
+        float w = 0.0f;
+        if (wave == 0) {
+            const uint32_t hk = __hip_atomic_load(&a.hkey[0], __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+            float ck;
+            wave_topk<NE, 0>(cr, sr, 0u, a.E, a.K, a.renorm, a.routed_scale, l.idx[0], l.w[0],
+                             lane, &ex, &w, &ck);
+            if (lane == 0) {
+                l.need[0] = slack_reaches(hk, ck);
+                if (hk) a.hkey[0] = 0u;      // read: cleared for the next call's router
+            }
+        }
+        __syncthreads();
+        const int nex = l.need[0] ? ks_resolve<NE>(a, l, 0, l.idx[0], l.w[0], &ex, &w) : 0;
         if (wave != 0) return 0;
-        int ex;
-        float w;
-        wave_topk<NE, 0>(cr, sr, 0u, a.E, a.K, a.renorm, a.routed_scale, l.idx[0], l.w[0],
-                         lane, &ex, &w);
         const bool on = lane < a.K;
         bool first = on;
         float wsum = 0.0f;
@@ -144,6 +319,7 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish, unsigned seq = 
             }
             if (lane == 0) {
                 pub_i(&a.route->nu, nu);
+                pub_i(&a.route->nexact, nex);
                 if (seq) pub_t(&a.route->tnu, seq, (uint32_t)nu);
             }
         }
@@ -156,11 +332,27 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish, unsigned seq = 
         const uint32_t ro[2] = {(uint32_t)(wave * a.E * 4), (uint32_t)(t1 * a.E * 4)};
         int *const si[2] = {l.idx[wave], l.idx[t1]};
         float *const sw[2] = {l.w[wave], l.w[t1]};
-        wave_topk_n<NE, 0, 2>(cr, sr, ro, wave + NW < a.T ? 2 : 1, a.E, a.K, a.renorm,
-                              a.routed_scale, si, sw, lane);
+        const int nt = wave + NW < a.T ? 2 : 1;
+        const uint32_t hk0 = __hip_atomic_load(&a.hkey[wave], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t hk1 = nt == 2 ? __hip_atomic_load(&a.hkey[t1], __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        float ck[2];
+        wave_topk_n<NE, 0, 2>(cr, sr, ro, nt, a.E, a.K, a.renorm, a.routed_scale, si, sw, lane, ck);
+        if (lane == 0) {                     // read: cleared for the next call's router
+            l.need[wave] = slack_reaches(hk0, ck[0]);
+            if (hk0) a.hkey[wave] = 0u;
+            if (nt == 2) {
+                l.need[t1] = slack_reaches(hk1, ck[1]);
+                if (hk1) a.hkey[t1] = 0u;
+            }
+        }
     }
     for (int e = threadIdx.x; e < a.E; e += NT) l.first[e] = 0x7FFFFFFF;
     __syncthreads();
+    int nex = 0;
+    for (int t = 0; t < a.T; t++)
+        if (l.need[t]) nex += ks_resolve<NE>(a, l, t, l.idx[t], l.w[t]);
     const int TK = a.T * a.K;
     for (int i = threadIdx.x; i < TK; i += NT) {
         const int t = i / a.K, j = i % a.K;
@@ -205,6 +397,7 @@ __device__ int ks_route(const KSArgs &a, KSLds &l, bool publish, unsigned seq = 
         }
         if (threadIdx.x == 0) {
             pub_i(&a.route->nu, base);
+            pub_i(&a.route->nexact, nex);
             if (seq) pub_t(&a.route->tnu, seq, (uint32_t)base);
         }
     }
@@ -219,6 +412,9 @@ struct K1Args {
     int          x_bf16;
     int          T, H, E;
     float       *score, *choice;   // [T][E]
+    float       *slack;            // [T][E] (choice_slack)
+    unsigned    *hkey;             // [T] largest slack_key of each row (atomic maximum)
+    float       *ninv;             // [T] 1/rms of each row, with norm_w
     uint16_t    *xB;               // compact B set of x over whole super-quads
     int          n_rwg;            // workgroups
     unsigned    *seq;              // the call sequence, advanced here
@@ -271,20 +467,50 @@ __device__ void k1_norm_inv(const K1Args &a, float *lds, float *s_inv)
     __syncthreads();
 }
 
+// The slack of a choice whose logit v was summed in another order than the reference's
+// single chain (k3_ops.c:1666-1688), from asum, the float sum of |W[e][i] x[i]|.  The
+// products are exact in double, so the two sums differ only by their roundings: the
+// chain's H - 1 additions and this kernel's at most H/256 + 12 per product (a thread's
+// run of products, the wave's shuffle tree, the four waves' pairs), together at most
+// d = (H + H/128 + 16) 2^-53 (1 + 2^-16) times sum |p| (Higham, Accuracy and Stability
+// of Numerical Algorithms, 2nd ed., eq. 4.4).  asum bounds sum |p| once widened by
+// (H + 64) 2^-23 (its own float roundings) plus H 2^-126 (products below float's range).
+// The reference's logit is then a double in [v - d, v + d], so its float lies in
+// [(float)(v - d), (float)(v + d)] (rounding is monotonic); where both ends round to
+// (float)v the float logit, and with it the score and the choice, are the reference's,
+// and the slack is 0.  Otherwise the slack bounds the distance of the reference's choice
+// from this one: a quarter of the float interval's half-width (the sigmoid's slope is at
+// most 1/4) plus the roundings of the sigmoid and of the bias add (a few units in the last
+// place of |choice| <= 2 + |bias|).  NaN logits give a NaN slack, which marks nothing (a
+// NaN choice is never selected, here or in the reference).
+__device__ __forceinline__ float choice_slack(double v, float asum, int H, float bias)
+{
+    const double g = ((double)H + (double)(H >> 7) + 16.0) * 0x1p-53 * (1.0 + 0x1p-16);
+    const double au = (double)asum * (1.0 + ((double)H + 64.0) * 0x1p-23) + (double)H * 0x1p-126;
+    const double d = g * au;
+    const float f = (float)v, lo = (float)(v - d), hi = (float)(v + d);
+    if (lo == f && hi == f) return 0.0f;
+    const double df = fmax((double)hi - (double)f, (double)f - (double)lo);
+    return (float)((df * 0.25 + (2.0 + fabs((double)bias)) * 0x1p-21) * 1.01);
+}
+
 // Router logits: four waves per expert, sum_i W[e][i] x[i] in double (a product of two
 // floats is exact in double; only the order of the additions differs from the
-// reference's single chain), then score = sigmoid((float)logit), choice = score + bias.
+// reference's single chain), then score = sigmoid((float)logit), choice = score + bias,
+// and the choice's slack (choice_slack; the float sum of |W[e][i] x[i]| runs beside).
 // With a.norm_w, x[i] is the normalised nw[i] * x[i] * inv (float, the reference's order);
 // the expert's weights are in flight while the norm is worked out.
+template <int TM>
 __device__ void k1_router(const K1Args &a, float *lds, float *s_inv, bool bset)
 {
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int grp = wave / RWAVES, wq = wave % RWAVES;          // expert slot, quarter
     const int e = blockIdx.x * (NT1 / WAVE / RWAVES) + grp;
     const int nf4 = a.H >> 2;
-    double acc[K3X_DECODE_MAX_T];
+    double acc[TM];
+    float aa[TM];
 #pragma unroll
-    for (int t = 0; t < K3X_DECODE_MAX_T; t++) acc[t] = 0.0;
+    for (int t = 0; t < TM; t++) { acc[t] = 0.0; aa[t] = 0.0f; }
     const float *row = a.router + (size_t)(e < a.E ? e : 0) * a.H;
     const int tl = wq * WAVE + lane;                            // 0..255 within the expert
     for (int f0 = 0; f0 < nf4; f0 += RWAVES * WAVE * RCH) {
@@ -298,6 +524,7 @@ __device__ void k1_router(const K1Args &a, float *lds, float *s_inv, bool bset)
         f32x4 nw[RCH];
         if (a.norm_w) {                         // uniform; then f0 == 0 (H <= 8192)
             k1_norm_inv(a, lds, s_inv);
+            if (blockIdx.x == 0 && threadIdx.x < a.T) a.ninv[threadIdx.x] = s_inv[threadIdx.x];
 #pragma unroll
             for (int c = 0; c < RCH; c++) {
                 const int f = tl + RWAVES * WAVE * c;
@@ -313,7 +540,7 @@ __device__ void k1_router(const K1Args &a, float *lds, float *s_inv, bool bset)
                       s_inv);
         }
 #pragma unroll
-        for (int t = 0; t < K3X_DECODE_MAX_T; t++) {
+        for (int t = 0; t < TM; t++) {
             if (t < a.T) {
                 float xv[RCH][4];
 #pragma unroll
@@ -332,28 +559,46 @@ __device__ void k1_router(const K1Args &a, float *lds, float *s_inv, bool bset)
 #pragma unroll
                 for (int c = 0; c < RCH; c++)
 #pragma unroll
-                    for (int k = 0; k < 4; k++) acc[t] += (double)w[c][k] * (double)xv[c][k];
+                    for (int k = 0; k < 4; k++) {
+                        acc[t] += (double)w[c][k] * (double)xv[c][k];
+                        aa[t] = fmaf(fabsf(w[c][k]), fabsf(xv[c][k]), aa[t]);
+                    }
             }
         }
     }
-    double *dl = (double *)lds;                                 // [16 waves][8]
+    double *dl = (double *)lds;                                 // [4 waves][8]
+    float *al = (float *)(dl + NT1 / WAVE * K3X_DECODE_MAX_T);  // [4 waves][8]
 #pragma unroll
-    for (int t = 0; t < K3X_DECODE_MAX_T; t++) {
+    for (int t = 0; t < TM; t++) {
         if (t < a.T) {
             double v = acc[t];
-            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-            if (lane == 0) dl[wave * K3X_DECODE_MAX_T + t] = v;
+            float av = aa[t];
+            for (int off = 32; off >= 1; off >>= 1) {
+                v += __shfl_xor(v, off);
+                av += __shfl_xor(av, off);
+            }
+            if (lane == 0) {
+                dl[wave * K3X_DECODE_MAX_T + t] = v;
+                al[wave * K3X_DECODE_MAX_T + t] = av;
+            }
         }
     }
     __syncthreads();
     if (wq == 0 && lane < a.T && e < a.E) {
         const int t = lane;
         const double *g = dl + grp * RWAVES * K3X_DECODE_MAX_T;
+        const float *ga = al + grp * RWAVES * K3X_DECODE_MAX_T;
         const double v = (g[t] + g[K3X_DECODE_MAX_T + t]) +
                          (g[2 * K3X_DECODE_MAX_T + t] + g[3 * K3X_DECODE_MAX_T + t]);
+        const float as = (ga[t] + ga[K3X_DECODE_MAX_T + t]) +
+                         (ga[2 * K3X_DECODE_MAX_T + t] + ga[3 * K3X_DECODE_MAX_T + t]);
         const float sc = sigmoid_ref((float)v);
-        a.score[(size_t)t * a.E + e] = sc;
-        a.choice[(size_t)t * a.E + e] = sc + a.bias[e];
+        const size_t o = (size_t)t * a.E + e;
+        const float ch = sc + a.bias[e], sl = choice_slack(v, as, a.H, a.bias[e]);
+        a.score[o] = sc;
+        a.choice[o] = ch;
+        a.slack[o] = sl;
+        if (sl > 0.0f) atomicMax(&a.hkey[t], slack_key(ch, sl));
     }
 }
 
@@ -469,7 +714,9 @@ __global__ void __launch_bounds__(NT1) k1_zdown(K1Args a)
 }
 
 // Router logits of NT1 / WAVE / RWAVES experts (of the RMSNorm of x when norm_w is given),
-// and a share of x's B set for k2.
+// and a share of x's B set for k2; TM: the most tokens a call carries (1, or
+// K3X_DECODE_MAX_T).
+template <int TM>
 __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
 {
     __shared__ float lds[(NT1 / WAVE - 1) * 8 * WAVE];
@@ -482,7 +729,7 @@ __global__ void __launch_bounds__(NT1) k1_router_bset(K1Args a)
     }
     // the B set's entries are dealt across the workgroups (a few per workgroup) and
     // converted while the router's weights are in flight
-    k1_router(a, lds, s_inv, true);
+    k1_router<TM>(a, lds, s_inv, true);
     tr.end();
 }
 
@@ -501,6 +748,7 @@ __global__ void __launch_bounds__(NT1 * RM_EPW) k1_router_mt(K1Args a)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
     __shared__ double dl[RM_EPW * RWAVES][K3X_DECODE_MAX_T];
+    __shared__ float al[RM_EPW * RWAVES][K3X_DECODE_MAX_T];
     WgTrace tr;
     tr.start(a.trace);
     if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -555,6 +803,7 @@ __global__ void __launch_bounds__(NT1 * RM_EPW) k1_router_mt(K1Args a)
 #pragma unroll 1
         for (int g = 0; g < ng; g++) {
             double v = 0.0;
+            float av = 0.0f;
 #pragma unroll
             for (int c = 0; c < RCH; c++) {
                 const int f = tl + NT1 * c;
@@ -571,10 +820,19 @@ __global__ void __launch_bounds__(NT1 * RM_EPW) k1_router_mt(K1Args a)
                     }
                 }
 #pragma unroll
-                for (int k = 0; k < 4; k++) v += (double)w[c][k] * (double)xv[k];
+                for (int k = 0; k < 4; k++) {
+                    v += (double)w[c][k] * (double)xv[k];
+                    av = fmaf(fabsf(w[c][k]), fabsf(xv[k]), av);
+                }
             }
-            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-            if (lane == 0) dl[wave][t0 + g] = v;
+            for (int off = 32; off >= 1; off >>= 1) {
+                v += __shfl_xor(v, off);
+                av += __shfl_xor(av, off);
+            }
+            if (lane == 0) {
+                dl[wave][t0 + g] = v;
+                al[wave][t0 + g] = av;
+            }
         }
     }
     __syncthreads();
@@ -582,9 +840,14 @@ __global__ void __launch_bounds__(NT1 * RM_EPW) k1_router_mt(K1Args a)
     if (wq == 0 && lane < TT && e < a.E) {
         const int t = lane, w0 = grp * RWAVES;
         const double v = (dl[w0][t] + dl[w0 + 1][t]) + (dl[w0 + 2][t] + dl[w0 + 3][t]);
+        const float as = (al[w0][t] + al[w0 + 1][t]) + (al[w0 + 2][t] + al[w0 + 3][t]);
         const float sc = sigmoid_ref((float)v);
-        a.score[(size_t)t * a.E + e] = sc;
-        a.choice[(size_t)t * a.E + e] = sc + a.bias[e];
+        const size_t o = (size_t)t * a.E + e;
+        const float ch = sc + a.bias[e], sl = choice_slack(v, as, a.H, a.bias[e]);
+        a.score[o] = sc;
+        a.choice[o] = ch;
+        a.slack[o] = sl;
+        if (sl > 0.0f) atomicMax(&a.hkey[t], slack_key(ch, sl));
     }
     tr.end();
 }
@@ -619,7 +882,8 @@ static unsigned launch_k1(const K1Args &a1, hipStream_t s)
 #undef K1MT
         return g.x;
     }
-    hipLaunchKernelGGL(k1_router_bset, dim3(a1.n_rwg), dim3(NT1), 0, s, a1);
+    if (T == 1) hipLaunchKernelGGL(k1_router_bset<1>, dim3(a1.n_rwg), dim3(NT1), 0, s, a1);
+    else hipLaunchKernelGGL(k1_router_bset<K3X_DECODE_MAX_T>, dim3(a1.n_rwg), dim3(NT1), 0, s, a1);
     return (unsigned)a1.n_rwg;
 }
 
@@ -717,9 +981,11 @@ __device__ void k2_shared(const K2Args &a, float *lds, int rt)
 // are coherent, so a word read with this call's seq holds the value workgroup 0 stored
 // in this call, and the reader needs neither a release/acquire pair nor the cache
 // invalidation of an acquire fence (measured: 1.85 us of k2 at b = 1).  The wait is
-// bounded (wait_ticks of the 100 MHz clock, by default 50 ms, far above the selection's
-// few microseconds): a workgroup that gives up sets the error word (k3x_moe_layer_check
-// reports it) and leaves without touching the expert weights.
+// bounded (wait_ticks of the 100 MHz clock, by default 1 s, far above the selection's
+// few microseconds, and above its worst case where every expert's logit of eight tokens
+// is worked out again as the reference's chain, about 20 us each): a workgroup that
+// gives up sets the error word (k3x_moe_layer_check reports it) and leaves without
+// touching the expert weights.
 
 // Gate and up products of rtw row tiles (16 rows each) of one unique expert: the waves
 // are dealt over the tiles (4/rtw waves per tile, on interleaved super-quads of it);
@@ -751,10 +1017,14 @@ __device__ void k2_gateup_body(const K2Args &a, float *lds, int *s_go_p)
 {
     int &s_go = *s_go_p;
     if (blockIdx.x == 0) {
-        if (a.sel_done) return;
-        // publish = 0 (the failure-handling test) leaves the tagged words unwritten, so
-        // that the routed workgroups' bound runs out
-        ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true, a.publish ? *a.seq : 0u);
+        // NE = 0: the launches after an earlier launch's selection (sel_done), built
+        // without the selection's code and its registers
+        if constexpr (NE > 0) {
+            if (a.sel_done) return;
+            // publish = 0 (the failure-handling test) leaves the tagged words unwritten,
+            // so that the routed workgroups' bound runs out
+            ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true, a.publish ? *a.seq : 0u);
+        }
         return;
     }
     if ((int)blockIdx.x <= a.n_sh) {
@@ -1675,6 +1945,7 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a1.router = L->router; a1.bias = L->bias; a1.x = x; a1.x_bf16 = (x_dtype == K3X_BF16);
     a1.T = T; a1.H = H; a1.E = c->n_experts;
     a1.score = L->score; a1.choice = L->choice; a1.xB = L->xB;
+    a1.slack = L->slack; a1.ninv = L->ninv; a1.hkey = L->route->hkey;
     a1.n_rwg = (c->n_experts + NT1 / WAVE / RWAVES - 1) / (NT1 / WAVE / RWAVES);
     a1.seq = &L->route->seq;
     a1.norm_w = norm_w; a1.eps = eps;
@@ -1694,6 +1965,8 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     ks.score = L->score; ks.choice = L->choice; ks.E = c->n_experts; ks.K = c->topk;
     ks.renorm = c->moe_renorm; ks.routed_scale = c->routed_scale; ks.route = L->route;
     ks.idx = L->idx; ks.wt = L->wt; ks.uidx = idx; ks.uwt = wt; ks.T = T;
+    ks.slack = L->slack; ks.hkey = L->route->hkey; ks.router = L->router; ks.bias = L->bias; ks.x = x;
+    ks.x_bf16 = a1.x_bf16; ks.H = H; ks.norm_w = norm_w; ks.ninv = L->ninv;
     if (L->lat) {
         a1.ks = ks;
         const dim3 gz(1 + X / 16);
@@ -1733,7 +2006,8 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     a2.sb = (!st2 && a2.rtw == 2) ? 1 : 0;
     if (a2.sb && l2 < (size_t)K2SB_R * K2SB_STAGE) l2 = (size_t)K2SB_R * K2SB_STAGE;
     auto k2_launch = [&](bool ex, dim3 g) {
-        if (c->n_experts <= 128)      launch_k2<2>(a2, ex, st2, g, l2, s);
+        if (a2.sel_done)              launch_k2<0>(a2, ex, st2, g, l2, s);
+        else if (c->n_experts <= 128) launch_k2<2>(a2, ex, st2, g, l2, s);
         else if (c->n_experts <= 256) launch_k2<4>(a2, ex, st2, g, l2, s);
         else if (c->n_experts <= 384) launch_k2<6>(a2, ex, st2, g, l2, s);
         else if (c->n_experts <= 512) launch_k2<8>(a2, ex, st2, g, l2, s);

@@ -53,7 +53,7 @@ extern "C" {
                                     are split into (partial aggregates, added in order) */
 #define K3X_STAGE_MAX    65536   /* bytes of activation fragments a workgroup stages in LDS */
 #define K3X_MAX_TOPK     64      /* K3_MAX_TOPK, k3.h:857-864 */
-#define K3X_ROUTE_WAIT_DEFAULT 5000000ull  /* 50 ms at 100 MHz: decode's bound on the wait */
+#define K3X_ROUTE_WAIT_DEFAULT 100000000ull  /* 1 s at 100 MHz: decode's bound on the wait */
 #define K3X_PF_CHUNK     4096    /* prefill: most tokens per pipeline run */
 #define K3X_NOALLOC_BYTES (64u << 20)  /* the no-allocation prefill's static device array */
 #define K3X_CACHE_IO     8       /* expert-cache misses read from the store concurrently */
@@ -72,7 +72,14 @@ typedef struct k3x_route {
     unsigned seq;                               /* call sequence: 1 at creation, never
                                                    0; advanced by k1 before its use    */
     int   err;                                  /* a routed workgroup gave up waiting */
-    int   pad[61];
+    int   nexact;                               /* router logits the last selection
+                                                   worked out as the reference's chain */
+    unsigned hkey[K3X_DECODE_MAX_T];            /* per token: the largest upper bound
+                                                   (as a choice key) of a choice whose
+                                                   logit is not proven; 0 = none.  Set
+                                                   by the router (atomic maximum),
+                                                   cleared by the selection that reads it */
+    int   pad[60 - K3X_DECODE_MAX_T];
     int   uniq[K3X_DECODE_MAX_T * K3X_MAX_TOPK];        /* first-seen order           */
     float wtok[K3X_DECODE_MAX_T * K3X_MAX_TOPK][K3X_DECODE_MAX_T]; /* [u][token], 0 = not chosen */
     /* the same routing as k2's routed workgroups read it inside the launch that works it
@@ -139,6 +146,10 @@ struct k3x_moe_layer {
     float    *lnw;                /* [XL] latent RMSNorm weights, or NULL */
     /* decode working buffers */
     float    *score, *choice;     /* [DECODE_MAX_T][E] */
+    float    *slack;              /* [DECODE_MAX_T][E] choice slack: 0 where the router's
+                                     float logit is proven to be the reference's chain's */
+    float    *ninv;               /* [DECODE_MAX_T] 1/rms of the rows the router normalised
+                                     (inside the slack allocation) */
     int      *idx;                /* [DECODE_MAX_T][K] */
     float    *wt;                 /* [DECODE_MAX_T][K] */
     k3x_route *route;

@@ -115,6 +115,8 @@ static int layer_alloc(k3x_moe_layer *L)
     }
     RCCHK(dmalloc((void **)&L->score, (size_t)K3X_DECODE_MAX_T * E * 4, b));
     RCCHK(dmalloc((void **)&L->choice, (size_t)K3X_DECODE_MAX_T * E * 4, b));
+    RCCHK(dmalloc((void **)&L->slack, (size_t)K3X_DECODE_MAX_T * (E + 1) * 4, b));
+    L->ninv = L->slack + (size_t)K3X_DECODE_MAX_T * E;
     RCCHK(dmalloc((void **)&L->idx, (size_t)K3X_DECODE_MAX_T * K * 4, b));
     RCCHK(dmalloc((void **)&L->wt, (size_t)K3X_DECODE_MAX_T * K * 4, b));
     RCCHK(dmalloc((void **)&L->route, sizeof(k3x_route), b));
@@ -131,7 +133,9 @@ static int layer_alloc(k3x_moe_layer *L)
         RCCHK(dmalloc((void **)&L->latB, xs * 2 * K3X_DECODE_MAX_T * 2, b));
     }
     if (c->latent_norm) RCCHK(dmalloc((void **)&L->lnw, (size_t)L->XL * 4, b));
-    if (hipMemset(L->route, 0, sizeof(k3x_route)) != hipSuccess) return K3X_E_HIP;
+    if (hipMemset(L->route, 0, sizeof(k3x_route)) != hipSuccess ||
+        hipMemset(L->slack, 0, (size_t)K3X_DECODE_MAX_T * (E + 1) * 4) != hipSuccess)
+        return K3X_E_HIP;
     {
         /* the call tag starts at 1: words tagged 0 (the zeroed buffers) match no call */
         const unsigned one = 1u;
@@ -160,7 +164,7 @@ static void layer_free(k3x_moe_layer *L)
 {
     if (!L) return;
     void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shB,
-                 L->score, L->choice, L->idx, L->wt, L->route,
+                 L->score, L->choice, L->slack, L->idx, L->wt, L->route,
                  L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out,
                  L->ldown, L->lup, L->lnw, L->zB, L->accL, L->latB, L->tr,
                  L->pacc};
@@ -1063,6 +1067,27 @@ int k3x_moe_layer_check(k3x_moe_layer *L)
     if (hipMemcpy(&L->route->err, &zero, sizeof zero, hipMemcpyHostToDevice) != hipSuccess)
         return K3X_E_HIP;
     return K3X_E_WAIT;
+}
+
+int k3x_moe_layer_exact_count(k3x_moe_layer *L, int *n)
+{
+    if (!L || !n) return K3X_E_ARG;
+    if (hipSetDevice(L->device) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+        return K3X_E_HIP;
+    if (hipMemcpy(n, &L->route->nexact, sizeof *n, hipMemcpyDeviceToHost) != hipSuccess)
+        return K3X_E_HIP;
+    return 0;
+}
+
+int k3x_moe_layer_last_route(k3x_moe_layer *L, int T, int *idx, float *wt)
+{
+    if (!L || !idx || !wt || T <= 0 || T > K3X_DECODE_MAX_T) return K3X_E_ARG;
+    const size_t n = (size_t)T * L->cfg.topk;
+    if (hipSetDevice(L->device) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(idx, L->idx, n * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(wt, L->wt, n * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return K3X_E_HIP;
+    return 0;
 }
 
 int k3x_attn_res(float *h, const float *blocks, int maxb, int nb, const float *pref,

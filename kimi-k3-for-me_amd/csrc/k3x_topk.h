@@ -17,6 +17,12 @@ __device__ __forceinline__ uint32_t choice_key(float f)
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// The choice value of a key (the inverse of choice_key on the values it keeps).
+__device__ __forceinline__ float key_choice(uint32_t k)
+{
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
 __device__ __forceinline__ int lanes_below(uint64_t m)
 {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
@@ -60,12 +66,15 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 // Branch-free.  NaN and -inf are never taken; a round with nothing left gives index 0,
 // weight 0.  Weights are the unbiased scores, renormalised through a double sum in slot
 // order and a float reciprocal, then scaled (:1710-1716).  Results in s_idx/s_w, and
-// lane j's (slot j's) in out_e/out_w when given.  This form takes the choices and
-// scores in registers (lane l: experts l*NE + c); wave_topk below loads them first.
+// lane j's (slot j's) in out_e/out_w when given, and the last round's choice (the K-th
+// largest; -inf when fewer than K were selectable) in out_ck.  This form takes the
+// choices and scores in registers (lane l: experts l*NE + c); wave_topk below loads them
+// first.
 template <int NE>
 __device__ void wave_topk_vals(const float (&cv)[NE], const float (&sc)[NE], int E, int K,
                                int renorm, float routed_scale, int *s_idx, float *s_w,
-                               int lane, int *out_e = nullptr, float *out_w = nullptr)
+                               int lane, int *out_e = nullptr, float *out_w = nullptr,
+                               float *out_ck = nullptr)
 {
     uint64_t pk[NE];
 #pragma unroll
@@ -77,6 +86,8 @@ __device__ void wave_topk_vals(const float (&cv)[NE], const float (&sc)[NE], int
     uint64_t prev = ~0ull;        // the previous round's winner (none yet: above all)
     int mine_e = 0;               // lane j keeps round j's expert and score
     float mine_s = 0.0f;
+    float ck = -__builtin_inff(); // the last round's choice (-inf when a round finds none:
+                                  // the later rounds find none either)
     for (int j = 0; j < K; j++) {
         uint64_t best = 0ull;
         float bs = 0.0f;
@@ -92,6 +103,7 @@ __device__ void wave_topk_vals(const float (&cv)[NE], const float (&sc)[NE], int
         const uint64_t holders = __ballot(m != 0u && bk == m);
         if (holders == 0ull) {                  // nothing left (uniform)
             if (lane == j) { mine_e = 0; mine_s = 0.0f; }
+            ck = -__builtin_inff();
             continue;
         }
         const int w = (int)__builtin_ctzll(holders);
@@ -99,7 +111,9 @@ __device__ void wave_topk_vals(const float (&cv)[NE], const float (&sc)[NE], int
         const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs), w));
         prev = ((uint64_t)m << 32) | lo;
         if (lane == j) { mine_e = (int)~lo; mine_s = ws; }
+        ck = key_choice(m);
     }
+    if (out_ck) *out_ck = ck;
     float wgt = mine_s;
     if (renorm && K > 1) {
         double sum = 0.0;
@@ -119,7 +133,8 @@ __device__ void wave_topk_vals(const float (&cv)[NE], const float (&sc)[NE], int
 template <int NE, int CP>
 __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, int renorm,
                           float routed_scale, int *s_idx, float *s_w, int lane,
-                          int *out_e = nullptr, float *out_w = nullptr)
+                          int *out_e = nullptr, float *out_w = nullptr,
+                          float *out_ck = nullptr)
 {
     float sc[NE], cv[NE];
 #pragma unroll
@@ -130,18 +145,19 @@ __device__ void wave_topk(rsrc_t cr, rsrc_t sr, uint32_t row_off, int E, int K, 
         sc[c] = bload_f32<CP>(sr, o);
     }
     SCHED_FENCE();      // both rows' loads in flight together: one memory round trip
-    wave_topk_vals<NE>(cv, sc, E, K, renorm, routed_scale, s_idx, s_w, lane, out_e, out_w);
+    wave_topk_vals<NE>(cv, sc, E, K, renorm, routed_scale, s_idx, s_w, lane, out_e, out_w,
+                       out_ck);
 }
 
 // wave_topk for N tokens of one wave together (tokens past ntok load nothing and store
 // nothing): every token's rows are loaded at once (one memory round trip for all), and
 // each round runs for every token before the next, so that one token's wave maximum
 // fills the other's latency.  Per token, the same operations in the same order as
-// wave_topk, so the same results.
+// wave_topk, so the same results; out_ck[r] is token r's K-th choice.
 template <int NE, int CP, int N>
 __device__ void wave_topk_n(rsrc_t cr, rsrc_t sr, const uint32_t (&row_off)[N], int ntok, int E,
                             int K, int renorm, float routed_scale, int *const (&s_idx)[N],
-                            float *const (&s_w)[N], int lane)
+                            float *const (&s_w)[N], int lane, float (&out_ck)[N])
 {
     uint64_t pk[N][NE];
     float sc[N][NE], cv[N][NE];
@@ -165,12 +181,13 @@ __device__ void wave_topk_n(rsrc_t cr, rsrc_t sr, const uint32_t (&row_off)[N], 
         }
     uint64_t prev[N];
     int mine_e[N];
-    float mine_s[N];
+    float mine_s[N], ck[N];
 #pragma unroll
     for (int r = 0; r < N; r++) {
         prev[r] = ~0ull;
         mine_e[r] = 0;
         mine_s[r] = 0.0f;
+        ck[r] = -__builtin_inff();
     }
     for (int j = 0; j < K; j++) {
 #pragma unroll
@@ -189,6 +206,7 @@ __device__ void wave_topk_n(rsrc_t cr, rsrc_t sr, const uint32_t (&row_off)[N], 
             const uint64_t holders = __ballot(m != 0u && bk == m);
             if (holders == 0ull) {                  // nothing left (uniform)
                 if (lane == j) { mine_e[r] = 0; mine_s[r] = 0.0f; }
+                ck[r] = -__builtin_inff();
                 continue;
             }
             const int w = (int)__builtin_ctzll(holders);
@@ -196,8 +214,11 @@ __device__ void wave_topk_n(rsrc_t cr, rsrc_t sr, const uint32_t (&row_off)[N], 
             const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs), w));
             prev[r] = ((uint64_t)m << 32) | lo;
             if (lane == j) { mine_e[r] = (int)~lo; mine_s[r] = ws; }
+            ck[r] = key_choice(m);
         }
     }
+#pragma unroll
+    for (int r = 0; r < N; r++) out_ck[r] = ck[r];
 #pragma unroll
     for (int r = 0; r < N; r++) {
         float wgt = mine_s[r];

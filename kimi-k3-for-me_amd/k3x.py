@@ -38,6 +38,7 @@ EXPORTS = [
     "k3x_attn_res", "k3x_moe_half", "k3x_attn_res_v", "k3x_moe_half_v",
     "k3x_moe_layer_reserve", "k3x_moe_layer_dequant",
     "k3x_moe_prefill_noalloc", "k3x_moe_layer_trace", "k3x_moe_layer_set_prefill_mode",
+    "k3x_moe_layer_exact_count", "k3x_moe_layer_last_route",
     # include/k3x_store.h
     "k3x_store_open", "k3x_store_close", "k3x_store_count", "k3x_store_shards",
     "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
@@ -142,6 +143,8 @@ def lib():
         L.k3x_moe_forward.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
         L.k3x_moe_prefill_noalloc.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
         L.k3x_moe_layer_trace.argtypes = [vp, i, vp, i]
+        L.k3x_moe_layer_exact_count.argtypes = [vp, C.POINTER(i)]
+        L.k3x_moe_layer_last_route.argtypes = [vp, i, vp, vp]
         L.k3x_rmsnorm.argtypes = [vp, vp, vp, i, i, f, vp]
         L.k3x_moe.argtypes = [vp, vp, vp, i, vp, vp]
         L.k3x_moe_prefill.argtypes = [vp, vp, vp, i, vp, vp]
@@ -510,6 +513,23 @@ class MoELayer:
         n = _check(lib().k3x_moe_layer_trace(self.h, kernel, buf.ctypes.data, max_wg),
                    "k3x_moe_layer_trace")
         return buf[:n] if n else None
+
+    def exact_count(self):
+        """How many (token, expert) router logits the last decode-path selection worked
+        out again as the reference's sequential chain (k3x_moe_layer_exact_count)."""
+        n = C.c_int(0)
+        _check(lib().k3x_moe_layer_exact_count(self.h, C.byref(n)), "k3x_moe_layer_exact_count")
+        return n.value
+
+    def last_route(self, T):
+        """The last decode-path call's routing: (idx [T][K] int32, wt [T][K] float32)
+        (k3x_moe_layer_last_route)."""
+        K = self.cfg.topk
+        idx = np.empty((T, K), np.int32)
+        wt = np.empty((T, K), np.float32)
+        _check(lib().k3x_moe_layer_last_route(self.h, T, idx.ctypes.data, wt.ctypes.data),
+               "k3x_moe_layer_last_route")
+        return idx, wt
 
     def set_timing(self, on):
         _check(lib().k3x_moe_layer_set_timing(self.h, 1 if on else 0), "set_timing")

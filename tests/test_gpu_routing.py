@@ -81,7 +81,7 @@ def test_wait_bound_reports_and_recovers(torch, k3x):
         layer.check()
     assert "gave up waiting" in str(ei.value)
     layer.check()                           # reported once
-    layer.set_route_wait(5000000, publish=True)
+    layer.set_route_wait(100000000, publish=True)
     out2, i2, _ = dev_forward(torch, k3x, layer, x)
     assert np.array_equal(i2, idx)
     assert synth.rel_l2(out2, o) < TOL
@@ -102,7 +102,7 @@ def test_wait_bound_host_call_returns_wait(torch, k3x):
         layer.moe(x)
     assert ei.value.status == -7, str(ei.value)
     layer.check()                           # the host call cleared the word
-    layer.set_route_wait(5000000, publish=True)
+    layer.set_route_wait(100000000, publish=True)
     out, il, _ = layer.moe(x)
     assert np.array_equal(il, idx[-1])
     assert synth.rel_l2(out, o) < TOL
@@ -151,6 +151,119 @@ def test_prefill_router_sequential_chain_bitwise(torch, k3x):
                               ol.ptr(L.bias, ol.F32P), H, E, K, 0, 1.0)
     assert np.array_equal(idx, ri)
     assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+    layer.close()
+
+
+def cancelling_tokens(H, T, p, seed, big, bf16):
+    """T tokens N(0, 1) (bf16 values when bf16) carrying +big and -big (a random sign a
+    token) at columns p and p + 1."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    if bf16:
+        x = synth.bf16_to_f32(synth.f32_to_bf16(x.ravel())).reshape(T, H)
+    sgn = np.where(rng.integers(0, 2, T) == 1, 1.0, -1.0).astype(np.float32)
+    x[:, p] = sgn * np.float32(big)
+    x[:, p + 1] = -sgn * np.float32(big)
+    return x
+
+
+def four_chain_changes(W, x):
+    """Fraction of float logits that summing in four interleaved chains instead of the
+    reference's single chain changes (the test data's teeth)."""
+    W64, X64 = W.astype(np.float64), x.astype(np.float64)
+    seq = np.zeros((x.shape[0], W.shape[0]))
+    ch = np.zeros((4,) + seq.shape)
+    for i in range(x.shape[1]):
+        term = X64[:, i:i + 1] * W64[:, i][None, :]
+        seq = seq + term
+        ch[i % 4] = ch[i % 4] + term
+    four = ((ch[0] + ch[1]) + ch[2]) + ch[3]
+    return np.mean(seq.astype(np.float32) != four.astype(np.float32))
+
+
+def oracle_routes(L, x):
+    import oracle_lib as ol
+    T, H = x.shape
+    ri = np.empty((T, L.K), np.int32)
+    rw = np.empty((T, L.K), np.float32)
+    for t in range(T):
+        xt = np.ascontiguousarray(x[t])
+        ol.oracle().ko_router(ol.ptr(ri[t], ol.I32P), ol.ptr(rw[t], ol.F32P),
+                              ol.ptr(xt, ol.F32P), ol.ptr(L.gate, ol.F32P),
+                              ol.ptr(L.bias, ol.F32P), H, L.E, L.K, L.renorm, L.routed_scale)
+    return ri, rw
+
+
+@pytest.mark.parametrize("big", [2.0 ** 28, 2.0 ** 40])
+@pytest.mark.parametrize("H,E,bf16", [(1024, 100, False), (1024, 100, True), (7168, 384, True)])
+@pytest.mark.parametrize("T", [1, 8])
+def test_decode_router_sequential_chain_bitwise(torch, k3x, T, H, E, bf16, big):
+    """The decode path's routing is the reference's (k3_ops.c:1624-1719) bit for bit where
+    its parallel logit sums round differently from the reference's single double chain:
+    every logit whose float is not proven equal and that could change the selection or a
+    selected weight is worked out again as that chain.  The router rows are equal at
+    columns p and p + 1 and every token carries +big and -big there, so the pair cancels
+    but first rounds away low bits of the partial sum it meets.  Renorm off and scale 1:
+    the weights are the sigmoid scores, compared bitwise with the oracle's.  T = 1 runs
+    k1_router_bset, T = 8 k1_router_mt; 2^28 changes about one float logit in eight
+    (some experts proven, some worked out again), 2^40 nearly all."""
+    say(f"case: decode router on cancelling data, H={H} E={E} T={T} bf16={bf16} big=2^"
+        f"{int(np.log2(big))}, weights bitwise")
+    K, p = 8, H // 2
+    L = synth.Layer(H=H, E=E, K=K, I=128, seed=61, renorm=0, routed_scale=1.0)
+    L.gate[:, p + 1] = L.gate[:, p]
+    x = cancelling_tokens(H, T, p, 61 + T, big, bf16)
+    if H == 1024:
+        differ = four_chain_changes(L.gate, x)
+        say(f"  float logits that a four-chain order changes: {differ:.1%}")
+        assert differ > 0.05
+    layer = bank_layer(k3x, L)
+    _, idx, wt = dev_forward(torch, k3x, layer, x, bf16=bf16)
+    n = layer.exact_count()
+    ri, rw = oracle_routes(L, x)
+    say(f"  logits worked out as the reference's chain: {n} of {T * E}")
+    assert n > 0
+    assert np.array_equal(idx, ri)
+    assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+    layer.close()
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_decode_router_sequential_chain_bitwise_norm(torch, k3x, T):
+    """The same for the stacked layers' decode calls, whose router reads the RMSNorm of h
+    worked out in its own launch: norm weights of 2^30 at the cancelling columns, so that
+    the normalised pair still dominates every partial sum.  The routing is read back with
+    k3x_moe_layer_last_route and compared bitwise with the oracle's RMSNorm then router."""
+    import oracle_lib as ol
+    say(f"case: stacked decode router on cancelling data, T={T}, weights bitwise")
+    H, E, K, p, eps = 1024, 100, 8, 512, 1e-5
+    L = synth.Layer(H=H, E=E, K=K, I=128, seed=71, renorm=0, routed_scale=1.0)
+    L.gate[:, p + 1] = L.gate[:, p]
+    nw = np.ones(H, np.float32)
+    nw[p] = nw[p + 1] = np.float32(2.0 ** 30)
+    x = cancelling_tokens(H, T, p, 71 + T, 2.0 ** 10, False)
+    y = np.empty_like(x)
+    for t in range(T):
+        xt = np.ascontiguousarray(x[t])
+        ol.oracle().ko_rmsnorm(ol.ptr(y[t], ol.F32P), ol.ptr(xt, ol.F32P), ol.ptr(nw, ol.F32P),
+                               H, eps)
+    differ = four_chain_changes(L.gate, y)
+    say(f"  float logits that a four-chain order changes: {differ:.1%}")
+    assert differ > 0.05
+    layer = bank_layer(k3x, L)
+    nd = torch.from_numpy(nw).cuda()
+    S = k3x.Stack([layer], [nd.data_ptr()], eps=eps, max_T=8)
+    h = torch.from_numpy(x).cuda()
+    S.forward(h.data_ptr(), T, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    idx, wt = layer.last_route(T)
+    n = layer.exact_count()
+    ri, rw = oracle_routes(L, y)
+    say(f"  logits worked out as the reference's chain: {n} of {T * E}")
+    assert n > 0
+    assert np.array_equal(idx, ri)
+    assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+    S.close()
     layer.close()
 
 

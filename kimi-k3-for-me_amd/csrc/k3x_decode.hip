@@ -432,9 +432,11 @@ struct K1Args {
 #define RCH    8                     // float4 chunks per lane held at once
 
 // RMSNorm's 1/rms of every token (k3_rmsnorm, k3_ops.c:132-140) in the order of
-// rmsnorm_kernel (k3x_layout.hip), so the normalised rows are bitwise that kernel's:
-// thread i sums the squares of its float4 chunks i, i + 256, ... in double, a shuffle tree
-// per wave, the four waves added in order.  Needs 256 threads and H <= 8192.
+// rmsnorm_kernel (k3x_layout.hip): thread i sums the squares of its float4 chunks i,
+// i + 256, ... in double, a shuffle tree per wave, the four waves added in order; a row
+// whose float 1/rms that order does not prove (rms_inv_proven) sums its squares again as
+// the reference's chain, so the scale is the reference's, as rmsnorm_kernel's is.  Needs
+// 256 threads, H <= 8192, and lds of 1152 floats.
 __device__ void k1_norm_inv(const K1Args &a, float *lds, float *s_inv)
 {
     static_assert(NT1 == 256 && RWAVES * WAVE == NT1, "one 256-thread workgroup per row");
@@ -459,35 +461,39 @@ __device__ void k1_norm_inv(const K1Args &a, float *lds, float *s_inv)
         if (lane == 0) dl[wave * K3X_DECODE_MAX_T + t] = ss;
     }
     __syncthreads();
+    int *redo = (int *)(dl + NT1 / WAVE * K3X_DECODE_MAX_T);   // [8]: rows to work out again
     if (threadIdx.x < a.T) {
         double tot = 0.0;
         for (int w = 0; w < NT1 / WAVE; w++) tot += dl[w * K3X_DECODE_MAX_T + threadIdx.x];
-        s_inv[threadIdx.x] = (float)(1.0 / sqrt(tot / (double)a.H + (double)a.eps));
+        s_inv[threadIdx.x] = rms_inv(tot, a.H, a.eps);
+        redo[threadIdx.x] = !rms_inv_proven(tot, a.H, a.eps);
     }
     __syncthreads();
+    // a row whose float 1/rms this order does not prove: its squares summed again as the
+    // reference's chain (rare: about one row in 10^5 at the hidden width of 7168)
+    for (int t = 0; t < a.T; t++) {
+        if (!redo[t]) continue;                 // uniform
+        const float *xr = x + (size_t)t * a.H;
+        const double ss = wg_dot_chain(xr, 1.0f, xr, a.H, lds + 128, 512, NT1);
+        if (threadIdx.x == 0) s_inv[t] = rms_inv(ss, a.H, a.eps);
+        __syncthreads();
+    }
 }
 
 // The slack of a choice whose logit v was summed in another order than the reference's
-// single chain (k3_ops.c:1666-1688), from asum, the float sum of |W[e][i] x[i]|.  The
-// products are exact in double, so the two sums differ only by their roundings: the
-// chain's H - 1 additions and this kernel's at most H/256 + 12 per product (a thread's
-// run of products, the wave's shuffle tree, the four waves' pairs), together at most
-// d = (H + H/128 + 16) 2^-53 (1 + 2^-16) times sum |p| (Higham, Accuracy and Stability
-// of Numerical Algorithms, 2nd ed., eq. 4.4).  asum bounds sum |p| once widened by
-// (H + 64) 2^-23 (its own float roundings) plus H 2^-126 (products below float's range).
-// The reference's logit is then a double in [v - d, v + d], so its float lies in
-// [(float)(v - d), (float)(v + d)] (rounding is monotonic); where both ends round to
-// (float)v the float logit, and with it the score and the choice, are the reference's,
-// and the slack is 0.  Otherwise the slack bounds the distance of the reference's choice
-// from this one: a quarter of the float interval's half-width (the sigmoid's slope is at
-// most 1/4) plus the roundings of the sigmoid and of the bias add (a few units in the last
-// place of |choice| <= 2 + |bias|).  NaN logits give a NaN slack, which marks nothing (a
-// NaN choice is never selected, here or in the reference).
+// single chain (k3_ops.c:1666-1688), from asum, the float sum of |W[e][i] x[i]|.  Each
+// product here takes part in at most H/256 + 12 additions (a thread's run, the wave's
+// shuffle tree, the four waves' pairs), so the reference's logit is a double within
+// d = chain_gap of v, and its float lies in [(float)(v - d), (float)(v + d)]; where both
+// ends round to (float)v, the float logit, and with it the score and the choice, are the
+// reference's, and the slack is 0.  Otherwise the slack bounds the distance of the
+// reference's choice from this one: a quarter of the float interval's half-width (the
+// sigmoid's slope is at most 1/4) plus the roundings of the sigmoid and of the bias add (a
+// few units in the last place of |choice| <= 2 + |bias|).  NaN logits give a NaN slack,
+// which marks nothing (a NaN choice is never selected, here or in the reference).
 __device__ __forceinline__ float choice_slack(double v, float asum, int H, float bias)
 {
-    const double g = ((double)H + (double)(H >> 7) + 16.0) * 0x1p-53 * (1.0 + 0x1p-16);
-    const double au = (double)asum * (1.0 + ((double)H + 64.0) * 0x1p-23) + (double)H * 0x1p-126;
-    const double d = g * au;
+    const double d = chain_gap(abs_bound(asum, H), H);
     const float f = (float)v, lo = (float)(v - d), hi = (float)(v + d);
     if (lo == f && hi == f) return 0.0f;
     const double df = fmax((double)hi - (double)f, (double)f - (double)lo);

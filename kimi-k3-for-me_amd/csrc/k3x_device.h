@@ -38,6 +38,75 @@ __device__ __forceinline__ void split_bf16(float v, uint32_t &hi, uint32_t &lo)
 }
 
 // ------------------------------------------------------------------ reference math
+// ------------------------------------------------------------------ exact sums
+// The reference sums n products p_i, each exact in double (a product of two floats), in
+// one chain i = 0 .. n-1.  A kernel that adds them in another order, each product taking
+// part in at most n/128 + 16 additions (a thread's run of at most n/256 + 4 of them, a
+// wave's shuffle tree, a few wave partials), differs from that chain by at most
+// (n + n/128 + 16) 2^-53 sum |p_i| in total (Higham, Accuracy and Stability of Numerical
+// Algorithms, 2nd ed., eq. 4.4, applied to both sums); the factor 1 + 2^-16 covers the
+// bound's own second-order terms.  chain_gap takes sum |p_i| as asum, an upper bound.
+__device__ __forceinline__ double chain_gap(double asum, int n)
+{
+    return ((double)n + (double)(n >> 7) + 16.0) * 0x1p-53 * (1.0 + 0x1p-16) * asum;
+}
+
+// An upper bound of sum |p_i| from a float sum of the |p_i| formed like the products'
+// (at most n/128 + 16 roundings of 2^-24 each on a product's way) with products below
+// float's range flushed: widened by (n + 64) 2^-23 and n 2^-126.
+__device__ __forceinline__ double abs_bound(float fsum, int n)
+{
+    return (double)fsum * (1.0 + ((double)n + 64.0) * 0x1p-23) + (double)n * 0x1p-126;
+}
+
+// The reference's RMSNorm scale from a sum of squares (k3_ops.c:137).
+__device__ __forceinline__ float rms_inv(double ss, int n, float eps)
+{
+    return (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+}
+
+// Whether rms_inv of a sum of squares ss formed in another order (as chain_gap describes)
+// is the reference's: its chain lies in [ss - d, ss + d] (the terms are non-negative, so
+// ss itself bounds their sum within the gap's slack), and rms_inv is monotonic (each step
+// is a correctly rounded monotonic operation), so the two ends rounding alike proves it.
+__device__ __forceinline__ bool rms_inv_proven(double ss, int n, float eps)
+{
+    const double d = chain_gap(ss, n);
+    return rms_inv(ss - d, n, eps) == rms_inv(ss + d, n, eps);
+}
+
+// Whether (float)v of a sum v formed in another order is the float of the reference's
+// chain, given the gap bound d: the chain is a double in [v - d, v + d], and rounding is
+// monotonic.
+__device__ __forceinline__ bool float_proven(double v, double d)
+{
+    const float f = (float)v;
+    return (float)(v - d) == f && (float)(v + d) == f;
+}
+
+// The reference's chain sum_i (double)(a[i] * s) * (double)b[i] for i = 0 .. n-1 in order
+// (s = 1: sum_i a[i] b[i]; a = b: the sum of squares of k3_ops.c:135-136), worked out by
+// a workgroup of nt threads: chunks of C elements of a and b staged in buf (2C floats of
+// LDS), thread 0 adds them.  Every thread calls; the value in thread 0.  For the rare
+// sums whose float result another order does not prove.
+__device__ double wg_dot_chain(const float *a, float s, const float *b, int n, float *buf, int C,
+                               int nt)
+{
+    double acc = 0.0;
+    for (int i0 = 0; i0 < n; i0 += C) {
+        const int m = n - i0 < C ? n - i0 : C;
+        for (int i = threadIdx.x; i < m; i += nt) {
+            buf[i] = a[i0 + i];
+            buf[C + i] = b[i0 + i];
+        }
+        __syncthreads();
+        if (threadIdx.x == 0)
+            for (int i = 0; i < m; i++) acc += (double)(buf[i] * s) * (double)buf[C + i];
+        __syncthreads();
+    }
+    return acc;
+}
+
 // The reference's sigmoid, 1/(1+expf(-x)) in float (k3_ops.c:143).  exp is evaluated in
 // double and rounded once: the correctly rounded expf(-x) except within ~2^-29
 // relative of a float rounding midpoint.

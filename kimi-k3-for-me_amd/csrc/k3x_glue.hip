@@ -29,7 +29,10 @@ __device__ __forceinline__ double ar_sum(double v, double *red)
 // t's block count: nbv[t * nbs] when nbv is given (device memory; nbs 0 for one count
 // shared by every row, 1 for a count per row: K3_NB(t), k3_ops.c:2481-2483, 2493), else
 // nb0.  Each source's key is its RMS-normalised row (inv rounded to float, v*inv in
-// float) dotted with fold in double; softmax with exp evaluated in double and rounded to
+// float) dotted with fold in double, the two double sums formed in a tree; where the
+// tree does not prove the float result (inv, or the key rounded to float) to be the
+// reference's chain's, that sum is formed again as the chain (rms_inv_proven,
+// float_proven, wg_dot_chain); softmax with exp evaluated in double and rounded to
 // float (the reference's expf), the double sum z; p = (float)(e/z); h = sum_s p_s v_s in
 // float, in source order from 0 (the raw rows are the values).  A device count outside
 // 0 .. min(maxb, AR_MAXSRC - 1) (or above 0 without blocks) fills row t with quiet NaNs
@@ -42,6 +45,8 @@ __global__ void __launch_bounds__(AR_NT) attn_res_kernel(float *h, const float *
     __shared__ double red[AR_NT / WAVE];
     __shared__ float p[AR_MAXSRC];
     __shared__ float sc[AR_MAXSRC];
+    __shared__ float buf[2 * 512];
+    __shared__ double s_ss;
     const int t = blockIdx.x;
     const int nb = nbv ? nbv[(size_t)t * nbs] : nb0;
     if (nb < 0 || nb > maxb || nb + 1 > AR_MAXSRC || (nb > 0 && !blocks)) {
@@ -54,10 +59,24 @@ __global__ void __launch_bounds__(AR_NT) attn_res_kernel(float *h, const float *
         double ss = 0.0;
         for (int i = threadIdx.x; i < n; i += AR_NT) ss += (double)v[i] * (double)v[i];
         ss = ar_sum(ss, red);
-        const float inv = (float)(1.0 / sqrt(ss / (double)n + (double)eps));
+        if (!rms_inv_proven(ss, n, eps)) {             // uniform; rare
+            const double c = wg_dot_chain(v, 1.0f, v, n, buf, 512, AR_NT);
+            if (threadIdx.x == 0) s_ss = c;
+            __syncthreads();
+            ss = s_ss;
+        }
+        const float inv = rms_inv(ss, n, eps);
         double acc = 0.0;
-        for (int i = threadIdx.x; i < n; i += AR_NT) acc += (double)(v[i] * inv) * (double)fold[i];
+        float aa = 0.0f;                               // sum |v*inv| |fold|, for the gap
+        for (int i = threadIdx.x; i < n; i += AR_NT) {
+            const float vi = v[i] * inv;
+            acc += (double)vi * (double)fold[i];
+            aa = fmaf(fabsf(vi), fabsf(fold[i]), aa);
+        }
         acc = ar_sum(acc, red);
+        const double asum = ar_sum((double)aa, red);
+        if (!float_proven(acc, chain_gap(abs_bound((float)asum, n), n)))   // uniform; rare
+            acc = wg_dot_chain(v, inv, fold, n, buf, 512, AR_NT);          // thread 0's
         if (threadIdx.x == 0) sc[s] = (float)acc;
     }
     __syncthreads();

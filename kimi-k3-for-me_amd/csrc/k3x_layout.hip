@@ -163,6 +163,9 @@ __global__ void synth_fp4_kernel(uint8_t *dst, int R, int K, uint64_t ck, uint64
 // RMSNorm of one row per workgroup (k3_rmsnorm, k3_ops.c:132-140): the sum of squares in
 // double (each product exact; the additions in a tree rather than the reference's
 // chain), inv rounded to float, then y = w * x * inv in float in the reference's order.
+// Where the tree's sum does not prove the float inv to be the reference's
+// (rms_inv_proven), the squares are summed again as the reference's chain, so inv is the
+// reference's on every row.
 // Rows of up to RN_MAX * NT * 4 floats (16-byte aligned) are loaded once, x and w
 // together with every load issued before the first use, and kept in registers between
 // the two passes; other rows take the plain loop.
@@ -171,6 +174,8 @@ __global__ void __launch_bounds__(NT) rmsnorm_kernel(float *y, const float *x, c
                                                       int n, float eps)
 {
     __shared__ double red[NT / WAVE];
+    __shared__ float buf[2 * 512];
+    __shared__ double s_ss;
     const float *xr = x + (size_t)blockIdx.x * n;
     float *yr = y + (size_t)blockIdx.x * n;
     const bool vec = (n & 3) == 0 && n <= RN_MAX * NT * 4 &&
@@ -197,7 +202,14 @@ __global__ void __launch_bounds__(NT) rmsnorm_kernel(float *y, const float *x, c
     __syncthreads();
     double tot = 0.0;
     for (int i = 0; i < NT / WAVE; i++) tot += red[i];
-    const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
+    if (!rms_inv_proven(tot, n, eps)) {          // uniform; rare
+        // the squares summed again as the reference's chain
+        const double ss = wg_dot_chain(xr, 1.0f, xr, n, buf, 512, NT);
+        if (threadIdx.x == 0) s_ss = ss;
+        __syncthreads();
+        tot = s_ss;
+    }
+    const float inv = rms_inv(tot, n, eps);
     if (vec) {
 #pragma unroll
         for (int r = 0; r < RN_MAX; r++) {

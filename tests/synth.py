@@ -250,3 +250,34 @@ def rel_l2(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def rms_inv(ss, n, eps):
+    """The reference's RMSNorm scale from a sum of squares (k3_ops.c:137)."""
+    import math
+    return np.float32(1.0 / math.sqrt(ss / n + eps))
+
+
+def rms_window_row(n, eps, seed):
+    """A float row whose sum of squares lies within 2^-44 relative of the preimage of a
+    float rounding midpoint of the RMSNorm scale, so that a kernel summing the squares in
+    another order than the reference's chain cannot prove its float scale from its own
+    sum and must fall back to the chain.  Built from N(0, 1) entries, a coarse entry at
+    column 0 and a fine one at column 1 (its square steps by about 2^-43) that together
+    put the exact sum on the target."""
+    import math
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(n).astype(np.float32)
+    rest = math.fsum(float(v) * float(v) for v in x[2:])
+    f0 = rms_inv(rest + 1.0, n, eps)
+    f1 = np.nextafter(f0, np.float32(np.inf))
+    m = (float(f0) + float(f1)) / 2.0
+    R = n * (1.0 / (m * m) - eps) - rest          # the two entries' squares' target sum
+    c = np.float32(math.sqrt(R - 2.0 ** -21))
+    while float(c) * float(c) > R - 2.0 ** -22:
+        c = np.nextafter(c, np.float32(0))
+    f = np.float32(math.sqrt(R - float(c) * float(c)))
+    x[0], x[1] = c, f
+    ss = math.fsum(float(v) * float(v) for v in x)
+    assert abs(ss - n * (1.0 / (m * m) - eps)) <= 2.0 ** -44 * ss, "window missed"
+    return x

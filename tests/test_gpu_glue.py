@@ -43,6 +43,53 @@ def test_attn_res_vs_oracle(torch, k3x, n, nb):
     assert err < 1e-6
 
 
+@pytest.mark.parametrize("nb", [0, 3])
+def test_attn_res_cancelling_keys_bitwise(torch, k3x, nb):
+    """Sources whose keys cancel: every source row carries +B and -B at columns p and
+    p + 1 where fold holds 2^20 twice, so the normalised pair's products cancel but first
+    round away low bits of the partial sum they meet, which depends on the order of the
+    additions; with nb = 3, block 0 of each row is instead a row at the RMSNorm scale's
+    rounding midpoint (synth.rms_window_row).  The kernel's tree sums cannot prove
+    those floats, forms them again as the reference's chains, and the output is the
+    reference's bit for bit.  Teeth: a four-chain order changes most keys' floats."""
+    say(f"case: attn_res with cancelling keys and RMSNorm window rows, nb={nb}, bitwise")
+    T, maxb, n, p, eps = 4, 4, 1024, 512, 1e-5
+    rng = np.random.default_rng(90 + nb)
+    blocks = rng.standard_normal((T, maxb, n)).astype(np.float32)
+    pref = rng.standard_normal((T, n)).astype(np.float32)
+    fold = (rng.standard_normal(n) * 0.05).astype(np.float32)
+    fold[p] = fold[p + 1] = np.float32(2.0 ** 20)
+    for t in range(T):
+        for s in range(maxb):
+            b = np.float32(2.0 ** 10) * (1 if (t + s) % 2 else -1)
+            blocks[t, s, p], blocks[t, s, p + 1] = b, -b
+        pref[t, p], pref[t, p + 1] = np.float32(2.0 ** 10), np.float32(-2.0 ** 10)
+        if nb > 0:
+            blocks[t, 0] = synth.rms_window_row(n, eps, 300 + t)
+    # teeth (CPU): keys by the reference's chain against a four-chain order
+    chg = 0
+    srcs = [blocks[t, s] for t in range(T) for s in range(nb)] + [pref[t] for t in range(T)]
+    for v in srcs:
+        ss = float(np.sum(v.astype(np.float64) ** 2))
+        inv = synth.rms_inv(ss, n, eps)
+        term = (v * inv).astype(np.float64) * fold.astype(np.float64)
+        seq = 0.0
+        ch = [0.0] * 4
+        for i in range(n):
+            seq += term[i]
+            ch[i % 4] += term[i]
+        chg += np.float32(seq) != np.float32((ch[0] + ch[1]) + (ch[2] + ch[3]))
+    say(f"  keys that a four-chain order changes: {chg} of {len(srcs)}")
+    assert chg >= len(srcs) // 3
+    bd, pd, fd = (torch.from_numpy(a).cuda() for a in (blocks, pref, fold))
+    hd = torch.empty_like(pd)
+    k3x.attn_res(hd.data_ptr(), bd.data_ptr(), maxb, nb, pd.data_ptr(), fd.data_ptr(), n, T, eps,
+                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got, want = hd.cpu().numpy(), oracle_attn_res(blocks, nb, pref, fold, eps)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def oracle_half(L, h, pref, blocks, nb, fold, post, eps):
     cfg = L.ko_cfg()
     w, cb, keep = L._weights()

@@ -138,6 +138,33 @@ def test_rmsnorm_device(torch, k3x):
     np.testing.assert_allclose(yd.cpu().numpy(), want, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("n", [1024, 7168])
+def test_rmsnorm_window_rows_bitwise(torch, k3x, n):
+    """Rows whose sum of squares lies on the preimage of a float rounding midpoint of the
+    scale (synth.rms_window_row): the kernel's tree sum cannot prove its float scale, sums
+    the squares again as the reference's chain (k3_ops.c:135-136), and the normalised rows
+    are the reference's bit for bit.  Two ordinary rows ride along."""
+    say(f"case: RMSNorm on rows at the scale's rounding midpoints, n={n}, bitwise")
+    from oracle_lib import F32P, oracle, ptr
+    eps = 1e-5
+    rng = np.random.default_rng(n)
+    x = np.stack([synth.rms_window_row(n, eps, 100 + r) for r in range(4)] +
+                 [rng.standard_normal(n).astype(np.float32) for _ in range(2)])
+    T = x.shape[0]
+    w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    want = np.empty_like(x)
+    for t in range(T):
+        xt = np.ascontiguousarray(x[t])
+        oracle().ko_rmsnorm(ptr(want[t], F32P), ptr(xt, F32P), ptr(w, F32P), n, eps)
+    xd = torch.from_numpy(x).cuda()
+    wd = torch.from_numpy(w).cuda()
+    yd = torch.empty_like(xd)
+    k3x.rmsnorm(yd.data_ptr(), xd.data_ptr(), wd.data_ptr(), n, T, eps,
+                torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(yd.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
 # ------------------------------------------------------------------ full-size layer
 @pytest.fixture(scope="module")
 def full_normal(torch, k3x):

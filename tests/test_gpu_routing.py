@@ -267,6 +267,37 @@ def test_decode_router_sequential_chain_bitwise_norm(torch, k3x, T):
     layer.close()
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_stacked_router_on_norm_window_rows_bitwise(torch, k3x, T):
+    """The stacked layers' decode router reads the RMSNorm of h worked out in its own
+    launch; on rows at the scale's rounding midpoints (synth.rms_window_row) that launch
+    sums the squares again as the reference's chain, so the normalised rows, and with
+    them the routing weights (renorm off, scale 1), are the reference's bit for bit."""
+    import oracle_lib as ol
+    say(f"case: stacked decode router on RMSNorm window rows, T={T}, weights bitwise")
+    H, E, K, eps = 1024, 100, 8, 1e-5
+    L = synth.Layer(H=H, E=E, K=K, I=128, seed=81, renorm=0, routed_scale=1.0)
+    nw = (1 + 0.1 * np.random.default_rng(81).standard_normal(H)).astype(np.float32)
+    x = np.stack([synth.rms_window_row(H, eps, 200 + t) for t in range(T)])
+    y = np.empty_like(x)
+    for t in range(T):
+        xt = np.ascontiguousarray(x[t])
+        ol.oracle().ko_rmsnorm(ol.ptr(y[t], ol.F32P), ol.ptr(xt, ol.F32P), ol.ptr(nw, ol.F32P),
+                               H, eps)
+    layer = bank_layer(k3x, L)
+    nd = torch.from_numpy(nw).cuda()
+    S = k3x.Stack([layer], [nd.data_ptr()], eps=eps, max_T=8)
+    h = torch.from_numpy(x).cuda()
+    S.forward(h.data_ptr(), T, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    idx, wt = layer.last_route(T)
+    ri, rw = oracle_routes(L, y)
+    assert np.array_equal(idx, ri)
+    assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+    S.close()
+    layer.close()
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("H,E", [(1024, 100), (7168, 384)])
 def test_decode_router_same_bits_for_any_token_count(torch, k3x, bf16, H, E):

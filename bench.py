@@ -710,6 +710,22 @@ def main():
     for l in layers:
         l.set_timing(False)
         l.check()               # no decode workgroup gave up waiting for the selection
+    # how often the selection works a router logit out again as the reference's single
+    # chain (a logit whose float the parallel sum does not prove and that could change the
+    # selection or a selected weight): 512 further tokens, one synchronised call each,
+    # outside the timed region
+    n_ex = 512
+    xe = k3x.synth_normal_f32(n_ex * H, k3x.synth_key(1, 0, k3x.STREAM_X, 101))
+    xe = torch.from_numpy(xe.reshape(n_ex, H)).to(dev).to(torch.bfloat16).contiguous()
+    tok_ex = logit_ex = 0
+    with torch.cuda.stream(stream):
+        for i in range(n_ex):
+            layers[i % NROT].forward(out.data_ptr(), xe.data_ptr() + i * row, 1, k3x.K3X_BF16,
+                                     stream=sh)
+            c = layers[i % NROT].exact_count()
+            tok_ex += int(c > 0)
+            logit_ex += c
+    del xe
     avg = {n: float(np.mean(v)) for n, v in per.items()}
     kb = kernel_bytes(U=K, T=1)
     dom = max(avg, key=lambda n: avg[n])
@@ -741,6 +757,8 @@ def main():
                      "algorithmic_bytes_per_launch": kb[dom]},
         "layer_build_s": round(build_s, 2),
         "warm_one_layer_us_per_token": round(warm_ms * 1e3, 2),
+        "router_exact_chain": {"tokens": n_ex, "tokens_with_a_chain": tok_ex,
+                               "logits_worked_out": logit_ex},
     }
     for l in layers:
         l.close()

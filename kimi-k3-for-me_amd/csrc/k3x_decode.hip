@@ -500,6 +500,41 @@ __device__ __forceinline__ float choice_slack(double v, float asum, int H, float
     return (float)((df * 0.25 + (2.0 + fabs((double)bias)) * 0x1p-21) * 1.01);
 }
 
+// A thread's RCH chunks of four activations of one row (chunk c: elements 4f .. 4f + 3,
+// f = tl + NT1 c; zero past the row), all loads issued before any is used: one memory
+// round trip per row.  (Loaded and converted chunk by chunk behind a range branch, each
+// load was waited for on its own: eight round trips, about 1 us of the router's 5.5 us a
+// workgroup.)
+__device__ __forceinline__ void load_x_chunks(rsrc_t rx, int x_bf16, uint32_t row_el, int tl,
+                                              int nf4, float (&xv)[RCH][4])
+{
+    if (x_bf16) {
+        u32x2 r[RCH];
+#pragma unroll
+        for (int c = 0; c < RCH; c++) {
+            const int f = tl + NT1 * c;
+            r[c] = __builtin_amdgcn_raw_buffer_load_b64(
+                rx, f < nf4 ? (row_el + 4u * (uint32_t)f) * 2u : K3X_OOB, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < RCH; c++) {
+            xv[c][0] = bf2f(r[c][0] & 0xFFFFu); xv[c][1] = bf2f(r[c][0] >> 16);
+            xv[c][2] = bf2f(r[c][1] & 0xFFFFu); xv[c][3] = bf2f(r[c][1] >> 16);
+        }
+    } else {
+        u32x4 r[RCH];
+#pragma unroll
+        for (int c = 0; c < RCH; c++) {
+            const int f = tl + NT1 * c;
+            r[c] = bload16(rx, f < nf4 ? (row_el + 4u * (uint32_t)f) * 4u : K3X_OOB);
+        }
+#pragma unroll
+        for (int c = 0; c < RCH; c++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) xv[c][k] = __uint_as_float(r[c][k]);
+    }
+}
+
 // Router logits: four waves per expert, sum_i W[e][i] x[i] in double (a product of two
 // floats is exact in double; only the order of the additions differs from the
 // reference's single chain), then score = sigmoid((float)logit), choice = score + bias,
@@ -517,16 +552,21 @@ __device__ void k1_router(const K1Args &a, float *lds, float *s_inv, bool bset)
     float aa[TM];
 #pragma unroll
     for (int t = 0; t < TM; t++) { acc[t] = 0.0; aa[t] = 0.0f; }
-    const float *row = a.router + (size_t)(e < a.E ? e : 0) * a.H;
     const int tl = wq * WAVE + lane;                            // 0..255 within the expert
+    const rsrc_t rr = make_rsrc(a.router + (size_t)(e < a.E ? e : 0) * a.H,
+                                e < a.E ? (uint32_t)a.H * 4u : 0u);
+    const rsrc_t rx = make_rsrc(a.x, (uint32_t)(a.T * a.H) * (a.x_bf16 ? 2u : 4u));
     for (int f0 = 0; f0 < nf4; f0 += RWAVES * WAVE * RCH) {
         f32x4 w[RCH];
 #pragma unroll
         for (int c = 0; c < RCH; c++) {
             const int f = f0 + tl + RWAVES * WAVE * c;
-            w[c] = (f < nf4 && e < a.E) ? __builtin_nontemporal_load((const f32x4 *)(row + 4 * f))
-                                        : (f32x4){0.f, 0.f, 0.f, 0.f};
+            w[c] = __builtin_bit_cast(f32x4, wld16(rr, f < nf4 ? 16u * (uint32_t)f : K3X_OOB));
         }
+        // one token without the norm: its row's loads in flight with the weights
+        float x0[RCH][4];
+        const bool pre = TM == 1 && !a.norm_w;
+        if (pre) load_x_chunks(rx, a.x_bf16, 0u, f0 + tl, nf4, x0);
         f32x4 nw[RCH];
         if (a.norm_w) {                         // uniform; then f0 == 0 (H <= 8192)
             k1_norm_inv(a, lds, s_inv);
@@ -549,11 +589,13 @@ __device__ void k1_router(const K1Args &a, float *lds, float *s_inv, bool bset)
         for (int t = 0; t < TM; t++) {
             if (t < a.T) {
                 float xv[RCH][4];
+                if (pre) {
 #pragma unroll
-                for (int c = 0; c < RCH; c++) {
-                    const int f = f0 + tl + RWAVES * WAVE * c;
-                    if (f < nf4) load_x4(a.x, a.x_bf16, (size_t)t * a.H + 4 * f, xv[c]);
-                    else xv[c][0] = xv[c][1] = xv[c][2] = xv[c][3] = 0.f;
+                    for (int c = 0; c < RCH; c++)
+#pragma unroll
+                        for (int k = 0; k < 4; k++) xv[c][k] = x0[c][k];
+                } else {
+                    load_x_chunks(rx, a.x_bf16, (uint32_t)(t * a.H), f0 + tl, nf4, xv);
                 }
                 if (a.norm_w) {
                     const float inv = s_inv[t];
@@ -1059,15 +1101,20 @@ __device__ void k2_gateup_body(const K2Args &a, float *lds, int *s_go_p)
     __shared__ int s_e;
     const k3x_route *rte = a.route;
     if (a.sel_done) {
-        if (threadIdx.x == 0) {
-            int go = 1, e = 0;
-            if (u >= rte->nu) go = 0;
-            else {
-                e = rte->uniq[u];
-                for (int t = 0; t < a.T; t++) s_w[t] = rte->wtok[u][t];
+        if (wave == 0) {
+            // lane 0 the unique count, lane 1 its slot's expert, lanes 2 .. T + 1 the slot's
+            // weight per token: one load each, all at once
+            const int nw = 2 + a.T;
+            const int *p = lane == 0 ? &rte->nu
+                         : lane == 1 ? &rte->uniq[u]
+                                     : (const int *)&rte->wtok[u][lane < nw ? lane - 2 : 0];
+            const int v = lane < nw ? *p : 0;
+            const int nu = __shfl(v, 0), e = __shfl(v, 1);
+            if (u < nu && lane >= 2 && lane < nw) s_w[lane - 2] = __int_as_float(v);
+            if (lane == 0) {
+                s_go = u < nu;
+                s_e = u < nu ? e : 0;
             }
-            s_go = go;
-            s_e = e;
         }
     } else if (wave == 0) {
         // lane 0 reads the unique count, lane 1 its slot's expert, lanes 2 .. T + 1 the

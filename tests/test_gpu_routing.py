@@ -63,19 +63,21 @@ def test_fewer_selectable_than_slots(torch, k3x):
         assert sorted(idx[t][:3]) == [5, 9, 14] and idx[t][3] == 0
 
 
-def test_wait_bound_reports_and_recovers(torch, k3x):
-    """Failure handling of the decode wait, forced from the host: the selection's flag is
-    withheld and the bound set to 2 us, so every routed workgroup gives up (and exits);
-    the check reports K3X_E_WAIT once, and the next call with the defaults is valid."""
-    say("case: decode wait bound forced (flag withheld, 2 us), then restored")
+@pytest.mark.parametrize("T", [1, 2])
+def test_wait_bound_reports_and_recovers(torch, k3x, T):
+    """Failure handling of the decode wait, forced from the host: the selection's routing
+    words are withheld and the bound set to 2 us, so every routed workgroup gives up (and
+    exits), for one token as for several; the check reports K3X_E_WAIT once, and the next
+    call with the defaults is valid."""
+    say(f"case: decode wait bound forced (words withheld, 2 us), then restored, T={T}")
     L = synth.tiny(seed=34)
     layer = bank_layer(k3x, L)
-    x = L.x(2, bf16=False, stream_sub=12)
+    x = L.x(T, bf16=False, stream_sub=12)
     o, idx, _, _ = L.oracle_moe(x)
     layer.set_route_wait(200, publish=False)
     xt = torch.from_numpy(np.ascontiguousarray(x)).cuda()
     out = torch.empty_like(xt)
-    layer.forward(out.data_ptr(), xt.data_ptr(), 2, k3x.K3X_F32)
+    layer.forward(out.data_ptr(), xt.data_ptr(), T, k3x.K3X_F32)
     torch.cuda.synchronize()
     with pytest.raises(k3x.K3XError) as ei:
         layer.check()
@@ -88,14 +90,15 @@ def test_wait_bound_reports_and_recovers(torch, k3x):
     layer.close()
 
 
-def test_wait_bound_host_call_returns_wait(torch, k3x):
+@pytest.mark.parametrize("T", [1, 3])
+def test_wait_bound_host_call_returns_wait(torch, k3x, T):
     """The host-pointer drop-in (k3x_moe, behind the reference binding's k3_moe_gpu) must
     not return success on a call whose routed workgroups gave up waiting: with the flag
     withheld it raises K3X_E_WAIT, and the next call with the defaults is valid."""
-    say("case: host-pointer k3x_moe with the decode wait forced, then restored")
+    say(f"case: host-pointer k3x_moe with the decode wait forced, then restored, T={T}")
     L = synth.tiny(seed=35)
     layer = bank_layer(k3x, L)
-    x = L.x(3, bf16=False, stream_sub=13)
+    x = L.x(T, bf16=False, stream_sub=13)
     o, idx, _, _ = L.oracle_moe(x)
     layer.set_route_wait(200, publish=False)
     with pytest.raises(k3x.K3XError) as ei:

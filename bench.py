@@ -503,57 +503,17 @@ def measured_traffic(kernel):
     return None
 
 
-def cpu_baseline(n_tokens=24, min_seconds=10.0):
-    """The layer on the host CPU over a bounded sample of tokens (same seeded layer)."""
+def _host():
+    """The compiled reference for this host (its AVX-512 build where the host has
+    x86-64-v4, what its -march=native build selects there, else the AVX2 build), or None
+    (then the oracle port is timed), and the host facts every CPU baseline reports."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import ctypes as C
     import oracle_lib as ol
-    import synth
+    import platform
 
-    L = synth.full(seed=1)
-    x = L.x(n_tokens, bf16=True, stream_sub=7)
-    # the reference's best build for this host: its AVX-512 paths where the host has
-    # x86-64-v4 (what its -march=native build selects there), else the AVX2 build
     isa = "x86-64-v4" if ol.ref("x86-64-v4") is not None else "x86-64-v3"
     ref = ol.ref(isa)
     kind = "reference" if ref is not None else "port"
-    # route once to know which experts the sample needs, then generate only those
-    idx = np.empty((n_tokens, K), np.int32)
-    wt = np.empty((n_tokens, K), np.float32)
-    for t in range(n_tokens):
-        xt = np.ascontiguousarray(x[t])
-        ol.oracle().ko_router(ol.ptr(idx[t], ol.I32P), ol.ptr(wt[t], ol.F32P),
-                              ol.ptr(xt, ol.F32P), ol.ptr(L.gate, ol.F32P),
-                              ol.ptr(L.bias, ol.F32P), H, E, K, 1, 2.5)
-    need = sorted(set(idx.ravel().tolist()))
-    bank = (ol.KoExpert * E)()
-    keep = {}
-    for e in need:
-        d = {k: v.copy() for k, v in L.expert(e).items()}
-        keep[e] = d
-        for k in ("p1", "s1", "p3", "s3", "p2", "s2"):
-            setattr(bank[e], k, d[k].ctypes.data_as(ol.U8P))
-    out = np.empty((1, H), np.float32)
-    ii = np.empty((1, K), np.int32)
-    ww = np.empty((1, K), np.float32)
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        for t in range(n_tokens):
-            xt = np.ascontiguousarray(x[t:t + 1])
-            t0 = time.perf_counter()
-            if ref is not None:
-                ref.refdrv_k2_tokens(ol.ptr(out, ol.F32P), ol.ptr(xt, ol.F32P), 1, H, E, K, I, SI,
-                                     2.5, 1, ol.ptr(L.gate, ol.F32P), ol.ptr(L.bias, ol.F32P),
-                                     bank, ol.ptr(L.sh1, ol.U16P), ol.ptr(L.sh3, ol.U16P),
-                                     ol.ptr(L.sh2, ol.U16P), ol.ptr(ii, ol.I32P),
-                                     ol.ptr(ww, ol.F32P))
-            else:
-                L.oracle_moe(xt)
-            times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start >= min_seconds:
-            break
-    us = float(np.median(times) * 1e6)
     cores = int(ol.oracle().ko_threads())
     cpu_model = "unknown"
     try:
@@ -564,16 +524,199 @@ def cpu_baseline(n_tokens=24, min_seconds=10.0):
                     break
     except OSError:
         pass
-    import platform
     libc = platform.libc_ver()
-    return {"value": round(us, 1), "unit": "us/token", "cores": cores, "kind": kind,
+    info = {"cores": cores, "kind": kind,
             "isa": isa if kind == "reference" else "x86-64-v3 (oracle port)",
             "build": "gcc -O3 -fopenmp -ffp-contract=off -march=" + isa
                      + " (oracle/Makefile, the reference's flags but -march)",
-            "cpu_model": cpu_model, "glibc": f"{libc[0]} {libc[1]}",
-            "sample": f"{len(times)} layer calls over {n_tokens} distinct bf16 tokens of the "
-                      f"same seeded layer ({len(need)} experts generated), median per token, "
-                      f"OpenMP threads {cores}"}
+            "cpu_model": cpu_model, "glibc": f"{libc[0]} {libc[1]}"}
+    return ref, info
+
+
+def _bank(L, experts):
+    """The experts' arrays of layer L in the reference's layout, as the harness's bank
+    (the arrays are kept alive by the returned dict)."""
+    import oracle_lib as ol
+    bank = (ol.KoExpert * L.E)()
+    keep = {}
+    for e in experts:
+        d = {k: v.copy() for k, v in L.expert(e).items()}
+        keep[e] = d
+        for k in ("p1", "s1", "p3", "s3", "p2", "s2"):
+            setattr(bank[e], k, d[k].ctypes.data_as(ol.U8P))
+    return bank, keep
+
+
+def _route(L, x):
+    """Every row's top-k experts by the oracle's router (to know which to generate)."""
+    import oracle_lib as ol
+    idx = np.empty((x.shape[0], L.K), np.int32)
+    wt = np.empty((x.shape[0], L.K), np.float32)
+    for t in range(x.shape[0]):
+        xt = np.ascontiguousarray(x[t])
+        ol.oracle().ko_router(ol.ptr(idx[t], ol.I32P), ol.ptr(wt[t], ol.F32P),
+                              ol.ptr(xt, ol.F32P), ol.ptr(L.gate, ol.F32P),
+                              ol.ptr(L.bias, ol.F32P), L.H, L.E, L.K, L.renorm,
+                              L.routed_scale)
+    return idx
+
+
+def _k2_args(L, bank):
+    import oracle_lib as ol
+    return (L.H, L.E, L.K, L.I, L.I * L.n_shared, L.routed_scale, L.renorm,
+            ol.ptr(L.gate, ol.F32P), ol.ptr(L.bias, ol.F32P), bank, ol.ptr(L.sh1, ol.U16P),
+            ol.ptr(L.sh3, ol.U16P), ol.ptr(L.sh2, ol.U16P))
+
+
+def cpu_baseline(n_tokens=24, min_seconds=10.0):
+    """The decode layer on the host CPU over a bounded sample of tokens (same seeded
+    layer): the reference's k3_moe work per token (refdrv_k2_tokens), median per token."""
+    t_setup = time.perf_counter()
+    ref, info = _host()               # puts the test infrastructure on the path
+    import oracle_lib as ol
+    import synth
+
+    L = synth.full(seed=1)
+    x = L.x(n_tokens, bf16=True, stream_sub=7)
+    need = sorted(set(_route(L, x).ravel().tolist()))
+    bank, keep = _bank(L, need)
+    out = np.empty((1, H), np.float32)
+    ii = np.empty((1, K), np.int32)
+    ww = np.empty((1, K), np.float32)
+    setup_s = time.perf_counter() - t_setup   # weights generated on the host, untimed
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        for t in range(n_tokens):
+            xt = np.ascontiguousarray(x[t:t + 1])
+            t0 = time.perf_counter()
+            if ref is not None:
+                ref.refdrv_k2_tokens(ol.ptr(out, ol.F32P), ol.ptr(xt, ol.F32P), 1,
+                                     *_k2_args(L, bank), ol.ptr(ii, ol.I32P),
+                                     ol.ptr(ww, ol.F32P))
+            else:
+                L.oracle_moe(xt)
+            times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start >= min_seconds:
+            break
+    us = float(np.median(times) * 1e6)
+    rec = {"value": round(us, 1), "unit": "us/token"}
+    rec.update(info)
+    rec["setup_s"] = round(setup_s, 1)
+    rec["sample"] = (f"{len(times)} layer calls over {n_tokens} distinct bf16 tokens of the "
+                     f"same seeded layer ({len(need)} experts generated), median per token, "
+                     f"OpenMP threads {info['cores']}")
+    return rec
+
+
+def cpu_baseline_prefill(min_seconds=10.0, n_tokens=64):
+    """The prefill leg's layer and chunk on the host CPU over a bounded sample: the
+    chunk's first n_tokens rows (64: one of the sub-chunks in which the reference's
+    k3_moe_prefill routes, fetches each unique expert once and applies it to every token
+    that chose it), as one prefill call of the reference's kernels (refdrv_k2_prefill,
+    with the shared expert's batched products); median over calls, as tokens/s."""
+    t_setup = time.perf_counter()
+    ref, info = _host()               # puts the test infrastructure on the path
+    import oracle_lib as ol
+    import synth
+
+    L = synth.full(seed=3, zipf_alpha=1.0)
+    x = L.x(n_tokens, bf16=True, stream_sub=5)      # rows 0 .. n_tokens - 1 of the chunk
+    need = sorted(set(_route(L, x).ravel().tolist()))
+    bank, keep = _bank(L, need)
+    out = np.empty((n_tokens, H), np.float32)
+    ii = np.empty((n_tokens, K), np.int32)
+    ww = np.empty((n_tokens, K), np.float32)
+    setup_s = time.perf_counter() - t_setup   # weights generated on the host, untimed
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        if ref is not None:
+            ref.refdrv_k2_prefill(ol.ptr(out, ol.F32P), ol.ptr(x, ol.F32P), n_tokens,
+                                  *_k2_args(L, bank), ol.ptr(ii, ol.I32P), ol.ptr(ww, ol.F32P))
+        else:
+            L.oracle_moe(x, prefill=True)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start >= min_seconds and len(times) >= 3:
+            break
+    s = float(np.median(times))
+    rec = {"value": round(n_tokens / s, 1), "unit": "tokens/s",
+           "ms_per_sample": round(s * 1e3, 2)}
+    rec.update(info)
+    rec["setup_s"] = round(setup_s, 1)
+    rec["sample"] = (f"rows 0-{n_tokens - 1} of the 2048-token chunk (one 64-position "
+                     f"sub-chunk of the reference's prefill; {len(need)} unique experts, "
+                     f"generated), {len(times)} calls, median, OpenMP threads {info['cores']}")
+    return rec
+
+
+def cpu_baseline_stack(min_seconds=10.0, n_tokens=2):
+    """The stack leg's eight layers on the host CPU for the stack's first n_tokens
+    tokens: per layer h = h + MoE(RMSNorm(h)) with the reference's k3_rmsnorm and k3_moe
+    work (refdrv_k2_norm_layer); median time of a token through the eight layers."""
+    t_setup = time.perf_counter()
+    ref, info = _host()               # puts the test infrastructure on the path
+    import oracle_lib as ol
+    import synth
+
+    Ls = [synth.full(seed=10 + l, layer=l) for l in range(STACK_LAYERS)]
+    norms = [synth.normal_f32(H, synth.key(10 + l, l, synth.S_NORM), 1.0, 0.1)
+             for l in range(STACK_LAYERS)]
+    x = Ls[0].x(n_tokens, bf16=False, stream_sub=7)    # the stack leg's first tokens
+    ii = np.empty((1, K), np.int32)
+    ww = np.empty((1, K), np.float32)
+
+    def layer_step(l, bank, h):
+        if ref is not None:
+            rc = ref.refdrv_k2_norm_layer(ol.ptr(h, ol.F32P), h.shape[0],
+                                          ol.ptr(norms[l], ol.F32P), 1e-5,
+                                          *_k2_args(Ls[l], bank), ol.ptr(ii, ol.I32P),
+                                          ol.ptr(ww, ol.F32P))
+            assert rc == 0
+            return h
+        hin = np.empty_like(h)
+        for t in range(h.shape[0]):
+            ol.oracle().ko_rmsnorm(ol.ptr(hin[t], ol.F32P),
+                                   ol.ptr(np.ascontiguousarray(h[t]), ol.F32P),
+                                   ol.ptr(norms[l], ol.F32P), H, 1e-5)
+        return h + Ls[l].oracle_moe(hin)[0]
+
+    # the experts each layer's routing needs, layer by layer (a layer's input is the
+    # previous layer's output)
+    banks, n_exp = [], 0
+    h = x.copy()
+    for l in range(STACK_LAYERS):
+        hin = np.empty_like(h)
+        for t in range(n_tokens):
+            ol.oracle().ko_rmsnorm(ol.ptr(hin[t], ol.F32P),
+                                   ol.ptr(np.ascontiguousarray(h[t]), ol.F32P),
+                                   ol.ptr(norms[l], ol.F32P), H, 1e-5)
+        need = sorted(set(_route(Ls[l], hin).ravel().tolist()))
+        n_exp += len(need)
+        banks.append(_bank(Ls[l], need))
+        for t in range(n_tokens):
+            h[t:t + 1] = layer_step(l, banks[l][0], np.ascontiguousarray(h[t:t + 1]))
+    setup_s = time.perf_counter() - t_setup   # weights generated on the host, untimed
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        for t in range(n_tokens):
+            ht = x[t:t + 1].copy()            # the layers update their rows in place
+            t0 = time.perf_counter()
+            for l in range(STACK_LAYERS):
+                ht = layer_step(l, banks[l][0], ht)
+            times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start >= min_seconds:
+            break
+    us = float(np.median(times) * 1e6)
+    rec = {"value": round(us, 1), "unit": "us/token", "us_per_layer": round(us / STACK_LAYERS, 1)}
+    rec.update(info)
+    rec["setup_s"] = round(setup_s, 1)
+    rec["sample"] = (f"the stack's tokens 0-{n_tokens - 1} through its {STACK_LAYERS} layers "
+                     f"({n_exp} experts generated), {len(times)} passes, median per token, "
+                     f"OpenMP threads {info['cores']}")
+    return rec
 
 
 def copy_calibration(torch, mib, reps):
@@ -779,6 +922,10 @@ def main():
         rec["trunk"] = trunk_leg(torch, k3x)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(min_seconds=args.cpu_seconds)
+        if "prefill" in rec:
+            rec["prefill"]["cpu_baseline"] = cpu_baseline_prefill(min_seconds=args.cpu_seconds)
+        if "stack" in rec:
+            rec["stack"]["cpu_baseline"] = cpu_baseline_stack(min_seconds=args.cpu_seconds)
     else:
         rec["cpu_baseline"] = None
     print(json.dumps(rec), flush=True)

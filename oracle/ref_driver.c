@@ -279,6 +279,109 @@ long refdrv_k2_tokens(float *out, const float *x, int T, int H, int E, int K, in
     return 0;
 }
 
+/* One K2-class layer over a prefill chunk of T tokens with the reference's own kernels,
+ * in the order of its k3_moe_prefill (k3_ops.c:2008-2053) without the identity latent
+ * projections of refdrv_moe: per sub-chunk of 64 positions (MOE_DEDUP_CHUNK, :1993)
+ * route every token with k3_router and list the unique experts in first-seen order
+ * (:2067-2082), apply each unique expert once to every (token, slot) that chose it,
+ * 3 x k3_matmul_mxfp4 + k3_situ_glu (:2086-2113), and sum each token's slots in top-k
+ * order (:2115-2130); then the shared expert over all T positions with the batched bf16
+ * products k3_mmw_batch_ld (moe_shared, :1848-1860).  What the CPU baseline of a prefill
+ * chunk times.  Bit-identical to refdrv_moe(..., prefill = 1).  idx/wt: [T][K]. */
+long refdrv_k2_prefill(float *out, const float *x, int T, int H, int E, int K, int I,
+                       int SI, float routed_scale, int renorm, const float *gate,
+                       const float *bias, const drv_expert *bank, const uint16_t *sh1,
+                       const uint16_t *sh3, const uint16_t *sh2, int *idx, float *wt)
+{
+    enum { SUB = 64 };
+    const float b = 0x1p64f;
+    float *gu = (float *)malloc((size_t)2 * I * sizeof(float));
+    float *act = (float *)malloc((size_t)I * sizeof(float));
+    float *contrib = (float *)malloc((size_t)SUB * K * H * sizeof(float));
+    int *uniq = (int *)malloc((size_t)E * sizeof(int));
+    unsigned char *seen = (unsigned char *)malloc((size_t)E);
+    float *sgu = (float *)malloc((size_t)T * 2 * (SI > 0 ? SI : 1) * sizeof(float));
+    float *sdn = (float *)malloc((size_t)T * H * sizeof(float));
+    long rc = 0;
+    if (!gu || !act || !contrib || !uniq || !seen || !sgu || !sdn) { rc = -1; goto done; }
+    for (int t0 = 0; t0 < T; t0 += SUB) {
+        const int n = T - t0 < SUB ? T - t0 : SUB;
+        memset(seen, 0, (size_t)E);
+        int nu = 0;
+        for (int t = 0; t < n; t++) {
+            int *it = idx + (size_t)(t0 + t) * K;
+            k3_router(it, wt + (size_t)(t0 + t) * K, x + (size_t)(t0 + t) * H, gate, bias, H,
+                      E, K, renorm, routed_scale);
+            for (int j = 0; j < K; j++)
+                if (it[j] >= 0 && it[j] < E && !seen[it[j]]) { seen[it[j]] = 1; uniq[nu++] = it[j]; }
+        }
+        for (int u = 0; u < nu; u++) {
+            const drv_expert *q = &bank[uniq[u]];
+            for (int t = 0; t < n; t++) {
+                const int *it = idx + (size_t)(t0 + t) * K;
+                const float *xt = x + (size_t)(t0 + t) * H;
+                for (int j = 0; j < K; j++) {
+                    if (it[j] != uniq[u]) continue;
+                    float *cb = contrib + ((size_t)t * K + j) * H;
+                    k3_matmul_mxfp4(gu, xt, q->p1, q->s1, H, I, K3_MXFP4_GROUP);
+                    k3_matmul_mxfp4(gu + I, xt, q->p3, q->s3, H, I, K3_MXFP4_GROUP);
+                    k3_situ_glu(act, gu, I, b, b);
+                    k3_matmul_mxfp4(cb, act, q->p2, q->s2, I, H, K3_MXFP4_GROUP);
+                }
+            }
+        }
+        for (int t = 0; t < n; t++) {
+            const int *it = idx + (size_t)(t0 + t) * K;
+            const float *wtt = wt + (size_t)(t0 + t) * K;
+            float *acc = out + (size_t)(t0 + t) * H;
+            for (int i = 0; i < H; i++) acc[i] = 0.0f;
+            for (int j = 0; j < K; j++) {
+                if (it[j] < 0) continue;
+                const float *cb = contrib + ((size_t)t * K + j) * H;
+                for (int i = 0; i < H; i++) acc[i] += wtt[j] * cb[i];
+            }
+        }
+    }
+    if (SI > 0) {
+        k3_mmw_batch_ld(sgu, 2 * SI, x, H, sh1, K3_WBF16, H, SI, T);
+        k3_mmw_batch_ld(sgu + SI, 2 * SI, x, H, sh3, K3_WBF16, H, SI, T);
+        for (int t = 0; t < T; t++) {
+            float *sg = sgu + (size_t)t * 2 * SI;
+            k3_situ_glu(sg, sg, SI, b, b);
+        }
+        k3_mmw_batch_ld(sdn, H, sgu, 2 * SI, sh2, K3_WBF16, SI, H, T);
+        for (size_t i = 0; i < (size_t)T * H; i++) out[i] += sdn[i];
+    }
+done:
+    free(gu); free(act); free(contrib); free(uniq); free(seen); free(sgu); free(sdn);
+    return rc;
+}
+
+/* One layer of a stack of K2-class layers for T rows: h = h + MoE(RMSNorm(h; norm_w)),
+ * the RMSNorm by the reference's k3_rmsnorm and the layer as refdrv_k2_tokens computes it
+ * (k3_moe's work, row by row).  What the stack's CPU baseline times, layer by layer.
+ * idx/wt: [T][K]. */
+long refdrv_k2_norm_layer(float *h, int T, const float *norm_w, float eps, int H, int E,
+                          int K, int I, int SI, float routed_scale, int renorm,
+                          const float *gate, const float *bias, const drv_expert *bank,
+                          const uint16_t *sh1, const uint16_t *sh3, const uint16_t *sh2,
+                          int *idx, float *wt)
+{
+    float *hin = (float *)malloc((size_t)T * H * sizeof(float));
+    float *tmp = (float *)malloc((size_t)T * H * sizeof(float));
+    long rc = -1;
+    if (hin && tmp) {
+        for (int t = 0; t < T; t++)
+            k3_rmsnorm(hin + (size_t)t * H, h + (size_t)t * H, norm_w, H, eps);
+        rc = refdrv_k2_tokens(tmp, hin, T, H, E, K, I, SI, routed_scale, renorm, gate, bias,
+                              bank, sh1, sh3, sh2, idx, wt);
+        if (rc == 0)
+            for (size_t i = 0; i < (size_t)T * H; i++) h[i] += tmp[i];
+    }
+    free(hin); free(tmp);
+    return rc;
+}
+
 #ifdef K3X_ADAPTER
 /* The reference-side binding of libk3x (kimi-k3-for-me_amd/csrc/k3x_ref_adapter.c). */
 int    k3_moe_gpu(float *out, const float *x, const K3MoeW *w, const K3Cfg *c, int T,

@@ -196,5 +196,12 @@ def ref(isa="x86-64-v3"):
         lib.refdrv_k2_tokens.argtypes = [F32P, F32P, C.c_int, C.c_int, C.c_int, C.c_int,
                                          C.c_int, C.c_int, C.c_float, C.c_int, F32P, F32P,
                                          C.POINTER(KoExpert), U16P, U16P, U16P, I32P, F32P]
+        lib.refdrv_k2_prefill.restype = C.c_long
+        lib.refdrv_k2_prefill.argtypes = lib.refdrv_k2_tokens.argtypes
+        lib.refdrv_k2_norm_layer.restype = C.c_long
+        lib.refdrv_k2_norm_layer.argtypes = [F32P, C.c_int, F32P, C.c_float, C.c_int,
+                                             C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
+                                             C.c_int, F32P, F32P, C.POINTER(KoExpert), U16P,
+                                             U16P, U16P, I32P, F32P]
         _ref[path] = lib
     return _ref[path]

@@ -97,6 +97,7 @@ class Layer:
     up: np.ndarray = None
     lnorm: np.ndarray = None
     _cache: dict = field(default_factory=dict)
+    _held: dict = field(default_factory=dict)
 
     @property
     def XL(self):
@@ -126,6 +127,8 @@ class Layer:
 
     def expert(self, e):
         """Expert e's six arrays in the reference's row-major layout (cached)."""
+        if e in self._held:
+            return self._held[e]
         if e in self._cache:
             return self._cache[e]
         H, I, s, l = self.XL, self.I, self.seed, self.layer
@@ -139,6 +142,17 @@ class Layer:
             self._cache.clear()
         self._cache[e] = d
         return d
+
+    def hold(self, experts):
+        """Generates these experts once and keeps them until release(): the cache of
+        expert() keeps at most 64, which a check over many tokens would regenerate."""
+        for e in experts:
+            e = int(e)
+            if e not in self._held:
+                self._held[e] = self.expert(e)
+
+    def release(self):
+        self._held.clear()
 
     def x(self, T, bf16=True, stream_sub=0):
         """T tokens N(0,1); rounded to bf16 values (returned as fp32) when bf16."""

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import synth
-from gpu_util import bank_layer, dev_forward, say, synth_layer
+from gpu_util import bank_layer, dev_forward, host_layer, per_token_rel, say, synth_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -242,7 +242,8 @@ def test_latent_prefill_variants(torch, k3x, norm, shared):
 
 def test_k3_prefill_256(torch, k3x, k3_layer):
     """The K3 shape, one call of 256 bf16 tokens: routing of every token against the
-    oracle's router, every token against the decode path, a sample against the oracle."""
+    oracle's router, every token against the decode path and against the whole layer on
+    the host (the reference's k3_moe_prefill), each within TOL."""
     import oracle_lib as ol
     say("case: K3 shape prefill, 256 bf16 tokens")
     L, layer = k3_layer
@@ -265,9 +266,9 @@ def test_k3_prefill_256(torch, k3x, k3_layer):
     err = synth.rel_l2(out, o2)
     say(f"  rel_l2(prefill, decode) over {T} tokens = {err:.3e}")
     assert err < 1e-5
-    sample = [0, 100, 255]
-    o, oi, _, _ = L.oracle_moe(x[sample])
-    assert np.array_equal(idx[sample], oi)
-    err = synth.rel_l2(out[sample], o)
-    say(f"  rel_l2(prefill, oracle) on tokens {sample} = {err:.3e}")
-    assert err < TOL
+    # every token against the whole layer on the host, token by token
+    o, what = host_layer(L, x, ri)
+    r = per_token_rel(out, o)
+    say(f"  {T} tokens against {what}: per-token rel_l2 median {np.median(r):.2e} "
+        f"max {r.max():.2e}")
+    assert r.max() < TOL

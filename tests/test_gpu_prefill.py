@@ -3,15 +3,15 @@
 Same bar as the decode path: selected expert indices bit-exact (ties to the lower index),
 routing weights to float rounding, outputs within TOL relative L2 of the oracle, which is
 bitwise the reference's k3_moe / k3_moe_prefill.  At the full size (2048 tokens, Zipf-
-skewed routing) the oracle's router runs for every token and its whole layer for a
-sample of tokens; every token is also checked against the decode path, whose grouping of
-tokens must not change any result.
+skewed routing) every token is checked against the oracle's router, the whole layer on
+the host (the compiled reference's prefill, pinned bitwise to the oracle) and the
+decode path, whose grouping of tokens must not change any result.
 """
 import numpy as np
 import pytest
 
 import synth
-from gpu_util import bank_layer, dev_forward, say, synth_layer
+from gpu_util import bank_layer, dev_forward, host_layer, per_token_rel, say, synth_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -82,7 +82,10 @@ def test_tiny_prefill_grouping_invariant(torch, k3x):
 
 
 def test_full_prefill_2048_zipf(torch, k3x):
-    """The full-size layer, one 2048-token chunk of bf16 activations, Zipf-skewed bias."""
+    """The full-size layer, one 2048-token chunk of bf16 activations, Zipf-skewed bias:
+    the routing of every token against the oracle's router, and every token against the
+    decode path and against the whole layer on the host (the reference's prefill;
+    t_moe_prefill holds a whole chunk bitwise, test_ops.c:891-1014), each within TOL."""
     import oracle_lib as ol
     say("case: full-size prefill, 2048 bf16 tokens, Zipf bias (alpha 1.0, s 1.1)")
     L = synth.full(seed=3, zipf_alpha=1.0)
@@ -110,13 +113,12 @@ def test_full_prefill_2048_zipf(torch, k3x):
     err = synth.rel_l2(out, o2)
     say(f"  rel_l2(prefill, decode) over 2048 tokens = {err:.3e}")
     assert err < 1e-5
-    # a sample of tokens against the whole oracle layer
-    sample = [0, 1, 777, 2047]
-    o, oi, _, _ = L.oracle_moe(x[sample])
-    assert np.array_equal(idx[sample], oi)
-    err = synth.rel_l2(out[sample], o)
-    say(f"  rel_l2(prefill, oracle) on tokens {sample} = {err:.3e}")
-    assert err < TOL
+    # every token against the whole layer on the host, token by token
+    o, what = host_layer(L, x, ri)
+    r = per_token_rel(out, o)
+    say(f"  {T} tokens against {what}: per-token rel_l2 median {np.median(r):.2e} "
+        f"max {r.max():.2e}")
+    assert r.max() < TOL
     layer.close()
 
 

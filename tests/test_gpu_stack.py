@@ -164,3 +164,56 @@ def test_full_stack_fused_norm_bitwise(torch, k3x, full_stack, T):
     torch.cuda.synchronize()
     assert torch.equal(h, ref)
     S.close()
+
+
+def test_full_stack_8_layers_per_layer(torch, k3x):
+    """Eight full-size layers (the stack the benchmark replays: seeds 10 + l, RMSNorm
+    weights 1 + N(0, 0.1) from the generator), one token (the benchmark's first): the
+    replayed stack equals per-layer calls (k3x_rmsnorm, then the MoE call with the
+    residual, its selection returned) bit for bit, and at every layer, on that layer's
+    own input, the RMSNorm is the oracle's bit for bit, the selected experts are the
+    oracle router's (weights to float rounding), and the layer's MoE output is within TOL
+    of the oracle's whole layer."""
+    import oracle_lib as ol
+    NL, H = 8, 7168
+    say(f"building {NL} full-size synthetic layers (75 GB) on the device")
+    Ls = [synth.full(seed=10 + l, layer=l) for l in range(NL)]
+    norms = [synth.normal_f32(H, synth.key(10 + l, l, synth.S_NORM), 1.0, 0.1)
+             for l in range(NL)]
+    layers = [synth_layer(k3x, L) for L in Ls]
+    nd = [torch.from_numpy(w).cuda() for w in norms]
+    s = torch.cuda.current_stream().cuda_stream
+    S = k3x.Stack(layers, [w.data_ptr() for w in nd], eps=EPS, max_T=1)
+    h0 = Ls[0].x(1, bf16=False, stream_sub=7)
+    h = torch.from_numpy(h0).cuda()
+    for r in range(2):                          # record, then replay on the same token
+        h.copy_(torch.from_numpy(h0).cuda())
+        S.forward(h.data_ptr(), 1, s)
+    torch.cuda.synchronize()
+    cur = torch.from_numpy(h0).cuda()
+    y = torch.empty_like(cur)
+    idx = torch.empty((1, Ls[0].K), dtype=torch.int32, device="cuda")
+    wt = torch.empty((1, Ls[0].K), dtype=torch.float32, device="cuda")
+    for l, (L, layer, w) in enumerate(zip(Ls, layers, nd)):
+        inp = cur.cpu().numpy()
+        k3x.rmsnorm(y.data_ptr(), cur.data_ptr(), w.data_ptr(), H, 1, EPS, s)
+        layer.forward(cur.data_ptr(), y.data_ptr(), 1, k3x.K3X_F32, cur.data_ptr(),
+                      idx.data_ptr(), wt.data_ptr(), s)
+        torch.cuda.synchronize()
+        layer.check()
+        hin = np.empty_like(inp)
+        ol.oracle().ko_rmsnorm(ol.ptr(hin[0], ol.F32P), ol.ptr(inp[0], ol.F32P),
+                               ol.ptr(norms[l], ol.F32P), H, EPS)
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), hin.view(np.uint32))
+        o, oi, ow, _ = L.oracle_moe(hin)
+        di = idx.cpu().numpy()
+        assert np.array_equal(di, oi), (l, di, oi)
+        np.testing.assert_allclose(wt.cpu().numpy(), ow, rtol=1e-6)
+        moe = cur.cpu().numpy() - inp
+        err = synth.rel_l2(moe, o)
+        say(f"  layer {l}: experts {di[0].tolist()}, MoE rel_l2 {err:.2e}")
+        assert err < TOL
+    assert torch.equal(h, cur)
+    S.close()
+    for l in layers:
+        l.close()

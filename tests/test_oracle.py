@@ -363,6 +363,67 @@ def test_moe_prefill_dedup_bitwise(ref_lib):
     assert rg == want_gets
 
 
+def k2_direct(lib, fn, L, x):
+    """One of the harness's K2 compositions of the reference's kernels (refdrv_k2_tokens,
+    refdrv_k2_prefill) over the rows of x; routing of every row returned."""
+    bank, keep = ref_bank(L)
+    T = x.shape[0]
+    out = np.empty_like(x)
+    idx = np.empty((T, L.K), np.int32)
+    wt = np.empty((T, L.K), np.float32)
+    rc = getattr(lib, fn)(ptr(out, F32P), ptr(x, F32P), T, L.H, L.E, L.K, L.I,
+                          L.I * L.n_shared, L.routed_scale, L.renorm, ptr(L.gate, F32P),
+                          ptr(L.bias, F32P), bank, ptr(L.sh1, U16P), ptr(L.sh3, U16P),
+                          ptr(L.sh2, U16P), ptr(idx, I32P), ptr(wt, F32P))
+    assert rc == 0
+    return out, idx, wt
+
+
+def test_ref_k2_compositions_bitwise(ref_lib):
+    """The compositions of the reference's own kernels that the CPU baselines time
+    (refdrv_k2_tokens: a decode token; refdrv_k2_prefill: a prefill chunk, sub-chunks
+    of 64, unique experts expert-major, the batched shared products) give the bits of
+    the reference's k3_moe and k3_moe_prefill themselves: 130 tokens over three
+    sub-chunks, top-16 of 40, and every token's routing is the oracle's."""
+    L = synth.Layer(H=256, E=40, K=16, I=128, seed=4, scale_lo=121, scale_hi=124)
+    x = L.x(130, bf16=False)
+    rp = ref_moe(ref_lib, L, x, prefill=True)[0]
+    rd = ref_moe(ref_lib, L, x, prefill=False)[0]
+    p, pidx, pwt = k2_direct(ref_lib, "refdrv_k2_prefill", L, x)
+    d, didx, dwt = k2_direct(ref_lib, "refdrv_k2_tokens", L, x)
+    assert np.array_equal(p.view(np.uint32), rp.view(np.uint32))
+    assert np.array_equal(d.view(np.uint32), rd.view(np.uint32))
+    _, oidx, owt, _ = L.oracle_moe(x)
+    for i, w in ((pidx, pwt), (didx, dwt)):
+        assert np.array_equal(i, oidx) and np.array_equal(w.view(np.uint32), owt.view(np.uint32))
+
+
+def test_ref_k2_norm_layer_bitwise(ref_lib):
+    """refdrv_k2_norm_layer, the step the stack's CPU baseline times (h = h +
+    MoE(RMSNorm(h)), the reference's k3_rmsnorm and k3_moe work), against the oracle's
+    RMSNorm, whole layer and float residual add: three layers in turn, five rows."""
+    layers = [synth.tiny(seed=10 + l, layer=l) for l in range(3)]
+    h = layers[0].x(5, bf16=False, stream_sub=7)
+    hr = h.copy()
+    for L in layers:
+        w = synth.normal_f32(L.H, synth.key(L.seed, L.layer, synth.S_NORM), 1.0, 0.1)
+        hin = np.empty_like(h)
+        for t in range(h.shape[0]):
+            oracle().ko_rmsnorm(ptr(hin[t], F32P), ptr(np.ascontiguousarray(h[t]), F32P),
+                                ptr(w, F32P), L.H, 1e-5)
+        h = h + L.oracle_moe(hin)[0]
+        bank, keep = ref_bank(L)
+        idx = np.empty((h.shape[0], L.K), np.int32)
+        wt = np.empty((h.shape[0], L.K), np.float32)
+        rc = ref_lib.refdrv_k2_norm_layer(ptr(hr, F32P), hr.shape[0], ptr(w, F32P), 1e-5, L.H,
+                                          L.E, L.K, L.I, L.I * L.n_shared, L.routed_scale,
+                                          L.renorm, ptr(L.gate, F32P), ptr(L.bias, F32P), bank,
+                                          ptr(L.sh1, U16P), ptr(L.sh3, U16P), ptr(L.sh2, U16P),
+                                          ptr(idx, I32P), ptr(wt, F32P))
+        assert rc == 0
+        assert np.array_equal(h.view(np.uint32), hr.view(np.uint32))
+
+
 def test_moe_combine_order_teeth():
     """Summing a token's expert outputs in first-seen (fetch) order instead of top-k
     order changes the floats at top-16 (the slip k3_ops.c:2113-2118 warns about)."""
@@ -470,3 +531,20 @@ def test_reference_avx512_build_bitwise():
         o, _, _, _ = L.oracle_moe(xt, prefill=prefill)[:4]
         ro, _, _, rd, _ = ref_moe(r4, L, xt, prefill=prefill)
         assert rd == 0 and np.array_equal(o.view(np.uint32), ro.view(np.uint32))
+
+
+@pytest.mark.parametrize("latent", [False, True])
+def test_host_layer_check_bitwise(ref_lib, latent):
+    """The host side of the GPU tests' many-token checks (gpu_util.host_layer: the
+    compiled reference's prefill over a sample of rows, only the chosen experts
+    generated) equals the oracle's whole layer bit for bit, K2 and latent forms, on rows
+    taken from over a larger call."""
+    from gpu_util import host_layer
+    L = synth.tiny_latent(seed=6) if latent else synth.tiny(seed=6)
+    x = L.x(150, bf16=True, stream_sub=3)
+    o, idx, _, _ = L.oracle_moe(x)
+    rows = np.r_[np.arange(0, 150, 2), 149]
+    h, what = host_layer(L, x[rows], idx[rows])
+    assert "compiled reference" in what
+    assert np.array_equal(h.view(np.uint32), o[rows].view(np.uint32))
+    assert not L._held

@@ -7,7 +7,7 @@
 //   pf_topk     each token's top-k by one wave (:1700-1716) and the per-expert histogram
 //   pf_scan     per-expert offsets (prefix sum) and the GEMM tile lists
 //   pf_scatter  each (token, slot) to its row in its expert's segment
-//               (pf_split again, with the rows in that order: the routed input's planes)
+//   pf_gather   the routed input's planes, rows in that order
 //   pf_gemm32   grouped GEMMs: gate/up of every expert segment with SwiGLU and the
 //               routing weight (k3_matmul_mxfp4 :3323-3776, k3_situ_glu :148-161), then
 //               down (pf_gemm_mx in the MXFP8 mode)
@@ -33,9 +33,7 @@
 // Activation planes, the GEMMs' B source: x [T][H] (bf16 or fp32, rows ldx elements
 // apart) -> xg [2][H/8][T][8] bf16, plane 0 the hi parts, plane 1 the lo parts, each
 // k-group of 8 elements token-major, so that one k-group of consecutive rows is
-// contiguous.  With a row map, output row t is x's row rowmap[t] (the routed experts'
-// input in permuted order, from the rows themselves rather than from their planes,
-// whose 16-byte pieces of one row lie T*16 bytes apart).  For bf16 rows the lo parts are zero and no GEMM reads plane 1 (they take
+// contiguous.  For bf16 rows the lo parts are zero and no GEMM reads plane 1 (they take
 // one column per token, HL = 1): it is not written.  A workgroup transposes a tile of
 // SP_T tokens by SP_G k-groups through LDS, so that both its reads (along the rows) and
 // its writes (along the tokens of a k-group) are contiguous.  Block 0 also clears the
@@ -49,8 +47,7 @@ static inline unsigned pf_split_grid(int T, int H)
 }
 
 __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int T, int H,
-                                                  int ldx, uint16_t *xg, int *counts, int E,
-                                                  const int *rowmap)
+                                                  int ldx, uint16_t *xg, int *counts, int E)
 {
     __shared__ u32x4 sh[2][SP_G][SP_T + 1];
     if (blockIdx.x == 0 && counts)
@@ -62,7 +59,7 @@ __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int
         const int i = j * PF_NT + threadIdx.x, r = i / SP_G, g = i % SP_G;
         const int t = t0 + r, gi = g0 + g;
         u32x4 h = {0u, 0u, 0u, 0u}, l = {0u, 0u, 0u, 0u};
-        const size_t src = (size_t)(t < T && rowmap ? rowmap[t] : t) * ldx + (size_t)gi * 8;
+        const size_t src = (size_t)t * ldx + (size_t)gi * 8;
         if (t < T && gi < G8 && x_bf16) {
             h = *(const u32x4 *)((const uint16_t *)x + src);        // bf16: hi = x, lo = 0
         } else if (t < T && gi < G8) {
@@ -88,6 +85,68 @@ __global__ void __launch_bounds__(PF_NT) pf_split(const void *x, int x_bf16, int
         if (t < T && gi < G8) {
             *(u32x4 *)(xg + ((size_t)gi * T + t) * 8) = sh[0][g][r];
             if (!x_bf16) *(u32x4 *)(xg + ((size_t)(G8 + gi) * T + t) * 8) = sh[1][g][r];
+        }
+    }
+}
+
+// ------------------------------------------------------------------ gather
+// The routed experts' input planes in permuted order: xg[h][g][p][8] = part h of
+// x[rowmap[p]][8g .. 8g+7], the layout pf_split writes, for TK rows.  A lane owns one
+// permuted row p (consecutive lanes, consecutive p: each store of a k-group is 1 KB
+// contiguous per wave) and walks PG_GS k-groups of its source row, eight at a time: the
+// eight 16-byte pieces of a row's consecutive k-groups (32-byte for fp32 rows) share
+// cache lines, so the walk reads every line once.  The row map is read once per lane
+// and no LDS transpose is needed.
+#define PG_GS 56
+
+static inline unsigned pf_gather_grid(int TK, int H)
+{
+    const int ns = ((H >> 3) + PG_GS - 1) / PG_GS;
+    return (unsigned)((((TK + WAVE - 1) / WAVE) * ns + PF_NT / WAVE - 1) / (PF_NT / WAVE));
+}
+
+__global__ void __launch_bounds__(PF_NT) pf_gather(const void *x, int x_bf16, int TK, int H,
+                                                   int ldx, uint16_t *xg, const int *rowmap)
+{
+    const int G8 = H >> 3, ns = (G8 + PG_GS - 1) / PG_GS;
+    const int w = blockIdx.x * (PF_NT / WAVE) + (int)(threadIdx.x / WAVE);
+    const int pb = w / ns, sl = w % ns;
+    const int p = pb * WAVE + (int)(threadIdx.x % WAVE);
+    if (p >= TK) return;
+    const size_t row = (size_t)rowmap[p] * ldx;
+    const int g0 = sl * PG_GS, g1 = min(G8, g0 + PG_GS);
+    const size_t plane = (size_t)G8 * TK * 8;
+    // G8 is a multiple of 16 (H of 128), so every step of 8 k-groups is whole
+    for (int g = g0; g < g1; g += 8) {
+        if (x_bf16) {
+            u32x4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = ld16((const uint16_t *)x + row + (size_t)(g + j) * 8);
+#pragma unroll
+            for (int j = 0; j < 8; j++) *(u32x4 *)(xg + ((size_t)(g + j) * TK + p) * 8) = v[j];
+        } else {
+            f32x4 v[8][2];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float *src = (const float *)x + row + (size_t)(g + j) * 8;
+                v[j][0] = *(const f32x4 *)src;
+                v[j][1] = *(const f32x4 *)(src + 4);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                uint32_t hi[8], lo[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) split_bf16(v[j][k >> 2][k & 3], hi[k], lo[k]);
+                u32x4 h, l;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    h[k] = hi[2 * k] | (hi[2 * k + 1] << 16);
+                    l[k] = lo[2 * k] | (lo[2 * k + 1] << 16);
+                }
+                const size_t o = ((size_t)(g + j) * TK + p) * 8;
+                *(u32x4 *)(xg + o) = h;
+                *(u32x4 *)(xg + plane + o) = l;
+            }
         }
     }
 }
@@ -1307,7 +1366,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     int rc;
 
     hipLaunchKernelGGL(pf_split, dim3(pf_split_grid(T, H)), dim3(PF_NT), 0, s,
-                       x, x_bf16, T, H, H, B->xhl, B->counts, E, (const int *)NULL);
+                       x, x_bf16, T, H, H, B->xhl, B->counts, E);
     if ((rc = launch_ok())) return rc;
 
     // The shared expert (bf16 weights, every token) needs only the split activations: its
@@ -1414,8 +1473,8 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         // the routed input's planes in permuted order, from x's rows (z's in the latent
         // form), so that one k-group of an expert's segment is contiguous
         const void *src = L->lat ? (const void *)B->zf : x;
-        hipLaunchKernelGGL(pf_split, dim3(pf_split_grid(TK, X)), dim3(PF_NT), 0, s,
-                           src, L->lat ? 0 : x_bf16, TK, X, X, B->xp, (int *)NULL, 0, B->perm_tok);
+        hipLaunchKernelGGL(pf_gather, dim3(pf_gather_grid(TK, X)), dim3(PF_NT), 0, s,
+                           src, L->lat ? 0 : x_bf16, TK, X, X, B->xp, B->perm_tok);
     }
     if ((rc = launch_ok())) PF_RET(rc);
 
@@ -1601,7 +1660,7 @@ extern "C" int k3x_dev_trunk_gemm(const uint16_t *W, int in, int out, float *y, 
     hipStream_t s = (hipStream_t)stream;
     const int x_bf16 = (x_dtype == K3X_BF16), HL = x_bf16 ? 1 : 2;
     hipLaunchKernelGGL(pf_split, dim3(pf_split_grid(T, in)), dim3(PF_NT), 0, s,
-                       x, x_bf16, T, in, ldx, planes, (int *)NULL, 0, (const int *)NULL);
+                       x, x_bf16, T, in, ldx, planes, (int *)NULL, 0);
     int rc = launch_ok();
     if (rc) return rc;
     PfGemmArgs g;

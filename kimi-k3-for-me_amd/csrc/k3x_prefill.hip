@@ -889,9 +889,8 @@ __device__ __forceinline__ uint32_t e4m3_rne(float v)
     return sign | (m == 16u ? (uint32_t)(E + 8) << 3 : ((uint32_t)(E + 7) << 3) | (m - 8u));
 }
 
-// SiTU out of line: its capped form evaluates tanh in double, whose inlined expansion
-// over the sixteen values of a quantisation block would take the registers the
-// accumulators need
+// SiTU out of line: its inlined expansion over the sixteen values of a quantisation block
+// would take the registers the accumulators need
 __device__ __attribute__((noinline)) float situ_call(float g, float u, float b1, float b2)
 {
     return situ(g, u, b1, b2);

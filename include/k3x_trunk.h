@@ -9,11 +9,14 @@
  *                       int out, int T);                              k3.h:480-484
  *
  * Y[t*ldy + o] = W[o] . X[t*ldx] for t < T, W bf16 [out][in] (K3_WBF16).  Here a matrix
- * is uploaded once (re-laid out for the matrix cores) and applied on the device: T <= 8
- * rows stream the matrix once through a GEMV on the matrix cores, larger T run a GEMM
- * over hi/lo bf16 planes of X.  Products are exact (bf16 weights, X split into hi + lo
- * bf16), accumulation is fp32 (the reference accumulates in double), so results agree
- * with the reference to fp32 rounding rather than bit for bit.
+ * is uploaded once and applied on the device: T <= 8 rows stream it once through a GEMV
+ * on the matrix cores (over a copy re-laid out for them), larger T run a plain GEMM on
+ * hipBLASLt (over the row-major copy; fp32 X as two bf16 GEMMs, its hi parts, then its lo
+ * parts accumulated), or the library's absence, the hand-written dense GEMM.  The handle
+ * holds both copies (4 bytes per weight).  Products are exact (bf16 weights, X split into
+ * hi + lo bf16), accumulation is fp32 (the reference accumulates in double), so results
+ * agree with the reference to fp32 rounding rather than bit for bit; a call repeats its
+ * bits exactly (one kernel per shape, chosen at the shape's first call).
  */
 #ifndef K3X_TRUNK_H
 #define K3X_TRUNK_H

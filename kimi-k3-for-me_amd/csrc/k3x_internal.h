@@ -267,6 +267,15 @@ int k3x_dev_trunk_gemm(const uint16_t *W, int in, int out, float *y, int ldy, co
                        int x_dtype, int ldx, int T, uint16_t *planes, void *stream);
 int k3x_dev_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
                     void *stream);
+/* fp32 rows [T][ldx] -> bf16 hi and lo rows [T][n] (hi + lo = 16 significant bits of x) */
+int k3x_dev_split_rows(const float *x, int ldx, int T, int n, uint16_t *hi, uint16_t *lo,
+                       void *stream);
+/* plain bf16 GEMMs on hipBLASLt (k3x_blas.cpp): k3x_blas_init once per device, outside
+ * graph capture; then Y[t*ldy + o] (+)= W[o] . X[t*ldx], W row-major bf16 [out][in], X
+ * bf16 rows, Y fp32.  Non-zero when no kernel serves the shape (the caller falls back). */
+int k3x_blas_init(int device);
+int k3x_blas_gemm_bf16(int device, const uint16_t *W, int in, int out, float *Y, int ldy,
+                       const uint16_t *X, int ldx, int T, int accumulate, void *stream);
 
 #ifdef __cplusplus
 }

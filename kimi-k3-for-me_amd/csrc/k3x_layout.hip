@@ -276,6 +276,42 @@ extern "C" int k3x_dev_dequant_fp4(float *out, const uint8_t *src, int R, int K,
     return launch_ok();
 }
 
+// fp32 rows -> bf16 hi and lo rows (the GEMM operands of fp32 activations), eight
+// elements a thread: two 16-byte reads, two 16-byte writes
+__global__ void split_rows_kernel(const float *x, int ldx, int T, int n, uint16_t *hi,
+                                  uint16_t *lo)
+{
+    const int n8 = n >> 3;
+    const long total = (long)T * n8;
+    for (long f = blockIdx.x * (long)blockDim.x + threadIdx.x; f < total;
+         f += (long)gridDim.x * blockDim.x) {
+        const int t = (int)(f / n8), c = (int)(f % n8) * 8;
+        const float *src = x + (size_t)t * ldx + c;
+        const f32x4 a = *(const f32x4 *)src, b = *(const f32x4 *)(src + 4);
+        uint32_t h[8], l[8];
+        for (int k = 0; k < 4; k++) {
+            split_bf16(a[k], h[k], l[k]);
+            split_bf16(b[k], h[4 + k], l[4 + k]);
+        }
+        u32x4 hv, lv;
+        for (int k = 0; k < 4; k++) {
+            hv[k] = h[2 * k] | (h[2 * k + 1] << 16);
+            lv[k] = l[2 * k] | (l[2 * k + 1] << 16);
+        }
+        *(u32x4 *)(hi + (size_t)t * n + c) = hv;
+        *(u32x4 *)(lo + (size_t)t * n + c) = lv;
+    }
+}
+
+extern "C" int k3x_dev_split_rows(const float *x, int ldx, int T, int n, uint16_t *hi,
+                                  uint16_t *lo, void *stream)
+{
+    const long total = (long)T * (n >> 3);
+    hipLaunchKernelGGL(split_rows_kernel, dim3(grid_for(total, NT)), dim3(NT), 0,
+                       (hipStream_t)stream, x, ldx, T, n, hi, lo);
+    return launch_ok();
+}
+
 extern "C" int k3x_dev_tile_bf16(uint16_t *dst, const uint16_t *src, int R, int K,
                                  void *stream)
 {

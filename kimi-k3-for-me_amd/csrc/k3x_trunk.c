@@ -1,5 +1,8 @@
 /* k3x_trunk.c - host side of the trunk's bf16 products (include/k3x_trunk.h): upload and
- * tiling of a matrix, argument checks, the workspace, the host-pointer form. */
+ * tiling of a matrix, argument checks, the workspace, the host-pointer form.  T <= 8 rows
+ * run the GEMV on the tiled copy; more rows run a plain GEMM on hipBLASLt over a row-major
+ * copy (k3x_blas.cpp; fp32 rows as two bf16 GEMMs, hi then lo accumulated), or the
+ * hand-written dense GEMM over the tiled copy when the library offers no kernel. */
 #include "k3x_internal.h"
 #include "../../include/k3x_trunk.h"
 
@@ -11,6 +14,8 @@
 struct k3x_trunk {
     int       device, in, out;
     uint16_t *w;              /* tiled bf16 [out][in]                        */
+    uint16_t *wr;             /* row-major bf16 [out][in] (the library GEMM)  */
+    int       blas;           /* the library GEMM is available               */
     uint16_t *planes;         /* workspace for T > K3X_DECODE_MAX_T           */
     size_t    planes_bytes;
     uint16_t *retired[TRUNK_RETIRED];   /* earlier workspaces: a graph recorded over
@@ -70,7 +75,9 @@ int k3x_trunk_create(const uint16_t *W, int in, int out, int device, k3x_trunk *
     if (hipMemcpy(stage, W, n, hipMemcpyHostToDevice) != hipSuccess) goto fail;
     if ((rc = k3x_dev_tile_bf16(m->w, (const uint16_t *)stage, out, in, NULL))) goto fail;
     if (hipDeviceSynchronize() != hipSuccess) { rc = K3X_E_HIP; goto fail; }
-    hipFree(stage);
+    /* the row-major upload stays as the library GEMM's operand */
+    m->wr = (uint16_t *)stage;
+    m->blas = k3x_blas_init(device) == 0;
     *t = m;
     return 0;
 fail:
@@ -85,6 +92,7 @@ void k3x_trunk_destroy(k3x_trunk *t)
     hipSetDevice(t->device);
     hipDeviceSynchronize();
     if (t->w) hipFree(t->w);
+    if (t->wr) hipFree(t->wr);
     if (t->planes) hipFree(t->planes);
     for (int i = 0; i < t->nretired; i++) hipFree(t->retired[i]);
     if (t->hx) hipFree(t->hx);
@@ -103,8 +111,28 @@ int k3x_trunk_apply(k3x_trunk *t, float *Y, int ldy, const void *X, int x_dtype,
         return k3x_dev_trunk_gemv(t->w, t->in, t->out, Y, ldy, X, x_dtype, ldx, T, stream);
     const size_t need = (size_t)T * t->in * 4;
     if (need > ((size_t)1 << 31)) return K3X_E_SHAPE;      /* 32-bit buffer offsets */
-    const int rc = trunk_workspace(t, need, stream);
+    int rc = trunk_workspace(t, need, stream);
     if (rc) return rc;
+    if (t->blas) {
+        if (x_dtype == K3X_BF16) {
+            rc = k3x_blas_gemm_bf16(t->device, t->wr, t->in, t->out, Y, ldy,
+                                    (const uint16_t *)X, ldx, T, 0, stream);
+        } else {
+            /* X = hi + lo: Y = W.hi, then Y += W.lo */
+            uint16_t *hi = t->planes, *lo = t->planes + (size_t)T * t->in;
+            rc = k3x_dev_split_rows((const float *)X, ldx, T, t->in, hi, lo, stream);
+            if (!rc)
+                rc = k3x_blas_gemm_bf16(t->device, t->wr, t->in, t->out, Y, ldy, hi, t->in,
+                                        T, 0, stream);
+            if (!rc)
+                rc = k3x_blas_gemm_bf16(t->device, t->wr, t->in, t->out, Y, ldy, lo, t->in,
+                                        T, 1, stream);
+        }
+        if (rc != K3X_E_HIP) return rc;
+        /* a shape the library does not serve (the same answer for every call of that
+         * shape): the dense kernel computes the whole product instead, over Y */
+        if (hipGetLastError() != hipSuccess) return K3X_E_HIP;
+    }
     return k3x_dev_trunk_gemm(t->w, t->in, t->out, Y, ldy, X, x_dtype, ldx, T, t->planes,
                               stream);
 }

@@ -13,13 +13,17 @@ static long  n_malloc, n_free;     /* calls made                                
 static void *live[256];            /* allocations not yet freed                   */
 static int   n_live;
 static void *last_planes;          /* the workspace the last GEMM launch was given */
-static long  n_gemm, n_gemv;
+static long  n_gemm, n_gemv;       /* products of more than / at most 8 rows      */
+static int   blas;                 /* what k3x_blas_init reports: library present */
+static long  n_blas;               /* library GEMM calls                           */
 
 void mock_reset(void)
 {
     capturing = 0; n_malloc = n_free = 0; n_live = 0; last_planes = NULL;
-    n_gemm = n_gemv = 0;
+    n_gemm = n_gemv = 0; n_blas = 0;
 }
+void  mock_set_blas(int on) { blas = on; }
+long  mock_blas_calls(void) { return n_blas; }
 void  mock_set_capturing(int on) { capturing = on; }
 long  mock_mallocs(void) { return n_malloc; }
 long  mock_frees(void) { return n_free; }
@@ -66,6 +70,26 @@ hipError_t hipStreamIsCapturing(hipStream_t s, hipStreamCaptureStatus *st)
 }
 
 int k3x_dev_check(int device) { (void)device; return 0; }
+hipError_t hipGetLastError(void) { return hipSuccess; }
+int k3x_blas_init(int device) { (void)device; return blas ? 0 : -5; }
+int k3x_blas_gemm_bf16(int device, const uint16_t *W, int in, int out, float *Y, int ldy,
+                       const uint16_t *X, int ldx, int T, int accumulate, void *stream)
+{
+    (void)device; (void)W; (void)in; (void)out; (void)Y; (void)ldy; (void)X; (void)ldx;
+    (void)T; (void)accumulate; (void)stream;
+    n_blas++;
+    return 0;
+}
+/* the fp32 rows' split into the workspace: the library path's one use of it (counted as
+ * that path's product, with the workspace it was given) */
+int k3x_dev_split_rows(const float *x, int ldx, int T, int n, uint16_t *hi, uint16_t *lo,
+                       void *stream)
+{
+    (void)x; (void)ldx; (void)T; (void)n; (void)lo; (void)stream;
+    n_gemm++;
+    last_planes = hi;
+    return 0;
+}
 int k3x_dev_tile_bf16(uint16_t *dst, const uint16_t *src, int R, int K, void *stream)
 {
     (void)stream;

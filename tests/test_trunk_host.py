@@ -2,7 +2,9 @@
 runtime (tests/mock/hip_mock.c): the workspace of calls past eight rows grows (at least
 doubling) outside capture only; a call that would grow it on a stream under capture
 returns K3X_E_SHAPE and launches nothing; an outgrown workspace is retired, not freed,
-so a graph captured over it stays valid, and destroy frees every generation."""
+so a graph captured over it stays valid, and destroy frees every generation.  Both
+product paths are covered: the library GEMM (fp32 rows split into the workspace, then two
+bf16 GEMMs) and the dense kernel used where the library is absent."""
 import ctypes as C
 import os
 import shutil
@@ -37,8 +39,10 @@ def mock(tmp_path_factory):
     return lib
 
 
-def test_workspace_growth_capture_and_retirement(mock):
+@pytest.mark.parametrize("blas", [0, 1])
+def test_workspace_growth_capture_and_retirement(mock, blas):
     mock.mock_reset()
+    mock.mock_set_blas(blas)
     IN, OUT = 256, 32
     W = np.zeros((OUT, IN), np.uint16)
     t = C.c_void_p()
@@ -72,6 +76,8 @@ def test_workspace_growth_capture_and_retirement(mock):
     p = mock.mock_last_planes()
     assert p != p32 and p != p16 and mock.mock_is_live(p32) and mock.mock_is_live(p16)
     mock.mock_set_capturing(0)
+    # the library path: two GEMMs (hi, then lo accumulated) per product past 8 rows
+    assert mock.mock_blas_calls() == (2 * mock.mock_gemms() if blas else 0)
     live = mock.mock_live()
     frees = mock.mock_frees()
     mock.k3x_trunk_destroy(t)

@@ -1,9 +1,11 @@
 // k3x_blas.cpp - plain bf16 GEMMs on hipBLASLt: the trunk products of more than eight
-// rows (k3_mmw_batch_ld, k3.h:457-478), Y[t*ldy + o] = sum_k W[o][k] X[t*ldx + k] with W
-// and X bf16, Y fp32, accumulated in fp32 on the matrix cores.  These products carry no
-// fused epilogue, so the library's tuned GEMMs serve them (about 1.6 PFLOP/s at 2048 x
-// 7168 x 7168 on gfx950, against 0.77 for the hand-written dense kernel, which keeps the
-// fused products: the shared experts, the latent projections).
+// rows (k3_mmw_batch_ld, k3.h:457-478) and the prefill shared expert's products
+// (moe_shared, k3_ops.c:1848-1860), Y[t*ldy + o] = sum_k W[o][k] X[t*ldx + k] with W and X
+// bf16, Y fp32, accumulated in fp32 on the matrix cores.  These products carry no fused
+// epilogue (the shared expert's SiTU runs as its own small kernel between them), so the
+// library's tuned GEMMs serve them: about 1.2 PFLOP/s at 2048 x 7168 x 7168 on gfx950,
+// against 0.77 for the hand-written dense kernel, which keeps the products whose
+// epilogues feed the routed GEMMs' layouts.
 //
 // One handle per device, created with the first matrix uploaded to it.  The algorithm of
 // a shape (in, out, T, accumulate) is chosen once, for packed rows, among those that need
@@ -82,14 +84,9 @@ extern "C" int k3x_blas_init(int device)
     return 0;
 }
 
-extern "C" int k3x_blas_gemm_bf16(int device, const uint16_t *W, int in, int out, float *Y,
-                                  int ldy, const uint16_t *X, int ldx, int T, int accumulate,
-                                  void *stream)
+// The kept kernel of a shape, chosen at its first use (g_mu held)
+static const Shape *shape_of(Dev &d, int in, int out, int T, int accumulate)
 {
-    if (device < 0 || device >= kMaxDevices) return K3X_E_ARG;
-    std::lock_guard<std::mutex> g(g_mu);
-    Dev &d = g_dev[device];
-    if (!d.h) return K3X_E_HIP;
     const auto key = std::make_tuple(in, out, T, accumulate ? 1 : 0);
     auto it = d.shapes.find(key);
     if (it == d.shapes.end()) {
@@ -114,12 +111,33 @@ extern "C" int k3x_blas_gemm_bf16(int device, const uint16_t *W, int in, int out
         if (pref) hipblasLtMatmulPreferenceDestroy(pref);
         it = d.shapes.emplace(key, sh).first;
     }
-    if (!it->second.ok) return K3X_E_HIP;
+    return &it->second;
+}
+
+extern "C" int k3x_blas_ready(int device, int in, int out, int T, int accumulate)
+{
+    if (device < 0 || device >= kMaxDevices) return K3X_E_ARG;
+    std::lock_guard<std::mutex> g(g_mu);
+    Dev &d = g_dev[device];
+    if (!d.h) return K3X_E_HIP;
+    return shape_of(d, in, out, T, accumulate)->ok ? 0 : K3X_E_HIP;
+}
+
+extern "C" int k3x_blas_gemm_bf16(int device, const uint16_t *W, int in, int out, float *Y,
+                                  int ldy, const uint16_t *X, int ldx, int T, int accumulate,
+                                  void *stream)
+{
+    if (device < 0 || device >= kMaxDevices) return K3X_E_ARG;
+    std::lock_guard<std::mutex> g(g_mu);
+    Dev &d = g_dev[device];
+    if (!d.h) return K3X_E_HIP;
+    const Shape *sh = shape_of(d, in, out, T, accumulate);
+    if (!sh->ok) return K3X_E_HIP;
     Desc dc;
     if (!dc.make(in, out, T, ldx, ldy)) return K3X_E_HIP;
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
     const hipblasStatus_t st =
         hipblasLtMatmul(d.h, dc.md, &alpha, W, dc.la, X, dc.lb, &beta, Y, dc.lc, Y, dc.lc,
-                        &it->second.algo, nullptr, 0, (hipStream_t)stream);
+                        &sh->algo, nullptr, 0, (hipStream_t)stream);
     return st == HIPBLAS_STATUS_SUCCESS ? 0 : K3X_E_HIP;
 }

@@ -142,6 +142,11 @@ struct k3x_moe_layer {
                                      scale byte outside 1..252 (the exact dequantisation
                                      kernels are launched) */
     uint16_t *sh_gate, *sh_up, *sh_down;   /* tiled bf16, NULL when SI == 0 */
+    /* row-major bf16 copies for the prefill's library GEMMs, when 2*SI <= hidden (the
+     * gate/up output then fits the shared rows of the prefill's output buffer): gate rows
+     * then up rows [2*SI][H], and down [H][SI]; NULL otherwise */
+    uint16_t *sh_gu_rm, *sh_down_rm;
+    int       blas;                         /* hipBLASLt is available on the device */
     uint16_t *ldown, *lup;        /* latent projections, tiled bf16 [XL][H] and [H][XL] */
     float    *lnw;                /* [XL] latent RMSNorm weights, or NULL */
     /* decode working buffers */
@@ -267,6 +272,10 @@ int k3x_dev_trunk_gemm(const uint16_t *W, int in, int out, float *y, int ldy, co
                        int x_dtype, int ldx, int T, uint16_t *planes, void *stream);
 int k3x_dev_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
                     void *stream);
+/* the prefill shared expert's activation from its library gate/up product: ygu [T][2*SI]
+ * fp32 (gate columns, then up) -> SiTU, split into bf16 hi and lo rows [T][SI] */
+int k3x_dev_glu_rows(const float *ygu, int T, int SI, float b1, float b2, uint16_t *hi,
+                     uint16_t *lo, void *stream);
 /* fp32 rows [T][ldx] -> bf16 hi and lo rows [T][n] (hi + lo = 16 significant bits of x) */
 int k3x_dev_split_rows(const float *x, int ldx, int T, int n, uint16_t *hi, uint16_t *lo,
                        void *stream);
@@ -274,6 +283,8 @@ int k3x_dev_split_rows(const float *x, int ldx, int T, int n, uint16_t *hi, uint
  * graph capture; then Y[t*ldy + o] (+)= W[o] . X[t*ldx], W row-major bf16 [out][in], X
  * bf16 rows, Y fp32.  Non-zero when no kernel serves the shape (the caller falls back). */
 int k3x_blas_init(int device);
+/* 0 when a kernel serves the shape (chosen now and kept; nothing is enqueued) */
+int k3x_blas_ready(int device, int in, int out, int T, int accumulate);
 int k3x_blas_gemm_bf16(int device, const uint16_t *W, int in, int out, float *Y, int ldy,
                        const uint16_t *X, int ldx, int T, int accumulate, void *stream);
 

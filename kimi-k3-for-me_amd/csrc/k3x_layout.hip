@@ -303,6 +303,35 @@ __global__ void split_rows_kernel(const float *x, int ldx, int T, int n, uint16_
     }
 }
 
+// The shared expert's activation from its gate/up product rows: ygu [T][2*SI] fp32 (gate
+// columns 0 .. SI-1, up columns SI .. 2*SI-1) -> SiTU (as k3_situ_glu, k3_ops.c:148-161)
+// split into bf16 hi and lo rows [T][SI], four elements a thread
+__global__ void glu_rows_kernel(const float *ygu, int T, int SI, float b1, float b2,
+                                uint16_t *hi, uint16_t *lo)
+{
+    const int n4 = SI >> 2;
+    const long total = (long)T * n4;
+    for (long f = blockIdx.x * (long)blockDim.x + threadIdx.x; f < total;
+         f += (long)gridDim.x * blockDim.x) {
+        const int t = (int)(f / n4), c = (int)(f % n4) * 4;
+        const float *row = ygu + (size_t)t * 2 * SI;
+        const f32x4 g = *(const f32x4 *)(row + c), u = *(const f32x4 *)(row + SI + c);
+        uint32_t h[4], l[4];
+        for (int k = 0; k < 4; k++) split_bf16(situ(g[k], u[k], b1, b2), h[k], l[k]);
+        *(u32x2 *)(hi + (size_t)t * SI + c) = (u32x2){h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        *(u32x2 *)(lo + (size_t)t * SI + c) = (u32x2){l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+    }
+}
+
+extern "C" int k3x_dev_glu_rows(const float *ygu, int T, int SI, float b1, float b2,
+                                uint16_t *hi, uint16_t *lo, void *stream)
+{
+    const long total = (long)T * (SI >> 2);
+    hipLaunchKernelGGL(glu_rows_kernel, dim3(grid_for(total, NT)), dim3(NT), 0,
+                       (hipStream_t)stream, ygu, T, SI, b1, b2, hi, lo);
+    return launch_ok();
+}
+
 extern "C" int k3x_dev_split_rows(const float *x, int ldx, int T, int n, uint16_t *hi,
                                   uint16_t *lo, void *stream)
 {

@@ -104,6 +104,10 @@ static int layer_alloc(k3x_moe_layer *L)
         RCCHK(dmalloc((void **)&L->sh_gate, k3x_bf16_matrix_bytes(L->SI, H), b));
         RCCHK(dmalloc((void **)&L->sh_up, k3x_bf16_matrix_bytes(L->SI, H), b));
         RCCHK(dmalloc((void **)&L->sh_down, k3x_bf16_matrix_bytes(H, L->SI), b));
+        if (2 * L->SI <= H) {
+            RCCHK(dmalloc((void **)&L->sh_gu_rm, (size_t)2 * L->SI * H * 2, b));
+            RCCHK(dmalloc((void **)&L->sh_down_rm, (size_t)H * L->SI * 2, b));
+        }
         RCCHK(dmalloc((void **)&L->shB, (size_t)L->SI * 2 * K3X_DECODE_MAX_T * 2, b));
         if (hipStreamCreateWithFlags((hipStream_t *)&L->pf_side, hipStreamNonBlocking) !=
                 hipSuccess ||
@@ -155,6 +159,8 @@ static int layer_alloc(k3x_moe_layer *L)
     RCCHK(dmalloc((void **)&L->xB, hs * 2 * K3X_DECODE_MAX_T * 2, b));
     RCCHK(dmalloc((void **)&L->actB, (size_t)K3X_DECODE_MAX_T * K * is * 2 * K3X_DECODE_MAX_T * 2, b));
     if (hipMemset(L->bias, 0, (size_t)E * 4) != hipSuccess) return K3X_E_HIP;
+    /* the prefill's shared-expert products run on the library where it is present */
+    L->blas = L->sh_gu_rm && k3x_blas_init(L->device) == 0;
     return 0;
 fail:
     return rc;
@@ -164,6 +170,7 @@ static void layer_free(k3x_moe_layer *L)
 {
     if (!L) return;
     void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shB,
+                 L->sh_gu_rm, L->sh_down_rm,
                  L->score, L->choice, L->slack, L->idx, L->wt, L->route,
                  L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out,
                  L->ldown, L->lup, L->lnw, L->zB, L->accL, L->latB, L->tr,
@@ -233,7 +240,8 @@ static int new_layer_slots(const k3x_cfg *c, int device, int nslot, k3x_moe_laye
     return 0;
 }
 
-/* Shared expert upload: three bf16 matrices, re-laid out on the device. */
+/* Shared expert upload: three bf16 matrices, re-laid out on the device (and kept
+ * row-major as well where the layer holds those copies). */
 static int upload_shared(k3x_moe_layer *L, const uint16_t *sh1, const uint16_t *sh3,
                          const uint16_t *sh2)
 {
@@ -242,16 +250,20 @@ static int upload_shared(k3x_moe_layer *L, const uint16_t *sh1, const uint16_t *
     void *stage = NULL;
     if (SI <= 0) return 0;
     if (!sh1 || !sh3 || !sh2) return K3X_E_ARG;
-    const size_t n = (size_t)SI * H * 2;
-    HIPCHK(hipMalloc(&stage, n));
-    HIPCHK(hipMemcpy(stage, sh1, n, hipMemcpyHostToDevice));
-    RCCHK(k3x_dev_tile_bf16(L->sh_gate, (const uint16_t *)stage, SI, H, NULL));
+    const size_t n = (size_t)SI * H * 2, ne = (size_t)SI * H;
+    uint16_t *g = L->sh_gu_rm, *u = L->sh_gu_rm ? L->sh_gu_rm + ne : NULL, *d = L->sh_down_rm;
+    if (!g) {
+        HIPCHK(hipMalloc(&stage, n));
+        g = u = d = (uint16_t *)stage;
+    }
+    HIPCHK(hipMemcpy(g, sh1, n, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_bf16(L->sh_gate, g, SI, H, NULL));
     HIPCHK(hipDeviceSynchronize());
-    HIPCHK(hipMemcpy(stage, sh3, n, hipMemcpyHostToDevice));
-    RCCHK(k3x_dev_tile_bf16(L->sh_up, (const uint16_t *)stage, SI, H, NULL));
+    HIPCHK(hipMemcpy(u, sh3, n, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_bf16(L->sh_up, u, SI, H, NULL));
     HIPCHK(hipDeviceSynchronize());
-    HIPCHK(hipMemcpy(stage, sh2, n, hipMemcpyHostToDevice));
-    RCCHK(k3x_dev_tile_bf16(L->sh_down, (const uint16_t *)stage, H, SI, NULL));
+    HIPCHK(hipMemcpy(d, sh2, n, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_bf16(L->sh_down, d, H, SI, NULL));
     HIPCHK(hipDeviceSynchronize());
 fail:
     if (stage) hipFree(stage);

@@ -1375,12 +1375,39 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     // against 3.83, 3.88 and 3.91 ms at 2048 tokens).  Its T rows follow the TK routed rows
     // in y, which nothing on s writes.
     bool forked = false;
+    // The library path (bf16 rows, 2*SI <= H, a kernel for each shape): the gate/up product
+    // into fp32 rows [T][2*SI] held in the shared rows of y (nothing else writes them before
+    // the down product, which overwrites them), SiTU into bf16 hi and lo rows [T][SI] (in
+    // act_sh), then the down product as two GEMMs, hi then lo accumulated, into the shared
+    // rows of y.
+    const bool sh_blas = SI > 0 && L->blas && x_bf16 &&
+                         k3x_blas_ready(L->device, H, 2 * SI, T, 0) == 0 &&
+                         k3x_blas_ready(L->device, SI, H, T, 0) == 0 &&
+                         k3x_blas_ready(L->device, SI, H, T, 1) == 0;
     auto fork_shared = [&]() -> int {
         if (SI <= 0) return 0;
         hipStream_t side = (hipStream_t)L->pf_side;
         if (hipEventRecord((hipEvent_t)L->pf_ev[0], s) != hipSuccess ||
             hipStreamWaitEvent(side, (hipEvent_t)L->pf_ev[0], 0) != hipSuccess)
             return K3X_E_HIP;
+        if (sh_blas) {
+            float *ysh = B->y + (size_t)TK * H;
+            uint16_t *ahi = B->act_sh, *alo = B->act_sh + (size_t)T * SI;
+            int r = k3x_blas_gemm_bf16(L->device, L->sh_gu_rm, H, 2 * SI, ysh, 2 * SI,
+                                       (const uint16_t *)x, H, T, 0, side);
+            if (!r) r = k3x_dev_glu_rows(ysh, T, SI, L->b1, L->b2, ahi, alo, side);
+            if (!r) r = k3x_blas_gemm_bf16(L->device, L->sh_down_rm, SI, H, ysh, H, ahi, SI, T, 0,
+                                           side);
+            if (!r) r = k3x_blas_gemm_bf16(L->device, L->sh_down_rm, SI, H, ysh, H, alo, SI, T, 1,
+                                           side);
+            if (hipEventRecord((hipEvent_t)L->pf_ev[1], side) != hipSuccess) return K3X_E_HIP;
+            if (r) {
+                (void)hipStreamWaitEvent(s, (hipEvent_t)L->pf_ev[1], 0);
+                return r;
+            }
+            forked = true;
+            return 0;
+        }
         PfGemmArgs sg;
         memset(&sg, 0, sizeof sg);
         sg.wm[0] = (const uint8_t *)L->sh_gate; sg.wm[1] = (const uint8_t *)L->sh_up;

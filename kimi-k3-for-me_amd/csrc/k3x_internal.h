@@ -146,6 +146,7 @@ struct k3x_moe_layer {
      * gate/up output then fits the shared rows of the prefill's output buffer): gate rows
      * then up rows [2*SI][H], and down [H][SI]; NULL otherwise */
     uint16_t *sh_gu_rm, *sh_down_rm;
+    uint16_t *ldown_rm, *lup_rm;            /* row-major latent projections [XL][H], [H][XL] */
     int       blas;                         /* hipBLASLt is available on the device */
     uint16_t *ldown, *lup;        /* latent projections, tiled bf16 [XL][H] and [H][XL] */
     float    *lnw;                /* [XL] latent RMSNorm weights, or NULL */

@@ -131,6 +131,8 @@ static int layer_alloc(k3x_moe_layer *L)
         const size_t xs = (size_t)(X + 511) / 512 * 512;
         RCCHK(dmalloc((void **)&L->ldown, k3x_bf16_matrix_bytes(X, H), b));
         RCCHK(dmalloc((void **)&L->lup, k3x_bf16_matrix_bytes(H, X), b));
+        RCCHK(dmalloc((void **)&L->ldown_rm, (size_t)X * H * 2, b));
+        RCCHK(dmalloc((void **)&L->lup_rm, (size_t)H * X * 2, b));
         RCCHK(dmalloc((void **)&L->zB, xs * 2 * K3X_DECODE_MAX_T * 2, b));
         const size_t np = K3X_WIDE_PMAX > K3X_DECODE_PARTS ? K3X_WIDE_PMAX : K3X_DECODE_PARTS;
         RCCHK(dmalloc((void **)&L->accL, np * K3X_DECODE_MAX_T * X * 4, b));
@@ -159,8 +161,9 @@ static int layer_alloc(k3x_moe_layer *L)
     RCCHK(dmalloc((void **)&L->xB, hs * 2 * K3X_DECODE_MAX_T * 2, b));
     RCCHK(dmalloc((void **)&L->actB, (size_t)K3X_DECODE_MAX_T * K * is * 2 * K3X_DECODE_MAX_T * 2, b));
     if (hipMemset(L->bias, 0, (size_t)E * 4) != hipSuccess) return K3X_E_HIP;
-    /* the prefill's shared-expert products run on the library where it is present */
-    L->blas = L->sh_gu_rm && k3x_blas_init(L->device) == 0;
+    /* the prefill's plain products (the shared expert's, the latent projections) run on
+     * the library where it is present */
+    L->blas = k3x_blas_init(L->device) == 0;
     return 0;
 fail:
     return rc;
@@ -170,7 +173,7 @@ static void layer_free(k3x_moe_layer *L)
 {
     if (!L) return;
     void *p[] = {L->router, L->bias, L->experts, L->sh_gate, L->sh_up, L->sh_down, L->shB,
-                 L->sh_gu_rm, L->sh_down_rm,
+                 L->sh_gu_rm, L->sh_down_rm, L->ldown_rm, L->lup_rm,
                  L->score, L->choice, L->slack, L->idx, L->wt, L->route,
                  L->xB, L->actB, L->pf.base, L->h_dev_x, L->h_dev_out,
                  L->ldown, L->lup, L->lnw, L->zB, L->accL, L->latB, L->tr,
@@ -278,7 +281,6 @@ static int upload_latent(k3x_moe_layer *L, const uint16_t *down, const uint16_t 
 {
     const int H = L->cfg.hidden, X = L->XL;
     int rc = 0;
-    void *stage = NULL;
     if (L->cfg.latent_norm) {
         if (!nw) return K3X_E_ARG;
         HIPCHK(hipMemcpy(L->lnw, nw, (size_t)X * 4, hipMemcpyHostToDevice));
@@ -286,15 +288,13 @@ static int upload_latent(k3x_moe_layer *L, const uint16_t *down, const uint16_t 
     if (!L->lat) return 0;
     if (!down || !up) return K3X_E_ARG;
     const size_t n = (size_t)X * H * 2;
-    HIPCHK(hipMalloc(&stage, n));
-    HIPCHK(hipMemcpy(stage, down, n, hipMemcpyHostToDevice));
-    RCCHK(k3x_dev_tile_bf16(L->ldown, (const uint16_t *)stage, X, H, NULL));
-    HIPCHK(hipDeviceSynchronize());
-    HIPCHK(hipMemcpy(stage, up, n, hipMemcpyHostToDevice));
-    RCCHK(k3x_dev_tile_bf16(L->lup, (const uint16_t *)stage, H, X, NULL));
+    /* the row-major uploads stay: the prefill's library products read them */
+    HIPCHK(hipMemcpy(L->ldown_rm, down, n, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_bf16(L->ldown, L->ldown_rm, X, H, NULL));
+    HIPCHK(hipMemcpy(L->lup_rm, up, n, hipMemcpyHostToDevice));
+    RCCHK(k3x_dev_tile_bf16(L->lup, L->lup_rm, H, X, NULL));
     HIPCHK(hipDeviceSynchronize());
 fail:
-    if (stage) hipFree(stage);
     return rc;
 }
 

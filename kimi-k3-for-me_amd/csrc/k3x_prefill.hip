@@ -1204,10 +1204,11 @@ __global__ void __launch_bounds__(NW * WAVE) pf_gemm_mx(PfGemmArgs a)
 // ------------------------------------------------------------------ latent norm
 // The latent form's aggregates (agg [T][X], one workgroup per token): RMSNorm with the
 // latent norm weights (k3_rmsnorm, k3_ops.c:132-140 and :1946; double sum of squares, inv
-// rounded to float, w*x*inv), or none when nw is NULL, then the hi/lo planes
-// [2][X/8][T][8] for the up projection (pf_split's layout).
+// rounded to float, w*x*inv), or none when nw is NULL, then the hi and lo parts for the
+// up projection: planes [2][X/8][T][8] (pf_split's layout) for the dense kernel, or with
+// rows set, rows [2][T][X] for the library GEMMs.
 __global__ void __launch_bounds__(PF_NT) pf_latnorm(const float *agg, const float *nw, float eps,
-                                                    int T, int X, uint16_t *hl)
+                                                    int T, int X, uint16_t *hl, int rows)
 {
     __shared__ double red[PF_NT / WAVE];
     __shared__ float s_inv;
@@ -1245,8 +1246,13 @@ __global__ void __launch_bounds__(PF_NT) pf_latnorm(const float *agg, const floa
             h[j] = hi[2 * j] | (hi[2 * j + 1] << 16);
             l[j] = lo[2 * j] | (lo[2 * j + 1] << 16);
         }
-        *(u32x4 *)(hl + ((size_t)gi * T + t) * 8) = h;
-        *(u32x4 *)(hl + ((size_t)(G8 + gi) * T + t) * 8) = l;
+        if (rows) {
+            *(u32x4 *)(hl + (size_t)t * X + (size_t)gi * 8) = h;
+            *(u32x4 *)(hl + ((size_t)T + t) * X + (size_t)gi * 8) = l;
+        } else {
+            *(u32x4 *)(hl + ((size_t)gi * T + t) * 8) = h;
+            *(u32x4 *)(hl + ((size_t)(G8 + gi) * T + t) * 8) = l;
+        }
     }
 }
 
@@ -1380,7 +1386,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     // the down product, which overwrites them), SiTU into bf16 hi and lo rows [T][SI] (in
     // act_sh), then the down product as two GEMMs, hi then lo accumulated, into the shared
     // rows of y.
-    const bool sh_blas = SI > 0 && L->blas && x_bf16 &&
+    const bool sh_blas = SI > 0 && L->blas && L->sh_gu_rm && x_bf16 &&
                          k3x_blas_ready(L->device, H, 2 * SI, T, 0) == 0 &&
                          k3x_blas_ready(L->device, SI, H, T, 0) == 0 &&
                          k3x_blas_ready(L->device, SI, H, T, 1) == 0;
@@ -1478,14 +1484,21 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
                        (int4 *)B->desc_gu, (int4 *)B->desc_dn);
     if ((rc = launch_ok())) PF_RET(rc);
     if (L->lat) {
-        // z = down . x for every token (k3_mmw_batch, k3_ops.c:1871), then its hi/lo planes
-        PfGemmArgs zg;
-        memset(&zg, 0, sizeof zg);
-        zg.wm[0] = (const uint8_t *)L->ldown; zg.R = X; zg.K = H; zg.n0 = T;
-        zg.bsrc = B->xhl; zg.brows = T; zg.row_base = 0;
-        zg.y = B->zf; zg.out_base = 0;
-        launch_dense<1, DENSE_RW, DENSE_CW, false>(zg, HLg, s);
-        if ((rc = launch_ok())) PF_RET(rc);
+        // z = down . x for every token (k3_mmw_batch, k3_ops.c:1871): a plain product, on
+        // the library where it serves the shape (bf16 rows), else the dense kernel
+        if (L->blas && x_bf16 && k3x_blas_ready(L->device, H, X, T, 0) == 0) {
+            if ((rc = k3x_blas_gemm_bf16(L->device, L->ldown_rm, H, X, B->zf, X,
+                                         (const uint16_t *)x, H, T, 0, s)))
+                PF_RET(rc);
+        } else {
+            PfGemmArgs zg;
+            memset(&zg, 0, sizeof zg);
+            zg.wm[0] = (const uint8_t *)L->ldown; zg.R = X; zg.K = H; zg.n0 = T;
+            zg.bsrc = B->xhl; zg.brows = T; zg.row_base = 0;
+            zg.y = B->zf; zg.out_base = 0;
+            launch_dense<1, DENSE_RW, DENSE_CW, false>(zg, HLg, s);
+            if ((rc = launch_ok())) PF_RET(rc);
+        }
     }
     // MXFP8 mode: the routed input quantised in permuted order, codes then scales in xp;
     // the gate/up output's codes then scales in act
@@ -1580,16 +1593,30 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         hipLaunchKernelGGL(pf_combine, dim3(cdiv((size_t)T * (X / 4), PF_NT)), dim3(PF_NT), 0, s,
                            B->y, B->pos_of, T, K, X, -1, (const float *)NULL, B->zf);
         if ((rc = launch_ok())) PF_RET(rc);
+        // the up projection: a plain product over the normalised aggregates' hi and lo
+        // parts, on the library where it serves the shapes (rows [T][X] of each part),
+        // else the dense kernel (k-group planes)
+        const bool up_blas = L->blas && k3x_blas_ready(L->device, X, H, T, 0) == 0 &&
+                             k3x_blas_ready(L->device, X, H, T, 1) == 0;
         hipLaunchKernelGGL(pf_latnorm, dim3(T), dim3(PF_NT), 0, s, B->zf,
-                           c->latent_norm ? L->lnw : (const float *)NULL, c->rms_eps, T, X, B->zhl);
+                           c->latent_norm ? L->lnw : (const float *)NULL, c->rms_eps, T, X, B->zhl,
+                           up_blas ? 1 : 0);
         if ((rc = launch_ok())) PF_RET(rc);
-        PfGemmArgs ug;
-        memset(&ug, 0, sizeof ug);
-        ug.wm[0] = (const uint8_t *)L->lup; ug.R = H; ug.K = X; ug.n0 = T;
-        ug.bsrc = B->zhl; ug.brows = T; ug.row_base = 0;
-        ug.y = B->y; ug.out_base = 0;
-        launch_dense<1, DENSE_RW, DENSE_CW, false>(ug, 2, s);
-        if ((rc = launch_ok())) PF_RET(rc);
+        if (up_blas) {
+            if ((rc = k3x_blas_gemm_bf16(L->device, L->lup_rm, X, H, B->y, H, B->zhl, X, T, 0,
+                                         s)) ||
+                (rc = k3x_blas_gemm_bf16(L->device, L->lup_rm, X, H, B->y, H,
+                                         B->zhl + (size_t)T * X, X, T, 1, s)))
+                PF_RET(rc);
+        } else {
+            PfGemmArgs ug;
+            memset(&ug, 0, sizeof ug);
+            ug.wm[0] = (const uint8_t *)L->lup; ug.R = H; ug.K = X; ug.n0 = T;
+            ug.bsrc = B->zhl; ug.brows = T; ug.row_base = 0;
+            ug.y = B->y; ug.out_base = 0;
+            launch_dense<1, DENSE_RW, DENSE_CW, false>(ug, 2, s);
+            if ((rc = launch_ok())) PF_RET(rc);
+        }
         pos = NULL;
         KC = 1;
     }

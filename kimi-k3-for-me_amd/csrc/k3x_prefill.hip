@@ -1304,6 +1304,21 @@ static void launch_topk(const PfTopkArgs &a, hipStream_t s)
 #define DN_RT32_S 2
 #define DN_CT32_S 2
 #define DN_CT32_B 3
+// The small class of a gate/up over hi and lo columns (fp32 input, or z in the latent
+// form): 32 tokens in two column tiles, eight waves of one 32-row tile (256 rows).  With
+// the single 16-token column tile of the bf16 shape, the K3 chunk's experts of 17 to 32
+// tokens (656 of 896) fell to the large class, one 96-KB-LDS workgroup a CU: 8.07 to 8.13
+// ms per chunk now against 8.39 to 8.49 (four waves of 128 rows: the same; four waves of
+// 256 rows, one wave a SIMD: 8.57 to 8.64).
+#ifndef NW_GS2
+#define NW_GS2    8
+#endif
+#ifndef GU_RT32_S2
+#define GU_RT32_S2 1
+#endif
+#ifndef GU_CT32_S2
+#define GU_CT32_S2 2
+#endif
 
 template <bool EXACT, int HL, int CT32, int NW, int RT32 = GU_RT32>
 static void launch_gu(const PfGemmArgs &a, unsigned grid, hipStream_t s)
@@ -1467,9 +1482,10 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     sa.counts = B->counts; sa.E = E; sa.offsets = B->offsets; sa.cursor = B->cursor;
     sa.tb[0] = B->tb_gu; sa.tb[1] = B->tb_dn;
     const bool mx = L->pf_mode == K3X_PREFILL_MXFP8;
-    sa.tpb_s[0] = mx ? MX_CT_S * 32 : GU_CT32_S * 32 / HLr;
+    sa.tpb_s[0] = mx ? MX_CT_S * 32 : (HLr == 1 ? GU_CT32_S : GU_CT32_S2) * 32 / HLr;
     sa.tpb_b[0] = mx ? MX_CT_B * 32 : GU_CT32_B * 32 / HLr;
-    sa.nrb_s[0] = cdiv(I, mx ? MX_NW * MX_GU_RT32_S * 32 : NW_GS * GU_RT32_S * 32);
+    sa.nrb_s[0] = cdiv(I, mx ? MX_NW * MX_GU_RT32_S * 32
+                             : (HLr == 1 ? NW_GS * GU_RT32_S : NW_GS2 * GU_RT32_S2) * 32);
     sa.nrb_b[0] = cdiv(I, (mx ? MX_NW : NW_B) * GU_RT32 * 32);
     sa.tpb_s[1] = mx ? MX_CT_S * 32 : DN_CT32_S * 32 / 2;
     sa.tpb_b[1] = mx ? MX_CT_B * 32 : DN_CT32_B * 32 / 2;
@@ -1559,10 +1575,10 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         hipLaunchKernelGGL((pf_gemm_mx<2, MX_GU_RT32_S, MX_CT_S, true, MX_NW>), dim3(grid_s[0]), dim3(MX_NW * WAVE), 0, s, g);
     } else if (ex_gu) {
         if (HLr == 1) launch_gu<true, 1, GU_CT32_S, NW_GS, GU_RT32_S>(g, grid_s[0], s);
-        else          launch_gu<true, 2, GU_CT32_S, NW_GS, GU_RT32_S>(g, grid_s[0], s);
+        else          launch_gu<true, 2, GU_CT32_S2, NW_GS2, GU_RT32_S2>(g, grid_s[0], s);
     } else {
         if (HLr == 1) launch_gu<false, 1, GU_CT32_S, NW_GS, GU_RT32_S>(g, grid_s[0], s);
-        else          launch_gu<false, 2, GU_CT32_S, NW_GS, GU_RT32_S>(g, grid_s[0], s);
+        else          launch_gu<false, 2, GU_CT32_S2, NW_GS2, GU_RT32_S2>(g, grid_s[0], s);
     }
     if ((rc = launch_ok())) PF_RET(rc);
 

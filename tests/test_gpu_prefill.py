@@ -122,26 +122,30 @@ def test_full_prefill_2048_zipf(torch, k3x):
     layer.close()
 
 
-def test_prefill_graph_replays(torch, k3x):
+@pytest.mark.parametrize("latent,bf16", [(False, False), (False, True), (True, True)])
+def test_prefill_graph_replays(torch, k3x, latent, bf16):
     """A prefill chunk (T = 40) captured once into a HIP graph and replayed on new inputs,
     with eager work and synchronisations between the replays: every replay equals the eager
     call bit for bit (routing, permute, grouped GEMMs and combine are all kernels with
-    host-computed grids, so the per-layer sequence captures)."""
-    say("case: prefill T=40 captured in a graph, 3 replays with eager copies between")
-    L = synth.tiny(seed=35)
+    host-computed grids, so the per-layer sequence captures).  bf16 input takes the shared
+    expert's library GEMMs (and in the latent form the projections' library GEMMs) into
+    the graph; fp32 input the dense kernel."""
+    say(f"case: prefill T=40 captured in a graph, 3 replays with eager copies between, "
+        f"latent={latent} bf16={bf16}")
+    L = synth.tiny_latent(seed=35) if latent else synth.tiny(seed=35)
     layer = bank_layer(k3x, L)
     T, H, K = 40, L.H, L.K
-    xd = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    xd = torch.empty((T, H), dtype=torch.bfloat16 if bf16 else torch.float32, device="cuda")
     out = torch.empty((T, H), dtype=torch.float32, device="cuda")
     idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
     wt = torch.empty((T, K), dtype=torch.float32, device="cuda")
     s = torch.cuda.Stream()
 
     def run():
-        layer.forward(out.data_ptr(), xd.data_ptr(), T, k3x.K3X_F32, 0, idx.data_ptr(),
-                      wt.data_ptr(), stream=s.cuda_stream)
+        layer.forward(out.data_ptr(), xd.data_ptr(), T, k3x.K3X_BF16 if bf16 else k3x.K3X_F32,
+                      0, idx.data_ptr(), wt.data_ptr(), stream=s.cuda_stream)
 
-    xd.copy_(torch.from_numpy(L.x(T, bf16=False, stream_sub=20)))
+    xd.copy_(torch.from_numpy(L.x(T, bf16=bf16, stream_sub=20)))
     with torch.cuda.stream(s):
         run()                                   # eager: reserves the chunk buffers
     torch.cuda.synchronize()
@@ -150,7 +154,7 @@ def test_prefill_graph_replays(torch, k3x):
         run()
     torch.cuda.synchronize()
     for r in range(3):
-        x = L.x(T, bf16=False, stream_sub=21 + r)
+        x = L.x(T, bf16=bf16, stream_sub=21 + r)
         xd.copy_(torch.from_numpy(x))
         torch.cuda.synchronize()
         g.replay()

@@ -173,10 +173,15 @@ int  k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, i
                      const float *resid, int *idx, float *wt, void *stream);
 
 /* The prefill path of k3x_moe_forward (8 < T tokens) for callers that cannot allocate
- * device memory (code under HIP graph capture, tight serving loops): same arguments and
- * results (bit for bit), but the working buffers come from a static device array of
- * 64 MiB that each GPU holds until the process ends, instead of the layer's buffers that
- * k3x_moe_forward may grow.  Calls no allocating routine.  One call's buffers must fit
+ * device memory (code under HIP graph capture, tight serving loops): same arguments, but
+ * the working buffers come from a static device array of 64 MiB that each GPU holds until
+ * the process ends, instead of the layer's buffers that k3x_moe_forward may grow.  Calls
+ * no allocating routine: the plain products that k3x_moe_forward hands to hipBLASLt
+ * (bf16 input: the shared expert's where 2*SI <= hidden, the latent projections), whose
+ * first call of a shape may load code into device memory, run on the dense kernel here.
+ * Results: the same selected experts and routing weights bit for bit; outputs bit for bit
+ * where k3x_moe_forward uses no library product (fp32 input), else within fp32 rounding
+ * of it (a different order of the same exact products).  One call's buffers must fit
  * the array (about 590 KB per token at the K2 shape: T <= 111 there); larger T, or
  * T <= 8 (k3x_moe_forward's decode path allocates nothing), returns K3X_E_SHAPE.  Every
  * call on a GPU shares that GPU's array: calls that overlap on one GPU race, so order

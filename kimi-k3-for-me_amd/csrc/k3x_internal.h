@@ -123,6 +123,8 @@ typedef struct k3x_prefill_buf {
     float    *zf;           /* [T][X] z = down . x, then the routed aggregates        */
     uint16_t *zhl;          /* [2][X/8][T][8] hi/lo planes of the normalised
                                aggregates                                             */
+    int       no_lib;       /* 1: no library GEMMs (the no-allocation entry point: a
+                               library call may load code objects into device memory) */
 } k3x_prefill_buf;
 
 struct k3x_moe_layer {

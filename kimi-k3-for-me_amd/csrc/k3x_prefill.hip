@@ -1401,7 +1401,8 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     // the down product, which overwrites them), SiTU into bf16 hi and lo rows [T][SI] (in
     // act_sh), then the down product as two GEMMs, hi then lo accumulated, into the shared
     // rows of y.
-    const bool sh_blas = SI > 0 && L->blas && L->sh_gu_rm && x_bf16 &&
+    const bool lib = L->blas && !B->no_lib;
+    const bool sh_blas = SI > 0 && lib && L->sh_gu_rm && x_bf16 &&
                          k3x_blas_ready(L->device, H, 2 * SI, T, 0) == 0 &&
                          k3x_blas_ready(L->device, SI, H, T, 0) == 0 &&
                          k3x_blas_ready(L->device, SI, H, T, 1) == 0;
@@ -1502,7 +1503,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     if (L->lat) {
         // z = down . x for every token (k3_mmw_batch, k3_ops.c:1871): a plain product, on
         // the library where it serves the shape (bf16 rows), else the dense kernel
-        if (L->blas && x_bf16 && k3x_blas_ready(L->device, H, X, T, 0) == 0) {
+        if (lib && x_bf16 && k3x_blas_ready(L->device, H, X, T, 0) == 0) {
             if ((rc = k3x_blas_gemm_bf16(L->device, L->ldown_rm, H, X, B->zf, X,
                                          (const uint16_t *)x, H, T, 0, s)))
                 PF_RET(rc);
@@ -1612,7 +1613,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
         // the up projection: a plain product over the normalised aggregates' hi and lo
         // parts, on the library where it serves the shapes (rows [T][X] of each part),
         // else the dense kernel (k-group planes)
-        const bool up_blas = L->blas && k3x_blas_ready(L->device, X, H, T, 0) == 0 &&
+        const bool up_blas = lib && k3x_blas_ready(L->device, X, H, T, 0) == 0 &&
                              k3x_blas_ready(L->device, X, H, T, 1) == 0;
         hipLaunchKernelGGL(pf_latnorm, dim3(T), dim3(PF_NT), 0, s, B->zf,
                            c->latent_norm ? L->lnw : (const float *)NULL, c->rms_eps, T, X, B->zhl,
@@ -1716,6 +1717,7 @@ extern "C" int k3x_dev_prefill_noalloc(k3x_moe_layer *L, float *out, const void 
     k3x_prefill_buf B;
     memset(&B, 0, sizeof B);
     k3x_pf_layout(L, T, (char *)p, &B);
+    B.no_lib = 1;
     return pf_chunk(L, &B, out, x, x_dtype, T, resid, idx, wt, (hipStream_t)stream);
 }
 

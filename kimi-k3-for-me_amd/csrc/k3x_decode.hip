@@ -717,14 +717,55 @@ __device__ __forceinline__ void bf16_tile_x(const uint16_t *wtile, int K, const 
     wave_sum_lds<4, NW>(acc, lds, wave, lane);
 }
 
+// One 16-row tile of a tiled bf16 matrix (K columns) times x's compact B set (built by
+// the router launch), staged in LDS: four waves on interleaved quads, as bf16_tile_x, so
+// the same sums; ZR quads of weights in flight a wave (bf16_tile_x keeps two, its ring
+// also holding x's fragments).
+#define ZR 4
+__device__ __forceinline__ void bf16_tile_bset(const uint16_t *wtile, int K, const uint16_t *xB,
+                                               int NC, float *lds, float (&acc)[4])
+{
+    const int wave = wave_id(), lane = threadIdx.x % WAVE;
+    constexpr int NW = NT1 / WAVE;
+    const int nQ = K >> 7, nS = (nQ + 3) >> 2;
+    const int cnt = strided_count(wave, NW, nQ);
+    const uint32_t bbytes = (uint32_t)nS * 1024u * NC;
+    Stage<8> st;
+    st.issue(xB, bbytes, NT1);
+    const rsrc_t rw = make_rsrc(wtile, (uint32_t)nQ * 4096u);
+    QB w[ZR];
+    auto ld = [&](int i, int k) AI {
+        qb_load(w[i], rw, k < cnt ? (uint32_t)(wave + NW * k) * 4096u : K3X_OOB, lane);
+    };
+    ring_prime<ZR>(ld);
+    st.commit(NT1);
+    __syncthreads();
+    BFrag<true> bf;
+    bf.init(xB, bbytes, NC, lane);
+    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+    ring_loop<ZR>(cnt, ld, [&](int i, int k) AI {
+        const int q = wave + NW * k;
+        u32x4 b[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) b[t] = bf.get(0u, q, t);
+        qb_mfma(d, w[i], b);
+    });
+    acc[0] = d[0]; acc[1] = d[1]; acc[2] = d[2]; acc[3] = d[3];
+    wave_sum_lds<4, NW>(acc, lds, wave, lane);
+}
+
 // The latent down projection z = down . x (k3_mmw_batch, k3_ops.c:1871) for rows
-// 16*rt .. +15, and z's hi/lo B fragments into zB for k2's routed products.
+// 16*rt .. +15, and z's hi/lo B fragments into zB for k2's routed products.  LDSB: x's
+// B set (the router launch's, with the same fragments bf16_tile_x forms from x) staged in
+// LDS, for calls whose set fits (1 or 2 tokens).
+template <bool LDSB>
 __device__ void k1_down(const K1Args &a, float *lds, int rt)
 {
     const int wave = wave_id(), lane = threadIdx.x % WAVE;
     const int NC = 2 * a.T;
     float acc[4];
-    bf16_tile_x(a.ldown + (size_t)rt * 16 * a.H, a.H, a.x, a.x_bf16, a.H, a.T, lds, acc);
+    if (LDSB) bf16_tile_bset(a.ldown + (size_t)rt * 16 * a.H, a.H, a.xB, NC, lds, acc);
+    else bf16_tile_x(a.ldown + (size_t)rt * 16 * a.H, a.H, a.x, a.x_bf16, a.H, a.T, lds, acc);
     // z's set holds whole super-quads; its quads past XL/128 stay zero
     const int nSX = ((a.XL >> 7) + 3) >> 2;
     if (rt == 0)
@@ -750,7 +791,7 @@ __device__ void k1_down(const K1Args &a, float *lds, int rt)
 // behind the streaming workgroups' (about 14 us at the K3 shape).  A launch of its own:
 // folded into k1_router_bset's grid, the two paths' register allocation merges badly
 // (spills).
-template <int NE>
+template <int NE, bool LDSB>
 __global__ void __launch_bounds__(NT1) k1_zdown(K1Args a)
 {
     __shared__ float lds[(NT1 / WAVE - 1) * 4 * WAVE];
@@ -758,7 +799,7 @@ __global__ void __launch_bounds__(NT1) k1_zdown(K1Args a)
         ks_route<NE>(a.ks, *(KSLds *)dyn_lds, true);
         return;
     }
-    k1_down(a, lds, blockIdx.x - 1);
+    k1_down<LDSB>(a, lds, blockIdx.x - 1);
 }
 
 // Router logits of NT1 / WAVE / RWAVES experts (of the RMSNorm of x when norm_w is given),
@@ -2023,12 +2064,19 @@ extern "C" int k3x_dev_decode(k3x_moe_layer *L, float *out, const void *x, int x
     if (L->lat) {
         a1.ks = ks;
         const dim3 gz(1 + X / 16);
-        const size_t lz = sizeof(KSLds);
-        if (c->n_experts <= 128)      hipLaunchKernelGGL(k1_zdown<2>, gz, dim3(NT1), lz, s, a1);
-        else if (c->n_experts <= 256) hipLaunchKernelGGL(k1_zdown<4>, gz, dim3(NT1), lz, s, a1);
-        else if (c->n_experts <= 384) hipLaunchKernelGGL(k1_zdown<6>, gz, dim3(NT1), lz, s, a1);
-        else if (c->n_experts <= 512) hipLaunchKernelGGL(k1_zdown<8>, gz, dim3(NT1), lz, s, a1);
-        else                          hipLaunchKernelGGL(k1_zdown<16>, gz, dim3(NT1), lz, s, a1);
+        // x's B set staged in LDS where it fits beside two workgroups a CU
+        const size_t xbb = (size_t)nS * 1024u * 2 * T;
+        const bool zl = xbb <= 64 * 1024;
+        const size_t lz = std::max(sizeof(KSLds), zl ? xbb : (size_t)0);
+#define K1Z(NE_) \
+        if (zl) hipLaunchKernelGGL((k1_zdown<NE_, true>), gz, dim3(NT1), lz, s, a1); \
+        else    hipLaunchKernelGGL((k1_zdown<NE_, false>), gz, dim3(NT1), lz, s, a1);
+        if (c->n_experts <= 128)      { K1Z(2) }
+        else if (c->n_experts <= 256) { K1Z(4) }
+        else if (c->n_experts <= 384) { K1Z(6) }
+        else if (c->n_experts <= 512) { K1Z(8) }
+        else                          { K1Z(16) }
+#undef K1Z
         if ((rc = launch_ok())) return rc;
         if ((rc = record(L, ev++, s))) return rc;
     }

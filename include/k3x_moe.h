@@ -172,6 +172,20 @@ int  k3x_moe_layer_read_expert(const k3x_moe_layer *L, int e, unsigned char *p1,
 int  k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                      const float *resid, int *idx, float *wt, void *stream);
 
+/* The router alone: every token's top-k experts and combine weights for T tokens of
+ * device activations, the reference's k3_router (k3.h:294-313, k3_ops.c:1624-1719) over
+ * the layer's router and bias: logits as its sequential double chain, score
+ * sigmoid((float)logit), choice score + bias, the top-k by repeated maximum with the lower
+ * index first among equal choices, the unbiased scores renormalised and scaled; idx and
+ * wt bit for bit the reference's.  idx int [T][topk], wt fp32 [T][topk] device; x
+ * [T][hidden] device, K3X_F32 or K3X_BF16, 16-byte aligned.  The plain router: a layer's
+ * cache-only setting (draft routing, applied by the MoE call) does not apply.  Uses the
+ * layer's prefill buffers, growing them on a first call of more tokens than before (not
+ * while the stream is being captured: K3X_E_SHAPE then; reserve first with
+ * k3x_moe_layer_reserve).  Asynchronous on stream. */
+int  k3x_moe_route(k3x_moe_layer *L, int *idx, float *wt, const void *x, int x_dtype, int T,
+                   void *stream);
+
 /* The prefill path of k3x_moe_forward (8 < T tokens) for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops): same arguments, but
  * the working buffers come from a static device array of 64 MiB that each GPU holds until

@@ -242,6 +242,10 @@ int k3x_dev_decode(struct k3x_moe_layer *L, float *out, const void *x, int x_dty
                    void *stream);
 int k3x_dev_prefill(struct k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                     const float *resid, int *idx, float *wt, void *stream);
+/* the router alone over T tokens (k3x_moe_route): pf_router and pf_topk per prefill chunk,
+ * on the layer's prefill buffers (k3x_prefill.hip) */
+int k3x_dev_route(struct k3x_moe_layer *L, int *idx, float *wt, const void *x, int x_dtype,
+                  int T, void *stream);
 /* prefill working buffers for runs of min(T, the chunk) tokens; refuses to grow while
  * `stream` is being captured (k3x_moe.c) */
 int k3x_pf_reserve(struct k3x_moe_layer *L, int T, void *stream);

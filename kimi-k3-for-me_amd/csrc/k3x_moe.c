@@ -1035,6 +1035,16 @@ int k3x_moe_forward(k3x_moe_layer *L, float *out, const void *x, int x_dtype, in
     return k3x_dev_prefill(L, out, x, x_dtype, T, resid, idx, wt, stream);
 }
 
+int k3x_moe_route(k3x_moe_layer *L, int *idx, float *wt, const void *x, int x_dtype, int T,
+                  void *stream)
+{
+    if (!L || (T > 0 && (!x || !idx || !wt))) return K3X_E_ARG;
+    if (T < 0 || (x_dtype != K3X_F32 && x_dtype != K3X_BF16)) return K3X_E_ARG;
+    if ((uintptr_t)x & 15) return K3X_E_ARG;
+    if (T == 0) return 0;
+    return k3x_dev_route(L, idx, wt, x, x_dtype, T, stream);
+}
+
 int k3x_moe_prefill_noalloc(k3x_moe_layer *L, float *out, const void *x, int x_dtype, int T,
                             const float *resid, int *idx, float *wt, void *stream)
 {

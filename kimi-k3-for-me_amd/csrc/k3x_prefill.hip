@@ -276,7 +276,7 @@ __global__ void __launch_bounds__(PF_NT) pf_topk(PfTopkArgs a)
         a.idx[o] = e;
         a.wt[o] = s_w[wave][lane];
         if (a.uidx) { a.uidx[o] = e; a.uwt[o] = s_w[wave][lane]; }
-        atomicAdd(&a.counts[e], 1);
+        if (a.counts) atomicAdd(&a.counts[e], 1);
     }
 }
 
@@ -1665,6 +1665,42 @@ extern "C" int k3x_dev_prefill(k3x_moe_layer *L, float *out, const void *x, int 
                       resid ? resid + (size_t)t0 * H : NULL, idx ? idx + (size_t)t0 * K : NULL,
                       wt ? wt + (size_t)t0 * K : NULL, (hipStream_t)stream);
         if (rc) return rc;
+    }
+    return 0;
+}
+
+// The router alone (k3x_moe_route): per chunk, every (token, expert) logit as the
+// reference's chain (pf_router) and each token's top-k into the caller's arrays (pf_topk,
+// no histogram).
+extern "C" int k3x_dev_route(k3x_moe_layer *L, int *idx, float *wt, const void *x, int x_dtype,
+                             int T, void *stream)
+{
+    const k3x_cfg *c = &L->cfg;
+    const int H = c->hidden, E = c->n_experts, K = c->topk;
+    const size_t es = (x_dtype == K3X_BF16) ? 2 : 4;
+    const int chunk = k3x_pf_chunk_tokens(L);
+    hipStream_t s = (hipStream_t)stream;
+    int rc = k3x_pf_reserve(L, T, stream);
+    if (rc) return rc;
+    for (int t0 = 0; t0 < T; t0 += chunk) {
+        const int n = T - t0 < chunk ? T - t0 : chunk;
+        PfRouterArgs ar;
+        ar.x = (const char *)x + (size_t)t0 * H * es; ar.x_bf16 = x_dtype == K3X_BF16;
+        ar.W = L->router; ar.bias = L->bias; ar.T = n; ar.H = H; ar.E = E;
+        ar.score = L->pf.score; ar.choice = L->pf.choice;
+        hipLaunchKernelGGL(pf_router, dim3(cdiv(n, RM_T) * cdiv(E, RM_E)), dim3(RM_NT), 0, s, ar);
+        if ((rc = launch_ok())) return rc;
+        PfTopkArgs at;
+        at.score = L->pf.score; at.choice = L->pf.choice; at.T = n; at.E = E; at.K = K;
+        at.renorm = c->moe_renorm; at.routed_scale = c->routed_scale;
+        at.idx = idx + (size_t)t0 * K; at.wt = wt + (size_t)t0 * K;
+        at.uidx = NULL; at.uwt = NULL; at.counts = NULL;
+        if (E <= 128)      launch_topk<2>(at, s);
+        else if (E <= 256) launch_topk<4>(at, s);
+        else if (E <= 384) launch_topk<6>(at, s);
+        else if (E <= 512) launch_topk<8>(at, s);
+        else               launch_topk<16>(at, s);
+        if ((rc = launch_ok())) return rc;
     }
     return 0;
 }

@@ -38,7 +38,7 @@ EXPORTS = [
     "k3x_attn_res", "k3x_moe_half", "k3x_attn_res_v", "k3x_moe_half_v",
     "k3x_moe_layer_reserve", "k3x_moe_layer_dequant",
     "k3x_moe_prefill_noalloc", "k3x_moe_layer_trace", "k3x_moe_layer_set_prefill_mode",
-    "k3x_moe_layer_exact_count", "k3x_moe_layer_last_route",
+    "k3x_moe_layer_exact_count", "k3x_moe_layer_last_route", "k3x_moe_route",
     # include/k3x_store.h
     "k3x_store_open", "k3x_store_close", "k3x_store_count", "k3x_store_shards",
     "k3x_store_find", "k3x_store_read", "k3x_store_expert_ref", "k3x_store_expert_load",
@@ -142,6 +142,7 @@ def lib():
         L.k3x_moe_layer_dequant.argtypes = [vp, i, i, vp]
         L.k3x_moe_forward.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
         L.k3x_moe_prefill_noalloc.argtypes = [vp, vp, vp, i, i, vp, vp, vp, vp]
+        L.k3x_moe_route.argtypes = [vp, vp, vp, vp, i, i, vp]
         L.k3x_moe_layer_trace.argtypes = [vp, i, vp, i]
         L.k3x_moe_layer_exact_count.argtypes = [vp, C.POINTER(i)]
         L.k3x_moe_layer_last_route.argtypes = [vp, i, vp, vp]
@@ -437,6 +438,12 @@ class MoELayer:
         _check(lib().k3x_moe_forward(self.h, out_ptr, x_ptr, x_dtype, T, resid_ptr or None,
                                      idx_ptr or None, wt_ptr or None, stream or None),
                "k3x_moe_forward")
+
+    def route(self, idx_ptr, wt_ptr, x_ptr, T, x_dtype=K3X_F32, stream=0):
+        """k3x_moe_route: every token's experts and weights (device pointers; asynchronous
+        on `stream`)."""
+        _check(lib().k3x_moe_route(self.h, idx_ptr, wt_ptr, x_ptr, x_dtype, T, stream or None),
+               "k3x_moe_route")
 
     def prefill_noalloc(self, out_ptr, x_ptr, T, x_dtype=K3X_F32, resid_ptr=0, idx_ptr=0,
                         wt_ptr=0, stream=0):

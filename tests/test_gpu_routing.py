@@ -321,3 +321,75 @@ def test_decode_router_same_bits_for_any_token_count(torch, k3x, bf16, H, E):
         assert np.array_equal(iT, i1[:T]), T
         assert np.array_equal(wT.view(np.uint32), w1[:T].view(np.uint32)), T
     layer.close()
+
+
+def dev_route(torch, k3x, layer, x, bf16=False):
+    """k3x_moe_route on device copies; (idx, wt) on the host."""
+    T = x.shape[0]
+    K = layer.cfg.topk
+    xt = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    if bf16:
+        xt = xt.to(torch.bfloat16)
+    idx = torch.full((T, K), -7, dtype=torch.int32, device="cuda")
+    wt = torch.full((T, K), -7.0, dtype=torch.float32, device="cuda")
+    layer.route(idx.data_ptr(), wt.data_ptr(), xt.data_ptr(), T,
+                k3x.K3X_BF16 if bf16 else k3x.K3X_F32, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return idx.cpu().numpy(), wt.cpu().numpy()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_route_alone_matches_oracle_and_forward(torch, k3x, bf16):
+    """k3x_moe_route (the router alone, k3_router k3_ops.c:1624-1719) gives the oracle's
+    experts and weights bit for bit at 1, 3 and 20 tokens, with NaN, -inf and +inf biases
+    and a tie in the ranking, and the same routing k3x_moe_forward reports for the same
+    tokens."""
+    say(f"case: router alone, E=200 K=8, ties and NaN/inf biases, bf16={bf16}")
+    L = synth.Layer(H=256, E=200, K=8, I=128, seed=71)
+    L.gate[77] = L.gate[160]
+    L.bias[77] = L.bias[160]
+    L.bias[[5, 9]] = np.nan
+    L.bias[[11]] = -np.inf
+    L.bias[42] = np.inf
+    x = L.x(20, bf16=bf16, stream_sub=71)
+    layer = bank_layer(k3x, L)
+    ri, rw = oracle_routes(L, x)
+    for T in (1, 3, 20):
+        idx, wt = dev_route(torch, k3x, layer, x[:T], bf16=bf16)
+        assert np.array_equal(idx, ri[:T]), (T, idx, ri[:T])
+        assert np.array_equal(wt.view(np.uint32), rw[:T].view(np.uint32))
+        _, i2, w2 = dev_forward(torch, k3x, layer, x[:T], bf16=bf16)
+        assert np.array_equal(i2, idx) and np.array_equal(w2.view(np.uint32), wt.view(np.uint32))
+        say(f"  T={T}: bitwise")
+    assert (ri[:, 0] == 42).all()
+    layer.close()
+
+
+def test_route_alone_cancelling_data_bitwise(torch, k3x):
+    """The router alone on the cancelling data of the prefill router test (a four-chain
+    order changes most float logits): weights bitwise the oracle's, renorm off."""
+    say("case: router alone on cancelling data, E=100 H=1024 T=70, weights bitwise")
+    H, E, K, T, p = 1024, 100, 8, 70, 512
+    L = synth.Layer(H=H, E=E, K=K, I=128, seed=72, renorm=0, routed_scale=1.0)
+    L.gate[:, p + 1] = L.gate[:, p]
+    x = cancelling_tokens(H, T, p, 72, 2.0 ** 40, False)
+    layer = bank_layer(k3x, L)
+    idx, wt = dev_route(torch, k3x, layer, x)
+    ri, rw = oracle_routes(L, x)
+    assert np.array_equal(idx, ri)
+    assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+    layer.close()
+
+
+def test_route_alone_full_shape(torch, k3x):
+    """The router alone at the K2 shape (7168 x 384, top-8, Zipf-skewed biases), 300 bf16
+    tokens: experts and weights bitwise the oracle's."""
+    say("case: router alone, full K2 router, 300 bf16 tokens, Zipf-skewed")
+    L = synth.full(seed=73, zipf_alpha=1.0)
+    layer = synth_layer(k3x, L)
+    x = L.x(300, bf16=True, stream_sub=73)
+    idx, wt = dev_route(torch, k3x, layer, x, bf16=True)
+    ri, rw = oracle_routes(L, x)
+    assert np.array_equal(idx, ri)
+    assert np.array_equal(wt.view(np.uint32), rw.view(np.uint32))
+    layer.close()

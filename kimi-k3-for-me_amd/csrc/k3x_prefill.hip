@@ -257,27 +257,41 @@ struct PfTopkArgs {
     int         *counts;                 // [E] histogram
 };
 
+// One wave per token, TK_W tokens a workgroup.  The per-expert histogram is counted in LDS
+// first and added to the global counts once per workgroup and expert: a device-scope
+// atomic per (token, slot) serialised on the busiest experts' counters (the Zipf chunk's
+// first expert takes every token).
+#define TK_W 16
 template <int NE>
-__global__ void __launch_bounds__(PF_NT) pf_topk(PfTopkArgs a)
+__global__ void __launch_bounds__(TK_W * WAVE) pf_topk(PfTopkArgs a)
 {
-    __shared__ int      s_idx[PF_NT / WAVE][K3X_MAX_TOPK];
-    __shared__ float    s_w[PF_NT / WAVE][K3X_MAX_TOPK];
+    __shared__ int      s_idx[TK_W][K3X_MAX_TOPK];
+    __shared__ float    s_w[TK_W][K3X_MAX_TOPK];
+    __shared__ int      hist[1024];
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    const int t = blockIdx.x * (PF_NT / WAVE) + wave;
-    if (t >= a.T) return;
-    const rsrc_t cr = make_rsrc(a.choice, (uint32_t)((size_t)a.T * a.E * 4));
-    const rsrc_t sr = make_rsrc(a.score, (uint32_t)((size_t)a.T * a.E * 4));
-    wave_topk<NE, 0>(cr, sr, (uint32_t)((size_t)t * a.E * 4), a.E, a.K, a.renorm, a.routed_scale,
-                  s_idx[wave], s_w[wave], lane);
-    __builtin_amdgcn_wave_barrier();
-    if (lane < a.K) {
-        const size_t o = (size_t)t * a.K + lane;
-        const int e = s_idx[wave][lane];
-        a.idx[o] = e;
-        a.wt[o] = s_w[wave][lane];
-        if (a.uidx) { a.uidx[o] = e; a.uwt[o] = s_w[wave][lane]; }
-        if (a.counts) atomicAdd(&a.counts[e], 1);
+    const int t = blockIdx.x * TK_W + wave;
+    if (a.counts)
+        for (int e = threadIdx.x; e < a.E; e += TK_W * WAVE) hist[e] = 0;
+    __syncthreads();
+    if (t < a.T) {                                       // uniform over the wave
+        const rsrc_t cr = make_rsrc(a.choice, (uint32_t)((size_t)a.T * a.E * 4));
+        const rsrc_t sr = make_rsrc(a.score, (uint32_t)((size_t)a.T * a.E * 4));
+        wave_topk<NE, 0>(cr, sr, (uint32_t)((size_t)t * a.E * 4), a.E, a.K, a.renorm,
+                         a.routed_scale, s_idx[wave], s_w[wave], lane);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < a.K) {
+            const size_t o = (size_t)t * a.K + lane;
+            const int e = s_idx[wave][lane];
+            a.idx[o] = e;
+            a.wt[o] = s_w[wave][lane];
+            if (a.uidx) { a.uidx[o] = e; a.uwt[o] = s_w[wave][lane]; }
+            if (a.counts) atomicAdd(&hist[e], 1);
+        }
     }
+    if (!a.counts) return;                               // uniform
+    __syncthreads();
+    for (int e = threadIdx.x; e < a.E; e += TK_W * WAVE)
+        if (hist[e]) atomicAdd(&a.counts[e], hist[e]);
 }
 
 // ------------------------------------------------------------------ scan
@@ -342,14 +356,26 @@ __global__ void __launch_bounds__(1024) pf_scan(PfScanArgs a)
 }
 
 // ------------------------------------------------------------------ scatter
+// Each (token, slot) to a row of its expert's segment: a workgroup ranks its items per
+// expert in LDS, reserves each expert's run with one device-scope atomic, and places its
+// items in that run (the order within a segment is free: every row's products are its
+// own, and the combine finds each row through pos_of).
 __global__ void __launch_bounds__(PF_NT) pf_scatter(const int *idx, const float *wt, int TK, int K,
-                                                    const int *offsets, int *cursor,
+                                                    int E, const int *offsets, int *cursor,
                                                     int *perm_tok, float *perm_w, int *pos_of)
 {
+    __shared__ int cnt[1024], base[1024];
+    for (int e = threadIdx.x; e < E; e += PF_NT) cnt[e] = 0;
+    __syncthreads();
     const int i = blockIdx.x * PF_NT + threadIdx.x;
+    const int e = i < TK ? idx[i] : 0;
+    const int r = i < TK ? atomicAdd(&cnt[e], 1) : 0;
+    __syncthreads();
+    for (int f = threadIdx.x; f < E; f += PF_NT)
+        if (cnt[f]) base[f] = offsets[f] + atomicAdd(&cursor[f], cnt[f]);
+    __syncthreads();
     if (i >= TK) return;
-    const int e = idx[i];
-    const int p = offsets[e] + atomicAdd(&cursor[e], 1);
+    const int p = base[e] + r;
     perm_tok[p] = i / K;
     perm_w[p] = wt[i];
     pos_of[i] = p;
@@ -1286,7 +1312,7 @@ static inline unsigned cdiv(size_t a, size_t b) { return (unsigned)((a + b - 1) 
 template <int NE>
 static void launch_topk(const PfTopkArgs &a, hipStream_t s)
 {
-    hipLaunchKernelGGL(pf_topk<NE>, dim3(cdiv(a.T, PF_NT / WAVE)), dim3(PF_NT), 0, s, a);
+    hipLaunchKernelGGL(pf_topk<NE>, dim3(cdiv(a.T, TK_W)), dim3(TK_W * WAVE), 0, s, a);
 }
 
 // Launch shapes of the routed GEMMs (pf_gemm32): NW waves of RT32 32-row tiles per
@@ -1495,7 +1521,7 @@ static int pf_chunk(k3x_moe_layer *L, const k3x_prefill_buf *B, float *out, cons
     hipLaunchKernelGGL(pf_scan, dim3(1), dim3(1024), 0, s, sa);
     if ((rc = launch_ok())) PF_RET(rc);
     hipLaunchKernelGGL(pf_scatter, dim3(cdiv(TK, PF_NT)), dim3(PF_NT), 0, s, B->idx, B->wt, TK, K,
-                       B->offsets, B->cursor, B->perm_tok, B->perm_w, B->pos_of);
+                       E, B->offsets, B->cursor, B->perm_tok, B->perm_w, B->pos_of);
     if ((rc = launch_ok())) PF_RET(rc);
     hipLaunchKernelGGL(pf_tiles, dim3(E), dim3(PF_NT), 0, s, B->counts, B->offsets, sa,
                        (int4 *)B->desc_gu, (int4 *)B->desc_dn);

@@ -300,7 +300,8 @@ __global__ void __launch_bounds__(TK_W * WAVE) pf_topk(PfTopkArgs a)
 // most tpb_s tokens takes nrb_s tiles of tpb_s columns (one column block), a larger one
 // nrb_b x ceil(count/tpb_b) tiles of tpb_b columns.  tb[0..E] are the small class's bases
 // (tb[E] = its tile count), tb[E+1 .. 2E+1] the large class's.  Cursors cleared.  Five
-// inclusive scans in LDS, one element per thread.
+// inclusive scans, one element per thread (shuffles within each wave, then the waves'
+// totals).
 struct PfScanArgs {
     const int *counts;
     int        E;
@@ -312,8 +313,8 @@ struct PfScanArgs {
 
 __global__ void __launch_bounds__(1024) pf_scan(PfScanArgs a)
 {
-    __shared__ int s[5][1024];
-    const int e = threadIdx.x, E = a.E;
+    __shared__ int wsum[5][16], woff[5][16];
+    const int e = threadIdx.x, E = a.E, wave = e / WAVE, lane = e % WAVE;
     const int c = e < E ? a.counts[e] : 0;
     int v[5];
     v[0] = c;
@@ -324,33 +325,49 @@ __global__ void __launch_bounds__(1024) pf_scan(PfScanArgs a)
         v[2 + 2 * m] = big ? a.nrb_b[m] * ((c + a.tpb_b[m] - 1) / a.tpb_b[m]) : 0;
     }
     if (e < E) a.cursor[e] = 0;
-    for (int d = 1; d < 1024; d <<= 1) {
+    // inclusive sums: within each wave by shuffles, then the waves' totals (wave 0)
+    int in[5];
 #pragma unroll
-        for (int i = 0; i < 5; i++) s[i][e] = v[i];
-        __syncthreads();
-        if (e >= d)
+    for (int i = 0; i < 5; i++) {
+        in[i] = v[i];
 #pragma unroll
-            for (int i = 0; i < 5; i++) v[i] += s[i][e - d];
-        __syncthreads();
+        for (int o = 1; o < WAVE; o <<= 1) {
+            const int t = __shfl_up(in[i], o);
+            if (lane >= o) in[i] += t;
+        }
+        if (lane == WAVE - 1) wsum[i][wave] = in[i];
     }
-    // v = inclusive sums; the exclusive value of e is the inclusive value of e - 1
-#pragma unroll
-    for (int i = 0; i < 5; i++) s[i][e] = v[i];
     __syncthreads();
+    if (wave == 0 && lane < 16) {
+#pragma unroll
+        for (int i = 0; i < 5; i++) {
+            int x = wsum[i][lane], inc = x;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const int t = __shfl_up(inc, o, 16);
+                if (lane >= o) inc += t;
+            }
+            woff[i][lane] = inc - x;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 5; i++) in[i] += woff[i][wave];
+    // the exclusive value of e is its inclusive sum less its own
     if (e < E) {
-        a.offsets[e] = e == 0 ? 0 : s[0][e - 1];
+        a.offsets[e] = in[0] - v[0];
 #pragma unroll
         for (int m = 0; m < 2; m++) {
-            a.tb[m][e] = e == 0 ? 0 : s[1 + 2 * m][e - 1];
-            a.tb[m][E + 1 + e] = e == 0 ? 0 : s[2 + 2 * m][e - 1];
+            a.tb[m][e] = in[1 + 2 * m] - v[1 + 2 * m];
+            a.tb[m][E + 1 + e] = in[2 + 2 * m] - v[2 + 2 * m];
         }
     }
     if (e == E - 1) {
-        a.offsets[E] = v[0];
+        a.offsets[E] = in[0];
 #pragma unroll
         for (int m = 0; m < 2; m++) {
-            a.tb[m][E] = v[1 + 2 * m];
-            a.tb[m][2 * E + 1] = v[2 + 2 * m];
+            a.tb[m][E] = in[1 + 2 * m];
+            a.tb[m][2 * E + 1] = in[2 + 2 * m];
         }
     }
 }

@@ -261,7 +261,7 @@ struct PfTopkArgs {
 // first and added to the global counts once per workgroup and expert: a device-scope
 // atomic per (token, slot) serialised on the busiest experts' counters (the Zipf chunk's
 // first expert takes every token).
-#define TK_W 16
+#define TK_W 8
 template <int NE>
 __global__ void __launch_bounds__(TK_W * WAVE) pf_topk(PfTopkArgs a)
 {

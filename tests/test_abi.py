@@ -81,6 +81,7 @@ def test_null_arguments(k3x):
     assert lib.k3x_moe(None, None, None, 1, None, None) == -1
     assert lib.k3x_moe_layer_create(None, None, 0, None) == -1
     assert lib.k3x_rmsnorm(None, None, None, 8, 1, 1e-5, None) == -1
+    assert lib.k3x_moe_route(None, None, None, None, 0, 1, None) == -1
 
 
 def test_synth_generator_matches_oracle(k3x):
